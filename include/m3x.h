@@ -1,0 +1,162 @@
+/* m3x: MI355X (gfx950) kernels of the Maya3 per-frame decode step, as a C ABI.
+ *
+ * Conventions (every entry point):
+ *   - pointers are device pointers (from any HIP allocator); sizes/strides are in ELEMENTS;
+ *   - 16-bit tensors are bf16 (dtype M3X_BF16 = 0) or fp16 (M3X_F16 = 1) stored as raw 16-bit words;
+ *   - `stream` is a hipStream_t (NULL = the default stream); launches are stream-ordered, never synchronise and
+ *     never allocate, so every call can be captured into a hipGraph; scratch memory comes in as `workspace`;
+ *   - the return value is 0 (M3X_OK) when the kernels were launched, else a negative status:
+ *       -1 M3X_EINVAL bad shape/stride/alignment, -2 M3X_ENULL missing pointer, -3 M3X_EWORKSPACE workspace too
+ *       small, -4 M3X_ELAUNCH launch failed, -5 M3X_EUNSUPPORTED shape/dtype not implemented.
+ * Reference citations are to MayaResearch/maya2-native.
+ */
+#ifndef M3X_H
+#define M3X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { M3X_OK = 0, M3X_EINVAL = -1, M3X_ENULL = -2, M3X_EWORKSPACE = -3, M3X_ELAUNCH = -4, M3X_EUNSUPPORTED = -5 };
+enum { M3X_BF16 = 0, M3X_F16 = 1 };
+enum { M3X_NORM_LAYER = 0, M3X_NORM_RMS = 1 };
+enum { M3X_ACT_SWIGLU = 0, M3X_ACT_GELU = 1 };
+
+int m3x_version(void);
+
+/* ---- backbone step (serve/fast_backbone.py StaticBackbone._forward, fuse_rope path :176-234) ---------------- */
+
+/* pos[r] = lengths[slots[r]] + offset[r] (offset may be NULL).
+ * Replaces `pos=self.lengths[slots]; pos=pos+offset` (serve/fast_backbone.py:178-179). */
+int m3x_positions(const int64_t* lengths, const int64_t* slots, const int64_t* offset, int32_t* pos, int R,
+                  void* stream);
+
+/* lengths[slots[r]] += real[r] (duplicates accumulate).
+ * Replaces `self.lengths.index_add_(0,slots,real)` (serve/fast_backbone.py:233). */
+int m3x_lengths_add(int64_t* lengths, const int64_t* slots, const int64_t* real, int R, void* stream);
+
+/* h_out = bf16(h + a); y = bf16(bf16(h_out * 1/sqrt(mean(h_out^2) + eps)) * w); a == NULL: y = RMSNorm(h).
+ * n in {512, 1024, 2048}; h_out may alias h. Fixed fp32 reduction order (bit-exact vs the oracle).
+ * Replaces `_add_rms` + `_add_norm` (serve/fast_backbone.py:95-104,236-240) and the HF input RMSNorm (:190). */
+int m3x_add_rms(const void* h, long s_h, const void* a, long s_a, void* h_out, long s_ho, void* y, long s_y,
+                const void* w, float eps, int rows, int n, void* stream);
+
+/* Per-head q/k RMSNorm + RoPE (rotate_half) of qkv rows [q heads | k heads | v heads]; q heads -> q_out
+ * [rows, heads, D]; k heads -> k_cache[slots[r], kh, pos[r], :]; v heads copied to v_cache at the same place.
+ * head_dim in {64, 128}; cos/sin are [cap, head_dim] tables in bf16.
+ * Replaces `_qk_norm_rope_cache` (serve/fast_backbone.py:61-92, launch :195-197). */
+int m3x_qk_norm_rope_cache(const void* qkv, long s_qkv, void* q_out, long s_qo_b, long s_qo_h, void* k_cache,
+                           void* v_cache, long sk_s, long sk_h, long sk_t, const int64_t* slots, const int32_t* pos,
+                           const void* cos, const void* sin, long s_cos, const void* wq, const void* wk, float eps,
+                           int rows, int heads, int kv_heads, int head_dim, int cap, void* stream);
+
+/* Bytes of workspace m3x_decode_attn needs for (rows, kv_heads, max_ctx, chunk). */
+size_t m3x_decode_attn_workspace(int rows, int kv_heads, int max_ctx, int chunk);
+
+/* GQA decode attention in place over the static cache: out[r, h, :] = softmax(q[r,h]·K[slot,h/G,0..pos]^T * scale)
+ * · V[...]; heads/kv_heads in {1, 2}; head_dim 128; chunk = keys per split (multiple of 128); max_ctx >= pos+1
+ * for every row; cap % 32 == 0.
+ * Replaces `_decode_attn` + `StaticBackbone._launch` (serve/fast_backbone.py:31-58,242-247). */
+int m3x_decode_attn(const void* q, long sq_b, long sq_h, const void* k_cache, const void* v_cache, long sk_s,
+                    long sk_h, long sk_t, int cap, void* out, long so_b, long so_h, const int64_t* slots,
+                    const int32_t* pos, float scale, int rows, int heads, int kv_heads, int head_dim, int max_ctx,
+                    int chunk, void* workspace, size_t ws_bytes, void* stream);
+
+/* Bytes of workspace m3x_linear needs (0 when it runs without splitting K). */
+size_t m3x_linear_workspace(int M, int N, int K, int splits_hint);
+
+/* y[M,N] = x[M,K] · w[N,K]^T, 16-bit in/out, fp32 accumulation (MFMA); K % 32 == 0; splits_hint 0 = auto.
+ * Replaces `F.linear` / `nn.Linear` on the path: q|k|v, o, gate|up, down (serve/fast_backbone.py:193,200-202),
+ * cb0 head (tts/model/backbone.py:135-136), depth trunk and heads (serve/fast_depth.py:104,122-125,185-191). */
+int m3x_linear(const void* x, long ldx, const void* w, long ldw, void* y, long ldy, int M, int N, int K,
+               int splits_hint, void* workspace, size_t ws_bytes, int dtype, void* stream);
+
+/* out[r, :I] = act(in[r, :]): M3X_ACT_SWIGLU: bf16(silu(g)) * u with in = [g | u] (2*I wide);
+ * M3X_ACT_GELU: gelu(in[r, :I]) (erf form).
+ * Replaces `F.silu(g_)*u_` (serve/fast_backbone.py:201-202) and `F.gelu` (serve/fast_depth.py:123,186). */
+int m3x_act(const void* in, long ld_in, void* out, long ld_out, int rows, int I, int kind, int dtype, void* stream);
+
+/* ---- depth frame step (serve/fast_depth.py FastDepth._compute/_compute_fused :84-203) ----------------------- */
+
+/* Row r = (b, t) = (r / T, r % T): x_out = dt(x + a) [then dt(x_out + c[b])]; y = norm(x_out) with LayerNorm
+ * (w, b) or RMSNorm (w). x and a are read at base + b*s?b + t*s?t; x_out and y are contiguous [rows, n]; c rows
+ * have stride s_c (0 broadcasts); a, c, x_out may be NULL; n in {1024, 2048}.
+ * Replaces `_add_ln`/`add_ln` (serve/fast_depth_kernels.py:14-45) and the first-layer `n1` (serve/fast_depth.py:164). */
+int m3x_add_norm(const void* x, long sxb, long sxt, const void* a, long sab, long sat, const void* c, long s_c,
+                 void* x_out, void* y, const void* w, const void* b, float eps, int rows, int T, int n, int kind,
+                 int dtype, void* stream);
+
+/* out[r] = dt(x[r] + bias[r * ld_bias]) (ld_bias = 0 broadcasts one row); n % 8 == 0.
+ * Replaces `d.in_proj(h) + self.level0` (serve/fast_depth.py:150). */
+int m3x_add_rows(const void* x, long ld_x, const void* bias, long ld_bias, void* out, long ld_out, int rows, int n,
+                 int dtype, void* stream);
+
+/* Depth self-attention over one frame's positions: qkv rows (b, t) at positions p0+t, read at
+ * qkv + b*sqb + t*sqt ([q|k|v] x heads x head_dim); write_kv stores their K/V into the scratch kd/vd
+ * [B, heads, np, head_dim]; queries t >= tq0 attend keys 0..p0+t; output row (b, t-tq0) at out + b*sob + tq*sot.
+ * np <= 64, head_dim <= 128.
+ * Replaces the trunk's `F.scaled_dot_product_attention` + within-group KV (serve/fast_depth.py:102-121,165-183). */
+int m3x_depth_attn(const void* qkv, long sqb, long sqt, void* kd, void* vd, void* out, long sob, long sot, int B,
+                   int T, int p0, int tq0, int heads, int head_dim, int np, float scale, int write_kv, int dtype,
+                   void* stream);
+
+/* Top-k sampler with caller uniforms (x = logit * inv_temp; inverse CDF over the kept set, order x desc / index
+ * asc; greedy = argmax); V <= 4096; writes int32 or int64 codes to out[b * ld_out].
+ * Replaces `_topk_sample`/`topk_sample` (serve/fast_depth_kernels.py:48-79) and the unfused sampler
+ * (serve/fast_depth.py:125-132). */
+int m3x_topk_sample(const void* logits, long ld_l, int V, const float* u, long ld_u, float inv_temp, int top_k,
+                    int greedy, void* out, long ld_out, int out_i64, int B, int dtype, void* stream);
+
+/* cb0 controlled stop + sampling per seat (per-slot state indexed by slots[b]); any per-slot pointer may be NULL.
+ * Replaces `Engine._cb0` (maya3/engine.py:652-694) with caller uniforms in place of `row_exponential`
+ * (serve/fast_depth_kernels.py:82-98). */
+int m3x_cb0_sample(const void* logits, long ld_l, int V, int aeos, const int64_t* slots, const float* u, long ld_u,
+                   const float* temp_t, float temp, const int64_t* topk_t, int top_k, const float* aeos_bias,
+                   const float* rep_t, int64_t* hist_t, int hist_w, int64_t* frames_t, const int64_t* min_t,
+                   float* hazard_t, int32_t* ctr_t, int64_t* cb0_out, int32_t* cb0_i32, long ld_cb0_i32,
+                   int64_t* stop_out, int B, void* stream);
+
+/* u[b, j] = Philox4x32-10 uniform for counter (ctrs[s], level0 + j, 0, 0), key (seeds[s], 0), s = slots[b].
+ * Replaces the per-request Philox streams keyed by (seed, frame counter, level)
+ * (serve/fast_depth_kernels.py:63,90; maya3/engine.py:436-437). */
+int m3x_philox_uniforms(const int32_t* seeds, const int32_t* ctrs, const int64_t* slots, float* out, long ld_out,
+                        int level0, int nlevels, int B, void* stream);
+
+/* out[b, c] = -log(max(u, 1e-12)) with u the Philox uniform of counter (ctrs[b], level, c, 0), key (seeds[b], 0),
+ * for c < V (per-row seeds/counters, already gathered by the caller).
+ * Replaces `_row_exponential`/`row_exponential` (serve/fast_depth_kernels.py:82-98). */
+int m3x_philox_exponential(const int32_t* seeds, const int32_t* ctrs, float* out, long ld_out, int level, int V, int B,
+                           void* stream);
+
+/* One raw Philox4x32-10 block (for known-answer tests); all pointers on the device. */
+int m3x_philox_block(const uint32_t* counter, const uint32_t* key, uint32_t* out, void* stream);
+
+/* ctr[slots[b]] += 1. Replaces `self.row_ctr.index_add_(...)` (serve/fast_depth.py:199). */
+int m3x_ctr_add(int32_t* ctr, const int64_t* slots, int B, void* stream);
+
+/* Feedback embedding: y[b] = RMSNorm(dt(dt(sum_l table[codes[b,l] + n_codes*l]) / scale)) (fp32 sum, one final
+ * rounding); n in {1024, 2048}.
+ * Replaces `audio_in.table(codes+offsets)` + `audio_in.norm(e.sum(1)/scale)` (serve/fast_depth.py:200-203,
+ * tts/model/audio_io.py:27-35). */
+int m3x_feedback(const void* table, const int32_t* codes, long s_codes, void* out, long s_out, const void* w, float eps,
+                 float scale, int B, int n, int n_q, int n_codes, int dtype, void* stream);
+
+/* Row copy with optional gather (src_idx[r]+src_off, clamped to [0, src_rows)) and scatter (dst_idx[r]) of n
+ * 16-bit elements per row (n % 8 == 0); indices int64 or int32 (idx_i32) with stride ld_idx.
+ * Replaces `F.embedding(code, self.embed[level])` (serve/fast_depth.py:135,196) and the engine's
+ * `self.feedback[idx]` gather / `self.feedback[idx] = fb` scatter (maya3/engine.py:542,556). */
+int m3x_copy_rows(const void* src, long ld_src, const void* src_idx, long src_off, long src_rows, void* dst,
+                  long ld_dst, const int64_t* dst_idx, int rows, int n, int idx_i32, long ld_idx, void* stream);
+
+/* ring[(*head) % depth, b, :] = codes[b, :nq] for b < B, then *head += 1 (int32 [depth, seats, nq] ring).
+ * Replaces the per-tick code readout (serve/fast_depth.py:137,257; maya3/engine.py:559-563) with a device ring. */
+int m3x_code_ring_write(const int32_t* codes, long ld_codes, int32_t* ring, int32_t* head, int depth, int seats, int nq,
+                        int B, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* M3X_H */

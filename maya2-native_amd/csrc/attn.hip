@@ -1,0 +1,336 @@
+// Attention kernels.
+//
+// decode_attn: GQA decode attention over the static KV cache, in place (serve/fast_backbone.py:31-58, launcher
+// :242-247). Cache layout [slots, kv_heads, cap, D] bf16 (serve/fast_backbone.py:146-148). Row r attends keys
+// 0..pos[r] of slot slots[r]; scale = D^-1/2; online softmax in fp32; output bf16.
+//
+// Mapping: one workgroup = (split c, row r, kv head kh) and handles the G query heads that share kh, so each K/V
+// byte of a (row, kv head) is read once. The keys of a row are cut into splits of `chunk` keys (a multiple of
+// 128); each of the 4 waves takes every 4th 32-key tile of its split. Per tile:
+//   QK: S^T[key][head] = K[key][:] . Q^T  -> 2 x 4 MFMA 16x16x32 (K is the A operand, loaded straight from the
+//       cache: lane l reads 16 contiguous bytes of key row l%16).
+//   PV: O[head][dim] += P[head][key] . V[key][dim] -> 8 MFMAs. The P operand is exactly the S^T accumulator a
+//       lane already holds (keys 4g..4g+3 of both 16-key halves); the V operand needs 8 keys of one dim per lane,
+//       so a lane loads 8 full 16-byte key-row pieces and transposes 8x8 bf16 in registers (V stays out of LDS).
+//       Output tile T holds dims {8c+T : c = 0..15}.
+// The 4 waves merge through LDS; a split that is not the whole row writes (m, l, acc) partials and
+// decode_attn_combine folds them in split order (deterministic).
+#include "m3x_common.h"
+
+namespace {
+constexpr int AD = 128;       // head dim of the decode kernel
+constexpr int PART_STRIDE = 264;  // floats per (row, kv head, split) partial: m[2] l[2] pad[4] o[2][128]
+}
+
+template <int G>
+__global__ __launch_bounds__(256) void decode_attn_kernel(
+    const uint16_t* __restrict__ q, long sq_b, long sq_h, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, long sk_s, long sk_h, long sk_t, uint16_t* __restrict__ out, long so_b,
+    long so_h, const int64_t* __restrict__ slots, const int32_t* __restrict__ pos, float scale_log2, int chunk,
+    float* __restrict__ part, int max_splits, int cap) {
+  const int split = blockIdx.x;
+  const int row = blockIdx.y;
+  const int kh = blockIdx.z;
+  const int KV = gridDim.z;
+  const int ps = min(pos[row], cap - 1);  // the host guarantees pos < cap; the clamp keeps every access in the slot
+  const int kstart = split * chunk;
+  if (kstart > ps) return;  // this split is past the row's context (uniform per block)
+  const int kend = min(kstart + chunk, ps + 1);
+  const int nsplit = min((ps + chunk) / chunk, max_splits);  // ceil((ps + 1) / chunk)
+
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int li = lane & 15;  // MFMA row/col index
+  const int lg = lane >> 4;  // MFMA k group
+
+  const long slot = slots[row];
+  const uint16_t* kbase = kc + slot * sk_s + (long)kh * sk_h;
+  const uint16_t* vbase = vc + slot * sk_s + (long)kh * sk_h;
+
+  // Q^T operand: lane holds q[head li][32kk + 8lg .. +8] for li < G, zero otherwise.
+  u16x8 qop[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    if (li < G) {
+      qop[kk] = ld16(q + (long)row * sq_b + (long)(kh * G + li) * sq_h + 32 * kk + 8 * lg);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qop[kk].v[e] = 0;
+    }
+  }
+
+  float m_run = -INFINITY, l_run = 0.f;  // per head li (meaningful for li < G), equal across lanes of one li
+  f32x4_t acc[8];
+#pragma unroll
+  for (int T = 0; T < 8; ++T) acc[T] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int k0 = kstart + 32 * wave; k0 < kend; k0 += 128) {
+    // ---- loads: K rows k0 + 16*g2 + li (A operand), V rows key(lg, e) = k0 + 16*(e/4) + 4*lg + e%4
+    u16x8 kop[2][4];
+#pragma unroll
+    for (int g2 = 0; g2 < 2; ++g2) {
+      const uint16_t* kr = kbase + (long)(k0 + 16 * g2 + li) * sk_t + 8 * lg;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) kop[g2][kk] = ld16(kr + 32 * kk);
+    }
+    u16x8 vld[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vld[e] = ld16(vbase + (long)(k0 + 16 * (e >> 2) + 4 * lg + (e & 3)) * sk_t + 8 * li);
+
+    // ---- scores S^T[key][head]: lane holds keys k0 + 16*g2 + 4*lg + r for head li
+    f32x4_t s[2];
+#pragma unroll
+    for (int g2 = 0; g2 < 2; ++g2) {
+      s[g2] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) s[g2] = mfma16x16x32<M3X_BF16>(kop[g2][kk], qop[kk], s[g2]);
+    }
+    const bool tail = k0 + 32 > kend;
+    float sv[8];
+#pragma unroll
+    for (int g2 = 0; g2 < 2; ++g2)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = k0 + 16 * g2 + 4 * lg + r;
+        const float x = s[g2][r] * scale_log2;
+        sv[4 * g2 + r] = (tail && key >= kend) ? -INFINITY : x;
+      }
+    float tmax = sv[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) tmax = fmaxf(tmax, sv[e]);
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float m_new = fmaxf(m_run, tmax);
+    const float alpha = exp2f(m_run - m_new);
+    float p[8], psum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      p[e] = (li < G) ? exp2f(sv[e] - m_new) : 0.f;
+      psum += p[e];
+    }
+    psum += __shfl_xor(psum, 16, 64);
+    psum += __shfl_xor(psum, 32, 64);
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+
+    // ---- rescale the accumulator rows (heads 0..G-1 live in lanes 0..15, register = head)
+    float al[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) al[h] = __shfl(alpha, h, 64);
+#pragma unroll
+    for (int T = 0; T < 8; ++T)
+#pragma unroll
+      for (int h = 0; h < G; ++h) acc[T][h] *= al[h];
+
+    // ---- P operand (bf16): element e = 4*g2 + r is key k0 + 16*g2 + 4*lg + r
+    u16x8 pop;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pop.v[e] = f2bf(p[e]);
+
+    // ---- V operand: zero keys past the context in the tail tile (stale cache rows may hold anything)
+    if (tail) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int key = k0 + 16 * (e >> 2) + 4 * lg + (e & 3);
+        if (key >= kend) {
+#pragma unroll
+          for (int x = 0; x < 8; ++x) vld[e].v[x] = 0;
+        }
+      }
+    }
+#pragma unroll
+    for (int T = 0; T < 8; ++T) {
+      u16x8 vop;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vop.v[e] = vld[e].v[T];
+      acc[T] = mfma16x16x32<M3X_BF16>(pop, vop, acc[T]);
+    }
+  }
+
+  // ---- merge the 4 waves: lds_o[wave][h][dim], lds_ml[wave][h] = (m, l)
+  __shared__ float lds_o[4][G][AD];
+  __shared__ float lds_m[4][G], lds_l[4][G];
+  if (lane < 16) {
+#pragma unroll
+    for (int T = 0; T < 8; ++T)
+#pragma unroll
+      for (int h = 0; h < G; ++h) lds_o[wave][h][8 * lane + T] = acc[T][h];
+  }
+  if (lane < G) {
+    lds_m[wave][lane] = m_run;
+    lds_l[wave][lane] = l_run;
+  }
+  __syncthreads();
+  if (threadIdx.x >= G * AD) return;
+  const int h = threadIdx.x / AD;
+  const int d = threadIdx.x % AD;
+  float M = lds_m[0][h];
+#pragma unroll
+  for (int w = 1; w < 4; ++w) M = fmaxf(M, lds_m[w][h]);
+  float L = 0.f, O = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float f = exp2f(lds_m[w][h] - M);  // 0 for a wave that saw no tile (m = -inf)
+    L += lds_l[w][h] * f;
+    O += lds_o[w][h][d] * f;
+  }
+  if (nsplit == 1) {
+    out[(long)row * so_b + (long)(kh * G + h) * so_h + d] = f2bf(O / L);
+  } else {
+    float* pp = part + (((long)row * KV + kh) * max_splits + split) * PART_STRIDE;
+    if (d == 0) {
+      pp[h] = M;
+      pp[2 + h] = L;
+    }
+    pp[8 + h * AD + d] = O;
+  }
+}
+
+template <int G>
+__global__ __launch_bounds__(256) void decode_attn_combine_kernel(uint16_t* __restrict__ out, long so_b, long so_h,
+                                                                  const int32_t* __restrict__ pos, int chunk,
+                                                                  const float* __restrict__ part, int max_splits,
+                                                                  int cap) {
+  const int row = blockIdx.x;
+  const int kh = blockIdx.y;
+  const int KV = gridDim.y;
+  const int nsplit = min((min(pos[row], cap - 1) + chunk) / chunk, max_splits);
+  if (nsplit <= 1 || threadIdx.x >= G * AD) return;
+  const int h = threadIdx.x / AD;
+  const int d = threadIdx.x % AD;
+  const float* pp = part + ((long)row * KV + kh) * max_splits * PART_STRIDE;
+  float M = -INFINITY;
+  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, pp[s * PART_STRIDE + h]);
+  float L = 0.f, O = 0.f;
+  for (int s = 0; s < nsplit; ++s) {
+    const float f = exp2f(pp[s * PART_STRIDE + h] - M);
+    L += pp[s * PART_STRIDE + 2 + h] * f;
+    O += pp[s * PART_STRIDE + 8 + h * AD + d] * f;
+  }
+  out[(long)row * so_b + (long)(kh * G + h) * so_h + d] = f2bf(O / L);
+}
+
+M3X_API size_t m3x_decode_attn_workspace(int rows, int kv_heads, int max_ctx, int chunk) {
+  if (rows <= 0 || kv_heads <= 0 || max_ctx <= 0 || chunk <= 0) return 0;
+  const long splits = (max_ctx + chunk - 1) / chunk;
+  return (size_t)rows * kv_heads * splits * PART_STRIDE * sizeof(float);
+}
+
+// max_ctx: an upper bound on pos[r] + 1 for every row (the caller's context bucket); it sizes the grid.
+// chunk: keys per split, a multiple of 128. cap (the cache's per-slot capacity) must be a multiple of 32 so the
+// last 32-key tile of a row stays inside its slot.
+M3X_API int m3x_decode_attn(const void* q, long sq_b, long sq_h, const void* k_cache, const void* v_cache, long sk_s,
+                            long sk_h, long sk_t, int cap, void* out, long so_b, long so_h, const int64_t* slots,
+                            const int32_t* pos, float scale, int rows, int heads, int kv_heads, int head_dim,
+                            int max_ctx, int chunk, void* workspace, size_t ws_bytes, void* stream) {
+  if (rows < 0 || heads <= 0 || kv_heads <= 0 || max_ctx <= 0) return M3X_EINVAL;
+  if (rows == 0) return M3X_OK;
+  if (!q || !k_cache || !v_cache || !out || !slots || !pos) return M3X_ENULL;
+  if (head_dim != AD || heads % kv_heads) return M3X_EUNSUPPORTED;
+  const int G = heads / kv_heads;
+  if (G != 1 && G != 2) return M3X_EUNSUPPORTED;
+  if (chunk <= 0 || chunk % 128 || cap % 32 || max_ctx > cap) return M3X_EINVAL;
+  if ((sq_b | sq_h | sk_s | sk_h | sk_t) & 7) return M3X_EINVAL;
+  if (!m3x_aligned16(q) || !m3x_aligned16(k_cache) || !m3x_aligned16(v_cache)) return M3X_EINVAL;
+  const int max_splits = (max_ctx + chunk - 1) / chunk;
+  if (max_splits > 1) {
+    if (!workspace) return M3X_ENULL;
+    if (ws_bytes < m3x_decode_attn_workspace(rows, kv_heads, max_ctx, chunk)) return M3X_EWORKSPACE;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  const float scale_log2 = scale * 1.44269504088896341f;
+  dim3 grid(max_splits, rows, kv_heads);
+  if (G == 2) {
+    hipLaunchKernelGGL(decode_attn_kernel<2>, grid, dim3(256), 0, st, (const uint16_t*)q, sq_b, sq_h,
+                       (const uint16_t*)k_cache, (const uint16_t*)v_cache, sk_s, sk_h, sk_t, (uint16_t*)out, so_b, so_h,
+                       slots, pos, scale_log2, chunk, (float*)workspace, max_splits, cap);
+    if (max_splits > 1)
+      hipLaunchKernelGGL(decode_attn_combine_kernel<2>, dim3(rows, kv_heads), dim3(256), 0, st, (uint16_t*)out, so_b,
+                         so_h, pos, chunk, (const float*)workspace, max_splits, cap);
+  } else {
+    hipLaunchKernelGGL(decode_attn_kernel<1>, grid, dim3(256), 0, st, (const uint16_t*)q, sq_b, sq_h,
+                       (const uint16_t*)k_cache, (const uint16_t*)v_cache, sk_s, sk_h, sk_t, (uint16_t*)out, so_b, so_h,
+                       slots, pos, scale_log2, chunk, (float*)workspace, max_splits, cap);
+    if (max_splits > 1)
+      hipLaunchKernelGGL(decode_attn_combine_kernel<1>, dim3(rows, kv_heads), dim3(256), 0, st, (uint16_t*)out, so_b,
+                         so_h, pos, chunk, (const float*)workspace, max_splits, cap);
+  }
+  M3X_CHECK_LAUNCH();
+  return M3X_OK;
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// Depth-transformer self-attention over one frame's positions (serve/fast_depth.py:102-121, SDPA causal at a
+// group start, incremental over the within-group KV otherwise).
+// qkv rows (b, t) at positions p0 + t, read at qkv + b*sqb + t*sqt, laid out q | k | v with heads inside
+// (view(B,T,3,H,hd)). kd/vd: per-frame scratch [B, H, np, hd]. If write_kv, the T new K/V rows are stored at
+// positions p0..p0+T-1. Queries t in [tq0, T) attend keys 0..p0+t; output row (b, t - tq0) at out + b*sob + tq*sot.
+// One workgroup (64 threads) per (b, head); hd <= 128, np <= 64.
+template <int DT>
+__global__ __launch_bounds__(64) void depth_attn_kernel(const uint16_t* __restrict__ qkv, long sqb, long sqt,
+                                                        uint16_t* kd, uint16_t* vd, uint16_t* __restrict__ out,
+                                                        long sob, long sot, int T, int p0, int tq0, int H, int hd,
+                                                        int np, float scale, int write_kv) {
+  const int b = blockIdx.x;
+  const int h = blockIdx.y;
+  const int lane = threadIdx.x;
+  uint16_t* kb = kd + ((long)b * H + h) * np * hd;
+  uint16_t* vb = vd + ((long)b * H + h) * np * hd;
+  if (write_kv) {
+    for (int t = 0; t < T; ++t) {
+      const uint16_t* src = qkv + (long)b * sqb + (long)t * sqt;
+      for (int d = lane; d < hd; d += 64) {
+        kb[(long)(p0 + t) * hd + d] = src[(long)H * hd + h * hd + d];
+        vb[(long)(p0 + t) * hd + d] = src[2L * H * hd + h * hd + d];
+      }
+    }
+    __syncthreads();
+  }
+  __shared__ float qs[128];
+  __shared__ float ps[64];
+  for (int t = tq0; t < T; ++t) {
+    const int nk = p0 + t + 1;
+    const uint16_t* src = qkv + (long)b * sqb + (long)t * sqt + (long)h * hd;
+    for (int d = lane; d < hd; d += 64) qs[d] = E<DT>::to_f(src[d]);
+    __syncthreads();
+    float sc = -INFINITY;
+    if (lane < nk) {
+      const uint16_t* kr = kb + (long)lane * hd;
+      float a = 0.f;
+      for (int d = 0; d < hd; ++d) a = fmaf(qs[d], E<DT>::to_f(kr[d]), a);
+      sc = a * scale;
+    }
+    const float m = wave_max_xor(sc, 64);
+    const float pe = lane < nk ? expf(sc - m) : 0.f;
+    const float l = wave_sum_xor(pe, 64);
+    ps[lane] = pe;
+    __syncthreads();
+    uint16_t* o = out + (long)b * sob + (long)(t - tq0) * sot + (long)h * hd;
+    for (int d = lane; d < hd; d += 64) {
+      float a = 0.f;
+      for (int j = 0; j < nk; ++j) a = fmaf(ps[j], E<DT>::to_f(vb[(long)j * hd + d]), a);
+      o[d] = E<DT>::from_f(a / l);
+    }
+    __syncthreads();
+  }
+}
+
+M3X_API int m3x_depth_attn(const void* qkv, long sqb, long sqt, void* kd, void* vd, void* out, long sob, long sot,
+                           int B, int T, int p0, int tq0, int heads, int head_dim, int np, float scale, int write_kv,
+                           int dtype, void* stream) {
+  if (B < 0 || T <= 0 || p0 < 0 || tq0 < 0 || tq0 >= T || heads <= 0) return M3X_EINVAL;
+  if (B == 0) return M3X_OK;
+  if (!qkv || !kd || !vd || !out) return M3X_ENULL;
+  if (head_dim <= 0 || head_dim > 128 || p0 + T > np || np > 64) return M3X_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+#define M3X_DA(DTT)                                                                                                 \
+  hipLaunchKernelGGL(depth_attn_kernel<DTT>, dim3(B, heads), dim3(64), 0, st, (const uint16_t*)qkv, sqb, sqt,      \
+                     (uint16_t*)kd, (uint16_t*)vd, (uint16_t*)out, sob, sot, T, p0, tq0, heads, head_dim, np, scale, \
+                     write_kv)
+  if (dtype == M3X_BF16) M3X_DA(M3X_BF16);
+  else if (dtype == M3X_F16) M3X_DA(M3X_F16);
+  else return M3X_EUNSUPPORTED;
+#undef M3X_DA
+  M3X_CHECK_LAUNCH();
+  return M3X_OK;
+}

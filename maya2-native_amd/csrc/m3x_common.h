@@ -1,0 +1,122 @@
+// Shared device helpers for the m3x kernels (gfx950 / CDNA4, wave64).
+//
+// Everything here is compiled with -ffp-contract=off: a float expression means exactly the IEEE operations
+// written, so the kernels that must be bit-exact against the CPU restatement (add+RMSNorm, q/k-norm+RoPE,
+// the samplers) can spell their rounding order out. Fused multiply-adds are written as fmaf() where wanted.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define M3X_API extern "C" __attribute__((visibility("default")))
+
+// Status codes returned by every entry point (0 = launched).
+enum {
+  M3X_OK = 0,
+  M3X_EINVAL = -1,      // bad shape, stride, size or alignment
+  M3X_ENULL = -2,       // a required pointer is null
+  M3X_EWORKSPACE = -3,  // workspace too small
+  M3X_ELAUNCH = -4,     // hipGetLastError() reported a launch failure
+  M3X_EUNSUPPORTED = -5 // a shape/dtype combination no kernel here implements
+};
+
+enum { M3X_BF16 = 0, M3X_F16 = 1, M3X_F32 = 2 };
+
+#define M3X_CHECK_LAUNCH()                                  \
+  do {                                                      \
+    if (hipGetLastError() != hipSuccess) return M3X_ELAUNCH; \
+  } while (0)
+
+// ------------------------------------------------------------------ 16-bit float storage
+// Storage is uint16_t for both bf16 and fp16; the conversions below are the only way values enter or
+// leave fp32, so both the kernels and the C oracle round identically (round-to-nearest-even).
+__device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
+
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+// Element-type traits: DT = M3X_BF16 or M3X_F16.
+template <int DT> struct E;
+template <> struct E<M3X_BF16> {
+  static __device__ __forceinline__ float to_f(uint16_t v) { return bf2f(v); }
+  static __device__ __forceinline__ uint16_t from_f(float f) { return f2bf(f); }
+};
+template <> struct E<M3X_F16> {
+  static __device__ __forceinline__ float to_f(uint16_t v) { return h2f(v); }
+  static __device__ __forceinline__ uint16_t from_f(float f) { return f2h(f); }
+};
+
+// round a float through the storage type
+template <int DT> __device__ __forceinline__ float rnd(float f) { return E<DT>::to_f(E<DT>::from_f(f)); }
+
+// ------------------------------------------------------------------ 16-byte vectors
+struct __align__(16) u16x8 { uint16_t v[8]; };
+__device__ __forceinline__ u16x8 ld16(const uint16_t* p) {
+  uint4 r = *reinterpret_cast<const uint4*>(p);
+  return __builtin_bit_cast(u16x8, r);
+}
+__device__ __forceinline__ void st16(uint16_t* p, const u16x8& x) {
+  *reinterpret_cast<uint4*>(p) = __builtin_bit_cast(uint4, x);
+}
+
+// ------------------------------------------------------------------ exp for the samplers
+// Cody-Waite argument reduction (W. J. Cody and W. Waite, "Software Manual for the Elementary Functions",
+// 1980): x = n*ln2 + r with ln2 split into a 16-bit-exact high part and a low part, |r| <= ln2/2, then a
+// degree-7 Taylor polynomial for e^r by Horner's rule with fused multiply-adds, scaled by 2^n.
+// Only called with x <= 0 (a logit minus the row maximum); x < -87 returns 0 so the result is never a
+// subnormal (the weight of such a candidate is below 2^-125 of the top one). The C oracle carries the same
+// function; both compile with contraction off, so they agree bit for bit.
+__device__ __forceinline__ float m3x_expf(float x) {
+  if (x < -87.0f) return 0.0f;
+  const float L2E = 1.44269504088896341f;
+  const float LN2_HI = 0.693145751953125f;         // 0x3f317200: 15 significant bits, n*LN2_HI exact for |n| < 512
+  const float LN2_LO = 1.42860682030941723212e-6f; // ln2 - LN2_HI
+  float n = rintf(x * L2E);
+  float r = fmaf(-n, LN2_HI, x);
+  r = fmaf(-n, LN2_LO, r);
+  float p = 1.98412698412698413e-4f;  // 1/7!
+  p = fmaf(p, r, 1.38888888888888889e-3f);  // 1/6!
+  p = fmaf(p, r, 8.33333333333333333e-3f);  // 1/5!
+  p = fmaf(p, r, 4.16666666666666667e-2f);  // 1/4!
+  p = fmaf(p, r, 1.66666666666666667e-1f);  // 1/3!
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  return ldexpf(p, (int)n);
+}
+
+// ------------------------------------------------------------------ wave reductions (wave64)
+__device__ __forceinline__ float wave_sum_xor(float v, int width) {
+  for (int s = width >> 1; s > 0; s >>= 1) v = v + __shfl_xor(v, s, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max_xor(float v, int width) {
+  for (int s = width >> 1; s > 0; s >>= 1) v = fmaxf(v, __shfl_xor(v, s, 64));
+  return v;
+}
+
+// ------------------------------------------------------------------ MFMA (gfx950)
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// v_mfma_f32_16x16x32_{bf16,f16}: A is 16x32, B is 32x16, D is 16x16 fp32.
+// Lane l holds A[l%16][8*(l/16)+e] and B[8*(l/16)+e][l%16] for e = 0..7, and D[4*(l/16)+r][l%16] for r = 0..3.
+template <int DT> __device__ __forceinline__ f32x4_t mfma16x16x32(const u16x8& a, const u16x8& b, f32x4_t c);
+template <> __device__ __forceinline__ f32x4_t mfma16x16x32<M3X_BF16>(const u16x8& a, const u16x8& b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                 0, 0, 0);
+}
+template <> __device__ __forceinline__ f32x4_t mfma16x16x32<M3X_F16>(const u16x8& a, const u16x8& b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                0, 0, 0);
+}
+
+static inline int m3x_ceil_div(long a, long b) { return (int)((a + b - 1) / b); }
+static inline bool m3x_aligned16(const void* p) { return (((uintptr_t)p) & 15u) == 0; }

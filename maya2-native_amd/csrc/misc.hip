@@ -1,0 +1,123 @@
+// Small index kernels of the frame step: per-row positions, lengths update, row gathers/scatters, the frame's
+// code ring and per-slot counters. All integer work, exact by construction.
+#include "m3x_common.h"
+
+// pos[r] = lengths[slots[r]] + offset[r]   (serve/fast_backbone.py:178-179; offset null = 0)
+__global__ void positions_kernel(const int64_t* __restrict__ lengths, const int64_t* __restrict__ slots,
+                                 const int64_t* __restrict__ offset, int32_t* __restrict__ pos, int R) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= R) return;
+  pos[r] = (int32_t)(lengths[slots[r]] + (offset ? offset[r] : 0));
+}
+
+M3X_API int m3x_positions(const int64_t* lengths, const int64_t* slots, const int64_t* offset, int32_t* pos, int R,
+                          void* stream) {
+  if (R < 0) return M3X_EINVAL;
+  if (R == 0) return M3X_OK;
+  if (!lengths || !slots || !pos) return M3X_ENULL;
+  hipLaunchKernelGGL(positions_kernel, dim3(m3x_ceil_div(R, 256)), dim3(256), 0, (hipStream_t)stream, lengths, slots,
+                     offset, pos, R);
+  M3X_CHECK_LAUNCH();
+  return M3X_OK;
+}
+
+// lengths[slots[r]] += real[r] for every row (duplicates accumulate, like index_add_; serve/fast_backbone.py:233)
+__global__ void lengths_add_kernel(int64_t* lengths, const int64_t* __restrict__ slots,
+                                   const int64_t* __restrict__ real, int R) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= R) return;
+  const int64_t v = real[r];
+  if (v) atomicAdd((unsigned long long*)&lengths[slots[r]], (unsigned long long)v);
+}
+
+M3X_API int m3x_lengths_add(int64_t* lengths, const int64_t* slots, const int64_t* real, int R, void* stream) {
+  if (R < 0) return M3X_EINVAL;
+  if (R == 0) return M3X_OK;
+  if (!lengths || !slots || !real) return M3X_ENULL;
+  hipLaunchKernelGGL(lengths_add_kernel, dim3(m3x_ceil_div(R, 256)), dim3(256), 0, (hipStream_t)stream, lengths, slots,
+                     real, R);
+  M3X_CHECK_LAUNCH();
+  return M3X_OK;
+}
+
+// dst[dst_idx[r] or r][:] = src[src_idx[r] + src_off or r][:], rows of n 16-bit elements (n % 8 == 0).
+// Indices are int64 (idx_i32 = 0) or int32 (idx_i32 = 1) with element stride ld_idx; src indices are clamped to
+// [0, src_rows) so an out-of-range code cannot read outside the table (the reference raises on the host instead,
+// tts/model/audio_io.py:30-32; the host surfaces validate before the step).
+// Used for: prefix rows = embed[level][code] (serve/fast_depth.py:135,196), x = feedback[slots], feedback[slots] = y.
+__global__ void copy_rows_kernel(const uint16_t* __restrict__ src, long ld_src, const void* src_idx, long src_off,
+                                 long src_rows, uint16_t* __restrict__ dst, long ld_dst, const int64_t* dst_idx,
+                                 int rows, int nvec, int idx_i32, long ld_idx) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long)rows * nvec) return;
+  const int r = (int)(i / nvec), v = (int)(i % nvec);
+  long sr = r;
+  if (src_idx) {
+    sr = (idx_i32 ? (long)((const int32_t*)src_idx)[(long)r * ld_idx] : ((const int64_t*)src_idx)[(long)r * ld_idx]) +
+         src_off;
+    sr = sr < 0 ? 0 : (sr >= src_rows ? src_rows - 1 : sr);
+  }
+  const long dr = dst_idx ? dst_idx[r] : r;
+  st16(dst + dr * ld_dst + 8 * v, ld16(src + sr * ld_src + 8 * v));
+}
+
+M3X_API int m3x_copy_rows(const void* src, long ld_src, const void* src_idx, long src_off, long src_rows, void* dst,
+                          long ld_dst, const int64_t* dst_idx, int rows, int n, int idx_i32, long ld_idx,
+                          void* stream) {
+  if (rows < 0 || n <= 0 || (n & 7) || (ld_src & 7) || (ld_dst & 7)) return M3X_EINVAL;
+  if (rows == 0) return M3X_OK;
+  if (!src || !dst) return M3X_ENULL;
+  if (src_idx && src_rows <= 0) return M3X_EINVAL;
+  if (!m3x_aligned16(src) || !m3x_aligned16(dst)) return M3X_EINVAL;
+  const long total = (long)rows * (n / 8);
+  hipLaunchKernelGGL(copy_rows_kernel, dim3(m3x_ceil_div(total, 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)src, ld_src, src_idx, src_off, src_rows, (uint16_t*)dst, ld_dst, dst_idx, rows,
+                     n / 8, idx_i32, ld_idx);
+  M3X_CHECK_LAUNCH();
+  return M3X_OK;
+}
+
+// Frame code ring: ring[(*head) % depth][b][0..nq) = codes[b][0..nq) for b < B, then *head += 1.
+// One workgroup, so the head update is ordered after every copy of this launch.
+__global__ __launch_bounds__(256) void code_ring_kernel(const int32_t* __restrict__ codes, long ld_codes,
+                                                        int32_t* __restrict__ ring, int32_t* head, int depth,
+                                                        int seats, int nq, int B) {
+  const int h = *head;
+  const int slotr = ((h % depth) + depth) % depth;
+  int32_t* dst = ring + (long)slotr * seats * nq;
+  for (int i = threadIdx.x; i < B * nq; i += blockDim.x) {
+    const int b = i / nq, j = i % nq;
+    dst[(long)b * nq + j] = codes[(long)b * ld_codes + j];
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) *head = h + 1;
+}
+
+M3X_API int m3x_code_ring_write(const int32_t* codes, long ld_codes, int32_t* ring, int32_t* head, int depth,
+                                int seats, int nq, int B, void* stream) {
+  if (B < 0 || depth <= 0 || nq <= 0 || B > seats || ld_codes < nq) return M3X_EINVAL;
+  if (B == 0) return M3X_OK;
+  if (!codes || !ring || !head) return M3X_ENULL;
+  hipLaunchKernelGGL(code_ring_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, codes, ld_codes, ring, head, depth,
+                     seats, nq, B);
+  M3X_CHECK_LAUNCH();
+  return M3X_OK;
+}
+
+// ctr[slots[b]] += 1 (serve/fast_depth.py:199, row_ctr.index_add_)
+__global__ void ctr_add_kernel(int32_t* ctr, const int64_t* __restrict__ slots, int B) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b < B) atomicAdd(&ctr[slots[b]], 1);
+}
+
+M3X_API int m3x_ctr_add(int32_t* ctr, const int64_t* slots, int B, void* stream) {
+  if (B < 0) return M3X_EINVAL;
+  if (B == 0) return M3X_OK;
+  if (!ctr || !slots) return M3X_ENULL;
+  hipLaunchKernelGGL(ctr_add_kernel, dim3(m3x_ceil_div(B, 256)), dim3(256), 0, (hipStream_t)stream, ctr, slots, B);
+  M3X_CHECK_LAUNCH();
+  return M3X_OK;
+}
+
+// The library's version, so a host binding can check it loaded the build it expects.
+M3X_API int m3x_version(void) { return 1; }

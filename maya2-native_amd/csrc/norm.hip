@@ -1,0 +1,423 @@
+// Row-normalisation kernels of the frame step.
+//
+// Reduction order (the one the C oracle restates; bit-exactness depends on it): a row of N elements is read
+// as N/8 groups of 8 contiguous elements, one group per thread. A thread sums its 8 squares left to right
+// (each product and each sum rounded to fp32), then the N/8 partials are folded in half repeatedly:
+// p[g] = p[g] + p[g + s] for s = N/16, N/32, ..., 1. Within a wave the fold is an xor butterfly, which gives
+// lane g < s exactly p[g] + p[g + s].
+#include "m3x_common.h"
+
+// ---------------------------------------------------------------------------------------------------------
+// fold-in-half tree over TPR threads per row; rows are packed 256/TPR per block. Returns the row total in
+// every thread of the row.
+template <int TPR>
+__device__ __forceinline__ float row_tree_sum(float p, float* red, float* bcast) {
+  const int t = threadIdx.x % TPR;
+  const int rb = threadIdx.x / TPR;
+  if constexpr (TPR > 64) {
+    red[threadIdx.x] = p;
+    __syncthreads();
+#pragma unroll
+    for (int s = TPR / 2; s >= 64; s >>= 1) {
+      if (t < s) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + s];
+      __syncthreads();
+    }
+    p = red[threadIdx.x];
+  }
+  constexpr int W = TPR < 64 ? TPR : 64;
+#pragma unroll
+  for (int s = W / 2; s > 0; s >>= 1) p = p + __shfl_xor(p, s, 64);
+  if (t == 0) bcast[rb] = p;
+  __syncthreads();
+  float r = bcast[rb];
+  __syncthreads();
+  return r;
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// K3: h' = bf16(h + a); y = bf16(bf16(h' * (1/sqrt(mean(h'^2) + eps))) * w).  a == nullptr: plain RMSNorm of h.
+// serve/fast_backbone.py:95-104 (_add_rms) and HF Qwen3RMSNorm for the layer-0 input norm (:190).
+template <int TPR>
+__global__ __launch_bounds__(256) void add_rms_kernel(const uint16_t* __restrict__ h, long s_h,
+                                                      const uint16_t* __restrict__ a, long s_a, uint16_t* ho,
+                                                      long s_ho, uint16_t* __restrict__ y, long s_y,
+                                                      const uint16_t* __restrict__ w, float eps, int rows) {
+  constexpr int N = TPR * 8;
+  constexpr int RPB = 256 / TPR;
+  __shared__ float red[TPR > 64 ? 256 : 1];
+  __shared__ float bcast[RPB];
+  const int t = threadIdx.x % TPR;
+  const int row = blockIdx.x * RPB + threadIdx.x / TPR;
+  const bool active = row < rows;
+  float x[8];
+  float p = 0.f;
+  if (active) {
+    u16x8 hv = ld16(h + (long)row * s_h + 8 * t);
+    if (a) {
+      u16x8 av = ld16(a + (long)row * s_a + 8 * t);
+      u16x8 sv;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sv.v[e] = f2bf(bf2f(hv.v[e]) + bf2f(av.v[e]));
+      if (ho) st16(ho + (long)row * s_ho + 8 * t, sv);
+      hv = sv;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = bf2f(hv.v[e]);
+    p = x[0] * x[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) p = p + x[e] * x[e];
+  }
+  float ss = row_tree_sum<TPR>(p, red, bcast);
+  if (!active) return;
+  const float inv = 1.0f / sqrtf(ss / (float)N + eps);
+  u16x8 wv = ld16(w + 8 * t), yv;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) yv.v[e] = f2bf(bf2f(f2bf(x[e] * inv)) * bf2f(wv.v[e]));
+  st16(y + (long)row * s_y + 8 * t, yv);
+}
+
+M3X_API int m3x_add_rms(const void* h, long s_h, const void* a, long s_a, void* h_out, long s_ho, void* y, long s_y,
+                        const void* w, float eps, int rows, int n, void* stream) {
+  if (rows < 0) return M3X_EINVAL;
+  if (rows == 0) return M3X_OK;
+  if (!h || !y || !w) return M3X_ENULL;
+  if ((s_h | s_y | (a ? s_a : 0) | (h_out ? s_ho : 0)) & 7) return M3X_EINVAL;
+  if (!m3x_aligned16(h) || !m3x_aligned16(y) || !m3x_aligned16(w) || (a && !m3x_aligned16(a)) ||
+      (h_out && !m3x_aligned16(h_out)))
+    return M3X_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+  const uint16_t *H = (const uint16_t*)h, *A = (const uint16_t*)a, *Wt = (const uint16_t*)w;
+  uint16_t *HO = (uint16_t*)h_out, *Y = (uint16_t*)y;
+  switch (n) {
+#define M3X_ADD_RMS_CASE(NN)                                                                                   \
+  case NN: {                                                                                                   \
+    constexpr int TPR = NN / 8;                                                                                \
+    hipLaunchKernelGGL(add_rms_kernel<TPR>, dim3(m3x_ceil_div(rows, 256 / TPR)), dim3(256), 0, st, H, s_h, A, \
+                       s_a, HO, s_ho, Y, s_y, Wt, eps, rows);                                                  \
+    break;                                                                                                     \
+  }
+    M3X_ADD_RMS_CASE(512)
+    M3X_ADD_RMS_CASE(1024)
+    M3X_ADD_RMS_CASE(2048)
+#undef M3X_ADD_RMS_CASE
+    default:
+      return M3X_EUNSUPPORTED;
+  }
+  M3X_CHECK_LAUNCH();
+  return M3X_OK;
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// K2: per-head q/k RMSNorm + RoPE, query heads to q_out, key heads into the static cache at [slot, kh, pos],
+// value heads copied verbatim. serve/fast_backbone.py:61-92 (_qk_norm_rope_cache), rounding points :77-81.
+// One item = (row, j) with j < H a query head and H <= j < H+KV a key head; D/8 threads per item.
+//   y = bf16(bf16(x*inv) * w);  first half:  o = y*c - y'*s;  second half: o = y*c + y'*s  (y' = rotate partner)
+template <int D>
+__global__ __launch_bounds__(256) void qk_norm_rope_cache_kernel(
+    const uint16_t* __restrict__ qkv, long s_qkv, uint16_t* __restrict__ qo, long s_qo_b, long s_qo_h,
+    uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, long sk_s, long sk_h, long sk_t,
+    const int64_t* __restrict__ slots, const int32_t* __restrict__ pos, const uint16_t* __restrict__ cosb,
+    const uint16_t* __restrict__ sinb, long s_cos, const uint16_t* __restrict__ wq, const uint16_t* __restrict__ wk,
+    float eps, int rows, int H, int KV, int cap) {
+  constexpr int TPI = D / 8;  // threads per item
+  constexpr int IPB = 256 / TPI;
+  const int t = threadIdx.x % TPI;
+  const long item = (long)blockIdx.x * IPB + threadIdx.x / TPI;
+  const int NH = H + KV;
+  const int row = (int)(item / NH);
+  const int j = (int)(item % NH);
+  const bool active = row < rows;
+  float x[8], yv[8];
+  float p = 0.f;
+  int ps = 0;
+  if (active) {
+    ps = min(pos[row], cap - 1);  // the host guarantees pos < cap; the clamp keeps the cache write in the slot
+    u16x8 xv = ld16(qkv + (long)row * s_qkv + (long)j * D + 8 * t);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = bf2f(xv.v[e]);
+    p = x[0] * x[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) p = p + x[e] * x[e];
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = 0.f;
+  }
+#pragma unroll
+  for (int s = TPI / 2; s > 0; s >>= 1) p = p + __shfl_xor(p, s, 64);
+  const float inv = 1.0f / sqrtf(p / (float)D + eps);
+  if (active) {
+    u16x8 wv = ld16((j < H ? wq : wk) + 8 * t);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) yv[e] = bf2f(f2bf(bf2f(f2bf(x[e] * inv)) * bf2f(wv.v[e])));
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) yv[e] = 0.f;
+  }
+  float yp[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) yp[e] = __shfl_xor(yv[e], TPI / 2, 64);
+  if (!active) return;
+  u16x8 cv = ld16(cosb + (long)ps * s_cos + 8 * t);
+  u16x8 sv = ld16(sinb + (long)ps * s_cos + 8 * t);
+  const bool first = t < TPI / 2;
+  u16x8 ov;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float a1 = yv[e] * bf2f(cv.v[e]);
+    float a2 = yp[e] * bf2f(sv.v[e]);
+    ov.v[e] = f2bf(first ? a1 - a2 : a1 + a2);
+  }
+  if (j < H) {
+    st16(qo + (long)row * s_qo_b + (long)j * s_qo_h + 8 * t, ov);
+  } else {
+    const int kh = j - H;
+    const long slot = slots[row];
+    const long off = slot * sk_s + (long)kh * sk_h + (long)ps * sk_t + 8 * t;
+    st16(kc + off, ov);
+    st16(vc + off, ld16(qkv + (long)row * s_qkv + (long)(H + KV + kh) * D + 8 * t));
+  }
+}
+
+M3X_API int m3x_qk_norm_rope_cache(const void* qkv, long s_qkv, void* q_out, long s_qo_b, long s_qo_h, void* k_cache,
+                                   void* v_cache, long sk_s, long sk_h, long sk_t, const int64_t* slots,
+                                   const int32_t* pos, const void* cos, const void* sin, long s_cos, const void* wq,
+                                   const void* wk, float eps, int rows, int heads, int kv_heads, int head_dim,
+                                   int cap, void* stream) {
+  if (rows < 0 || heads <= 0 || kv_heads <= 0 || cap <= 0) return M3X_EINVAL;
+  if (rows == 0) return M3X_OK;
+  if (!qkv || !q_out || !k_cache || !v_cache || !slots || !pos || !cos || !sin || !wq || !wk) return M3X_ENULL;
+  if ((s_qkv | s_qo_b | s_qo_h | sk_s | sk_h | sk_t | s_cos) & 7) return M3X_EINVAL;
+  if (!m3x_aligned16(qkv) || !m3x_aligned16(q_out) || !m3x_aligned16(k_cache) || !m3x_aligned16(v_cache) ||
+      !m3x_aligned16(cos) || !m3x_aligned16(sin) || !m3x_aligned16(wq) || !m3x_aligned16(wk))
+    return M3X_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+  const long items = (long)rows * (heads + kv_heads);
+#define M3X_QKN_ARGS                                                                                              \
+  (const uint16_t*)qkv, s_qkv, (uint16_t*)q_out, s_qo_b, s_qo_h, (uint16_t*)k_cache, (uint16_t*)v_cache, sk_s, sk_h, \
+      sk_t, slots, pos, (const uint16_t*)cos, (const uint16_t*)sin, s_cos, (const uint16_t*)wq, (const uint16_t*)wk,  \
+      eps, rows, heads, kv_heads, cap
+  if (head_dim == 128) {
+    hipLaunchKernelGGL(qk_norm_rope_cache_kernel<128>, dim3(m3x_ceil_div(items, 16)), dim3(256), 0, st, M3X_QKN_ARGS);
+  } else if (head_dim == 64) {
+    hipLaunchKernelGGL(qk_norm_rope_cache_kernel<64>, dim3(m3x_ceil_div(items, 32)), dim3(256), 0, st, M3X_QKN_ARGS);
+  } else {
+    return M3X_EUNSUPPORTED;
+  }
+#undef M3X_QKN_ARGS
+  M3X_CHECK_LAUNCH();
+  return M3X_OK;
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// Depth residual + norm: x' = dt(x + a) [then dt(x' + c[row / T])]; x' stored to xo (if given);
+// y = LayerNorm(x') (fp32 statistics, affine w/b) or RMSNorm(x') (bf16(bf16(x*inv)*w), Qwen3 convention).
+// serve/fast_depth_kernels.py:14-45 (_add_ln); the RMS variant serves the SwiGLU/RMSNorm depth trunk.
+// a == nullptr: x' = x (plain norm of the input, serve/fast_depth.py:164).
+enum { M3X_NORM_LAYER = 0, M3X_NORM_RMS = 1 };
+
+template <int TPR, int DT>
+__global__ __launch_bounds__(256) void add_norm_kernel(const uint16_t* __restrict__ x, long sxb, long sxt,
+                                                       const uint16_t* __restrict__ a, long sab, long sat,
+                                                       const uint16_t* __restrict__ c, long s_c, uint16_t* xo,
+                                                       uint16_t* __restrict__ y, const uint16_t* __restrict__ w,
+                                                       const uint16_t* __restrict__ b, float eps, int rows, int T,
+                                                       int kind) {
+  constexpr int N = TPR * 8;
+  constexpr int RPB = 256 / TPR;
+  __shared__ float red[TPR > 64 ? 256 : 1];
+  __shared__ float bcast[RPB];
+  const int t = threadIdx.x % TPR;
+  const int row = blockIdx.x * RPB + threadIdx.x / TPR;
+  const bool active = row < rows;
+  const int rb = active ? row / T : 0, rt = active ? row % T : 0;
+  float v[8];
+  float p = 0.f;
+  if (active) {
+    u16x8 xv = ld16(x + rb * sxb + rt * sxt + 8 * t);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = E<DT>::to_f(xv.v[e]);
+    if (a) {
+      u16x8 av = ld16(a + rb * sab + rt * sat + 8 * t);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = rnd<DT>(v[e] + E<DT>::to_f(av.v[e]));
+    }
+    if (c) {
+      u16x8 cv = ld16(c + (long)rb * s_c + 8 * t);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = rnd<DT>(v[e] + E<DT>::to_f(cv.v[e]));
+    }
+    if (xo) {
+      u16x8 ov;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ov.v[e] = E<DT>::from_f(v[e]);
+      st16(xo + (long)row * N + 8 * t, ov);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = 0.f;
+  }
+  u16x8 yv;
+  if (kind == M3X_NORM_LAYER) {
+    p = v[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) p = p + v[e];
+    const float mean = row_tree_sum<TPR>(p, red, bcast) / (float)N;
+    float d[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) d[e] = v[e] - mean;
+    p = d[0] * d[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) p = p + d[e] * d[e];
+    const float var = row_tree_sum<TPR>(p, red, bcast) / (float)N;
+    if (!active) return;
+    const float sd = sqrtf(var + eps);
+    u16x8 wv = ld16(w + 8 * t), bv = ld16(b + 8 * t);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) yv.v[e] = E<DT>::from_f(d[e] / sd * E<DT>::to_f(wv.v[e]) + E<DT>::to_f(bv.v[e]));
+  } else {
+    p = v[0] * v[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) p = p + v[e] * v[e];
+    const float ss = row_tree_sum<TPR>(p, red, bcast);
+    if (!active) return;
+    const float inv = 1.0f / sqrtf(ss / (float)N + eps);
+    u16x8 wv = ld16(w + 8 * t);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) yv.v[e] = E<DT>::from_f(rnd<DT>(v[e] * inv) * E<DT>::to_f(wv.v[e]));
+  }
+  st16(y + (long)row * N + 8 * t, yv);
+}
+
+// Row r = (b, t) = (r / T, r % T) of x is read at x + b*sxb + t*sxt (likewise a); x_out and y are contiguous
+// [rows, n]; c is indexed by b with stride s_c (s_c = 0 broadcasts one vector).
+M3X_API int m3x_add_norm(const void* x, long sxb, long sxt, const void* a, long sab, long sat, const void* c, long s_c,
+                         void* x_out, void* y, const void* w, const void* b, float eps, int rows, int T, int n,
+                         int kind, int dtype, void* stream) {
+  if (rows < 0 || T <= 0) return M3X_EINVAL;
+  if (rows == 0) return M3X_OK;
+  if (!x || !y || !w) return M3X_ENULL;
+  if (kind == M3X_NORM_LAYER && !b) return M3X_ENULL;
+  if (kind != M3X_NORM_LAYER && kind != M3X_NORM_RMS) return M3X_EINVAL;
+  if ((sxb | sxt | (a ? (sab | sat) : 0) | (c ? s_c : 0)) & 7) return M3X_EINVAL;
+  if (!m3x_aligned16(x) || !m3x_aligned16(y) || !m3x_aligned16(w) || (a && !m3x_aligned16(a)) ||
+      (c && !m3x_aligned16(c)) || (x_out && !m3x_aligned16(x_out)) || (b && !m3x_aligned16(b)))
+    return M3X_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+  const uint16_t *X = (const uint16_t*)x, *A = (const uint16_t*)a, *C = (const uint16_t*)c;
+  const uint16_t *Wt = (const uint16_t*)w, *Bt = (const uint16_t*)b;
+  uint16_t *XO = (uint16_t*)x_out, *Y = (uint16_t*)y;
+#define M3X_ADD_NORM_LAUNCH(NN, DTT)                                                                               \
+  hipLaunchKernelGGL((add_norm_kernel<NN / 8, DTT>), dim3(m3x_ceil_div(rows, 256 / (NN / 8))), dim3(256), 0, st, X, \
+                     sxb, sxt, A, sab, sat, C, s_c, XO, Y, Wt, Bt, eps, rows, T, kind)
+  if (dtype == M3X_BF16 && n == 1024) M3X_ADD_NORM_LAUNCH(1024, M3X_BF16);
+  else if (dtype == M3X_F16 && n == 1024) M3X_ADD_NORM_LAUNCH(1024, M3X_F16);
+  else if (dtype == M3X_BF16 && n == 2048) M3X_ADD_NORM_LAUNCH(2048, M3X_BF16);
+  else if (dtype == M3X_F16 && n == 2048) M3X_ADD_NORM_LAUNCH(2048, M3X_F16);
+  else return M3X_EUNSUPPORTED;
+#undef M3X_ADD_NORM_LAUNCH
+  M3X_CHECK_LAUNCH();
+  return M3X_OK;
+}
+
+// out[r] = dt(x[r] + bias[r * ld_bias]) for rows of n elements (ld_bias = 0 broadcasts one vector).
+// Replaces `d.in_proj(h) + self.level0` (serve/fast_depth.py:150).
+template <int DT>
+__global__ __launch_bounds__(256) void add_rows_kernel(const uint16_t* __restrict__ x, long ld_x,
+                                                       const uint16_t* __restrict__ bias, long ld_b,
+                                                       uint16_t* __restrict__ out, long ld_o, int rows, int nvec) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long)rows * nvec) return;
+  const int r = (int)(i / nvec), v = (int)(i % nvec);
+  u16x8 xv = ld16(x + r * ld_x + 8 * v), bv = ld16(bias + r * ld_b + 8 * v), ov;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ov.v[e] = E<DT>::from_f(E<DT>::to_f(xv.v[e]) + E<DT>::to_f(bv.v[e]));
+  st16(out + r * ld_o + 8 * v, ov);
+}
+
+M3X_API int m3x_add_rows(const void* x, long ld_x, const void* bias, long ld_bias, void* out, long ld_out, int rows,
+                         int n, int dtype, void* stream) {
+  if (rows < 0 || n <= 0 || (n & 7) || ((ld_x | ld_bias | ld_out) & 7)) return M3X_EINVAL;
+  if (rows == 0) return M3X_OK;
+  if (!x || !bias || !out) return M3X_ENULL;
+  if (!m3x_aligned16(x) || !m3x_aligned16(bias) || !m3x_aligned16(out)) return M3X_EINVAL;
+  const long total = (long)rows * (n / 8);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == M3X_BF16)
+    hipLaunchKernelGGL(add_rows_kernel<M3X_BF16>, dim3(m3x_ceil_div(total, 256)), dim3(256), 0, st,
+                       (const uint16_t*)x, ld_x, (const uint16_t*)bias, ld_bias, (uint16_t*)out, ld_out, rows, n / 8);
+  else if (dtype == M3X_F16)
+    hipLaunchKernelGGL(add_rows_kernel<M3X_F16>, dim3(m3x_ceil_div(total, 256)), dim3(256), 0, st,
+                       (const uint16_t*)x, ld_x, (const uint16_t*)bias, ld_bias, (uint16_t*)out, ld_out, rows, n / 8);
+  else
+    return M3X_EUNSUPPORTED;
+  M3X_CHECK_LAUNCH();
+  return M3X_OK;
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// Feedback embedding for the next backbone step: e = sum_l table[codes[b,l] + n_codes*l] (fp32, l ascending),
+// rounded to dt, divided by sqrt(n_q) (rounded), then RMSNorm in fp32 with one final rounding:
+// y = dt((x * (1/sqrt(mean x^2 + eps))) * w). serve/fast_depth.py:200-203, tts/model/audio_io.py:27-35
+// (nn.RMSNorm with eps = finfo(dtype).eps when the module was built with eps=None).
+// Codes outside [0, n_codes) are clamped (the reference trusts its sampler; a clamp keeps the gather in bounds).
+template <int TPR, int DT>
+__global__ __launch_bounds__(256) void feedback_kernel(const uint16_t* __restrict__ table,
+                                                       const int32_t* __restrict__ codes, long s_codes,
+                                                       uint16_t* __restrict__ out, long s_out,
+                                                       const uint16_t* __restrict__ w, float eps, float scale, int B,
+                                                       int n_q, int n_codes) {
+  constexpr int N = TPR * 8;
+  constexpr int RPB = 256 / TPR;
+  __shared__ float red[TPR > 64 ? 256 : 1];
+  __shared__ float bcast[RPB];
+  const int t = threadIdx.x % TPR;
+  const int row = blockIdx.x * RPB + threadIdx.x / TPR;
+  const bool active = row < B;
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = 0.f;
+  float p = 0.f;
+  if (active) {
+    for (int l = 0; l < n_q; ++l) {
+      int cd = codes[(long)row * s_codes + l];
+      cd = cd < 0 ? 0 : (cd >= n_codes ? n_codes - 1 : cd);
+      u16x8 tv = ld16(table + ((long)cd + (long)n_codes * l) * N + 8 * t);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = v[e] + E<DT>::to_f(tv.v[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = rnd<DT>(rnd<DT>(v[e]) / scale);
+    p = v[0] * v[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) p = p + v[e] * v[e];
+  }
+  const float ss = row_tree_sum<TPR>(p, red, bcast);
+  if (!active) return;
+  const float inv = 1.0f / sqrtf(ss / (float)N + eps);
+  u16x8 wv = ld16(w + 8 * t), yv;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) yv.v[e] = E<DT>::from_f(v[e] * inv * E<DT>::to_f(wv.v[e]));
+  st16(out + (long)row * s_out + 8 * t, yv);
+}
+
+M3X_API int m3x_feedback(const void* table, const int32_t* codes, long s_codes, void* out, long s_out, const void* w,
+                         float eps, float scale, int B, int n, int n_q, int n_codes, int dtype, void* stream) {
+  if (B < 0 || n_q <= 0 || n_codes <= 0) return M3X_EINVAL;
+  if (B == 0) return M3X_OK;
+  if (!table || !codes || !out || !w) return M3X_ENULL;
+  if (s_out & 7) return M3X_EINVAL;
+  if (!m3x_aligned16(table) || !m3x_aligned16(out) || !m3x_aligned16(w)) return M3X_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+#define M3X_FB_LAUNCH(NN, DTT)                                                                                   \
+  hipLaunchKernelGGL((feedback_kernel<NN / 8, DTT>), dim3(m3x_ceil_div(B, 256 / (NN / 8))), dim3(256), 0, st,   \
+                     (const uint16_t*)table, codes, s_codes, (uint16_t*)out, s_out, (const uint16_t*)w, eps, scale, \
+                     B, n_q, n_codes)
+  if (dtype == M3X_BF16 && n == 1024) M3X_FB_LAUNCH(1024, M3X_BF16);
+  else if (dtype == M3X_F16 && n == 1024) M3X_FB_LAUNCH(1024, M3X_F16);
+  else if (dtype == M3X_BF16 && n == 2048) M3X_FB_LAUNCH(2048, M3X_BF16);
+  else if (dtype == M3X_F16 && n == 2048) M3X_FB_LAUNCH(2048, M3X_F16);
+  else return M3X_EUNSUPPORTED;
+#undef M3X_FB_LAUNCH
+  M3X_CHECK_LAUNCH();
+  return M3X_OK;
+}

@@ -1,0 +1,441 @@
+// Codebook samplers driven by caller-supplied uniforms, and the counter-based uniform generator.
+//
+// Sampling contract (one row of V logits, one uniform u in [0,1)):
+//   x_i      = transform(logit_i)                      (depth: logit*inv_temp; cb0: logit/temp + bias - penalty)
+//   kth      = the k-th largest x (counting repeats)   (torch topk(k).values[-1])
+//   kept     = { i : x_i >= kth }                      (ties kept: serve/fast_depth_kernels.py:55-56,
+//                                                       maya3/engine.py:666-668)
+//   order    = kept sorted by x descending, index ascending (+0 before -0)
+//   w_j      = m3x_expf(x_j - x_first)                 (Cody-Waite exp shared with the oracle)
+//   S        = w_0 + w_1 + ... in order (sequential fp32), t = u * S
+//   sample   = first j in order with (w_0 + ... + w_j) > t, else the last kept
+//   greedy   = the first in order (argmax, lowest index on ties)
+// This is inverse-CDF sampling of the top-k renormalised softmax, the distribution the reference draws with
+// Gumbel/exponential races (serve/fast_depth_kernels.py:60-68, maya3/engine.py:687-688).
+//
+// Selection inside one 256-thread workgroup per row: the row max m, a 256-bin histogram of the bucket
+// floor(32*(m - x)) (bin 255 = everything 8 or more below the max, not counted), the first bin b* at which the
+// cumulative count reaches k, then every x with bucket <= b* is a candidate. The bucket is monotone in x, so
+// the candidates contain the top k and all its ties; a bitonic sort of the candidates gives the exact order.
+#include "m3x_common.h"
+
+namespace {
+constexpr int ST = 256;      // threads per row
+constexpr int SMAXV = 4096;  // largest vocabulary
+constexpr int SEPT = SMAXV / ST;
+
+__device__ __forceinline__ uint32_t ordkey(float f) {
+  uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float ordkey_inv(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+struct SampleSmem {
+  unsigned long long cand[SMAXV];
+  float w[SMAXV];
+  unsigned int hist[256];
+  float red[ST / 64];
+  int ncand, nkeep, bstar;
+};
+
+__device__ float block_max(float v, float* red) {
+  v = wave_max_xor(v, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int i = 1; i < ST / 64; ++i) r = fmaxf(r, red[i]);
+  __syncthreads();
+  return r;
+}
+
+// After this returns, sm.cand[0 .. sm.nkeep) holds the kept candidates in sampling order and sm.w their weights.
+// x[] holds this thread's elements i = tid + 256*e (e < SEPT) of the transformed row.
+__device__ void topk_select(const float (&x)[SEPT], int V, int k, SampleSmem& sm) {
+  const int tid = threadIdx.x;
+  const float NEG = -INFINITY;
+  float lm = NEG;
+#pragma unroll
+  for (int e = 0; e < SEPT; ++e)
+    if (tid + ST * e < V) lm = fmaxf(lm, x[e]);
+  const float m = block_max(lm, sm.red);
+  sm.hist[tid] = 0;
+  if (tid == 0) sm.ncand = 0, sm.nkeep = 0;
+  __syncthreads();
+  int bk[SEPT];
+#pragma unroll
+  for (int e = 0; e < SEPT; ++e) {
+    bk[e] = 256;
+    if (tid + ST * e < V) {
+      const float d = (m - x[e]) * 32.0f;
+      bk[e] = (d >= 255.0f || d != d) ? 255 : (int)d;
+      if (bk[e] < 255) atomicAdd(&sm.hist[bk[e]], 1u);
+    }
+  }
+  __syncthreads();
+  if (tid < 64) {
+    // lane owns bins 4*lane .. 4*lane+3 (bin 255 is excluded from the count)
+    unsigned int c[4], s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int bin = 4 * tid + i;
+      c[i] = bin < 255 ? sm.hist[bin] : 0u;
+      s += c[i];
+    }
+    unsigned int incl = s;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const unsigned int o = __shfl_up(incl, off, 64);
+      if (tid >= off) incl += o;
+    }
+    unsigned int run = incl - s;
+    int found = 255;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      run += c[i];
+      if (found == 255 && run >= (unsigned)k && 4 * tid + i < 255) found = 4 * tid + i;
+    }
+    // first lane (lowest bin) that found it
+    unsigned long long mask = __ballot(found < 255);
+    if (tid == 0) sm.bstar = mask ? 0 : 255;
+    if (mask) {
+      const int first = __ffsll((long long)mask) - 1;
+      const int b = __shfl(found, first, 64);
+      if (tid == 0) sm.bstar = b;
+    }
+  }
+  __syncthreads();
+  const int bstar = sm.bstar;
+#pragma unroll
+  for (int e = 0; e < SEPT; ++e) {
+    const int i = tid + ST * e;
+    if (i < V && bk[e] <= bstar) {
+      const int slot = atomicAdd(&sm.ncand, 1);
+      sm.cand[slot] = ((unsigned long long)ordkey(x[e]) << 32) | (unsigned long long)(0xffffffffu - (uint32_t)i);
+    }
+  }
+  __syncthreads();
+  const int nc = sm.ncand;
+  int P2 = 2;
+  while (P2 < nc) P2 <<= 1;
+  for (int i = nc + tid; i < P2; i += ST) sm.cand[i] = 0ull;
+  __syncthreads();
+  for (int kk = 2; kk <= P2; kk <<= 1) {
+    for (int j = kk >> 1; j > 0; j >>= 1) {
+      for (int t = tid; t < (P2 >> 1); t += ST) {
+        const int i = ((t & ~(j - 1)) << 1) | (t & (j - 1));
+        const int p = i | j;
+        const unsigned long long a = sm.cand[i], b = sm.cand[p];
+        const bool desc = (i & kk) == 0;
+        if (desc ? (a < b) : (a > b)) {
+          sm.cand[i] = b;
+          sm.cand[p] = a;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  const int kk = k < nc ? k : nc;
+  const float kth = ordkey_inv((uint32_t)(sm.cand[kk - 1] >> 32));
+  const float x0 = ordkey_inv((uint32_t)(sm.cand[0] >> 32));
+  int local = 0;
+  for (int j = tid; j < nc; j += ST) {
+    const float xj = ordkey_inv((uint32_t)(sm.cand[j] >> 32));
+    if (xj >= kth) {
+      ++local;
+      sm.w[j] = m3x_expf(xj - x0);
+    }
+  }
+  if (local) atomicAdd(&sm.nkeep, local);
+  __syncthreads();
+}
+
+__device__ __forceinline__ int cand_index(unsigned long long c) { return (int)(0xffffffffu - (uint32_t)c); }
+
+// Inverse-CDF pick over cand[0..n) skipping index `skip` (-1: none); returns -1 when the weights sum to 0.
+__device__ int pick(const SampleSmem& sm, int n, float u, int skip) {
+  float S = 0.f;
+  int last = -1;
+  for (int j = 0; j < n; ++j) {
+    if (cand_index(sm.cand[j]) == skip) continue;
+    S = S + sm.w[j];
+    last = j;
+  }
+  if (last < 0 || !(S > 0.f)) return -1;
+  const float t = u * S;
+  float c = 0.f;
+  for (int j = 0; j < n; ++j) {
+    if (cand_index(sm.cand[j]) == skip) continue;
+    c = c + sm.w[j];
+    if (c > t) return cand_index(sm.cand[j]);
+  }
+  return cand_index(sm.cand[last]);
+}
+}  // namespace
+
+// ---------------------------------------------------------------------------------------------------------
+// Depth codebook sampler (serve/fast_depth_kernels.py:48-79 _topk_sample; unfused twin serve/fast_depth.py:125-132):
+// x = float(logit) * inv_temp. Writes the code of row b to out[b * ld_out] (int32, or int64 if out_i64).
+template <int DT>
+__global__ __launch_bounds__(ST) void topk_sample_kernel(const uint16_t* __restrict__ logits, long ld_l, int V,
+                                                         const float* __restrict__ u, long ld_u, float inv_temp,
+                                                         int top_k, int greedy, void* out, long ld_out, int out_i64) {
+  __shared__ SampleSmem sm;
+  const int row = blockIdx.x;
+  float x[SEPT];
+#pragma unroll
+  for (int e = 0; e < SEPT; ++e) {
+    const int i = threadIdx.x + ST * e;
+    x[e] = i < V ? E<DT>::to_f(logits[(long)row * ld_l + i]) * inv_temp : -INFINITY;
+  }
+  topk_select(x, V, top_k, sm);
+  if (threadIdx.x != 0) return;
+  int code = cand_index(sm.cand[0]);
+  if (!greedy) {
+    const int c = pick(sm, sm.nkeep, u[(long)row * ld_u], -1);
+    if (c >= 0) code = c;
+  }
+  if (out_i64)
+    ((int64_t*)out)[(long)row * ld_out] = code;
+  else
+    ((int32_t*)out)[(long)row * ld_out] = code;
+}
+
+M3X_API int m3x_topk_sample(const void* logits, long ld_l, int V, const float* u, long ld_u, float inv_temp,
+                            int top_k, int greedy, void* out, long ld_out, int out_i64, int B, int dtype,
+                            void* stream) {
+  if (B < 0 || V <= 0 || V > SMAXV || top_k <= 0) return M3X_EINVAL;
+  if (B == 0) return M3X_OK;
+  if (!logits || !out || (!greedy && !u)) return M3X_ENULL;
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == M3X_BF16)
+    hipLaunchKernelGGL(topk_sample_kernel<M3X_BF16>, dim3(B), dim3(ST), 0, st, (const uint16_t*)logits, ld_l, V, u,
+                       ld_u, inv_temp, top_k, greedy, out, ld_out, out_i64);
+  else if (dtype == M3X_F16)
+    hipLaunchKernelGGL(topk_sample_kernel<M3X_F16>, dim3(B), dim3(ST), 0, st, (const uint16_t*)logits, ld_l, V, u,
+                       ld_u, inv_temp, top_k, greedy, out, ld_out, out_i64);
+  else
+    return M3X_EUNSUPPORTED;
+  M3X_CHECK_LAUNCH();
+  return M3X_OK;
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// cb0 step: controlled stop + codebook-0 sampling for each seat (maya3/engine.py:652-694, Engine._cb0).
+// Per row b with slot s = slots[b] (per-slot tensors are indexed by s, like the engine's [max_seats+1] state):
+//   x_i = float(logit_i) / temp[s];  x_aeos += aeos_bias[s];  x_i -= rep[s] for every i != aeos seen in
+//   hist[s, :] (entries >= 0);  top-k (k = topk[s], clamped to [1, V]) as in the contract above.
+//   With an AEOS class (aeos >= 0): probs = w / S over the kept set; pa = w_aeos / S; arg = first in order;
+//   can = frames[s] >= min_frames[s]; hz = can ? 1 - (1 - hazard[s]) * (1 - pa) : hazard[s];
+//   stop = can & arg==aeos ? 2 : can & pa>=0.35 ? 3 : can & hz>=0.6 ? 4 : 0;
+//   cb0 = inverse-CDF pick over the kept set without aeos (0 if nothing else is kept).
+//   State: ctr[s] += 1, hist[s] shifts left and appends cb0, hazard[s] = hz, frames[s] += 1.
+// Per-slot pointers may be null: temp/topk fall back to the scalars, no bias/penalty, no stop logic/state.
+struct Cb0Args {
+  const uint16_t* logits;
+  long ld_l;
+  int V;
+  int aeos;
+  const int64_t* slots;
+  const float* u;
+  long ld_u;
+  const float* temp_t;
+  float temp;
+  const int64_t* topk_t;
+  int top_k;
+  const float* aeos_bias;
+  const float* rep_t;
+  int64_t* hist_t;
+  int hist_w;
+  int64_t* frames_t;
+  const int64_t* min_t;
+  float* hazard_t;
+  int32_t* ctr_t;
+  int64_t* cb0_out;    // [B] int64 or null
+  int32_t* cb0_i32;    // [B * ld_cb0_i32] or null (column 0 of the frame's code matrix)
+  long ld_cb0_i32;
+  int64_t* stop_out;   // [B] int64 or null
+};
+
+__global__ __launch_bounds__(ST) void cb0_sample_kernel(Cb0Args a) {
+  __shared__ SampleSmem sm;
+  const int row = blockIdx.x;
+  const long s = a.slots[row];
+  const float temp = a.temp_t ? a.temp_t[s] : a.temp;
+  int k = a.topk_t ? (int)a.topk_t[s] : a.top_k;
+  k = k < 1 ? 1 : (k > a.V ? a.V : k);
+  const float bias = a.aeos_bias ? a.aeos_bias[s] : 0.f;
+  const float rep = a.rep_t ? a.rep_t[s] : 0.f;
+  float x[SEPT];
+#pragma unroll
+  for (int e = 0; e < SEPT; ++e) {
+    const int i = threadIdx.x + ST * e;
+    float v = -INFINITY;
+    if (i < a.V) {
+      v = bf2f(a.logits[(long)row * a.ld_l + i]) / temp;
+      if (i == a.aeos) v = v + bias;
+      if (a.hist_t && a.rep_t && i != a.aeos) {
+        bool seen = false;
+        for (int j = 0; j < a.hist_w; ++j) seen |= a.hist_t[s * a.hist_w + j] == (int64_t)i;
+        if (seen) v = v - rep;
+      }
+    }
+    x[e] = v;
+  }
+  topk_select(x, a.V, k, sm);
+  if (threadIdx.x != 0) return;
+  const int n = sm.nkeep;
+  const float uu = a.u[(long)row * a.ld_u];
+  int cb0;
+  int64_t stop = 0;
+  if (a.aeos >= 0) {
+    float S = 0.f, wa = 0.f;
+    for (int j = 0; j < n; ++j) {
+      S = S + sm.w[j];
+      if (cand_index(sm.cand[j]) == a.aeos) wa = sm.w[j];
+    }
+    const float pa = wa / S;
+    const int arg = cand_index(sm.cand[0]);
+    if (a.frames_t && a.min_t && a.hazard_t) {
+      const bool can = a.frames_t[s] >= a.min_t[s];
+      const float hz0 = a.hazard_t[s];
+      const float hz = can ? 1.0f - (1.0f - hz0) * (1.0f - pa) : hz0;
+      if (can && arg == a.aeos) stop = 2;
+      else if (can && pa >= 0.35f) stop = 3;
+      else if (can && hz >= 0.6f) stop = 4;
+      a.hazard_t[s] = hz;
+      a.frames_t[s] = a.frames_t[s] + 1;
+    }
+    const int c = pick(sm, n, uu, a.aeos);
+    cb0 = c < 0 ? 0 : c;
+  } else {
+    const int c = pick(sm, n, uu, -1);
+    cb0 = c < 0 ? cand_index(sm.cand[0]) : c;
+  }
+  if (a.ctr_t) a.ctr_t[s] = a.ctr_t[s] + 1;
+  if (a.hist_t && a.hist_w > 0) {
+    for (int j = 0; j + 1 < a.hist_w; ++j) a.hist_t[s * a.hist_w + j] = a.hist_t[s * a.hist_w + j + 1];
+    a.hist_t[s * a.hist_w + a.hist_w - 1] = cb0;
+  }
+  if (a.cb0_out) a.cb0_out[row] = cb0;
+  if (a.cb0_i32) a.cb0_i32[(long)row * a.ld_cb0_i32] = cb0;
+  if (a.stop_out) a.stop_out[row] = stop;
+}
+
+M3X_API int m3x_cb0_sample(const void* logits, long ld_l, int V, int aeos, const int64_t* slots, const float* u,
+                           long ld_u, const float* temp_t, float temp, const int64_t* topk_t, int top_k,
+                           const float* aeos_bias, const float* rep_t, int64_t* hist_t, int hist_w, int64_t* frames_t,
+                           const int64_t* min_t, float* hazard_t, int32_t* ctr_t, int64_t* cb0_out, int32_t* cb0_i32,
+                           long ld_cb0_i32, int64_t* stop_out, int B, void* stream) {
+  if (B < 0 || V <= 0 || V > SMAXV || aeos >= V || hist_w < 0) return M3X_EINVAL;
+  if (B == 0) return M3X_OK;
+  if (!logits || !slots || !u) return M3X_ENULL;
+  if (!temp_t && !(temp > 0.f)) return M3X_EINVAL;
+  Cb0Args a{(const uint16_t*)logits, ld_l, V, aeos, slots, u, ld_u, temp_t, temp, topk_t, top_k, aeos_bias, rep_t,
+            hist_t, hist_w, frames_t, min_t, hazard_t, ctr_t, cb0_out, cb0_i32, ld_cb0_i32, stop_out};
+  hipLaunchKernelGGL(cb0_sample_kernel, dim3(B), dim3(ST), 0, (hipStream_t)stream, a);
+  M3X_CHECK_LAUNCH();
+  return M3X_OK;
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// Counter-based uniforms: Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as easy as
+// 1, 2, 3", SC11), counter = (ctr[s], level, 0, 0), key = (seed[s], 0); u = (word0 >> 8) * 2^-24 in [0, 1).
+// One draw per (seat, level): the per-request streams the engine keys by (seed, frame counter, level)
+// (maya3/engine.py:436-437, serve/fast_depth_kernels.py:63,90).
+__device__ __forceinline__ uint32_t philox_word0(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32_t k0,
+                                                 uint32_t k1) {
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    if (r) {
+      k0 += 0x9E3779B9u;
+      k1 += 0xBB67AE85u;
+    }
+    const uint32_t lo0 = 0xD2511F53u * c0, hi0 = __umulhi(0xD2511F53u, c0);
+    const uint32_t lo1 = 0xCD9E8D57u * c2, hi1 = __umulhi(0xCD9E8D57u, c2);
+    const uint32_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
+    c0 = n0;
+    c1 = lo1;
+    c2 = n2;
+    c3 = lo0;
+  }
+  return c0;
+}
+
+__global__ void philox_uniforms_kernel(const int32_t* __restrict__ seeds, const int32_t* __restrict__ ctrs,
+                                       const int64_t* __restrict__ slots, float* __restrict__ out, long ld_out,
+                                       int level0, int nlevels, int B) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long)B * nlevels) return;
+  const int b = (int)(i / nlevels), j = (int)(i % nlevels);
+  const long s = slots[b];
+  const uint32_t w = philox_word0((uint32_t)ctrs[s], (uint32_t)(level0 + j), 0u, 0u, (uint32_t)seeds[s], 0u);
+  out[(long)b * ld_out + j] = (float)(w >> 8) * 5.9604644775390625e-8f;
+}
+
+M3X_API int m3x_philox_uniforms(const int32_t* seeds, const int32_t* ctrs, const int64_t* slots, float* out,
+                                long ld_out, int level0, int nlevels, int B, void* stream) {
+  if (B < 0 || nlevels <= 0 || level0 < 0) return M3X_EINVAL;
+  if (B == 0) return M3X_OK;
+  if (!seeds || !ctrs || !slots || !out) return M3X_ENULL;
+  const long total = (long)B * nlevels;
+  hipLaunchKernelGGL(philox_uniforms_kernel, dim3(m3x_ceil_div(total, 256)), dim3(256), 0, (hipStream_t)stream, seeds,
+                     ctrs, slots, out, ld_out, level0, nlevels, B);
+  M3X_CHECK_LAUNCH();
+  return M3X_OK;
+}
+
+// Per-row Exp(1) noise: out[b, c] = -log(max(u, 1e-12)), u from counter (ctrs[b], level, c, 0), key (seeds[b], 0).
+// Surface of row_exponential (serve/fast_depth_kernels.py:82-98) for callers that still take argmax(q/E).
+__global__ void philox_exponential_kernel(const int32_t* __restrict__ seeds, const int32_t* __restrict__ ctrs,
+                                          float* __restrict__ out, long ld_out, int level, int V, int B) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long)B * V) return;
+  const int b = (int)(i / V), c = (int)(i % V);
+  const uint32_t w = philox_word0((uint32_t)ctrs[b], (uint32_t)level, (uint32_t)c, 0u, (uint32_t)seeds[b], 0u);
+  const float u = (float)(w >> 8) * 5.9604644775390625e-8f;
+  out[(long)b * ld_out + c] = -logf(fmaxf(u, 1e-12f));
+}
+
+M3X_API int m3x_philox_exponential(const int32_t* seeds, const int32_t* ctrs, float* out, long ld_out, int level,
+                                   int V, int B, void* stream) {
+  if (B < 0 || V <= 0 || level < 0) return M3X_EINVAL;
+  if (B == 0) return M3X_OK;
+  if (!seeds || !ctrs || !out) return M3X_ENULL;
+  const long total = (long)B * V;
+  hipLaunchKernelGGL(philox_exponential_kernel, dim3(m3x_ceil_div(total, 256)), dim3(256), 0, (hipStream_t)stream,
+                     seeds, ctrs, out, ld_out, level, V, B);
+  M3X_CHECK_LAUNCH();
+  return M3X_OK;
+}
+
+// raw Philox4x32-10 block (known-answer tests), out[0..3] for counter c[0..3] and key k[0..1]
+__global__ void philox_block_kernel(const uint32_t* c, const uint32_t* k, uint32_t* out) {
+  uint32_t c0 = c[0], c1 = c[1], c2 = c[2], c3 = c[3], k0 = k[0], k1 = k[1];
+  for (int r = 0; r < 10; ++r) {
+    if (r) {
+      k0 += 0x9E3779B9u;
+      k1 += 0xBB67AE85u;
+    }
+    const uint32_t lo0 = 0xD2511F53u * c0, hi0 = __umulhi(0xD2511F53u, c0);
+    const uint32_t lo1 = 0xCD9E8D57u * c2, hi1 = __umulhi(0xCD9E8D57u, c2);
+    const uint32_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
+    c0 = n0;
+    c1 = lo1;
+    c2 = n2;
+    c3 = lo0;
+  }
+  out[0] = c0;
+  out[1] = c1;
+  out[2] = c2;
+  out[3] = c3;
+}
+
+M3X_API int m3x_philox_block(const uint32_t* counter, const uint32_t* key, uint32_t* out, void* stream) {
+  if (!counter || !key || !out) return M3X_ENULL;
+  hipLaunchKernelGGL(philox_block_kernel, dim3(1), dim3(1), 0, (hipStream_t)stream, counter, key, out);
+  M3X_CHECK_LAUNCH();
+  return M3X_OK;
+}

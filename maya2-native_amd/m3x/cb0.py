@@ -1,0 +1,99 @@
+"""Codebook-0 step on m3x kernels: cb0 head GEMM + one sampler kernel (controlled stop, per-seat settings).
+
+Equivalent of Engine._cb0 (maya3/engine.py:652-694) and the per-slot sampler state Engine._build_fast allocates
+(:208-233) and Engine._bind writes (:429-444). Where the engine draws Exp(1) noise with `row_exponential` and
+takes argmax(q/E), this draws one Philox uniform per seat from the same (seed, frame counter, level 0) stream key
+and inverts the CDF of the same renormalised top-k distribution (the kernel's contract is in csrc/sample.hip).
+Top-p below 1 is not implemented here and is rejected when a seat asks for it.
+"""
+from __future__ import annotations
+
+from types import SimpleNamespace
+
+import torch
+
+from . import ops
+from ._lib import lib
+
+
+class Cb0Sampler:
+    def __init__(self, head_weight, max_seats, aeos=None, temp=0.9, top_k=64, rep=0.8, rep_win=12, stop=True):
+        """head_weight [V0, hidden] bf16 (Backbone.cb0_head, tts/model/backbone.py:121). aeos: the AEOS class
+        (default 2048 when V0 == 2049, else none). stop=False skips the controlled-stop bookkeeping."""
+        lib()
+        self.w = head_weight
+        self.V = head_weight.shape[0]
+        self.aeos = (2048 if self.V == 2049 else -1) if aeos is None else int(aeos)
+        self.stop = bool(stop) and self.aeos >= 0
+        self.rep_win = int(rep_win)
+        dev = head_weight.device
+        m = max_seats + 1
+        self.max_seats = max_seats
+        self.temp_t = torch.full((m,), float(temp), device=dev, dtype=torch.float32)
+        self.topk_t = torch.full((m,), int(top_k), device=dev, dtype=torch.long)
+        self.rep_t = torch.full((m,), float(rep), device=dev, dtype=torch.float32)
+        self.seed_t = torch.zeros(m, device=dev, dtype=torch.int32)
+        self.ctr_t = torch.zeros(m, device=dev, dtype=torch.int32)
+        self.hist_t = torch.full((m, max(1, self.rep_win)), -1, device=dev, dtype=torch.long)
+        self.frames_t = torch.zeros(m, device=dev, dtype=torch.long)
+        self.min_t = torch.zeros(m, device=dev, dtype=torch.long)
+        self.hazard_t = torch.zeros(m, device=dev, dtype=torch.float32)
+        self.aeos_bias = torch.zeros(m, device=dev, dtype=torch.float32)
+        self.any_rep = float(rep) > 0 and self.rep_win > 0
+
+    @torch.inference_mode()
+    def bind(self, slot, seed, temperature=None, top_k=None, top_p=None, repetition_penalty=None, min_frames=0):
+        """Per-seat settings at admission (maya3/engine.py:429-444)."""
+        if top_p is not None and float(top_p) < 1.0:
+            raise ValueError('top_p < 1 is not implemented by the m3x cb0 sampler')
+        self.seed_t[slot] = int(seed)
+        self.ctr_t[slot] = 0
+        self.frames_t[slot] = 0
+        self.min_t[slot] = int(min_frames)
+        self.hazard_t[slot] = 0
+        self.aeos_bias[slot] = 0
+        self.hist_t[slot] = -1
+        if temperature is not None:
+            self.temp_t[slot] = float(temperature)
+        if top_k is not None:
+            self.topk_t[slot] = int(top_k)
+        if repetition_penalty is not None:
+            self.rep_t[slot] = float(repetition_penalty)
+            self.any_rep = self.any_rep or float(repetition_penalty) > 0
+
+    def make_buffers(self, B, h=None, codes=None):
+        dev = self.w.device
+        b = SimpleNamespace(B=B)
+        b.slots = torch.full((B,), self.max_seats, dtype=torch.long, device=dev)
+        b.h = h if h is not None else torch.zeros(B, self.w.shape[1], dtype=self.w.dtype, device=dev)
+        b.logits = torch.empty(B, self.V, dtype=self.w.dtype, device=dev)
+        b.u = torch.zeros(B, 1, dtype=torch.float32, device=dev)
+        b.cb0 = torch.zeros(B, dtype=torch.long, device=dev)
+        b.stop = torch.zeros(B, dtype=torch.long, device=dev)
+        b.codes = codes
+        lw = ops.linear_workspace(B, self.V, self.w.shape[1])
+        b.lin_ws = torch.empty(max(lw, 16) // 4, dtype=torch.float32, device=dev)
+        return b
+
+    def run(self, b, uniforms=True):
+        """logits = h @ head^T; u from (seed_t, ctr_t, level 0); sample -> b.cb0 (and column 0 of b.codes)."""
+        ops.linear(b.h, self.w, b.logits, b.lin_ws)
+        if uniforms:
+            ops.philox_uniforms(self.seed_t, self.ctr_t, b.slots, b.u, 0)
+        rep = self.any_rep and self.rep_win > 0
+        ops.cb0_sample(b.logits, self.aeos, b.slots, b.u[:, 0], temp_t=self.temp_t, topk_t=self.topk_t,
+                       aeos_bias=self.aeos_bias if self.aeos >= 0 else None, rep_t=self.rep_t if rep else None,
+                       hist_t=self.hist_t if self.rep_win > 0 else None,
+                       frames_t=self.frames_t if self.stop else None, min_t=self.min_t if self.stop else None,
+                       hazard_t=self.hazard_t if self.stop else None, ctr_t=self.ctr_t, cb0_out=b.cb0,
+                       cb0_i32=None if b.codes is None else b.codes[:, 0], stop_out=b.stop)
+        return b.stop, b.cb0
+
+    @torch.inference_mode()
+    def __call__(self, h, idx):
+        """Eager step for seats idx with hidden states h [B, hidden]: returns (stop code [B], cb0 [B]) as int64."""
+        b = self.make_buffers(h.shape[0])
+        b.slots.copy_(idx)
+        b.h.copy_(h)
+        stop, cb0 = self.run(b)
+        return stop.clone(), cb0.clone()

@@ -1,0 +1,277 @@
+"""Tensor-level wrappers over the m3x C ABI (include/m3x.h).
+
+Each wrapper checks devices, dtypes and shapes (ValueError, like the reference surfaces), passes raw pointers,
+element strides and torch's current HIP stream, and raises RuntimeError on a non-zero status. Nothing here
+allocates on the device except where a function documents that it returns a new tensor; graph-captured code
+passes preallocated outputs and workspaces.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from ._lib import check, lib
+
+NORM_LAYER, NORM_RMS = 0, 1
+ACT_SWIGLU, ACT_GELU = 0, 1
+_DT = {torch.bfloat16: 0, torch.float16: 1}
+
+
+def _p(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _dt(t: torch.Tensor) -> int:
+    if t.dtype not in _DT:
+        raise ValueError(f"m3x kernels take bfloat16 or float16 tensors, got {t.dtype}")
+    return _DT[t.dtype]
+
+
+def _dev(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("m3x kernels take device tensors")
+
+
+def _rows2d(t: torch.Tensor, name: str):
+    if t.dim() != 2 or t.stride(-1) != 1:
+        raise ValueError(f"{name} must be a 2-D tensor with a contiguous last dimension, got {tuple(t.shape)}")
+
+
+def _need(t: torch.Tensor, dtype, name: str):
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+
+
+# ---------------------------------------------------------------- backbone step
+def positions(lengths, slots, offset, pos):
+    _dev(lengths, slots, offset, pos)
+    _need(lengths, torch.long, "lengths")
+    _need(slots, torch.long, "slots")
+    _need(pos, torch.int32, "pos")
+    if offset is not None:
+        _need(offset, torch.long, "offset")
+    check(lib().m3x_positions(_p(lengths), _p(slots), _p(offset), _p(pos), slots.numel(), _stream()), "positions")
+
+
+def lengths_add(lengths, slots, real):
+    _dev(lengths, slots, real)
+    check(lib().m3x_lengths_add(_p(lengths), _p(slots), _p(real), slots.numel(), _stream()), "lengths_add")
+
+
+def add_rms(h, a, w, eps, h_out=None, y=None):
+    """h_out = bf16(h + a); y = RMSNorm(h_out) (a None: y = RMSNorm(h), h_out unused). Returns (h_out, y)."""
+    _dev(h, a, w, h_out, y)
+    _rows2d(h, "h")
+    if h.dtype != torch.bfloat16:
+        raise ValueError("fused add+norm kernel is bf16-only")
+    rows, n = h.shape
+    if y is None:
+        y = torch.empty_like(h)
+    if a is not None:
+        _rows2d(a, "a")
+        if a.shape != h.shape:
+            raise ValueError(f"add_rms: a {tuple(a.shape)} != h {tuple(h.shape)}")
+        if h_out is None:
+            h_out = torch.empty_like(h)
+    check(lib().m3x_add_rms(_p(h), h.stride(0), _p(a), 0 if a is None else a.stride(0), _p(h_out),
+                            0 if h_out is None else h_out.stride(0), _p(y), y.stride(0), _p(w), float(eps), rows, n,
+                            _stream()), "add_rms")
+    return h_out, y
+
+
+def qk_norm_rope_cache(qkv, q_out, k_cache, v_cache, slots, pos, cos, sin, wq, wk, eps, heads, kv_heads):
+    _dev(qkv, q_out, k_cache, v_cache, slots, pos, cos, sin, wq, wk)
+    D = k_cache.shape[-1]
+    rows = qkv.shape[0]
+    if qkv.shape[1] != (heads + 2 * kv_heads) * D:
+        raise ValueError(f"qkv width {qkv.shape[1]} != (heads + 2*kv_heads)*head_dim")
+    check(lib().m3x_qk_norm_rope_cache(
+        _p(qkv), qkv.stride(0), _p(q_out), q_out.stride(0), q_out.stride(1), _p(k_cache), _p(v_cache),
+        k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), _p(slots), _p(pos), _p(cos), _p(sin), cos.stride(0),
+        _p(wq), _p(wk), float(eps), rows, heads, kv_heads, D, k_cache.shape[2], _stream()), "qk_norm_rope_cache")
+
+
+def decode_attn_workspace(rows, kv_heads, max_ctx, chunk) -> int:
+    return int(lib().m3x_decode_attn_workspace(rows, kv_heads, max_ctx, chunk))
+
+
+def decode_attn(q, k_cache, v_cache, out, slots, pos, scale, max_ctx, chunk, workspace, heads, kv_heads):
+    """q, out: [rows, heads, D] (any row/head strides, contiguous D); caches [slots, kv_heads, cap, D]."""
+    _dev(q, k_cache, v_cache, out, slots, pos, workspace)
+    rows = q.shape[0]
+    ws = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(lib().m3x_decode_attn(
+        _p(q), q.stride(0), q.stride(1), _p(k_cache), _p(v_cache), k_cache.stride(0), k_cache.stride(1),
+        k_cache.stride(2), k_cache.shape[2], _p(out), out.stride(0), out.stride(1), _p(slots), _p(pos), float(scale),
+        rows, heads, kv_heads, k_cache.shape[-1], int(max_ctx), int(chunk), _p(workspace), ws, _stream()),
+        "decode_attn")
+
+
+def linear_workspace(M, N, K, splits=0) -> int:
+    return int(lib().m3x_linear_workspace(M, N, K, splits))
+
+
+def linear(x, w, y=None, workspace=None, splits=0):
+    """y = x @ w.T with x [M, K], w [N, K] (16-bit, same dtype); returns y [M, N]."""
+    _dev(x, w, y, workspace)
+    _rows2d(x, "x")
+    _rows2d(w, "w")
+    M, K = x.shape
+    N = w.shape[0]
+    if w.shape[1] != K or w.dtype != x.dtype:
+        raise ValueError(f"linear: x {tuple(x.shape)} {x.dtype} vs w {tuple(w.shape)} {w.dtype}")
+    if y is None:
+        y = torch.empty(M, N, dtype=x.dtype, device=x.device)
+    _rows2d(y, "y")
+    need = linear_workspace(M, N, K, splits)
+    if need and workspace is None:
+        workspace = torch.empty(need // 4, dtype=torch.float32, device=x.device)
+    ws = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(lib().m3x_linear(_p(x), x.stride(0), _p(w), w.stride(0), _p(y), y.stride(0), M, N, K, splits,
+                           _p(workspace), ws, _dt(x), _stream()), "linear")
+    return y
+
+
+def act(inp, out, kind):
+    """SWIGLU: out[:, :I] = bf16(silu(g))*u for inp = [g | u]; GELU: out = gelu(inp[:, :I])."""
+    _dev(inp, out)
+    _rows2d(inp, "inp")
+    _rows2d(out, "out")
+    check(lib().m3x_act(_p(inp), inp.stride(0), _p(out), out.stride(0), inp.shape[0], out.shape[1], kind, _dt(inp),
+                        _stream()), "act")
+    return out
+
+
+# ---------------------------------------------------------------- depth step
+def _bt_strides(t, T):
+    """(row-of-b stride, row-of-t stride) of a [B, T, N] view or a contiguous [B*T, N] tensor."""
+    if t.dim() == 3:
+        if t.stride(-1) != 1:
+            raise ValueError("last dimension must be contiguous")
+        return t.stride(0), t.stride(1)
+    _rows2d(t, "x")
+    return T * t.stride(0), t.stride(0)
+
+
+def add_norm(x, a, c, x_out, y, w, b, eps, T, kind):
+    """x, a: [B, T, N] views or [B*T, N]; c: [B, N] (row stride may be 0) or None; x_out/y contiguous [B*T, N]."""
+    _dev(x, a, c, x_out, y, w, b)
+    n = x.shape[-1]
+    rows = y.shape[0]
+    sxb, sxt = _bt_strides(x, T)
+    sab, sat = _bt_strides(a, T) if a is not None else (0, 0)
+    check(lib().m3x_add_norm(_p(x), sxb, sxt, _p(a), sab, sat, _p(c), 0 if c is None else c.stride(0), _p(x_out),
+                             _p(y), _p(w), _p(b), float(eps), rows, T, n, kind, _dt(y), _stream()), "add_norm")
+
+
+def add_rows(x, bias, out):
+    """out = x + bias (bias [N] broadcast, or [rows, N])."""
+    _dev(x, bias, out)
+    ldb = 0 if bias.dim() == 1 else bias.stride(0)
+    check(lib().m3x_add_rows(_p(x), x.stride(0), _p(bias), ldb, _p(out), out.stride(0), x.shape[0], x.shape[-1],
+                             _dt(x), _stream()), "add_rows")
+
+
+def depth_attn(qkv, kd, vd, out, B, T, p0, tq0, heads, head_dim, scale, write_kv=True):
+    _dev(qkv, kd, vd, out)
+    sqb, sqt = _bt_strides(qkv, T)
+    sob, sot = _bt_strides(out, T - tq0)
+    check(lib().m3x_depth_attn(_p(qkv), sqb, sqt, _p(kd), _p(vd), _p(out), sob, sot, B, T, p0, tq0, heads, head_dim,
+                               kd.shape[2], float(scale), int(write_kv), _dt(qkv), _stream()), "depth_attn")
+
+
+def topk_sample(logits, u, inv_temp, top_k, greedy, out, out_i64=False):
+    """logits [B, V] 16-bit; u [B] view (any stride) or None for greedy; out [B] view (int32/int64)."""
+    _dev(logits, u, out)
+    _rows2d(logits, "logits")
+    B, V = logits.shape
+    check(lib().m3x_topk_sample(_p(logits), logits.stride(0), V, _p(u), 0 if u is None else u.stride(0),
+                                float(inv_temp), int(top_k), int(greedy), _p(out), out.stride(0), int(out_i64), B,
+                                _dt(logits), _stream()), "topk_sample")
+
+
+def cb0_sample(logits, aeos, slots, u, temp_t=None, temp=1.0, topk_t=None, top_k=50, aeos_bias=None, rep_t=None,
+               hist_t=None, frames_t=None, min_t=None, hazard_t=None, ctr_t=None, cb0_out=None, cb0_i32=None,
+               stop_out=None):
+    _dev(logits, slots, u, temp_t, topk_t, aeos_bias, rep_t, hist_t, frames_t, min_t, hazard_t, ctr_t, cb0_out,
+         cb0_i32, stop_out)
+    _rows2d(logits, "logits")
+    if logits.dtype != torch.bfloat16:
+        raise ValueError("cb0 logits must be bfloat16")
+    B, V = logits.shape
+    check(lib().m3x_cb0_sample(
+        _p(logits), logits.stride(0), V, int(aeos), _p(slots), _p(u), u.stride(0), _p(temp_t), float(temp),
+        _p(topk_t), int(top_k), _p(aeos_bias), _p(rep_t), _p(hist_t), 0 if hist_t is None else hist_t.shape[1],
+        _p(frames_t), _p(min_t), _p(hazard_t), _p(ctr_t), _p(cb0_out), _p(cb0_i32),
+        0 if cb0_i32 is None else cb0_i32.stride(0), _p(stop_out), B, _stream()), "cb0_sample")
+
+
+def philox_uniforms(seeds, ctrs, slots, out, level0):
+    """out [B, nlevels] (row stride free) = Philox uniforms for levels level0.. of each slot's stream."""
+    _dev(seeds, ctrs, slots, out)
+    _need(seeds, torch.int32, "seeds")
+    _need(ctrs, torch.int32, "ctrs")
+    _need(out, torch.float32, "out")
+    check(lib().m3x_philox_uniforms(_p(seeds), _p(ctrs), _p(slots), _p(out), out.stride(0), int(level0),
+                                    out.shape[1], slots.numel(), _stream()), "philox_uniforms")
+
+
+def philox_exponential(seeds, ctrs, out, level):
+    """out [B, V] = Exp(1) noise of each row's (seed, counter) stream at `level`."""
+    _dev(seeds, ctrs, out)
+    _need(seeds, torch.int32, "seeds")
+    _need(ctrs, torch.int32, "ctrs")
+    _need(out, torch.float32, "out")
+    check(lib().m3x_philox_exponential(_p(seeds), _p(ctrs), _p(out), out.stride(0), int(level), out.shape[1],
+                                       out.shape[0], _stream()), "philox_exponential")
+
+
+def philox_block(counter, key, out):
+    check(lib().m3x_philox_block(_p(counter), _p(key), _p(out), _stream()), "philox_block")
+
+
+def ctr_add(ctr, slots):
+    _dev(ctr, slots)
+    check(lib().m3x_ctr_add(_p(ctr), _p(slots), slots.numel(), _stream()), "ctr_add")
+
+
+def feedback(table, codes, out, w, eps, scale, n_q, n_codes):
+    _dev(table, codes, out, w)
+    _need(codes, torch.int32, "codes")
+    check(lib().m3x_feedback(_p(table), _p(codes), codes.stride(0), _p(out), out.stride(0), _p(w), float(eps),
+                             float(scale), out.shape[0], out.shape[1], int(n_q), int(n_codes), _dt(table),
+                             _stream()), "feedback")
+
+
+def copy_rows(src, dst, src_idx=None, src_off=0, dst_idx=None, rows=None):
+    """dst[dst_idx[r] or r] = src[src_idx[r] + src_off or r] for r < rows (16-bit rows, width % 8 == 0)."""
+    _dev(src, dst, src_idx, dst_idx)
+    n = src.shape[-1]
+    if dst.shape[-1] != n:
+        raise ValueError("copy_rows: row widths differ")
+    if rows is None:
+        rows = src_idx.numel() if src_idx is not None else (dst_idx.numel() if dst_idx is not None else src.shape[0])
+    idx_i32 = 0
+    ld_idx = 1
+    if src_idx is not None:
+        if src_idx.dtype == torch.int32:
+            idx_i32 = 1
+        elif src_idx.dtype != torch.long:
+            raise ValueError("indices must be int32 or int64")
+        ld_idx = src_idx.stride(0)
+    if dst_idx is not None:
+        _need(dst_idx, torch.long, "dst_idx")
+    check(lib().m3x_copy_rows(_p(src), src.stride(-2), _p(src_idx), int(src_off), src.shape[-2], _p(dst),
+                              dst.stride(-2), _p(dst_idx), int(rows), n, idx_i32, ld_idx, _stream()), "copy_rows")
+
+
+def code_ring_write(codes, ring, head, B):
+    _dev(codes, ring, head)
+    check(lib().m3x_code_ring_write(_p(codes), codes.stride(0), _p(ring), _p(head), ring.shape[0], ring.shape[1],
+                                    ring.shape[2], int(B), _stream()), "code_ring_write")

@@ -1,0 +1,105 @@
+"""StaticBackbone (drop-in of serve/fast_backbone.py) on the GPU vs the gather-path oracle on the CPU."""
+import pytest
+import torch
+
+from helpers import close
+from m3x import synth
+from oracle import torch_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+LAYERS, S, CAP = 3, 6, 512
+PREFIX = [0, 1, 37, 200, 300, 0]
+
+
+def _setup(gpu, use_graphs=True):
+    from m3x.serve.fast_backbone import StaticBackbone
+    bb_g = synth.qwen3_backbone(layers=LAYERS, seed=21, device=gpu)
+    bb_c = synth.qwen3_backbone(layers=LAYERS, seed=21, device="cpu")
+    sb = StaticBackbone(bb_g, S, capacity=CAP, batch_buckets=(1, 2, 4, 8, 64), ctx_buckets=(256, 512),
+                        attention="triton", fuse_rope=True, use_graphs=use_graphs)
+    g = torch.Generator().manual_seed(22)
+    kc = [torch.zeros(S + 1, 8, CAP, 128, dtype=torch.bfloat16) for _ in range(LAYERS)]
+    vc = [torch.zeros(S + 1, 8, CAP, 128, dtype=torch.bfloat16) for _ in range(LAYERS)]
+    for s, n in enumerate(PREFIX):
+        kv = []
+        for i in range(LAYERS):
+            k = torch.randn(1, 8, n, 128, generator=g).to(torch.bfloat16)
+            v = torch.randn(1, 8, n, 128, generator=g).to(torch.bfloat16)
+            kc[i][s, :, :n] = k[0]
+            vc[i][s, :, :n] = v[0]
+            kv.append((k.to(gpu), v.to(gpu)))
+        sb.load_prefix(s, kv, n)
+    lengths = torch.tensor(PREFIX + [0])
+    cos, sin = O.rope_tables(128, 1e6, CAP, torch.bfloat16)
+    return sb, bb_c, kc, vc, lengths, cos, sin
+
+
+def test_step_matches_oracle(gpu):
+    sb, bb_c, kc, vc, lengths, cos, sin = _setup(gpu)
+    g = torch.Generator().manual_seed(23)
+    slots = [0, 2, 3, 4]
+    for t in range(3):
+        x = torch.randn(len(slots), 1024, generator=g).to(torch.bfloat16)
+        out = sb.step(slots, x.to(gpu))
+        ref = O.backbone_step(bb_c, kc, vc, lengths, torch.tensor(slots), x, cos, sin)
+        ok, info = close(out, ref)
+        assert ok, (t, info)
+    assert sb.lengths.cpu().tolist() == lengths.tolist() and sb.lengths_cpu == lengths.tolist()
+    assert sb.lengths[S].item() == 0
+    for i in range(LAYERS):
+        for s in slots:
+            n = int(lengths[s])
+            ok, info = close(sb.k[i][s, :, :n], kc[i][s, :, :n])
+            assert ok, (i, s, info)
+            ok, info = close(sb.v[i][s, :, :n], vc[i][s, :, :n])
+            assert ok, (i, s, info)
+        # slots that did not step are untouched
+        assert torch.equal(sb.k[i][1].cpu(), kc[i][1]) and torch.equal(sb.k[i][5].cpu(), kc[i][5])
+
+
+def test_step_mixed_prefill_matches_oracle(gpu):
+    sb, bb_c, kc, vc, lengths, cos, sin = _setup(gpu)
+    g = torch.Generator().manual_seed(24)
+    x = torch.randn(2, 1024, generator=g).to(torch.bfloat16)
+    p5 = (torch.randn(20, 1024, generator=g) * 0.5).to(torch.bfloat16)
+    p1 = (torch.randn(7, 1024, generator=g) * 0.5).to(torch.bfloat16)
+    dec, last = sb.step_mixed([0, 3], x.to(gpu), [(5, p5.to(gpu)), (1, p1.to(gpu))])
+    slots = torch.tensor([0, 3] + [5] * 20 + [1] * 7)
+    offset = torch.tensor([0, 0] + list(range(20)) + list(range(7)))
+    ref = O.backbone_step(bb_c, kc, vc, lengths, slots, torch.cat([x, p5, p1]), cos, sin, offset=offset)
+    ok, info = close(dec, ref[:2])
+    assert ok, info
+    ok, info = close(torch.stack(last), ref[[21, 28]])
+    assert ok, info
+    assert sb.lengths_cpu[:S] == [1, 8, 37, 201, 300, 20] == lengths[:S].tolist()
+    # the next decode step of the prefilled slot continues from its new length
+    y = torch.randn(1, 1024, generator=g).to(torch.bfloat16)
+    ok, info = close(sb.step([5], y.to(gpu)), O.backbone_step(bb_c, kc, vc, lengths, torch.tensor([5]), y, cos, sin))
+    assert ok, info
+
+
+def test_graph_replay_equals_eager(gpu):
+    a = _setup(gpu, use_graphs=True)[0]
+    b = _setup(gpu, use_graphs=False)[0]
+    g = torch.Generator().manual_seed(25)
+    for slots in ([0, 2, 3, 4], [0, 2, 3, 4], [1], [4, 0]):
+        x = torch.randn(len(slots), 1024, generator=g).to(torch.bfloat16).to(gpu)
+        assert torch.equal(a.step(slots, x), b.step(slots, x))
+    for i in range(LAYERS):
+        assert torch.equal(a.k[i], b.k[i]) and torch.equal(a.v[i], b.v[i])
+
+
+def test_errors_match_reference_conventions(gpu):
+    sb = _setup(gpu)[0]
+    x = torch.zeros(2, 1024, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(ValueError):
+        sb.step([1, 1], x)
+    with pytest.raises(IndexError):
+        sb.step([0, S], x)
+    with pytest.raises(ValueError):
+        sb.step_mixed([], None, [(1, torch.zeros(CAP, 1024, dtype=torch.bfloat16, device=gpu))])
+    with pytest.raises(IndexError):
+        sb.load_prefix(S, [], 0)
+    with pytest.raises(ValueError):
+        type(sb)(synth.qwen3_backbone(layers=1, device=gpu), 2, attention="flash")

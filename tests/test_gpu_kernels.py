@@ -1,0 +1,338 @@
+"""Kernel-level parity on the GPU: bit-exact against the C oracle where the contract is exact (add+RMSNorm,
+q/k-norm+RoPE+KV write, samplers, Philox, index kernels), bf16 tolerance against an fp32 torch reference for
+GEMMs and attention."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import bf16_bits, close, from_bits
+from oracle import coracle as C
+
+pytestmark = pytest.mark.gpu
+
+
+def _g(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+# ---------------------------------------------------------------- GEMM
+@pytest.mark.parametrize("M,N,K", [(1, 1024, 1024), (5, 4096, 1024), (16, 2048, 1024), (33, 1024, 3072),
+                                   (100, 2049, 1024), (224, 6144, 1024), (7, 1024, 2816), (448, 2816, 1024),
+                                   (2264, 4096, 1024)])
+def test_linear_bf16(gpu, M, N, K):
+    from m3x import ops
+    g = _g(M * 7 + N)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    y = ops.linear(x.to(gpu), w.to(gpu))
+    ref = (x.float() @ w.float().t())
+    ok, info = close(y, ref, atol=1e-2)
+    assert ok, info
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 8])
+def test_linear_fp16_and_forced_splits(gpu, splits):
+    from m3x import ops
+    g = _g(splits)
+    x = torch.randn(24, 1024, generator=g).to(torch.float16)
+    w = (torch.randn(3072, 1024, generator=g) * 0.02).to(torch.float16)
+    y = ops.linear(x.to(gpu), w.to(gpu), splits=splits)
+    ok, info = close(y, x.float() @ w.float().t(), atol=1e-2)
+    assert ok, info
+
+
+def test_linear_strided_output(gpu):
+    from m3x import ops
+    g = _g(3)
+    x = torch.randn(9, 1024, generator=g).to(torch.bfloat16).to(gpu)
+    w = (torch.randn(512, 1024, generator=g) * 0.02).to(torch.bfloat16).to(gpu)
+    big = torch.zeros(9, 1536, dtype=torch.bfloat16, device=gpu)
+    ops.linear(x, w, big[:, 256:768])
+    ok, info = close(big[:, 256:768], x.float() @ w.float().t(), atol=1e-2)
+    assert ok, info
+    assert big[:, :256].abs().sum() == 0 and big[:, 768:].abs().sum() == 0
+
+
+# ---------------------------------------------------------------- add + RMSNorm (bit-exact)
+@pytest.mark.parametrize("n,rows", [(1024, 7), (1024, 224), (2048, 3)])
+def test_add_rms_bitexact(gpu, n, rows):
+    from m3x import ops
+    g = _g(n + rows)
+    h = torch.randn(rows, n, generator=g).to(torch.bfloat16)
+    a = torch.randn(rows, n, generator=g).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(n, generator=g)).to(torch.bfloat16)
+    ho, y = ops.add_rms(h.to(gpu), a.to(gpu), w.to(gpu), 1e-6)
+    ref_ho, ref_y = C.add_rms(bf16_bits(h), bf16_bits(a), bf16_bits(w), 1e-6)
+    assert np.array_equal(bf16_bits(ho), ref_ho)
+    assert np.array_equal(bf16_bits(y), ref_y)
+    _, y0 = ops.add_rms(h.to(gpu), None, w.to(gpu), 1e-6)
+    assert np.array_equal(bf16_bits(y0), C.add_rms(bf16_bits(h), None, bf16_bits(w), 1e-6)[1])
+    hg = h.to(gpu)
+    ops.add_rms(hg, a.to(gpu), w.to(gpu), 1e-6, h_out=hg)  # in place, as the step runs it
+    assert np.array_equal(bf16_bits(hg), ref_ho)
+
+
+# ---------------------------------------------------------------- q/k norm + RoPE + cache write (bit-exact)
+def test_qk_norm_rope_cache_bitexact(gpu):
+    from m3x import ops
+    from oracle.torch_oracle import rope_tables
+    g = _g(0)
+    B, H, KV, D, CAP, S = 6, 16, 8, 128, 512, 8
+    qkv = (torch.randn(B, (H + 2 * KV) * D, generator=g) * 2).to(torch.bfloat16)
+    wq = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    wk = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    pos = torch.tensor([0, 7, 100, 300, 511, 31], dtype=torch.int32)
+    slots = torch.tensor([0, 1, 2, 3, 4, 7])
+    cos, sin = rope_tables(D, 1e6, CAP, torch.bfloat16)
+    K = torch.zeros(S, KV, CAP, D, dtype=torch.bfloat16, device=gpu)
+    V = torch.zeros_like(K)
+    q = torch.empty(B, H, D, dtype=torch.bfloat16, device=gpu)
+    ops.qk_norm_rope_cache(qkv.to(gpu), q, K, V, slots.to(gpu), pos.to(gpu), cos.to(gpu), sin.to(gpu), wq.to(gpu),
+                           wk.to(gpu), 1e-6, H, KV)
+    rq, rk = C.qk_norm_rope(bf16_bits(qkv), H, KV, D, pos.numpy(), bf16_bits(cos), bf16_bits(sin), bf16_bits(wq),
+                            bf16_bits(wk), 1e-6)
+    assert np.array_equal(bf16_bits(q), rq)
+    Kc, Vc = K.cpu(), V.cpu()
+    for r in range(B):
+        assert np.array_equal(bf16_bits(Kc[slots[r], :, pos[r]]), rk[r])
+        assert torch.equal(Vc[slots[r], :, pos[r]], qkv[r, (H + KV) * D:].view(KV, D))
+        Kc[slots[r], :, pos[r]] = 0
+        Vc[slots[r], :, pos[r]] = 0
+    assert Kc.abs().sum() == 0 and Vc.abs().sum() == 0  # nothing else written
+
+
+# ---------------------------------------------------------------- decode attention
+def _attn_ref(q, K, V, slots, pos, scale, G):
+    out = torch.empty(q.shape, dtype=torch.float32)
+    for r in range(q.shape[0]):
+        p = int(pos[r])
+        k = K[slots[r], :, :p + 1].float()  # [KV, n, D]
+        v = V[slots[r], :, :p + 1].float()
+        qq = q[r].float().view(k.shape[0], G, -1)
+        s = torch.einsum('kgd,knd->kgn', qq, k) * scale
+        out[r] = torch.einsum('kgn,knd->kgd', s.softmax(-1), v).reshape(q.shape[1:])
+    return out
+
+
+@pytest.mark.parametrize("heads,kv,chunk", [(16, 8, 128), (16, 8, 256), (16, 8, 1024), (8, 8, 128)])
+def test_decode_attn(gpu, heads, kv, chunk):
+    from m3x import ops
+    g = _g(heads + chunk)
+    D, CAP, S = 128, 2048, 9
+    K = torch.randn(S, kv, CAP, D, generator=g).to(torch.bfloat16)
+    V = torch.randn(S, kv, CAP, D, generator=g).to(torch.bfloat16)
+    slots = torch.tensor([0, 1, 2, 3, 4, 5, 6, 8, 1])
+    pos = torch.tensor([0, 31, 32, 127, 128, 1000, 2047, 513, 5], dtype=torch.int32)
+    # stale cache rows past each row's context hold NaN: nothing past pos may leak into the output
+    for r in range(len(slots)):
+        if slots[r] != 1:
+            K[slots[r], :, pos[r] + 1:] = float('nan')
+            V[slots[r], :, pos[r] + 1:] = float('nan')
+    q = torch.randn(len(slots), heads, D, generator=g).to(torch.bfloat16)
+    out = torch.empty(q.shape, dtype=torch.bfloat16, device=gpu)
+    ws = torch.empty(max(ops.decode_attn_workspace(len(slots), kv, CAP, chunk), 16) // 4, device=gpu)
+    ops.decode_attn(q.to(gpu), K.to(gpu), V.to(gpu), out, slots.to(gpu), pos.to(gpu), D ** -0.5, CAP, chunk, ws,
+                    heads, kv)
+    ref = _attn_ref(q, K, V, slots, pos, D ** -0.5, heads // kv)
+    assert torch.isfinite(out.float()).all()
+    ok, info = close(out, ref, atol=1e-2)
+    assert ok, info
+
+
+# ---------------------------------------------------------------- activations, depth norm / attention
+def test_swiglu_and_gelu(gpu):
+    from m3x import ops
+    g = _g(5)
+    gu = torch.randn(37, 2 * 2816, generator=g).to(torch.bfloat16)
+    out = torch.empty(37, 2816, dtype=torch.bfloat16, device=gpu)
+    ops.act(gu.to(gpu), out, ops.ACT_SWIGLU)
+    ref = torch.nn.functional.silu(gu[:, :2816].float()).to(torch.bfloat16).float() * gu[:, 2816:].float()
+    assert torch.equal(out.cpu(), ref.to(torch.bfloat16)) or close(out, ref, atol=0, rel_ulps=1)[0]
+    x = torch.randn(11, 3072, generator=g).to(torch.float16)
+    o2 = torch.empty(11, 3072, dtype=torch.float16, device=gpu)
+    ops.act(x.to(gpu), o2, ops.ACT_GELU)
+    ok, info = close(o2, torch.nn.functional.gelu(x.float()), atol=1e-3, rel_ulps=1)
+    assert ok, info
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+def test_add_norm_strided(gpu, kind):
+    from m3x import ops
+    g = _g(10 + kind)
+    B, NP, T, D = 3, 32, 5, 1024
+    pre = torch.randn(B, NP, D, generator=g).to(torch.bfloat16)
+    a = torch.randn(B * T, D, generator=g).to(torch.bfloat16)
+    c = torch.randn(B, 4 * D, generator=g).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    b = (0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    p0 = 7
+    pg = pre.to(gpu)
+    xo = torch.empty(B * T, D, dtype=torch.bfloat16, device=gpu)
+    y = torch.empty_like(xo)
+    cg = c.to(gpu)
+    ops.add_norm(pg[:, p0:p0 + T], a.to(gpu), cg[:, D:2 * D], xo, y, w.to(gpu), b.to(gpu) if kind == 0 else None,
+                 1e-5, T, kind)
+    x = pre[:, p0:p0 + T].reshape(B * T, D)
+    xr = (x.float() + a.float()).to(torch.bfloat16)
+    xr = (xr.float() + c[:, D:2 * D].repeat_interleave(T, 0).float()).to(torch.bfloat16)
+    assert torch.equal(xo.cpu(), xr)
+    xf = xr.float()
+    if kind == 0:
+        d = xf - xf.mean(-1, keepdim=True)
+        ref = d / torch.sqrt((d * d).mean(-1, keepdim=True) + 1e-5) * w.float() + b.float()
+    else:
+        ref = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-5)).to(torch.bfloat16).float() * w.float()
+    ok, info = close(y, ref, atol=0, rel_ulps=1)
+    assert ok, info
+
+
+@pytest.mark.parametrize("T,p0,tq0", [(2, 0, 0), (1, 5, 0), (9, 0, 8), (17, 0, 0)])
+def test_depth_attn(gpu, T, p0, tq0):
+    from m3x import ops
+    g = _g(T * 100 + p0)
+    B, H, hd, NP = 3, 8, 128, 32
+    D = H * hd
+    kd = torch.randn(B, H, NP, hd, generator=g).to(torch.bfloat16)
+    vd = torch.randn(B, H, NP, hd, generator=g).to(torch.bfloat16)
+    qkv = torch.randn(B * T, 3 * D, generator=g).to(torch.bfloat16)
+    kdg, vdg = kd.to(gpu), vd.to(gpu)
+    Tq = T - tq0
+    out = torch.empty(B * Tq, D, dtype=torch.bfloat16, device=gpu)
+    ops.depth_attn(qkv.to(gpu), kdg, vdg, out, B, T, p0, tq0, H, hd, hd ** -0.5, True)
+    q3 = qkv.view(B, T, 3, H, hd)
+    kd[:, :, p0:p0 + T] = q3[:, :, 1].transpose(1, 2)
+    vd[:, :, p0:p0 + T] = q3[:, :, 2].transpose(1, 2)
+    assert torch.equal(kdg.cpu(), kd) and torch.equal(vdg.cpu(), vd)
+    ref = torch.empty(B, Tq, H, hd)
+    for t in range(tq0, T):
+        n = p0 + t + 1
+        s = torch.einsum('bhd,bhnd->bhn', q3[:, t, 0].float(), kd[:, :, :n].float()) * hd ** -0.5
+        ref[:, t - tq0] = torch.einsum('bhn,bhnd->bhd', s.softmax(-1), vd[:, :, :n].float())
+    ok, info = close(out, ref.reshape(B * Tq, D), atol=1e-2)
+    assert ok, info
+
+
+# ---------------------------------------------------------------- samplers (bit-exact)
+@pytest.mark.parametrize("dtype,V,k", [(torch.bfloat16, 2048, 50), (torch.float16, 2048, 64),
+                                       (torch.bfloat16, 2049, 2049), (torch.bfloat16, 4096, 1)])
+def test_topk_sample_bitexact(gpu, dtype, V, k):
+    from m3x import ops
+    g = _g(V + k)
+    B = 64
+    logits = (torch.randn(B, V, generator=g) * 2).to(dtype)
+    logits[3] = 1.0                       # all tied: every index kept
+    logits[4, :100] = logits[4, 100]      # a block of ties at the top
+    logits[5, 7] = float('-inf')
+    u = torch.rand(B, generator=g)
+    u[0] = 0.0
+    out = torch.empty(B, dtype=torch.int32, device=gpu)
+    ops.topk_sample(logits.to(gpu), u.to(gpu), 1 / 0.9, k, False, out)
+    ref = C.topk_sample_rows(bf16_bits(logits), 1 / 0.9, k, u.numpy(), is_f16=dtype == torch.float16)
+    assert np.array_equal(out.cpu().numpy(), ref)
+    out64 = torch.empty(B, dtype=torch.long, device=gpu)
+    ops.topk_sample(logits.to(gpu), None, 1 / 0.9, k, True, out64, out_i64=True)
+    refg = C.topk_sample_rows(bf16_bits(logits), 1 / 0.9, k, None, greedy=True, is_f16=dtype == torch.float16)
+    assert np.array_equal(out64.cpu().numpy(), refg)
+
+
+def test_cb0_sample_bitexact(gpu):
+    from m3x import ops
+    g = _g(21)
+    B, V, S, W = 48, 2049, 64, 12
+    logits = (torch.randn(B, V, generator=g) * 2).to(torch.bfloat16)
+    logits[:8, 2048] = 9.0
+    logits[8:16, 2048] = 4.5
+    slots = torch.randperm(S, generator=g)[:B]
+    temp = 0.6 + torch.rand(S, generator=g)
+    topk = torch.randint(1, 80, (S,), generator=g)
+    bias = torch.zeros(S)
+    bias[slots[20:24]] = 2.0
+    rep = torch.rand(S, generator=g)
+    hist = torch.randint(-1, 2048, (S, W), generator=g)
+    frames = torch.randint(0, 8, (S,), generator=g)
+    min_t = torch.full((S,), 3)
+    hazard = torch.rand(S, generator=g) * 0.7
+    ctr = torch.randint(0, 100, (S,), generator=g).int()
+    u = torch.rand(B, generator=g)
+    st = [t.clone().to(gpu) for t in (hist, frames, hazard, ctr)]
+    cb0 = torch.zeros(B, dtype=torch.long, device=gpu)
+    stop = torch.zeros(B, dtype=torch.long, device=gpu)
+    codes = torch.zeros(B, 32, dtype=torch.int32, device=gpu)
+    ops.cb0_sample(logits.to(gpu), 2048, slots.to(gpu), u.to(gpu), temp_t=temp.to(gpu), topk_t=topk.to(gpu),
+                   aeos_bias=bias.to(gpu), rep_t=rep.to(gpu), hist_t=st[0], frames_t=st[1], min_t=min_t.to(gpu),
+                   hazard_t=st[2], ctr_t=st[3], cb0_out=cb0, cb0_i32=codes[:, 0], stop_out=stop)
+    bits = bf16_bits(logits)
+    for b in range(B):
+        s = int(slots[b])
+        h = hist[s].numpy().astype(np.int64).copy()
+        fr = np.array([frames[s].item()], np.int64)
+        hz = np.array([hazard[s].item()], np.float32)
+        ct = np.array([ctr[s].item()], np.int32)
+        c, sp = C.cb0_sample(bits[b], 2048, float(temp[s]), int(topk[s]), float(bias[s]), float(rep[s]), h, fr, 3, hz,
+                             ct, float(u[b]))
+        assert (c, sp) == (cb0[b].item(), stop[b].item()), b
+        assert codes[b, 0].item() == c
+        assert np.array_equal(st[0][s].cpu().numpy(), h) and st[1][s].item() == fr[0]
+        assert st[2][s].item() == hz[0] and st[3][s].item() == ct[0]
+
+
+# ---------------------------------------------------------------- Philox, feedback, index kernels
+def test_philox_known_answers_and_uniforms(gpu):
+    from m3x import ops
+    for ctr, key, expect in [([0, 0, 0, 0], [0, 0], [0x6627e8d5, 0xe169c58d, 0xbc57ac4c, 0x9b00dbd8]),
+                             ([0x243f6a88, 0x85a308d3, 0x13198a2e, 0x03707344], [0xa4093822, 0x299f31d0],
+                              [0xd16cfe09, 0x94fdcceb, 0x5001e420, 0x24126ea1])]:
+        c = torch.tensor(np.array(ctr, np.uint32).view(np.int32), device=gpu)
+        k = torch.tensor(np.array(key, np.uint32).view(np.int32), device=gpu)
+        o = torch.zeros(4, dtype=torch.int32, device=gpu)
+        ops.philox_block(c, k, o)
+        assert o.cpu().numpy().view(np.uint32).tolist() == expect
+    seeds = torch.tensor([3, 99, 2 ** 31 - 2, 12345], dtype=torch.int32)
+    ctrs = torch.tensor([0, 5, 77, 1], dtype=torch.int32)
+    slots = torch.tensor([2, 0, 3, 1, 2])
+    out = torch.zeros(5, 31, device=gpu)
+    ops.philox_uniforms(seeds.to(gpu), ctrs.to(gpu), slots.to(gpu), out, 1)
+    ref = np.array([[C.philox_uniform(int(seeds[s]), int(ctrs[s]), 1 + j) for j in range(31)] for s in slots],
+                   np.float32)
+    assert np.array_equal(out.cpu().numpy(), ref)
+
+
+def test_feedback(gpu):
+    from m3x import ops, synth
+    from oracle import torch_oracle as O
+    g = _g(31)
+    table = (torch.randn(32 * 2048, 1024, generator=g) * 0.02).to(torch.bfloat16)
+    audio_in = synth.SimpleNamespace(n_codes=2048, table=synth.Lin(table),
+                                     norm=synth.Norm(torch.ones(1024, dtype=torch.bfloat16), None))
+    codes = torch.randint(0, 2048, (6, 32), generator=g, dtype=torch.int32)
+    out = torch.empty(6, 1024, dtype=torch.bfloat16, device=gpu)
+    ops.feedback(table.to(gpu), codes.to(gpu), out, torch.ones(1024, dtype=torch.bfloat16, device=gpu),
+                 torch.finfo(torch.bfloat16).eps, 32 ** 0.5, 32, 2048)
+    ok, info = close(out, O.feedback(audio_in, codes).float(), atol=0, rel_ulps=1)
+    assert ok, info
+
+
+def test_index_kernels(gpu):
+    from m3x import ops
+    g = _g(41)
+    lengths = torch.tensor([5, 0, 17, 3, 0], device=gpu)
+    slots = torch.tensor([2, 0, 2, 4], device=gpu)
+    offset = torch.tensor([0, 0, 1, 0], device=gpu)
+    pos = torch.zeros(4, dtype=torch.int32, device=gpu)
+    ops.positions(lengths, slots, offset, pos)
+    assert pos.tolist() == [17, 5, 18, 0]
+    ops.lengths_add(lengths, slots, torch.tensor([1, 1, 1, 0], device=gpu))
+    assert lengths.tolist() == [6, 0, 19, 3, 0]
+    table = torch.randn(50, 64, generator=g).to(torch.bfloat16).to(gpu)
+    idx = torch.tensor([3, 49, 0, 7], dtype=torch.int32, device=gpu)
+    dst = torch.zeros(10, 64, dtype=torch.bfloat16, device=gpu)
+    ops.copy_rows(table, dst, src_idx=idx, dst_idx=torch.tensor([9, 0, 4, 2], device=gpu))
+    assert torch.equal(dst[[9, 0, 4, 2]], table[[3, 49, 0, 7]])
+    codes = torch.randint(0, 2048, (5, 32), dtype=torch.int32, device=gpu)
+    ring = torch.zeros(3, 8, 32, dtype=torch.int32, device=gpu)
+    head = torch.tensor([4], dtype=torch.int32, device=gpu)
+    ops.code_ring_write(codes, ring, head, 5)
+    assert torch.equal(ring[1, :5], codes) and head.item() == 5 and ring[[0, 2]].abs().sum() == 0
+    ctr = torch.zeros(6, dtype=torch.int32, device=gpu)
+    ops.ctr_add(ctr, torch.tensor([1, 5, 5, 0], device=gpu))
+    assert ctr.tolist() == [1, 1, 0, 0, 0, 2]
