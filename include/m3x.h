@@ -65,17 +65,22 @@ int m3x_decode_attn(const void* q, long sq_b, long sq_h, const void* k_cache, co
                     const int32_t* pos, float scale, int rows, int heads, int kv_heads, int head_dim, int max_ctx,
                     int chunk, void* workspace, size_t ws_bytes, void* stream);
 
-/* Bytes of workspace m3x_linear needs (0 when it runs without splitting K). */
-size_t m3x_linear_workspace(int M, int N, int K, int splits_hint);
+/* y[M,N] = x[M,K] · w[N,K]^T, 16-bit in/out, fp32 accumulation (MFMA); K % 32 == 0. Deterministic (K slices
+ * are summed in a fixed order inside the workgroup), one launch, no workspace.
+ * Replaces `F.linear` / `nn.Linear` on the path: q|k|v, o, down (serve/fast_backbone.py:193,200,202),
+ * cb0 head (tts/model/backbone.py:135-136), depth trunk and heads (serve/fast_depth.py:104,122,125,185-191). */
+int m3x_linear(const void* x, long ldx, const void* w, long ldw, void* y, long ldy, int M, int N, int K, int dtype,
+               void* stream);
 
-/* y[M,N] = x[M,K] · w[N,K]^T, 16-bit in/out, fp32 accumulation (MFMA); K % 32 == 0; splits_hint 0 = auto.
- * Replaces `F.linear` / `nn.Linear` on the path: q|k|v, o, gate|up, down (serve/fast_backbone.py:193,200-202),
- * cb0 head (tts/model/backbone.py:135-136), depth trunk and heads (serve/fast_depth.py:104,122-125,185-191). */
-int m3x_linear(const void* x, long ldx, const void* w, long ldw, void* y, long ldy, int M, int N, int K,
-               int splits_hint, void* workspace, size_t ws_bytes, int dtype, void* stream);
+/* Projection with a fused gated epilogue. kind M3X_ACT_SWIGLU: y[:, :I] = dt(dt(silu(dt(x·w_gate^T))) *
+ * dt(x·w_up^T)) with w_gate, w_up [I, K] sharing ldw; kind M3X_ACT_GELU: y[:, :I] = gelu(dt(x·w_gate^T)).
+ * Replaces `gu=F.linear(y2,wgu); g,u=gu.chunk(2,-1); F.silu(g)*u` (serve/fast_backbone.py:201-202) and
+ * `F.gelu(block.f1(y2))` (serve/fast_depth.py:123,186). */
+int m3x_linear_act(const void* x, long ldx, const void* w_gate, const void* w_up, long ldw, void* y, long ldy, int M,
+                   int I, int K, int kind, int dtype, void* stream);
 
 /* out[r, :I] = act(in[r, :]): M3X_ACT_SWIGLU: bf16(silu(g)) * u with in = [g | u] (2*I wide);
- * M3X_ACT_GELU: gelu(in[r, :I]) (erf form).
+ * M3X_ACT_GELU: gelu(in[r, :I]) (erf form), for callers that already hold the projection output.
  * Replaces `F.silu(g_)*u_` (serve/fast_backbone.py:201-202) and `F.gelu` (serve/fast_depth.py:123,186). */
 int m3x_act(const void* in, long ld_in, void* out, long ld_out, int rows, int I, int kind, int dtype, void* stream);
 
@@ -97,7 +102,7 @@ int m3x_add_rows(const void* x, long ld_x, const void* bias, long ld_bias, void*
 /* Depth self-attention over one frame's positions: qkv rows (b, t) at positions p0+t, read at
  * qkv + b*sqb + t*sqt ([q|k|v] x heads x head_dim); write_kv stores their K/V into the scratch kd/vd
  * [B, heads, np, head_dim]; queries t >= tq0 attend keys 0..p0+t; output row (b, t-tq0) at out + b*sob + tq*sot.
- * np <= 64, head_dim <= 128.
+ * np <= 64, head_dim in {64, 128}.
  * Replaces the trunk's `F.scaled_dot_product_attention` + within-group KV (serve/fast_depth.py:102-121,165-183). */
 int m3x_depth_attn(const void* qkv, long sqb, long sqt, void* kd, void* vd, void* out, long sob, long sot, int B,
                    int T, int p0, int tq0, int heads, int head_dim, int np, float scale, int write_kv, int dtype,

@@ -28,10 +28,12 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(
     const uint16_t* __restrict__ vc, long sk_s, long sk_h, long sk_t, uint16_t* __restrict__ out, long so_b,
     long so_h, const int64_t* __restrict__ slots, const int32_t* __restrict__ pos, float scale_log2, int chunk,
     float* __restrict__ part, int max_splits, int cap) {
-  const int split = blockIdx.x;
-  const int row = blockIdx.y;
-  const int kh = blockIdx.z;
-  const int KV = gridDim.z;
+  // rows vary fastest: consecutive workgroups (dispatched round-robin over the 8 XCDs) are live work, and the
+  // splits past a row's context, which exit at once, gather in the last grid slices
+  const int row = blockIdx.x;
+  const int kh = blockIdx.y;
+  const int split = blockIdx.z;
+  const int KV = gridDim.y;
   const int ps = min(pos[row], cap - 1);  // the host guarantees pos < cap; the clamp keeps every access in the slot
   const int kstart = split * chunk;
   if (kstart > ps) return;  // this split is past the row's context (uniform per block)
@@ -239,7 +241,8 @@ M3X_API int m3x_decode_attn(const void* q, long sq_b, long sq_h, const void* k_c
   }
   hipStream_t st = (hipStream_t)stream;
   const float scale_log2 = scale * 1.44269504088896341f;
-  dim3 grid(max_splits, rows, kv_heads);
+  if (rows > 65535 * 64 || kv_heads > 65535) return M3X_EINVAL;
+  dim3 grid(rows, kv_heads, max_splits);
   if (G == 2) {
     hipLaunchKernelGGL(decode_attn_kernel<2>, grid, dim3(256), 0, st, (const uint16_t*)q, sq_b, sq_h,
                        (const uint16_t*)k_cache, (const uint16_t*)v_cache, sk_s, sk_h, sk_t, (uint16_t*)out, so_b, so_h,
@@ -265,51 +268,64 @@ M3X_API int m3x_decode_attn(const void* q, long sq_b, long sq_h, const void* k_c
 // qkv rows (b, t) at positions p0 + t, read at qkv + b*sqb + t*sqt, laid out q | k | v with heads inside
 // (view(B,T,3,H,hd)). kd/vd: per-frame scratch [B, H, np, hd]. If write_kv, the T new K/V rows are stored at
 // positions p0..p0+T-1. Queries t in [tq0, T) attend keys 0..p0+t; output row (b, t - tq0) at out + b*sob + tq*sot.
-// One workgroup (64 threads) per (b, head); hd <= 128, np <= 64.
-template <int DT>
+// One workgroup (64 threads) per (b, head); HD in {64, 128}, np <= 64. Scores: lane j owns key j and reads its
+// K row as 16-byte pieces (4 independent fp32 partial sums); P.V: lane c owns dims 2c, 2c+1 (32-bit loads, rows
+// coalesced across the wave).
+template <int DT, int HD>
 __global__ __launch_bounds__(64) void depth_attn_kernel(const uint16_t* __restrict__ qkv, long sqb, long sqt,
                                                         uint16_t* kd, uint16_t* vd, uint16_t* __restrict__ out,
-                                                        long sob, long sot, int T, int p0, int tq0, int H, int hd,
-                                                        int np, float scale, int write_kv) {
+                                                        long sob, long sot, int T, int p0, int tq0, int H, int np,
+                                                        float scale, int write_kv) {
+  constexpr int VEC = HD / 8;
   const int b = blockIdx.x;
   const int h = blockIdx.y;
   const int lane = threadIdx.x;
-  uint16_t* kb = kd + ((long)b * H + h) * np * hd;
-  uint16_t* vb = vd + ((long)b * H + h) * np * hd;
+  uint16_t* kb = kd + ((long)b * H + h) * np * HD;
+  uint16_t* vb = vd + ((long)b * H + h) * np * HD;
   if (write_kv) {
-    for (int t = 0; t < T; ++t) {
-      const uint16_t* src = qkv + (long)b * sqb + (long)t * sqt;
-      for (int d = lane; d < hd; d += 64) {
-        kb[(long)(p0 + t) * hd + d] = src[(long)H * hd + h * hd + d];
-        vb[(long)(p0 + t) * hd + d] = src[2L * H * hd + h * hd + d];
-      }
+    for (int i = lane; i < T * VEC; i += 64) {
+      const int t = i / VEC, c = i % VEC;
+      const uint16_t* src = qkv + (long)b * sqb + (long)t * sqt + (long)h * HD + 8 * c;
+      st16(kb + (long)(p0 + t) * HD + 8 * c, ld16(src + (long)H * HD));
+      st16(vb + (long)(p0 + t) * HD + 8 * c, ld16(src + 2L * H * HD));
     }
     __syncthreads();
   }
-  __shared__ float qs[128];
+  __shared__ float qs[HD];
   __shared__ float ps[64];
   for (int t = tq0; t < T; ++t) {
     const int nk = p0 + t + 1;
-    const uint16_t* src = qkv + (long)b * sqb + (long)t * sqt + (long)h * hd;
-    for (int d = lane; d < hd; d += 64) qs[d] = E<DT>::to_f(src[d]);
+    const uint16_t* src = qkv + (long)b * sqb + (long)t * sqt + (long)h * HD;
+    for (int d = lane; d < HD; d += 64) qs[d] = E<DT>::to_f(src[d]);
     __syncthreads();
     float sc = -INFINITY;
     if (lane < nk) {
-      const uint16_t* kr = kb + (long)lane * hd;
-      float a = 0.f;
-      for (int d = 0; d < hd; ++d) a = fmaf(qs[d], E<DT>::to_f(kr[d]), a);
-      sc = a * scale;
+      const uint16_t* kr = kb + (long)lane * HD;
+      u16x8 kv[VEC];
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) kv[c] = ld16(kr + 8 * c);
+      float a[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < VEC; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[e & 3] = fmaf(qs[8 * c + e], E<DT>::to_f(kv[c].v[e]), a[e & 3]);
+      sc = ((a[0] + a[1]) + (a[2] + a[3])) * scale;
     }
     const float m = wave_max_xor(sc, 64);
     const float pe = lane < nk ? expf(sc - m) : 0.f;
     const float l = wave_sum_xor(pe, 64);
     ps[lane] = pe;
     __syncthreads();
-    uint16_t* o = out + (long)b * sob + (long)(t - tq0) * sot + (long)h * hd;
-    for (int d = lane; d < hd; d += 64) {
-      float a = 0.f;
-      for (int j = 0; j < nk; ++j) a = fmaf(ps[j], E<DT>::to_f(vb[(long)j * hd + d]), a);
-      o[d] = E<DT>::from_f(a / l);
+    if (2 * lane < HD) {
+      uint16_t* o = out + (long)b * sob + (long)(t - tq0) * sot + (long)h * HD + 2 * lane;
+      float a0 = 0.f, a1 = 0.f;
+      for (int j = 0; j < nk; ++j) {
+        const uint32_t v2 = *reinterpret_cast<const uint32_t*>(vb + (long)j * HD + 2 * lane);
+        a0 = fmaf(ps[j], E<DT>::to_f((uint16_t)(v2 & 0xffffu)), a0);
+        a1 = fmaf(ps[j], E<DT>::to_f((uint16_t)(v2 >> 16)), a1);
+      }
+      const uint32_t packed = (uint32_t)E<DT>::from_f(a0 / l) | ((uint32_t)E<DT>::from_f(a1 / l) << 16);
+      *reinterpret_cast<uint32_t*>(o) = packed;
     }
     __syncthreads();
   }
@@ -321,14 +337,20 @@ M3X_API int m3x_depth_attn(const void* qkv, long sqb, long sqt, void* kd, void* 
   if (B < 0 || T <= 0 || p0 < 0 || tq0 < 0 || tq0 >= T || heads <= 0) return M3X_EINVAL;
   if (B == 0) return M3X_OK;
   if (!qkv || !kd || !vd || !out) return M3X_ENULL;
-  if (head_dim <= 0 || head_dim > 128 || p0 + T > np || np > 64) return M3X_EINVAL;
+  if (p0 + T > np || np > 64) return M3X_EINVAL;
+  if (head_dim != 64 && head_dim != 128) return M3X_EUNSUPPORTED;
+  if (((sqb | sqt | sob | sot) & 7) || !m3x_aligned16(qkv) || !m3x_aligned16(kd) || !m3x_aligned16(vd) ||
+      !m3x_aligned16(out))
+    return M3X_EINVAL;
   hipStream_t st = (hipStream_t)stream;
-#define M3X_DA(DTT)                                                                                                 \
-  hipLaunchKernelGGL(depth_attn_kernel<DTT>, dim3(B, heads), dim3(64), 0, st, (const uint16_t*)qkv, sqb, sqt,      \
-                     (uint16_t*)kd, (uint16_t*)vd, (uint16_t*)out, sob, sot, T, p0, tq0, heads, head_dim, np, scale, \
+#define M3X_DA(DTT, HDD)                                                                                        \
+  hipLaunchKernelGGL((depth_attn_kernel<DTT, HDD>), dim3(B, heads), dim3(64), 0, st, (const uint16_t*)qkv, sqb, \
+                     sqt, (uint16_t*)kd, (uint16_t*)vd, (uint16_t*)out, sob, sot, T, p0, tq0, heads, np, scale,  \
                      write_kv)
-  if (dtype == M3X_BF16) M3X_DA(M3X_BF16);
-  else if (dtype == M3X_F16) M3X_DA(M3X_F16);
+  if (dtype == M3X_BF16 && head_dim == 128) M3X_DA(M3X_BF16, 128);
+  else if (dtype == M3X_BF16) M3X_DA(M3X_BF16, 64);
+  else if (dtype == M3X_F16 && head_dim == 128) M3X_DA(M3X_F16, 128);
+  else if (dtype == M3X_F16) M3X_DA(M3X_F16, 64);
   else return M3X_EUNSUPPORTED;
 #undef M3X_DA
   M3X_CHECK_LAUNCH();

@@ -31,8 +31,8 @@ SIGNATURES = {
     "m3x_decode_attn_workspace": (_Z, [_I, _I, _I, _I]),
     "m3x_decode_attn": (_I, [_P, _L, _L, _P, _P, _L, _L, _L, _I, _P, _L, _L, _P, _P, _F, _I, _I, _I, _I, _I, _I, _P,
                              _Z, _P]),
-    "m3x_linear_workspace": (_Z, [_I, _I, _I, _I]),
-    "m3x_linear": (_I, [_P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _P, _Z, _I, _P]),
+    "m3x_linear": (_I, [_P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _P]),
+    "m3x_linear_act": (_I, [_P, _L, _P, _P, _L, _P, _L, _I, _I, _I, _I, _I, _P]),
     "m3x_act": (_I, [_P, _L, _P, _L, _I, _I, _I, _I, _P]),
     "m3x_add_norm": (_I, [_P, _L, _L, _P, _L, _L, _P, _L, _P, _P, _P, _P, _F, _I, _I, _I, _I, _I, _P]),
     "m3x_add_rows": (_I, [_P, _L, _P, _L, _P, _L, _I, _I, _I, _P]),

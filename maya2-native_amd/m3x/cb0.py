@@ -71,13 +71,11 @@ class Cb0Sampler:
         b.cb0 = torch.zeros(B, dtype=torch.long, device=dev)
         b.stop = torch.zeros(B, dtype=torch.long, device=dev)
         b.codes = codes
-        lw = ops.linear_workspace(B, self.V, self.w.shape[1])
-        b.lin_ws = torch.empty(max(lw, 16) // 4, dtype=torch.float32, device=dev)
         return b
 
     def run(self, b, uniforms=True):
         """logits = h @ head^T; u from (seed_t, ctr_t, level 0); sample -> b.cb0 (and column 0 of b.codes)."""
-        ops.linear(b.h, self.w, b.logits, b.lin_ws)
+        ops.linear(b.h, self.w, b.logits)
         if uniforms:
             ops.philox_uniforms(self.seed_t, self.ctr_t, b.slots, b.u, 0)
         rep = self.any_rep and self.rep_win > 0

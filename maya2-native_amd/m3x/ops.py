@@ -113,28 +113,40 @@ def decode_attn(q, k_cache, v_cache, out, slots, pos, scale, max_ctx, chunk, wor
         "decode_attn")
 
 
-def linear_workspace(M, N, K, splits=0) -> int:
-    return int(lib().m3x_linear_workspace(M, N, K, splits))
-
-
-def linear(x, w, y=None, workspace=None, splits=0):
-    """y = x @ w.T with x [M, K], w [N, K] (16-bit, same dtype); returns y [M, N]."""
-    _dev(x, w, y, workspace)
+def _lin_args(x, w, y, N):
+    _dev(x, w, y)
     _rows2d(x, "x")
     _rows2d(w, "w")
     M, K = x.shape
-    N = w.shape[0]
     if w.shape[1] != K or w.dtype != x.dtype:
         raise ValueError(f"linear: x {tuple(x.shape)} {x.dtype} vs w {tuple(w.shape)} {w.dtype}")
     if y is None:
         y = torch.empty(M, N, dtype=x.dtype, device=x.device)
     _rows2d(y, "y")
-    need = linear_workspace(M, N, K, splits)
-    if need and workspace is None:
-        workspace = torch.empty(need // 4, dtype=torch.float32, device=x.device)
-    ws = 0 if workspace is None else workspace.numel() * workspace.element_size()
-    check(lib().m3x_linear(_p(x), x.stride(0), _p(w), w.stride(0), _p(y), y.stride(0), M, N, K, splits,
-                           _p(workspace), ws, _dt(x), _stream()), "linear")
+    if y.shape != (M, N) or y.dtype != x.dtype:
+        raise ValueError(f"linear: y {tuple(y.shape)} {y.dtype}, expected {(M, N)} {x.dtype}")
+    return M, K, y
+
+
+def linear(x, w, y=None):
+    """y = x @ w.T with x [M, K], w [N, K] (16-bit, same dtype); returns y [M, N]."""
+    N = w.shape[0]
+    M, K, y = _lin_args(x, w, y, N)
+    check(lib().m3x_linear(_p(x), x.stride(0), _p(w), w.stride(0), _p(y), y.stride(0), M, N, K, _dt(x), _stream()),
+          "linear")
+    return y
+
+
+def linear_act(x, w_gate, w_up, kind, y=None):
+    """SWIGLU: y = bf16(silu(x @ w_gate.T)) * (x @ w_up.T); GELU: y = gelu(x @ w_gate.T) (w_up None)."""
+    I = w_gate.shape[0]
+    M, K, y = _lin_args(x, w_gate, y, I)
+    if kind == ACT_SWIGLU:
+        _dev(w_up)
+        if w_up is None or w_up.shape != w_gate.shape or w_up.stride(0) != w_gate.stride(0):
+            raise ValueError("linear_act: w_up must match w_gate's shape and row stride")
+    check(lib().m3x_linear_act(_p(x), x.stride(0), _p(w_gate), _p(w_up if kind == ACT_SWIGLU else None),
+                               w_gate.stride(0), _p(y), y.stride(0), M, I, K, kind, _dt(x), _stream()), "linear_act")
     return y
 
 

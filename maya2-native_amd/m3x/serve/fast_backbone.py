@@ -22,10 +22,13 @@ from .._lib import lib
 
 
 def attn_chunk(rows: int, kv_heads: int, ctx: int) -> int:
-    """Keys per split of the decode attention: about 4096 workgroups over the context bucket, 128..1024 keys each."""
-    want = rows * kv_heads * ctx / 4096.0
-    c = 128
-    while c < want and c < 1024:
+    """Keys per split of the decode attention: about 1024 workgroups over the context bucket, 256..4096 keys each.
+
+    Measured on MI355X (graph-timed, 8 kv heads, head_dim 128): 224 rows at 2048 keys run best unsplit (one
+    workgroup per (row, kv head), no combine launch); a single row at 2048 keys runs best at 256-key splits."""
+    want = rows * kv_heads * ctx / 1024.0
+    c = 256
+    while c < want and c < 4096:
         c *= 2
     return c
 
@@ -155,16 +158,12 @@ class StaticBackbone:
         b.q = torch.empty(rows, H, D, dtype=dt, device=dev)
         b.o = torch.empty(rows, H * D, dtype=dt, device=dev)
         b.a = torch.empty(rows, hid, dtype=dt, device=dev)
-        b.gu = torch.empty(rows, 2 * I, dtype=dt, device=dev)
         b.act = torch.empty(rows, I, dtype=dt, device=dev)
         b.pend = torch.empty(rows, hid, dtype=dt, device=dev)
         b.out = torch.empty(rows, hid, dtype=dt, device=dev)
         b.chunk = attn_chunk(rows, KV, ctx)
         ws = ops.decode_attn_workspace(rows, KV, ctx, b.chunk)
         b.attn_ws = torch.empty(max(ws, 16) // 4, dtype=torch.float32, device=dev)
-        lw = max(ops.linear_workspace(rows, n, k) for n, k in
-                 (((H + 2 * KV) * D, hid), (hid, H * D), (2 * I, hid), (hid, I)))
-        b.lin_ws = torch.empty(max(lw, 16) // 4, dtype=torch.float32, device=dev)
         return b
 
     def forward(self, b):
@@ -179,16 +178,16 @@ class StaticBackbone:
                 ops.add_rms(b.x, None, layer.input_layernorm.weight, eps, y=b.y)
             else:
                 ops.add_rms(b.h, b.pend, layer.input_layernorm.weight, eps, h_out=b.h, y=b.y)
-            ops.linear(b.y, self.wqkv[i], b.qkv, b.lin_ws)
+            ops.linear(b.y, self.wqkv[i], b.qkv)
             ops.qk_norm_rope_cache(b.qkv, b.q, self.k[i], self.v[i], b.slots, b.pos, self.cos, self.sin,
                                    attn.q_norm.weight, attn.k_norm.weight, eps, H, KV)
             ops.decode_attn(b.q, self.k[i], self.v[i], o3, b.slots, b.pos, self.scaling, b.ctx, b.chunk, b.attn_ws,
                             H, KV)
-            ops.linear(b.o, attn.o_proj.weight, b.a, b.lin_ws)
+            ops.linear(b.o, attn.o_proj.weight, b.a)
             ops.add_rms(b.x if i == 0 else b.h, b.a, layer.post_attention_layernorm.weight, eps, h_out=b.h, y=b.y)
-            ops.linear(b.y, self.wgu[i], b.gu, b.lin_ws)
-            ops.act(b.gu, b.act, ops.ACT_SWIGLU)
-            ops.linear(b.act, layer.mlp.down_proj.weight, b.pend, b.lin_ws)
+            I = self.inter
+            ops.linear_act(b.y, self.wgu[i][:I], self.wgu[i][I:], ops.ACT_SWIGLU, b.act)
+            ops.linear(b.act, layer.mlp.down_proj.weight, b.pend)
         ops.add_rms(b.h, b.pend, self.norm.weight, eps, h_out=b.h, y=b.out)
         ops.lengths_add(self.lengths, b.slots, b.real)
         return b.out

@@ -104,6 +104,8 @@ class FastDepth:
                 self.cross_w = [(_w(c.kv, dtype, dev), _w(c.o, dtype, dev)) for c in self.cross]
             self.audio_in = model.audio_in  # shared, read-only (engine dtype)
             self.fb_table = model.audio_in.table.weight
+            if self.fb_table.dtype not in (torch.bfloat16, torch.float16):
+                self.fb_table = self.fb_table.detach().to(torch.bfloat16).contiguous()  # serving keeps it in bf16
             self.fb_norm = _norm(model.audio_in.norm, self.fb_table.dtype, dev)
             self.feedback_scale = math.sqrt(N_LEVELS)
             self.cross_const = torch.zeros(self.max_slots + 1, self.layers, self.D, device=dev, dtype=dtype)
@@ -152,7 +154,6 @@ class FastDepth:
         b.qkv = torch.empty(R, 3 * D, dtype=dt, device=dev)
         b.att = torch.empty(R, D, dtype=dt, device=dev)
         b.a = torch.empty(R, D, dtype=dt, device=dev)
-        b.ffn_in = torch.empty(R, 2 * Fmax, dtype=dt, device=dev)
         b.ffn_act = torch.empty(R, Fmax, dtype=dt, device=dev)
         b.f = torch.empty(R, D, dtype=dt, device=dev)
         b.kd = [torch.zeros(B, self.H, NP, self.hd, dtype=dt, device=dev) for _ in range(self.layers)]
@@ -160,12 +161,6 @@ class FastDepth:
         b.logits = torch.empty(B, self.n_codes, dtype=dt, device=dev)
         b.crossb = torch.zeros(B, self.layers * D, dtype=dt, device=dev) if self.cross_w is not None else None
         b.feedback = torch.empty(B, self.fb_table.shape[1], dtype=self.fb_table.dtype, device=dev)
-        shapes = [(D, self.in_proj.shape[1]), (self.n_codes, D)]
-        for t in self.trunks:
-            for L in t:
-                shapes += [(3 * D, D), (D, D), (L.w1.shape[0], D), (D, L.ffn)]
-        lw = max(ops.linear_workspace(m, n, k) for n, k in shapes for m in (B, R))
-        b.lin_ws = torch.empty(max(lw, 16) // 4, dtype=torch.float32, device=dev)
         return b
 
     def run(self, b, uniforms=True, trace=None):
@@ -177,7 +172,7 @@ class FastDepth:
             ops.copy_rows(self.cross_const.view(self.max_slots + 1, self.layers * D), b.crossb, src_idx=b.slots)
         if uniforms:
             ops.philox_uniforms(self.row_seed, self.row_ctr, b.slots, b.u, 1)
-        ops.linear(b.h, self.in_proj, b.tmp, b.lin_ws)
+        ops.linear(b.h, self.in_proj, b.tmp)
         ops.add_rows(b.tmp, self.level0, b.prefix[:, 0])
         ops.copy_rows(self.embed[0], b.prefix[:, 1], src_idx=b.codes[:, 0])
         scale = hd ** -0.5
@@ -198,23 +193,22 @@ class FastDepth:
                 tq0 = T - 1 if last_only else 0
                 Tq = T - tq0
                 R2 = B * Tq
-                ops.linear(b.yw[:R], L.qkv, b.qkv[:R], b.lin_ws)
+                ops.linear(b.yw[:R], L.qkv, b.qkv[:R])
                 ops.depth_attn(b.qkv[:R], b.kd[li], b.vd[li], b.att[:R2], B, T, p0, tq0, H, hd, scale, True)
-                ops.linear(b.att[:R2], L.o, b.a[:R2], b.lin_ws)
+                ops.linear(b.att[:R2], L.o, b.a[:R2])
                 x_res = b.xw[:R].view(B, T, D)[:, tq0:]
                 ops.add_norm(x_res, b.a[:R2], None, b.xw2[:R2], b.y2[:R2], L.n2.w, L.n2.b, L.n2.eps, Tq, L.n2.kind)
                 F = L.ffn
                 if L.act == ops.ACT_SWIGLU:
-                    ops.linear(b.y2[:R2], L.w1, b.ffn_in[:R2, :2 * F], b.lin_ws)
+                    ops.linear_act(b.y2[:R2], L.w1[:F], L.w1[F:], L.act, b.ffn_act[:R2, :F])
                 else:
-                    ops.linear(b.y2[:R2], L.w1, b.ffn_in[:R2, :F], b.lin_ws)
-                ops.act(b.ffn_in[:R2], b.ffn_act[:R2, :F], L.act)
-                ops.linear(b.ffn_act[:R2, :F], L.w2, b.f[:R2], b.lin_ws)
+                    ops.linear_act(b.y2[:R2], L.w1, None, L.act, b.ffn_act[:R2, :F])
+                ops.linear(b.ffn_act[:R2, :F], L.w2, b.f[:R2])
                 nxt = layers[li + 1].n1 if li + 1 < self.layers else self.final_norm
                 c = b.crossb[:, li * D:(li + 1) * D] if b.crossb is not None else None
                 ops.add_norm(b.xw2[:R2], b.f[:R2], c, b.xw[:R2], b.yw[:R2], nxt.w, nxt.b, nxt.eps, Tq, nxt.kind)
                 R, T, p0 = R2, Tq, p0 + tq0
-            ops.linear(b.yw[:B], self.heads[level - 1], b.logits, b.lin_ws)
+            ops.linear(b.yw[:B], self.heads[level - 1], b.logits)
             if trace is not None:
                 trace.append(b.logits.clone())
             ops.topk_sample(b.logits, b.u[:, level - 1], inv_temp, self.top_k, self.greedy, b.codes[:, level])

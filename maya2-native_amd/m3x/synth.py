@@ -140,12 +140,13 @@ def depthv2_like(d_backbone=1024, d=1024, heads=16, ffn=3072, layers=4, n_q=32, 
     cross = [SimpleNamespace(kv=Lin(_normal(g, (2 * d, d), std, device, dtype)),
                              o=Lin(_normal(g, (d, d), std, device, dtype))) for _ in range(layers)]
     heads_l = [Lin(_normal(g, (n_codes, d), std, device, dtype)) for _ in range(n_q - 1)]
-    table = _normal(g, (n_q * n_codes, d_backbone), std, device, dtype)
+    # the backbone-side feedback embedding lives at the engine dtype (bf16), whatever the depth's
+    table = _normal(g, (n_q * n_codes, d_backbone), std, device, torch.bfloat16)
     depth = SimpleNamespace(n_q=n_q, n_codes=n_codes, n_heads=heads, in_proj=in_proj, code_lo=code_lo,
                             code_up=code_up, level_emb=level_emb, groups=groups, group_of_level=list(gol),
                             norm=ln(), heads=heads_l, cross=cross)
     audio_in = SimpleNamespace(n_q=n_q, n_codes=n_codes, table=Lin(table),
-                               norm=Norm(torch.ones(d_backbone, dtype=dtype, device=device),
+                               norm=Norm(torch.ones(d_backbone, dtype=torch.bfloat16, device=device),
                                          torch.finfo(torch.bfloat16).eps))
     return SimpleNamespace(depth=depth, audio_in=audio_in)
 

@@ -54,9 +54,13 @@ def rope_tables(head_dim, theta, cap, dtype):
     return emb.cos().to(dtype), emb.sin().to(dtype)
 
 
-def backbone_step(bb, kc, vc, lengths, slots, x, cos, sin, offset=None, real=None, ctx=None):
+def backbone_step(bb, kc, vc, lengths, slots, x, cos, sin, offset=None, real=None, ctx=None, attention='triton'):
     """One decode step. bb: synth/HF-shaped backbone (CPU tensors); kc/vc: lists of [S+1, KV, cap, D] caches
-    (updated in place); lengths [S+1] long (updated); slots [R] long; x [R, hidden]. Returns the normed hidden."""
+    (updated in place); lengths [S+1] long (updated); slots [R] long; x [R, hidden]. Returns the normed hidden.
+    attention='triton': the engine's attention (`_decode_attn`, serve/fast_backbone.py:31-58: fp32 scores, fp32
+    softmax and fp32 P.V, one rounding of the output) — the configuration the reference's own parity test uses as
+    its unfused baseline (maya3/tests/test_backbone_fused.py:16-17); attention='gather': the eager gather branch
+    (:215-218: bf16 scores, bf16 probabilities)."""
     cfg = bb.lm.config
     H, KV = cfg.num_attention_heads, cfg.num_key_value_heads
     D = getattr(cfg, 'head_dim', None) or cfg.hidden_size // H
@@ -86,9 +90,13 @@ def backbone_step(bb, kc, vc, lengths, slots, x, cos, sin, offset=None, real=Non
         vc[i][slots, :, pos] = v
         K = kc[i][:, :, :ctx].index_select(0, slots)
         V = vc[i][:, :, :ctx].index_select(0, slots)
-        scores = torch.matmul(q.view(B, KV, G, D).float(), K.float().transpose(-1, -2)).to(q.dtype).float()
-        scores = scores * scaling + bias
-        o = torch.matmul(scores.softmax(-1).to(q.dtype).float(), V.float()).to(q.dtype).reshape(B, H * D)
+        scores = torch.matmul(q.view(B, KV, G, D).float(), K.float().transpose(-1, -2))
+        if attention == 'gather':
+            scores = scores.to(q.dtype).float() * scaling + bias
+            o = torch.matmul(scores.softmax(-1).to(q.dtype).float(), V.float()).to(q.dtype).reshape(B, H * D)
+        else:
+            scores = scores * scaling + bias
+            o = torch.matmul(scores.softmax(-1), V.float()).to(q.dtype).reshape(B, H * D)
         h = h + lin(o, a.o_proj.weight)
         y2 = rms_hf(h, layer.post_attention_layernorm.weight, eps)
         m = layer.mlp

@@ -26,3 +26,42 @@ def close(a, b, atol=2e-2, min_cos=0.9995, rel_ulps=2):
     cos = torch.nn.functional.cosine_similarity(a[None], b[None]).item()
     worst = (err - bound).max().item()
     return worst <= 0 and cos >= min_cos, dict(max_abs=err.max().item(), cos=cos, worst_over_bound=worst)
+
+
+def rel_l2(a, b):
+    a = a.detach().float().cpu()
+    b = b.detach().float().cpu()
+    return ((a - b).norm() / b.norm()).item()
+
+
+def floor_check(got, ref16, truth, min_cos=0.9995):
+    """The reference's fused-vs-unfused bar (maya3/tests/test_backbone_fused.py:12-46) with an fp32 truth:
+    the kernel's relative L2 error against the fp32 evaluation of the same math must stay within twice that of
+    the bf16 eager oracle (the bf16 noise floor) or 1e-3, and its cosine to the eager oracle >= min_cos."""
+    import torch
+    floor = rel_l2(ref16, truth)
+    err = rel_l2(got, truth)
+    a = got.detach().float().cpu().flatten()
+    b = ref16.detach().float().cpu().flatten()
+    cos = torch.nn.functional.cosine_similarity(a[None], b[None]).item()
+    info = dict(rel_err=err, floor=floor, cos=cos, max_abs_vs_oracle=(a - b).abs().max().item())
+    return err <= max(2 * floor, 1e-3) and cos >= min_cos, info
+
+
+def convert(obj, dtype):
+    """Copy of a synth model tree with every floating tensor cast to dtype (integer tensors kept)."""
+    import copy
+    import torch
+
+    def f(o):
+        if isinstance(o, torch.Tensor):
+            return o.to(dtype) if o.is_floating_point() else o
+        if isinstance(o, list):
+            return [f(x) for x in o]
+        if hasattr(o, "__dict__") and not callable(o):
+            new = copy.copy(o)
+            for k, v in vars(o).items():
+                setattr(new, k, f(v))
+            return new
+        return o
+    return f(obj)

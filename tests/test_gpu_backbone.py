@@ -2,7 +2,7 @@
 import pytest
 import torch
 
-from helpers import close
+from helpers import close, convert, floor_check
 from m3x import synth
 from oracle import torch_oracle as O
 
@@ -32,34 +32,43 @@ def _setup(gpu, use_graphs=True):
         sb.load_prefix(s, kv, n)
     lengths = torch.tensor(PREFIX + [0])
     cos, sin = O.rope_tables(128, 1e6, CAP, torch.bfloat16)
-    return sb, bb_c, kc, vc, lengths, cos, sin
+    # fp32 evaluation of the same math on the same (bf16-valued) weights and cache: the truth for the floor
+    truth = dict(bb=convert(bb_c, torch.float32), kc=[t.float() for t in kc], vc=[t.float() for t in vc],
+                 lengths=lengths.clone(), cos=cos.float(), sin=sin.float())
+    return sb, bb_c, kc, vc, lengths, cos, sin, truth
+
+
+def _truth_step(T, slots, x, offset=None):
+    return O.backbone_step(T["bb"], T["kc"], T["vc"], T["lengths"], slots, x.float(), T["cos"], T["sin"],
+                           offset=offset)
 
 
 def test_step_matches_oracle(gpu):
-    sb, bb_c, kc, vc, lengths, cos, sin = _setup(gpu)
+    sb, bb_c, kc, vc, lengths, cos, sin, T = _setup(gpu)
     g = torch.Generator().manual_seed(23)
     slots = [0, 2, 3, 4]
     for t in range(3):
         x = torch.randn(len(slots), 1024, generator=g).to(torch.bfloat16)
         out = sb.step(slots, x.to(gpu))
         ref = O.backbone_step(bb_c, kc, vc, lengths, torch.tensor(slots), x, cos, sin)
-        ok, info = close(out, ref)
+        truth = _truth_step(T, torch.tensor(slots), x)
+        ok, info = floor_check(out, ref, truth)
         assert ok, (t, info)
     assert sb.lengths.cpu().tolist() == lengths.tolist() and sb.lengths_cpu == lengths.tolist()
     assert sb.lengths[S].item() == 0
     for i in range(LAYERS):
         for s in slots:
-            n = int(lengths[s])
-            ok, info = close(sb.k[i][s, :, :n], kc[i][s, :, :n])
-            assert ok, (i, s, info)
-            ok, info = close(sb.v[i][s, :, :n], vc[i][s, :, :n])
-            assert ok, (i, s, info)
+            n0, n = PREFIX[s], int(lengths[s])
+            assert torch.equal(sb.k[i][s, :, :n0].cpu(), kc[i][s, :, :n0])  # the prefix is untouched
+            for name, got, ref, tr in (("k", sb.k[i], kc[i], T["kc"][i]), ("v", sb.v[i], vc[i], T["vc"][i])):
+                ok, info = floor_check(got[s, :, n0:n], ref[s, :, n0:n], tr[s, :, n0:n])
+                assert ok, (name, i, s, info)
         # slots that did not step are untouched
         assert torch.equal(sb.k[i][1].cpu(), kc[i][1]) and torch.equal(sb.k[i][5].cpu(), kc[i][5])
 
 
 def test_step_mixed_prefill_matches_oracle(gpu):
-    sb, bb_c, kc, vc, lengths, cos, sin = _setup(gpu)
+    sb, bb_c, kc, vc, lengths, cos, sin, T = _setup(gpu)
     g = torch.Generator().manual_seed(24)
     x = torch.randn(2, 1024, generator=g).to(torch.bfloat16)
     p5 = (torch.randn(20, 1024, generator=g) * 0.5).to(torch.bfloat16)
@@ -68,14 +77,15 @@ def test_step_mixed_prefill_matches_oracle(gpu):
     slots = torch.tensor([0, 3] + [5] * 20 + [1] * 7)
     offset = torch.tensor([0, 0] + list(range(20)) + list(range(7)))
     ref = O.backbone_step(bb_c, kc, vc, lengths, slots, torch.cat([x, p5, p1]), cos, sin, offset=offset)
-    ok, info = close(dec, ref[:2])
-    assert ok, info
-    ok, info = close(torch.stack(last), ref[[21, 28]])
+    truth = _truth_step(T, slots, torch.cat([x, p5, p1]), offset=offset)
+    ok, info = floor_check(torch.cat([dec, torch.stack(last)]), ref[[0, 1, 21, 28]], truth[[0, 1, 21, 28]])
     assert ok, info
     assert sb.lengths_cpu[:S] == [1, 8, 37, 201, 300, 20] == lengths[:S].tolist()
     # the next decode step of the prefilled slot continues from its new length
     y = torch.randn(1, 1024, generator=g).to(torch.bfloat16)
-    ok, info = close(sb.step([5], y.to(gpu)), O.backbone_step(bb_c, kc, vc, lengths, torch.tensor([5]), y, cos, sin))
+    out = sb.step([5], y.to(gpu))
+    ok, info = floor_check(out, O.backbone_step(bb_c, kc, vc, lengths, torch.tensor([5]), y, cos, sin),
+                           _truth_step(T, torch.tensor([5]), y))
     assert ok, info
 
 

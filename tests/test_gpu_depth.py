@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import bf16_bits, close
+from helpers import bf16_bits, close, convert, floor_check
 from m3x import synth
 from oracle import coracle as C
 from oracle import torch_oracle as O
@@ -45,9 +45,12 @@ def _check(fd, model_c, h, cb0, gpu, dt, temp, top_k, cross=None, logit_tol=None
                                  is_f16=dt == torch.float16)
         assert np.array_equal(codes[:, lv].numpy(), ref), lv
     assert torch.equal(codes[:, 0], cb0)
-    # logits: teacher-forced CPU oracle on the same codes
+    # logits: teacher-forced CPU oracle on the same codes, against the fp32 evaluation's noise floor
     _, ref_logits = O.depth_frame(model_c, h, cb0, u, temp, top_k, forced=codes, cross=cross, dt=dt)
-    ok, info = close(logits, ref_logits.float(), **(logit_tol or {}))
+    m32 = convert(model_c, torch.float32)
+    _, truth = O.depth_frame(m32, h.float(), cb0, u, temp, top_k, forced=codes,
+                             cross=None if cross is None else cross.float(), dt=torch.float32)
+    ok, info = floor_check(logits, ref_logits, truth)
     assert ok, info
     ok, info = close(fb, O.feedback(model_c.audio_in, codes).float())
     assert ok, info

@@ -30,14 +30,50 @@ def test_linear_bf16(gpu, M, N, K):
     assert ok, info
 
 
-@pytest.mark.parametrize("splits", [1, 2, 3, 8])
-def test_linear_fp16_and_forced_splits(gpu, splits):
+@pytest.mark.parametrize("M,N,K", [(24, 3072, 1024), (1, 2816, 1024), (3, 1024, 96)])
+def test_linear_fp16(gpu, M, N, K):
     from m3x import ops
-    g = _g(splits)
-    x = torch.randn(24, 1024, generator=g).to(torch.float16)
-    w = (torch.randn(3072, 1024, generator=g) * 0.02).to(torch.float16)
-    y = ops.linear(x.to(gpu), w.to(gpu), splits=splits)
+    g = _g(M + K)
+    x = torch.randn(M, K, generator=g).to(torch.float16)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.float16)
+    y = ops.linear(x.to(gpu), w.to(gpu))
     ok, info = close(y, x.float() @ w.float().t(), atol=1e-2)
+    assert ok, info
+
+
+@pytest.mark.parametrize("M,I,K,dtype", [(1, 3072, 1024, torch.bfloat16), (224, 2816, 1024, torch.bfloat16),
+                                         (37, 3072, 1024, torch.float16)])
+def test_linear_swiglu_epilogue(gpu, M, I, K, dtype):
+    """Fused gate|up GEMM + silu*mul against the separate GEMM + activation kernel (the two launches may slice K
+    differently, so the fp32 sums can round apart by an ulp) and against an fp32 reference."""
+    from m3x import ops
+    g = _g(M + I)
+    x = torch.randn(M, K, generator=g).to(dtype).to(gpu)
+    wgu = (torch.randn(2 * I, K, generator=g) * 0.02).to(dtype).to(gpu)
+    fused = ops.linear_act(x, wgu[:I], wgu[I:], ops.ACT_SWIGLU)
+    gu = ops.linear(x, wgu)
+    sep = torch.empty(M, I, dtype=dtype, device=gpu)
+    ops.act(gu, sep, ops.ACT_SWIGLU)
+    # near-zero outputs come from cancelling sums, where one fp32 ulp of the sum is many ulps of the result
+    ok, info = close(fused, sep.float(), atol=1e-3, rel_ulps=2)
+    assert ok, info
+    ref = torch.nn.functional.silu((x.float() @ wgu[:I].float().t()).to(dtype).float()).to(dtype).float() * \
+        (x.float() @ wgu[I:].float().t()).to(dtype).float()
+    ok, info = close(fused, ref.cpu(), atol=1e-2)
+    assert ok, info
+
+
+def test_linear_gelu_epilogue(gpu):
+    from m3x import ops
+    g = _g(77)
+    x = torch.randn(9, 1024, generator=g).to(torch.float16).to(gpu)
+    w = (torch.randn(3072, 1024, generator=g) * 0.02).to(torch.float16).to(gpu)
+    fused = ops.linear_act(x, w, None, ops.ACT_GELU)
+    sep = torch.empty(9, 3072, dtype=torch.float16, device=gpu)
+    ops.act(ops.linear(x, w), sep, ops.ACT_GELU)
+    ok, info = close(fused, sep.float(), atol=1e-3, rel_ulps=2)
+    assert ok, info
+    ok, info = close(fused, torch.nn.functional.gelu(x.float() @ w.float().t()).cpu(), atol=1e-2)
     assert ok, info
 
 

@@ -1,0 +1,82 @@
+"""Host-side logic that needs no GPU: launch planning, workload formulas, cache interop, surface errors."""
+import os
+import subprocess
+import sys
+
+import pytest
+import torch
+
+from m3x import roofline, synth
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_attn_chunk_plan():
+    from m3x.serve.fast_backbone import attn_chunk
+    assert attn_chunk(1, 8, 2048) == 256          # one row: 8 splits per kv head to spread over the chip
+    assert attn_chunk(224, 8, 2048) == 4096       # 224 rows: 1792 workgroups unsplit, no combine launch
+    for rows, ctx in [(1, 512), (64, 2048), (2264, 4096)]:
+        c = attn_chunk(rows, 8, ctx)
+        assert c % 128 == 0 and 256 <= c <= 4096
+
+
+def test_roofline_matches_published_shapes():
+    # BASELINE: backbone weights 880,803,840 B; 112 KiB of KV per token per seat
+    assert roofline.backbone_weight_bytes() == 880_803_840
+    assert roofline.decode_attn_bytes(1, 0) * 28 == 112 * 1024
+    # per depth codebook step: trunk 102,760,448 B + head 4,194,304 B
+    assert roofline.depth_frame_bytes(seats=0) == 31 * (102_760_448 + 4_194_304) + 1024 * 1024 * 2
+
+
+def test_synth_is_seeded_and_shaped():
+    a = synth.qwen3_backbone(layers=1, seed=3)
+    b = synth.qwen3_backbone(layers=1, seed=3)
+    la, lb = a.lm.model.layers[0], b.lm.model.layers[0]
+    assert torch.equal(la.self_attn.q_proj.weight, lb.self_attn.q_proj.weight)
+    assert la.self_attn.q_proj.weight.shape == (2048, 1024) and la.mlp.down_proj.weight.shape == (1024, 3072)
+    assert a.cb0_head.weight.shape == (2048, 1024)
+    lens = synth.c5_lengths(224)
+    assert lens.shape == (224,) and 1900 < float(lens.float().mean()) < 2200 and int(lens.max()) <= 4096
+    c4 = synth.c4_decode_lengths()
+    assert c4.min() >= 128 and c4.max() < 4096
+
+
+def test_cache_pack_split_roundtrip():
+    from m3x.serve.cache import cache_from_owned_tensors, pack_caches, split_cache
+    g = torch.Generator().manual_seed(1)
+    caches = []
+    for n in (3, 0, 5):
+        if n == 0:
+            caches.append(None)
+            continue
+        caches.append(cache_from_owned_tensors([(torch.randn(1, 2, n, 4, generator=g), torch.randn(1, 2, n, 4,
+                                                                                              generator=g))
+                                                for _ in range(2)]))
+    packed, mask, lengths = pack_caches(caches, 2, "cpu")
+    assert lengths == [3, 0, 5] and packed.layers[0].keys.shape == (3, 2, 5, 4)
+    assert mask.shape == (3, 7) and mask[0].tolist() == [False, False, True, True, True, True, True]
+    rows = split_cache(packed, lengths)
+    for c, r, n in zip(caches, rows, lengths):
+        if n:
+            for la, lb in zip(c.layers, r.layers):
+                assert torch.equal(la.keys, lb.keys) and torch.equal(la.values, lb.values)
+
+
+def test_surfaces_reject_host_models():
+    from m3x.serve.fast_backbone import StaticBackbone
+    from m3x.serve.fast_depth import FastDepth
+    with pytest.raises(ValueError):
+        StaticBackbone(synth.qwen3_backbone(layers=1), 2, attention="gather")
+    with pytest.raises(ValueError):
+        StaticBackbone(synth.qwen3_backbone(layers=1), 2, attention="flash")
+    with pytest.raises(ValueError):
+        StaticBackbone(synth.qwen3_backbone(layers=1, dtype=torch.float32), 2)
+    small = synth.swiglu_depth(d=1024, n_q=16)
+    with pytest.raises(ValueError):
+        FastDepth(small, 2)
+
+
+def test_bench_refuses_multi_gpu():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2 and "one GPU" in r.stderr
