@@ -65,18 +65,27 @@ int m3x_decode_attn(const void* q, long sq_b, long sq_h, const void* k_cache, co
                     const int32_t* pos, float scale, int rows, int heads, int kv_heads, int head_dim, int max_ctx,
                     int chunk, void* workspace, size_t ws_bytes, void* stream);
 
-/* y[M,N] = x[M,K] · w[N,K]^T, 16-bit in/out, fp32 accumulation (MFMA); K % 32 == 0. Deterministic (K slices
- * are summed in a fixed order inside the workgroup), one launch, no workspace.
+/* Elements of the packed form of an [N, K] weight (N rounded up to a multiple of 16, times K); -1 if K % 32. */
+long m3x_packed_weight_elems(int N, int K);
+
+/* Packs w[N, K] (row stride ldw, 16-bit) into MFMA fragment order for m3x_linear / m3x_linear_act: the 16 x 32
+ * fragment (row tile t, k step s) is 1 KB at element (t * K/32 + s) * 512, lane l's 8 values at + 8 l holding
+ * w[16 t + l % 16][32 s + 8 (l / 16) + e]; rows past N are zero. Done once per weight at load time.
+ * Replaces nothing at run time: the reference multiplies nn.Linear weights in place (F.linear). */
+int m3x_pack_weight(const void* w, long ldw, int N, int K, void* out, void* stream);
+
+/* y[M,N] = x[M,K] · w[N,K]^T with w packed by m3x_pack_weight; 16-bit in/out, fp32 accumulation (MFMA);
+ * K % 32 == 0. Deterministic (K slices are summed in a fixed order inside the workgroup), one launch, no workspace.
  * Replaces `F.linear` / `nn.Linear` on the path: q|k|v, o, down (serve/fast_backbone.py:193,200,202),
  * cb0 head (tts/model/backbone.py:135-136), depth trunk and heads (serve/fast_depth.py:104,122,125,185-191). */
-int m3x_linear(const void* x, long ldx, const void* w, long ldw, void* y, long ldy, int M, int N, int K, int dtype,
+int m3x_linear(const void* x, long ldx, const void* w_packed, void* y, long ldy, int M, int N, int K, int dtype,
                void* stream);
 
-/* Projection with a fused gated epilogue. kind M3X_ACT_SWIGLU: y[:, :I] = dt(dt(silu(dt(x·w_gate^T))) *
- * dt(x·w_up^T)) with w_gate, w_up [I, K] sharing ldw; kind M3X_ACT_GELU: y[:, :I] = gelu(dt(x·w_gate^T)).
+/* Projection with a fused gated epilogue, weights packed by m3x_pack_weight. kind M3X_ACT_SWIGLU:
+ * y[:, :I] = dt(dt(silu(dt(x·wg^T))) * dt(x·wu^T)) with wg, wu [I, K]; kind M3X_ACT_GELU: y[:, :I] = gelu(dt(x·wg^T)).
  * Replaces `gu=F.linear(y2,wgu); g,u=gu.chunk(2,-1); F.silu(g)*u` (serve/fast_backbone.py:201-202) and
  * `F.gelu(block.f1(y2))` (serve/fast_depth.py:123,186). */
-int m3x_linear_act(const void* x, long ldx, const void* w_gate, const void* w_up, long ldw, void* y, long ldy, int M,
+int m3x_linear_act(const void* x, long ldx, const void* wg_packed, const void* wu_packed, void* y, long ldy, int M,
                    int I, int K, int kind, int dtype, void* stream);
 
 /* out[r, :I] = act(in[r, :]): M3X_ACT_SWIGLU: bf16(silu(g)) * u with in = [g | u] (2*I wide);

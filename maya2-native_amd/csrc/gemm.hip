@@ -3,12 +3,18 @@
 // serve/fast_backbone.py:193,200-202 (q|k|v, o, gate|up + silu*mul, down), the cb0 head
 // (tts/model/backbone.py:135-136) and the depth trunk/heads (serve/fast_depth.py:104,122-125,167,185-191).
 //
-// The decode shapes are skinny (M = seats, 1..2264). W is the MFMA A operand (16 weight rows per wave,
-// 16 contiguous bytes per lane per 32-k step), the activations the B operand (16*MT rows per wave). A workgroup
-// has 4 waves arranged as NW weight-row tiles x KW = 4/NW slices of K; the KW partial sums meet in LDS and are
-// added in slice order, so the result does not depend on scheduling and no second launch or workspace is needed.
-// The k loop keeps the next 4 k-steps of loads in flight while the current 4 run on the MFMAs.
-// Blocks are ordered m-fastest, so the M tiles that share a weight slab are dispatched together.
+// Weights are packed once (m3x_pack_weight) into MFMA fragment order: the 16 x 32 fragment (row tile nt, k step s)
+// occupies 1 KB at element offset (nt * K/32 + s) * 512 and lane l's 8 elements sit at + 8 l, holding
+// W[16 nt + l % 16][32 s + 8 (l / 16) + e] - exactly the A operand of v_mfma_f32_16x16x32. A wave reads a
+// fragment as one contiguous 1 KB (16 bytes per lane, in lane order), which the vector L1 serves as 16 cache-line
+// accesses; the row-major operand pattern (16 rows per instruction) costs 64.
+//
+// Activations are the B operand. A workgroup (4 waves = NW weight tiles x KW = 4/NW slices of K) stages the
+// 16*MT activation rows of each 128-wide K chunk in LDS with row-contiguous loads, double-buffered, and every
+// wave reads its fragments from there. Weight fragments run two chunks ahead in registers, activations three.
+// The KW partial sums meet in LDS and are added in slice order: the result is independent of scheduling.
+// Workgroups are numbered so that the row blocks sharing one weight slab run on one XCD (ids equal mod 8) and
+// the slab is fetched into that XCD's L2 once.
 //
 // Epilogues (each rounds exactly where the reference's eager ops round):
 //   EPI_NONE    y = dt(acc)
@@ -19,107 +25,167 @@
 
 enum { EPI_NONE = 0, EPI_SWIGLU = 1, EPI_GELU = 2 };
 
+__global__ __launch_bounds__(256) void pack_weight_kernel(const uint16_t* __restrict__ W, long ldw, int N, int K,
+                                                          uint16_t* __restrict__ out) {
+  const long v = (long)blockIdx.x * 256 + threadIdx.x;  // one 16-byte lane vector of the packed layout
+  const int ks = K >> 5;
+  const long total = (long)((N + 15) >> 4) * ks * 64;
+  if (v >= total) return;
+  const int lane = (int)(v & 63);
+  const long f = v >> 6;
+  const int s = (int)(f % ks);
+  const int n = (int)(f / ks) * 16 + (lane & 15);
+  u16x8 x;
+  if (n < N) {
+    x = ld16(W + (long)n * ldw + s * 32 + 8 * (lane >> 4));
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x.v[e] = 0;
+  }
+  st16(out + v * 8, x);
+}
+
 template <int DT, int MT, int NW, int EPI>
 __global__ __launch_bounds__(256) void linear_kernel(const uint16_t* __restrict__ X, long ldx,
-                                                     const uint16_t* __restrict__ W, const uint16_t* __restrict__ W2,
-                                                     long ldw, uint16_t* __restrict__ Y, long ldy, int M, int N,
-                                                     int K, int mfast) {
+                                                     const uint16_t* __restrict__ Wp,
+                                                     const uint16_t* __restrict__ W2p, uint16_t* __restrict__ Y,
+                                                     long ldy, int M, int N, int K, int mblk, int nblk) {
   constexpr int KW = 4 / NW;
-  constexpr int U = 4;
+  static_assert(MT * KW <= 4, "activation chunks must fit the LDS budget");
+  constexpr int U = 4;                 // k steps (of 32) per chunk
+  constexpr int ROWS = 16 * MT;
+  constexpr int LDR = 32 * U + 8;      // LDS row stride in halfwords: 272 bytes, conflict-free fragment reads
+  constexpr int VPR = 4 * U;           // 16-byte vectors per row per chunk
+  constexpr int NVEC = KW * ROWS * VPR;
+  constexpr int VPT = (NVEC + 255) / 256;
   constexpr bool DUAL = EPI == EPI_SWIGLU;
   constexpr int NA = DUAL ? 2 : 1;
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
+  __shared__ __align__(16) uint16_t xs[2][KW * ROWS * LDR];
+
+  const int xcd = blockIdx.x & 7;
+  const int slot = blockIdx.x >> 3;
+  const int nb = (slot / mblk) * 8 + xcd;
+  const int mb = slot - (slot / mblk) * mblk;
+  if (nb >= nblk) return;  // padding block: the whole workgroup leaves before any barrier
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
   const int li = lane & 15;
   const int lg = lane >> 4;
   const int wn = wave % NW;
   const int wk = wave / NW;
-  const int mblock = mfast ? blockIdx.x : blockIdx.y;
-  const int nblock = mfast ? blockIdx.y : blockIdx.x;
-  const int n0 = (nblock * NW + wn) * 16;
-  const int mbase = mblock * (16 * MT);
-  const int ksteps = K / 32;
-  const int per = (ksteps + KW - 1) / KW;
-  const int s0 = wk * per;
-  const int s1 = min(ksteps, s0 + per);
+  const int ntiles = (N + 15) >> 4;
+  const int n0 = (nb * NW + wn) * 16;
+  const int nt = min(nb * NW + wn, ntiles - 1);  // tiles past N read a valid tile; nothing of them is stored
+  const int m0 = mb * ROWS;
+  const int ksteps = K >> 5;
+  const int nch = ((ksteps + KW - 1) / KW + U - 1) / U;  // chunks per slice (equal for all slices)
+  const int span = nch * U;
+  const int s0 = wk * span;
+  const int s1 = min(ksteps, s0 + span);
 
-  const int nrow = n0 + li;
-  const bool nvalid = nrow < N;
   const uint16_t* wp[NA];
-  wp[0] = W + (long)(nvalid ? nrow : 0) * ldw + 8 * lg;
-  if constexpr (DUAL) wp[NA - 1] = W2 + (long)(nvalid ? nrow : 0) * ldw + 8 * lg;
-  const uint16_t* xp[MT];
-  bool mvalid[MT];
+  wp[0] = Wp + ((long)nt * ksteps * 64 + lane) * 8;
+  if constexpr (DUAL) wp[NA - 1] = W2p + ((long)nt * ksteps * 64 + lane) * 8;
+
+  // Activation vectors: v = tid + 256 j -> slice q, row r, 16-byte column c16 of the chunk. Rows past M and
+  // steps past a slice are not loaded: their registers keep finite earlier values, whose products are never
+  // stored.
+  u16x8 X0[VPT], X1[VPT];
 #pragma unroll
-  for (int t = 0; t < MT; ++t) {
-    const int m = mbase + 16 * t + li;
-    mvalid[t] = m < M;
-    xp[t] = X + (long)(mvalid[t] ? m : 0) * ldx + 8 * lg;
-  }
-  // Rows past N or M read a valid (clamped) row and their results are never stored, so no loaded value is
-  // ever inspected before its MFMA: the loads of the next group stay in flight behind the current group.
+  for (int j = 0; j < VPT; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) X0[j].v[e] = X1[j].v[e] = 0;
+  auto xload = [&](int c, u16x8(&Xr)[VPT]) {
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int v = tid + 256 * j;
+      if (NVEC % 256 == 0 || v < NVEC) {
+        const int q = v / (ROWS * VPR);
+        const int rem = v - q * (ROWS * VPR);
+        const int r = rem / VPR;
+        const int c16 = rem - r * VPR;
+        const int m = m0 + r;
+        const int step = q * span + c * U + (c16 >> 2);
+        if (m < M && step < min(ksteps, (q + 1) * span)) Xr[j] = ld16(X + (long)m * ldx + step * 32 + (c16 & 3) * 8);
+      }
+    }
+  };
+  auto xstore = [&](int buf, const u16x8(&Xr)[VPT]) {
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int v = tid + 256 * j;
+      if (NVEC % 256 == 0 || v < NVEC) {
+        const int q = v / (ROWS * VPR);
+        const int rem = v - q * (ROWS * VPR);
+        const int r = rem / VPR;
+        const int c16 = rem - r * VPR;
+        st16(&xs[buf][(q * ROWS + r) * LDR + c16 * 8], Xr[j]);
+      }
+    }
+  };
+  u16x8 W0[U][NA], W1[U][NA];
+  auto wload = [&](int c, u16x8(&Wr)[U][NA]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int s = min(s0 + c * U + u, ksteps - 1);  // past the slice: a valid fragment, never multiplied
+#pragma unroll
+      for (int a = 0; a < NA; ++a) Wr[u][a] = ld16(wp[a] + (long)s * 512);
+    }
+  };
   f32x4_t acc[NA][MT];
 #pragma unroll
   for (int a = 0; a < NA; ++a)
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[a][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  auto load = [&](int st, u16x8(&A)[U][NA], u16x8(&Bv)[U][MT]) {
+  auto compute = [&](int c, int buf, const u16x8(&Wr)[U][NA]) {
+    const uint16_t* xb = &xs[buf][(wk * ROWS + li) * LDR + 8 * lg];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int k = (st + u) * 32;
+      if (s0 + c * U + u < s1) {
 #pragma unroll
-      for (int a = 0; a < NA; ++a) A[u][a] = ld16(wp[a] + k);
+        for (int t = 0; t < MT; ++t) {
+          const u16x8 b = *reinterpret_cast<const u16x8*>(xb + t * 16 * LDR + u * 32);
 #pragma unroll
-      for (int t = 0; t < MT; ++t) Bv[u][t] = ld16(xp[t] + k);
+          for (int a = 0; a < NA; ++a) acc[a][t] = mfma16x16x32<DT>(Wr[u][a], b, acc[a][t]);
+        }
+      }
     }
   };
-  auto compute = [&](const u16x8(&A)[U][NA], const u16x8(&Bv)[U][MT]) {
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int a = 0; a < NA; ++a)
-#pragma unroll
-        for (int t = 0; t < MT; ++t) acc[a][t] = mfma16x16x32<DT>(A[u][a], Bv[u][t], acc[a][t]);
-  };
-  // two register buffers in ping-pong: group g+1 loads while group g multiplies; no copies between them
-  const int nfull = max(s1 - s0, 0) / U;
-  int s = s0;
-  u16x8 A0[U][NA], B0[U][MT], A1[U][NA], B1[U][MT];
-  if (nfull > 0) load(s0, A0, B0);
-  int g = 0;
-  for (; g + 1 < nfull; g += 2) {
-    load(s + U, A1, B1);
-    compute(A0, B0);
-    s += U;
-    load(g + 2 < nfull ? s + U : s, A0, B0);  // past the end: reload this group (in bounds, unused)
-    compute(A1, B1);
-    s += U;
+
+  // chunk c: LDS buffer c & 1, weight registers W(c & 1), activation registers X(c & 1)
+  xload(0, X0);
+  wload(0, W0);
+  if (nch > 1) {
+    xload(1, X1);
+    wload(1, W1);
   }
-  if (g < nfull) {
-    compute(A0, B0);
-    s += U;
-  }
-  for (; s < s1; ++s) {
-    u16x8 a1[NA], b1[MT];
-#pragma unroll
-    for (int a = 0; a < NA; ++a) a1[a] = ld16(wp[a] + s * 32);
-#pragma unroll
-    for (int t = 0; t < MT; ++t) b1[t] = ld16(xp[t] + s * 32);
-#pragma unroll
-    for (int a = 0; a < NA; ++a)
-#pragma unroll
-      for (int t = 0; t < MT; ++t) acc[a][t] = mfma16x16x32<DT>(a1[a], b1[t], acc[a][t]);
+  xstore(0, X0);
+  if (nch > 2) xload(2, X0);
+  __syncthreads();
+  for (int c = 0; c < nch; c += 2) {
+    compute(c, 0, W0);
+    if (c + 1 < nch) xstore(1, X1);
+    if (c + 3 < nch) xload(c + 3, X1);
+    if (c + 2 < nch) wload(c + 2, W0);
+    __syncthreads();
+    if (c + 1 >= nch) break;
+    compute(c + 1, 1, W1);
+    if (c + 2 < nch) xstore(0, X0);
+    if (c + 4 < nch) xload(c + 4, X0);
+    if (c + 3 < nch) wload(c + 3, W1);
+    __syncthreads();
   }
 
-  // ---- the KW slices of one weight tile meet in LDS, summed in slice order by slice 0
+  // ---- the KW slices of one weight tile meet in LDS (free after the loop's last barrier), in slice order
   if constexpr (KW > 1) {
-    __shared__ f32x4_t red[KW - 1][NW][NA * MT][64];
+    f32x4_t* red = reinterpret_cast<f32x4_t*>(&xs[0][0]);
     if (wk > 0) {
 #pragma unroll
       for (int a = 0; a < NA; ++a)
 #pragma unroll
-        for (int t = 0; t < MT; ++t) red[wk - 1][wn][a * MT + t][lane] = acc[a][t];
+        for (int t = 0; t < MT; ++t) red[(((wk - 1) * NW + wn) * NA * MT + a * MT + t) * 64 + lane] = acc[a][t];
     }
     __syncthreads();
     if (wk > 0) return;
@@ -129,18 +195,18 @@ __global__ __launch_bounds__(256) void linear_kernel(const uint16_t* __restrict_
       for (int a = 0; a < NA; ++a)
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
-          const f32x4_t v = red[j][wn][a * MT + t][lane];
+          const f32x4_t v = red[((j * NW + wn) * NA * MT + a * MT + t) * 64 + lane];
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc[a][t][r] = acc[a][t][r] + v[r];
         }
   }
 
-  // ---- epilogue: lane holds weight rows n0 + 4*lg + r of activation row mbase + 16*t + li
+  // ---- epilogue: lane holds weight rows n0 + 4*lg + r of activation row m0 + 16*t + li
   const int n = n0 + 4 * lg;
   const bool vec = (ldy & 3) == 0 && (((uintptr_t)Y) & 7) == 0 && n + 3 < N;
 #pragma unroll
   for (int t = 0; t < MT; ++t) {
-    const int m = mbase + 16 * t + li;
+    const int m = m0 + 16 * t + li;
     if (m >= M) continue;
     uint16_t o[4];
 #pragma unroll
@@ -169,74 +235,75 @@ __global__ __launch_bounds__(256) void linear_kernel(const uint16_t* __restrict_
   }
 }
 
-// Launch geometry: MT activation tiles of 16 rows per wave; NW weight tiles per workgroup (4 / NW K slices).
-// The widest NW that still gives about one workgroup per CU keeps the whole K of a tile in one wave.
+// Launch geometry: MT activation tiles of 16 rows per workgroup; NW weight tiles per workgroup (4 / NW K slices).
 struct LinearPlan {
-  int mt, nw, mblk, nblk, mfast;
+  int mt, nw, mblk, nblk;
 };
 
+// Tile choice measured on MI355X (graph-timed sweep over the decode shapes, M = 1..2264): the best plan is the
+// largest tile that still gives at least ~400 workgroups; MT = 2 pays off only above ~112 rows.
 static LinearPlan linear_plan(int M, int N, int K) {
-  LinearPlan p;
-  p.mt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
-  p.mblk = m3x_ceil_div(M, 16 * p.mt);
+  const int ntiles = m3x_ceil_div(N, 16);
   const int ksteps = K / 32;
-  p.nw = 1;
-  for (int nw = 4; nw >= 1; nw >>= 1) {
-    const long blocks = (long)m3x_ceil_div(N, 16 * nw) * p.mblk;
-    if (blocks >= 240 || nw == 1) {
-      p.nw = nw;
-      break;
-    }
+  auto blocks = [&](int mt, int nw) { return (long)m3x_ceil_div(M, 16 * mt) * m3x_ceil_div(ntiles, nw); };
+  LinearPlan p;
+  if (M > 512) {
+    p.mt = 4;
+    p.nw = 4;
+  } else if (M > 112 && blocks(2, 2) >= 400) {
+    p.mt = 2;
+    p.nw = blocks(2, 4) >= 400 ? 4 : 2;
+  } else {
+    p.mt = 1;
+    p.nw = blocks(1, 4) >= 400 ? 4 : (blocks(1, 2) >= 400 ? 2 : 1);
   }
-  // keep at least 4 k-steps per slice
-  while (p.nw < 4 && ksteps / (4 / p.nw) < 4) p.nw <<= 1;
-  p.nblk = m3x_ceil_div(N, 16 * p.nw);
-  p.mfast = 1;
+  while (p.nw < 4 && ksteps / (4 / p.nw) < 4) p.nw <<= 1;  // at least one chunk per K slice
+  p.mblk = m3x_ceil_div(M, 16 * p.mt);
+  p.nblk = m3x_ceil_div(ntiles, p.nw);
   return p;
 }
 
 template <int DT, int EPI>
 static void launch_linear(const LinearPlan& p, hipStream_t st, const uint16_t* X, long ldx, const uint16_t* W,
-                          const uint16_t* W2, long ldw, uint16_t* Y, long ldy, int M, int N, int K) {
-  dim3 grid(p.mfast ? p.mblk : p.nblk, p.mfast ? p.nblk : p.mblk);
-#define M3X_LIN(MTT, NWW)                                                                                       \
-  hipLaunchKernelGGL((linear_kernel<DT, MTT, NWW, EPI>), grid, dim3(256), 0, st, X, ldx, W, W2, ldw, Y, ldy, M, N, \
-                     K, p.mfast)
-#define M3X_LIN_NW(MTT)          \
-  if (p.nw == 4) M3X_LIN(MTT, 4); \
-  else if (p.nw == 2) M3X_LIN(MTT, 2); \
-  else M3X_LIN(MTT, 1);
+                          const uint16_t* W2, uint16_t* Y, long ldy, int M, int N, int K) {
+  const dim3 grid(m3x_ceil_div(p.nblk, 8) * 8 * p.mblk);
+#define M3X_LIN(MTT, NWW)                                                                                           \
+  hipLaunchKernelGGL((linear_kernel<DT, MTT, NWW, EPI>), grid, dim3(256), 0, st, X, ldx, W, W2, Y, ldy, M, N, K, \
+                     p.mblk, p.nblk)
   if (p.mt == 1) {
-    M3X_LIN_NW(1)
+    if (p.nw == 4) M3X_LIN(1, 4);
+    else if (p.nw == 2) M3X_LIN(1, 2);
+    else M3X_LIN(1, 1);
   } else if (p.mt == 2) {
-    M3X_LIN_NW(2)
+    if (p.nw == 4) M3X_LIN(2, 4);
+    else M3X_LIN(2, 2);
   } else {
-    M3X_LIN_NW(4)
+    M3X_LIN(4, 4);
   }
-#undef M3X_LIN_NW
 #undef M3X_LIN
 }
 
-static int linear_common(const void* x, long ldx, const void* w, const void* w2, long ldw, void* y, long ldy, int M,
-                         int N, int K, int epi, int dtype, void* stream) {
+static int linear_common(const void* x, long ldx, const void* w, const void* w2, void* y, long ldy, int M, int N,
+                         int K, int epi, int dtype, void* stream) {
   if (M < 0 || N <= 0 || K <= 0) return M3X_EINVAL;
   if (M == 0) return M3X_OK;
   if (!x || !w || !y || (epi == EPI_SWIGLU && !w2)) return M3X_ENULL;
-  if (K % 32 || (ldx & 7) || (ldw & 7) || ldx < K || ldw < K || ldy < N) return M3X_EINVAL;
+  if (K % 32 || (ldx & 7) || ldx < K || ldy < N) return M3X_EINVAL;
   if (!m3x_aligned16(x) || !m3x_aligned16(w) || (w2 && !m3x_aligned16(w2)) || (((uintptr_t)y) & 1))
     return M3X_EINVAL;
   const LinearPlan p = linear_plan(M, N, K);
+  if ((long)m3x_ceil_div(p.nblk, 8) * 8 * p.mblk > 0x7fffffffL) return M3X_EINVAL;
   hipStream_t st = (hipStream_t)stream;
   const uint16_t *X = (const uint16_t*)x, *Wt = (const uint16_t*)w, *W2 = (const uint16_t*)w2;
   uint16_t* Y = (uint16_t*)y;
   if (dtype == M3X_BF16) {
-    if (epi == EPI_NONE) launch_linear<M3X_BF16, EPI_NONE>(p, st, X, ldx, Wt, W2, ldw, Y, ldy, M, N, K);
-    else if (epi == EPI_SWIGLU) launch_linear<M3X_BF16, EPI_SWIGLU>(p, st, X, ldx, Wt, W2, ldw, Y, ldy, M, N, K);
-    else launch_linear<M3X_BF16, EPI_GELU>(p, st, X, ldx, Wt, W2, ldw, Y, ldy, M, N, K);
+    if (epi == EPI_NONE) launch_linear<M3X_BF16, EPI_NONE>(p, st, X, ldx, Wt, W2, Y, ldy, M, N, K);
+    else if (epi == EPI_SWIGLU) launch_linear<M3X_BF16, EPI_SWIGLU>(p, st, X, ldx, Wt, W2, Y, ldy, M, N, K);
+    else launch_linear<M3X_BF16, EPI_GELU>(p, st, X, ldx, Wt, W2, Y, ldy, M, N, K);
   } else if (dtype == M3X_F16) {
-    if (epi == EPI_NONE) launch_linear<M3X_F16, EPI_NONE>(p, st, X, ldx, Wt, W2, ldw, Y, ldy, M, N, K);
-    else if (epi == EPI_SWIGLU) launch_linear<M3X_F16, EPI_SWIGLU>(p, st, X, ldx, Wt, W2, ldw, Y, ldy, M, N, K);
-    else launch_linear<M3X_F16, EPI_GELU>(p, st, X, ldx, Wt, W2, ldw, Y, ldy, M, N, K);
+    if (epi == EPI_NONE) launch_linear<M3X_F16, EPI_NONE>(p, st, X, ldx, Wt, W2, Y, ldy, M, N, K);
+    else if (epi == EPI_SWIGLU) launch_linear<M3X_F16, EPI_SWIGLU>(p, st, X, ldx, Wt, W2, Y, ldy, M, N, K);
+    else launch_linear<M3X_F16, EPI_GELU>(p, st, X, ldx, Wt, W2, Y, ldy, M, N, K);
   } else {
     return M3X_EUNSUPPORTED;
   }
@@ -244,17 +311,34 @@ static int linear_common(const void* x, long ldx, const void* w, const void* w2,
   return M3X_OK;
 }
 
-M3X_API int m3x_linear(const void* x, long ldx, const void* w, long ldw, void* y, long ldy, int M, int N, int K,
-                       int dtype, void* stream) {
-  return linear_common(x, ldx, w, nullptr, ldw, y, ldy, M, N, K, EPI_NONE, dtype, stream);
+// Elements of the packed form of an [N, K] weight: N rounded up to 16 rows, times K.
+M3X_API long m3x_packed_weight_elems(int N, int K) {
+  if (N <= 0 || K <= 0 || K % 32) return -1;
+  return (long)m3x_ceil_div(N, 16) * 16 * K;
 }
 
-// kind 0 (SwiGLU): y[:, :I] = dt(silu(x.Wg^T)) * (x.Wu^T) with gate rows w_gate[I, K], up rows w_up[I, K];
-// kind 1 (GELU): y[:, :I] = gelu(x.Wg^T) (w_up unused).
-M3X_API int m3x_linear_act(const void* x, long ldx, const void* w_gate, const void* w_up, long ldw, void* y, long ldy,
+M3X_API int m3x_pack_weight(const void* w, long ldw, int N, int K, void* out, void* stream) {
+  if (N <= 0 || K <= 0 || K % 32 || ldw < K || (ldw & 7)) return M3X_EINVAL;
+  if (!w || !out) return M3X_ENULL;
+  if (!m3x_aligned16(w) || !m3x_aligned16(out)) return M3X_EINVAL;
+  const long total = (long)m3x_ceil_div(N, 16) * (K / 32) * 64;
+  hipLaunchKernelGGL(pack_weight_kernel, dim3(m3x_ceil_div(total, 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)w, ldw, N, K, (uint16_t*)out);
+  M3X_CHECK_LAUNCH();
+  return M3X_OK;
+}
+
+M3X_API int m3x_linear(const void* x, long ldx, const void* w_packed, void* y, long ldy, int M, int N, int K,
+                       int dtype, void* stream) {
+  return linear_common(x, ldx, w_packed, nullptr, y, ldy, M, N, K, EPI_NONE, dtype, stream);
+}
+
+// kind 0 (SwiGLU): y[:, :I] = dt(silu(x.Wg^T)) * (x.Wu^T) with packed gate rows wg[I, K] and up rows wu[I, K];
+// kind 1 (GELU): y[:, :I] = gelu(x.Wg^T) (wu unused).
+M3X_API int m3x_linear_act(const void* x, long ldx, const void* wg_packed, const void* wu_packed, void* y, long ldy,
                            int M, int I, int K, int kind, int dtype, void* stream) {
   if (kind != 0 && kind != 1) return M3X_EINVAL;
-  return linear_common(x, ldx, w_gate, kind == 0 ? w_up : nullptr, ldw, y, ldy, M, I, K,
+  return linear_common(x, ldx, wg_packed, kind == 0 ? wu_packed : nullptr, y, ldy, M, I, K,
                        kind == 0 ? EPI_SWIGLU : EPI_GELU, dtype, stream);
 }
 

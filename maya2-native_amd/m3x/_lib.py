@@ -12,7 +12,7 @@ import os
 import torch  # noqa: F401  (must precede the CDLL load, see above)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libm3x.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -31,8 +31,10 @@ SIGNATURES = {
     "m3x_decode_attn_workspace": (_Z, [_I, _I, _I, _I]),
     "m3x_decode_attn": (_I, [_P, _L, _L, _P, _P, _L, _L, _L, _I, _P, _L, _L, _P, _P, _F, _I, _I, _I, _I, _I, _I, _P,
                              _Z, _P]),
-    "m3x_linear": (_I, [_P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _P]),
-    "m3x_linear_act": (_I, [_P, _L, _P, _P, _L, _P, _L, _I, _I, _I, _I, _I, _P]),
+    "m3x_packed_weight_elems": (_L, [_I, _I]),
+    "m3x_pack_weight": (_I, [_P, _L, _I, _I, _P, _P]),
+    "m3x_linear": (_I, [_P, _L, _P, _P, _L, _I, _I, _I, _I, _P]),
+    "m3x_linear_act": (_I, [_P, _L, _P, _P, _P, _L, _I, _I, _I, _I, _I, _P]),
     "m3x_act": (_I, [_P, _L, _P, _L, _I, _I, _I, _I, _P]),
     "m3x_add_norm": (_I, [_P, _L, _L, _P, _L, _L, _P, _L, _P, _P, _P, _P, _F, _I, _I, _I, _I, _I, _P]),
     "m3x_add_rows": (_I, [_P, _L, _P, _L, _P, _L, _I, _I, _I, _P]),

@@ -22,6 +22,9 @@ class Cb0Sampler:
         (default 2048 when V0 == 2049, else none). stop=False skips the controlled-stop bookkeeping."""
         lib()
         self.w = head_weight
+        with torch.inference_mode():
+            self.pw = ops.pack_weight(head_weight)  # fragment-order copy for the head GEMM
+            torch.cuda.current_stream(head_weight.device).synchronize()
         self.V = head_weight.shape[0]
         self.aeos = (2048 if self.V == 2049 else -1) if aeos is None else int(aeos)
         self.stop = bool(stop) and self.aeos >= 0
@@ -75,7 +78,7 @@ class Cb0Sampler:
 
     def run(self, b, uniforms=True):
         """logits = h @ head^T; u from (seed_t, ctr_t, level 0); sample -> b.cb0 (and column 0 of b.codes)."""
-        ops.linear(b.h, self.w, b.logits)
+        ops.linear(b.h, self.pw, b.logits)
         if uniforms:
             ops.philox_uniforms(self.seed_t, self.ctr_t, b.slots, b.u, 0)
         rep = self.any_rep and self.rep_win > 0

@@ -113,13 +113,49 @@ def decode_attn(q, k_cache, v_cache, out, slots, pos, scale, max_ctx, chunk, wor
         "decode_attn")
 
 
-def _lin_args(x, w, y, N):
-    _dev(x, w, y)
-    _rows2d(x, "x")
+class PackedWeight:
+    """An [N, K] 16-bit weight in MFMA fragment order (see m3x_pack_weight): `data` holds ceil(N/16)*16*K elements."""
+    __slots__ = ("data", "N", "K")
+
+    def __init__(self, data, N, K):
+        self.data, self.N, self.K = data, N, K
+
+    @property
+    def dtype(self):
+        return self.data.dtype
+
+    @property
+    def device(self):
+        return self.data.device
+
+    def rows(self, start, stop):
+        """Rows [start, stop) as their own packed weight (start % 16 == 0); shares storage."""
+        if start % 16 or not 0 <= start < stop <= self.N:
+            raise ValueError(f"rows({start}, {stop}) of a packed [{self.N}, {self.K}] weight")
+        return PackedWeight(self.data[start * self.K:-(-stop // 16) * 16 * self.K], stop - start, self.K)
+
+
+def pack_weight(w):
+    """Pack w [N, K] (row stride % 8 == 0, K % 32 == 0) into fragment order; one launch on the current stream."""
+    _dev(w)
     _rows2d(w, "w")
+    N, K = w.shape
+    n = int(lib().m3x_packed_weight_elems(N, K))
+    if n < 0:
+        raise ValueError(f"pack_weight: K={K} must be a multiple of 32")
+    out = torch.empty(n, dtype=w.dtype, device=w.device)
+    check(lib().m3x_pack_weight(_p(w), w.stride(0), N, K, _p(out), _stream()), "pack_weight")
+    return PackedWeight(out, N, K)
+
+
+def _lin_args(x, w, y, N):
+    if not isinstance(w, PackedWeight):
+        raise TypeError("linear: the weight must be packed with ops.pack_weight")
+    _dev(x, w.data, y)
+    _rows2d(x, "x")
     M, K = x.shape
-    if w.shape[1] != K or w.dtype != x.dtype:
-        raise ValueError(f"linear: x {tuple(x.shape)} {x.dtype} vs w {tuple(w.shape)} {w.dtype}")
+    if w.K != K or w.dtype != x.dtype:
+        raise ValueError(f"linear: x {tuple(x.shape)} {x.dtype} vs packed w [{w.N}, {w.K}] {w.dtype}")
     if y is None:
         y = torch.empty(M, N, dtype=x.dtype, device=x.device)
     _rows2d(y, "y")
@@ -129,24 +165,23 @@ def _lin_args(x, w, y, N):
 
 
 def linear(x, w, y=None):
-    """y = x @ w.T with x [M, K], w [N, K] (16-bit, same dtype); returns y [M, N]."""
-    N = w.shape[0]
-    M, K, y = _lin_args(x, w, y, N)
-    check(lib().m3x_linear(_p(x), x.stride(0), _p(w), w.stride(0), _p(y), y.stride(0), M, N, K, _dt(x), _stream()),
+    """y = x @ W.T with x [M, K] and W [N, K] packed by pack_weight (same dtype); returns y [M, N]."""
+    M, K, y = _lin_args(x, w, y, w.N)
+    check(lib().m3x_linear(_p(x), x.stride(0), _p(w.data), _p(y), y.stride(0), M, w.N, K, _dt(x), _stream()),
           "linear")
     return y
 
 
 def linear_act(x, w_gate, w_up, kind, y=None):
-    """SWIGLU: y = bf16(silu(x @ w_gate.T)) * (x @ w_up.T); GELU: y = gelu(x @ w_gate.T) (w_up None)."""
-    I = w_gate.shape[0]
+    """SWIGLU: y = bf16(silu(x @ Wg.T)) * (x @ Wu.T); GELU: y = gelu(x @ Wg.T) (w_up None); weights packed."""
+    I = w_gate.N
     M, K, y = _lin_args(x, w_gate, y, I)
     if kind == ACT_SWIGLU:
-        _dev(w_up)
-        if w_up is None or w_up.shape != w_gate.shape or w_up.stride(0) != w_gate.stride(0):
-            raise ValueError("linear_act: w_up must match w_gate's shape and row stride")
-    check(lib().m3x_linear_act(_p(x), x.stride(0), _p(w_gate), _p(w_up if kind == ACT_SWIGLU else None),
-                               w_gate.stride(0), _p(y), y.stride(0), M, I, K, kind, _dt(x), _stream()), "linear_act")
+        if not isinstance(w_up, PackedWeight) or (w_up.N, w_up.K) != (w_gate.N, w_gate.K):
+            raise ValueError("linear_act: w_up must be a packed weight of w_gate's shape")
+        _dev(w_up.data)
+    check(lib().m3x_linear_act(_p(x), x.stride(0), _p(w_gate.data), _p(w_up.data if kind == ACT_SWIGLU else None),
+                               _p(y), y.stride(0), M, I, K, kind, _dt(x), _stream()), "linear_act")
     return y
 
 

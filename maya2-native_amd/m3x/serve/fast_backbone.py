@@ -3,8 +3,9 @@
 Drop-in for serve/fast_backbone.py (StaticBackbone, :111-362): same constructor, methods, attributes, errors and
 static KV layout — per layer `k[i], v[i]: [max_slots+1, kv_heads, capacity, head_dim]` in the model dtype, slot
 `max_slots` a dummy whose length stays 0 and pads a batch up to its bucket (:3-4,146-150). One hipGraph per
-(row bucket, context bucket), all graphs in one memory pool; HF module weights used in place (q|k|v and gate|up
-are concatenated once and the HF weights re-viewed into them, :130-141).
+(row bucket, context bucket), all graphs in one memory pool; q|k|v and gate|up are concatenated once and the HF
+weights re-viewed into them (:130-141), and every projection weight gets one packed copy in MFMA fragment order
+(ops.pack_weight) that the projection kernels stream with fully contiguous loads.
 
 Per layer the step runs: [add+]RMSNorm -> q|k|v GEMM -> q/k-norm + RoPE + K/V cache write -> decode attention
 over the cache in place -> o GEMM -> add+RMSNorm -> gate|up GEMM -> SwiGLU -> down GEMM (deferred into the next
@@ -92,6 +93,15 @@ class StaticBackbone:
                 _reweight(m.up_proj, g[ng:])
                 self.wgu.append(g)
             self.inter = self.wgu[0].shape[0] // 2
+            # MFMA fragment-order copies for the projection kernels (the module weights stay as they are)
+            I = self.inter
+            self.pqkv = [ops.pack_weight(w) for w in self.wqkv]
+            pgu = [ops.pack_weight(g) for g in self.wgu]
+            self.pgate = [p.rows(0, I) for p in pgu]
+            self.pup = [p.rows(I, 2 * I) for p in pgu]
+            self.po = [ops.pack_weight(layer.self_attn.o_proj.weight) for layer in self.layers]
+            self.pdown = [ops.pack_weight(layer.mlp.down_proj.weight) for layer in self.layers]
+            torch.cuda.current_stream(self.device).synchronize()
             self.batch_buckets = tuple(sorted(set(batch_buckets)))
             if self.batch_buckets[-1] < max_slots:
                 self.batch_buckets += (max_slots,)
@@ -178,16 +188,15 @@ class StaticBackbone:
                 ops.add_rms(b.x, None, layer.input_layernorm.weight, eps, y=b.y)
             else:
                 ops.add_rms(b.h, b.pend, layer.input_layernorm.weight, eps, h_out=b.h, y=b.y)
-            ops.linear(b.y, self.wqkv[i], b.qkv)
+            ops.linear(b.y, self.pqkv[i], b.qkv)
             ops.qk_norm_rope_cache(b.qkv, b.q, self.k[i], self.v[i], b.slots, b.pos, self.cos, self.sin,
                                    attn.q_norm.weight, attn.k_norm.weight, eps, H, KV)
             ops.decode_attn(b.q, self.k[i], self.v[i], o3, b.slots, b.pos, self.scaling, b.ctx, b.chunk, b.attn_ws,
                             H, KV)
-            ops.linear(b.o, attn.o_proj.weight, b.a)
+            ops.linear(b.o, self.po[i], b.a)
             ops.add_rms(b.x if i == 0 else b.h, b.a, layer.post_attention_layernorm.weight, eps, h_out=b.h, y=b.y)
-            I = self.inter
-            ops.linear_act(b.y, self.wgu[i][:I], self.wgu[i][I:], ops.ACT_SWIGLU, b.act)
-            ops.linear(b.act, layer.mlp.down_proj.weight, b.pend)
+            ops.linear_act(b.y, self.pgate[i], self.pup[i], ops.ACT_SWIGLU, b.act)
+            ops.linear(b.act, self.pdown[i], b.pend)
         ops.add_rms(b.h, b.pend, self.norm.weight, eps, h_out=b.h, y=b.out)
         ops.lengths_add(self.lengths, b.slots, b.real)
         return b.out

@@ -33,6 +33,11 @@ def _w(mod, dtype, device):
     return mod.weight.detach().to(device=device, dtype=dtype).contiguous()
 
 
+def _pw(mod, dtype, device):
+    """The module's weight in MFMA fragment order for the projection kernels."""
+    return ops.pack_weight(_w(mod, dtype, device))
+
+
 def _norm(mod, dtype, device):
     """(kind, weight, bias, eps) of a LayerNorm- or RMSNorm-like module."""
     b = getattr(mod, 'bias', None)
@@ -70,7 +75,7 @@ class FastDepth:
             self.H = int(getattr(d, 'n_heads', 16))
             self.hd = self.D // self.H
             self.group_of_level = list(getattr(d, 'group_of_level', REFERENCE_GROUP_OF_LEVEL))
-            self.in_proj = _w(d.in_proj, dtype, dev)
+            self.in_proj = _pw(d.in_proj, dtype, dev)
             if hasattr(d, 'embed'):
                 self.embed = d.embed.detach().to(device=dev, dtype=dtype).contiguous()
                 self.level0 = d.level0.detach().to(device=dev, dtype=dtype).contiguous()
@@ -86,22 +91,23 @@ class FastDepth:
                 layers = []
                 for blk in blocks:
                     L = SimpleNamespace(n1=_norm(blk.n1, dtype, dev), n2=_norm(blk.n2, dtype, dev),
-                                        qkv=_w(blk.qkv, dtype, dev), o=_w(blk.o, dtype, dev))
+                                        qkv=_pw(blk.qkv, dtype, dev), o=_pw(blk.o, dtype, dev))
                     if hasattr(blk, 'gate_up'):
-                        L.act, L.w1, L.w2 = ops.ACT_SWIGLU, _w(blk.gate_up, dtype, dev), _w(blk.down, dtype, dev)
-                        L.ffn = L.w1.shape[0] // 2
+                        w1 = _pw(blk.gate_up, dtype, dev)
+                        L.act, L.ffn, L.w2 = ops.ACT_SWIGLU, w1.N // 2, _pw(blk.down, dtype, dev)
+                        L.wg, L.wu = w1.rows(0, L.ffn), w1.rows(L.ffn, w1.N)
                     else:
-                        L.act, L.w1, L.w2 = ops.ACT_GELU, _w(blk.f1, dtype, dev), _w(blk.f2, dtype, dev)
-                        L.ffn = L.w1.shape[0]
+                        L.act, L.wg, L.wu, L.w2 = ops.ACT_GELU, _pw(blk.f1, dtype, dev), None, _pw(blk.f2, dtype, dev)
+                        L.ffn = L.wg.N
                     layers.append(L)
                 self.trunks.append(layers)
             self.layers = len(self.trunks[0])
             self.final_norm = _norm(d.norm, dtype, dev)
-            self.heads = torch.stack([_w(h, dtype, dev) for h in d.heads]).contiguous()  # [31, n_codes, D]
+            self.heads = [_pw(h, dtype, dev) for h in d.heads]  # 31 x [n_codes, D]
             self.cross = getattr(d, 'cross', None)
             self.cross_w = None
             if self.cross is not None:
-                self.cross_w = [(_w(c.kv, dtype, dev), _w(c.o, dtype, dev)) for c in self.cross]
+                self.cross_w = [(_pw(c.kv, dtype, dev), _pw(c.o, dtype, dev)) for c in self.cross]
             self.audio_in = model.audio_in  # shared, read-only (engine dtype)
             self.fb_table = model.audio_in.table.weight
             if self.fb_table.dtype not in (torch.bfloat16, torch.float16):
@@ -109,6 +115,7 @@ class FastDepth:
             self.fb_norm = _norm(model.audio_in.norm, self.fb_table.dtype, dev)
             self.feedback_scale = math.sqrt(N_LEVELS)
             self.cross_const = torch.zeros(self.max_slots + 1, self.layers, self.D, device=dev, dtype=dtype)
+            torch.cuda.current_stream(dev).synchronize()  # packing ran on the current stream
         self.pool = None
         self.graphs = {}
         self.seed_t = torch.full((1,), int(seed) % (2 ** 31 - 1), device=self.device, dtype=torch.int32)
@@ -141,7 +148,7 @@ class FastDepth:
         Fmax = max(L.ffn for t in self.trunks for L in t)
         b = SimpleNamespace(B=B)
         b.slots = torch.full((B,), self.max_slots, dtype=torch.long, device=dev)
-        b.h = h if h is not None else torch.zeros(B, self.in_proj.shape[1], dtype=dt, device=dev)
+        b.h = h if h is not None else torch.zeros(B, self.in_proj.K, dtype=dt, device=dev)
         b.codes = codes if codes is not None else torch.zeros(B, N_LEVELS, dtype=torch.int32, device=dev)
         b.u = torch.zeros(B, N_LEVELS - 1, dtype=torch.float32, device=dev)
         b.prefix = torch.zeros(B, NP, D, dtype=dt, device=dev)
@@ -199,10 +206,7 @@ class FastDepth:
                 x_res = b.xw[:R].view(B, T, D)[:, tq0:]
                 ops.add_norm(x_res, b.a[:R2], None, b.xw2[:R2], b.y2[:R2], L.n2.w, L.n2.b, L.n2.eps, Tq, L.n2.kind)
                 F = L.ffn
-                if L.act == ops.ACT_SWIGLU:
-                    ops.linear_act(b.y2[:R2], L.w1[:F], L.w1[F:], L.act, b.ffn_act[:R2, :F])
-                else:
-                    ops.linear_act(b.y2[:R2], L.w1, None, L.act, b.ffn_act[:R2, :F])
+                ops.linear_act(b.y2[:R2], L.wg, L.wu, L.act, b.ffn_act[:R2, :F])
                 ops.linear(b.ffn_act[:R2, :F], L.w2, b.f[:R2])
                 nxt = layers[li + 1].n1 if li + 1 < self.layers else self.final_norm
                 c = b.crossb[:, li * D:(li + 1) * D] if b.crossb is not None else None

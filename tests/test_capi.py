@@ -13,7 +13,7 @@ def _declared():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     decls = {}
-    for m in re.finditer(r"\b(int|size_t)\s+(m3x_\w+)\s*\(([^)]*)\)\s*;", text):
+    for m in re.finditer(r"\b(int|long|size_t)\s+(m3x_\w+)\s*\(([^)]*)\)\s*;", text):
         args = [a.strip() for a in m.group(3).split(",") if a.strip() and a.strip() != "void"]
         decls[m.group(2)] = len(args)
     return decls
@@ -52,3 +52,11 @@ def test_workspace_queries_are_host_only():
     # attention partials: rows x kv heads x splits x (m[2], l[2], pad[4], o[2][128]) fp32
     assert ops.decode_attn_workspace(224, 8, 4096, 1024) == 224 * 8 * 4 * 264 * 4
     assert ops.decode_attn_workspace(0, 8, 4096, 1024) == 0
+
+
+def test_packed_weight_size_query_is_host_only():
+    from m3x._lib import lib
+    L = lib()
+    assert L.m3x_packed_weight_elems(2049, 1024) == 2064 * 1024  # rows padded to a multiple of 16
+    assert L.m3x_packed_weight_elems(16, 32) == 512
+    assert L.m3x_packed_weight_elems(16, 48) == -1  # K must be a multiple of 32

@@ -24,7 +24,7 @@ def test_linear_bf16(gpu, M, N, K):
     g = _g(M * 7 + N)
     x = torch.randn(M, K, generator=g).to(torch.bfloat16)
     w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
-    y = ops.linear(x.to(gpu), w.to(gpu))
+    y = ops.linear(x.to(gpu), ops.pack_weight(w.to(gpu)))
     ref = (x.float() @ w.float().t())
     ok, info = close(y, ref, atol=1e-2)
     assert ok, info
@@ -36,7 +36,7 @@ def test_linear_fp16(gpu, M, N, K):
     g = _g(M + K)
     x = torch.randn(M, K, generator=g).to(torch.float16)
     w = (torch.randn(N, K, generator=g) * 0.02).to(torch.float16)
-    y = ops.linear(x.to(gpu), w.to(gpu))
+    y = ops.linear(x.to(gpu), ops.pack_weight(w.to(gpu)))
     ok, info = close(y, x.float() @ w.float().t(), atol=1e-2)
     assert ok, info
 
@@ -50,8 +50,9 @@ def test_linear_swiglu_epilogue(gpu, M, I, K, dtype):
     g = _g(M + I)
     x = torch.randn(M, K, generator=g).to(dtype).to(gpu)
     wgu = (torch.randn(2 * I, K, generator=g) * 0.02).to(dtype).to(gpu)
-    fused = ops.linear_act(x, wgu[:I], wgu[I:], ops.ACT_SWIGLU)
-    gu = ops.linear(x, wgu)
+    pgu = ops.pack_weight(wgu)
+    fused = ops.linear_act(x, pgu.rows(0, I), pgu.rows(I, 2 * I), ops.ACT_SWIGLU)
+    gu = ops.linear(x, pgu)
     sep = torch.empty(M, I, dtype=dtype, device=gpu)
     ops.act(gu, sep, ops.ACT_SWIGLU)
     # near-zero outputs come from cancelling sums, where one fp32 ulp of the sum is many ulps of the result
@@ -68,9 +69,10 @@ def test_linear_gelu_epilogue(gpu):
     g = _g(77)
     x = torch.randn(9, 1024, generator=g).to(torch.float16).to(gpu)
     w = (torch.randn(3072, 1024, generator=g) * 0.02).to(torch.float16).to(gpu)
-    fused = ops.linear_act(x, w, None, ops.ACT_GELU)
+    pw = ops.pack_weight(w)
+    fused = ops.linear_act(x, pw, None, ops.ACT_GELU)
     sep = torch.empty(9, 3072, dtype=torch.float16, device=gpu)
-    ops.act(ops.linear(x, w), sep, ops.ACT_GELU)
+    ops.act(ops.linear(x, pw), sep, ops.ACT_GELU)
     ok, info = close(fused, sep.float(), atol=1e-3, rel_ulps=2)
     assert ok, info
     ok, info = close(fused, torch.nn.functional.gelu(x.float() @ w.float().t()).cpu(), atol=1e-2)
@@ -83,10 +85,56 @@ def test_linear_strided_output(gpu):
     x = torch.randn(9, 1024, generator=g).to(torch.bfloat16).to(gpu)
     w = (torch.randn(512, 1024, generator=g) * 0.02).to(torch.bfloat16).to(gpu)
     big = torch.zeros(9, 1536, dtype=torch.bfloat16, device=gpu)
-    ops.linear(x, w, big[:, 256:768])
+    ops.linear(x, ops.pack_weight(w), big[:, 256:768])
     ok, info = close(big[:, 256:768], x.float() @ w.float().t(), atol=1e-2)
     assert ok, info
     assert big[:, :256].abs().sum() == 0 and big[:, 768:].abs().sum() == 0
+
+
+@pytest.mark.parametrize("N,K", [(2049, 1024), (16, 32), (48, 96)])
+def test_pack_weight_layout(gpu, N, K):
+    """The packed layout bit for bit: fragment (t, s), lane l, element e holds W[16t + l%16][32s + 8(l//16) + e]
+    (zero rows past N), checked against the same layout written as a reshape/permute of the padded matrix."""
+    from m3x import ops
+    g = _g(N + K)
+    w = torch.randn(N, K, generator=g).to(torch.bfloat16)
+    pw = ops.pack_weight(w.to(gpu))
+    Np = -(-N // 16) * 16
+    wpad = torch.zeros(Np, K, dtype=torch.bfloat16)
+    wpad[:N] = w
+    want = wpad.view(Np // 16, 16, K // 32, 4, 8).permute(0, 2, 3, 1, 4).reshape(-1)
+    assert pw.data.numel() == Np * K and (pw.N, pw.K) == (N, K)
+    assert np.array_equal(bf16_bits(pw.data.cpu()), bf16_bits(want))
+    # a row block of a packed weight is the packed form of those rows
+    if N >= 32:
+        sub = ops.pack_weight(w[16:].contiguous().to(gpu))
+        assert np.array_equal(bf16_bits(pw.rows(16, N).data.cpu()), bf16_bits(sub.data.cpu()))
+
+
+def test_linear_deterministic_and_graph_replay(gpu):
+    """Same inputs, same bits: eager twice and four graph replays with eager work in between."""
+    from m3x import ops
+    g = _g(5)
+    x = torch.randn(224, 1024, generator=g).to(torch.bfloat16).to(gpu)
+    pw = ops.pack_weight((torch.randn(3072, 1024, generator=g) * 0.02).to(torch.bfloat16).to(gpu))
+    y0 = ops.linear(x, pw).clone()
+    assert torch.equal(ops.linear(x, pw), y0)
+    y = torch.zeros_like(y0)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.linear(x, pw, y)
+    torch.cuda.current_stream().wait_stream(s)
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr, stream=s):
+        ops.linear(x, pw, y)
+    for _ in range(4):
+        y.zero_()
+        gr.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, y0)
+        ops.linear(x[:7], pw)  # eager work between replays
+        torch.cuda.synchronize()
 
 
 # ---------------------------------------------------------------- add + RMSNorm (bit-exact)
