@@ -94,6 +94,19 @@ def cpu_baseline(torch, seconds, seats=2):
                        f"{el:.1f} s on {threads} host threads")
 
 
+def _traffic_ratio():
+    """HBM bytes per algorithmic byte of the decode attention, measured with rocprofv3 --pmc (FETCH_SIZE +
+    WRITE_SIZE, each scaled by the counts of a plain copy of known size) on this workload and recorded in
+    profiles/; None if the record is absent."""
+    path = os.path.join(ROOT, "profiles", "decode_attn_b224_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_per_algorithmic_byte:"):
+            return float(line.split(":", 1)[1].split()[0])
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -101,7 +114,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--batch", type=int, default=224)
     ap.add_argument("--b1-replays", type=int, default=200)
-    ap.add_argument("--attn-iters", type=int, default=40)
+    ap.add_argument("--attn-iters", type=int, default=56)
+    ap.add_argument("--copy-probe", action="store_true", help="also run one 256 MiB device copy (counter scale)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-b1", action="store_true")
@@ -148,28 +162,37 @@ def main():
             raise SystemExit("codes out of range")
         attended = attended0 + (K - 1) * B // 2  # mean over the timed steps
 
-        # decode attention alone, live, on the launch stream (layer 0, the frame's own buffers)
+        # decode attention alone, live, on the launch stream: the frame's own buffers, each layer over its own
+        # cache as in the frame (a cache is 1.9 GB, far above the 256 MB MALL, so every launch streams from HBM)
         bufs = g["bufs"][0]
         sb = fs.bb
         o = torch.empty_like(bufs.q)
         att_keys = int((bufs.pos[:B].long() + 1).sum())
         stream = torch.cuda.current_stream()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        nl = len(sb.k)
 
-        def attn_launch():
-            ops.decode_attn(bufs.q, sb.k[0], sb.v[0], o, bufs.slots, bufs.pos, sb.scaling, bufs.ctx, bufs.chunk,
-                            bufs.attn_ws, sb.heads, sb.kv_heads)
-        for _ in range(3):
-            attn_launch()
+        def attn_launch(i):
+            ops.decode_attn(bufs.q, sb.k[i % nl], sb.v[i % nl], o, bufs.slots, bufs.pos, sb.scaling, bufs.ctx,
+                            bufs.chunk, bufs.attn_ws, sb.heads, sb.kv_heads)
+        for i in range(3):
+            attn_launch(i)
         e0.record(stream)
-        for _ in range(args.attn_iters):
-            attn_launch()
+        for i in range(args.attn_iters):
+            attn_launch(i)
         e1.record(stream)
         torch.cuda.synchronize()
         attn_us = e0.elapsed_time(e1) * 1e3 / args.attn_iters
         attn_bytes = roofline.decode_attn_bytes(att_keys, B)
         attn_gbs = attn_bytes / (attn_us * 1e-6) / 1e9
         log(f"decode attention: {attn_us:.1f} us/launch, {attn_gbs:.0f} GB/s ({attn_gbs / roofline.HBM_PEAK_GBS:.1%})")
+        if args.copy_probe:
+            # a plain device copy of known size: what FETCH_SIZE / WRITE_SIZE read for it scales their counts
+            src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+            dst = torch.empty_like(src)
+            dst.copy_(src)
+            torch.cuda.synchronize()
+            del src, dst
         step_bytes = roofline.backbone_step_bytes(attended, B) + roofline.depth_frame_bytes(seats=B)
         del fs, g, bufs, o
         torch.cuda.empty_cache()
@@ -201,6 +224,7 @@ def main():
         log(f"CPU baseline (~{args.cpu_seconds:.0f} s)")
         cpu = cpu_baseline(torch, args.cpu_seconds)
 
+    ratio = _traffic_ratio()
     out = {
         "metric": "audio frames/sec at B=224 frame step; B=1 frame µs; % HBM/MFMA roofline",
         "value": round(fps, 1),
@@ -224,9 +248,9 @@ def main():
         "audio_s_per_s": round(fps * 0.08, 1),
         "frame_bytes_algorithmic": step_bytes,
         "frame_hbm_fraction": round(step_bytes / (ms * 1e-3) / 1e9 / roofline.HBM_PEAK_GBS, 4),
-        "roofline": {"kernel": "decode_attn (split + combine), layer 0 of the B=224 step", "bound": "hbm",
+        "roofline": {"kernel": "decode_attn over the B=224 step's caches (layers in turn)", "bound": "hbm",
                      "achieved": round(attn_gbs, 1), "peak": roofline.HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(attn_gbs / roofline.HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(attn_gbs / roofline.HBM_PEAK_GBS, 4), "traffic": None if ratio is None else int(ratio * attn_bytes),
                      "launch_us": round(attn_us, 2), "bytes_per_launch": attn_bytes},
         "cpu_baseline": cpu,
     }
