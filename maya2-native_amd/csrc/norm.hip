@@ -51,10 +51,13 @@ __global__ __launch_bounds__(256) void add_rms_kernel(const uint16_t* __restrict
   const bool active = row < rows;
   float x[8];
   float p = 0.f;
+  u16x8 wv;
   if (active) {
     u16x8 hv = ld16(h + (long)row * s_h + 8 * t);
+    u16x8 av;
+    if (a) av = ld16(a + (long)row * s_a + 8 * t);
+    wv = ld16(w + 8 * t);  // after the row's loads: it arrives while the reduction runs
     if (a) {
-      u16x8 av = ld16(a + (long)row * s_a + 8 * t);
       u16x8 sv;
 #pragma unroll
       for (int e = 0; e < 8; ++e) sv.v[e] = f2bf(bf2f(hv.v[e]) + bf2f(av.v[e]));
@@ -70,7 +73,7 @@ __global__ __launch_bounds__(256) void add_rms_kernel(const uint16_t* __restrict
   float ss = row_tree_sum<TPR>(p, red, bcast);
   if (!active) return;
   const float inv = 1.0f / sqrtf(ss / (float)N + eps);
-  u16x8 wv = ld16(w + 8 * t), yv;
+  u16x8 yv;
 #pragma unroll
   for (int e = 0; e < 8; ++e) yv.v[e] = f2bf(bf2f(f2bf(x[e] * inv)) * bf2f(wv.v[e]));
   st16(y + (long)row * s_y + 8 * t, yv);
@@ -127,38 +130,32 @@ __global__ __launch_bounds__(256) void qk_norm_rope_cache_kernel(
   const int row = (int)(item / NH);
   const int j = (int)(item % NH);
   const bool active = row < rows;
+  // Every load is issued up front from clamped (valid) addresses, so one memory latency covers them all;
+  // only cos/sin wait for the position. Inactive items compute on row 0 and store nothing.
+  const int r = active ? row : 0;
+  const int ps = min(pos[r], cap - 1);  // the host guarantees pos < cap; the clamp keeps the cache write in the slot
+  const long slot = slots[r];
+  const u16x8 xv = ld16(qkv + (long)r * s_qkv + (long)j * D + 8 * t);
+  const u16x8 wv = ld16((j < H ? wq : wk) + 8 * t);
+  const int kh = j < H ? 0 : j - H;
+  const u16x8 vv = ld16(qkv + (long)r * s_qkv + (long)(H + KV + kh) * D + 8 * t);
+  const u16x8 cv = ld16(cosb + (long)ps * s_cos + 8 * t);
+  const u16x8 sv = ld16(sinb + (long)ps * s_cos + 8 * t);
   float x[8], yv[8];
-  float p = 0.f;
-  int ps = 0;
-  if (active) {
-    ps = min(pos[row], cap - 1);  // the host guarantees pos < cap; the clamp keeps the cache write in the slot
-    u16x8 xv = ld16(qkv + (long)row * s_qkv + (long)j * D + 8 * t);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = bf2f(xv.v[e]);
-    p = x[0] * x[0];
+  for (int e = 0; e < 8; ++e) x[e] = bf2f(xv.v[e]);
+  float p = x[0] * x[0];
 #pragma unroll
-    for (int e = 1; e < 8; ++e) p = p + x[e] * x[e];
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = 0.f;
-  }
+  for (int e = 1; e < 8; ++e) p = p + x[e] * x[e];
 #pragma unroll
   for (int s = TPI / 2; s > 0; s >>= 1) p = p + __shfl_xor(p, s, 64);
   const float inv = 1.0f / sqrtf(p / (float)D + eps);
-  if (active) {
-    u16x8 wv = ld16((j < H ? wq : wk) + 8 * t);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) yv[e] = bf2f(f2bf(bf2f(f2bf(x[e] * inv)) * bf2f(wv.v[e])));
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) yv[e] = 0.f;
-  }
+  for (int e = 0; e < 8; ++e) yv[e] = bf2f(f2bf(bf2f(f2bf(x[e] * inv)) * bf2f(wv.v[e])));
   float yp[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) yp[e] = __shfl_xor(yv[e], TPI / 2, 64);
   if (!active) return;
-  u16x8 cv = ld16(cosb + (long)ps * s_cos + 8 * t);
-  u16x8 sv = ld16(sinb + (long)ps * s_cos + 8 * t);
   const bool first = t < TPI / 2;
   u16x8 ov;
 #pragma unroll
@@ -170,11 +167,9 @@ __global__ __launch_bounds__(256) void qk_norm_rope_cache_kernel(
   if (j < H) {
     st16(qo + (long)row * s_qo_b + (long)j * s_qo_h + 8 * t, ov);
   } else {
-    const int kh = j - H;
-    const long slot = slots[row];
     const long off = slot * sk_s + (long)kh * sk_h + (long)ps * sk_t + 8 * t;
     st16(kc + off, ov);
-    st16(vc + off, ld16(qkv + (long)row * s_qkv + (long)(H + KV + kh) * D + 8 * t));
+    st16(vc + off, vv);
   }
 }
 
@@ -232,6 +227,7 @@ __global__ __launch_bounds__(256) void add_norm_kernel(const uint16_t* __restric
   const int rb = active ? row / T : 0, rt = active ? row % T : 0;
   float v[8];
   float p = 0.f;
+  u16x8 wv, bv;
   if (active) {
     u16x8 xv = ld16(x + rb * sxb + rt * sxt + 8 * t);
 #pragma unroll
@@ -246,6 +242,9 @@ __global__ __launch_bounds__(256) void add_norm_kernel(const uint16_t* __restric
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[e] = rnd<DT>(v[e] + E<DT>::to_f(cv.v[e]));
     }
+    // affine parameters after the row's own loads: they arrive while the reductions run
+    wv = ld16(w + 8 * t);
+    if (kind == M3X_NORM_LAYER) bv = ld16(b + 8 * t);
     if (xo) {
       u16x8 ov;
 #pragma unroll
@@ -271,7 +270,6 @@ __global__ __launch_bounds__(256) void add_norm_kernel(const uint16_t* __restric
     const float var = row_tree_sum<TPR>(p, red, bcast) / (float)N;
     if (!active) return;
     const float sd = sqrtf(var + eps);
-    u16x8 wv = ld16(w + 8 * t), bv = ld16(b + 8 * t);
 #pragma unroll
     for (int e = 0; e < 8; ++e) yv.v[e] = E<DT>::from_f(d[e] / sd * E<DT>::to_f(wv.v[e]) + E<DT>::to_f(bv.v[e]));
   } else {
@@ -281,7 +279,6 @@ __global__ __launch_bounds__(256) void add_norm_kernel(const uint16_t* __restric
     const float ss = row_tree_sum<TPR>(p, red, bcast);
     if (!active) return;
     const float inv = 1.0f / sqrtf(ss / (float)N + eps);
-    u16x8 wv = ld16(w + 8 * t);
 #pragma unroll
     for (int e = 0; e < 8; ++e) yv.v[e] = E<DT>::from_f(rnd<DT>(v[e] * inv) * E<DT>::to_f(wv.v[e]));
   }

@@ -108,18 +108,53 @@ __device__ void topk_select(const float (&x)[SEPT], int V, int k, SampleSmem& sm
   }
   __syncthreads();
   const int bstar = sm.bstar;
+  // compaction: one LDS atomic per wave; lanes take consecutive places by ballot rank
+  const int lane = tid & 63;
+  const unsigned long long below = (1ull << lane) - 1ull;
+  unsigned long long masks[SEPT];
+  int total = 0;
+#pragma unroll
+  for (int e = 0; e < SEPT; ++e) {
+    masks[e] = __ballot(tid + ST * e < V && bk[e] <= bstar);
+    total += __popcll(masks[e]);
+  }
+  int base = 0;
+  if (total) {
+    if (lane == 0) base = atomicAdd(&sm.ncand, total);
+    base = __builtin_amdgcn_readfirstlane(base);
+  }
 #pragma unroll
   for (int e = 0; e < SEPT; ++e) {
     const int i = tid + ST * e;
-    if (i < V && bk[e] <= bstar) {
-      const int slot = atomicAdd(&sm.ncand, 1);
-      sm.cand[slot] = ((unsigned long long)ordkey(x[e]) << 32) | (unsigned long long)(0xffffffffu - (uint32_t)i);
-    }
+    if ((masks[e] >> lane) & 1ull)
+      sm.cand[base + __popcll(masks[e] & below)] =
+          ((unsigned long long)ordkey(x[e]) << 32) | (unsigned long long)(0xffffffffu - (uint32_t)i);
+    base += __popcll(masks[e]);
   }
   __syncthreads();
   const int nc = sm.ncand;
   int P2 = 2;
   while (P2 < nc) P2 <<= 1;
+  if (nc <= ST) {
+    // The usual case (top-k of a peaked row): rank placement. Keys are distinct (the index is part of the key),
+    // so candidate t goes to position #{j : key_j > key_t}; the reads of key_j are LDS broadcasts.
+    const unsigned long long key = tid < nc ? sm.cand[tid] : 0ull;
+    int rank = 0;
+    if ((tid & ~63) < nc) {  // waves holding no candidate skip the count
+      int j = 0;
+      for (; j + 8 <= nc; j += 8) {  // eight broadcast reads in flight per step
+        unsigned long long c8[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) c8[q] = sm.cand[j + q];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) rank += c8[q] > key ? 1 : 0;
+      }
+      for (; j < nc; ++j) rank += sm.cand[j] > key ? 1 : 0;
+    }
+    __syncthreads();
+    if (tid < nc) sm.cand[rank] = key;
+    __syncthreads();
+  } else {
   for (int i = nc + tid; i < P2; i += ST) sm.cand[i] = 0ull;
   __syncthreads();
   for (int kk = 2; kk <= P2; kk <<= 1) {
@@ -137,39 +172,78 @@ __device__ void topk_select(const float (&x)[SEPT], int V, int k, SampleSmem& sm
       __syncthreads();
     }
   }
+  }
   const int kk = k < nc ? k : nc;
   const float kth = ordkey_inv((uint32_t)(sm.cand[kk - 1] >> 32));
   const float x0 = ordkey_inv((uint32_t)(sm.cand[0] >> 32));
-  int local = 0;
+  // the kept set (x >= kth) is a prefix of the sorted order: its last member records the length
   for (int j = tid; j < nc; j += ST) {
     const float xj = ordkey_inv((uint32_t)(sm.cand[j] >> 32));
     if (xj >= kth) {
-      ++local;
       sm.w[j] = m3x_expf(xj - x0);
+      if (j + 1 == nc || !(ordkey_inv((uint32_t)(sm.cand[j + 1] >> 32)) >= kth)) sm.nkeep = j + 1;
     }
   }
-  if (local) atomicAdd(&sm.nkeep, local);
   __syncthreads();
 }
 
 __device__ __forceinline__ int cand_index(unsigned long long c) { return (int)(0xffffffffu - (uint32_t)c); }
 
-// Inverse-CDF pick over cand[0..n) skipping index `skip` (-1: none); returns -1 when the weights sum to 0.
-__device__ int pick(const SampleSmem& sm, int n, float u, int skip) {
-  float S = 0.f;
-  int last = -1;
-  for (int j = 0; j < n; ++j) {
-    if (cand_index(sm.cand[j]) == skip) continue;
-    S = S + sm.w[j];
-    last = j;
+__device__ __forceinline__ float lanef(float v, int q) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), q));
+}
+
+// Sequential fp32 sums of w over cand[0..n) in order, skipping index `skip` (-1: none), by one wave. The weights
+// of 64 candidates sit one per lane (a skipped or absent one as +0.0, which leaves a sum that is never -0 exactly
+// unchanged) and are added in order through readlane; every lane keeps the running sum at its own position.
+// Running sums of chunks after the first are stored over their weights in sm.w. Returns the total (same value
+// in every lane); *last = position of the last term, -1 if none; *first_use / *first_run = the first chunk's
+// ballot of terms and this lane's running sum.
+__device__ float wave_prefix(SampleSmem& sm, int n, int skip, int* last, unsigned long long* first_use,
+                             float* first_run) {
+  const int lane = threadIdx.x & 63;
+  float c = 0.f;
+  int l = -1;
+  for (int j0 = 0; j0 < n; j0 += 64) {
+    const int j = j0 + lane;
+    const bool in = j < n && cand_index(sm.cand[j]) != skip;
+    const float wsel = in ? sm.w[j] : 0.f;
+    const unsigned long long use = __ballot(in);
+    float mine = 0.f;
+#pragma unroll
+    for (int q = 0; q < 64; ++q) {
+      c = c + lanef(wsel, q);
+      mine = lane == q ? c : mine;
+    }
+    if (use) l = j0 + 63 - __clzll((long long)use);
+    if (j0 == 0) {
+      *first_use = use;
+      *first_run = mine;
+    } else if (j < n) {
+      sm.w[j] = mine;
+    }
   }
+  *last = l;
+  return c;
+}
+
+// Inverse-CDF pick over cand[0..n) skipping index `skip`: the first position whose running sum (the same
+// sequential fp32 order as the total S) exceeds u * S, else the last term; -1 when the weights sum to 0.
+// Called by one whole wave; every lane returns the same index. Overwrites sm.w past the first 64 candidates.
+__device__ int pick(SampleSmem& sm, int n, float u, int skip) {
+  const int lane = threadIdx.x & 63;
+  int last;
+  unsigned long long use0 = 0;
+  float run0 = 0.f;
+  const float S = wave_prefix(sm, n, skip, &last, &use0, &run0);
   if (last < 0 || !(S > 0.f)) return -1;
   const float t = u * S;
-  float c = 0.f;
-  for (int j = 0; j < n; ++j) {
-    if (cand_index(sm.cand[j]) == skip) continue;
-    c = c + sm.w[j];
-    if (c > t) return cand_index(sm.cand[j]);
+  unsigned long long hit = use0 & __ballot(run0 > t);
+  if (hit) return cand_index(sm.cand[__ffsll((long long)hit) - 1]);
+  for (int j0 = 64; j0 < n; j0 += 64) {
+    const int j = j0 + lane;
+    hit = __ballot(j < n && cand_index(sm.cand[j]) != skip && sm.w[j] > t);
+    if (hit) return cand_index(sm.cand[j0 + __ffsll((long long)hit) - 1]);
   }
   return cand_index(sm.cand[last]);
 }
@@ -184,6 +258,7 @@ __global__ __launch_bounds__(ST) void topk_sample_kernel(const uint16_t* __restr
                                                          int top_k, int greedy, void* out, long ld_out, int out_i64) {
   __shared__ SampleSmem sm;
   const int row = blockIdx.x;
+  const float ur = greedy ? 0.f : u[(long)row * ld_u];  // loaded first: its latency overlaps the selection
   float x[SEPT];
 #pragma unroll
   for (int e = 0; e < SEPT; ++e) {
@@ -191,12 +266,13 @@ __global__ __launch_bounds__(ST) void topk_sample_kernel(const uint16_t* __restr
     x[e] = i < V ? E<DT>::to_f(logits[(long)row * ld_l + i]) * inv_temp : -INFINITY;
   }
   topk_select(x, V, top_k, sm);
-  if (threadIdx.x != 0) return;
+  if (threadIdx.x >= 64) return;  // wave 0 draws
   int code = cand_index(sm.cand[0]);
   if (!greedy) {
-    const int c = pick(sm, sm.nkeep, u[(long)row * ld_u], -1);
+    const int c = pick(sm, sm.nkeep, ur, -1);
     if (c >= 0) code = c;
   }
+  if (threadIdx.x != 0) return;
   if (out_i64)
     ((int64_t*)out)[(long)row * ld_out] = code;
   else
@@ -268,6 +344,7 @@ __global__ __launch_bounds__(ST) void cb0_sample_kernel(Cb0Args a) {
   k = k < 1 ? 1 : (k > a.V ? a.V : k);
   const float bias = a.aeos_bias ? a.aeos_bias[s] : 0.f;
   const float rep = a.rep_t ? a.rep_t[s] : 0.f;
+  const float uu = a.u[(long)row * a.ld_u];  // loaded first: its latency overlaps the selection
   float x[SEPT];
 #pragma unroll
   for (int e = 0; e < SEPT; ++e) {
@@ -285,18 +362,27 @@ __global__ __launch_bounds__(ST) void cb0_sample_kernel(Cb0Args a) {
     x[e] = v;
   }
   topk_select(x, a.V, k, sm);
-  if (threadIdx.x != 0) return;
+  if (threadIdx.x >= 64) return;  // wave 0 draws; lane 0 writes
   const int n = sm.nkeep;
-  const float uu = a.u[(long)row * a.ld_u];
   int cb0;
   int64_t stop = 0;
   if (a.aeos >= 0) {
-    float S = 0.f, wa = 0.f;
-    for (int j = 0; j < n; ++j) {
-      S = S + sm.w[j];
-      if (cand_index(sm.cand[j]) == a.aeos) wa = sm.w[j];
+    float wa = 0.f;  // weight of the AEOS candidate (indices are distinct: at most one)
+    for (int j0 = 0; j0 < n; j0 += 64) {
+      const int j = j0 + (int)(threadIdx.x & 63);
+      const unsigned long long m = __ballot(j < n && cand_index(sm.cand[j]) == a.aeos);
+      if (m) wa = sm.w[j0 + __ffsll((long long)m) - 1];
+    }
+    float S = 0.f;  // every kept weight in order (sequential fp32), read before pick reuses sm.w
+    for (int j0 = 0; j0 < n; j0 += 64) {
+      const int j = j0 + (int)(threadIdx.x & 63);
+      const float wj = j < n ? sm.w[j] : 0.f;
+#pragma unroll
+      for (int q = 0; q < 64; ++q) S = S + lanef(wj, q);
     }
     const float pa = wa / S;
+    const int c = pick(sm, n, uu, a.aeos);
+    if (threadIdx.x != 0) return;
     const int arg = cand_index(sm.cand[0]);
     if (a.frames_t && a.min_t && a.hazard_t) {
       const bool can = a.frames_t[s] >= a.min_t[s];
@@ -308,10 +394,10 @@ __global__ __launch_bounds__(ST) void cb0_sample_kernel(Cb0Args a) {
       a.hazard_t[s] = hz;
       a.frames_t[s] = a.frames_t[s] + 1;
     }
-    const int c = pick(sm, n, uu, a.aeos);
     cb0 = c < 0 ? 0 : c;
   } else {
     const int c = pick(sm, n, uu, -1);
+    if (threadIdx.x != 0) return;
     cb0 = c < 0 ? cand_index(sm.cand[0]) : c;
   }
   if (a.ctr_t) a.ctr_t[s] = a.ctr_t[s] + 1;
