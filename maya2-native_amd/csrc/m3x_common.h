@@ -31,12 +31,9 @@ enum { M3X_BF16 = 0, M3X_F16 = 1, M3X_F32 = 2 };
 // leave fp32, so both the kernels and the C oracle round identically (round-to-nearest-even).
 __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
 
-__device__ __forceinline__ uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
+// gfx950's v_cvt_pk_bf16_f32 (two values per instruction, round-to-nearest-even): identical to the oracle's
+// integer rounding for every non-NaN input; a NaN stays a NaN (its payload bits may differ).
+__device__ __forceinline__ uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
