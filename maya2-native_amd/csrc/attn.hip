@@ -270,40 +270,53 @@ M3X_API int m3x_decode_attn(const void* q, long sq_b, long sq_h, const void* k_c
 // positions p0..p0+T-1. Queries t in [tq0, T) attend keys 0..p0+t; output row (b, t - tq0) at out + b*sob + tq*sot.
 // One workgroup (64 threads) per (b, head); HD in {64, 128}, np <= 64. Scores: lane j owns key j and reads its
 // K row as 16-byte pieces (4 independent fp32 partial sums); P.V: lane c owns dims 2c, 2c+1 (32-bit loads, rows
-// coalesced across the wave).
+// coalesced across the wave), keys taken in ascending order 16 loads at a time.
+// With write_kv the keys and values of this call's own positions are read from qkv (the bytes being stored), so
+// no load waits on this kernel's own stores and every load is issued before the first wait.
 template <int DT, int HD>
 __global__ __launch_bounds__(64) void depth_attn_kernel(const uint16_t* __restrict__ qkv, long sqb, long sqt,
                                                         uint16_t* kd, uint16_t* vd, uint16_t* __restrict__ out,
                                                         long sob, long sot, int T, int p0, int tq0, int H, int np,
                                                         float scale, int write_kv) {
   constexpr int VEC = HD / 8;
+  constexpr int KQ = 16;  // V rows in flight per step
   const int b = blockIdx.x;
   const int h = blockIdx.y;
   const int lane = threadIdx.x;
   uint16_t* kb = kd + ((long)b * H + h) * np * HD;
   uint16_t* vb = vd + ((long)b * H + h) * np * HD;
+  const uint16_t* qb = qkv + (long)b * sqb + (long)h * HD;  // q of row t at qb + t*sqt; k at +H*HD; v at +2*H*HD
+  // key/value row j of this (b, h): the scratch below p0 (or always without write_kv), else this call's qkv row
+  const int own = write_kv ? p0 : np;
+  auto krow = [&](int j) { return j < own ? kb + (long)j * HD : qb + (long)(j - p0) * sqt + (long)H * HD; };
+  auto vrow = [&](int j) { return j < own ? vb + (long)j * HD : qb + (long)(j - p0) * sqt + 2L * H * HD; };
   if (write_kv) {
     for (int i = lane; i < T * VEC; i += 64) {
       const int t = i / VEC, c = i % VEC;
-      const uint16_t* src = qkv + (long)b * sqb + (long)t * sqt + (long)h * HD + 8 * c;
+      const uint16_t* src = qb + (long)t * sqt + 8 * c;
       st16(kb + (long)(p0 + t) * HD + 8 * c, ld16(src + (long)H * HD));
       st16(vb + (long)(p0 + t) * HD + 8 * c, ld16(src + 2L * H * HD));
     }
-    __syncthreads();
   }
   __shared__ float qs[HD];
   __shared__ float ps[64];
   for (int t = tq0; t < T; ++t) {
     const int nk = p0 + t + 1;
-    const uint16_t* src = qkv + (long)b * sqb + (long)t * sqt + (long)h * HD;
-    for (int d = lane; d < HD; d += 64) qs[d] = E<DT>::to_f(src[d]);
+    // issue the K row (lane j < nk), this query's q, and the first V rows before any wait
+    u16x8 kv[VEC];
+    const uint16_t* kr = krow(min(lane, nk - 1));
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) kv[c] = ld16(kr + 8 * c);
+    const bool pv = 2 * lane < HD;
+    const int dcol = pv ? 2 * lane : 0;
+    uint32_t v2[KQ];
+#pragma unroll
+    for (int q = 0; q < KQ; ++q) v2[q] = *reinterpret_cast<const uint32_t*>(vrow(min(q, nk - 1)) + dcol);
+    const uint16_t* qsrc = qb + (long)t * sqt;
+    for (int d = lane; d < HD; d += 64) qs[d] = E<DT>::to_f(qsrc[d]);
     __syncthreads();
     float sc = -INFINITY;
     if (lane < nk) {
-      const uint16_t* kr = kb + (long)lane * HD;
-      u16x8 kv[VEC];
-#pragma unroll
-      for (int c = 0; c < VEC; ++c) kv[c] = ld16(kr + 8 * c);
       float a[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < VEC; ++c)
@@ -316,14 +329,24 @@ __global__ __launch_bounds__(64) void depth_attn_kernel(const uint16_t* __restri
     const float l = wave_sum_xor(pe, 64);
     ps[lane] = pe;
     __syncthreads();
-    if (2 * lane < HD) {
-      uint16_t* o = out + (long)b * sob + (long)(t - tq0) * sot + (long)h * HD + 2 * lane;
-      float a0 = 0.f, a1 = 0.f;
-      for (int j = 0; j < nk; ++j) {
-        const uint32_t v2 = *reinterpret_cast<const uint32_t*>(vb + (long)j * HD + 2 * lane);
-        a0 = fmaf(ps[j], E<DT>::to_f((uint16_t)(v2 & 0xffffu)), a0);
-        a1 = fmaf(ps[j], E<DT>::to_f((uint16_t)(v2 >> 16)), a1);
+    float a0 = 0.f, a1 = 0.f;
+    for (int j0 = 0; j0 < nk; j0 += KQ) {
+      if (j0 > 0) {
+#pragma unroll
+        for (int q = 0; q < KQ; ++q)
+          v2[q] = *reinterpret_cast<const uint32_t*>(vrow(min(j0 + q, nk - 1)) + dcol);
       }
+#pragma unroll
+      for (int q = 0; q < KQ; ++q) {
+        if (j0 + q < nk) {
+          const float p = ps[j0 + q];
+          a0 = fmaf(p, E<DT>::to_f((uint16_t)(v2[q] & 0xffffu)), a0);
+          a1 = fmaf(p, E<DT>::to_f((uint16_t)(v2[q] >> 16)), a1);
+        }
+      }
+    }
+    if (pv) {
+      uint16_t* o = out + (long)b * sob + (long)(t - tq0) * sot + (long)h * HD + 2 * lane;
       const uint32_t packed = (uint32_t)E<DT>::from_f(a0 / l) | ((uint32_t)E<DT>::from_f(a1 / l) << 16);
       *reinterpret_cast<uint32_t*>(o) = packed;
     }

@@ -45,6 +45,70 @@ __global__ __launch_bounds__(256) void pack_weight_kernel(const uint16_t* __rest
   st16(out + v * 8, x);
 }
 
+// The KW K-slice partials of one weight tile meet in LDS (`red`, free when this runs) and are added in slice
+// order by slice 0, which then applies the epilogue. Lane (li, lg) holds weight rows n0 + 4*lg + r of
+// activation row m0 + 16*t + li.
+template <int DT, int MT, int NW, int EPI>
+__device__ __forceinline__ void linear_finish(f32x4_t (&acc)[EPI == EPI_SWIGLU ? 2 : 1][MT], f32x4_t* red, int wn,
+                                              int wk, int lane, int n0, int m0, uint16_t* __restrict__ Y, long ldy,
+                                              int M, int N) {
+  constexpr int KW = 4 / NW;
+  constexpr int NA = EPI == EPI_SWIGLU ? 2 : 1;
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+  if constexpr (KW > 1) {
+    if (wk > 0) {
+#pragma unroll
+      for (int a = 0; a < NA; ++a)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) red[(((wk - 1) * NW + wn) * NA * MT + a * MT + t) * 64 + lane] = acc[a][t];
+    }
+    __syncthreads();
+    if (wk > 0) return;
+#pragma unroll
+    for (int j = 0; j < KW - 1; ++j)
+#pragma unroll
+      for (int a = 0; a < NA; ++a)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          const f32x4_t v = red[((j * NW + wn) * NA * MT + a * MT + t) * 64 + lane];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[a][t][r] = acc[a][t][r] + v[r];
+        }
+  }
+  const int n = n0 + 4 * lg;
+  const bool vec = (ldy & 3) == 0 && (((uintptr_t)Y) & 7) == 0 && n + 3 < N;
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const int m = m0 + 16 * t + li;
+    if (m >= M) continue;
+    uint16_t o[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v = rnd<DT>(acc[0][t][r]);
+      if constexpr (EPI == EPI_SWIGLU) {
+        const float g = v;
+        const float u = rnd<DT>(acc[NA - 1][t][r]);
+        v = rnd<DT>(g / (1.0f + expf(-g))) * u;
+      } else if constexpr (EPI == EPI_GELU) {
+        v = 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+      }
+      o[r] = E<DT>::from_f(v);
+    }
+    uint16_t* yp = Y + (long)m * ldy + n;
+    if (vec) {
+      uint2 pk;
+      pk.x = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
+      pk.y = (uint32_t)o[2] | ((uint32_t)o[3] << 16);
+      *reinterpret_cast<uint2*>(yp) = pk;
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (n + r < N) yp[r] = o[r];
+    }
+  }
+}
+
 template <int DT, int MT, int NW, int EPI>
 __global__ __launch_bounds__(256) void linear_kernel(const uint16_t* __restrict__ X, long ldx,
                                                      const uint16_t* __restrict__ Wp,
@@ -178,67 +242,118 @@ __global__ __launch_bounds__(256) void linear_kernel(const uint16_t* __restrict_
     __syncthreads();
   }
 
-  // ---- the KW slices of one weight tile meet in LDS (free after the loop's last barrier), in slice order
-  if constexpr (KW > 1) {
-    f32x4_t* red = reinterpret_cast<f32x4_t*>(&xs[0][0]);
-    if (wk > 0) {
-#pragma unroll
-      for (int a = 0; a < NA; ++a)
-#pragma unroll
-        for (int t = 0; t < MT; ++t) red[(((wk - 1) * NW + wn) * NA * MT + a * MT + t) * 64 + lane] = acc[a][t];
-    }
-    __syncthreads();
-    if (wk > 0) return;
-#pragma unroll
-    for (int j = 0; j < KW - 1; ++j)
-#pragma unroll
-      for (int a = 0; a < NA; ++a)
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-          const f32x4_t v = red[((j * NW + wn) * NA * MT + a * MT + t) * 64 + lane];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[a][t][r] = acc[a][t][r] + v[r];
-        }
-  }
+  linear_finish<DT, MT, NW, EPI>(acc, reinterpret_cast<f32x4_t*>(&xs[0][0]), wn, wk, lane, n0, m0, Y, ldy, M, N);
+}
 
-  // ---- epilogue: lane holds weight rows n0 + 4*lg + r of activation row m0 + 16*t + li
-  const int n = n0 + 4 * lg;
-  const bool vec = (ldy & 3) == 0 && (((uintptr_t)Y) & 7) == 0 && n + 3 < N;
+// One-shot variant for short K slices (S = K / KW / 32 steps of 32, S in {8, 16}): every weight fragment of the
+// wave's slice and the workgroup's whole activation block are loaded at once, so the kernel pays one memory
+// latency instead of one per chunk. The block sits in LDS without padding; 16-byte granule g of row r is stored
+// at g ^ (r % 16), so the 16 rows a fragment read touches fall in 16 different bank groups.
+template <int DT, int MT, int NW, int EPI, int S>
+__global__ __launch_bounds__(256) void linear_oneshot_kernel(const uint16_t* __restrict__ X, long ldx,
+                                                             const uint16_t* __restrict__ Wp,
+                                                             const uint16_t* __restrict__ W2p,
+                                                             uint16_t* __restrict__ Y, long ldy, int M, int N, int K,
+                                                             int mblk, int nblk) {
+  constexpr int KW = 4 / NW;
+  constexpr int ROWS = 16 * MT;
+  constexpr int KS = 32 * S;          // k per slice
+  constexpr int GR = 4 * S;           // 16-byte granules per row of a slice
+  constexpr int NVEC = KW * ROWS * GR;
+  static_assert(NVEC % 256 == 0 && GR >= 16, "one-shot geometry");
+  constexpr int VPT = NVEC / 256;
+  constexpr bool DUAL = EPI == EPI_SWIGLU;
+  constexpr int NA = DUAL ? 2 : 1;
+  __shared__ __align__(16) uint16_t xs[KW * ROWS * KS];
+
+  const int xcd = blockIdx.x & 7;
+  const int slot = blockIdx.x >> 3;
+  const int nb = (slot / mblk) * 8 + xcd;
+  const int mb = slot - (slot / mblk) * mblk;
+  if (nb >= nblk) return;  // padding block: the whole workgroup leaves before any barrier
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+  const int wn = wave % NW;
+  const int wk = wave / NW;
+  const int ntiles = (N + 15) >> 4;
+  const int n0 = (nb * NW + wn) * 16;
+  const int nt = min(nb * NW + wn, ntiles - 1);
+  const int m0 = mb * ROWS;
+  const int ksteps = K >> 5;
+  const int s0 = wk * S;
+
+  u16x8 Wr[S][NA];
+  {
+    const uint16_t* w0 = Wp + ((long)nt * ksteps * 64 + lane) * 8;
+    const uint16_t* w1 = DUAL ? W2p + ((long)nt * ksteps * 64 + lane) * 8 : w0;
 #pragma unroll
-  for (int t = 0; t < MT; ++t) {
-    const int m = m0 + 16 * t + li;
-    if (m >= M) continue;
-    uint16_t o[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float v = rnd<DT>(acc[0][t][r]);
-      if constexpr (EPI == EPI_SWIGLU) {
-        const float g = v;
-        const float u = rnd<DT>(acc[NA - 1][t][r]);
-        v = rnd<DT>(g / (1.0f + expf(-g))) * u;
-      } else if constexpr (EPI == EPI_GELU) {
-        v = 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
-      }
-      o[r] = E<DT>::from_f(v);
-    }
-    uint16_t* yp = Y + (long)m * ldy + n;
-    if (vec) {
-      uint2 pk;
-      pk.x = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
-      pk.y = (uint32_t)o[2] | ((uint32_t)o[3] << 16);
-      *reinterpret_cast<uint2*>(yp) = pk;
-    } else {
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (n + r < N) yp[r] = o[r];
+    for (int s = 0; s < S; ++s) {
+      Wr[s][0] = ld16(w0 + (long)(s0 + s) * 512);
+      if constexpr (DUAL) Wr[s][NA - 1] = ld16(w1 + (long)(s0 + s) * 512);
     }
   }
+  u16x8 Xr[VPT];
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int v = tid + 256 * j;
+    const int q = v / (ROWS * GR);
+    const int rem = v - q * (ROWS * GR);
+    const int r = rem / GR;
+    const int g = rem - r * GR;
+    const int m = m0 + r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) Xr[j].v[e] = 0;
+    if (m < M) Xr[j] = ld16(X + (long)m * ldx + q * KS + g * 8);
+  }
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int v = tid + 256 * j;
+    const int q = v / (ROWS * GR);
+    const int rem = v - q * (ROWS * GR);
+    const int r = rem / GR;
+    const int g = rem - r * GR;
+    st16(&xs[(q * ROWS + r) * KS + ((g ^ (r & 15)) << 3)], Xr[j]);
+  }
+  __syncthreads();
+
+  f32x4_t acc[NA][MT];
+#pragma unroll
+  for (int a = 0; a < NA; ++a)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[a][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const uint16_t* xb = &xs[(wk * ROWS + li) * KS];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const u16x8 b = *reinterpret_cast<const u16x8*>(xb + t * 16 * KS + (((4 * s + lg) ^ li) << 3));
+#pragma unroll
+      for (int a = 0; a < NA; ++a) acc[a][t] = mfma16x16x32<DT>(Wr[s][a], b, acc[a][t]);
+    }
+  }
+  __syncthreads();  // every wave is done with the block before it holds the slice partials
+  linear_finish<DT, MT, NW, EPI>(acc, reinterpret_cast<f32x4_t*>(xs), wn, wk, lane, n0, m0, Y, ldy, M, N);
 }
 
 // Launch geometry: MT activation tiles of 16 rows per workgroup; NW weight tiles per workgroup (4 / NW K slices).
 struct LinearPlan {
   int mt, nw, mblk, nblk;
+  int oneshot;  // steps per K slice for the one-shot kernel (8 or 16), 0 for the chunked kernel
 };
+
+// One-shot applies when each of the 4/nw K slices is exactly 8 or 16 steps of 32 and the activation block
+// (16*mt rows x K) fits in 64 KB of LDS.
+static int oneshot_steps(int mt, int nw, int K) {
+  const int kw = 4 / nw;
+  if (K % (32 * kw)) return 0;
+  const int s = K / 32 / kw;
+  if ((s != 8 && s != 16) || (long)16 * mt * K * 2 > 65536) return 0;
+  return s;
+}
 
 // Tile choice measured on MI355X (graph-timed sweep over the decode shapes, M = 1..2264): the best plan is the
 // largest tile that still gives at least ~400 workgroups; MT = 2 pays off only above ~112 rows.
@@ -258,27 +373,59 @@ static LinearPlan linear_plan(int M, int N, int K) {
     p.nw = blocks(1, 4) >= 400 ? 4 : (blocks(1, 2) >= 400 ? 2 : 1);
   }
   while (p.nw < 4 && ksteps / (4 / p.nw) < 4) p.nw <<= 1;  // at least one chunk per K slice
+  // Small weights (N <= 2048, K <= 1024) at up to 512 rows: 16-row blocks through the one-shot kernel.
+  if (M > 112 && M <= 512 && N <= 2048 && K <= 1024 && oneshot_steps(1, 2, K)) {
+    p.mt = 1;
+    p.nw = blocks(1, 2) >= 400 || !oneshot_steps(1, 1, K) ? 2 : 1;
+  }
   p.mblk = m3x_ceil_div(M, 16 * p.mt);
   p.nblk = m3x_ceil_div(ntiles, p.nw);
+  // One-shot when its activation block leaves room for several workgroups per CU (<= 32 KB), or when only a
+  // handful of rows exist (a 64 KB block then costs nothing in latency): measured on the decode shapes, the
+  // one-shot kernel is 0.5-1.1 us faster in those cases and slower with 32-row blocks of 64 KB.
+  p.oneshot = oneshot_steps(p.mt, p.nw, K);
+  if (p.oneshot && (long)16 * p.mt * K * 2 > 32768 && M > 16) p.oneshot = 0;
   return p;
 }
 
+// Launches the plan's kernel; false (nothing launched) for a plan no kernel instance covers.
 template <int DT, int EPI>
-static void launch_linear(const LinearPlan& p, hipStream_t st, const uint16_t* X, long ldx, const uint16_t* W,
+static bool launch_linear(const LinearPlan& p, hipStream_t st, const uint16_t* X, long ldx, const uint16_t* W,
                           const uint16_t* W2, uint16_t* Y, long ldy, int M, int N, int K) {
   const dim3 grid(m3x_ceil_div(p.nblk, 8) * 8 * p.mblk);
+#define M3X_ONE(MTT, NWW, SS)                                                                                  \
+  hipLaunchKernelGGL((linear_oneshot_kernel<DT, MTT, NWW, EPI, SS>), grid, dim3(256), 0, st, X, ldx, W, W2, Y, \
+                     ldy, M, N, K, p.mblk, p.nblk)
+  if (p.oneshot) {
+    const int key = p.mt * 100 + p.nw * 10 + (p.oneshot == 16 ? 1 : 0);
+    switch (key) {
+      case 121: M3X_ONE(1, 2, 16); return true;
+      case 120: M3X_ONE(1, 2, 8); return true;
+      case 111: M3X_ONE(1, 1, 16); return true;
+      case 110: M3X_ONE(1, 1, 8); return true;
+      case 141: M3X_ONE(1, 4, 16); return true;
+      case 140: M3X_ONE(1, 4, 8); return true;
+      case 221: M3X_ONE(2, 2, 16); return true;
+      case 220: M3X_ONE(2, 2, 8); return true;
+      case 241: M3X_ONE(2, 4, 16); return true;
+      case 240: M3X_ONE(2, 4, 8); return true;
+      case 210: M3X_ONE(2, 1, 8); return true;
+      default: return false;
+    }
+  }
+#undef M3X_ONE
 #define M3X_LIN(MTT, NWW)                                                                                           \
   hipLaunchKernelGGL((linear_kernel<DT, MTT, NWW, EPI>), grid, dim3(256), 0, st, X, ldx, W, W2, Y, ldy, M, N, K, \
                      p.mblk, p.nblk)
-  if (p.mt == 1) {
-    if (p.nw == 4) M3X_LIN(1, 4);
-    else if (p.nw == 2) M3X_LIN(1, 2);
-    else M3X_LIN(1, 1);
-  } else if (p.mt == 2) {
-    if (p.nw == 4) M3X_LIN(2, 4);
-    else M3X_LIN(2, 2);
-  } else {
-    M3X_LIN(4, 4);
+  const int key = p.mt * 10 + p.nw;
+  switch (key) {
+    case 14: M3X_LIN(1, 4); return true;
+    case 12: M3X_LIN(1, 2); return true;
+    case 11: M3X_LIN(1, 1); return true;
+    case 24: M3X_LIN(2, 4); return true;
+    case 22: M3X_LIN(2, 2); return true;
+    case 44: M3X_LIN(4, 4); return true;
+    default: return false;
   }
 #undef M3X_LIN
 }
@@ -296,17 +443,19 @@ static int linear_common(const void* x, long ldx, const void* w, const void* w2,
   hipStream_t st = (hipStream_t)stream;
   const uint16_t *X = (const uint16_t*)x, *Wt = (const uint16_t*)w, *W2 = (const uint16_t*)w2;
   uint16_t* Y = (uint16_t*)y;
+  bool ok;
   if (dtype == M3X_BF16) {
-    if (epi == EPI_NONE) launch_linear<M3X_BF16, EPI_NONE>(p, st, X, ldx, Wt, W2, Y, ldy, M, N, K);
-    else if (epi == EPI_SWIGLU) launch_linear<M3X_BF16, EPI_SWIGLU>(p, st, X, ldx, Wt, W2, Y, ldy, M, N, K);
-    else launch_linear<M3X_BF16, EPI_GELU>(p, st, X, ldx, Wt, W2, Y, ldy, M, N, K);
+    if (epi == EPI_NONE) ok = launch_linear<M3X_BF16, EPI_NONE>(p, st, X, ldx, Wt, W2, Y, ldy, M, N, K);
+    else if (epi == EPI_SWIGLU) ok = launch_linear<M3X_BF16, EPI_SWIGLU>(p, st, X, ldx, Wt, W2, Y, ldy, M, N, K);
+    else ok = launch_linear<M3X_BF16, EPI_GELU>(p, st, X, ldx, Wt, W2, Y, ldy, M, N, K);
   } else if (dtype == M3X_F16) {
-    if (epi == EPI_NONE) launch_linear<M3X_F16, EPI_NONE>(p, st, X, ldx, Wt, W2, Y, ldy, M, N, K);
-    else if (epi == EPI_SWIGLU) launch_linear<M3X_F16, EPI_SWIGLU>(p, st, X, ldx, Wt, W2, Y, ldy, M, N, K);
-    else launch_linear<M3X_F16, EPI_GELU>(p, st, X, ldx, Wt, W2, Y, ldy, M, N, K);
+    if (epi == EPI_NONE) ok = launch_linear<M3X_F16, EPI_NONE>(p, st, X, ldx, Wt, W2, Y, ldy, M, N, K);
+    else if (epi == EPI_SWIGLU) ok = launch_linear<M3X_F16, EPI_SWIGLU>(p, st, X, ldx, Wt, W2, Y, ldy, M, N, K);
+    else ok = launch_linear<M3X_F16, EPI_GELU>(p, st, X, ldx, Wt, W2, Y, ldy, M, N, K);
   } else {
     return M3X_EUNSUPPORTED;
   }
+  if (!ok) return M3X_EUNSUPPORTED;
   M3X_CHECK_LAUNCH();
   return M3X_OK;
 }
