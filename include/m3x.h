@@ -124,6 +124,16 @@ int m3x_depth_attn(const void* qkv, long sqb, long sqt, void* kd, void* vd, void
 int m3x_topk_sample(const void* logits, long ld_l, int V, const float* u, long ld_u, float inv_temp, int top_k,
                     int greedy, void* out, long ld_out, int out_i64, int B, int dtype, void* stream);
 
+/* m3x_topk_sample, then the next codebook's input from each drawn code: prefix[b*ld_prefix + j] =
+ * table[code*ld_table + j] (j < n, n = 1024 or 2048, codes clamped to [0, table_rows)); with y given, also
+ * x_out[b*n + j] = that row and y[b*n + j] = its LayerNorm (kind 0: w, bias) or RMSNorm (kind 1: w), the
+ * arithmetic of m3x_add_norm with no addend. Replaces, per codebook, the sampler + the prefix-row gather
+ * (serve/fast_depth.py:137-138) + the next level's input norm (serve/fast_depth.py:164). */
+int m3x_topk_sample_embed(const void* logits, long ld_l, int V, const float* u, long ld_u, float inv_temp, int top_k,
+                          int greedy, void* out, long ld_out, int out_i64, int B, const void* table, long ld_table,
+                          long table_rows, void* prefix, long ld_prefix, void* x_out, void* y, const void* w,
+                          const void* b, float eps, int kind, int n, int dtype, void* stream);
+
 /* cb0 controlled stop + sampling per seat (per-slot state indexed by slots[b]); any per-slot pointer may be NULL.
  * Replaces `Engine._cb0` (maya3/engine.py:652-694) with caller uniforms in place of `row_exponential`
  * (serve/fast_depth_kernels.py:82-98). */

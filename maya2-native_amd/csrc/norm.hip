@@ -1,38 +1,7 @@
 // Row-normalisation kernels of the frame step.
 //
-// Reduction order (the one the C oracle restates; bit-exactness depends on it): a row of N elements is read
-// as N/8 groups of 8 contiguous elements, one group per thread. A thread sums its 8 squares left to right
-// (each product and each sum rounded to fp32), then the N/8 partials are folded in half repeatedly:
-// p[g] = p[g] + p[g + s] for s = N/16, N/32, ..., 1. Within a wave the fold is an xor butterfly, which gives
-// lane g < s exactly p[g] + p[g + s].
-#include "m3x_common.h"
-
-// ---------------------------------------------------------------------------------------------------------
-// fold-in-half tree over TPR threads per row; rows are packed 256/TPR per block. Returns the row total in
-// every thread of the row.
-template <int TPR>
-__device__ __forceinline__ float row_tree_sum(float p, float* red, float* bcast) {
-  const int t = threadIdx.x % TPR;
-  const int rb = threadIdx.x / TPR;
-  if constexpr (TPR > 64) {
-    red[threadIdx.x] = p;
-    __syncthreads();
-#pragma unroll
-    for (int s = TPR / 2; s >= 64; s >>= 1) {
-      if (t < s) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + s];
-      __syncthreads();
-    }
-    p = red[threadIdx.x];
-  }
-  constexpr int W = TPR < 64 ? TPR : 64;
-#pragma unroll
-  for (int s = W / 2; s > 0; s >>= 1) p = p + __shfl_xor(p, s, 64);
-  if (t == 0) bcast[rb] = p;
-  __syncthreads();
-  float r = bcast[rb];
-  __syncthreads();
-  return r;
-}
+// The reduction order every kernel here follows (row_tree_sum, m3x_norm.h) is the one the C oracle restates.
+#include "m3x_norm.h"
 
 // ---------------------------------------------------------------------------------------------------------
 // K3: h' = bf16(h + a); y = bf16(bf16(h' * (1/sqrt(mean(h'^2) + eps))) * w).  a == nullptr: plain RMSNorm of h.
@@ -208,7 +177,6 @@ M3X_API int m3x_qk_norm_rope_cache(const void* qkv, long s_qkv, void* q_out, lon
 // y = LayerNorm(x') (fp32 statistics, affine w/b) or RMSNorm(x') (bf16(bf16(x*inv)*w), Qwen3 convention).
 // serve/fast_depth_kernels.py:14-45 (_add_ln); the RMS variant serves the SwiGLU/RMSNorm depth trunk.
 // a == nullptr: x' = x (plain norm of the input, serve/fast_depth.py:164).
-enum { M3X_NORM_LAYER = 0, M3X_NORM_RMS = 1 };
 
 template <int TPR, int DT>
 __global__ __launch_bounds__(256) void add_norm_kernel(const uint16_t* __restrict__ x, long sxb, long sxt,
@@ -226,8 +194,7 @@ __global__ __launch_bounds__(256) void add_norm_kernel(const uint16_t* __restric
   const bool active = row < rows;
   const int rb = active ? row / T : 0, rt = active ? row % T : 0;
   float v[8];
-  float p = 0.f;
-  u16x8 wv, bv;
+  u16x8 wv = {}, bv = {};
   if (active) {
     u16x8 xv = ld16(x + rb * sxb + rt * sxt + 8 * t);
 #pragma unroll
@@ -255,33 +222,8 @@ __global__ __launch_bounds__(256) void add_norm_kernel(const uint16_t* __restric
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = 0.f;
   }
-  u16x8 yv;
-  if (kind == M3X_NORM_LAYER) {
-    p = v[0];
-#pragma unroll
-    for (int e = 1; e < 8; ++e) p = p + v[e];
-    const float mean = row_tree_sum<TPR>(p, red, bcast) / (float)N;
-    float d[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) d[e] = v[e] - mean;
-    p = d[0] * d[0];
-#pragma unroll
-    for (int e = 1; e < 8; ++e) p = p + d[e] * d[e];
-    const float var = row_tree_sum<TPR>(p, red, bcast) / (float)N;
-    if (!active) return;
-    const float sd = sqrtf(var + eps);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) yv.v[e] = E<DT>::from_f(d[e] / sd * E<DT>::to_f(wv.v[e]) + E<DT>::to_f(bv.v[e]));
-  } else {
-    p = v[0] * v[0];
-#pragma unroll
-    for (int e = 1; e < 8; ++e) p = p + v[e] * v[e];
-    const float ss = row_tree_sum<TPR>(p, red, bcast);
-    if (!active) return;
-    const float inv = 1.0f / sqrtf(ss / (float)N + eps);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) yv.v[e] = E<DT>::from_f(rnd<DT>(v[e] * inv) * E<DT>::to_f(wv.v[e]));
-  }
+  const u16x8 yv = norm_vec<TPR, DT>(v, wv, bv, kind, eps, red, bcast);
+  if (!active) return;
   st16(y + (long)row * N + 8 * t, yv);
 }
 
@@ -375,12 +317,28 @@ __global__ __launch_bounds__(256) void feedback_kernel(const uint16_t* __restric
   for (int e = 0; e < 8; ++e) v[e] = 0.f;
   float p = 0.f;
   if (active) {
-    for (int l = 0; l < n_q; ++l) {
-      int cd = codes[(long)row * s_codes + l];
-      cd = cd < 0 ? 0 : (cd >= n_codes ? n_codes - 1 : cd);
-      u16x8 tv = ld16(table + ((long)cd + (long)n_codes * l) * N + 8 * t);
+    // 32 codebooks at a time: their codes in one round trip, then their rows 16 at a time; the sum still runs
+    // over the codebooks in ascending order
+    for (int l0 = 0; l0 < n_q; l0 += 32) {
+      int cd[32];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = v[e] + E<DT>::to_f(tv.v[e]);
+      for (int i = 0; i < 32; ++i) {
+        const int c = l0 + i < n_q ? codes[(long)row * s_codes + l0 + i] : 0;
+        cd[i] = c < 0 ? 0 : (c >= n_codes ? n_codes - 1 : c);
+      }
+#pragma unroll
+      for (int h = 0; h < 32; h += 16) {
+        u16x8 tv[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (l0 + h + i < n_q) tv[i] = ld16(table + ((long)cd[h + i] + (long)n_codes * (l0 + h + i)) * N + 8 * t);
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (l0 + h + i < n_q) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = v[e] + E<DT>::to_f(tv[i].v[e]);
+          }
+      }
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = rnd<DT>(rnd<DT>(v[e]) / scale);

@@ -17,7 +17,7 @@
 // floor(32*(m - x)) (bin 255 = everything 8 or more below the max, not counted), the first bin b* at which the
 // cumulative count reaches k, then every x with bucket <= b* is a candidate. The bucket is monotone in x, so
 // the candidates contain the top k and all its ties; a bitonic sort of the candidates gives the exact order.
-#include "m3x_common.h"
+#include "m3x_norm.h"
 
 namespace {
 constexpr int ST = 256;      // threads per row
@@ -38,6 +38,7 @@ struct SampleSmem {
   unsigned int hist[256];
   float red[ST / 64];
   int ncand, nkeep, bstar;
+  int code;  // the drawn code, for the waves that build the next level's input
 };
 
 __device__ float block_max(float v, float* red) {
@@ -252,10 +253,29 @@ __device__ int pick(SampleSmem& sm, int n, float u, int skip) {
 // ---------------------------------------------------------------------------------------------------------
 // Depth codebook sampler (serve/fast_depth_kernels.py:48-79 _topk_sample; unfused twin serve/fast_depth.py:125-132):
 // x = float(logit) * inv_temp. Writes the code of row b to out[b * ld_out] (int32, or int64 if out_i64).
-template <int DT>
+//
+// With TPR > 0 the workgroup also builds the next level's input from the code it drew (serve/fast_depth.py:
+// 137-138 and the first norm of the next level, :164): e = table[code] is written to prefix[b]; with y given,
+// xo[b] = e and y[b] = norm(e) (norm_vec over 8*TPR elements, the add+norm kernel's arithmetic with no addend),
+// which replaces a row copy and a norm launch per codebook.
+struct EmbedArgs {
+  const uint16_t* table;
+  long ld_table, table_rows;
+  uint16_t* prefix;
+  long ld_prefix;
+  uint16_t* xo;
+  uint16_t* y;
+  const uint16_t* w;
+  const uint16_t* b;
+  float eps;
+  int kind;
+};
+
+template <int DT, int TPR>
 __global__ __launch_bounds__(ST) void topk_sample_kernel(const uint16_t* __restrict__ logits, long ld_l, int V,
                                                          const float* __restrict__ u, long ld_u, float inv_temp,
-                                                         int top_k, int greedy, void* out, long ld_out, int out_i64) {
+                                                         int top_k, int greedy, void* out, long ld_out, int out_i64,
+                                                         EmbedArgs ea) {
   __shared__ SampleSmem sm;
   const int row = blockIdx.x;
   const float ur = greedy ? 0.f : u[(long)row * ld_u];  // loaded first: its latency overlaps the selection
@@ -266,17 +286,50 @@ __global__ __launch_bounds__(ST) void topk_sample_kernel(const uint16_t* __restr
     x[e] = i < V ? E<DT>::to_f(logits[(long)row * ld_l + i]) * inv_temp : -INFINITY;
   }
   topk_select(x, V, top_k, sm);
-  if (threadIdx.x >= 64) return;  // wave 0 draws
-  int code = cand_index(sm.cand[0]);
-  if (!greedy) {
-    const int c = pick(sm, sm.nkeep, ur, -1);
-    if (c >= 0) code = c;
+  if (TPR == 0 && threadIdx.x >= 64) return;  // wave 0 draws
+  if (threadIdx.x < 64) {
+    int code = cand_index(sm.cand[0]);
+    if (!greedy) {
+      const int c = pick(sm, sm.nkeep, ur, -1);
+      if (c >= 0) code = c;
+    }
+    if (threadIdx.x == 0) {
+      if (out_i64)
+        ((int64_t*)out)[(long)row * ld_out] = code;
+      else
+        ((int32_t*)out)[(long)row * ld_out] = code;
+      sm.code = code;
+    }
   }
-  if (threadIdx.x != 0) return;
-  if (out_i64)
-    ((int64_t*)out)[(long)row * ld_out] = code;
-  else
-    ((int32_t*)out)[(long)row * ld_out] = code;
+  if constexpr (TPR > 0) {
+    constexpr int N = 8 * TPR;
+    __shared__ float red[256];
+    __shared__ float bcast[ST / TPR];
+    __syncthreads();
+    const int t = threadIdx.x % TPR;
+    const bool act = threadIdx.x < TPR;
+    long cr = sm.code;
+    cr = cr < 0 ? 0 : (cr >= ea.table_rows ? ea.table_rows - 1 : cr);
+    float v[8];
+    u16x8 wv = {}, bv = {};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = 0.f;
+    if (act) {
+      const u16x8 ev = ld16(ea.table + cr * ea.ld_table + 8 * t);
+      if (ea.y) {
+        wv = ld16(ea.w + 8 * t);
+        if (ea.kind == M3X_NORM_LAYER) bv = ld16(ea.b + 8 * t);
+      }
+      st16(ea.prefix + (long)row * ea.ld_prefix + 8 * t, ev);
+      if (ea.xo) st16(ea.xo + (long)row * N + 8 * t, ev);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = E<DT>::to_f(ev.v[e]);
+    }
+    if (ea.y) {
+      const u16x8 yv = norm_vec<TPR, DT>(v, wv, bv, ea.kind, ea.eps, red, bcast);
+      if (act) st16(ea.y + (long)row * N + 8 * t, yv);
+    }
+  }
 }
 
 M3X_API int m3x_topk_sample(const void* logits, long ld_l, int V, const float* u, long ld_u, float inv_temp,
@@ -286,14 +339,48 @@ M3X_API int m3x_topk_sample(const void* logits, long ld_l, int V, const float* u
   if (B == 0) return M3X_OK;
   if (!logits || !out || (!greedy && !u)) return M3X_ENULL;
   hipStream_t st = (hipStream_t)stream;
+  const EmbedArgs ea{};
   if (dtype == M3X_BF16)
-    hipLaunchKernelGGL(topk_sample_kernel<M3X_BF16>, dim3(B), dim3(ST), 0, st, (const uint16_t*)logits, ld_l, V, u,
-                       ld_u, inv_temp, top_k, greedy, out, ld_out, out_i64);
+    hipLaunchKernelGGL((topk_sample_kernel<M3X_BF16, 0>), dim3(B), dim3(ST), 0, st, (const uint16_t*)logits, ld_l, V,
+                       u, ld_u, inv_temp, top_k, greedy, out, ld_out, out_i64, ea);
   else if (dtype == M3X_F16)
-    hipLaunchKernelGGL(topk_sample_kernel<M3X_F16>, dim3(B), dim3(ST), 0, st, (const uint16_t*)logits, ld_l, V, u,
-                       ld_u, inv_temp, top_k, greedy, out, ld_out, out_i64);
+    hipLaunchKernelGGL((topk_sample_kernel<M3X_F16, 0>), dim3(B), dim3(ST), 0, st, (const uint16_t*)logits, ld_l, V,
+                       u, ld_u, inv_temp, top_k, greedy, out, ld_out, out_i64, ea);
   else
     return M3X_EUNSUPPORTED;
+  M3X_CHECK_LAUNCH();
+  return M3X_OK;
+}
+
+// m3x_topk_sample, then per row b: prefix[b * ld_prefix + j] = table[code_b * ld_table + j] for j < n, and, when
+// y is given, x_out[b * n + j] = the same row and y[b * n + j] = its LayerNorm (kind 0, w and bias) or RMSNorm
+// (kind 1, w). Codes are clamped to [0, table_rows). n is 1024 or 2048.
+M3X_API int m3x_topk_sample_embed(const void* logits, long ld_l, int V, const float* u, long ld_u, float inv_temp,
+                                  int top_k, int greedy, void* out, long ld_out, int out_i64, int B,
+                                  const void* table, long ld_table, long table_rows, void* prefix, long ld_prefix,
+                                  void* x_out, void* y, const void* w, const void* b, float eps, int kind, int n,
+                                  int dtype, void* stream) {
+  if (B < 0 || V <= 0 || V > SMAXV || top_k <= 0 || table_rows <= 0) return M3X_EINVAL;
+  if (B == 0) return M3X_OK;
+  if (!logits || !out || (!greedy && !u) || !table || !prefix) return M3X_ENULL;
+  if (y && (!w || (kind == M3X_NORM_LAYER && !b))) return M3X_ENULL;
+  if (y && kind != M3X_NORM_LAYER && kind != M3X_NORM_RMS) return M3X_EINVAL;
+  if (((ld_table | ld_prefix) & 7) || ld_table < n) return M3X_EINVAL;
+  if (!m3x_aligned16(table) || !m3x_aligned16(prefix) || (x_out && !m3x_aligned16(x_out)) ||
+      (y && !m3x_aligned16(y)) || (w && !m3x_aligned16(w)) || (b && !m3x_aligned16(b)))
+    return M3X_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+  const EmbedArgs ea{(const uint16_t*)table, ld_table, table_rows, (uint16_t*)prefix, ld_prefix,
+                     y ? (uint16_t*)x_out : nullptr, (uint16_t*)y, (const uint16_t*)w, (const uint16_t*)b, eps, kind};
+#define M3X_TSE(DTT, TT)                                                                                              \
+  hipLaunchKernelGGL((topk_sample_kernel<DTT, TT>), dim3(B), dim3(ST), 0, st, (const uint16_t*)logits, ld_l, V, u, \
+                     ld_u, inv_temp, top_k, greedy, out, ld_out, out_i64, ea)
+  if (dtype == M3X_BF16 && n == 1024) M3X_TSE(M3X_BF16, 128);
+  else if (dtype == M3X_F16 && n == 1024) M3X_TSE(M3X_F16, 128);
+  else if (dtype == M3X_BF16 && n == 2048) M3X_TSE(M3X_BF16, 256);
+  else if (dtype == M3X_F16 && n == 2048) M3X_TSE(M3X_F16, 256);
+  else return M3X_EUNSUPPORTED;
+#undef M3X_TSE
   M3X_CHECK_LAUNCH();
   return M3X_OK;
 }

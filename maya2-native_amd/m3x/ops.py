@@ -243,6 +243,32 @@ def topk_sample(logits, u, inv_temp, top_k, greedy, out, out_i64=False):
                                 _dt(logits), _stream()), "topk_sample")
 
 
+def topk_sample_embed(logits, u, inv_temp, top_k, greedy, out, table, prefix, x_out=None, y=None, w=None, b=None,
+                      eps=0.0, kind=NORM_RMS, out_i64=False):
+    """topk_sample, then prefix[r] = table[code_r]; with y given also x_out[r] = table[code_r] and
+    y[r] = norm(table[code_r]) (the add_norm arithmetic with no addend). prefix: [B, n] view (any row stride);
+    x_out, y: contiguous [B, n]."""
+    _dev(logits, u, out, table, prefix, x_out, y, w, b)
+    _rows2d(logits, "logits")
+    _rows2d(table, "table")
+    B, V = logits.shape
+    n = table.shape[-1]
+    if prefix.shape[-1] != n or prefix.shape[0] != B:
+        raise ValueError("topk_sample_embed: prefix must be [B, n]")
+    if table.shape[0] < V:
+        raise ValueError(f"topk_sample_embed: table has {table.shape[0]} rows for {V} codes")
+    if any(t is not None and t.dtype != logits.dtype for t in (table, prefix, x_out, y, w, b)):
+        raise ValueError("topk_sample_embed: logits, table, prefix, x_out, y, w and b share one dtype")
+    for t, name in ((x_out, "x_out"), (y, "y")):
+        if t is not None and (not t.is_contiguous() or tuple(t.shape) != (B, n)):
+            raise ValueError(f"topk_sample_embed: {name} must be contiguous [B, n]")
+    check(lib().m3x_topk_sample_embed(
+        _p(logits), logits.stride(0), V, _p(u), 0 if u is None else u.stride(0), float(inv_temp), int(top_k),
+        int(greedy), _p(out), out.stride(0), int(out_i64), B, _p(table), table.stride(0), table.shape[0], _p(prefix),
+        prefix.stride(0), _p(x_out), _p(y), _p(w), _p(b), float(eps), int(kind), n, _dt(logits), _stream()),
+        "topk_sample_embed")
+
+
 def cb0_sample(logits, aeos, slots, u, temp_t=None, temp=1.0, topk_t=None, top_k=50, aeos_bias=None, rep_t=None,
                hist_t=None, frames_t=None, min_t=None, hazard_t=None, ctr_t=None, cb0_out=None, cb0_i32=None,
                stop_out=None):

@@ -185,6 +185,7 @@ class FastDepth:
         scale = hd ** -0.5
         inv_temp = 1.0 / self.temp
         previous = None
+        normed = False  # the previous sampler already wrote this level's input row and its norm
         for level in range(1, N_LEVELS):
             group = self.group_of_level[level]
             n = level + 1
@@ -193,8 +194,9 @@ class FastDepth:
             layers = self.trunks[group]
             R = B * T
             first = layers[0].n1
-            ops.add_norm(b.prefix[:, p0:p0 + T], None, None, b.xw[:R], b.yw[:R], first.w, first.b, first.eps, T,
-                         first.kind)
+            if not normed:
+                ops.add_norm(b.prefix[:, p0:p0 + T], None, None, b.xw[:R], b.yw[:R], first.w, first.b, first.eps, T,
+                             first.kind)
             for li, L in enumerate(layers):
                 last_only = li == self.layers - 1 and not incremental
                 tq0 = T - 1 if last_only else 0
@@ -215,9 +217,20 @@ class FastDepth:
             ops.linear(b.yw[:B], self.heads[level - 1], b.logits)
             if trace is not None:
                 trace.append(b.logits.clone())
-            ops.topk_sample(b.logits, b.u[:, level - 1], inv_temp, self.top_k, self.greedy, b.codes[:, level])
+            u = b.u[:, level - 1]
             if n < N_LEVELS:
-                ops.copy_rows(self.embed[level], b.prefix[:, n], src_idx=b.codes[:, level])
+                # the sampler gathers the drawn code's prefix row; when the next level continues this group
+                # incrementally, its input is that one row, so the sampler also writes its norm
+                normed = self.group_of_level[n] == group
+                if normed:
+                    ops.topk_sample_embed(b.logits, u, inv_temp, self.top_k, self.greedy, b.codes[:, level],
+                                          self.embed[level], b.prefix[:, n], x_out=b.xw[:B], y=b.yw[:B], w=first.w,
+                                          b=first.b, eps=first.eps, kind=first.kind)
+                else:
+                    ops.topk_sample_embed(b.logits, u, inv_temp, self.top_k, self.greedy, b.codes[:, level],
+                                          self.embed[level], b.prefix[:, n])
+            else:
+                ops.topk_sample(b.logits, u, inv_temp, self.top_k, self.greedy, b.codes[:, level])
             previous = group
         ops.ctr_add(self.row_ctr, b.slots)
         ops.feedback(self.fb_table, b.codes, b.feedback, self.fb_norm.w, self.fb_norm.eps, self.feedback_scale,

@@ -319,6 +319,43 @@ def test_topk_sample_bitexact(gpu, dtype, V, k):
     assert np.array_equal(out64.cpu().numpy(), refg)
 
 
+@pytest.mark.parametrize("dtype,n,kind", [(torch.bfloat16, 1024, 1), (torch.bfloat16, 1024, 0),
+                                          (torch.float16, 2048, 0)])
+def test_topk_sample_embed(gpu, dtype, n, kind):
+    """The fused sampler draws the same codes as topk_sample, gathers table[code] into the prefix row and, with
+    y given, writes exactly what add_norm writes for that row alone."""
+    from m3x import ops
+    g = _g(n + kind)
+    B, V, k = 37, 2048, 50
+    logits = (torch.randn(B, V, generator=g) * 2).to(dtype).to(gpu)
+    u = torch.rand(B, generator=g).to(gpu)
+    table = torch.randn(V + 3, n, generator=g).to(dtype).to(gpu)
+    w = (1 + 0.1 * torch.randn(n, generator=g)).to(dtype).to(gpu)
+    bias = (0.1 * torch.randn(n, generator=g)).to(dtype).to(gpu) if kind == 0 else None
+    ref = torch.empty(B, dtype=torch.int32, device=gpu)
+    ops.topk_sample(logits, u, 1 / 0.9, k, False, ref)
+    codes = torch.full((B, 4), -7, dtype=torch.int32, device=gpu)
+    prefix = torch.zeros(B, 4, n, dtype=dtype, device=gpu)
+    xo = torch.empty(B, n, dtype=dtype, device=gpu)
+    y = torch.empty(B, n, dtype=dtype, device=gpu)
+    ops.topk_sample_embed(logits, u, 1 / 0.9, k, False, codes[:, 2], table, prefix[:, 2], x_out=xo, y=y, w=w, b=bias,
+                          eps=1e-5, kind=kind)
+    assert torch.equal(codes[:, 2], ref)
+    assert bool((codes[:, [0, 1, 3]] == -7).all())
+    rows = table[ref.long()]
+    assert torch.equal(prefix[:, 2], rows) and torch.equal(xo, rows)
+    assert not prefix[:, [0, 1, 3]].any()
+    xo2, y2 = torch.empty_like(xo), torch.empty_like(y)
+    ops.add_norm(rows, None, None, xo2, y2, w, bias, 1e-5, 1, kind)
+    assert torch.equal(y, y2)
+    # prefix only
+    prefix.zero_()
+    codes.fill_(-7)
+    ops.topk_sample_embed(logits, u, 1 / 0.9, k, False, codes[:, 1], table, prefix[:, 3])
+    assert torch.equal(codes[:, 1], ref) and torch.equal(prefix[:, 3], rows)
+    assert not prefix[:, :3].any()
+
+
 def test_cb0_sample_bitexact(gpu):
     from m3x import ops
     g = _g(21)
