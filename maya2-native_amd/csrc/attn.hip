@@ -301,21 +301,27 @@ M3X_API int m3x_decode_attn(const void* q, long sq_b, long sq_h, const void* k_c
 // qkv rows (b, t) at positions p0 + t, read at qkv + b*sqb + t*sqt, laid out q | k | v with heads inside
 // (view(B,T,3,H,hd)). kd/vd: per-frame scratch [B, H, np, hd]. If write_kv, the T new K/V rows are stored at
 // positions p0..p0+T-1. Queries t in [tq0, T) attend keys 0..p0+t; output row (b, t - tq0) at out + b*sob + tq*sot.
-// One workgroup (64 threads) per (b, head); HD in {64, 128}, np <= 64. Scores: lane j owns key j and reads its
-// K row as 16-byte pieces (4 independent fp32 partial sums); P.V: lane c owns dims 2c, 2c+1 (32-bit loads, rows
-// coalesced across the wave), keys taken in ascending order 16 loads at a time.
-// With write_kv the keys and values of this call's own positions are read from qkv (the bytes being stored), so
-// no load waits on this kernel's own stores and every load is issued before the first wait.
-template <int DT, int HD>
+// One wave per (b, head); HD in {64, 128}, np <= 64. The wave reads K and V rows RPI = 512/HD at a time, each
+// row as HD/8 adjacent 16-byte lane pieces, so a load instruction covers whole rows (lane = row r in the group x
+// piece c). Scores: a lane's 8-element partial dot product, summed over the row's lanes with DPP moves.
+// P.V: each lane accumulates p_j * V[j][8c..8c+7] over its rows, then the row groups are summed with DPP and
+// permlane swaps.
+// Every K and V load of a query is issued before the first wait: NG row groups (a power of two covering the
+// longest query's keys) are loaded unconditionally, rows past the query's last key clamped to it, because a
+// conditional load whose register is merged after the branch makes the compiler wait for it there.
+// With write_kv the keys and values of this call's own positions are read from qkv, and the last query's
+// registers, which hold every one of them, are what is stored to the scratch.
+template <int DT, int HD, int NG>
 __global__ __launch_bounds__(64) void depth_attn_kernel(const uint16_t* __restrict__ qkv, long sqb, long sqt,
                                                         uint16_t* kd, uint16_t* vd, uint16_t* __restrict__ out,
                                                         long sob, long sot, int T, int p0, int tq0, int H, int np,
                                                         float scale, int write_kv) {
-  constexpr int VEC = HD / 8;
-  constexpr int KQ = 16;  // V rows in flight per step
+  constexpr int PPR = HD / 8;   // 16-byte pieces per row
+  constexpr int RPI = 64 / PPR; // rows per load instruction
   const int b = blockIdx.x;
   const int h = blockIdx.y;
   const int lane = threadIdx.x;
+  const int r = lane / PPR, c = lane % PPR;
   uint16_t* kb = kd + ((long)b * H + h) * np * HD;
   uint16_t* vb = vd + ((long)b * H + h) * np * HD;
   const uint16_t* qb = qkv + (long)b * sqb + (long)h * HD;  // q of row t at qb + t*sqt; k at +H*HD; v at +2*H*HD
@@ -323,67 +329,68 @@ __global__ __launch_bounds__(64) void depth_attn_kernel(const uint16_t* __restri
   const int own = write_kv ? p0 : np;
   auto krow = [&](int j) { return j < own ? kb + (long)j * HD : qb + (long)(j - p0) * sqt + (long)H * HD; };
   auto vrow = [&](int j) { return j < own ? vb + (long)j * HD : qb + (long)(j - p0) * sqt + 2L * H * HD; };
-  if (write_kv) {
-    for (int i = lane; i < T * VEC; i += 64) {
-      const int t = i / VEC, c = i % VEC;
-      const uint16_t* src = qb + (long)t * sqt + 8 * c;
-      st16(kb + (long)(p0 + t) * HD + 8 * c, ld16(src + (long)H * HD));
-      st16(vb + (long)(p0 + t) * HD + 8 * c, ld16(src + 2L * H * HD));
-    }
-  }
-  __shared__ float qs[HD];
-  __shared__ float ps[64];
   for (int t = tq0; t < T; ++t) {
     const int nk = p0 + t + 1;
-    // issue the K row (lane j < nk), this query's q, and the first V rows before any wait
-    u16x8 kv[VEC];
-    const uint16_t* kr = krow(min(lane, nk - 1));
+    const int ng = (nk + RPI - 1) / RPI;
+    const u16x8 qv = ld16(qb + (long)t * sqt + 8 * c);
+    u16x8 kv[NG], vv[NG];
 #pragma unroll
-    for (int c = 0; c < VEC; ++c) kv[c] = ld16(kr + 8 * c);
-    const bool pv = 2 * lane < HD;
-    const int dcol = pv ? 2 * lane : 0;
-    uint32_t v2[KQ];
-#pragma unroll
-    for (int q = 0; q < KQ; ++q) v2[q] = *reinterpret_cast<const uint32_t*>(vrow(min(q, nk - 1)) + dcol);
-    const uint16_t* qsrc = qb + (long)t * sqt;
-    for (int d = lane; d < HD; d += 64) qs[d] = E<DT>::to_f(qsrc[d]);
-    __syncthreads();
-    float sc = -INFINITY;
-    if (lane < nk) {
-      float a[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int c = 0; c < VEC; ++c)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) a[e & 3] = fmaf(qs[8 * c + e], E<DT>::to_f(kv[c].v[e]), a[e & 3]);
-      sc = ((a[0] + a[1]) + (a[2] + a[3])) * scale;
+    for (int g = 0; g < NG; ++g) {
+      const int j = min(g * RPI + r, nk - 1);
+      kv[g] = ld16(krow(j) + 8 * c);
+      vv[g] = ld16(vrow(j) + 8 * c);
     }
-    const float m = wave_max_xor(sc, 64);
-    const float pe = lane < nk ? expf(sc - m) : 0.f;
-    const float l = wave_sum_xor(pe, 64);
-    ps[lane] = pe;
-    __syncthreads();
-    float a0 = 0.f, a1 = 0.f;
-    for (int j0 = 0; j0 < nk; j0 += KQ) {
-      if (j0 > 0) {
+    float qf[8];
 #pragma unroll
-        for (int q = 0; q < KQ; ++q)
-          v2[q] = *reinterpret_cast<const uint32_t*>(vrow(min(j0 + q, nk - 1)) + dcol);
+    for (int e = 0; e < 8; ++e) qf[e] = E<DT>::to_f(qv.v[e]);
+    float s[NG];
+    float m = -INFINITY;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      s[g] = -INFINITY;
+      if (g < ng) {
+        float a = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a = fmaf(qf[e], E<DT>::to_f(kv[g].v[e]), a);
+        a = group_sum<PPR>(a);
+        s[g] = g * RPI + r < nk ? a * scale : -INFINITY;
+        m = fmaxf(m, s[g]);
       }
+    }
+    m = across_max<PPR>(m);
+    float l = 0.f;
+    float acc[8];
 #pragma unroll
-      for (int q = 0; q < KQ; ++q) {
-        if (j0 + q < nk) {
-          const float p = ps[j0 + q];
-          a0 = fmaf(p, E<DT>::to_f((uint16_t)(v2[q] & 0xffffu)), a0);
-          a1 = fmaf(p, E<DT>::to_f((uint16_t)(v2[q] >> 16)), a1);
+    for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      if (g < ng) {
+        const float p = g * RPI + r < nk ? expf(s[g] - m) : 0.f;
+        l = l + p;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = fmaf(p, E<DT>::to_f(vv[g].v[e]), acc[e]);
+      }
+    }
+    l = across_sum<PPR>(l);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = across_sum<PPR>(acc[e]);
+    if (r == 0) {
+      u16x8 ov;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ov.v[e] = E<DT>::from_f(acc[e] / l);
+      st16(out + (long)b * sob + (long)(t - tq0) * sot + (long)h * HD + 8 * c, ov);
+    }
+    // the last query has loaded every new row (keys p0..p0+T-1, from qkv): store them to the scratch
+    if (write_kv && t == T - 1) {
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        const int j = g * RPI + r;
+        if (j >= p0 && j < nk) {
+          st16(kb + (long)j * HD + 8 * c, kv[g]);
+          st16(vb + (long)j * HD + 8 * c, vv[g]);
         }
       }
     }
-    if (pv) {
-      uint16_t* o = out + (long)b * sob + (long)(t - tq0) * sot + (long)h * HD + 2 * lane;
-      const uint32_t packed = (uint32_t)E<DT>::from_f(a0 / l) | ((uint32_t)E<DT>::from_f(a1 / l) << 16);
-      *reinterpret_cast<uint32_t*>(o) = packed;
-    }
-    __syncthreads();
   }
 }
 
@@ -399,15 +406,25 @@ M3X_API int m3x_depth_attn(const void* qkv, long sqb, long sqt, void* kd, void* 
       !m3x_aligned16(out))
     return M3X_EINVAL;
   hipStream_t st = (hipStream_t)stream;
-#define M3X_DA(DTT, HDD)                                                                                        \
-  hipLaunchKernelGGL((depth_attn_kernel<DTT, HDD>), dim3(B, heads), dim3(64), 0, st, (const uint16_t*)qkv, sqb, \
-                     sqt, (uint16_t*)kd, (uint16_t*)vd, (uint16_t*)out, sob, sot, T, p0, tq0, heads, np, scale,  \
-                     write_kv)
-  if (dtype == M3X_BF16 && head_dim == 128) M3X_DA(M3X_BF16, 128);
-  else if (dtype == M3X_BF16) M3X_DA(M3X_BF16, 64);
-  else if (dtype == M3X_F16 && head_dim == 128) M3X_DA(M3X_F16, 128);
-  else if (dtype == M3X_F16) M3X_DA(M3X_F16, 64);
+#define M3X_DA(DTT, HDD, NGG)                                                                                     \
+  hipLaunchKernelGGL((depth_attn_kernel<DTT, HDD, NGG>), dim3(B, heads), dim3(64), 0, st, (const uint16_t*)qkv,   \
+                     sqb, sqt, (uint16_t*)kd, (uint16_t*)vd, (uint16_t*)out, sob, sot, T, p0, tq0, heads, np,     \
+                     scale, write_kv)
+#define M3X_DA_NG(DTT, HDD)                                                        \
+  do {                                                                             \
+    const int groups = m3x_ceil_div(p0 + T, 512 / HDD);                            \
+    if (groups <= 1) M3X_DA(DTT, HDD, 1);                                          \
+    else if (groups <= 2) M3X_DA(DTT, HDD, 2);                                     \
+    else if (groups <= 4) M3X_DA(DTT, HDD, 4);                                     \
+    else if (groups <= 8) M3X_DA(DTT, HDD, 8);                                     \
+    else M3X_DA(DTT, HDD, 16);                                                     \
+  } while (0)
+  if (dtype == M3X_BF16 && head_dim == 128) M3X_DA_NG(M3X_BF16, 128);
+  else if (dtype == M3X_BF16) M3X_DA_NG(M3X_BF16, 64);
+  else if (dtype == M3X_F16 && head_dim == 128) M3X_DA_NG(M3X_F16, 128);
+  else if (dtype == M3X_F16) M3X_DA_NG(M3X_F16, 64);
   else return M3X_EUNSUPPORTED;
+#undef M3X_DA_NG
 #undef M3X_DA
   M3X_CHECK_LAUNCH();
   return M3X_OK;

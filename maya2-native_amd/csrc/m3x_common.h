@@ -98,6 +98,49 @@ __device__ __forceinline__ float wave_max_xor(float v, int width) {
   return v;
 }
 
+// Lane-group reductions without the LDS crossbar. Within a row of 16 lanes, DPP moves (quad_perm [1,0,3,2] and
+// [2,3,0,1], then the half-row and row mirrors; once lanes of a quad hold equal values, a mirror pairs each lane
+// with a lane of the partner quad or half). Across rows, gfx950's v_permlane16_swap / v_permlane32_swap applied
+// to (v, v) return the two halves of each swapped pair, so their sum is v[i] + v[i ^ 16] (resp. ^ 32) in every
+// lane, in the same order in both lanes of the pair.
+template <int CTRL> __device__ __forceinline__ float dppf(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// every lane gets the sum (max) over its aligned group of W lanes, W in {8, 16}
+template <int W> __device__ __forceinline__ float group_sum(float v) {
+  static_assert(W == 8 || W == 16, "group width");
+  v = v + dppf<0xB1>(v);
+  v = v + dppf<0x4E>(v);
+  v = v + dppf<0x141>(v);
+  if constexpr (W == 16) v = v + dppf<0x140>(v);
+  return v;
+}
+__device__ __forceinline__ float xor16_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// sum (max) over the lanes that share lane % W, W in {8, 16}: rows of W lanes combined
+template <int W> __device__ __forceinline__ float across_sum(float v) {
+  if constexpr (W == 8) v = v + dppf<0x128>(v);  // row_ror:8 pairs lane i with i ^ 8 within its row
+  return xor32_sum(xor16_sum(v));
+}
+template <int W> __device__ __forceinline__ float across_max(float v) {
+  if constexpr (W == 8) v = fmaxf(v, dppf<0x128>(v));
+  return xor32_max(xor16_max(v));
+}
+
 // ------------------------------------------------------------------ MFMA (gfx950)
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));

@@ -270,18 +270,21 @@ def test_add_norm_strided(gpu, kind):
     assert ok, info
 
 
-@pytest.mark.parametrize("T,p0,tq0", [(2, 0, 0), (1, 5, 0), (9, 0, 8), (17, 0, 0)])
-def test_depth_attn(gpu, T, p0, tq0):
+@pytest.mark.parametrize("T,p0,tq0,hd,NP,dtype", [(2, 0, 0, 128, 32, torch.bfloat16), (1, 5, 0, 128, 32, torch.bfloat16),
+                                                  (9, 0, 8, 128, 32, torch.bfloat16), (17, 0, 0, 128, 32, torch.bfloat16),
+                                                  (1, 31, 0, 128, 32, torch.bfloat16), (1, 63, 0, 128, 64, torch.float16),
+                                                  (24, 40, 0, 64, 64, torch.float16), (3, 6, 1, 64, 16, torch.bfloat16)])
+def test_depth_attn(gpu, T, p0, tq0, hd, NP, dtype):
     from m3x import ops
-    g = _g(T * 100 + p0)
-    B, H, hd, NP = 3, 8, 128, 32
+    g = _g(T * 100 + p0 + hd)
+    B, H = 3, 8
     D = H * hd
-    kd = torch.randn(B, H, NP, hd, generator=g).to(torch.bfloat16)
-    vd = torch.randn(B, H, NP, hd, generator=g).to(torch.bfloat16)
-    qkv = torch.randn(B * T, 3 * D, generator=g).to(torch.bfloat16)
+    kd = torch.randn(B, H, NP, hd, generator=g).to(dtype)
+    vd = torch.randn(B, H, NP, hd, generator=g).to(dtype)
+    qkv = torch.randn(B * T, 3 * D, generator=g).to(dtype)
     kdg, vdg = kd.to(gpu), vd.to(gpu)
     Tq = T - tq0
-    out = torch.empty(B * Tq, D, dtype=torch.bfloat16, device=gpu)
+    out = torch.empty(B * Tq, D, dtype=dtype, device=gpu)
     ops.depth_attn(qkv.to(gpu), kdg, vdg, out, B, T, p0, tq0, H, hd, hd ** -0.5, True)
     q3 = qkv.view(B, T, 3, H, hd)
     kd[:, :, p0:p0 + T] = q3[:, :, 1].transpose(1, 2)
