@@ -48,11 +48,10 @@ __global__ __launch_bounds__(256) void pack_weight_kernel(const uint16_t* __rest
 // The KW K-slice partials of one weight tile meet in LDS (`red`, free when this runs) and are added in slice
 // order by slice 0, which then applies the epilogue. Lane (li, lg) holds weight rows n0 + 4*lg + r of
 // activation row m0 + 16*t + li.
-template <int DT, int MT, int NW, int EPI>
+template <int DT, int MT, int NW, int KW, int EPI>
 __device__ __forceinline__ void linear_finish(f32x4_t (&acc)[EPI == EPI_SWIGLU ? 2 : 1][MT], f32x4_t* red, int wn,
                                               int wk, int lane, int n0, int m0, uint16_t* __restrict__ Y, long ldy,
                                               int M, int N) {
-  constexpr int KW = 4 / NW;
   constexpr int NA = EPI == EPI_SWIGLU ? 2 : 1;
   const int li = lane & 15;
   const int lg = lane >> 4;
@@ -242,29 +241,37 @@ __global__ __launch_bounds__(256) void linear_kernel(const uint16_t* __restrict_
     __syncthreads();
   }
 
-  linear_finish<DT, MT, NW, EPI>(acc, reinterpret_cast<f32x4_t*>(&xs[0][0]), wn, wk, lane, n0, m0, Y, ldy, M, N);
+  linear_finish<DT, MT, NW, KW, EPI>(acc, reinterpret_cast<f32x4_t*>(&xs[0][0]), wn, wk, lane, n0, m0, Y, ldy, M,
+                                     N);
 }
 
-// One-shot variant for short K slices (S = K / KW / 32 steps of 32, S in {8, 16}): every weight fragment of the
-// wave's slice and the workgroup's whole activation block are loaded at once, so the kernel pays one memory
-// latency instead of one per chunk. The block sits in LDS without padding; 16-byte granule g of row r is stored
-// at g ^ (r % 16), so the 16 rows a fragment read touches fall in 16 different bank groups.
-template <int DT, int MT, int NW, int EPI, int S>
-__global__ __launch_bounds__(256) void linear_oneshot_kernel(const uint16_t* __restrict__ X, long ldx,
-                                                             const uint16_t* __restrict__ Wp,
-                                                             const uint16_t* __restrict__ W2p,
-                                                             uint16_t* __restrict__ Y, long ldy, int M, int N, int K,
-                                                             int mblk, int nblk) {
-  constexpr int KW = 4 / NW;
+// One-shot variant: every weight fragment of the wave's K slice (S steps of 32) and the workgroup's whole
+// activation block are loaded at once, so the kernel pays one memory latency instead of one per chunk. A
+// workgroup is NWAVES waves = NW weight tiles x KW = NWAVES / NW slices of K. With 8 or 16 waves the block may
+// take up to 128 KB of gfx950's 160 KB LDS; one such workgroup per CU then streams its whole weight slab at
+// once. The block sits in LDS unpadded when a slice row is a multiple of 16 granules of 16 bytes, with granule
+// g of row r stored at g ^ (r % 16), so the 16 rows a fragment read touches fall in 16 different bank groups;
+// otherwise rows are padded by 16 bytes.
+template <int DT, int MT, int NW, int NWAVES, int EPI, int S>
+__global__ __launch_bounds__(64 * NWAVES) void linear_oneshot_kernel(const uint16_t* __restrict__ X, long ldx,
+                                                                     const uint16_t* __restrict__ Wp,
+                                                                     const uint16_t* __restrict__ W2p,
+                                                                     uint16_t* __restrict__ Y, long ldy, int M, int N,
+                                                                     int K, int mblk, int nblk) {
+  constexpr int NT = 64 * NWAVES;
+  constexpr int KW = NWAVES / NW;
   constexpr int ROWS = 16 * MT;
   constexpr int KS = 32 * S;          // k per slice
   constexpr int GR = 4 * S;           // 16-byte granules per row of a slice
+  constexpr bool SWZ = GR % 16 == 0;
+  constexpr int LDR = SWZ ? KS : KS + 8;
   constexpr int NVEC = KW * ROWS * GR;
-  static_assert(NVEC % 256 == 0 && GR >= 16, "one-shot geometry");
-  constexpr int VPT = NVEC / 256;
+  constexpr int VPT = (NVEC + NT - 1) / NT;
   constexpr bool DUAL = EPI == EPI_SWIGLU;
   constexpr int NA = DUAL ? 2 : 1;
-  __shared__ __align__(16) uint16_t xs[KW * ROWS * KS];
+  static_assert(KW * NW == NWAVES, "one-shot geometry");
+  static_assert((KW - 1) * NW * NA * MT * 1024 <= KW * ROWS * LDR * 2, "slice partials must fit the block");
+  __shared__ __align__(16) uint16_t xs[KW * ROWS * LDR];
 
   const int xcd = blockIdx.x & 7;
   const int slot = blockIdx.x >> 3;
@@ -296,10 +303,11 @@ __global__ __launch_bounds__(256) void linear_oneshot_kernel(const uint16_t* __r
       if constexpr (DUAL) Wr[s][NA - 1] = ld16(w1 + (long)(s0 + s) * 512);
     }
   }
+  // activation vector v = tid + NT j -> slice q, row r, granule g
   u16x8 Xr[VPT];
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int v = tid + 256 * j;
+    const int v = tid + NT * j;
     const int q = v / (ROWS * GR);
     const int rem = v - q * (ROWS * GR);
     const int r = rem / GR;
@@ -307,16 +315,16 @@ __global__ __launch_bounds__(256) void linear_oneshot_kernel(const uint16_t* __r
     const int m = m0 + r;
 #pragma unroll
     for (int e = 0; e < 8; ++e) Xr[j].v[e] = 0;
-    if (m < M) Xr[j] = ld16(X + (long)m * ldx + q * KS + g * 8);
+    if ((NVEC % NT == 0 || v < NVEC) && m < M) Xr[j] = ld16(X + (long)m * ldx + q * KS + g * 8);
   }
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int v = tid + 256 * j;
+    const int v = tid + NT * j;
     const int q = v / (ROWS * GR);
     const int rem = v - q * (ROWS * GR);
     const int r = rem / GR;
     const int g = rem - r * GR;
-    st16(&xs[(q * ROWS + r) * KS + ((g ^ (r & 15)) << 3)], Xr[j]);
+    if (NVEC % NT == 0 || v < NVEC) st16(&xs[(q * ROWS + r) * LDR + ((SWZ ? g ^ (r & 15) : g) << 3)], Xr[j]);
   }
   __syncthreads();
 
@@ -325,27 +333,30 @@ __global__ __launch_bounds__(256) void linear_oneshot_kernel(const uint16_t* __r
   for (int a = 0; a < NA; ++a)
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[a][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const uint16_t* xb = &xs[(wk * ROWS + li) * KS];
+  const uint16_t* xb = &xs[(wk * ROWS + li) * LDR];
 #pragma unroll
   for (int s = 0; s < S; ++s) {
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
-      const u16x8 b = *reinterpret_cast<const u16x8*>(xb + t * 16 * KS + (((4 * s + lg) ^ li) << 3));
+      const int gi = SWZ ? (4 * s + lg) ^ li : 4 * s + lg;
+      const u16x8 b = *reinterpret_cast<const u16x8*>(xb + t * 16 * LDR + (gi << 3));
 #pragma unroll
       for (int a = 0; a < NA; ++a) acc[a][t] = mfma16x16x32<DT>(Wr[s][a], b, acc[a][t]);
     }
   }
   __syncthreads();  // every wave is done with the block before it holds the slice partials
-  linear_finish<DT, MT, NW, EPI>(acc, reinterpret_cast<f32x4_t*>(xs), wn, wk, lane, n0, m0, Y, ldy, M, N);
+  linear_finish<DT, MT, NW, KW, EPI>(acc, reinterpret_cast<f32x4_t*>(xs), wn, wk, lane, n0, m0, Y, ldy, M, N);
 }
 
-// Launch geometry: MT activation tiles of 16 rows per workgroup; NW weight tiles per workgroup (4 / NW K slices).
+// Launch geometry: MT activation tiles of 16 rows per workgroup; NW weight tiles per workgroup; NWAVES waves
+// (NWAVES / NW K slices).
 struct LinearPlan {
   int mt, nw, mblk, nblk;
-  int oneshot;  // steps per K slice for the one-shot kernel (8 or 16), 0 for the chunked kernel
+  int nwaves;   // 4 for the chunked kernel and the small one-shot; 8 or 16 for the wide one-shot
+  int oneshot;  // steps per K slice for the one-shot kernel, 0 for the chunked kernel
 };
 
-// One-shot applies when each of the 4/nw K slices is exactly 8 or 16 steps of 32 and the activation block
+// Small one-shot (4 waves): each of the 4/nw K slices is exactly 8 or 16 steps of 32 and the activation block
 // (16*mt rows x K) fits in 64 KB of LDS.
 static int oneshot_steps(int mt, int nw, int K) {
   const int kw = 4 / nw;
@@ -355,13 +366,52 @@ static int oneshot_steps(int mt, int nw, int K) {
   return s;
 }
 
-// Tile choice measured on MI355X (graph-timed sweep over the decode shapes, M = 1..2264): the best plan is the
-// largest tile that still gives at least ~400 workgroups; MT = 2 pays off only above ~112 rows.
-static LinearPlan linear_plan(int M, int N, int K) {
+// Wide one-shot plans (measured on MI355X, graph-timed, 64..256 rows; 20-30 % under the chunked kernel on the
+// decode shapes). K = 1024: the first (MT, NW) of (2,2), (2,4), (3,4), (2,8) whose grid fits one workgroup per
+// CU (<= 256); 8 waves. K = 2048, 2816, 3072: 16-row blocks, 16 waves, NW = 4 above 160 rows, else 2.
+// Returns false when no instantiated plan covers (M, N, K).
+static bool wide_plan(int M, int N, int K, bool dual, LinearPlan& p) {
+  if (M < 64 || M > 256) return false;
+  const int ntiles = m3x_ceil_div(N, 16);
+  if (K == 1024) {
+    const int cand[4][2] = {{2, 2}, {2, 4}, {3, 4}, {2, 8}};
+    for (const auto& c : cand) {
+      if (dual && c[1] == 8) continue;  // the gate/up pair of 8 tiles does not fit the register file
+      const long wgs = (long)m3x_ceil_div(M, 16 * c[0]) * m3x_ceil_div(ntiles, c[1]);
+      if (wgs <= 256) {
+        p.mt = c[0];
+        p.nw = c[1];
+        p.nwaves = 8;
+        p.oneshot = K / 32 / (8 / c[1]);
+        return true;
+      }
+    }
+    return false;
+  }
+  if ((K == 2048 || K == 2816 || K == 3072) && !dual) {
+    p.mt = 1;
+    p.nw = M > 160 ? 4 : 2;
+    p.nwaves = 16;
+    p.oneshot = K / 32 / (16 / p.nw);
+    return true;
+  }
+  return false;
+}
+
+// Chunked / small one-shot tile choice, measured on MI355X (graph-timed sweep over the decode shapes,
+// M = 1..2264): the best plan is the largest tile that still gives at least ~400 workgroups; MT = 2 pays off
+// only above ~112 rows.
+static LinearPlan linear_plan(int M, int N, int K, bool dual) {
   const int ntiles = m3x_ceil_div(N, 16);
   const int ksteps = K / 32;
   auto blocks = [&](int mt, int nw) { return (long)m3x_ceil_div(M, 16 * mt) * m3x_ceil_div(ntiles, nw); };
   LinearPlan p;
+  p.nwaves = 4;
+  if (wide_plan(M, N, K, dual, p)) {
+    p.mblk = m3x_ceil_div(M, 16 * p.mt);
+    p.nblk = m3x_ceil_div(ntiles, p.nw);
+    return p;
+  }
   if (M > 512) {
     p.mt = 4;
     p.nw = 4;
@@ -393,23 +443,35 @@ template <int DT, int EPI>
 static bool launch_linear(const LinearPlan& p, hipStream_t st, const uint16_t* X, long ldx, const uint16_t* W,
                           const uint16_t* W2, uint16_t* Y, long ldy, int M, int N, int K) {
   const dim3 grid(m3x_ceil_div(p.nblk, 8) * 8 * p.mblk);
-#define M3X_ONE(MTT, NWW, SS)                                                                                  \
-  hipLaunchKernelGGL((linear_oneshot_kernel<DT, MTT, NWW, EPI, SS>), grid, dim3(256), 0, st, X, ldx, W, W2, Y, \
-                     ldy, M, N, K, p.mblk, p.nblk)
+#define M3X_ONE(MTT, NWW, NWV, SS)                                                                         \
+  hipLaunchKernelGGL((linear_oneshot_kernel<DT, MTT, NWW, NWV, EPI, SS>), grid, dim3(64 * NWV), 0, st, X, \
+                     ldx, W, W2, Y, ldy, M, N, K, p.mblk, p.nblk)
   if (p.oneshot) {
-    const int key = p.mt * 100 + p.nw * 10 + (p.oneshot == 16 ? 1 : 0);
+    const long key = ((p.mt * 10L + p.nw) * 100 + p.nwaves) * 100 + p.oneshot;
     switch (key) {
-      case 121: M3X_ONE(1, 2, 16); return true;
-      case 120: M3X_ONE(1, 2, 8); return true;
-      case 111: M3X_ONE(1, 1, 16); return true;
-      case 110: M3X_ONE(1, 1, 8); return true;
-      case 141: M3X_ONE(1, 4, 16); return true;
-      case 140: M3X_ONE(1, 4, 8); return true;
-      case 221: M3X_ONE(2, 2, 16); return true;
-      case 220: M3X_ONE(2, 2, 8); return true;
-      case 241: M3X_ONE(2, 4, 16); return true;
-      case 240: M3X_ONE(2, 4, 8); return true;
-      case 210: M3X_ONE(2, 1, 8); return true;
+      case 120416: M3X_ONE(1, 2, 4, 16); return true;
+      case 120408: M3X_ONE(1, 2, 4, 8); return true;
+      case 110416: M3X_ONE(1, 1, 4, 16); return true;
+      case 110408: M3X_ONE(1, 1, 4, 8); return true;
+      case 140416: M3X_ONE(1, 4, 4, 16); return true;
+      case 140408: M3X_ONE(1, 4, 4, 8); return true;
+      case 220416: M3X_ONE(2, 2, 4, 16); return true;
+      case 220408: M3X_ONE(2, 2, 4, 8); return true;
+      case 240416: M3X_ONE(2, 4, 4, 16); return true;
+      case 240408: M3X_ONE(2, 4, 4, 8); return true;
+      case 210408: M3X_ONE(2, 1, 4, 8); return true;
+      // wide, K = 1024
+      case 220808: M3X_ONE(2, 2, 8, 8); return true;
+      case 240816: M3X_ONE(2, 4, 8, 16); return true;
+      case 340816: M3X_ONE(3, 4, 8, 16); return true;
+      case 280832: if constexpr (EPI != EPI_SWIGLU) { M3X_ONE(2, 8, 8, 32); return true; } return false;
+      // wide, K = 2048 / 2816 / 3072
+      case 141616: if constexpr (EPI != EPI_SWIGLU) { M3X_ONE(1, 4, 16, 16); return true; } return false;
+      case 121608: if constexpr (EPI != EPI_SWIGLU) { M3X_ONE(1, 2, 16, 8); return true; } return false;
+      case 141622: if constexpr (EPI != EPI_SWIGLU) { M3X_ONE(1, 4, 16, 22); return true; } return false;
+      case 121611: if constexpr (EPI != EPI_SWIGLU) { M3X_ONE(1, 2, 16, 11); return true; } return false;
+      case 141624: if constexpr (EPI != EPI_SWIGLU) { M3X_ONE(1, 4, 16, 24); return true; } return false;
+      case 121612: if constexpr (EPI != EPI_SWIGLU) { M3X_ONE(1, 2, 16, 12); return true; } return false;
       default: return false;
     }
   }
@@ -438,7 +500,7 @@ static int linear_common(const void* x, long ldx, const void* w, const void* w2,
   if (K % 32 || (ldx & 7) || ldx < K || ldy < N) return M3X_EINVAL;
   if (!m3x_aligned16(x) || !m3x_aligned16(w) || (w2 && !m3x_aligned16(w2)) || (((uintptr_t)y) & 1))
     return M3X_EINVAL;
-  const LinearPlan p = linear_plan(M, N, K);
+  const LinearPlan p = linear_plan(M, N, K, epi == EPI_SWIGLU);
   if ((long)m3x_ceil_div(p.nblk, 8) * 8 * p.mblk > 0x7fffffffL) return M3X_EINVAL;
   hipStream_t st = (hipStream_t)stream;
   const uint16_t *X = (const uint16_t*)x, *Wt = (const uint16_t*)w, *W2 = (const uint16_t*)w2;

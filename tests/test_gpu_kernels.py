@@ -18,7 +18,11 @@ def _g(seed):
 # ---------------------------------------------------------------- GEMM
 @pytest.mark.parametrize("M,N,K", [(1, 1024, 1024), (5, 4096, 1024), (16, 2048, 1024), (33, 1024, 3072),
                                    (100, 2049, 1024), (224, 6144, 1024), (7, 1024, 2816), (448, 2816, 1024),
-                                   (2264, 4096, 1024)])
+                                   (2264, 4096, 1024),
+                                   # one-workgroup-per-CU plans: 8 waves at K = 1024, 16 waves at longer K
+                                   (224, 1024, 1024), (224, 2048, 1024), (224, 3072, 1024), (224, 4096, 1024),
+                                   (250, 3072, 1024), (64, 2049, 1024), (224, 1024, 2048), (224, 1024, 2816),
+                                   (200, 1024, 3072), (100, 1024, 2816), (70, 1024, 2048)])
 def test_linear_bf16(gpu, M, N, K):
     from m3x import ops
     g = _g(M * 7 + N)
@@ -42,7 +46,8 @@ def test_linear_fp16(gpu, M, N, K):
 
 
 @pytest.mark.parametrize("M,I,K,dtype", [(1, 3072, 1024, torch.bfloat16), (224, 2816, 1024, torch.bfloat16),
-                                         (37, 3072, 1024, torch.float16)])
+                                         (37, 3072, 1024, torch.float16), (224, 3072, 1024, torch.bfloat16),
+                                         (64, 3072, 1024, torch.float16), (130, 2816, 1024, torch.bfloat16)])
 def test_linear_swiglu_epilogue(gpu, M, I, K, dtype):
     """Fused gate|up GEMM + silu*mul against the separate GEMM + activation kernel (the two launches may slice K
     differently, so the fp32 sums can round apart by an ulp) and against an fp32 reference."""
@@ -64,14 +69,15 @@ def test_linear_swiglu_epilogue(gpu, M, I, K, dtype):
     assert ok, info
 
 
-def test_linear_gelu_epilogue(gpu):
+@pytest.mark.parametrize("M", [9, 150])
+def test_linear_gelu_epilogue(gpu, M):
     from m3x import ops
-    g = _g(77)
-    x = torch.randn(9, 1024, generator=g).to(torch.float16).to(gpu)
+    g = _g(77 + M)
+    x = torch.randn(M, 1024, generator=g).to(torch.float16).to(gpu)
     w = (torch.randn(3072, 1024, generator=g) * 0.02).to(torch.float16).to(gpu)
     pw = ops.pack_weight(w)
     fused = ops.linear_act(x, pw, None, ops.ACT_GELU)
-    sep = torch.empty(9, 3072, dtype=torch.float16, device=gpu)
+    sep = torch.empty(M, 3072, dtype=torch.float16, device=gpu)
     ops.act(ops.linear(x, pw), sep, ops.ACT_GELU)
     ok, info = close(fused, sep.float(), atol=1e-3, rel_ulps=2)
     assert ok, info
