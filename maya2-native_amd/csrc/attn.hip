@@ -28,6 +28,15 @@ constexpr int AD = 128;       // head dim of the decode kernel
 constexpr int PART_STRIDE = 264;  // floats per (row, kv head, split) partial: m[2] l[2] pad[4] o[2][128]
 }
 
+// K and V are read with the non-temporal hint: each cache byte is read once per step.
+#ifndef M3X_ATTN_NT
+#define M3X_ATTN_NT 1
+#endif
+__device__ __forceinline__ u16x8 kv_load(const uint16_t* p) {
+  if constexpr (M3X_ATTN_NT) return ld16_nt(p);
+  else return ld16(p);
+}
+
 // Three workgroups per CU (<= 168 VGPRs, no spill): measured 2 % faster than the unconstrained 190 VGPRs.
 #ifndef M3X_ATTN_MINB
 #define M3X_ATTN_MINB 3
@@ -88,18 +97,18 @@ __global__ __launch_bounds__(256, M3X_ATTN_MINB) void decode_attn_kernel(
     if constexpr (KL) {
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        kld[e] = ld16(kbase + (long)(k0 + 16 * (e >> 2) + 4 * lg + (e & 3)) * sk_t + 8 * li);
+        kld[e] = kv_load(kbase + (long)(k0 + 16 * (e >> 2) + 4 * lg + (e & 3)) * sk_t + 8 * li);
     } else {
 #pragma unroll
       for (int g2 = 0; g2 < 2; ++g2) {
         const uint16_t* kr = kbase + (long)(k0 + 16 * g2 + li) * sk_t + 8 * lg;
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) kop[g2][kk] = ld16(kr + 32 * kk);
+        for (int kk = 0; kk < 4; ++kk) kop[g2][kk] = kv_load(kr + 32 * kk);
       }
     }
     u16x8 vld[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) vld[e] = ld16(vbase + (long)(k0 + 16 * (e >> 2) + 4 * lg + (e & 3)) * sk_t + 8 * li);
+    for (int e = 0; e < 8; ++e) vld[e] = kv_load(vbase + (long)(k0 + 16 * (e >> 2) + 4 * lg + (e & 3)) * sk_t + 8 * li);
     if constexpr (KL) {
       uint16_t* kt = ktile[wave];
 #pragma unroll

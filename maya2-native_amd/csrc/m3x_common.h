@@ -58,6 +58,13 @@ __device__ __forceinline__ u16x8 ld16(const uint16_t* p) {
   uint4 r = *reinterpret_cast<const uint4*>(p);
   return __builtin_bit_cast(u16x8, r);
 }
+// Streaming read (non-temporal hint): for data read once per pass, such as the KV cache. A read-only stream
+// with the hint runs at ~7.0 TB/s on MI355X against ~6.3 TB/s with plain loads.
+__device__ __forceinline__ u16x8 ld16_nt(const uint16_t* p) {
+  typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+  const u32x4_t r = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return __builtin_bit_cast(u16x8, r);
+}
 __device__ __forceinline__ void st16(uint16_t* p, const u16x8& x) {
   *reinterpret_cast<uint4*>(p) = __builtin_bit_cast(uint4, x);
 }
