@@ -142,8 +142,7 @@ __global__ __launch_bounds__(256, M3X_ATTN_MINB) void decode_attn_kernel(
     float tmax = sv[0];
 #pragma unroll
     for (int e = 1; e < 8; ++e) tmax = fmaxf(tmax, sv[e]);
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    tmax = xor32_max(xor16_max(tmax));
     const float m_new = fmaxf(m_run, tmax);
     const float alpha = exp2f(m_run - m_new);
     float p[8], psum = 0.f;
@@ -152,15 +151,14 @@ __global__ __launch_bounds__(256, M3X_ATTN_MINB) void decode_attn_kernel(
       p[e] = (li < G) ? exp2f(sv[e] - m_new) : 0.f;
       psum += p[e];
     }
-    psum += __shfl_xor(psum, 16, 64);
-    psum += __shfl_xor(psum, 32, 64);
+    psum = xor32_sum(xor16_sum(psum));
     l_run = l_run * alpha + psum;
     m_run = m_new;
 
     // ---- rescale the accumulator rows (heads 0..G-1 live in lanes 0..15, register = head)
     float al[G];
 #pragma unroll
-    for (int h = 0; h < G; ++h) al[h] = __shfl(alpha, h, 64);
+    for (int h = 0; h < G; ++h) al[h] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), h));
 #pragma unroll
     for (int T = 0; T < 8; ++T)
 #pragma unroll

@@ -113,6 +113,29 @@ __device__ __forceinline__ float wave_max_xor(float v, int width) {
 template <int CTRL> __device__ __forceinline__ float dppf(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
+// DPP controls: row_shl:n (lane i reads lane i + n of its row of 16), row_ror:n (lane i reads lane (i + n) % 16),
+// row_newbcast:n (every lane of a row reads lane n of the row)
+constexpr int DPP_ROW_SHL(int n) { return 0x100 + n; }
+constexpr int DPP_ROW_ROR(int n) { return 0x120 + n; }
+constexpr int DPP_ROW_NEWBCAST(int n) { return 0x150 + n; }
+// Fold-in-half within aligned groups of W lanes (W <= 64, a power of two): after it, the first lane of each group
+// holds sum_g p[g] combined as p[g] + p[g + s] for s = W/2, ..., 1 (permlane swaps for s = 32, 16; DPP row
+// shifts below). The other lanes hold partial or undefined values.
+template <int W> __device__ __forceinline__ float fold_half_sum(float p) {
+  if constexpr (W == 64) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(p), __float_as_uint(p), false, false);
+    p = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  if constexpr (W >= 32) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(p), __float_as_uint(p), false, false);
+    p = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  if constexpr (W >= 16) p = p + dppf<DPP_ROW_SHL(8)>(p);
+  if constexpr (W >= 8) p = p + dppf<DPP_ROW_SHL(4)>(p);
+  if constexpr (W >= 4) p = p + dppf<DPP_ROW_SHL(2)>(p);
+  if constexpr (W >= 2) p = p + dppf<DPP_ROW_SHL(1)>(p);
+  return p;
+}
 // every lane gets the sum (max) over its aligned group of W lanes, W in {8, 16}
 template <int W> __device__ __forceinline__ float group_sum(float v) {
   static_assert(W == 8 || W == 16, "group width");

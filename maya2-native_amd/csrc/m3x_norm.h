@@ -3,8 +3,9 @@
 // Reduction order (the one the C oracle restates; bit-exactness depends on it): a row of N elements is read
 // as N/8 groups of 8 contiguous elements, one group per thread. A thread sums its 8 terms left to right
 // (each product and each sum rounded to fp32), then the N/8 partials are folded in half repeatedly:
-// p[g] = p[g] + p[g + s] for s = N/16, N/32, ..., 1. Within a wave the fold is an xor butterfly, which gives
-// lane g < s exactly p[g] + p[g + s].
+// p[g] = p[g] + p[g + s] for s = N/16, N/32, ..., 1. Folds across waves go through LDS; within a wave the fold
+// runs on permlane swaps (s = 32, 16) and DPP row shifts (s <= 8), which give lane g < s exactly
+// p[g] + p[g + s] (fold_half_sum).
 #pragma once
 #include "m3x_common.h"
 
@@ -26,9 +27,7 @@ __device__ __forceinline__ float row_tree_sum(float p, float* red, float* bcast)
     }
     p = red[threadIdx.x];
   }
-  constexpr int W = TPR < 64 ? TPR : 64;
-#pragma unroll
-  for (int s = W / 2; s > 0; s >>= 1) p = p + __shfl_xor(p, s, 64);
+  p = fold_half_sum<(TPR < 64 ? TPR : 64)>(p);
   if (t == 0) bcast[rb] = p;
   __syncthreads();
   float r = bcast[rb];

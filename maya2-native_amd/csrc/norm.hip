@@ -116,14 +116,19 @@ __global__ __launch_bounds__(256) void qk_norm_rope_cache_kernel(
   float p = x[0] * x[0];
 #pragma unroll
   for (int e = 1; e < 8; ++e) p = p + x[e] * x[e];
+  if constexpr (TPI == 16) {
+    p = dppf<DPP_ROW_NEWBCAST(0)>(fold_half_sum<16>(p));  // one DPP row per head: its total, from its first lane
+  } else {
 #pragma unroll
-  for (int s = TPI / 2; s > 0; s >>= 1) p = p + __shfl_xor(p, s, 64);
+    for (int s = TPI / 2; s > 0; s >>= 1) p = p + __shfl_xor(p, s, 64);
+  }
   const float inv = 1.0f / sqrtf(p / (float)D + eps);
 #pragma unroll
   for (int e = 0; e < 8; ++e) yv[e] = bf2f(f2bf(bf2f(f2bf(x[e] * inv)) * bf2f(wv.v[e])));
   float yp[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) yp[e] = __shfl_xor(yv[e], TPI / 2, 64);
+  for (int e = 0; e < 8; ++e)  // the rotate partner, lane t ^ TPI/2
+    yp[e] = TPI == 16 ? dppf<DPP_ROW_ROR(8)>(yv[e]) : __shfl_xor(yv[e], TPI / 2, 64);
   if (!active) return;
   const bool first = t < TPI / 2;
   u16x8 ov;
