@@ -59,7 +59,7 @@ __global__ __launch_bounds__(256, M3X_ATTN_MINB) void decode_attn_kernel(
   const int kend = min(kstart + chunk, ps + 1);
   const int nsplit = min((ps + chunk) / chunk, max_splits);  // ceil((ps + 1) / chunk)
 
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar branches
   const int lane = threadIdx.x & 63;
   const int li = lane & 15;  // MFMA row/col index
   const int lg = lane >> 4;  // MFMA k group

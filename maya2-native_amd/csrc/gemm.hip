@@ -132,7 +132,7 @@ __global__ __launch_bounds__(256) void linear_kernel(const uint16_t* __restrict_
   if (nb >= nblk) return;  // padding block: the whole workgroup leaves before any barrier
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
   const int lane = tid & 63;
   const int li = lane & 15;
   const int lg = lane >> 4;
@@ -280,7 +280,7 @@ __global__ __launch_bounds__(64 * NWAVES) void linear_oneshot_kernel(const uint1
   if (nb >= nblk) return;  // padding block: the whole workgroup leaves before any barrier
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
   const int lane = tid & 63;
   const int li = lane & 15;
   const int lg = lane >> 4;

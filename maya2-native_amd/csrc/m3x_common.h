@@ -176,7 +176,10 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-// v_mfma_f32_16x16x32_{bf16,f16}: A is 16x32, B is 32x16, D is 16x16 fp32.
+// v_mfma_f32_16x16x32_{bf16,f16}: A is 16x32, B is 32x16, D is 16x16 fp32. An MFMA writes its result whatever
+// the EXEC mask holds, so every condition around one must be wave-uniform as the compiler sees it (derive wave
+// indices with readfirstlane): a condition it takes as divergent becomes an EXEC-masked block that the MFMA
+// ignores.
 // Lane l holds A[l%16][8*(l/16)+e] and B[8*(l/16)+e][l%16] for e = 0..7, and D[4*(l/16)+r][l%16] for r = 0..3.
 template <int DT> __device__ __forceinline__ f32x4_t mfma16x16x32(const u16x8& a, const u16x8& b, f32x4_t c);
 template <> __device__ __forceinline__ f32x4_t mfma16x16x32<M3X_BF16>(const u16x8& a, const u16x8& b, f32x4_t c) {

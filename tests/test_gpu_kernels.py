@@ -22,7 +22,9 @@ def _g(seed):
                                    # one-workgroup-per-CU plans: 8 waves at K = 1024, 16 waves at longer K
                                    (224, 1024, 1024), (224, 2048, 1024), (224, 3072, 1024), (224, 4096, 1024),
                                    (250, 3072, 1024), (64, 2049, 1024), (224, 1024, 2048), (224, 1024, 2816),
-                                   (200, 1024, 3072), (100, 1024, 2816), (70, 1024, 2048)])
+                                   (200, 1024, 3072), (100, 1024, 2816), (70, 1024, 2048),
+                                   # K slices of unequal length: the last chunk of the last slice is partial
+                                   (40, 1024, 1056), (200, 1024, 1312), (3, 512, 160)])
 def test_linear_bf16(gpu, M, N, K):
     from m3x import ops
     g = _g(M * 7 + N)
