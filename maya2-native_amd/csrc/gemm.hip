@@ -367,10 +367,18 @@ static int oneshot_steps(int mt, int nw, int K) {
 }
 
 // Wide one-shot plans (measured on MI355X, graph-timed, 64..256 rows; 20-30 % under the chunked kernel on the
-// decode shapes). K = 1024: the first (MT, NW) of (2,2), (2,4), (3,4), (2,8) whose grid fits one workgroup per
+// decode shapes; up to 16 rows: 0.1-1.7 us under the 4-wave kernels). K = 1024: the first (MT, NW) of (2,2), (2,4), (3,4), (2,8) whose grid fits one workgroup per
 // CU (<= 256); 8 waves. K = 2048, 2816, 3072: 16-row blocks, 16 waves, NW = 4 above 160 rows, else 2.
 // Returns false when no instantiated plan covers (M, N, K).
 static bool wide_plan(int M, int N, int K, bool dual, LinearPlan& p) {
+  if (M <= 16 && (K == 1024 || K == 2048 || K == 2816 || K == 3072)) {
+    // one 16-row block: 8 waves, each a K/8 slice of one weight tile (3.7 against 5.3 us at 1 x 1024 x 2816)
+    p.mt = 1;
+    p.nw = 1;
+    p.nwaves = 8;
+    p.oneshot = K / 256;
+    return true;
+  }
   if (M < 64 || M > 256) return false;
   const int ntiles = m3x_ceil_div(N, 16);
   if (K == 1024) {
@@ -460,6 +468,11 @@ static bool launch_linear(const LinearPlan& p, hipStream_t st, const uint16_t* X
       case 240416: M3X_ONE(2, 4, 4, 16); return true;
       case 240408: M3X_ONE(2, 4, 4, 8); return true;
       case 210408: M3X_ONE(2, 1, 4, 8); return true;
+      // up to 16 rows, K = 1024 / 2048 / 2816 / 3072
+      case 110804: M3X_ONE(1, 1, 8, 4); return true;
+      case 110808: M3X_ONE(1, 1, 8, 8); return true;
+      case 110811: M3X_ONE(1, 1, 8, 11); return true;
+      case 110812: M3X_ONE(1, 1, 8, 12); return true;
       // wide, K = 1024
       case 220808: M3X_ONE(2, 2, 8, 8); return true;
       case 240816: M3X_ONE(2, 4, 8, 16); return true;

@@ -24,7 +24,9 @@ def _g(seed):
                                    (250, 3072, 1024), (64, 2049, 1024), (224, 1024, 2048), (224, 1024, 2816),
                                    (200, 1024, 3072), (100, 1024, 2816), (70, 1024, 2048),
                                    # K slices of unequal length: the last chunk of the last slice is partial
-                                   (40, 1024, 1056), (200, 1024, 1312), (3, 512, 160)])
+                                   (40, 1024, 1056), (200, 1024, 1312), (3, 512, 160),
+                                   # one 16-row block over 8 waves
+                                   (1, 1024, 2816), (16, 1024, 3072), (2, 2049, 2048), (1, 4096, 1024)])
 def test_linear_bf16(gpu, M, N, K):
     from m3x import ops
     g = _g(M * 7 + N)
