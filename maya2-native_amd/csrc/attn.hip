@@ -241,13 +241,36 @@ __global__ __launch_bounds__(256) void decode_attn_combine_kernel(uint16_t* __re
   const int h = threadIdx.x / AD;
   const int d = threadIdx.x % AD;
   const float* pp = part + ((long)row * KV + kh) * max_splits * PART_STRIDE;
+  // splits SB at a time, every load of a block issued before its first use (indices clamped, always in bounds);
+  // the max and the sums still run over the splits in order
+  constexpr int SB = 16;
   float M = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, pp[s * PART_STRIDE + h]);
+  for (int s0 = 0; s0 < nsplit; s0 += SB) {
+    float mv[SB];
+#pragma unroll
+    for (int i = 0; i < SB; ++i) mv[i] = pp[min(s0 + i, nsplit - 1) * PART_STRIDE + h];
+#pragma unroll
+    for (int i = 0; i < SB; ++i)
+      if (s0 + i < nsplit) M = fmaxf(M, mv[i]);
+  }
   float L = 0.f, O = 0.f;
-  for (int s = 0; s < nsplit; ++s) {
-    const float f = exp2f(pp[s * PART_STRIDE + h] - M);
-    L += pp[s * PART_STRIDE + 2 + h] * f;
-    O += pp[s * PART_STRIDE + 8 + h * AD + d] * f;
+  for (int s0 = 0; s0 < nsplit; s0 += SB) {
+    float mv[SB], lv[SB], ov[SB];
+#pragma unroll
+    for (int i = 0; i < SB; ++i) {
+      const float* ps = pp + min(s0 + i, nsplit - 1) * PART_STRIDE;
+      mv[i] = ps[h];
+      lv[i] = ps[2 + h];
+      ov[i] = ps[8 + h * AD + d];
+    }
+#pragma unroll
+    for (int i = 0; i < SB; ++i) {
+      if (s0 + i < nsplit) {
+        const float f = exp2f(mv[i] - M);
+        L += lv[i] * f;
+        O += ov[i] * f;
+      }
+    }
   }
   out[(long)row * so_b + (long)(kh * G + h) * so_h + d] = f2bf(O / L);
 }

@@ -208,15 +208,16 @@ def _attn_ref(q, K, V, slots, pos, scale, G):
     return out
 
 
-@pytest.mark.parametrize("heads,kv,chunk", [(16, 8, 128), (16, 8, 256), (16, 8, 1024), (8, 8, 128)])
-def test_decode_attn(gpu, heads, kv, chunk):
+@pytest.mark.parametrize("heads,kv,chunk,CAP", [(16, 8, 128, 2048), (16, 8, 256, 2048), (16, 8, 1024, 2048),
+                                               (8, 8, 128, 2048), (16, 8, 128, 4096)])
+def test_decode_attn(gpu, heads, kv, chunk, CAP):
     from m3x import ops
-    g = _g(heads + chunk)
-    D, CAP, S = 128, 2048, 9
+    g = _g(heads + chunk + CAP)
+    D, S = 128, 9
     K = torch.randn(S, kv, CAP, D, generator=g).to(torch.bfloat16)
     V = torch.randn(S, kv, CAP, D, generator=g).to(torch.bfloat16)
     slots = torch.tensor([0, 1, 2, 3, 4, 5, 6, 8, 1])
-    pos = torch.tensor([0, 31, 32, 127, 128, 1000, 2047, 513, 5], dtype=torch.int32)
+    pos = torch.tensor([0, 31, 32, 127, 128, 1000, CAP - 1, 513, 5], dtype=torch.int32)  # up to 32 splits
     # stale cache rows past each row's context hold NaN: nothing past pos may leak into the output
     for r in range(len(slots)):
         if slots[r] != 1:

@@ -13,11 +13,12 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def test_attn_chunk_plan():
     from m3x.serve.fast_backbone import attn_chunk
-    assert attn_chunk(1, 8, 2048) == 256          # one row: 8 splits per kv head to spread over the chip
+    assert attn_chunk(1, 8, 4096) == 128          # one row: 128-key splits spread over the chip
+    assert attn_chunk(16, 8, 4096) == 512
     assert attn_chunk(224, 8, 2048) == 4096       # 224 rows: 1792 workgroups unsplit, no combine launch
     for rows, ctx in [(1, 512), (64, 2048), (2264, 4096)]:
         c = attn_chunk(rows, 8, ctx)
-        assert c % 128 == 0 and 256 <= c <= 4096
+        assert c % 128 == 0 and 128 <= c <= 4096
 
 
 def test_roofline_matches_published_shapes():
