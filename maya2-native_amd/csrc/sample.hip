@@ -37,12 +37,36 @@ struct SampleSmem {
   float w[SMAXV];
   unsigned int hist[256];
   float red[ST / 64];
-  int ncand, nkeep, bstar;
+  int wtot[ST / 64];  // candidates per wave, for the compaction offsets
+  int nkeep, bstar;
   int code;  // the drawn code, for the waves that build the next level's input
 };
 
+// every lane gets the wave's maximum (DPP within rows, permlane swaps across them; max is exact in any order)
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dppf<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dppf<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dppf<0x141>(v));  // row_half_mirror: the partner quad's maximum
+  v = fmaxf(v, dppf<0x140>(v));  // row_mirror: the partner half-row's maximum
+  return xor32_max(xor16_max(v));
+}
+
+// inclusive prefix sum of an integer over the 64 lanes (integer adds: any order gives the same sums). DPP row
+// shifts build the sums within each row of 16, then row broadcasts carry the row totals forward.
+__device__ __forceinline__ unsigned int wave_incl_scan(unsigned int x) {
+  unsigned int v = x;
+  v = v + (unsigned int)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, true);  // row_shr:1
+  v = v + (unsigned int)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, true);  // row_shr:2
+  v = v + (unsigned int)__builtin_amdgcn_update_dpp(0, (int)x, 0x113, 0xf, 0xf, true);  // row_shr:3
+  v = v + (unsigned int)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xe, false);  // row_shr:4, lanes 4..15
+  v = v + (unsigned int)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xc, false);  // row_shr:8, lanes 8..15
+  v = v + (unsigned int)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false);  // row_bcast:15, rows 1, 3
+  v = v + (unsigned int)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false);  // row_bcast:31, rows 2, 3
+  return v;
+}
+
 __device__ float block_max(float v, float* red) {
-  v = wave_max_xor(v, 64);
+  v = wave_max_dpp(v);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
   float r = red[0];
@@ -53,21 +77,21 @@ __device__ float block_max(float v, float* red) {
 }
 
 // After this returns, sm.cand[0 .. sm.nkeep) holds the kept candidates in sampling order and sm.w their weights.
-// x[] holds this thread's elements i = tid + 256*e (e < SEPT) of the transformed row.
-__device__ void topk_select(const float (&x)[SEPT], int V, int k, SampleSmem& sm) {
+// x[] holds this thread's elements i = tid + 256*e (e < NE, NE * 256 >= V) of the transformed row.
+template <int NE>
+__device__ void topk_select(const float (&x)[NE], int V, int k, SampleSmem& sm) {
   const int tid = threadIdx.x;
   const float NEG = -INFINITY;
+  sm.hist[tid] = 0;  // ordered before the histogram by block_max's barriers
+  if (tid == 0) sm.nkeep = 0;
   float lm = NEG;
 #pragma unroll
-  for (int e = 0; e < SEPT; ++e)
+  for (int e = 0; e < NE; ++e)
     if (tid + ST * e < V) lm = fmaxf(lm, x[e]);
   const float m = block_max(lm, sm.red);
-  sm.hist[tid] = 0;
-  if (tid == 0) sm.ncand = 0, sm.nkeep = 0;
-  __syncthreads();
-  int bk[SEPT];
+  int bk[NE];
 #pragma unroll
-  for (int e = 0; e < SEPT; ++e) {
+  for (int e = 0; e < NE; ++e) {
     bk[e] = 256;
     if (tid + ST * e < V) {
       const float d = (m - x[e]) * 32.0f;
@@ -85,12 +109,7 @@ __device__ void topk_select(const float (&x)[SEPT], int V, int k, SampleSmem& sm
       c[i] = bin < 255 ? sm.hist[bin] : 0u;
       s += c[i];
     }
-    unsigned int incl = s;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const unsigned int o = __shfl_up(incl, off, 64);
-      if (tid >= off) incl += o;
-    }
+    const unsigned int incl = wave_incl_scan(s);
     unsigned int run = incl - s;
     int found = 255;
 #pragma unroll
@@ -109,23 +128,29 @@ __device__ void topk_select(const float (&x)[SEPT], int V, int k, SampleSmem& sm
   }
   __syncthreads();
   const int bstar = sm.bstar;
-  // compaction: one LDS atomic per wave; lanes take consecutive places by ballot rank
+  // compaction: each wave's count through LDS, a wave's base = the counts of the waves before it (candidates
+  // land in wave order); lanes take consecutive places by ballot rank
   const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const unsigned long long below = (1ull << lane) - 1ull;
-  unsigned long long masks[SEPT];
+  unsigned long long masks[NE];
   int total = 0;
 #pragma unroll
-  for (int e = 0; e < SEPT; ++e) {
+  for (int e = 0; e < NE; ++e) {
     masks[e] = __ballot(tid + ST * e < V && bk[e] <= bstar);
     total += __popcll(masks[e]);
   }
-  int base = 0;
-  if (total) {
-    if (lane == 0) base = atomicAdd(&sm.ncand, total);
-    base = __builtin_amdgcn_readfirstlane(base);
+  if (lane == 0) sm.wtot[wave] = total;
+  __syncthreads();
+  int base = 0, ncand = 0;
+#pragma unroll
+  for (int w = 0; w < ST / 64; ++w) {
+    const int c = sm.wtot[w];
+    base += w < wave ? c : 0;
+    ncand += c;
   }
 #pragma unroll
-  for (int e = 0; e < SEPT; ++e) {
+  for (int e = 0; e < NE; ++e) {
     const int i = tid + ST * e;
     if ((masks[e] >> lane) & 1ull)
       sm.cand[base + __popcll(masks[e] & below)] =
@@ -133,7 +158,7 @@ __device__ void topk_select(const float (&x)[SEPT], int V, int k, SampleSmem& sm
     base += __popcll(masks[e]);
   }
   __syncthreads();
-  const int nc = sm.ncand;
+  const int nc = ncand;
   int P2 = 2;
   while (P2 < nc) P2 <<= 1;
   if (nc <= ST) {
@@ -142,15 +167,13 @@ __device__ void topk_select(const float (&x)[SEPT], int V, int k, SampleSmem& sm
     const unsigned long long key = tid < nc ? sm.cand[tid] : 0ull;
     int rank = 0;
     if ((tid & ~63) < nc) {  // waves holding no candidate skip the count
-      int j = 0;
-      for (; j + 8 <= nc; j += 8) {  // eight broadcast reads in flight per step
-        unsigned long long c8[8];
+      for (int j = 0; j < nc; j += 16) {  // sixteen broadcast reads in flight per step (clamped, masked)
+        unsigned long long c16[16];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) c8[q] = sm.cand[j + q];
+        for (int q = 0; q < 16; ++q) c16[q] = sm.cand[min(j + q, nc - 1)];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) rank += c8[q] > key ? 1 : 0;
+        for (int q = 0; q < 16; ++q) rank += (j + q < nc && c16[q] > key) ? 1 : 0;
       }
-      for (; j < nc; ++j) rank += sm.cand[j] > key ? 1 : 0;
     }
     __syncthreads();
     if (tid < nc) sm.cand[rank] = key;
@@ -194,38 +217,40 @@ __device__ __forceinline__ float lanef(float v, int q) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), q));
 }
 
-// Sequential fp32 sums of w over cand[0..n) in order, skipping index `skip` (-1: none), by one wave. The weights
-// of 64 candidates sit one per lane (a skipped or absent one as +0.0, which leaves a sum that is never -0 exactly
-// unchanged) and are added in order through readlane; every lane keeps the running sum at its own position.
-// Running sums of chunks after the first are stored over their weights in sm.w. Returns the total (same value
-// in every lane); *last = position of the last term, -1 if none; *first_use / *first_run = the first chunk's
-// ballot of terms and this lane's running sum.
+// Running sums of the weights of cand[0..n) in order, skipping index `skip` (-1: none), by one wave: the weights of
+// 64 candidates sit one per lane (a skipped or absent one as +0.0) and are broadcast in order through readlane;
+// lane j adds weight q through fmaf(w_q, f, c) with f = 1 for q <= j and 0 after, so it holds exactly the
+// sequential fp32 sum w_0 + ... + w_j (fmaf(w, 1, c) rounds c + w once; fmaf(w, 0, c) = c), and lane 63 holds
+// the chunk's total, carried into the next chunk. No lane-dependent select is needed, so the chain is 64
+// independent-operand fmas. Running sums of chunks after the first are stored over their weights in sm.w.
+// Returns the total (same value in every lane); *last = position of the last term, -1 if none; *first_use /
+// *first_run = the first chunk's ballot of terms and this lane's running sum.
 __device__ float wave_prefix(SampleSmem& sm, int n, int skip, int* last, unsigned long long* first_use,
                              float* first_run) {
   const int lane = threadIdx.x & 63;
-  float c = 0.f;
+  const float lf = (float)lane;
+  float carry = 0.f;
   int l = -1;
   for (int j0 = 0; j0 < n; j0 += 64) {
     const int j = j0 + lane;
     const bool in = j < n && cand_index(sm.cand[j]) != skip;
     const float wsel = in ? sm.w[j] : 0.f;
     const unsigned long long use = __ballot(in);
-    float mine = 0.f;
+    float c = carry;
 #pragma unroll
-    for (int q = 0; q < 64; ++q) {
-      c = c + lanef(wsel, q);
-      mine = lane == q ? c : mine;
-    }
+    for (int q = 0; q < 64; ++q)
+      c = fmaf(lanef(wsel, q), __builtin_amdgcn_fmed3f(lf - (float)q + 1.0f, 0.0f, 1.0f), c);
+    carry = lanef(c, 63);
     if (use) l = j0 + 63 - __clzll((long long)use);
     if (j0 == 0) {
       *first_use = use;
-      *first_run = mine;
+      *first_run = c;
     } else if (j < n) {
-      sm.w[j] = mine;
+      sm.w[j] = c;
     }
   }
   *last = l;
-  return c;
+  return carry;
 }
 
 // Inverse-CDF pick over cand[0..n) skipping index `skip`: the first position whose running sum (the same
@@ -271,7 +296,7 @@ struct EmbedArgs {
   int kind;
 };
 
-template <int DT, int TPR>
+template <int DT, int TPR, int NE>
 __global__ __launch_bounds__(ST) void topk_sample_kernel(const uint16_t* __restrict__ logits, long ld_l, int V,
                                                          const float* __restrict__ u, long ld_u, float inv_temp,
                                                          int top_k, int greedy, void* out, long ld_out, int out_i64,
@@ -279,9 +304,9 @@ __global__ __launch_bounds__(ST) void topk_sample_kernel(const uint16_t* __restr
   __shared__ SampleSmem sm;
   const int row = blockIdx.x;
   const float ur = greedy ? 0.f : u[(long)row * ld_u];  // loaded first: its latency overlaps the selection
-  float x[SEPT];
+  float x[NE];
 #pragma unroll
-  for (int e = 0; e < SEPT; ++e) {
+  for (int e = 0; e < NE; ++e) {
     const int i = threadIdx.x + ST * e;
     x[e] = i < V ? E<DT>::to_f(logits[(long)row * ld_l + i]) * inv_temp : -INFINITY;
   }
@@ -340,14 +365,15 @@ M3X_API int m3x_topk_sample(const void* logits, long ld_l, int V, const float* u
   if (!logits || !out || (!greedy && !u)) return M3X_ENULL;
   hipStream_t st = (hipStream_t)stream;
   const EmbedArgs ea{};
-  if (dtype == M3X_BF16)
-    hipLaunchKernelGGL((topk_sample_kernel<M3X_BF16, 0>), dim3(B), dim3(ST), 0, st, (const uint16_t*)logits, ld_l, V,
-                       u, ld_u, inv_temp, top_k, greedy, out, ld_out, out_i64, ea);
-  else if (dtype == M3X_F16)
-    hipLaunchKernelGGL((topk_sample_kernel<M3X_F16, 0>), dim3(B), dim3(ST), 0, st, (const uint16_t*)logits, ld_l, V,
-                       u, ld_u, inv_temp, top_k, greedy, out, ld_out, out_i64, ea);
-  else
-    return M3X_EUNSUPPORTED;
+#define M3X_TS(DTT, NEE)                                                                                             \
+  hipLaunchKernelGGL((topk_sample_kernel<DTT, 0, NEE>), dim3(B), dim3(ST), 0, st, (const uint16_t*)logits, ld_l, V, \
+                     u, ld_u, inv_temp, top_k, greedy, out, ld_out, out_i64, ea)
+  if (dtype == M3X_BF16 && V <= 2048) M3X_TS(M3X_BF16, 8);
+  else if (dtype == M3X_BF16) M3X_TS(M3X_BF16, 16);
+  else if (dtype == M3X_F16 && V <= 2048) M3X_TS(M3X_F16, 8);
+  else if (dtype == M3X_F16) M3X_TS(M3X_F16, 16);
+  else return M3X_EUNSUPPORTED;
+#undef M3X_TS
   M3X_CHECK_LAUNCH();
   return M3X_OK;
 }
@@ -372,9 +398,15 @@ M3X_API int m3x_topk_sample_embed(const void* logits, long ld_l, int V, const fl
   hipStream_t st = (hipStream_t)stream;
   const EmbedArgs ea{(const uint16_t*)table, ld_table, table_rows, (uint16_t*)prefix, ld_prefix,
                      y ? (uint16_t*)x_out : nullptr, (uint16_t*)y, (const uint16_t*)w, (const uint16_t*)b, eps, kind};
-#define M3X_TSE(DTT, TT)                                                                                              \
-  hipLaunchKernelGGL((topk_sample_kernel<DTT, TT>), dim3(B), dim3(ST), 0, st, (const uint16_t*)logits, ld_l, V, u, \
-                     ld_u, inv_temp, top_k, greedy, out, ld_out, out_i64, ea)
+#define M3X_TSE(DTT, TT)                                                                                      \
+  do {                                                                                                     \
+    if (V <= 2048)                                                                                         \
+      hipLaunchKernelGGL((topk_sample_kernel<DTT, TT, 8>), dim3(B), dim3(ST), 0, st, (const uint16_t*)logits, \
+                         ld_l, V, u, ld_u, inv_temp, top_k, greedy, out, ld_out, out_i64, ea);               \
+    else                                                                                                   \
+      hipLaunchKernelGGL((topk_sample_kernel<DTT, TT, 16>), dim3(B), dim3(ST), 0, st, (const uint16_t*)logits, \
+                         ld_l, V, u, ld_u, inv_temp, top_k, greedy, out, ld_out, out_i64, ea);               \
+  } while (0)
   if (dtype == M3X_BF16 && n == 1024) M3X_TSE(M3X_BF16, 128);
   else if (dtype == M3X_F16 && n == 1024) M3X_TSE(M3X_F16, 128);
   else if (dtype == M3X_BF16 && n == 2048) M3X_TSE(M3X_BF16, 256);
