@@ -48,6 +48,83 @@ __global__ __launch_bounds__(256) void add_rms_kernel(const uint16_t* __restrict
   st16(y + (long)row * s_y + 8 * t, yv);
 }
 
+// Row counts up to which the one-wave-per-row kernels run (measured: below it they save a block barrier chain).
+constexpr int WAVE_ROWS_MAX = 16;
+
+// ---------------------------------------------------------------------------------------------------------
+// One wave per row of 1024, for a handful of rows (a one-row step is a chain of launches, and a lone row needs
+// no block barrier): lane l holds groups l and l + 64 (8 elements each), whose partials it adds as the first
+// fold (s = 64) of the same fold-in-half tree; the rest of the tree is fold_half_sum and lane 0's total is read
+// back with readlane. Same arithmetic, so the same bits, as the block kernels.
+template <int DT>
+__device__ __forceinline__ float wave_row_total(float p) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fold_half_sum<64>(p)), 0));
+}
+template <int DT>
+__device__ __forceinline__ void norm_pair_wave(const float (&v0)[8], const float (&v1)[8], const u16x8& w0,
+                                               const u16x8& w1, const u16x8& b0, const u16x8& b1, int kind, float eps,
+                                               u16x8& y0, u16x8& y1) {
+  constexpr float N = 1024.0f;
+  if (kind == M3X_NORM_LAYER) {
+    float p0 = v0[0], p1 = v1[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) p0 = p0 + v0[e], p1 = p1 + v1[e];
+    const float mean = wave_row_total<DT>(p0 + p1) / N;
+    float d0[8], d1[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) d0[e] = v0[e] - mean, d1[e] = v1[e] - mean;
+    p0 = d0[0] * d0[0];
+    p1 = d1[0] * d1[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) p0 = p0 + d0[e] * d0[e], p1 = p1 + d1[e] * d1[e];
+    const float var = wave_row_total<DT>(p0 + p1) / N;
+    const float sd = sqrtf(var + eps);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      y0.v[e] = E<DT>::from_f(d0[e] / sd * E<DT>::to_f(w0.v[e]) + E<DT>::to_f(b0.v[e]));
+      y1.v[e] = E<DT>::from_f(d1[e] / sd * E<DT>::to_f(w1.v[e]) + E<DT>::to_f(b1.v[e]));
+    }
+  } else {
+    float p0 = v0[0] * v0[0], p1 = v1[0] * v1[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) p0 = p0 + v0[e] * v0[e], p1 = p1 + v1[e] * v1[e];
+    const float inv = 1.0f / sqrtf(wave_row_total<DT>(p0 + p1) / N + eps);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      y0.v[e] = E<DT>::from_f(rnd<DT>(v0[e] * inv) * E<DT>::to_f(w0.v[e]));
+      y1.v[e] = E<DT>::from_f(rnd<DT>(v1[e] * inv) * E<DT>::to_f(w1.v[e]));
+    }
+  }
+}
+
+// add_rms_kernel's contract for n = 1024, one 64-thread workgroup per row.
+__global__ __launch_bounds__(64) void add_rms_wave_kernel(const uint16_t* __restrict__ h, long s_h,
+                                                          const uint16_t* __restrict__ a, long s_a, uint16_t* ho,
+                                                          long s_ho, uint16_t* __restrict__ y, long s_y,
+                                                          const uint16_t* __restrict__ w, float eps) {
+  const long row = blockIdx.x;
+  const int l = threadIdx.x;
+  u16x8 h0 = ld16(h + row * s_h + 8 * l), h1 = ld16(h + row * s_h + 8 * (l + 64));
+  u16x8 a0, a1;
+  if (a) a0 = ld16(a + row * s_a + 8 * l), a1 = ld16(a + row * s_a + 8 * (l + 64));
+  const u16x8 w0 = ld16(w + 8 * l), w1 = ld16(w + 8 * (l + 64));
+  if (a) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      h0.v[e] = f2bf(bf2f(h0.v[e]) + bf2f(a0.v[e]));
+      h1.v[e] = f2bf(bf2f(h1.v[e]) + bf2f(a1.v[e]));
+    }
+    if (ho) st16(ho + row * s_ho + 8 * l, h0), st16(ho + row * s_ho + 8 * (l + 64), h1);
+  }
+  float v0[8], v1[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v0[e] = bf2f(h0.v[e]), v1[e] = bf2f(h1.v[e]);
+  u16x8 y0, y1;
+  norm_pair_wave<M3X_BF16>(v0, v1, w0, w1, w0, w1, M3X_NORM_RMS, eps, y0, y1);
+  st16(y + row * s_y + 8 * l, y0);
+  st16(y + row * s_y + 8 * (l + 64), y1);
+}
+
 M3X_API int m3x_add_rms(const void* h, long s_h, const void* a, long s_a, void* h_out, long s_ho, void* y, long s_y,
                         const void* w, float eps, int rows, int n, void* stream) {
   if (rows < 0) return M3X_EINVAL;
@@ -60,6 +137,11 @@ M3X_API int m3x_add_rms(const void* h, long s_h, const void* a, long s_a, void* 
   hipStream_t st = (hipStream_t)stream;
   const uint16_t *H = (const uint16_t*)h, *A = (const uint16_t*)a, *Wt = (const uint16_t*)w;
   uint16_t *HO = (uint16_t*)h_out, *Y = (uint16_t*)y;
+  if (n == 1024 && rows <= WAVE_ROWS_MAX) {
+    hipLaunchKernelGGL(add_rms_wave_kernel, dim3(rows), dim3(64), 0, st, H, s_h, A, s_a, HO, s_ho, Y, s_y, Wt, eps);
+    M3X_CHECK_LAUNCH();
+    return M3X_OK;
+  }
   switch (n) {
 #define M3X_ADD_RMS_CASE(NN)                                                                                   \
   case NN: {                                                                                                   \
@@ -232,6 +314,45 @@ __global__ __launch_bounds__(256) void add_norm_kernel(const uint16_t* __restric
   st16(y + (long)row * N + 8 * t, yv);
 }
 
+// add_norm_kernel's contract for n = 1024, one 64-thread workgroup per row.
+template <int DT>
+__global__ __launch_bounds__(64) void add_norm_wave_kernel(const uint16_t* __restrict__ x, long sxb, long sxt,
+                                                           const uint16_t* __restrict__ a, long sab, long sat,
+                                                           const uint16_t* __restrict__ c, long s_c, uint16_t* xo,
+                                                           uint16_t* __restrict__ y, const uint16_t* __restrict__ w,
+                                                           const uint16_t* __restrict__ b, float eps, int T,
+                                                           int kind) {
+  const int row = blockIdx.x;
+  const int l = threadIdx.x;
+  const long rb = row / T, rt = row % T;
+  const uint16_t* xr = x + rb * sxb + rt * sxt;
+  u16x8 x0 = ld16(xr + 8 * l), x1 = ld16(xr + 8 * (l + 64));
+  u16x8 a0, a1, c0, c1, b0 = {}, b1 = {};
+  if (a) a0 = ld16(a + rb * sab + rt * sat + 8 * l), a1 = ld16(a + rb * sab + rt * sat + 8 * (l + 64));
+  if (c) c0 = ld16(c + rb * s_c + 8 * l), c1 = ld16(c + rb * s_c + 8 * (l + 64));
+  const u16x8 w0 = ld16(w + 8 * l), w1 = ld16(w + 8 * (l + 64));
+  if (kind == M3X_NORM_LAYER) b0 = ld16(b + 8 * l), b1 = ld16(b + 8 * (l + 64));
+  float v0[8], v1[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    v0[e] = E<DT>::to_f(x0.v[e]);
+    v1[e] = E<DT>::to_f(x1.v[e]);
+    if (a) v0[e] = rnd<DT>(v0[e] + E<DT>::to_f(a0.v[e])), v1[e] = rnd<DT>(v1[e] + E<DT>::to_f(a1.v[e]));
+    if (c) v0[e] = rnd<DT>(v0[e] + E<DT>::to_f(c0.v[e])), v1[e] = rnd<DT>(v1[e] + E<DT>::to_f(c1.v[e]));
+  }
+  if (xo) {
+    u16x8 o0, o1;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o0.v[e] = E<DT>::from_f(v0[e]), o1.v[e] = E<DT>::from_f(v1[e]);
+    st16(xo + (long)row * 1024 + 8 * l, o0);
+    st16(xo + (long)row * 1024 + 8 * (l + 64), o1);
+  }
+  u16x8 y0, y1;
+  norm_pair_wave<DT>(v0, v1, w0, w1, b0, b1, kind, eps, y0, y1);
+  st16(y + (long)row * 1024 + 8 * l, y0);
+  st16(y + (long)row * 1024 + 8 * (l + 64), y1);
+}
+
 // Row r = (b, t) = (r / T, r % T) of x is read at x + b*sxb + t*sxt (likewise a); x_out and y are contiguous
 // [rows, n]; c is indexed by b with stride s_c (s_c = 0 broadcasts one vector).
 M3X_API int m3x_add_norm(const void* x, long sxb, long sxt, const void* a, long sab, long sat, const void* c, long s_c,
@@ -250,6 +371,16 @@ M3X_API int m3x_add_norm(const void* x, long sxb, long sxt, const void* a, long 
   const uint16_t *X = (const uint16_t*)x, *A = (const uint16_t*)a, *C = (const uint16_t*)c;
   const uint16_t *Wt = (const uint16_t*)w, *Bt = (const uint16_t*)b;
   uint16_t *XO = (uint16_t*)x_out, *Y = (uint16_t*)y;
+  if (n == 1024 && rows <= WAVE_ROWS_MAX && (dtype == M3X_BF16 || dtype == M3X_F16)) {
+    if (dtype == M3X_BF16)
+      hipLaunchKernelGGL(add_norm_wave_kernel<M3X_BF16>, dim3(rows), dim3(64), 0, st, X, sxb, sxt, A, sab, sat, C, s_c,
+                         XO, Y, Wt, Bt, eps, T, kind);
+    else
+      hipLaunchKernelGGL(add_norm_wave_kernel<M3X_F16>, dim3(rows), dim3(64), 0, st, X, sxb, sxt, A, sab, sat, C, s_c,
+                         XO, Y, Wt, Bt, eps, T, kind);
+    M3X_CHECK_LAUNCH();
+    return M3X_OK;
+  }
 #define M3X_ADD_NORM_LAUNCH(NN, DTT)                                                                               \
   hipLaunchKernelGGL((add_norm_kernel<NN / 8, DTT>), dim3(m3x_ceil_div(rows, 256 / (NN / 8))), dim3(256), 0, st, X, \
                      sxb, sxt, A, sab, sat, C, s_c, XO, Y, Wt, Bt, eps, rows, T, kind)
