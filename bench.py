@@ -186,6 +186,40 @@ def main():
         attn_bytes = roofline.decode_attn_bytes(att_keys, B)
         attn_gbs = attn_bytes / (attn_us * 1e-6) / 1e9
         log(f"decode attention: {attn_us:.1f} us/launch, {attn_gbs:.0f} GB/s ({attn_gbs / roofline.HBM_PEAK_GBS:.1%})")
+        # fused residual add + RMSNorm (the backbone's norm kernel): at the frame's 224 rows, over rotating
+        # buffer sets, launched from a graph as in the frame, and at a streaming size (2 GB per launch) where
+        # launch latency is amortised
+        norm = {}
+        hw = torch.ones(1024, dtype=torch.bfloat16, device=dev)
+        for label, rows, sets, iters in (("frame", B, 8, 64), ("stream", 262144, 1, 8)):
+            bufsets = [[torch.randn(rows, 1024, device=dev).to(torch.bfloat16) for _ in range(4)] for _ in range(sets)]
+
+            def norms():
+                for i in range(iters):
+                    bs = bufsets[i % sets]
+                    ops.add_rms(bs[0], bs[1], hw, 1e-6, bs[2], bs[3])
+            side = torch.cuda.Stream()
+            side.wait_stream(stream)
+            with torch.cuda.stream(side):
+                norms()
+            stream.wait_stream(side)
+            ng = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(ng, stream=side):
+                norms()
+            ng.replay()
+            e0.record(stream)
+            for _ in range(3):
+                ng.replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            n_us = e0.elapsed_time(e1) * 1e3 / (3 * iters)
+            n_gbs = roofline.add_norm_bytes(rows) / (n_us * 1e-6) / 1e9
+            norm[label] = {"rows": rows, "launch_us": round(n_us, 2), "achieved": round(n_gbs, 1),
+                           "frac": round(n_gbs / roofline.HBM_PEAK_GBS, 4)}
+            log(f"add+RMSNorm {label} ({rows} rows): {n_us:.2f} us/launch, {n_gbs:.0f} GB/s "
+                f"({n_gbs / roofline.HBM_PEAK_GBS:.1%})")
+            del bufsets
+        torch.cuda.empty_cache()
         if args.copy_probe:
             # a plain device copy of known size: what FETCH_SIZE / WRITE_SIZE read for it scales their counts
             src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
@@ -252,6 +286,8 @@ def main():
                      "achieved": round(attn_gbs, 1), "peak": roofline.HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(attn_gbs / roofline.HBM_PEAK_GBS, 4), "traffic": None if ratio is None else int(ratio * attn_bytes),
                      "launch_us": round(attn_us, 2), "bytes_per_launch": attn_bytes},
+        "norm_roofline": {"kernel": "add_rms (residual add + RMSNorm, hidden 1024)", "bound": "hbm", "unit": "GB/s",
+                          "peak": roofline.HBM_PEAK_GBS, **norm},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

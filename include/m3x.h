@@ -136,9 +136,11 @@ int m3x_topk_sample_embed(const void* logits, long ld_l, int V, const float* u, 
 
 /* cb0 controlled stop + sampling per seat (per-slot state indexed by slots[b]); any per-slot pointer may be NULL.
  * Replaces `Engine._cb0` (maya3/engine.py:652-694) with caller uniforms in place of `row_exponential`
- * (serve/fast_depth_kernels.py:82-98). */
+ * (serve/fast_depth_kernels.py:82-98). topp_t[s] (or top_p when topp_t is NULL) below 1 applies the top-p cut
+ * of :669-672 to the top-k set. */
 int m3x_cb0_sample(const void* logits, long ld_l, int V, int aeos, const int64_t* slots, const float* u, long ld_u,
-                   const float* temp_t, float temp, const int64_t* topk_t, int top_k, const float* aeos_bias,
+                   const float* temp_t, float temp, const int64_t* topk_t, int top_k, const float* topp_t,
+                   float top_p, const float* aeos_bias,
                    const float* rep_t, int64_t* hist_t, int hist_w, int64_t* frames_t, const int64_t* min_t,
                    float* hazard_t, int32_t* ctr_t, int64_t* cb0_out, int32_t* cb0_i32, long ld_cb0_i32,
                    int64_t* stop_out, int B, void* stream);

@@ -273,6 +273,33 @@ __device__ int pick(SampleSmem& sm, int n, float u, int skip) {
   }
   return cand_index(sm.cand[last]);
 }
+
+// Top-p cut of the kept set cand[0..n) (maya3/engine.py:669-672: a candidate is dropped when the probability mass
+// sorted before it exceeds top_p): position j stays while run_(j-1) / S <= top_p, where run is the sequential fp32
+// running sum of the weights in order (the fmaf broadcast of wave_prefix) and S their total in the same order.
+// The kept set stays a prefix of the order. Called by one whole wave; leaves sm.w unchanged; returns the new
+// length (>= 1) in every lane.
+__device__ int top_p_keep(const SampleSmem& sm, int n, float top_p) {
+  const float lf = (float)(threadIdx.x & 63);
+  auto chunk_runs = [&](int j0, float carry) {
+    const int j = j0 + (int)(threadIdx.x & 63);
+    const float wj = j < n ? sm.w[j] : 0.f;
+    float c = carry;
+#pragma unroll
+    for (int q = 0; q < 64; ++q) c = fmaf(lanef(wj, q), __builtin_amdgcn_fmed3f(lf - (float)q + 1.0f, 0.0f, 1.0f), c);
+    return c;
+  };
+  float S = 0.f;
+  for (int j0 = 0; j0 < n; j0 += 64) S = lanef(chunk_runs(j0, S), 63);
+  float carry = 0.f;
+  for (int j0 = 0; j0 < n; j0 += 64) {
+    const float c = chunk_runs(j0, carry);  // lane l: run_(j0 + l)
+    carry = lanef(c, 63);
+    const unsigned long long cut = __ballot(j0 + (int)(threadIdx.x & 63) + 1 < n && c / S > top_p);
+    if (cut) return j0 + __ffsll((long long)cut);  // first j with run_j / S > top_p keeps 0..j
+  }
+  return n;
+}
 }  // namespace
 
 // ---------------------------------------------------------------------------------------------------------
@@ -421,7 +448,8 @@ M3X_API int m3x_topk_sample_embed(const void* logits, long ld_l, int V, const fl
 // cb0 step: controlled stop + codebook-0 sampling for each seat (maya3/engine.py:652-694, Engine._cb0).
 // Per row b with slot s = slots[b] (per-slot tensors are indexed by s, like the engine's [max_seats+1] state):
 //   x_i = float(logit_i) / temp[s];  x_aeos += aeos_bias[s];  x_i -= rep[s] for every i != aeos seen in
-//   hist[s, :] (entries >= 0);  top-k (k = topk[s], clamped to [1, V]) as in the contract above.
+//   hist[s, :] (entries >= 0);  top-k (k = topk[s], clamped to [1, V]) as in the contract above; then, with
+//   top_p = topp[s] < 1, the kept set is cut to its top-p prefix (top_p_keep).
 //   With an AEOS class (aeos >= 0): probs = w / S over the kept set; pa = w_aeos / S; arg = first in order;
 //   can = frames[s] >= min_frames[s]; hz = can ? 1 - (1 - hazard[s]) * (1 - pa) : hazard[s];
 //   stop = can & arg==aeos ? 2 : can & pa>=0.35 ? 3 : can & hz>=0.6 ? 4 : 0;
@@ -440,6 +468,8 @@ struct Cb0Args {
   float temp;
   const int64_t* topk_t;
   int top_k;
+  const float* topp_t;
+  float top_p;
   const float* aeos_bias;
   const float* rep_t;
   int64_t* hist_t;
@@ -463,6 +493,7 @@ __global__ __launch_bounds__(ST) void cb0_sample_kernel(Cb0Args a) {
   k = k < 1 ? 1 : (k > a.V ? a.V : k);
   const float bias = a.aeos_bias ? a.aeos_bias[s] : 0.f;
   const float rep = a.rep_t ? a.rep_t[s] : 0.f;
+  const float top_p = a.topp_t ? a.topp_t[s] : a.top_p;
   const float uu = a.u[(long)row * a.ld_u];  // loaded first: its latency overlaps the selection
   float x[SEPT];
 #pragma unroll
@@ -482,7 +513,8 @@ __global__ __launch_bounds__(ST) void cb0_sample_kernel(Cb0Args a) {
   }
   topk_select(x, a.V, k, sm);
   if (threadIdx.x >= 64) return;  // wave 0 draws; lane 0 writes
-  const int n = sm.nkeep;
+  int n = sm.nkeep;
+  if (top_p < 1.0f) n = top_p_keep(sm, n, top_p);
   int cb0;
   int64_t stop = 0;
   if (a.aeos >= 0) {
@@ -531,14 +563,15 @@ __global__ __launch_bounds__(ST) void cb0_sample_kernel(Cb0Args a) {
 
 M3X_API int m3x_cb0_sample(const void* logits, long ld_l, int V, int aeos, const int64_t* slots, const float* u,
                            long ld_u, const float* temp_t, float temp, const int64_t* topk_t, int top_k,
-                           const float* aeos_bias, const float* rep_t, int64_t* hist_t, int hist_w, int64_t* frames_t,
+                           const float* topp_t, float top_p, const float* aeos_bias, const float* rep_t, int64_t* hist_t, int hist_w, int64_t* frames_t,
                            const int64_t* min_t, float* hazard_t, int32_t* ctr_t, int64_t* cb0_out, int32_t* cb0_i32,
                            long ld_cb0_i32, int64_t* stop_out, int B, void* stream) {
   if (B < 0 || V <= 0 || V > SMAXV || aeos >= V || hist_w < 0) return M3X_EINVAL;
   if (B == 0) return M3X_OK;
   if (!logits || !slots || !u) return M3X_ENULL;
   if (!temp_t && !(temp > 0.f)) return M3X_EINVAL;
-  Cb0Args a{(const uint16_t*)logits, ld_l, V, aeos, slots, u, ld_u, temp_t, temp, topk_t, top_k, aeos_bias, rep_t,
+  Cb0Args a{(const uint16_t*)logits, ld_l, V, aeos, slots, u, ld_u, temp_t, temp, topk_t, top_k, topp_t, top_p,
+            aeos_bias, rep_t,
             hist_t, hist_w, frames_t, min_t, hazard_t, ctr_t, cb0_out, cb0_i32, ld_cb0_i32, stop_out};
   hipLaunchKernelGGL(cb0_sample_kernel, dim3(B), dim3(ST), 0, (hipStream_t)stream, a);
   M3X_CHECK_LAUNCH();

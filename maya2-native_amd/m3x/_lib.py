@@ -12,7 +12,7 @@ import os
 import torch  # noqa: F401  (must precede the CDLL load, see above)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libm3x.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -42,8 +42,8 @@ SIGNATURES = {
     "m3x_topk_sample": (_I, [_P, _L, _I, _P, _L, _F, _I, _I, _P, _L, _I, _I, _I, _P]),
     "m3x_topk_sample_embed": (_I, [_P, _L, _I, _P, _L, _F, _I, _I, _P, _L, _I, _I, _P, _L, _L, _P, _L, _P, _P, _P,
                                    _P, _F, _I, _I, _I, _P]),
-    "m3x_cb0_sample": (_I, [_P, _L, _I, _I, _P, _P, _L, _P, _F, _P, _I, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _L,
-                            _P, _I, _P]),
+    "m3x_cb0_sample": (_I, [_P, _L, _I, _I, _P, _P, _L, _P, _F, _P, _I, _P, _F, _P, _P, _P, _I, _P, _P, _P, _P, _P,
+                            _P, _L, _P, _I, _P]),
     "m3x_philox_uniforms": (_I, [_P, _P, _P, _P, _L, _I, _I, _I, _P]),
     "m3x_philox_exponential": (_I, [_P, _P, _P, _L, _I, _I, _I, _P]),
     "m3x_philox_block": (_I, [_P, _P, _P, _P]),

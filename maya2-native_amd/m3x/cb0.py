@@ -3,8 +3,8 @@
 Equivalent of Engine._cb0 (maya3/engine.py:652-694) and the per-slot sampler state Engine._build_fast allocates
 (:208-233) and Engine._bind writes (:429-444). Where the engine draws Exp(1) noise with `row_exponential` and
 takes argmax(q/E), this draws one Philox uniform per seat from the same (seed, frame counter, level 0) stream key
-and inverts the CDF of the same renormalised top-k distribution (the kernel's contract is in csrc/sample.hip).
-Top-p below 1 is not implemented here and is rejected when a seat asks for it.
+and inverts the CDF of the same renormalised top-k (then top-p) distribution (the kernel's contract is in
+csrc/sample.hip).
 """
 from __future__ import annotations
 
@@ -17,7 +17,8 @@ from ._lib import lib
 
 
 class Cb0Sampler:
-    def __init__(self, head_weight, max_seats, aeos=None, temp=0.9, top_k=64, rep=0.8, rep_win=12, stop=True):
+    def __init__(self, head_weight, max_seats, aeos=None, temp=0.9, top_k=64, rep=0.8, rep_win=12, stop=True,
+                 top_p=1.0):
         """head_weight [V0, hidden] bf16 (Backbone.cb0_head, tts/model/backbone.py:121). aeos: the AEOS class
         (default 2048 when V0 == 2049, else none). stop=False skips the controlled-stop bookkeeping."""
         lib()
@@ -34,6 +35,10 @@ class Cb0Sampler:
         self.max_seats = max_seats
         self.temp_t = torch.full((m,), float(temp), device=dev, dtype=torch.float32)
         self.topk_t = torch.full((m,), int(top_k), device=dev, dtype=torch.long)
+        if not 0.0 < float(top_p) <= 1.0:
+            raise ValueError("top_p must be in (0, 1]")
+        self.top_p = float(top_p)
+        self.topp_t = torch.full((m,), self.top_p, device=dev, dtype=torch.float32)
         self.rep_t = torch.full((m,), float(rep), device=dev, dtype=torch.float32)
         self.seed_t = torch.zeros(m, device=dev, dtype=torch.int32)
         self.ctr_t = torch.zeros(m, device=dev, dtype=torch.int32)
@@ -47,8 +52,8 @@ class Cb0Sampler:
     @torch.inference_mode()
     def bind(self, slot, seed, temperature=None, top_k=None, top_p=None, repetition_penalty=None, min_frames=0):
         """Per-seat settings at admission (maya3/engine.py:429-444)."""
-        if top_p is not None and float(top_p) < 1.0:
-            raise ValueError('top_p < 1 is not implemented by the m3x cb0 sampler')
+        if top_p is not None and not 0.0 < float(top_p) <= 1.0:
+            raise ValueError("top_p must be in (0, 1]")
         self.seed_t[slot] = int(seed)
         self.ctr_t[slot] = 0
         self.frames_t[slot] = 0
@@ -60,6 +65,7 @@ class Cb0Sampler:
             self.temp_t[slot] = float(temperature)
         if top_k is not None:
             self.topk_t[slot] = int(top_k)
+        self.topp_t[slot] = float(top_p) if top_p else self.top_p
         if repetition_penalty is not None:
             self.rep_t[slot] = float(repetition_penalty)
             self.any_rep = self.any_rep or float(repetition_penalty) > 0
@@ -83,6 +89,7 @@ class Cb0Sampler:
             ops.philox_uniforms(self.seed_t, self.ctr_t, b.slots, b.u, 0)
         rep = self.any_rep and self.rep_win > 0
         ops.cb0_sample(b.logits, self.aeos, b.slots, b.u[:, 0], temp_t=self.temp_t, topk_t=self.topk_t,
+                       topp_t=self.topp_t,
                        aeos_bias=self.aeos_bias if self.aeos >= 0 else None, rep_t=self.rep_t if rep else None,
                        hist_t=self.hist_t if self.rep_win > 0 else None,
                        frames_t=self.frames_t if self.stop else None, min_t=self.min_t if self.stop else None,

@@ -271,16 +271,18 @@ def topk_sample_embed(logits, u, inv_temp, top_k, greedy, out, table, prefix, x_
 
 def cb0_sample(logits, aeos, slots, u, temp_t=None, temp=1.0, topk_t=None, top_k=50, aeos_bias=None, rep_t=None,
                hist_t=None, frames_t=None, min_t=None, hazard_t=None, ctr_t=None, cb0_out=None, cb0_i32=None,
-               stop_out=None):
+               stop_out=None, topp_t=None, top_p=1.0):
     _dev(logits, slots, u, temp_t, topk_t, aeos_bias, rep_t, hist_t, frames_t, min_t, hazard_t, ctr_t, cb0_out,
-         cb0_i32, stop_out)
+         cb0_i32, stop_out, topp_t)
+    if topp_t is not None and topp_t.dtype != torch.float32:
+        raise ValueError("topp_t must be float32")
     _rows2d(logits, "logits")
     if logits.dtype != torch.bfloat16:
         raise ValueError("cb0 logits must be bfloat16")
     B, V = logits.shape
     check(lib().m3x_cb0_sample(
         _p(logits), logits.stride(0), V, int(aeos), _p(slots), _p(u), u.stride(0), _p(temp_t), float(temp),
-        _p(topk_t), int(top_k), _p(aeos_bias), _p(rep_t), _p(hist_t), 0 if hist_t is None else hist_t.shape[1],
+        _p(topk_t), int(top_k), _p(topp_t), float(top_p), _p(aeos_bias), _p(rep_t), _p(hist_t), 0 if hist_t is None else hist_t.shape[1],
         _p(frames_t), _p(min_t), _p(hazard_t), _p(ctr_t), _p(cb0_out), _p(cb0_i32),
         0 if cb0_i32 is None else cb0_i32.stride(0), _p(stop_out), B, _stream()), "cb0_sample")
 

@@ -16,6 +16,11 @@ def decode_attn_bytes(attended, rows, heads=16, kv_heads=8, head_dim=128, elem=2
     return attended * kv_heads * head_dim * elem * 2 + rows * heads * head_dim * elem * 2
 
 
+def add_norm_bytes(rows, hidden=1024, elem=2):
+    """Fused residual add + RMSNorm: h and a in, h + a and y out, plus the norm weight."""
+    return rows * hidden * elem * 4 + hidden * elem
+
+
 def decode_attn_flops(attended, heads=16, head_dim=128):
     return attended * heads * head_dim * 2 * 2
 

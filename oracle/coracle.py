@@ -38,7 +38,7 @@ def lib():
         L.o_topk_sample.restype = _I
         L.o_topk_sample_many.argtypes = [_P, _I, _I, _P, _I, _P]
         L.o_topk_sample_rows.argtypes = [_P, _I, _I, _I, _F, _I, _P, _I, _P]
-        L.o_cb0_sample.argtypes = [_P, _I, _I, _F, _I, _F, _F, _P, _I, _P, ctypes.c_int64, _P, _P, _F, _P]
+        L.o_cb0_sample.argtypes = [_P, _I, _I, _F, _I, _F, _F, _F, _P, _I, _P, ctypes.c_int64, _P, _P, _F, _P]
         L.o_cb0_sample.restype = _I
         L.o_philox4x32_10.argtypes = [_P, _P, _P]
         L.o_philox_uniform.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]
@@ -126,11 +126,11 @@ def topk_sample_rows(logits16: np.ndarray, inv_temp: float, k: int, u: np.ndarra
 
 def cb0_sample(logits16: np.ndarray, aeos: int, temp: float, k: int, bias: float, rep: float,
                hist: np.ndarray | None, frames: np.ndarray | None, min_frames: int, hazard: np.ndarray | None,
-               ctr: np.ndarray | None, u: float):
+               ctr: np.ndarray | None, u: float, top_p: float = 1.0):
     """One seat. hist int64 [W] / frames int64 [1] / hazard float32 [1] / ctr int32 [1] are updated in place."""
     logits16 = np.ascontiguousarray(logits16, np.uint16)
     stop = np.zeros(1, np.int64)
-    cb0 = lib().o_cb0_sample(_ptr(logits16), logits16.size, aeos, temp, k, bias, rep,
+    cb0 = lib().o_cb0_sample(_ptr(logits16), logits16.size, aeos, temp, k, top_p, bias, rep,
                              _ptr(hist) if hist is not None else None, 0 if hist is None else hist.size,
                              _ptr(frames) if frames is not None else None, min_frames,
                              _ptr(hazard) if hazard is not None else None, _ptr(ctr) if ctr is not None else None,

@@ -16,7 +16,8 @@
  *   o_topk_sample     vs the exact top-k softmax (total variation over uniform draws), k=1 / u=0 -> argmax,
  *                     ties kept (x >= kth)
  *   o_cb0_sample      vs a torch restatement of maya3/engine.py:652-694 with the Gumbel race replaced by the
- *                     same inverse CDF (stop codes, renormalisation, penalty, bias)
+ *                     same inverse CDF (stop codes, renormalisation, penalty, bias); its top-p cut vs the
+ *                     engine's softmax/sort/cumsum mask (:669-672) on distinct logits
  *   o_philox4x32_10   vs the Random123 known-answer vectors
  */
 #include <math.h>
@@ -260,10 +261,25 @@ void o_topk_sample_rows(const uint16_t* logits, int B, int V, int is_f16, float 
   free(x);
 }
 
+/* Top-p cut of a top-k kept set in sorted order (maya3/engine.py:669-672: drop a candidate when the probability
+ * mass sorted before it exceeds top_p). Position j stays while run_(j-1) / S <= top_p, with run the sequential
+ * fp32 running sum of the weights in order and S their total in the same order. Returns the kept length (>= 1). */
+static int top_p_keep(const float* w, int n, float top_p) {
+  float S = 0.f;
+  for (int j = 0; j < n; ++j) S = S + w[j];
+  float run = 0.f;
+  for (int j = 0; j + 1 < n; ++j) {
+    run = run + w[j];
+    if (run / S > top_p) return j + 1;
+  }
+  return n;
+}
+
 /* cb0 controlled stop + sampling for one seat (maya3/engine.py:652-694), caller uniform in place of the
  * exponential race. State arrays are this seat's (scalars passed by pointer; hist of length hist_w).
+ * top_p < 1 cuts the top-k set (top_p_keep) before the stop statistics and the draw.
  * Returns cb0; *stop gets the stop code. aeos < 0: no AEOS class (no stop logic, no exclusion). */
-int o_cb0_sample(const uint16_t* logits, int V, int aeos, float temp, int k, float bias, float rep,
+int o_cb0_sample(const uint16_t* logits, int V, int aeos, float temp, int k, float top_p, float bias, float rep,
                  int64_t* hist, int hist_w, int64_t* frames, int64_t min_frames, float* hazard, int32_t* ctr,
                  float u, int64_t* stop) {
   float* x = (float*)malloc(sizeof(float) * V);
@@ -281,8 +297,9 @@ int o_cb0_sample(const uint16_t* logits, int V, int aeos, float temp, int k, flo
   }
   if (k < 1) k = 1;
   if (k > V) k = V;
-  const int n = topk_order(x, V, k, c);
+  int n = topk_order(x, V, k, c);
   for (int j = 0; j < n; ++j) w[j] = o_expf(c[j].x - c[0].x);
+  if (top_p < 1.0f) n = top_p_keep(w, n, top_p);
   int cb0;
   *stop = 0;
   if (aeos >= 0) {

@@ -424,13 +424,17 @@ def test_cb0_sample_bitexact(gpu):
     hazard = torch.rand(S, generator=g) * 0.7
     ctr = torch.randint(0, 100, (S,), generator=g).int()
     u = torch.rand(B, generator=g)
+    # top-p per slot: half the slots keep 1 (no cut), the rest cut at 0.05..0.95 (some sets beyond 64 candidates)
+    topp = torch.where(torch.rand(S, generator=g) < 0.5, torch.ones(S), 0.05 + 0.9 * torch.rand(S, generator=g))
+    topk[slots[40:44]] = 200
     st = [t.clone().to(gpu) for t in (hist, frames, hazard, ctr)]
     cb0 = torch.zeros(B, dtype=torch.long, device=gpu)
     stop = torch.zeros(B, dtype=torch.long, device=gpu)
     codes = torch.zeros(B, 32, dtype=torch.int32, device=gpu)
     ops.cb0_sample(logits.to(gpu), 2048, slots.to(gpu), u.to(gpu), temp_t=temp.to(gpu), topk_t=topk.to(gpu),
                    aeos_bias=bias.to(gpu), rep_t=rep.to(gpu), hist_t=st[0], frames_t=st[1], min_t=min_t.to(gpu),
-                   hazard_t=st[2], ctr_t=st[3], cb0_out=cb0, cb0_i32=codes[:, 0], stop_out=stop)
+                   hazard_t=st[2], ctr_t=st[3], cb0_out=cb0, cb0_i32=codes[:, 0], stop_out=stop,
+                   topp_t=topp.to(gpu))
     bits = bf16_bits(logits)
     for b in range(B):
         s = int(slots[b])
@@ -439,7 +443,7 @@ def test_cb0_sample_bitexact(gpu):
         hz = np.array([hazard[s].item()], np.float32)
         ct = np.array([ctr[s].item()], np.int32)
         c, sp = C.cb0_sample(bits[b], 2048, float(temp[s]), int(topk[s]), float(bias[s]), float(rep[s]), h, fr, 3, hz,
-                             ct, float(u[b]))
+                             ct, float(u[b]), float(topp[s]))
         assert (c, sp) == (cb0[b].item(), stop[b].item()), b
         assert codes[b, 0].item() == c
         assert np.array_equal(st[0][s].cpu().numpy(), h) and st[1][s].item() == fr[0]

@@ -187,7 +187,7 @@ def test_topk_sampler_special_cases():
     assert ranks == sorted(ranks)
 
 
-def _engine_cb0_reference(logits, temp, aeos_bias, rep, hist, frames, min_t, hazard, top_k, aeos=2048):
+def _engine_cb0_reference(logits, temp, aeos_bias, rep, hist, frames, min_t, hazard, top_k, aeos=2048, top_p=None):
     """maya3/engine.py:657-686 in torch (deterministic part): probs, pa, arg, hazard, stop code, q."""
     lg = logits.float() / temp[:, None]
     lg[:, aeos] += aeos_bias
@@ -198,6 +198,10 @@ def _engine_cb0_reference(logits, temp, aeos_bias, rep, hist, frames, min_t, haz
     srt = lg.sort(-1, descending=True).values
     kth = srt.gather(1, (top_k - 1).clamp(0, lg.shape[1] - 1)[:, None])
     lg = lg.masked_fill(lg < kth, -float('inf'))
+    if top_p is not None:  # :669-672
+        sp_, si = lg.softmax(-1).sort(-1, descending=True)
+        drop = (sp_.cumsum(-1) - sp_) > top_p[:, None]
+        lg = lg.masked_fill(torch.zeros_like(drop).scatter(1, si, drop), -float('inf'))
     probs = lg.softmax(-1)
     pa = probs[:, aeos]
     arg = probs.argmax(-1)
@@ -253,3 +257,64 @@ def test_cb0_sample_distribution_excludes_aeos():
     emp = np.bincount(draws, minlength=2049) / draws.size
     tv = 0.5 * np.abs(emp - q[0].double().numpy()).sum()
     assert tv < 0.04 and emp[2048] == 0 and emp[q[0].numpy() == 0].sum() == 0
+
+
+def _distinct_head_logits(g, B, V, n_head=96):
+    """bf16 logits whose n_head largest are distinct multiples of 1/16 in (1, 7] (exact in bf16, no ties for the
+    top-k and top-p sorts) over a body below 1."""
+    body = (torch.randn(B, V, generator=g) * 0.3).clamp(-3, 0.9)
+    for b in range(B):
+        idx = torch.randperm(V, generator=g)[:n_head]
+        body[b, idx] = 7.0 - torch.arange(n_head, dtype=torch.float32) / 16
+    return body.to(torch.bfloat16)
+
+
+def test_cb0_top_p_matches_engine_mask():
+    """The oracle's top-p cut against maya3/engine.py:669-672: with no AEOS class, the codes drawn over a fine
+    grid of uniforms are exactly the engine's kept set, and the stop statistics (pa, hazard, stop code) and the
+    renormalised AEOS-free distribution agree when an AEOS class is present."""
+    g = torch.Generator().manual_seed(11)
+    B, V = 6, 2049
+    logits = _distinct_head_logits(g, B, V)
+    top_p = torch.tensor([0.05, 0.3, 0.5, 0.75, 0.9, 0.99])
+    top_k = torch.full((B,), 64)
+    z = torch.zeros(B)
+    none_hist = torch.full((B, 12), -1)
+    grid = (np.arange(4_000, dtype=np.float32) + 0.5) / 4_000
+    # no AEOS class: compare kept sets (the engine formula with aeos pointing at a class it never keeps)
+    logits_na = logits.clone()
+    logits_na[:, 2048] = -8.0
+    _, _, q = _engine_cb0_reference(logits_na, torch.full((B,), 0.9), z, z, none_hist, torch.zeros(B), torch.zeros(B),
+                                    z, top_k, top_p=top_p)
+    for b in range(B):
+        bits = _bits(logits_na[b])
+        drawn = {C.cb0_sample(bits, -1, 0.9, 64, 0.0, 0.0, None, None, 0, None, None, float(u), float(top_p[b]))[0]
+                 for u in grid}
+        kept = set(torch.nonzero(q[b] > 0).flatten().tolist())
+        assert drawn == kept, (b, sorted(drawn ^ kept))
+        assert len(kept) < 64
+    # top_p = 1 is the plain top-k draw; a tiny top_p keeps the argmax alone
+    bits = _bits(logits[0])
+    for u in (0.0, 0.3, 0.97):
+        assert (C.cb0_sample(bits, -1, 0.9, 64, 0.0, 0.0, None, None, 0, None, None, u, 1.0) ==
+                C.cb0_sample(bits, -1, 0.9, 64, 0.0, 0.0, None, None, 0, None, None, u))
+        assert C.cb0_sample(bits, -1, 0.9, 64, 0.0, 0.0, None, None, 0, None, None, u, 1e-6)[0] == \
+            int(logits[0].float().argmax())
+    # with an AEOS class inside the top-p set: stop code and hazard as the engine computes them on the cut set
+    logits_a = logits.clone()
+    logits_a[:, 2048] = torch.tensor([7.03125, 6.5, 5.0, 6.96875, 1.0, 4.0])  # distinct from the head values
+    frames = torch.full((B,), 5)
+    min_t = torch.full((B,), 4)
+    hazard = torch.full((B,), 0.3)
+    code, hz, q = _engine_cb0_reference(logits_a, torch.full((B,), 0.9), z, z, none_hist, frames, min_t, hazard, top_k,
+                                        top_p=top_p)
+    for b in range(B):
+        fr = np.array([5], np.int64)
+        hzb = np.array([0.3], np.float32)
+        bits = _bits(logits_a[b])
+        _, stop = C.cb0_sample(bits, 2048, 0.9, 64, 0.0, 0.0, None, fr, 4, hzb, None, 0.5, float(top_p[b]))
+        assert stop == code[b].item() and abs(hzb[0] - hz[b].item()) < 1e-5, b
+        drawn = {C.cb0_sample(bits, 2048, 0.9, 64, 0.0, 0.0, None, None, 0, None, None, float(u),
+                              float(top_p[b]))[0] for u in grid}
+        kept = set(torch.nonzero(q[b] > 0).flatten().tolist())
+        assert drawn == kept or (not kept and drawn == {0}), (b, sorted(drawn ^ kept))
