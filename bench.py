@@ -58,6 +58,89 @@ def build_frame(torch, seats, lengths, seed_base=0, backbone=None, depth_model=N
     return fs, bb, dm
 
 
+def secondary(torch, bb, steps):
+    """The backbone-only configurations, timed through the reference surfaces on the frame's backbone weights:
+    C3 = StaticBackbone.step over 64 seats (lengths U[64, 2048]) + cb0; C4 = StaticBackbone.step_mixed with 216
+    decoding seats (lengths log-uniform in [128, 4096)) and 8 inline prefills of 256 tokens (embedding rows of
+    uniform ids from a [151936, 1024] N(0, 0.02) table, starting at length 0) = 2264 rows + cb0 over the 224
+    seats. Lengths are reset before every step, so each timed step does the same work."""
+    from m3x import roofline, synth
+    from m3x.cb0 import Cb0Sampler
+    from m3x.serve.fast_backbone import StaticBackbone
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(300)
+    out = {}
+
+    def run(label, sb, base, step, rows, attended, note):
+        def reset():
+            sb.lengths[:len(base)].copy_(base.to(dev), non_blocking=True)
+            sb.lengths_cpu[:len(base)] = base.tolist()
+        for _ in range(2):
+            reset()
+            step()
+        torch.cuda.synchronize()
+        t = 0.0
+        for _ in range(steps):
+            reset()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            step()
+            torch.cuda.synchronize()
+            t += time.perf_counter() - t0
+        ms = t * 1e3 / steps
+        byt = roofline.backbone_step_bytes(attended, rows)
+        flo = roofline.backbone_step_flops(attended, rows)
+        out[label] = {"rows": rows, "ms_per_step": round(ms, 3), "bytes_algorithmic": byt, "flops_algorithmic": flo,
+                      "hbm_fraction": round(byt / (ms * 1e-3) / 1e9 / roofline.HBM_PEAK_GBS, 4),
+                      "mfma_fraction": round(flo / (ms * 1e-3) / 1e12 / roofline.MFMA_BF16_TFLOPS, 4), "note": note}
+        log(f"{label}: {rows} rows, {ms:.3f} ms/step ({out[label]['hbm_fraction']:.1%} of the HBM and "
+            f"{out[label]['mfma_fraction']:.1%} of the MFMA roofline)")
+
+    # C3
+    B3 = 64
+    sb = StaticBackbone(bb, B3, capacity=CAP, batch_buckets=(B3,), ctx_buckets=(CAP,), attention="triton",
+                        fuse_rope=True)
+    for i in range(len(sb.layers)):
+        sb.k[i].normal_(generator=g)
+        sb.v[i].normal_(generator=g)
+    cb = Cb0Sampler(bb.cb0_head.weight, B3, temp=0.9, top_k=50, rep=0.0)
+    len3 = synth.c3_lengths(B3)
+    x3 = torch.randn(B3, 1024, device=dev, generator=g).to(torch.bfloat16)
+    idx3 = torch.arange(B3, device=dev)
+    slots3 = list(range(B3))
+    run("c3", sb, len3, lambda: cb(sb.step(slots3, x3), idx3), B3, int(len3.sum()) + B3,
+        "StaticBackbone.step (host staging + one graph replay + clone) + eager cb0 (head GEMM, Philox, sampler)")
+    del sb, cb
+    torch.cuda.empty_cache()
+
+    # C4
+    nd, npf, T = 216, 8, 256
+    sb = StaticBackbone(bb, nd + npf, capacity=CAP, batch_buckets=(nd + npf * T,), ctx_buckets=(CAP,),
+                        attention="triton", fuse_rope=True)
+    for i in range(len(sb.layers)):
+        sb.k[i].normal_(generator=g)
+        sb.v[i].normal_(generator=g)
+    cb = Cb0Sampler(bb.cb0_head.weight, nd + npf, temp=0.9, top_k=50, rep=0.0)
+    len4 = torch.cat([synth.c4_decode_lengths(nd), torch.zeros(npf, dtype=torch.long)])
+    x4 = torch.randn(nd, 1024, device=dev, generator=g).to(torch.bfloat16)
+    table = (torch.randn(151936, 1024, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    ids = torch.randint(0, 151936, (npf, T), device=dev, generator=g)
+    pre = [(nd + j, table[ids[j]]) for j in range(npf)]
+    del table
+    idx4 = torch.arange(nd + npf, device=dev)
+    slots4 = list(range(nd))
+
+    def c4_step():
+        dec, last = sb.step_mixed(slots4, x4, pre)
+        return cb(torch.cat([dec, torch.stack(last)]), idx4)
+    run("c4", sb, len4, c4_step, nd + npf * T, int(len4[:nd].sum()) + nd + npf * T,
+        "StaticBackbone.step_mixed (216 decode + 8 x 256 prefill rows, one graph replay) + eager cb0 over 224 "
+        "seats; algorithmic bytes read each prefill key once")
+    del sb, cb, pre
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(torch, seconds, seats=2):
     """The oracle's eager frame (backbone gather path + cb0 + depth) on the host cores, C5 shapes, `seats` seats."""
     from m3x import synth
@@ -119,6 +202,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-b1", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true", help="skip the C3 / C4 backbone-step lines")
+    ap.add_argument("--secondary-steps", type=int, default=5)
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -250,6 +335,9 @@ def main():
             b1_us = lat[len(lat) // 2]
             log(f"B=1: median {b1_us:.0f} us over {len(lat)} replays")
             del fs1, g1
+        sec = None
+        if not args.no_secondary:
+            sec = secondary(torch, bb, args.secondary_steps)
         del bb, dm
         torch.cuda.empty_cache()
 
@@ -288,6 +376,7 @@ def main():
                      "launch_us": round(attn_us, 2), "bytes_per_launch": attn_bytes},
         "norm_roofline": {"kernel": "add_rms (residual add + RMSNorm, hidden 1024)", "bound": "hbm", "unit": "GB/s",
                           "peak": roofline.HBM_PEAK_GBS, **norm},
+        "backbone_configs": sec,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -37,6 +37,13 @@ def backbone_step_bytes(attended, rows, layers=28, hidden=1024, heads=16, kv_hea
             rows * hidden * 2 * 2 + v0 * hidden * 2)
 
 
+def backbone_step_flops(attended, rows, layers=28, hidden=1024, heads=16, kv_heads=8, head_dim=128, inter=3072,
+                        v0=2048):
+    """Projections (2 flops per weight per row), the cb0 head, and QK + PV over every attended key of every layer."""
+    params = backbone_weight_bytes(layers, hidden, heads, kv_heads, head_dim, inter) // 2
+    return 2 * rows * params + 2 * rows * hidden * v0 + layers * decode_attn_flops(attended, heads, head_dim)
+
+
 def depth_frame_bytes(d=1024, ffn=2816, layers=4, n_codes=2048, n_q=32, d_backbone=1024, seats=1):
     trunk = layers * (3 * d * d + d * d + 3 * ffn * d) * 2
     head = n_codes * d * 2
