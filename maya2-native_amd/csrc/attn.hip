@@ -17,6 +17,8 @@
 // decode_attn_combine folds them in split order (deterministic).
 #include "m3x_common.h"
 
+#include <algorithm>
+
 // K rows through a wave-private LDS tile (coalesced loads; bit-identical results): 1-2 % faster at 224 rows and
 // 7 % at one row than loading the MFMA A layout straight from memory (KL = 0).
 #ifndef M3X_ATTN_KL
@@ -228,6 +230,235 @@ __global__ __launch_bounds__(256, M3X_ATTN_MINB) void decode_attn_kernel(
   }
 }
 
+// One item of attn_block_kernel: rows row .. row + nb - 1, kv head kh, keys [kstart, kend) of split `split`.
+template <int G>
+__device__ __forceinline__ void attn_block_item(
+    const uint16_t* __restrict__ q, long sq_b, long sq_h, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, long sk_s, long sk_h, long sk_t, uint16_t* __restrict__ out, long so_b,
+    long so_h, const int64_t* __restrict__ slots, const int32_t* __restrict__ pos, float scale_log2, int chunk,
+    float* __restrict__ part, int max_splits, int cap, int row, int nb, int kh, int KV, int split, int kstart,
+    int kend, unsigned char* lds) {
+  constexpr int KT_LD = 136;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int li = lane & 15;  // query vector (column) of S^T: block row li / G, head li % G
+  const int lg = lane >> 4;
+  const int jq = li / G;
+  const bool qlive = jq < nb;
+  const int pq = qlive ? min(pos[row + jq], cap - 1) : -1;  // the vector's own position: it sees keys <= pq
+
+  const long slot = slots[row];
+  const uint16_t* kbase = kc + slot * sk_s + (long)kh * sk_h;
+  const uint16_t* vbase = vc + slot * sk_s + (long)kh * sk_h;
+  u16x8 qop[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    if (qlive) {
+      qop[kk] = ld16(q + (long)(row + jq) * sq_b + (long)(kh * G + li % G) * sq_h + 32 * kk + 8 * lg);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qop[kk].v[e] = 0;
+    }
+  }
+  float m_run = -INFINITY, l_run = 0.f;  // of vector li, equal across the 4 lanes of one li
+  f32x4_t acc[8];
+#pragma unroll
+  for (int T = 0; T < 8; ++T) acc[T] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  uint16_t* kt = reinterpret_cast<uint16_t*>(lds) + wave * 32 * KT_LD;
+  for (int k0 = kstart + 32 * wave; k0 < kend; k0 += 128) {
+    u16x8 kld[8], vld[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      kld[e] = kv_load(kbase + (long)(k0 + 16 * (e >> 2) + 4 * lg + (e & 3)) * sk_t + 8 * li);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vld[e] = kv_load(vbase + (long)(k0 + 16 * (e >> 2) + 4 * lg + (e & 3)) * sk_t + 8 * li);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) st16(kt + (16 * (e >> 2) + 4 * lg + (e & 3)) * KT_LD + 8 * li, kld[e]);
+    u16x8 kop[2][4];
+#pragma unroll
+    for (int g2 = 0; g2 < 2; ++g2)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+        kop[g2][kk] = *reinterpret_cast<const u16x8*>(kt + (16 * g2 + li) * KT_LD + 32 * kk + 8 * lg);
+    f32x4_t s[2];
+#pragma unroll
+    for (int g2 = 0; g2 < 2; ++g2) {
+      s[g2] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) s[g2] = mfma16x16x32<M3X_BF16>(kop[g2][kk], qop[kk], s[g2]);
+    }
+    // mask: keys past the split or the block, and keys after the vector's own position (causal); dead vectors
+    // see nothing
+    const int klim = min(kend - 1, pq);
+    float sv[8];
+#pragma unroll
+    for (int g2 = 0; g2 < 2; ++g2)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = k0 + 16 * g2 + 4 * lg + r;
+        sv[4 * g2 + r] = (qlive && key <= klim) ? s[g2][r] * scale_log2 : -INFINITY;
+      }
+    float tmax = sv[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) tmax = fmaxf(tmax, sv[e]);
+    tmax = xor32_max(xor16_max(tmax));
+    const float m_new = fmaxf(m_run, tmax);
+    // a vector with no visible key yet keeps m = -inf: its weights are 0 and its rescale 1
+    const float alpha = m_new == -INFINITY ? 1.f : exp2f(m_run - m_new);
+    float p[8], psum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      p[e] = sv[e] == -INFINITY ? 0.f : exp2f(sv[e] - m_new);
+      psum += p[e];
+    }
+    psum = xor32_sum(xor16_sum(psum));
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+    // O rows are vectors 4 * lg + r: their rescale comes from lane 4 * lg + r
+    float al[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) al[r] = __shfl(alpha, 4 * lg + r, 64);
+#pragma unroll
+    for (int T = 0; T < 8; ++T)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[T][r] *= al[r];
+    u16x8 pop;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pop.v[e] = f2bf(p[e]);
+    if (k0 + 32 > kend) {  // zero V rows past the block's context in the tail tile
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int key = k0 + 16 * (e >> 2) + 4 * lg + (e & 3);
+        if (key >= kend) {
+#pragma unroll
+          for (int x = 0; x < 8; ++x) vld[e].v[x] = 0;
+        }
+      }
+    }
+#pragma unroll
+    for (int T = 0; T < 8; ++T) {
+      u16x8 vop;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vop.v[e] = vld[e].v[T];
+      acc[T] = mfma16x16x32<M3X_BF16>(pop, vop, acc[T]);
+    }
+  }
+
+  // ---- merge the 4 waves (the K tiles are dead after the barrier)
+  __syncthreads();
+  float* lo = reinterpret_cast<float*>(lds);  // [4][16][AD]
+  float* lm = lo + 4 * 16 * AD;               // [4][16]
+  float* ll = lm + 4 * 16;                    // [4][16]
+#pragma unroll
+  for (int T = 0; T < 8; ++T)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) lo[(wave * 16 + 4 * lg + r) * AD + 8 * li + T] = acc[T][r];
+  if (lg == 0) {
+    lm[wave * 16 + li] = m_run;
+    ll[wave * 16 + li] = l_run;
+  }
+  __syncthreads();
+  // thread t: vector t / 16, dims 8 * (t % 16) .. + 7
+  const int vq = threadIdx.x >> 4;
+  const int d0 = 8 * (threadIdx.x & 15);
+  const int j = vq / G, h = vq % G;
+  if (j >= nb) return;
+  const int pj = min(pos[row + j], cap - 1);
+  const int nsplit = min((pj + chunk) / chunk, max_splits);
+  if (split >= nsplit) return;  // this row has no keys in this split (the caller's barrier follows)
+  float M = lm[vq];
+#pragma unroll
+  for (int w = 1; w < 4; ++w) M = fmaxf(M, lm[w * 16 + vq]);
+  float f[4], L = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    f[w] = exp2f(lm[w * 16 + vq] - M);  // 0 for a wave that saw no visible key (m = -inf)
+    L += ll[w * 16 + vq] * f[w];
+  }
+  float O[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    O[e] = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) O[e] += lo[(w * 16 + vq) * AD + d0 + e] * f[w];
+  }
+  if (nsplit == 1) {
+    u16x8 ov;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ov.v[e] = f2bf(O[e] / L);
+    st16(out + (long)(row + j) * so_b + (long)(kh * G + h) * so_h + d0, ov);
+  } else {
+    float* pp = part + (((long)(row + j) * KV + kh) * max_splits + split) * PART_STRIDE;
+    if (d0 == 0) {
+      pp[h] = M;
+      pp[2 + h] = L;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pp[8 + h * AD + d0 + e] = O[e];
+  }
+}
+
+// Steps that hold inline prefill rows (serve/fast_backbone.py:326-359). The rows of one prefill are one slot at
+// consecutive positions, and the caller groups them into items of up to QB = 16 / G rows (a decode row is an item
+// of one row): items[0] = the item count n, items[1 + i] = 32 * (first row) + (rows of item i). One workgroup
+// takes an item: its 16 query vectors (row j, head h), column j * G + h, fill all 16 columns of the MFMA query
+// operand, so a prefill costs one pass over its slot's keys per QB rows instead of one per row. Same tile
+// pipeline as decode_attn_kernel (K through the wave-private LDS tile, V in registers, S^T = K . Q^T,
+// O += P . V) and the same arithmetic per query vector, so every row gets the bits decode_attn_kernel would give
+// it; the differences are the causal mask (vector j sees keys <= pos[row + j]) and the per-vector rescale (O rows
+// are vectors 4 * lg + r, whose running max lives in lane 4 * lg + r). Rows whose context spans several splits
+// write partials for decode_attn_combine_kernel.
+// The grid is one workgroup per bin per (kv head, split) plane, ~3 workgroups per CU whatever the item count (a
+// workgroup launched only to exit costs a CU slot for microseconds). The caller deals the items into the bins
+// (longest processing time first balances them) and lists them bin by bin:
+//   items = [bins, start[0], ..., start[bins], code[0], code[1], ...], bin b = codes start[b] .. start[b + 1] - 1,
+// each code = 32 * (first row) + (rows of the item).
+template <int G>
+__global__ __launch_bounds__(256, 2) void attn_block_kernel(
+    const uint16_t* __restrict__ q, long sq_b, long sq_h, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, long sk_s, long sk_h, long sk_t, uint16_t* __restrict__ out, long so_b,
+    long so_h, const int64_t* __restrict__ slots, const int32_t* __restrict__ pos, float scale_log2, int chunk,
+    float* __restrict__ part, int max_splits, int cap, const int32_t* __restrict__ items, int rows) {
+  constexpr int QB = 16 / G;
+  const int kh = blockIdx.y;
+  const int split = blockIdx.z;
+  const int KV = gridDim.y;
+  const int bins = items[0];
+  if ((int)blockIdx.x >= bins || bins > rows) return;  // an item list sized for another grid does nothing
+  const int i0 = max(items[1 + blockIdx.x], 0), i1 = min(items[2 + blockIdx.x], rows);
+  const int32_t* codes = items + 2 + bins;
+  // LDS: the wave-private K tiles during the key loop, then the wave merge (after a barrier)
+  constexpr int KTILE_BYTES = 4 * 32 * 136 * 2;
+  constexpr int MERGE_BYTES = (4 * 16 * AD + 2 * 4 * 16) * 4;
+  __shared__ __align__(16) unsigned char lds[KTILE_BYTES > MERGE_BYTES ? KTILE_BYTES : MERGE_BYTES];
+  for (int it = i0; it < i1; ++it) {
+    const int code = codes[it];
+    const int row = code >> 5;
+    if (row < 0 || row >= rows) continue;
+    const int nb = min(min(code & 31, QB), rows - row);
+    if (nb <= 0) continue;
+    int plast = 0;
+    for (int j = 0; j < nb; ++j) plast = max(plast, min(pos[row + j], cap - 1));
+    const int kstart = split * chunk;
+    if (kstart > plast) continue;  // past the item's context (uniform per workgroup)
+    const int kend = min(kstart + chunk, plast + 1);
+    attn_block_item<G>(q, sq_b, sq_h, kc, vc, sk_s, sk_h, sk_t, out, so_b, so_h, slots, pos, scale_log2, chunk, part,
+                       max_splits, cap, row, nb, kh, KV, split, kstart, kend, lds);
+    __syncthreads();  // the next item's K tiles reuse the merge area
+  }
+}
+
+// Bins of an item launch: ~3 workgroups per CU over the (kv head, split) planes, at most one per row.
+static int attn_item_bins(int rows, int kv_heads, int max_splits) {
+  return std::max(1, std::min(rows, 768 / (kv_heads * max_splits)));
+}
+
+M3X_API int m3x_decode_attn_item_bins(int rows, int kv_heads, int max_ctx, int chunk) {
+  if (rows <= 0 || kv_heads <= 0 || max_ctx <= 0 || chunk <= 0) return 0;
+  return attn_item_bins(rows, kv_heads, (max_ctx + chunk - 1) / chunk);
+}
+
 template <int G>
 __global__ __launch_bounds__(256) void decode_attn_combine_kernel(uint16_t* __restrict__ out, long so_b, long so_h,
                                                                   const int32_t* __restrict__ pos, int chunk,
@@ -283,11 +514,12 @@ M3X_API size_t m3x_decode_attn_workspace(int rows, int kv_heads, int max_ctx, in
 
 // max_ctx: an upper bound on pos[r] + 1 for every row (the caller's context bucket); it sizes the grid.
 // chunk: keys per split, a multiple of 128. cap (the cache's per-slot capacity) must be a multiple of 32 so the
-// last 32-key tile of a row stays inside its slot.
+// last 32-key tile of a row stays inside its slot. items (nullable): the step's work items (attn_block_kernel);
+// with it, one launch of attn_block_kernel attends every row, the rows of an inline prefill QB at a time.
 M3X_API int m3x_decode_attn(const void* q, long sq_b, long sq_h, const void* k_cache, const void* v_cache, long sk_s,
                             long sk_h, long sk_t, int cap, void* out, long so_b, long so_h, const int64_t* slots,
-                            const int32_t* pos, float scale, int rows, int heads, int kv_heads, int head_dim,
-                            int max_ctx, int chunk, void* workspace, size_t ws_bytes, void* stream) {
+                            const int32_t* pos, const int32_t* items, float scale, int rows, int heads, int kv_heads,
+                            int head_dim, int max_ctx, int chunk, void* workspace, size_t ws_bytes, void* stream) {
   if (rows < 0 || heads <= 0 || kv_heads <= 0 || max_ctx <= 0) return M3X_EINVAL;
   if (rows == 0) return M3X_OK;
   if (!q || !k_cache || !v_cache || !out || !slots || !pos) return M3X_ENULL;
@@ -297,6 +529,7 @@ M3X_API int m3x_decode_attn(const void* q, long sq_b, long sq_h, const void* k_c
   if (chunk <= 0 || chunk % 128 || cap % 32 || max_ctx > cap) return M3X_EINVAL;
   if ((sq_b | sq_h | sk_s | sk_h | sk_t) & 7) return M3X_EINVAL;
   if (!m3x_aligned16(q) || !m3x_aligned16(k_cache) || !m3x_aligned16(v_cache)) return M3X_EINVAL;
+  if (items && (((so_b | so_h) & 7) || !m3x_aligned16(out))) return M3X_EINVAL;  // item rows store 16 bytes
   const int max_splits = (max_ctx + chunk - 1) / chunk;
   if (max_splits > 1) {
     if (!workspace) return M3X_ENULL;
@@ -306,21 +539,25 @@ M3X_API int m3x_decode_attn(const void* q, long sq_b, long sq_h, const void* k_c
   const float scale_log2 = scale * 1.44269504088896341f;
   if (rows > 65535 * 64 || kv_heads > 65535) return M3X_EINVAL;
   dim3 grid(rows, kv_heads, max_splits);
+  const dim3 igrid(attn_item_bins(rows, kv_heads, max_splits), kv_heads, max_splits);
+#define M3X_ATTN_LAUNCH(GG)                                                                                          \
+  if (items)                                                                                                         \
+    hipLaunchKernelGGL((attn_block_kernel<GG>), igrid, dim3(256), 0, st, (const uint16_t*)q, sq_b, sq_h,            \
+                       (const uint16_t*)k_cache, (const uint16_t*)v_cache, sk_s, sk_h, sk_t, (uint16_t*)out, so_b,   \
+                       so_h, slots, pos, scale_log2, chunk, (float*)workspace, max_splits, cap, items, rows);       \
+  else                                                                                                               \
+    hipLaunchKernelGGL((decode_attn_kernel<GG, M3X_ATTN_KL>), grid, dim3(256), 0, st, (const uint16_t*)q, sq_b,     \
+                       sq_h, (const uint16_t*)k_cache, (const uint16_t*)v_cache, sk_s, sk_h, sk_t, (uint16_t*)out,   \
+                       so_b, so_h, slots, pos, scale_log2, chunk, (float*)workspace, max_splits, cap);              \
+  if (max_splits > 1)                                                                                                \
+    hipLaunchKernelGGL(decode_attn_combine_kernel<GG>, dim3(rows, kv_heads), dim3(256), 0, st, (uint16_t*)out, so_b, \
+                       so_h, pos, chunk, (const float*)workspace, max_splits, cap)
   if (G == 2) {
-    hipLaunchKernelGGL((decode_attn_kernel<2, M3X_ATTN_KL>), grid, dim3(256), 0, st, (const uint16_t*)q, sq_b, sq_h,
-                       (const uint16_t*)k_cache, (const uint16_t*)v_cache, sk_s, sk_h, sk_t, (uint16_t*)out, so_b, so_h,
-                       slots, pos, scale_log2, chunk, (float*)workspace, max_splits, cap);
-    if (max_splits > 1)
-      hipLaunchKernelGGL(decode_attn_combine_kernel<2>, dim3(rows, kv_heads), dim3(256), 0, st, (uint16_t*)out, so_b,
-                         so_h, pos, chunk, (const float*)workspace, max_splits, cap);
+    M3X_ATTN_LAUNCH(2);
   } else {
-    hipLaunchKernelGGL((decode_attn_kernel<1, M3X_ATTN_KL>), grid, dim3(256), 0, st, (const uint16_t*)q, sq_b, sq_h,
-                       (const uint16_t*)k_cache, (const uint16_t*)v_cache, sk_s, sk_h, sk_t, (uint16_t*)out, so_b, so_h,
-                       slots, pos, scale_log2, chunk, (float*)workspace, max_splits, cap);
-    if (max_splits > 1)
-      hipLaunchKernelGGL(decode_attn_combine_kernel<1>, dim3(rows, kv_heads), dim3(256), 0, st, (uint16_t*)out, so_b,
-                         so_h, pos, chunk, (const float*)workspace, max_splits, cap);
+    M3X_ATTN_LAUNCH(1);
   }
+#undef M3X_ATTN_LAUNCH
   M3X_CHECK_LAUNCH();
   return M3X_OK;
 }

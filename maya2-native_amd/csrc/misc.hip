@@ -120,4 +120,4 @@ M3X_API int m3x_ctr_add(int32_t* ctr, const int64_t* slots, int B, void* stream)
 }
 
 // The library's version, so a host binding can check it loaded the build it expects.
-M3X_API int m3x_version(void) { return 4; }
+M3X_API int m3x_version(void) { return 5; }

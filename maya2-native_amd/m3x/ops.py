@@ -9,6 +9,10 @@ from __future__ import annotations
 
 import ctypes
 
+import heapq
+
+import numpy as np
+
 import torch
 
 from ._lib import check, lib
@@ -101,16 +105,62 @@ def decode_attn_workspace(rows, kv_heads, max_ctx, chunk) -> int:
     return int(lib().m3x_decode_attn_workspace(rows, kv_heads, max_ctx, chunk))
 
 
-def decode_attn(q, k_cache, v_cache, out, slots, pos, scale, max_ctx, chunk, workspace, heads, kv_heads):
-    """q, out: [rows, heads, D] (any row/head strides, contiguous D); caches [slots, kv_heads, cap, D]."""
-    _dev(q, k_cache, v_cache, out, slots, pos, workspace)
+def decode_attn(q, k_cache, v_cache, out, slots, pos, scale, max_ctx, chunk, workspace, heads, kv_heads,
+                items=None):
+    """q, out: [rows, heads, D] (any row/head strides, contiguous D); caches [slots, kv_heads, cap, D].
+    items (int32, optional): the step's work items (attn_items with attn_item_bins bins); the rows of an inline
+    prefill then share one pass over their slot's keys per 16 // (heads // kv_heads) rows."""
+    _dev(q, k_cache, v_cache, out, slots, pos, workspace, items)
     rows = q.shape[0]
+    if items is not None:
+        bins = attn_item_bins(rows, kv_heads, max_ctx, chunk)
+        if items.dtype != torch.int32 or not items.is_contiguous() or items.numel() < 2 + bins:
+            raise ValueError(f"decode_attn: items must be contiguous int32 with {bins} bins (attn_items)")
     ws = 0 if workspace is None else workspace.numel() * workspace.element_size()
     check(lib().m3x_decode_attn(
         _p(q), q.stride(0), q.stride(1), _p(k_cache), _p(v_cache), k_cache.stride(0), k_cache.stride(1),
-        k_cache.stride(2), k_cache.shape[2], _p(out), out.stride(0), out.stride(1), _p(slots), _p(pos), float(scale),
-        rows, heads, kv_heads, k_cache.shape[-1], int(max_ctx), int(chunk), _p(workspace), ws, _stream()),
-        "decode_attn")
+        k_cache.stride(2), k_cache.shape[2], _p(out), out.stride(0), out.stride(1), _p(slots), _p(pos), _p(items),
+        float(scale), rows, heads, kv_heads, k_cache.shape[-1], int(max_ctx), int(chunk), _p(workspace), ws,
+        _stream()), "decode_attn")
+
+
+def attn_item_bins(rows, kv_heads, max_ctx, chunk) -> int:
+    return int(lib().m3x_decode_attn_item_bins(rows, kv_heads, max_ctx, chunk))
+
+
+def attn_items(runs, heads, kv_heads, bins):
+    """Work items of decode_attn for rows laid out as runs: (first row, rows, first position) per run, a decode
+    row being a run of one row and an inline prefill of T tokens a run of T rows at consecutive positions of one
+    slot. Each run is cut into items of up to 16 // (heads // kv_heads) rows, and the items are dealt into `bins`
+    bins (attn_item_bins) longest processing time first: each goes to the least loaded bin, its cost its context
+    length plus a fixed 64 keys. Returns int32 [bins, start[0..bins], codes bin by bin], code =
+    32 * first_row + rows."""
+    qb = 16 // (heads // kv_heads)
+    costs, codes = [], []
+    for r0, n, p0 in runs:
+        if n == 1:
+            costs.append(p0 + 65)
+            codes.append(32 * r0 + 1)
+            continue
+        for s in range(0, n, qb):
+            m = min(qb, n - s)
+            costs.append(p0 + s + m + 64)
+            codes.append(32 * (r0 + s) + m)
+    order = np.argsort(-np.asarray(costs, dtype=np.int64), kind="stable").tolist()
+    k = min(bins, len(order))
+    per = [[codes[i]] for i in order[:k]] + [[] for _ in range(bins - k)]
+    heap = [(costs[i], b) for b, i in enumerate(order[:k])]
+    heapq.heapify(heap)
+    for i in order[k:]:
+        load, b = heap[0]
+        per[b].append(codes[i])
+        heapq.heapreplace(heap, (load + costs[i], b))
+    out = np.empty(2 + bins + len(codes), dtype=np.int32)
+    out[0] = bins
+    out[1] = 0
+    np.cumsum([len(p) for p in per], out=out[2:2 + bins])
+    out[2 + bins:] = [c for p in per for c in p]
+    return out
 
 
 class PackedWeight:

@@ -37,7 +37,7 @@ def attn_chunk(rows: int, kv_heads: int, ctx: int) -> int:
 
 class _Graph:
     __slots__ = ('graph', 'slots', 'slots_cpu', 'x', 'real', 'real_cpu', 'out', 'last', 'offset', 'offset_cpu',
-                 'offset_dirty', 'evt', 'bufs')
+                 'offset_dirty', 'evt', 'bufs', 'items_cpu')
 
 
 class StaticBackbone:
@@ -153,14 +153,17 @@ class StaticBackbone:
         self.lengths_cpu[slot] = length
 
     # ---------------------------------------------------------------- math
-    def make_buffers(self, rows, ctx):
-        """Static buffers of one (row bucket, context bucket) step; reused by every replay of its graph."""
+    def make_buffers(self, rows, ctx, mixed=False):
+        """Static buffers of one (row bucket, context bucket) step; reused by every replay of its graph.
+        mixed: the step may hold inline prefill rows (step_mixed), whose attention runs in blocks of consecutive
+        rows; a decode-only step (step, the frame step) leaves that launch out."""
         dev, dt = self.device, self.dtype
         H, KV, D, hid, I = self.heads, self.kv_heads, self.head_dim, self.hidden, self.inter
-        b = SimpleNamespace(rows=rows, ctx=ctx)
+        b = SimpleNamespace(rows=rows, ctx=ctx, mixed=mixed)
         b.slots = torch.full((rows,), self.dummy, dtype=torch.long, device=dev)
         b.real = torch.zeros(rows, dtype=torch.long, device=dev)
         b.offset = torch.zeros(rows, dtype=torch.long, device=dev)
+        b.items = None
         b.pos = torch.zeros(rows, dtype=torch.int32, device=dev)
         b.x = torch.zeros(rows, hid, dtype=dt, device=dev)
         b.h = torch.empty(rows, hid, dtype=dt, device=dev)
@@ -173,6 +176,13 @@ class StaticBackbone:
         b.pend = torch.empty(rows, hid, dtype=dt, device=dev)
         b.out = torch.empty(rows, hid, dtype=dt, device=dev)
         b.chunk = attn_chunk(rows, KV, ctx)
+        if mixed:
+            # attention work items of a mixed step (ops.attn_items): prefill rows attended 16 // G at a time; until
+            # a step stages its own, every row is an item of its own
+            b.item_bins = ops.attn_item_bins(rows, KV, ctx, b.chunk)
+            items = ops.attn_items([(r, 1, 0) for r in range(rows)], H, KV, b.item_bins)
+            b.items = torch.zeros(2 + b.item_bins + rows, dtype=torch.int32, device=dev)
+            b.items[:len(items)] = torch.from_numpy(items)
         ws = ops.decode_attn_workspace(rows, KV, ctx, b.chunk)
         b.attn_ws = torch.empty(max(ws, 16) // 4, dtype=torch.float32, device=dev)
         return b
@@ -193,7 +203,7 @@ class StaticBackbone:
             ops.qk_norm_rope_cache(b.qkv, b.q, self.k[i], self.v[i], b.slots, b.pos, self.cos, self.sin,
                                    attn.q_norm.weight, attn.k_norm.weight, eps, H, KV)
             ops.decode_attn(b.q, self.k[i], self.v[i], o3, b.slots, b.pos, self.scaling, b.ctx, b.chunk, b.attn_ws,
-                            H, KV)
+                            H, KV, items=b.items)
             ops.linear(b.o, self.po[i], b.a)
             ops.add_rms(b.x if i == 0 else b.h, b.a, layer.post_attention_layernorm.weight, eps, h_out=b.h, y=b.y)
             ops.linear_act(b.y, self.pgate[i], self.pup[i], ops.ACT_SWIGLU, b.act)
@@ -210,14 +220,15 @@ class StaticBackbone:
         raise ValueError(f'{what} {need} exceeds largest bucket {values[-1]}')
 
     @torch.inference_mode()
-    def _capture(self, bb, cb):
+    def _capture(self, bb, cb, mixed=False):
         g = _Graph()
-        g.bufs = self.make_buffers(bb, cb)
+        g.bufs = self.make_buffers(bb, cb, mixed)
         g.slots, g.real, g.offset, g.x = g.bufs.slots, g.bufs.real, g.bufs.offset, g.bufs.x
         g.offset_cpu = torch.zeros(bb, dtype=torch.long, pin_memory=True)
         g.offset_dirty = False
         g.slots_cpu = torch.full((bb,), self.dummy, dtype=torch.long, pin_memory=True)
         g.real_cpu = torch.zeros(bb, dtype=torch.long, pin_memory=True)
+        g.items_cpu = torch.zeros_like(g.bufs.items, device='cpu').pin_memory() if mixed else None
         g.last = None
         g.graph = None
         g.evt = None
@@ -234,17 +245,21 @@ class StaticBackbone:
             g.graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g.graph, pool=self.pool):
                 self.forward(g.bufs)
-        self.graphs[bb, cb] = g
+        self.graphs[(bb, cb, 'mixed') if mixed else (bb, cb)] = g
         return g
 
     @torch.inference_mode()
-    def warmup(self, batch_buckets=None, ctx_buckets=None):
+    def warmup(self, batch_buckets=None, ctx_buckets=None, mixed=False):
+        """Captures the decode graphs of the buckets (and with mixed=True also the graphs step_mixed uses for steps
+        with inline prefills; otherwise those are captured on their first use)."""
         # largest first so later (smaller) captures reuse the shared pool's blocks
         for bb in sorted(batch_buckets or self.batch_buckets, reverse=True):
             for cb in sorted(ctx_buckets or self.ctx_buckets, reverse=True):
                 cb = min(cb, self.capacity)
                 if (bb, cb) not in self.graphs:
                     self._capture(bb, cb)
+                if mixed and (bb, cb, 'mixed') not in self.graphs:
+                    self._capture(bb, cb, True)
         torch.cuda.synchronize()
 
     def _run(self, g):
@@ -319,7 +334,8 @@ class StaticBackbone:
             raise ValueError(f'context {need} exceeds capacity {self.capacity}')
         bb = self._bucket(self.batch_buckets, rows, 'batch')
         cb = self._bucket(self.ctx_buckets, need, 'context')
-        g = self.graphs.get((bb, cb)) or self._capture(bb, cb)
+        key = (bb, cb, 'mixed') if prefills else (bb, cb)
+        g = self.graphs.get(key) or self._capture(bb, cb, bool(prefills))
         if g.evt is not None:
             g.evt.synchronize()
         index = list(slots)
@@ -336,6 +352,16 @@ class StaticBackbone:
         g.slots.copy_(g.slots_cpu, non_blocking=True)
         g.real.copy_(g.real_cpu, non_blocking=True)
         g.offset.copy_(g.offset_cpu, non_blocking=True)
+        if g.items_cpu is not None:
+            runs = [(i, 1, self.lengths_cpu[s]) for i, s in enumerate(slots)]
+            at = B
+            for s, t in prefills:
+                runs.append((at, t.shape[0], self.lengths_cpu[s]))
+                at += t.shape[0]
+            runs += [(r, 1, 0) for r in range(rows, bb)]  # padding rows on the dummy slot
+            items = ops.attn_items(runs, self.heads, self.kv_heads, g.bufs.item_bins)
+            g.items_cpu[:len(items)] = torch.from_numpy(items)
+            g.bufs.items.copy_(g.items_cpu, non_blocking=True)
         g.last = None
         g.offset_dirty = bool(prefills)
         g.evt = torch.cuda.Event()

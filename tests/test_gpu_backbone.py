@@ -81,6 +81,12 @@ def test_step_mixed_prefill_matches_oracle(gpu):
     ok, info = floor_check(torch.cat([dec, torch.stack(last)]), ref[[0, 1, 21, 28]], truth[[0, 1, 21, 28]])
     assert ok, info
     assert sb.lengths_cpu[:S] == [1, 8, 37, 201, 300, 20] == lengths[:S].tolist()
+    # every prefill row's attention shows in the next layer's K/V writes at its position
+    for i in range(1, LAYERS):
+        for s, n0, n in ((5, 0, 20), (1, 1, 8)):
+            for name, got, rf, tr in (("k", sb.k[i], kc[i], T["kc"][i]), ("v", sb.v[i], vc[i], T["vc"][i])):
+                ok, info = floor_check(got[s, :, n0:n], rf[s, :, n0:n], tr[s, :, n0:n])
+                assert ok, (name, i, s, info)
     # the next decode step of the prefilled slot continues from its new length
     y = torch.randn(1, 1024, generator=g).to(torch.bfloat16)
     out = sb.step([5], y.to(gpu))

@@ -234,6 +234,56 @@ def test_decode_attn(gpu, heads, kv, chunk, CAP):
     assert ok, info
 
 
+@pytest.mark.parametrize("heads,kv,chunk", [(16, 8, 2048), (16, 8, 128), (8, 8, 256), (16, 8, 1024)])
+def test_prefill_items_match_decode_rows(gpu, heads, kv, chunk):
+    """Inline prefill rows attended as items (16 query vectors per pass over their slot's keys, one persistent
+    grid walking the items) give exactly the bits of attending each row alone, and match the fp32 reference.
+    Runs cover full items, a partial last item, an item of one row, lone rows and runs crossing split
+    boundaries; the same rows as one-row items, and with the items listed in another order, give the same bits."""
+    from m3x import ops
+    g = _g(heads * 3 + chunk)
+    D, S, CAP = 128, 8, 2048
+    K = torch.randn(S, kv, CAP, D, generator=g).to(torch.bfloat16)
+    V = torch.randn(S, kv, CAP, D, generator=g).to(torch.bfloat16)
+    # (slot, first position, rows)
+    runs = [(0, 500, 1), (1, 0, 20), (2, 1020, 9), (3, 37, 1), (4, 120, 13), (5, 2000, 17), (6, 250, 33),
+            (7, 1500, 1)]
+    slots, pos, spans = [], [], []
+    for s, p0, n in runs:
+        spans.append((len(slots), n, p0))
+        slots += [s] * n
+        pos += list(range(p0, p0 + n))
+        K[s, :, p0 + n:] = float("nan")  # past the run's last position nothing may leak
+        V[s, :, p0 + n:] = float("nan")
+    R = len(slots)
+    qb = 16 // (heads // kv)
+    bins = ops.attn_item_bins(R, kv, CAP, chunk)
+    items = ops.attn_items(spans, heads, kv, bins).tolist()
+    assert items[0] == bins and items[1] == 0 and items[1 + bins] == sum((n + qb - 1) // qb for _, n, _ in spans)
+    assert sorted(c & 31 for c in items[2 + bins:]) == sorted(
+        min(qb, n - s) for _, n, _ in spans for s in range(0, n, qb))
+    singles = ops.attn_items([(r, 1, p) for r, p in enumerate(pos)], heads, kv, bins).tolist()
+    # the same items dealt bin by bin in reverse order
+    rev = [bins] + items[1:2 + bins] + items[2 + bins:][::-1]
+    slots_g = torch.tensor(slots, device=gpu)
+    pos_g = torch.tensor(pos, dtype=torch.int32, device=gpu)
+    q = torch.randn(R, heads, D, generator=g).to(torch.bfloat16)
+    Kg, Vg, qg = K.to(gpu), V.to(gpu), q.to(gpu)
+    ws = torch.empty(max(ops.decode_attn_workspace(R, kv, CAP, chunk), 16) // 4, device=gpu)
+    outs = []
+    for it in (None, items, singles, rev):
+        o = torch.full(q.shape, float("nan"), dtype=torch.bfloat16, device=gpu)
+        itg = None if it is None else torch.tensor(it, dtype=torch.int32, device=gpu)
+        ops.decode_attn(qg, Kg, Vg, o, slots_g, pos_g, D ** -0.5, CAP, chunk, ws, heads, kv, items=itg)
+        outs.append(o)
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+    ref = _attn_ref(q, K, V, torch.tensor(slots), torch.tensor(pos), D ** -0.5, heads // kv)
+    ok, info = close(outs[1], ref, atol=1e-2)
+    assert ok, info
+
+
 # ---------------------------------------------------------------- activations, depth norm / attention
 def test_swiglu_and_gelu(gpu):
     from m3x import ops
