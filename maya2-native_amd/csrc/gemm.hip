@@ -348,12 +348,154 @@ __global__ __launch_bounds__(64 * NWAVES) void linear_oneshot_kernel(const uint1
   linear_finish<DT, MT, NW, KW, EPI>(acc, reinterpret_cast<f32x4_t*>(xs), wn, wk, lane, n0, m0, Y, ldy, M, N);
 }
 
+// Large-M projections (M > 512 rows: steps with inline prefills). A workgroup of 8 waves owns a 2-D tile of 128
+// activation rows x 128 weight rows (for SwiGLU: 64 gate rows from W and the same 64 up rows from W2, i.e. 64
+// output columns) and walks K in stages of 64. The packed weight fragments of a stage are copied to LDS as they are
+// (16 fragments of 1 KB: every fragment read is one contiguous 1 KB); the activation rows sit row-major with a
+// 144-byte row stride, so the 16 rows of a fragment read fall in 16 different bank groups and a row's 8 stores in
+// distinct banks. The waves are 2 x 4 blocks of 64 activation rows x 32 weight rows (4 x 2 MFMA tiles; with
+// SwiGLU a wave holds one gate tile and the matching up tile). Stages are double-buffered in LDS: the next stage's
+// global loads are in flight while the current one multiplies, with one barrier per stage. Every weight byte is
+// read by ceil(M / 128) workgroups and every activation byte by ceil(N / 128), against 36 and 64 for the 64 x 64
+// chunked tiles at 2264 rows.
+template <int DT, int EPI>
+__global__ __launch_bounds__(512, 2) void linear_tiled_kernel(const uint16_t* __restrict__ X, long ldx,
+                                                              const uint16_t* __restrict__ Wp,
+                                                              const uint16_t* __restrict__ W2p,
+                                                              uint16_t* __restrict__ Y, long ldy, int M, int N, int K,
+                                                              int mblk, int nblk) {
+  constexpr bool DUAL = EPI == EPI_SWIGLU;
+  constexpr int BM = 128;
+  constexpr int LDA = 72;  // activation row stride in LDS, halfwords
+  __shared__ __align__(16) uint16_t lw[2][16 * 512];
+  __shared__ __align__(16) uint16_t la[2][BM * LDA];
+
+  const int xcd = blockIdx.x & 7;
+  const int slot = blockIdx.x >> 3;
+  const int nb = (slot / mblk) * 8 + xcd;
+  const int mb = slot - (slot / mblk) * mblk;
+  if (nb >= nblk) return;  // padding block: the whole workgroup leaves before any barrier
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+  const int wm = wave & 1;   // activation tiles 4 wm .. 4 wm + 3
+  const int wn = wave >> 1;  // weight tiles (below)
+  const int ksteps = K >> 5;
+  const int ntiles = (N + 15) >> 4;
+  const int m0 = mb * BM;
+
+  // per-thread load slots: vector v = tid + 512 j of a stage; weights: fragment f = v / 64 = tid / 64 + 8 j (tile
+  // t = f / 2, step f % 2), lane v % 64, at LDS 8 v; activations: row v / 8 = tid / 8 + 64 j, 16-byte column v % 8.
+  // Offsets are 32-bit element offsets; with SwiGLU, slot j = 0 holds gate rows and j = 1 up rows.
+  int gw[2], ga[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int f = (tid >> 6) + 8 * j;
+    const int t = f >> 1, st = f & 1;
+    const int tt = min(DUAL ? nb * 4 + (t & 3) : nb * 8 + t, ntiles - 1);  // tiles past N: valid, never stored
+    gw[j] = (tt * ksteps + st) * 512 + (tid & 63) * 8;
+    ga[j] = min(m0 + (tid >> 3) + 64 * j, M - 1) * (int)ldx + 8 * (tid & 7);  // rows past M: re-read, never stored
+  }
+  const int la0 = (tid >> 3) * LDA + 8 * (tid & 7);
+  // the wave's 2 weight tiles: plain 2 wn + i; SwiGLU gate wn and up 4 + wn
+  int wt[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) wt[i] = DUAL ? (i == 0 ? wn : 4 + wn) : 2 * wn + i;
+
+  f32x4_t acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  u16x8 rw[2], ra[2];
+  auto gload = [&](int stg) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      rw[j] = ld16((DUAL && j == 1 ? W2p : Wp) + gw[j] + stg * 1024);
+      ra[j] = ld16(X + ga[j] + stg * 64);
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      st16(&lw[buf][tid * 8 + 4096 * j], rw[j]);
+      st16(&la[buf][la0 + 64 * j * LDA], ra[j]);
+    }
+  };
+  const int nst = K >> 6;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int stg = 0; stg < nst; ++stg) {
+    const int buf = stg & 1;
+    if (stg + 1 < nst) gload(stg + 1);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      u16x8 a[2], b[4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) a[i] = *reinterpret_cast<const u16x8*>(&lw[buf][(wt[i] * 2 + s) * 512 + lane * 8]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        b[j] = *reinterpret_cast<const u16x8*>(&la[buf][(16 * (4 * wm + j) + li) * LDA + 32 * s + 8 * lg]);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16x16x32<DT>(a[i], b[j], acc[i][j]);
+    }
+    if (stg + 1 < nst) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // epilogue: lane (li, lg) of tile pair (i, j) holds weight rows 4 lg + r of tile wt[i] for activation row
+  // m0 + 16 (4 wm + j) + li
+  const bool vec = (ldy & 3) == 0 && (((uintptr_t)Y) & 7) == 0;
+  constexpr int NI = DUAL ? 1 : 2;
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int n = DUAL ? (nb * 4 + wn) * 16 + 4 * lg : (nb * 8 + wt[i]) * 16 + 4 * lg;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int m = m0 + 16 * (4 * wm + j) + li;
+      if (m >= M) continue;
+      uint16_t o[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float v = rnd<DT>(acc[i][j][r]);
+        if constexpr (DUAL) {
+          const float g = v;
+          const float u = rnd<DT>(acc[1][j][r]);
+          v = rnd<DT>(g / (1.0f + expf(-g))) * u;
+        } else if constexpr (EPI == EPI_GELU) {
+          v = 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+        }
+        o[r] = E<DT>::from_f(v);
+      }
+      uint16_t* yp = Y + (long)m * ldy + n;
+      if (vec && n + 3 < N) {
+        uint2 pk;
+        pk.x = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
+        pk.y = (uint32_t)o[2] | ((uint32_t)o[3] << 16);
+        *reinterpret_cast<uint2*>(yp) = pk;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (n + r < N) yp[r] = o[r];
+      }
+    }
+  }
+}
+
 // Launch geometry: MT activation tiles of 16 rows per workgroup; NW weight tiles per workgroup; NWAVES waves
 // (NWAVES / NW K slices).
 struct LinearPlan {
   int mt, nw, mblk, nblk;
   int nwaves;   // 4 for the chunked kernel and the small one-shot; 8 or 16 for the wide one-shot
   int oneshot;  // steps per K slice for the one-shot kernel, 0 for the chunked kernel
+  int tiled;    // 1: linear_tiled_kernel (M > 512, K % 64 == 0)
 };
 
 // Small one-shot (4 waves): each of the 4/nw K slices is exactly 8 or 16 steps of 32 and the activation block
@@ -409,12 +551,23 @@ static bool wide_plan(int M, int N, int K, bool dual, LinearPlan& p) {
 // Chunked / small one-shot tile choice, measured on MI355X (graph-timed sweep over the decode shapes,
 // M = 1..2264): the best plan is the largest tile that still gives at least ~400 workgroups; MT = 2 pays off
 // only above ~112 rows.
-static LinearPlan linear_plan(int M, int N, int K, bool dual) {
+static LinearPlan linear_plan(int M, int N, int K, bool dual, long ldx) {
   const int ntiles = m3x_ceil_div(N, 16);
   const int ksteps = K / 32;
   auto blocks = [&](int mt, int nw) { return (long)m3x_ceil_div(M, 16 * mt) * m3x_ceil_div(ntiles, nw); };
   LinearPlan p;
   p.nwaves = 4;
+  p.tiled = 0;
+  // tiled: 32-bit element offsets into the packed weight and the activations
+  if (M > 512 && K % 64 == 0 && (long)ntiles * 16 * K < (1L << 31) && (long)M * ldx < (1L << 31)) {
+    p.tiled = 1;
+    p.mt = 8;
+    p.nw = dual ? 4 : 8;
+    p.oneshot = 0;
+    p.mblk = m3x_ceil_div(M, 128);
+    p.nblk = m3x_ceil_div(ntiles, p.nw);
+    return p;
+  }
   if (wide_plan(M, N, K, dual, p)) {
     p.mblk = m3x_ceil_div(M, 16 * p.mt);
     p.nblk = m3x_ceil_div(ntiles, p.nw);
@@ -451,6 +604,11 @@ template <int DT, int EPI>
 static bool launch_linear(const LinearPlan& p, hipStream_t st, const uint16_t* X, long ldx, const uint16_t* W,
                           const uint16_t* W2, uint16_t* Y, long ldy, int M, int N, int K) {
   const dim3 grid(m3x_ceil_div(p.nblk, 8) * 8 * p.mblk);
+  if (p.tiled) {
+    hipLaunchKernelGGL((linear_tiled_kernel<DT, EPI>), grid, dim3(512), 0, st, X, ldx, W, W2, Y, ldy, M, N, K, p.mblk,
+                       p.nblk);
+    return true;
+  }
 #define M3X_ONE(MTT, NWW, NWV, SS)                                                                         \
   hipLaunchKernelGGL((linear_oneshot_kernel<DT, MTT, NWW, NWV, EPI, SS>), grid, dim3(64 * NWV), 0, st, X, \
                      ldx, W, W2, Y, ldy, M, N, K, p.mblk, p.nblk)
@@ -513,7 +671,7 @@ static int linear_common(const void* x, long ldx, const void* w, const void* w2,
   if (K % 32 || (ldx & 7) || ldx < K || ldy < N) return M3X_EINVAL;
   if (!m3x_aligned16(x) || !m3x_aligned16(w) || (w2 && !m3x_aligned16(w2)) || (((uintptr_t)y) & 1))
     return M3X_EINVAL;
-  const LinearPlan p = linear_plan(M, N, K, epi == EPI_SWIGLU);
+  const LinearPlan p = linear_plan(M, N, K, epi == EPI_SWIGLU, ldx);
   if ((long)m3x_ceil_div(p.nblk, 8) * 8 * p.mblk > 0x7fffffffL) return M3X_EINVAL;
   hipStream_t st = (hipStream_t)stream;
   const uint16_t *X = (const uint16_t*)x, *Wt = (const uint16_t*)w, *W2 = (const uint16_t*)w2;

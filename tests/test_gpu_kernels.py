@@ -26,7 +26,10 @@ def _g(seed):
                                    # K slices of unequal length: the last chunk of the last slice is partial
                                    (40, 1024, 1056), (200, 1024, 1312), (3, 512, 160),
                                    # one 16-row block over 8 waves
-                                   (1, 1024, 2816), (16, 1024, 3072), (2, 2049, 2048), (1, 4096, 1024)])
+                                   (1, 1024, 2816), (16, 1024, 3072), (2, 2049, 2048), (1, 4096, 1024),
+                                   # 2-D LDS tiles above 512 rows: partial row / column blocks, N % 16 != 0
+                                   (513, 1024, 1024), (1000, 2049, 1024), (2264, 1024, 3072), (700, 1024, 2816),
+                                   (1300, 136, 2048)])
 def test_linear_bf16(gpu, M, N, K):
     from m3x import ops
     g = _g(M * 7 + N)
@@ -38,7 +41,7 @@ def test_linear_bf16(gpu, M, N, K):
     assert ok, info
 
 
-@pytest.mark.parametrize("M,N,K", [(24, 3072, 1024), (1, 2816, 1024), (3, 1024, 96)])
+@pytest.mark.parametrize("M,N,K", [(24, 3072, 1024), (1, 2816, 1024), (3, 1024, 96), (700, 3072, 1024)])
 def test_linear_fp16(gpu, M, N, K):
     from m3x import ops
     g = _g(M + K)
@@ -51,7 +54,9 @@ def test_linear_fp16(gpu, M, N, K):
 
 @pytest.mark.parametrize("M,I,K,dtype", [(1, 3072, 1024, torch.bfloat16), (224, 2816, 1024, torch.bfloat16),
                                          (37, 3072, 1024, torch.float16), (224, 3072, 1024, torch.bfloat16),
-                                         (64, 3072, 1024, torch.float16), (130, 2816, 1024, torch.bfloat16)])
+                                         (64, 3072, 1024, torch.float16), (130, 2816, 1024, torch.bfloat16),
+                                         (1100, 3072, 1024, torch.bfloat16), (600, 2816, 1024, torch.float16),
+                                         (2264, 3072, 1024, torch.bfloat16)])
 def test_linear_swiglu_epilogue(gpu, M, I, K, dtype):
     """Fused gate|up GEMM + silu*mul against the separate GEMM + activation kernel (the two launches may slice K
     differently, so the fp32 sums can round apart by an ulp) and against an fp32 reference."""
@@ -73,7 +78,7 @@ def test_linear_swiglu_epilogue(gpu, M, I, K, dtype):
     assert ok, info
 
 
-@pytest.mark.parametrize("M", [9, 150])
+@pytest.mark.parametrize("M", [9, 150, 700])
 def test_linear_gelu_epilogue(gpu, M):
     from m3x import ops
     g = _g(77 + M)
