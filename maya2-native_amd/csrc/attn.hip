@@ -409,11 +409,12 @@ __device__ __forceinline__ void attn_block_item(
 // it; the differences are the causal mask (vector j sees keys <= pos[row + j]) and the per-vector rescale (O rows
 // are vectors 4 * lg + r, whose running max lives in lane 4 * lg + r). Rows whose context spans several splits
 // write partials for decode_attn_combine_kernel.
-// The grid is one workgroup per bin per (kv head, split) plane, ~3 workgroups per CU whatever the item count (a
-// workgroup launched only to exit costs a CU slot for microseconds). The caller deals the items into the bins
-// (longest processing time first balances them) and lists them bin by bin:
+// The grid is one workgroup per bin per kv head, ~3 workgroups per CU whatever the item count (a workgroup
+// launched only to exit costs a CU slot for microseconds). An item is one split of its rows' keys, so a long
+// context is cut into several items that the bins balance. The caller deals the items into the bins (longest
+// processing time first balances them) and lists them bin by bin:
 //   items = [bins, start[0], ..., start[bins], code[0], code[1], ...], bin b = codes start[b] .. start[b + 1] - 1,
-// each code = 32 * (first row) + (rows of the item).
+// each code = 2048 * (first row) + 32 * split + (rows of the item).
 template <int G>
 __global__ __launch_bounds__(256, 2) void attn_block_kernel(
     const uint16_t* __restrict__ q, long sq_b, long sq_h, const uint16_t* __restrict__ kc,
@@ -422,11 +423,10 @@ __global__ __launch_bounds__(256, 2) void attn_block_kernel(
     float* __restrict__ part, int max_splits, int cap, const int32_t* __restrict__ items, int rows) {
   constexpr int QB = 16 / G;
   const int kh = blockIdx.y;
-  const int split = blockIdx.z;
   const int KV = gridDim.y;
   const int bins = items[0];
   if ((int)blockIdx.x >= bins || bins > rows) return;  // an item list sized for another grid does nothing
-  const int i0 = max(items[1 + blockIdx.x], 0), i1 = min(items[2 + blockIdx.x], rows);
+  const int i0 = max(items[1 + blockIdx.x], 0), i1 = min(items[2 + blockIdx.x], rows * max_splits);
   const int32_t* codes = items + 2 + bins;
   // LDS: the wave-private K tiles during the key loop, then the wave merge (after a barrier)
   constexpr int KTILE_BYTES = 4 * 32 * 136 * 2;
@@ -434,8 +434,9 @@ __global__ __launch_bounds__(256, 2) void attn_block_kernel(
   __shared__ __align__(16) unsigned char lds[KTILE_BYTES > MERGE_BYTES ? KTILE_BYTES : MERGE_BYTES];
   for (int it = i0; it < i1; ++it) {
     const int code = codes[it];
-    const int row = code >> 5;
-    if (row < 0 || row >= rows) continue;
+    const int row = code >> 11;
+    const int split = (code >> 5) & 63;
+    if (row < 0 || row >= rows || split >= max_splits) continue;
     const int nb = min(min(code & 31, QB), rows - row);
     if (nb <= 0) continue;
     int plast = 0;
@@ -449,14 +450,12 @@ __global__ __launch_bounds__(256, 2) void attn_block_kernel(
   }
 }
 
-// Bins of an item launch: ~3 workgroups per CU over the (kv head, split) planes, at most one per row.
-static int attn_item_bins(int rows, int kv_heads, int max_splits) {
-  return std::max(1, std::min(rows, 768 / (kv_heads * max_splits)));
-}
+// Bins of an item launch: ~3 workgroups per CU over the kv heads, at most one per row.
+static int attn_item_bins(int rows, int kv_heads) { return std::max(1, std::min(rows, 768 / kv_heads)); }
 
 M3X_API int m3x_decode_attn_item_bins(int rows, int kv_heads, int max_ctx, int chunk) {
   if (rows <= 0 || kv_heads <= 0 || max_ctx <= 0 || chunk <= 0) return 0;
-  return attn_item_bins(rows, kv_heads, (max_ctx + chunk - 1) / chunk);
+  return attn_item_bins(rows, kv_heads);
 }
 
 template <int G>
@@ -539,7 +538,8 @@ M3X_API int m3x_decode_attn(const void* q, long sq_b, long sq_h, const void* k_c
   const float scale_log2 = scale * 1.44269504088896341f;
   if (rows > 65535 * 64 || kv_heads > 65535) return M3X_EINVAL;
   dim3 grid(rows, kv_heads, max_splits);
-  const dim3 igrid(attn_item_bins(rows, kv_heads, max_splits), kv_heads, max_splits);
+  if (items && (rows >= (1 << 20) || max_splits > 64)) return M3X_EINVAL;  // item codes: row < 2^20, split < 64
+  const dim3 igrid(attn_item_bins(rows, kv_heads), kv_heads, 1);
 #define M3X_ATTN_LAUNCH(GG)                                                                                          \
   if (items)                                                                                                         \
     hipLaunchKernelGGL((attn_block_kernel<GG>), igrid, dim3(256), 0, st, (const uint16_t*)q, sq_b, sq_h,            \

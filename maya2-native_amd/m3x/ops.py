@@ -128,24 +128,22 @@ def attn_item_bins(rows, kv_heads, max_ctx, chunk) -> int:
     return int(lib().m3x_decode_attn_item_bins(rows, kv_heads, max_ctx, chunk))
 
 
-def attn_items(runs, heads, kv_heads, bins):
+def attn_items(runs, heads, kv_heads, bins, chunk):
     """Work items of decode_attn for rows laid out as runs: (first row, rows, first position) per run, a decode
     row being a run of one row and an inline prefill of T tokens a run of T rows at consecutive positions of one
-    slot. Each run is cut into items of up to 16 // (heads // kv_heads) rows, and the items are dealt into `bins`
-    bins (attn_item_bins) longest processing time first: each goes to the least loaded bin, its cost its context
-    length plus a fixed 64 keys. Returns int32 [bins, start[0..bins], codes bin by bin], code =
-    32 * first_row + rows."""
+    slot. Each run is cut into blocks of up to 16 // (heads // kv_heads) rows and each block's keys into splits of
+    `chunk` keys; an item is one split of one block. The items are dealt into `bins` bins (attn_item_bins) longest
+    processing time first: each goes to the least loaded bin, its cost its keys plus a fixed 64. Returns int32
+    [bins, start[0..bins], codes bin by bin], code = 2048 * first_row + 32 * split + rows."""
     qb = 16 // (heads // kv_heads)
     costs, codes = [], []
     for r0, n, p0 in runs:
-        if n == 1:
-            costs.append(p0 + 65)
-            codes.append(32 * r0 + 1)
-            continue
         for s in range(0, n, qb):
             m = min(qb, n - s)
-            costs.append(p0 + s + m + 64)
-            codes.append(32 * (r0 + s) + m)
+            keys = p0 + s + m  # the block's last row attends keys 0 .. p0 + s + m - 1
+            for sp in range(0, (keys + chunk - 1) // chunk):
+                costs.append(min(chunk, keys - sp * chunk) + 64)
+                codes.append(2048 * (r0 + s) + 32 * sp + m)
     order = np.argsort(-np.asarray(costs, dtype=np.int64), kind="stable").tolist()
     k = min(bins, len(order))
     per = [[codes[i]] for i in order[:k]] + [[] for _ in range(bins - k)]

@@ -180,8 +180,9 @@ class StaticBackbone:
             # attention work items of a mixed step (ops.attn_items): prefill rows attended 16 // G at a time; until
             # a step stages its own, every row is an item of its own
             b.item_bins = ops.attn_item_bins(rows, KV, ctx, b.chunk)
-            items = ops.attn_items([(r, 1, 0) for r in range(rows)], H, KV, b.item_bins)
-            b.items = torch.zeros(2 + b.item_bins + rows, dtype=torch.int32, device=dev)
+            items = ops.attn_items([(r, 1, 0) for r in range(rows)], H, KV, b.item_bins, b.chunk)
+            b.items = torch.zeros(2 + b.item_bins + rows * ((ctx + b.chunk - 1) // b.chunk), dtype=torch.int32,
+                                  device=dev)
             b.items[:len(items)] = torch.from_numpy(items)
         ws = ops.decode_attn_workspace(rows, KV, ctx, b.chunk)
         b.attn_ws = torch.empty(max(ws, 16) // 4, dtype=torch.float32, device=dev)
@@ -359,7 +360,7 @@ class StaticBackbone:
                 runs.append((at, t.shape[0], self.lengths_cpu[s]))
                 at += t.shape[0]
             runs += [(r, 1, 0) for r in range(rows, bb)]  # padding rows on the dummy slot
-            items = ops.attn_items(runs, self.heads, self.kv_heads, g.bufs.item_bins)
+            items = ops.attn_items(runs, self.heads, self.kv_heads, g.bufs.item_bins, g.bufs.chunk)
             g.items_cpu[:len(items)] = torch.from_numpy(items)
             g.bufs.items.copy_(g.items_cpu, non_blocking=True)
         g.last = None

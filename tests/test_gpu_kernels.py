@@ -263,11 +263,13 @@ def test_prefill_items_match_decode_rows(gpu, heads, kv, chunk):
     R = len(slots)
     qb = 16 // (heads // kv)
     bins = ops.attn_item_bins(R, kv, CAP, chunk)
-    items = ops.attn_items(spans, heads, kv, bins).tolist()
-    assert items[0] == bins and items[1] == 0 and items[1 + bins] == sum((n + qb - 1) // qb for _, n, _ in spans)
-    assert sorted(c & 31 for c in items[2 + bins:]) == sorted(
-        min(qb, n - s) for _, n, _ in spans for s in range(0, n, qb))
-    singles = ops.attn_items([(r, 1, p) for r, p in enumerate(pos)], heads, kv, bins).tolist()
+    items = ops.attn_items(spans, heads, kv, bins, chunk).tolist()
+    blocks = [(r0 + s, min(qb, n - s), p0 + s + min(qb, n - s)) for r0, n, p0 in spans for s in range(0, n, qb)]
+    nitems = sum((keys + chunk - 1) // chunk for _, _, keys in blocks)
+    assert items[0] == bins and items[1] == 0 and items[1 + bins] == nitems
+    assert sorted((c >> 11, (c >> 5) & 63, c & 31) for c in items[2 + bins:]) == sorted(
+        (r, sp, m) for r, m, keys in blocks for sp in range((keys + chunk - 1) // chunk))
+    singles = ops.attn_items([(r, 1, p) for r, p in enumerate(pos)], heads, kv, bins, chunk).tolist()
     # the same items dealt bin by bin in reverse order
     rev = [bins] + items[1:2 + bins] + items[2 + bins:][::-1]
     slots_g = torch.tensor(slots, device=gpu)

@@ -22,32 +22,37 @@ def test_attn_chunk_plan():
 
 
 def test_attn_items_cover_every_row_once():
-    """The work list of a mixed step: every row in exactly one item of one slot's run, items of at most 16 / G
-    rows that start at a run's start or a multiple of 16 / G into it, bins listed back to back, and the longest
-    processing time deal (no bin exceeds the lightest by more than its largest item)."""
+    """The work list of a mixed step: every split of every row in exactly one item of one slot's run, items of at
+    most 16 / G rows that start at a run's start or a multiple of 16 / G into it and cover one chunk of the block's
+    keys, bins listed back to back, and the longest processing time deal (no bin exceeds the lightest by more than
+    its largest item)."""
     from m3x import ops
     runs = [(0, 1, 3000), (1, 1, 10), (2, 20, 0), (22, 9, 700), (31, 1, 4000), (32, 256, 100)]
     rows = 288
-    for heads, kv, bins in [(16, 8, 96), (8, 8, 7), (16, 8, 1)]:
+    for heads, kv, bins, chunk in [(16, 8, 96, 4096), (8, 8, 7, 1024), (16, 8, 1, 512), (16, 8, 40, 128)]:
         qb = 16 // (heads // kv)
-        it = ops.attn_items(runs, heads, kv, bins).tolist()
+        it = ops.attn_items(runs, heads, kv, bins, chunk).tolist()
         assert it[0] == bins and it[1] == 0
         start = it[1:2 + bins]
         codes = it[2 + bins:]
         assert start == sorted(start) and start[-1] == len(codes)
         covered = []
+        cost = {}
         for c in codes:
-            r0, m = c >> 5, c & 31
+            r0, sp, m = c >> 11, (c >> 5) & 63, c & 31
             assert 1 <= m <= qb
             run = [r for r in runs if r[0] <= r0 < r[0] + r[1]][0]
             assert r0 + m <= run[0] + run[1] and (r0 - run[0]) % qb == 0
-            covered += range(r0, r0 + m)
-        assert sorted(covered) == list(range(rows))
-        cost = {}
+            keys = run[2] + (r0 - run[0]) + m  # keys of the block's last row
+            assert sp * chunk < keys
+            cost[c] = min(chunk, keys - sp * chunk) + 64
+            covered += [(r, sp) for r in range(r0, r0 + m)]
+        want = []
         for r0, n, p0 in runs:
             for s0 in range(0, n, qb):
                 m = min(qb, n - s0)
-                cost[32 * (r0 + s0) + m] = p0 + s0 + m + 64
+                want += [(r, sp) for r in range(r0 + s0, r0 + s0 + m) for sp in range((p0 + s0 + m + chunk - 1) // chunk)]
+        assert sorted(covered) == sorted(want) and len({r for r, _ in covered}) == rows
         loads = [sum(cost[c] for c in codes[start[b]:start[b + 1]]) for b in range(bins)]
         assert max(loads) - min(loads) <= max(cost.values())
 
