@@ -58,12 +58,13 @@ def build_frame(torch, seats, lengths, seed_base=0, backbone=None, depth_model=N
     return fs, bb, dm
 
 
-def secondary(torch, bb, steps):
-    """The backbone-only configurations, timed through the reference surfaces on the frame's backbone weights:
-    C3 = StaticBackbone.step over 64 seats (lengths U[64, 2048]) + cb0; C4 = StaticBackbone.step_mixed with 216
-    decoding seats (lengths log-uniform in [128, 4096)) and 8 inline prefills of 256 tokens (embedding rows of
-    uniform ids from a [151936, 1024] N(0, 0.02) table, starting at length 0) = 2264 rows + cb0 over the 224
-    seats. Lengths are reset before every step, so each timed step does the same work."""
+def secondary(torch, bb, dm, steps):
+    """The other GPU configurations, timed through the reference surfaces on the frame's weights:
+    C2 = FastDepth.__call__ over 16 seats (the 4-layer depth frame over codebooks 1..31, top-k 50, T 0.9, h N(0,1),
+    cb0 uniform in [0, 2048)); C3 = StaticBackbone.step over 64 seats (lengths U[64, 2048]) + cb0; C4 =
+    StaticBackbone.step_mixed with 216 decoding seats (lengths log-uniform in [128, 4096)) and 8 inline prefills of
+    256 tokens (embedding rows of uniform ids from a [151936, 1024] N(0, 0.02) table, starting at length 0) = 2264
+    rows + cb0 over the 224 seats. Lengths are reset before every step, so each timed step does the same work."""
     from m3x import roofline, synth
     from m3x.cb0 import Cb0Sampler
     from m3x.serve.fast_backbone import StaticBackbone
@@ -95,6 +96,37 @@ def secondary(torch, bb, steps):
                       "mfma_fraction": round(flo / (ms * 1e-3) / 1e12 / roofline.MFMA_BF16_TFLOPS, 4), "note": note}
         log(f"{label}: {rows} rows, {ms:.3f} ms/step ({out[label]['hbm_fraction']:.1%} of the HBM and "
             f"{out[label]['mfma_fraction']:.1%} of the MFMA roofline)")
+
+    # C2: the depth frame alone at 16 seats
+    from m3x.serve.fast_depth import FastDepth
+    B2 = 16
+    fd = FastDepth(dm, B2, dtype=torch.bfloat16, temp=0.9, top_k=50, batch_buckets=(B2,), fused=True)
+    fd.row_seed.copy_(torch.arange(B2 + 1, dtype=torch.int32, device=dev) * 69069 + 7)
+    h2 = torch.randn(B2, 1024, device=dev, generator=g).to(torch.bfloat16)
+    cb02 = torch.randint(0, 2048, (B2,), device=dev, generator=g)
+    slots2 = list(range(B2))
+    fd.warmup()
+    for _ in range(3):
+        fd(slots2, h2, cb02)
+    torch.cuda.synchronize()
+    t = 0.0
+    for _ in range(steps * 4):
+        t0 = time.perf_counter()
+        fd(slots2, h2, cb02)
+        torch.cuda.synchronize()
+        t += time.perf_counter() - t0
+    ms = t * 1e3 / (steps * 4)
+    byt = roofline.depth_frame_bytes(seats=B2)
+    flo = roofline.depth_frame_flops(B2)
+    out["c2"] = {"rows": B2, "ms_per_step": round(ms, 3), "bytes_algorithmic": byt, "flops_algorithmic": flo,
+                 "hbm_fraction": round(byt / (ms * 1e-3) / 1e9 / roofline.HBM_PEAK_GBS, 4),
+                 "mfma_fraction": round(flo / (ms * 1e-3) / 1e12 / roofline.MFMA_BF16_TFLOPS, 4),
+                 "note": "FastDepth.__call__ (host staging + one graph replay of the 31-codebook depth frame + clone); "
+                         "the bytes stream the trunk once per codebook (its 98 MB stays in the 256 MB MALL)"}
+    log(f"c2: {B2} seats, {ms:.3f} ms/frame ({out['c2']['hbm_fraction']:.1%} of the HBM and "
+        f"{out['c2']['mfma_fraction']:.1%} of the MFMA roofline)")
+    del fd
+    torch.cuda.empty_cache()
 
     # C3
     B3 = 64
@@ -175,6 +207,31 @@ def cpu_baseline(torch, seconds, seats=2):
                 sample=f"{frames} frame step(s) x {seats} seats of the B=224 workload shapes (28 layers, KV lengths "
                        f"{lengths.tolist()}, depth 31 codebooks) through the PyTorch-eager oracle, "
                        f"{el:.1f} s on {threads} host threads")
+
+
+def c1_cpu(torch, reps=20):
+    """C1: one Qwen3-0.6B-shaped decoder layer (+ final norm), one decode step at B=1 over a 256-token cache, fp32,
+    through the oracle's eager restatement of the reference path on the host cores (CPU-only by definition)."""
+    from m3x import synth
+    from oracle import torch_oracle as O
+    bb = synth.qwen3_backbone(layers=1, seed=0, dtype=torch.float32)
+    g = torch.Generator().manual_seed(10)
+    kc = [torch.zeros(2, 8, 512, 128)]
+    vc = [torch.zeros(2, 8, 512, 128)]
+    kc[0][0, :, :256] = torch.randn(8, 256, 128, generator=g)
+    vc[0][0, :, :256] = torch.randn(8, 256, 128, generator=g)
+    x = torch.randn(1, 1024, generator=g)
+    cos, sin = O.rope_tables(128, 1e6, 512, torch.float32)
+    slots = torch.tensor([0])
+    t = 0.0
+    for i in range(reps + 2):
+        lengths = torch.tensor([256, 0])
+        t0 = time.perf_counter()
+        O.backbone_step(bb, kc, vc, lengths, slots, x, cos, sin)
+        if i >= 2:
+            t += time.perf_counter() - t0
+    return {"ms_per_step": round(t * 1e3 / reps, 3), "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{reps} steps of one fp32 layer at B=1, cache 256 tokens"}
 
 
 def _traffic_ratio():
@@ -337,7 +394,7 @@ def main():
             del fs1, g1
         sec = None
         if not args.no_secondary:
-            sec = secondary(torch, bb, args.secondary_steps)
+            sec = secondary(torch, bb, dm, args.secondary_steps)
         del bb, dm
         torch.cuda.empty_cache()
 
@@ -345,6 +402,8 @@ def main():
     if not args.no_cpu_baseline:
         log(f"CPU baseline (~{args.cpu_seconds:.0f} s)")
         cpu = cpu_baseline(torch, args.cpu_seconds)
+        cpu["c1"] = c1_cpu(torch)
+        log(f"c1 (one fp32 decoder layer, B=1, CPU): {cpu['c1']['ms_per_step']:.2f} ms")
 
     ratio = _traffic_ratio()
     out = {
