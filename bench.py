@@ -170,7 +170,69 @@ def secondary(torch, bb, dm, steps):
         "seats; algorithmic bytes read each prefill key once")
     del sb, cb, pre
     torch.cuda.empty_cache()
+
+    # time to first audio: a 512-token prompt prefilled onto one empty seat through the graphed inline-prefill
+    # step (StaticBackbone.prefill), beside the eager HF forward the engine falls back to (maya3/engine.py:497-502)
+    Tp = 512
+    sb = StaticBackbone(bb, 2, capacity=CAP, batch_buckets=(Tp,), ctx_buckets=(CAP,), attention="triton",
+                        fuse_rope=True)
+    xp = (torch.randn(Tp, 1024, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    sb.prefill(0, xp)
+    ts = []
+    for _ in range(steps):
+        sb.free(0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        sb.prefill(0, xp)
+        torch.cuda.synchronize()
+        ts.append(time.perf_counter() - t0)
+    pre_ms = sorted(ts)[len(ts) // 2] * 1e3
+    out["ttfa_prefill"] = {"tokens": Tp, "ms": round(pre_ms, 3),
+                           "note": "StaticBackbone.prefill of 512 tokens onto an empty seat (one graph replay), median"}
+    try:
+        out["ttfa_prefill"]["hf_eager_ms"] = round(_hf_eager_prefill_ms(torch, bb, xp, steps), 3)
+    except Exception as e:  # the comparison is informative only
+        log(f"HF eager prefill comparison skipped: {e}")
+    log(f"prefill of {Tp} tokens: {pre_ms:.2f} ms (HF eager: {out['ttfa_prefill'].get('hf_eager_ms')})")
+    del sb
+    torch.cuda.empty_cache()
     return out
+
+
+def _hf_eager_prefill_ms(torch, bb, x, steps):
+    """The reference's eager fallback for a long prompt (`self.model.backbone(prompt, use_cache=True)`): HF
+    transformers' Qwen3Model on the same weights, bf16, on this GPU; median ms."""
+    from transformers import Qwen3Config, Qwen3Model
+    L0 = bb.lm.model.layers
+    cfg = Qwen3Config(hidden_size=1024, intermediate_size=3072, num_hidden_layers=len(L0), num_attention_heads=16,
+                      num_key_value_heads=8, head_dim=128, rms_norm_eps=1e-6, rope_theta=1e6, vocab_size=16,
+                      max_position_embeddings=4096)
+    dev = x.device
+    m = Qwen3Model(cfg).to(device=dev, dtype=torch.bfloat16).eval()
+    sd = {"norm.weight": bb.lm.model.norm.weight}
+    for i, L in enumerate(L0):
+        a, f = L.self_attn, L.mlp
+        for name, w in (("self_attn.q_proj", a.q_proj), ("self_attn.k_proj", a.k_proj), ("self_attn.v_proj", a.v_proj),
+                        ("self_attn.o_proj", a.o_proj), ("mlp.gate_proj", f.gate_proj), ("mlp.up_proj", f.up_proj),
+                        ("mlp.down_proj", f.down_proj)):
+            sd[f"layers.{i}.{name}.weight"] = w.weight
+        sd[f"layers.{i}.self_attn.q_norm.weight"] = a.q_norm.weight
+        sd[f"layers.{i}.self_attn.k_norm.weight"] = a.k_norm.weight
+        sd[f"layers.{i}.input_layernorm.weight"] = L.input_layernorm.weight
+        sd[f"layers.{i}.post_attention_layernorm.weight"] = L.post_attention_layernorm.weight
+    m.load_state_dict(sd, strict=False)
+    ts = []
+    with torch.inference_mode():
+        for i in range(steps + 1):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            m(inputs_embeds=x[None], use_cache=True)
+            torch.cuda.synchronize()
+            if i:
+                ts.append(time.perf_counter() - t0)
+    del m
+    torch.cuda.empty_cache()
+    return sorted(ts)[len(ts) // 2] * 1e3
 
 
 def cpu_baseline(torch, seconds, seats=2):

@@ -152,6 +152,38 @@ class StaticBackbone:
         self.lengths[slot] = length
         self.lengths_cpu[slot] = length
 
+    @torch.inference_mode()
+    def export_prefix(self, slot, length=None):
+        """The slot's first `length` (default: all) cached positions in load_prefix's format: a list of per-layer
+        (k, v) [1, kv_heads, length, head_dim] copies, e.g. a voice prefix computed once and installed into other
+        slots (the `voice.kv` of maya3/engine.py:276-277)."""
+        if not 0 <= slot < self.max_slots:
+            raise IndexError(slot)
+        n = self.lengths_cpu[slot] if length is None else int(length)
+        if not 0 <= n <= self.lengths_cpu[slot]:
+            raise ValueError(f'length {n} outside the slot\'s {self.lengths_cpu[slot]} cached positions')
+        return [(self.k[i][slot:slot + 1, :, :n].clone(), self.v[i][slot:slot + 1, :, :n].clone())
+                for i in range(len(self.layers))]
+
+    @torch.inference_mode()
+    def prefill(self, slot, x):
+        """Causal prefill of x [T, hidden] onto the slot's cached prefix, through the graphed inline-prefill step
+        (step_mixed with no decoding seats) in pieces of at most the largest row bucket; returns the last position's
+        hidden state [hidden]. Replaces the eager HF prefill that the engine falls back to for prompts longer than a
+        tick's row budget and that computes a voice's prefix KV (maya3/engine.py:270-279,497-506)."""
+        if not 0 <= slot < self.max_slots:
+            raise IndexError(slot)
+        if x.dim() != 2 or x.shape[1] != self.hidden or x.shape[0] == 0:
+            raise ValueError(f'x must be [T>0, {self.hidden}], got {tuple(x.shape)}')
+        if self.lengths_cpu[slot] + x.shape[0] > self.capacity:
+            raise ValueError(f'context {self.lengths_cpu[slot] + x.shape[0]} exceeds capacity {self.capacity}')
+        piece = self.batch_buckets[-1]
+        last = None
+        for t0 in range(0, x.shape[0], piece):
+            _, out = self.step_mixed([], None, [(slot, x[t0:t0 + piece])])
+            last = out[0]
+        return last
+
     # ---------------------------------------------------------------- math
     def make_buffers(self, rows, ctx, mixed=False):
         """Static buffers of one (row bucket, context bucket) step; reused by every replay of its graph.
