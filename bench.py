@@ -171,6 +171,46 @@ def secondary(torch, bb, dm, steps):
     del sb, cb, pre
     torch.cuda.empty_cache()
 
+    # the engine's loop guard for 224 seats (maya3/guards.py:80-107): device history push + rule, graph-timed,
+    # beside the same rule on the host over the same histories (the engine evaluates it on the host each tick)
+    from types import SimpleNamespace
+    from m3x.guards import LoopGuard
+    from oracle import torch_oracle as O
+    gcfg = SimpleNamespace(stall=32, period_win=64, period_thr=0.7, pmin=2, pmax=16, hist=96)
+    Bg = 224
+    lg = LoopGuard(Bg, gcfg, device=dev)
+    gslots = torch.arange(Bg, device=dev)
+    gcodes = torch.randint(0, 2048, (Bg,), device=dev, generator=g)
+    gout = torch.empty(Bg, dtype=torch.int32, device=dev)
+    for _ in range(100):
+        lg.push(gslots, gcodes)
+    stream = torch.cuda.current_stream()
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    gg = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gg, stream=side):
+        for _ in range(20):
+            lg.push(gslots, gcodes)
+            lg.detect(gslots, gout)
+    gg.replay()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(5):
+        gg.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    gpu_us = e0.elapsed_time(e1) * 1e3 / 100
+    Wh, nh = lg.hist[:Bg].cpu().numpy(), lg.frames[:Bg].cpu().numpy()
+    t0 = time.perf_counter()
+    for _ in range(5):
+        O.loop_detect_batch(Wh, nh)
+    cpu_us = (time.perf_counter() - t0) / 5 * 1e6
+    out["loop_guard"] = {"seats": Bg, "gpu_us": round(gpu_us, 2), "cpu_us": round(cpu_us, 1),
+                         "note": "push + rule per frame in the graph, against the rule over the same histories on "
+                                 "one host thread"}
+    log(f"loop guard, {Bg} seats: {gpu_us:.2f} us on the GPU (push + rule), {cpu_us:.0f} us on the host")
+    del lg
+
     # time to first audio: a 512-token prompt prefilled onto one empty seat through the graphed inline-prefill
     # step (StaticBackbone.prefill), beside the eager HF forward the engine falls back to (maya3/engine.py:497-502)
     Tp = 512

@@ -194,6 +194,26 @@ int m3x_copy_rows(const void* src, long ld_src, const void* src_idx, long src_of
 int m3x_code_ring_write(const int32_t* codes, long ld_codes, int32_t* ring, int32_t* head, int depth, int seats, int nq,
                         int B, void* stream);
 
+/* ---- loop guard (maya3/guards.py:80-107 loop_detect_batch; engine tick maya3/engine.py:585-617) ------------ */
+
+/* The code history of slot slots[b] (hist row of hist_len <= 256 int32 codes, oldest first, -1 = empty) shifts
+ * left by one and takes codes[b * ld_codes] as its newest entry; frames[slots[b]] += 1 when frames is not NULL.
+ * A slot repeated within one call (a graph bucket's padding rows on the dummy slot) gets an undefined row.
+ * Replaces the host-side `s.hist[:-1] = s.hist[1:]; s.hist[-1] = cb0` and `frames += 1` (maya3/engine.py:579,
+ * 585-586). */
+int m3x_hist_push(int32_t* hist, long ld_hist, int64_t* frames, const int64_t* slots, const int64_t* codes,
+                  long ld_codes, int B, int hist_len, void* stream);
+
+/* out[r] = 0 (no loop), -1 (stall) or p (period) for history row slots[r] of W (newest last) with n[slots[r]]
+ * frames (row r and n[r] when slots is NULL), with the
+ * rules of loop_detect_batch: stall = the last `stall` codes all equal, given n >= max(12, stall); period = the
+ * smallest p in [pmin, pmax] whose match fraction over the last period_win codes (count / (period_win - p), in
+ * float64) is >= period_thr, given n >= max(12, stall, period_win). Limits: 1 <= stall <= 64, 2 <= period_win <= 64,
+ * both <= hist_len; 1 <= pmin <= pmax < period_win.
+ * Replaces `loop_detect_batch` (maya3/guards.py:80-107), which the engine runs on the host after the tick's copy. */
+int m3x_loop_guard(const int32_t* W, long ld_w, const int64_t* slots, const int64_t* n, int32_t* out, int rows,
+                   int hist_len, int stall, int period_win, double period_thr, int pmin, int pmax, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

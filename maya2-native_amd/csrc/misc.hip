@@ -119,5 +119,102 @@ M3X_API int m3x_ctr_add(int32_t* ctr, const int64_t* slots, int B, void* stream)
   return M3X_OK;
 }
 
+// ---------------------------------------------------------------------------------------------------------
+// Loop guard (maya3/guards.py:80-107 loop_detect_batch; engine tick maya3/engine.py:594-617), on the device so the
+// check needs no host copy of the code history.
+//
+// hist_push: the history row of slot slots[b] (hist_len codes, oldest first, -1 = empty) shifts left by one and
+// takes codes[b * ld_codes] as its newest entry (maya3/engine.py:585-586), and frames[slots[b]] (if given) counts the
+// frame. One wave per seat; every lane reads its entries before any lane writes. Rows repeated within one call
+// (the padding rows of a graph bucket, all on the dummy slot) race: that slot's row is scratch.
+__global__ __launch_bounds__(64) void hist_push_kernel(int32_t* hist, long ld_hist, int64_t* frames,
+                                                       const int64_t* __restrict__ slots,
+                                                       const int64_t* __restrict__ codes, long ld_codes, int hist_len) {
+  const int b = blockIdx.x;
+  const long s = slots[b];
+  int32_t* row = hist + s * ld_hist;
+  const int l = threadIdx.x;
+  if (frames && l == 0) frames[s] = frames[s] + 1;
+  int32_t v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int i = l + 64 * e;
+    v[e] = i + 1 < hist_len ? row[i + 1] : (i + 1 == hist_len ? (int32_t)codes[(long)b * ld_codes] : 0);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int i = l + 64 * e;
+    if (i < hist_len) row[i] = v[e];
+  }
+}
+
+M3X_API int m3x_hist_push(int32_t* hist, long ld_hist, int64_t* frames, const int64_t* slots, const int64_t* codes,
+                          long ld_codes, int B, int hist_len, void* stream) {
+  if (B < 0 || hist_len <= 0 || hist_len > 256 || ld_hist < hist_len || ld_codes < 1) return M3X_EINVAL;
+  if (B == 0) return M3X_OK;
+  if (!hist || !slots || !codes) return M3X_ENULL;
+  hipLaunchKernelGGL(hist_push_kernel, dim3(B), dim3(64), 0, (hipStream_t)stream, hist, ld_hist, frames, slots, codes,
+                     ld_codes, hist_len);
+  M3X_CHECK_LAUNCH();
+  return M3X_OK;
+}
+
+// loop_guard: row slots[r] of W (hist_len codes, newest last) with n[slots[r]] frames (row r and n[r] when slots is
+// NULL) ->
+//   out[r] = 0 (no loop), -1 (stall: the last `stall` codes all equal the first of them, n >= max(12, stall)) or p
+//   (period: with win = the last period_win codes, the fraction of i < period_win - p with win[i + p] == win[i] is
+//   >= period_thr, for the smallest p in pmin..pmax; needs n >= max(12, stall, period_win)). The fraction is the
+//   reference's float64 mean, count / (period_win - p). One wave per row.
+__global__ __launch_bounds__(64) void loop_guard_kernel(const int32_t* __restrict__ W, long ld_w,
+                                                        const int64_t* __restrict__ slots,
+                                                        const int64_t* __restrict__ n, int32_t* __restrict__ out,
+                                                        int hist_len, int stall, int period_win, double period_thr,
+                                                        int pmin, int pmax) {
+  const int r = blockIdx.x;
+  const int l = threadIdx.x;
+  const long src = slots ? slots[r] : (long)r;
+  const int32_t* row = W + src * ld_w;
+  const long frames = n[src];
+  const int st0 = hist_len - stall;
+  const int32_t first = row[st0];
+  const bool same = l >= stall || row[st0 + l] == first;
+  const bool is_stall = __ballot(!same) == 0ull;
+  const int w0 = hist_len - period_win;
+  const int32_t wl = l < period_win ? row[w0 + l] : 0;
+  int hit = 0;
+  for (int p = pmin; p <= pmax && hit == 0; ++p) {
+    const int m = period_win - p;
+    const int32_t wp = l + p < period_win ? row[w0 + l + p] : 0;
+    const int count = __popcll(__ballot(l < m && wp == wl));
+    if ((double)count / (double)m >= period_thr) hit = p;
+  }
+  if (l == 0) {
+    const long need = stall > 12 ? stall : 12;
+    const long need_p = period_win > need ? period_win : need;
+    int code = 0;
+    if (frames >= need) {
+      if (is_stall) code = -1;
+      else if (frames >= need_p && hit) code = hit;
+    }
+    out[r] = code;
+  }
+}
+
+M3X_API int m3x_loop_guard(const int32_t* W, long ld_w, const int64_t* slots, const int64_t* n, int32_t* out,
+                           int rows, int hist_len, int stall, int period_win, double period_thr, int pmin, int pmax,
+                           void* stream) {
+  if (rows < 0 || hist_len <= 0 || ld_w < hist_len) return M3X_EINVAL;
+  if (stall < 1 || stall > 64 || stall > hist_len || period_win < 2 || period_win > 64 || period_win > hist_len)
+    return M3X_EINVAL;
+  if (pmin < 1 || pmax < pmin || pmax >= period_win) return M3X_EINVAL;
+  if (rows == 0) return M3X_OK;
+  if (!W || !n || !out) return M3X_ENULL;
+  hipLaunchKernelGGL(loop_guard_kernel, dim3(rows), dim3(64), 0, (hipStream_t)stream, W, ld_w, slots, n, out,
+                     hist_len, stall, period_win, period_thr, pmin, pmax);
+  M3X_CHECK_LAUNCH();
+  return M3X_OK;
+}
+
 // The library's version, so a host binding can check it loaded the build it expects.
-M3X_API int m3x_version(void) { return 5; }
+M3X_API int m3x_version(void) { return 6; }

@@ -17,12 +17,15 @@ N_CODEBOOKS = 32
 
 
 class FrameStep:
-    def __init__(self, backbone, cb0, depth, ring_depth=64):
-        """backbone: m3x StaticBackbone; cb0: Cb0Sampler; depth: m3x FastDepth (same dtype as the backbone)."""
+    def __init__(self, backbone, cb0, depth, ring_depth=64, guard=None):
+        """backbone: m3x StaticBackbone; cb0: Cb0Sampler; depth: m3x FastDepth (same dtype as the backbone);
+        guard: an optional m3x.guards.LoopGuard. With it each frame appends the seats' cb0 codes to their device
+        histories and writes each seat's loop-guard code (0, -1 stall, p period) to the buffer set's `loop`
+        (maya3/engine.py:585-617 evaluates the rule on the host after the tick's copy)."""
         lib()
         if depth.dtype != backbone.dtype:
             raise ValueError('the frame graph runs the depth in the backbone dtype')
-        self.bb, self.cb0, self.depth = backbone, cb0, depth
+        self.bb, self.cb0, self.depth, self.guard = backbone, cb0, depth, guard
         dev = backbone.device
         S = backbone.max_slots
         self.feedback = torch.zeros(S + 1, backbone.hidden, dtype=backbone.dtype, device=dev)
@@ -40,6 +43,7 @@ class FrameStep:
         # one slot index tensor for every stage
         cb.slots = bb.slots
         dp.slots = bb.slots
+        cb.loop = torch.zeros(B, dtype=torch.int32, device=self.bb.device)
         return bb, cb, dp, codes
 
     def run(self, bufs):
@@ -47,6 +51,9 @@ class FrameStep:
         ops.copy_rows(self.feedback, bb.x, src_idx=bb.slots)
         self.bb.forward(bb)
         self.cb0.run(cb)
+        if self.guard is not None:
+            self.guard.push(bb.slots, cb.cb0)
+            self.guard.detect(bb.slots, cb.loop)
         self.depth.run(dp)
         ops.code_ring_write(codes, self.ring, self.ring_head, bb.rows)
         ops.copy_rows(dp.feedback, self.feedback, dst_idx=bb.slots)
@@ -60,8 +67,10 @@ class FrameStep:
         g = {'bufs': bufs, 'graph': None, 'last': None}
         if use_graph:
             # warm-up replays touch only the dummy slot; restore every per-slot counter they move
-            saved = [t.clone() for t in (self.bb.lengths, self.cb0.ctr_t, self.cb0.hist_t, self.cb0.frames_t,
-                                         self.cb0.hazard_t, self.depth.row_ctr, self.ring_head)]
+            state = [self.bb.lengths, self.cb0.ctr_t, self.cb0.hist_t, self.cb0.frames_t, self.cb0.hazard_t,
+                     self.depth.row_ctr, self.ring_head] + ([self.guard.hist, self.guard.frames]
+                                                            if self.guard is not None else [])
+            saved = [t.clone() for t in state]
             stream = torch.cuda.Stream()
             stream.wait_stream(torch.cuda.current_stream())
             with torch.cuda.stream(stream):
@@ -73,8 +82,7 @@ class FrameStep:
             with torch.cuda.graph(graph, pool=self.pool, stream=stream):
                 self.run(bufs)
             torch.cuda.synchronize()
-            for t, v in zip((self.bb.lengths, self.cb0.ctr_t, self.cb0.hist_t, self.cb0.frames_t, self.cb0.hazard_t,
-                             self.depth.row_ctr, self.ring_head), saved):
+            for t, v in zip(state, saved):
                 t.copy_(v)
             g['graph'] = graph
         self.graphs[key] = g

@@ -14,6 +14,7 @@ Follows, op for op:
                   from GROUP_OF_LEVEL (tts/model/depth_v2.py:45); last trunk layer only at the last position at a
                   group start; sampling by the C oracle's top-k contract on the bf16/fp16 head logits.
   feedback        serve/fast_depth.py:200-203 + tts/model/audio_io.py:27-35.
+  loop_detect_batch  maya3/guards.py:80-107 (the engine's stall / period loop guard).
 Parity of each piece is pinned in tests/test_oracle_models.py (HF decoder layer, incremental-vs-full depth,
 closed forms).
 """
@@ -246,3 +247,31 @@ def cb0_step(head_w, h, u, temp, top_k, aeos=-1):
     out = [coracle.cb0_sample(bits[b], aeos, temp, top_k, 0.0, 0.0, None, None, 0, None, None, float(u[b]))[0]
            for b in range(h.shape[0])]
     return torch.tensor(out, dtype=torch.long), logits
+
+
+def loop_detect_batch(W, n, stall=32, period_win=64, period_thr=0.7, pmin=2, pmax=16):
+    """The engine's loop guard (maya3/guards.py:80-107): W [S, hist] int (newest last, -1 = empty), n [S] frames.
+    A row stalls when its last `stall` codes all equal the first of them (n >= max(12, stall)); otherwise it has
+    period p for the smallest p in pmin..pmax whose lag-p match fraction over the last period_win codes, a float64
+    mean, reaches period_thr (n >= max(12, stall, period_win)). Returns None | 'stall' | 'period:<p>' per row."""
+    W = np.asarray(W)
+    n = np.asarray(n)
+    out = []
+    for i in range(W.shape[0]):
+        row, frames = W[i], int(n[i])
+        if frames < max(12, stall):
+            out.append(None)
+            continue
+        tail = row[-stall:]
+        if np.all(tail == tail[0]):
+            out.append("stall")
+            continue
+        hit = None
+        if frames >= max(12, stall, period_win):
+            win = row[-period_win:]
+            for p in range(pmin, pmax + 1):
+                if np.mean(win[p:] == win[:-p]) >= period_thr:
+                    hit = p
+                    break
+        out.append(None if hit is None else f"period:{hit}")
+    return out

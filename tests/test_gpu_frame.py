@@ -82,3 +82,38 @@ def test_frame_cb0_matches_oracle_sampler(gpu):
         assert u == cbuf.u[b, 0].item()
         ref, _ = C.cb0_sample(logits[b], -1, 0.9, 50, 0.0, 0.0, None, None, 0, None, None, u)
         assert ref == codes[b, 0].item() == cbuf.cb0[b].item()
+
+
+def test_frame_loop_guard_in_graph(gpu):
+    """With a LoopGuard, every replay appends the seats' cb0 codes to their device histories, counts the frame and
+    writes each seat's loop code; the histories equal the cb0 column of the code ring and the codes equal the
+    oracle's rule (maya3/guards.py:80-107) on those histories."""
+    from types import SimpleNamespace
+    from m3x.guards import LoopGuard
+    from oracle import torch_oracle as O
+    fs = _frame(gpu, seed=71)
+    cfg = SimpleNamespace(stall=4, period_win=8, period_thr=0.5, pmin=2, pmax=4, hist=12)
+    fs.guard = LoopGuard(S, cfg, device=gpu)
+    slots = [2, 0, 5]
+    with torch.inference_mode():
+        g = fs.capture(4, CAP)
+        fs.set_slots(g, slots)
+        seen = {s: [] for s in slots}
+        for t in range(16):
+            fs.replay(g)
+            torch.cuda.synchronize()
+            cb0 = fs.codes(g)[:, 0].cpu().tolist()
+            for i, s in enumerate(slots):
+                seen[s].append(cb0[i])
+            loop = g['bufs'][1].loop[:3].cpu().tolist()
+            W = np.full((3, 12), -1)
+            for i, s in enumerate(slots):
+                h = seen[s][-12:]
+                W[i, 12 - len(h):] = h
+            want = O.loop_detect_batch(W, np.full(3, t + 1), 4, 8, 0.5, 2, 4)
+            got = [None if c == 0 else ("stall" if c < 0 else f"period:{c}") for c in loop]
+            assert got == want, t
+        hist = fs.guard.hist.cpu().numpy()
+        for i, s in enumerate(slots):
+            assert hist[s].tolist() == seen[s][-12:]
+        assert fs.guard.frames[slots].cpu().tolist() == [16] * 3

@@ -7,6 +7,7 @@ import torch
 
 from helpers import bf16_bits, close, from_bits
 from oracle import coracle as C
+from oracle import torch_oracle as O
 
 pytestmark = pytest.mark.gpu
 
@@ -567,3 +568,74 @@ def test_index_kernels(gpu):
     ctr = torch.zeros(6, dtype=torch.int32, device=gpu)
     ops.ctr_add(ctr, torch.tensor([1, 5, 5, 0], device=gpu))
     assert ctr.tolist() == [1, 1, 0, 0, 0, 2]
+
+
+# ---------------------------------------------------------------- loop guard (bit-exact vs the oracle)
+def _guard_cfg(**kw):
+    from types import SimpleNamespace
+    d = dict(stall=32, period_win=64, period_thr=0.7, pmin=2, pmax=16, hist=96)
+    d.update(kw)
+    return SimpleNamespace(**d)
+
+
+def test_loop_guard_matches_oracle(gpu):
+    """m3x.guards.loop_detect_batch == the oracle's restatement of maya3/guards.py:80-107, row for row, on random
+    histories with planted stalls, exact and noisy periods, empty entries and frame counts around the thresholds."""
+    from m3x import guards
+    rng = np.random.default_rng(5)
+    rows, ns = [], []
+    for i in range(400):
+        kind = i % 5
+        row = rng.integers(0, 64 if kind == 4 else 2048, 96)
+        if kind == 1:
+            row[-32:] = row[-32]
+        elif kind == 2:
+            p = int(rng.integers(2, 17))
+            pat = rng.integers(0, 2048, p)
+            row = np.tile(pat, 96 // p + 1)[:96]
+            flips = rng.random(96) < rng.uniform(0, 0.4)
+            row = np.where(flips, rng.integers(0, 2048, 96), row)
+        elif kind == 3:
+            row[:int(rng.integers(0, 96))] = -1
+        rows.append(row)
+        ns.append(int(rng.choice([0, 11, 12, 31, 32, 33, 63, 64, 65, 500])))
+    W, n = np.stack(rows), np.array(ns)
+    for cfg in (_guard_cfg(), _guard_cfg(stall=16, period_win=48, period_thr=0.55, pmin=3, pmax=12)):
+        got = guards.loop_detect_batch(W, n, cfg)
+        want = O.loop_detect_batch(W, n, cfg.stall, cfg.period_win, cfg.period_thr, cfg.pmin, cfg.pmax)
+        assert got == want
+        assert "stall" in got and None in got and any(g and g.startswith("period") for g in got)
+
+
+def test_loop_guard_device_history(gpu):
+    """LoopGuard keeps each slot's history on the device (push = the engine's shift-and-append) and detect() on a
+    subset of slots equals the oracle run on the host-kept histories."""
+    from m3x import guards
+    cfg = _guard_cfg()
+    S = 6
+    lg = guards.LoopGuard(S, cfg, device=gpu)
+    host = np.full((S + 1, 96), -1, dtype=np.int64)
+    frames = np.zeros(S + 1, dtype=np.int64)
+    rng = np.random.default_rng(6)
+    out = torch.empty(4, dtype=torch.int32, device=gpu)
+    for t in range(120):
+        slots = [0, 2, 3, 5] if t % 3 else [0, 2, 3, 5, 1]
+        codes = rng.integers(0, 2048, len(slots))
+        codes[0] = 9                     # slot 0 stalls
+        codes[1] = (t % 4) * 100         # slot 2 loops with period 4
+        if t == 60:  # a new seat on slot 3
+            lg.reset(3)
+            host[3] = -1
+            frames[3] = 0
+        lg.push(torch.tensor(slots, device=gpu), torch.tensor(codes, device=gpu))
+        for s, c in zip(slots, codes):
+            host[s, :-1] = host[s, 1:]
+            host[s, -1] = c
+            frames[s] += 1
+        q = [0, 2, 3, 5]
+        lg.detect(torch.tensor(q, device=gpu), out)
+        want = O.loop_detect_batch(host[q], frames[q])
+        got = [None if c == 0 else ("stall" if c < 0 else f"period:{c}") for c in out.cpu().tolist()]
+        assert got == want, t
+    assert torch.equal(lg.hist.cpu().long(), torch.from_numpy(host))
+    assert torch.equal(lg.frames.cpu(), torch.from_numpy(frames))
