@@ -211,6 +211,28 @@ def secondary(torch, bb, dm, steps):
     log(f"loop guard, {Bg} seats: {gpu_us:.2f} us on the GPU (push + rule), {cpu_us:.0f} us on the host")
     del lg
 
+    # the tick's readout for 224 seats: stop, cb0, loop code, 32 codes and 1920 PCM samples packed by one kernel
+    # and copied to pinned host memory in one transfer (maya3/engine.py:558-563), wall time to the host
+    from m3x.tick import TickReadout
+    rd = TickReadout(Bg, frame=1920, nq=32, with_loop=True, device=dev)
+    tstop = torch.zeros(Bg, dtype=torch.int64, device=dev)
+    tcb0 = torch.randint(0, 2048, (Bg,), device=dev, generator=g)
+    tcodes = torch.randint(0, 2048, (Bg, 32), device=dev, generator=g).to(torch.int32)
+    tpcm = torch.randn(Bg, 1920, device=dev, generator=g) * 0.3
+    ts = []
+    for i in range(22):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        rd.pack(tstop, tcb0, gout, tcodes, tpcm)
+        rd.wait()
+        if i >= 2:
+            ts.append(time.perf_counter() - t0)
+    out["tick_readout"] = {"seats": Bg, "bytes": Bg * rd.width * 8,
+                           "us": round(sorted(ts)[len(ts) // 2] * 1e6, 1),
+                           "note": "one pack kernel + one pinned D2H copy + event wait, median wall time"}
+    log(f"tick readout, {Bg} seats ({Bg * rd.width * 8 / 1e3:.0f} kB): {out['tick_readout']['us']:.0f} us")
+    del rd
+
     # time to first audio: a 512-token prompt prefilled onto one empty seat through the graphed inline-prefill
     # step (StaticBackbone.prefill), beside the eager HF forward the engine falls back to (maya3/engine.py:497-502)
     Tp = 512

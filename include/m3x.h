@@ -214,6 +214,19 @@ int m3x_hist_push(int32_t* hist, long ld_hist, int64_t* frames, const int64_t* s
 int m3x_loop_guard(const int32_t* W, long ld_w, const int64_t* slots, const int64_t* n, int32_t* out, int rows,
                    int hist_len, int stall, int period_win, double period_thr, int pmin, int pmax, void* stream);
 
+/* ---- tick readout (maya3/engine.py:558-563) ---------------------------------------------------------------- */
+
+/* int64 words per seat of m3x_tick_pack's row: 2 + with_loop + ceil(nq / 2) + ceil(frame / 4). */
+int m3x_tick_pack_width(int with_loop, int nq, int frame);
+
+/* Row b of out (ld_out int64 words): [stop[b], cb0[b], loop[b] (if loop), the nq codes of codes row b two int32 per
+ * word, low first (if codes), frame PCM samples of pcm row b as int16(rint(clamp(x, -1, 1) * 32767)) four per word,
+ * lowest first (if pcm)], for one pinned host copy per tick.
+ * Replaces `pcm16 = (pcm.clamp(-1, 1) * 32767).round().to(torch.int16); packed = torch.cat([code, cb0, pcm16...])`
+ * (maya3/engine.py:558-560). */
+int m3x_tick_pack(const int64_t* stop, const int64_t* cb0, const int32_t* loop, const int32_t* codes, long ld_codes,
+                  int nq, const float* pcm, long ld_pcm, int frame, int64_t* out, long ld_out, int B, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -216,5 +216,69 @@ M3X_API int m3x_loop_guard(const int32_t* W, long ld_w, const int64_t* slots, co
   return M3X_OK;
 }
 
+// ---------------------------------------------------------------------------------------------------------
+// Tick readout (maya3/engine.py:558-563): one int64 row per seat for a single pinned host copy,
+//   [stop, cb0, (loop code), (nq codes, two int32 per int64), (frame int16 PCM samples, four per int64)]
+// with pcm16 = int16(rint(clamp(pcm, -1, 1) * 32767)) (torch's round is half to even, as rintf). Optional parts are
+// left out when their pointer is NULL. One workgroup per seat.
+__global__ __launch_bounds__(256) void tick_pack_kernel(const int64_t* __restrict__ stop,
+                                                        const int64_t* __restrict__ cb0,
+                                                        const int32_t* __restrict__ loop,
+                                                        const int32_t* __restrict__ codes, long ld_codes, int nq,
+                                                        const float* __restrict__ pcm, long ld_pcm, int frame,
+                                                        int64_t* __restrict__ out, long ld_out) {
+  const int b = blockIdx.x;
+  int64_t* row = out + (long)b * ld_out;
+  int col = 2;
+  if (threadIdx.x == 0) {
+    row[0] = stop[b];
+    row[1] = cb0[b];
+  }
+  if (loop) {
+    if (threadIdx.x == 0) row[col] = loop[b];
+    col += 1;
+  }
+  if (codes) {
+    for (int i = threadIdx.x; 2 * i < nq; i += blockDim.x) {
+      const uint32_t lo = (uint32_t)codes[(long)b * ld_codes + 2 * i];
+      const uint32_t hi = 2 * i + 1 < nq ? (uint32_t)codes[(long)b * ld_codes + 2 * i + 1] : 0u;
+      row[col + i] = (int64_t)(((uint64_t)hi << 32) | lo);
+    }
+    col += (nq + 1) / 2;
+  }
+  if (pcm) {
+    const float* p = pcm + (long)b * ld_pcm;
+    for (int i = threadIdx.x; 4 * i < frame; i += blockDim.x) {
+      uint64_t v = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (4 * i + e < frame) {
+          const float x = fminf(fmaxf(p[4 * i + e], -1.0f), 1.0f) * 32767.0f;
+          v |= (uint64_t)(uint16_t)(int16_t)rintf(x) << (16 * e);
+        }
+      }
+      row[col + i] = (int64_t)v;
+    }
+  }
+}
+
+M3X_API int m3x_tick_pack_width(int with_loop, int nq, int frame) {
+  if (nq < 0 || frame < 0) return -1;
+  return 2 + (with_loop ? 1 : 0) + (nq + 1) / 2 + (frame + 3) / 4;
+}
+
+M3X_API int m3x_tick_pack(const int64_t* stop, const int64_t* cb0, const int32_t* loop, const int32_t* codes,
+                          long ld_codes, int nq, const float* pcm, long ld_pcm, int frame, int64_t* out, long ld_out,
+                          int B, void* stream) {
+  if (B < 0 || (codes && (nq <= 0 || ld_codes < nq)) || (pcm && (frame <= 0 || ld_pcm < frame))) return M3X_EINVAL;
+  if (B == 0) return M3X_OK;
+  if (!stop || !cb0 || !out) return M3X_ENULL;
+  if (ld_out < m3x_tick_pack_width(loop != nullptr, codes ? nq : 0, pcm ? frame : 0)) return M3X_EINVAL;
+  hipLaunchKernelGGL(tick_pack_kernel, dim3(B), dim3(256), 0, (hipStream_t)stream, stop, cb0, loop, codes, ld_codes,
+                     codes ? nq : 0, pcm, ld_pcm, pcm ? frame : 0, out, ld_out);
+  M3X_CHECK_LAUNCH();
+  return M3X_OK;
+}
+
 // The library's version, so a host binding can check it loaded the build it expects.
-M3X_API int m3x_version(void) { return 6; }
+M3X_API int m3x_version(void) { return 7; }

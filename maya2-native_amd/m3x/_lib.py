@@ -12,7 +12,7 @@ import os
 import torch  # noqa: F401  (must precede the CDLL load, see above)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libm3x.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -54,6 +54,8 @@ SIGNATURES = {
     "m3x_code_ring_write": (_I, [_P, _L, _P, _P, _I, _I, _I, _I, _P]),
     "m3x_hist_push": (_I, [_P, _L, _P, _P, _P, _L, _I, _I, _P]),
     "m3x_loop_guard": (_I, [_P, _L, _P, _P, _P, _I, _I, _I, _I, ctypes.c_double, _I, _I, _P]),
+    "m3x_tick_pack_width": (_I, [_I, _I, _I]),
+    "m3x_tick_pack": (_I, [_P, _P, _P, _P, _L, _I, _P, _L, _I, _P, _L, _I, _P]),
 }
 
 STATUS = {0: "ok", -1: "invalid argument", -2: "null pointer", -3: "workspace too small", -4: "launch failed",

@@ -113,3 +113,12 @@ class FrameStep:
 
     def codes(self, g):
         return g['bufs'][3]
+
+    def readout(self, g, rd, B=None, pcm=None):
+        """Starts the tick's one host copy (m3x.tick.TickReadout rd, built with nq = 32 and with_loop = whether
+        this frame has a guard): stop codes, cb0, loop codes, the 32 codes of the first B rows, and the seats' PCM
+        rows if given (maya3/engine.py:558-563)."""
+        bb, cb, dp, codes = g['bufs']
+        B = bb.rows if B is None else B
+        rd.pack(cb.stop[:B], cb.cb0[:B], cb.loop[:B] if self.guard is not None else None, codes[:B],
+                None if pcm is None else pcm[:B])

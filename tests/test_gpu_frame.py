@@ -117,3 +117,23 @@ def test_frame_loop_guard_in_graph(gpu):
         for i, s in enumerate(slots):
             assert hist[s].tolist() == seen[s][-12:]
         assert fs.guard.frames[slots].cpu().tolist() == [16] * 3
+
+
+def test_frame_readout_matches_buffers(gpu):
+    """FrameStep.readout copies the frame's stop codes, cb0 and 32 codes (and PCM rows given by the caller) to the
+    host in one transfer, equal to the graph's own buffers."""
+    from m3x.tick import TickReadout
+    fs = _frame(gpu, seed=81)
+    rd = TickReadout(4, frame=1920, nq=32, with_loop=False, device=gpu)
+    with torch.inference_mode():
+        g = fs.capture(4, CAP)
+        fs.set_slots(g, [1, 6])
+        fs.replay(g)
+        pcm = torch.rand(4, 1920, device=gpu) * 2.4 - 1.2
+        fs.readout(g, rd, B=2, pcm=pcm)
+        got = rd.wait()
+        bb, cb, dp, codes = g['bufs']
+        assert got["cb0"].tolist() == cb.cb0[:2].cpu().tolist()
+        assert got["stop"].tolist() == cb.stop[:2].cpu().tolist()
+        assert np.array_equal(got["codes"], codes[:2].cpu().numpy())
+        assert np.array_equal(got["pcm"], (pcm[:2].cpu().clamp(-1, 1) * 32767).round().to(torch.int16).numpy())

@@ -639,3 +639,33 @@ def test_loop_guard_device_history(gpu):
         assert got == want, t
     assert torch.equal(lg.hist.cpu().long(), torch.from_numpy(host))
     assert torch.equal(lg.frames.cpu(), torch.from_numpy(frames))
+
+
+# ---------------------------------------------------------------- tick readout (bit-exact vs the engine's torch ops)
+@pytest.mark.parametrize("nq,frame,with_loop", [(32, 1920, True), (0, 1920, False), (31, 0, True), (0, 7, False)])
+def test_tick_readout_packs_like_the_engine(gpu, nq, frame, with_loop):
+    """One packed row per seat, read back through one pinned copy: stop, cb0, loop and codes verbatim, and the PCM
+    equal to the engine's `(pcm.clamp(-1, 1) * 32767).round().to(torch.int16)` (maya3/engine.py:559) bit for bit,
+    including out-of-range samples and values that round half to even."""
+    from m3x.tick import TickReadout
+    g = _g(nq + frame)
+    B = 5
+    stop = torch.randint(0, 5, (B,), generator=g)
+    cb0 = torch.randint(0, 2049, (B,), generator=g)
+    loop = torch.randint(-1, 17, (B,), generator=g).to(torch.int32)
+    codes = torch.randint(0, 2048, (B, 40), generator=g).to(torch.int32)
+    pcm = (torch.randn(B, max(frame, 1), generator=g) * 0.6).float()
+    if frame >= 8:
+        pcm[0, :8] = torch.tensor([1.5, -3.0, 1.0, -1.0, 0.0, -0.0, 0.5 / 32767, 2.5 / 32767])
+    rd = TickReadout(8, frame=frame, nq=nq, with_loop=with_loop, device=gpu)
+    rd.pack(stop.to(gpu), cb0.to(gpu), loop.to(gpu) if with_loop else None,
+            codes[:, :nq].to(gpu) if nq else None, pcm[:, :frame].to(gpu).contiguous() if frame else None)
+    got = rd.wait()
+    assert got["stop"].tolist() == stop.tolist() and got["cb0"].tolist() == cb0.tolist()
+    if with_loop:
+        assert got["loop"].tolist() == loop.tolist()
+    if nq:
+        assert np.array_equal(got["codes"], codes[:, :nq].numpy())
+    if frame:
+        want = (pcm[:, :frame].clamp(-1, 1) * 32767).round().to(torch.int16).numpy()
+        assert np.array_equal(got["pcm"], want)
