@@ -172,3 +172,50 @@ def c5_lengths(B, seed=5, mean=2048, cap=4096):
 def uniforms(shape, seed=7):
     g = torch.Generator().manual_seed(seed)
     return torch.rand(*shape, generator=g, dtype=torch.float32)
+
+
+def mimi(seed=0, device="cpu", dtype=torch.float32):
+    """A Mimi codec (transformers MimiModel, default MimiConfig: 32 codebooks of 2048 x 256, an 8-layer 512-wide
+    sliding-window decoder transformer, SEANet decoder with ratios 8/6/5/4, 1920 samples per 12.5 Hz frame) with
+    seeded random weights: codebook rows N(0, 1); every conv and linear weight N(0, 1 / fan_in); biases and the
+    norms' affine terms N(0, 0.02) around their init; layer scales 0.1. There is no network for the kyutai weights."""
+    from transformers import MimiConfig, MimiModel
+    g = torch.Generator().manual_seed(seed)
+    m = MimiModel(MimiConfig()).eval()
+    with torch.no_grad():
+        for name, p in m.named_parameters():
+            if name.endswith("layer_scale.scale") or name.endswith("_layer_scale.scale"):
+                p.fill_(0.1)
+            elif p.dim() >= 2:
+                mod = _owner(m, name)
+                if isinstance(mod, torch.nn.ConvTranspose1d):  # [C_in, C_out / groups, k]: inputs per output
+                    fan_in = max(1, p.shape[0] // mod.groups * p.shape[2] // mod.stride[0])
+                else:
+                    fan_in = p[0].numel()
+                p.copy_(torch.randn(p.shape, generator=g) / math.sqrt(fan_in))
+            elif name.endswith("weight"):  # norm scales
+                p.copy_(1 + 0.02 * torch.randn(p.shape, generator=g))
+            else:  # biases
+                p.copy_(0.02 * torch.randn(p.shape, generator=g))
+        for name, b in m.named_buffers():
+            if name.endswith("embed_sum"):
+                b.copy_(torch.randn(b.shape, generator=g))
+            elif name.endswith("cluster_usage"):
+                b.fill_(1.0)
+        for mod in m.modules():
+            if hasattr(mod, "_embed"):
+                mod._embed = None
+    return m.to(device=device, dtype=dtype)
+
+
+def _owner(model, pname):
+    mod = model
+    for part in pname.split(".")[:-1]:
+        mod = getattr(mod, part)
+    return mod
+
+
+def mimi_codes(B, frames, seed=0):
+    """Uniform codes [B, 32, frames] in [0, 2048)."""
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(0, 2048, (B, 32, frames), generator=g)
