@@ -258,7 +258,63 @@ def secondary(torch, bb, dm, steps):
     log(f"prefill of {Tp} tokens: {pre_ms:.2f} ms (HF eager: {out['ttfa_prefill'].get('hf_eager_ms')})")
     del sb
     torch.cuda.empty_cache()
+    out["mimi_decode"] = mimi_decode(torch, dev, max(steps, 20))
     return out
+
+
+def mimi_decode(torch, dev, steps):
+    """One 80 ms Mimi frame per seat (32 codes -> 1920 PCM samples) through StaticMimi's graph at 1 and 64 seats
+    (HIP-event time of the replay, and the wall time of decode() with its slot/code uploads and the owned
+    output), beside one frame of the fp32 streaming oracle on the host at one seat."""
+    from m3x import synth
+    from m3x.serve.fast_codec import StaticMimi
+    from oracle.mimi_oracle import MimiStream
+    sm = StaticMimi(synth.mimi(seed=7, device=dev), 96, batch_buckets=(1, 64))
+    res = {}
+    stream = torch.cuda.current_stream()
+    with torch.inference_mode():
+        sm.warmup()
+        for B in (1, 64):
+            codes = synth.mimi_codes(B, 1, seed=8)[:, :, 0].to(dev)
+            slots = list(range(B))
+            for _ in range(3):
+                sm.decode(slots, codes)
+            bucket = sm._buckets[B]
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record(stream)
+            for _ in range(steps):
+                bucket.graph.replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            gpu_ms = e0.elapsed_time(e1) / steps
+            ts = []
+            for _ in range(steps):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                sm.decode(slots, codes)
+                torch.cuda.synchronize()
+                ts.append(time.perf_counter() - t0)
+            wall_ms = sorted(ts)[len(ts) // 2] * 1e3
+            res[f"b{B}"] = {"seats": B, "graph_ms": round(gpu_ms, 4), "decode_wall_ms": round(wall_ms, 4),
+                            "frames_per_s": round(B / gpu_ms * 1e3, 1),
+                            "realtime_x": round(B * 80.0 / gpu_ms, 1)}
+            log(f"Mimi decode, {B} seats: {gpu_ms:.3f} ms per frame in the graph, decode() {wall_ms:.3f} ms wall")
+    del sm
+    torch.cuda.empty_cache()
+    mc = synth.mimi(seed=7)
+    st = MimiStream(mc, 1)
+    c = synth.mimi_codes(1, 4, seed=8)
+    with torch.no_grad():
+        st.decode_frame(c[:, :, 0])
+        t0 = time.perf_counter()
+        for t in range(1, 4):
+            st.decode_frame(c[:, :, t])
+    res["cpu_oracle_ms_b1"] = round((time.perf_counter() - t0) / 3 * 1e3, 2)
+    res["cpu_cores"] = torch.get_num_threads()
+    res["note"] = ("StaticMimi computes in float16 with fp32 accumulation (the reference runs Mimi in float32); "
+                   "realtime_x = seconds of audio per second of GPU time; CPU: the fp32 streaming oracle, one seat")
+    return res
 
 
 def _hf_eager_prefill_ms(torch, bb, x, steps):
@@ -385,6 +441,7 @@ def main():
     ap.add_argument("--no-b1", action="store_true")
     ap.add_argument("--no-secondary", action="store_true", help="skip the C3 / C4 backbone-step lines")
     ap.add_argument("--secondary-steps", type=int, default=5)
+    ap.add_argument("--mimi-only", action="store_true", help="print only the Mimi decode line (for profiling)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -396,6 +453,10 @@ def main():
     from m3x import roofline, synth
     from m3x import ops
     torch.backends.cuda.matmul.allow_tf32 = False
+    if args.mimi_only:
+        print(json.dumps({"mimi_decode": mimi_decode(torch, torch.device("cuda:0"), max(args.secondary_steps, 20))}),
+              flush=True)
+        return
     B = args.batch
     K, W = args.steps, args.warmup
     dev = torch.device("cuda:0")

@@ -227,6 +227,61 @@ int m3x_tick_pack_width(int with_loop, int nq, int frame);
 int m3x_tick_pack(const int64_t* stop, const int64_t* cb0, const int32_t* loop, const int32_t* codes, long ld_codes,
                   int nq, const float* pcm, long ld_pcm, int frame, int64_t* out, long ld_out, int B, void* stream);
 
+/* ---- Mimi one-frame decode (serve/fast_codec.py StaticMimi :32-277) ------------------------------------------
+ * Activations are time-major [seat * T + t, channels], 16-bit with fp32 arithmetic; `slots` names each seat's
+ * state row (padding seats may all name the dummy row, whose contents are scratch). Stateful kernels take a
+ * `chunk` of rows per workgroup that is at least the state's depth. */
+
+/* out[b] = [table_0[codes[b,0]] | dt(sum_{q>=1} table_q[codes[b,q]])] from tables [nq, n_codes, dim]; codes outside
+ * [0, n_codes) are clamped. With one GEMM by [W_semantic | W_acoustic] it replaces `_quantizer`/`_rvq`
+ * (serve/fast_codec.py:134-149). */
+int m3x_rvq_decode(const int64_t* codes, long ld_codes, const void* tables, void* out, long ld_out, int B, int nq,
+                   int n_codes, int dim, int dtype, void* stream);
+
+/* Depthwise transposed conv (kernel k <= 2 s, stride s, no bias) of one frame per seat: out [B * s, C] = the
+ * frame's outputs plus the slot's tail; tail [slot, (k - s) * C] (frames x channels) becomes the new overlap.
+ * Replaces `_layer(self.m.upsample, ...)` (serve/fast_codec.py:112-130,188). */
+int m3x_dwconvt(const void* x, long ld_x, const void* w, void* tail, long ld_tail, const int64_t* slots, void* out,
+                int B, int C, int k, int s, int dtype, void* stream);
+
+/* GEMM rows of a causal conv: cols[b*T + t, j*C + c] = joined[t + j*dil][c], joined = the slot's (k-1)*dil stored
+ * frames then ELU(x) (use_elu) or x; the state becomes joined's last (k-1)*dil frames.
+ * Replaces the MimiConv1d branch of `_layer` (serve/fast_codec.py:104-111) with the ELU in front of it. */
+int m3x_conv_gather(const void* x, long ld_x, void* state, long ld_state, const int64_t* slots, void* cols,
+                    long ld_cols, int B, int T, int C, int k, int dil, int use_elu, int chunk, int dtype,
+                    void* stream);
+
+/* out = act(res + scale * (g + bias)) per row ([rows, C], C % 8 == 0; bias, scale, res optional; act = ELU when
+ * use_elu). Replaces the conv bias add, `shortcut + x` (serve/fast_codec.py:127-130) with the next ELU, and
+ * `h + layer_scale(a)` (:181-182). */
+int m3x_rows_op(const void* g, long ld_g, const void* bias, const void* scale, const void* res, long ld_res,
+                void* out, long ld_out, int rows, int C, int use_elu, int dtype, void* stream);
+
+/* Overlap-add of a transposed conv (kernel k, stride s, s < k <= 2 s) from its GEMM columns cols[b*Tin + t,
+ * j*C + c]: out [B * Tin * s, C] with the slot's tail added to the first k - s frames and bias; the new tail is the
+ * overflow without bias. Replaces the MimiConvTranspose1d branch of `_layer` (serve/fast_codec.py:112-126). */
+int m3x_convt_overlap(const void* cols, long ld_cols, void* tail, long ld_tail, const int64_t* slots,
+                      const void* bias, void* out, long ld_out, int B, int Tin, int C, int k, int s, int chunk,
+                      int dtype, void* stream);
+
+/* Sliding-window attention of T <= 8 new tokens per seat at positions tokens[slot] + t over the slot's ring
+ * (kring/vring [slots, ring, H, 64] post-RoPE, key_pos [slots, ring]); RoPE angle pos * inv_freq[i] (fp32),
+ * cos/sin times rope_scale; ring <= 256, ring >= window + T - 1. Replaces the ring writes, mask, RoPE and SDPA of
+ * `_transformer` (serve/fast_codec.py:157-180). */
+int m3x_ring_attn(const void* qkv, long ld_qkv, void* kring, void* vring, int64_t* key_pos, const int64_t* tokens,
+                  const int64_t* slots, const float* inv_freq, float rope_scale, void* out, long ld_out, int B, int T,
+                  int H, int head_dim, int ring, int window, int dtype, void* stream);
+
+/* tokens[slot] += T for each seat whose slot is not `dummy`, then tokens[dummy] = 0.
+ * Replaces `self.tokens.index_copy_(0, slots, start + count); self.tokens[self.dummy].zero_()` (:183-184). */
+int m3x_advance_tokens(int64_t* tokens, const int64_t* slots, int B, int T, int dummy, void* stream);
+
+/* Last conv (C -> 1 channel, kernel k, causal) to fp32 PCM [B, T] with fp32 weights w[j*C + c] and the slot's
+ * k - 1 stored input frames. Replaces the final MimiConv1d of `_forward` (serve/fast_codec.py:189-191). */
+int m3x_final_conv(const void* x, long ld_x, void* state, long ld_state, const int64_t* slots, const float* w,
+                   float bias, float* pcm, long ld_pcm, int B, int T, int C, int k, int chunk, int dtype,
+                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif

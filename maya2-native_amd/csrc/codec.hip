@@ -1,0 +1,498 @@
+// Mimi one-frame decode (serve/fast_codec.py StaticMimi, :32-277): the kernels around the projections and
+// convolutions, which run as GEMMs on m3x_linear. Activations are time-major [rows = seat * T + t, channels] in
+// 16-bit with fp32 arithmetic. Every stateful layer keeps one row per slot (the reference's conv_flat / kv /
+// key_pos rows); several padding seats of a batch may name the one dummy slot, whose rows are scratch.
+#include "m3x_common.h"
+
+// Stateful kernels split a seat's rows over workgroups (blockIdx.y); the chunk is at least the state's depth, so
+// only chunk 0 reads the old state, and chunk 0 alone writes the new state after a barrier. A thread keeps at
+// most CODEC_KEEP state values across that barrier.
+constexpr int CODEC_THREADS = 256;
+constexpr int CODEC_KEEP = 16;
+constexpr long NEVER_POS = -(1L << 40);  // key_pos of an empty ring entry
+
+__device__ __forceinline__ float elu1(float v) { return v > 0.f ? v : expm1f(v); }
+
+// ---------------------------------------------------------------------------------------------------------
+// RVQ decode (:134-149; transformers MimiSplitResidualVectorQuantizer.decode): out[b, :dim] = table_0[code_0]
+// (the semantic codebook), out[b, dim:] = dt(table_1[code_1] + ... + table_{nq-1}[code_{nq-1}]) summed in fp32 in
+// that order. A GEMM with [W_semantic | W_acoustic] then applies both 1x1 output projections and their sum.
+// Codes outside [0, n_codes) are clamped into it (the reference's embedding lookup raises on them).
+template <int DT>
+__global__ __launch_bounds__(256) void rvq_decode_kernel(const int64_t* __restrict__ codes, long ld_codes,
+                                                         const uint16_t* __restrict__ tables, uint16_t* __restrict__ out,
+                                                         long ld_out, int nq, int n_codes, int dim) {
+  const int b = blockIdx.x;
+  const int64_t* c = codes + (long)b * ld_codes;
+  auto code = [&](int q) -> long { return (long)min(max(c[q], (int64_t)0), (int64_t)(n_codes - 1)); };
+  for (int d = threadIdx.x; d < dim; d += blockDim.x) {
+    out[(long)b * ld_out + d] = tables[code(0) * dim + d];
+    float s = 0.f;
+    for (int q = 1; q < nq; ++q) s += E<DT>::to_f(tables[((long)q * n_codes + code(q)) * dim + d]);
+    out[(long)b * ld_out + dim + d] = E<DT>::from_f(s);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// Upsample (:186-188 -> :112-130): depthwise transposed conv with kernel k <= 2 s, stride s, no bias, one input
+// frame per seat: out[b * s + j, c] = x[b, c] w[c, j] + tail[slot, j, c] (j < k - s); the new tail[slot, j - s, c]
+// = x[b, c] w[c, j] for j >= s. Each thread owns channels, so its tail reads precede its tail writes.
+template <int DT>
+__global__ __launch_bounds__(256) void dwconvt_kernel(const uint16_t* __restrict__ x, long ld_x,
+                                                      const uint16_t* __restrict__ w, uint16_t* tail, long ld_tail,
+                                                      const int64_t* __restrict__ slots, uint16_t* __restrict__ out,
+                                                      int C, int k, int s) {
+  const int b = blockIdx.x;
+  uint16_t* tl = tail + slots[b] * ld_tail;  // [k - s][C]
+  for (int c = threadIdx.x; c < C; c += blockDim.x) {
+    const float xv = E<DT>::to_f(x[(long)b * ld_x + c]);
+    for (int j = 0; j < s; ++j) {
+      const float prev = j < k - s ? E<DT>::to_f(tl[(long)j * C + c]) : 0.f;
+      out[((long)b * s + j) * C + c] = E<DT>::from_f(xv * E<DT>::to_f(w[(long)c * k + j]) + prev);
+    }
+    for (int j = s; j < k; ++j) tl[(long)(j - s) * C + c] = E<DT>::from_f(xv * E<DT>::to_f(w[(long)c * k + j]));
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// Causal conv input as GEMM rows (:104-111): cols[b * T + t, j * C + c] = joined[t + j * dil][c], where joined =
+// the slot's pad = (k - 1) * dil stored frames followed by act(x[b * T + 0 .. T)), act = ELU (alpha 1) when
+// use_elu, the ELU module in front of the conv. The slot's state becomes joined's last pad frames (post-ELU, as
+// the reference stores the conv's own input). Grid (B, ceil(T / chunk)), chunk >= pad; 8 channels per thread.
+template <int DT>
+__device__ __forceinline__ u16x8 joined8(const uint16_t* st, const uint16_t* x, long ld_x, long row0, int pad, int i,
+                                         int c, int C, int use_elu) {
+  if (i < pad) return ld16(st + (long)i * C + c);
+  u16x8 v = ld16(x + (row0 + i - pad) * ld_x + c);
+  if (use_elu) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v.v[e] = E<DT>::from_f(elu1(E<DT>::to_f(v.v[e])));
+  }
+  return v;
+}
+
+template <int DT>
+__global__ __launch_bounds__(CODEC_THREADS) void conv_gather_kernel(const uint16_t* __restrict__ x, long ld_x,
+                                                                    uint16_t* state, long ld_state,
+                                                                    const int64_t* __restrict__ slots,
+                                                                    uint16_t* __restrict__ cols, long ld_cols, int T,
+                                                                    int C, int k, int dil, int use_elu, int chunk) {
+  const int b = blockIdx.x;
+  const int t0 = blockIdx.y * chunk, t1 = min(T, t0 + chunk);
+  const int pad = (k - 1) * dil;
+  const long row0 = (long)b * T;
+  uint16_t* st = pad ? state + slots[b] * ld_state : nullptr;  // [pad][C]
+  const int cv = C / 8, kcv = k * cv;
+  for (int e = threadIdx.x; e < (t1 - t0) * kcv; e += CODEC_THREADS) {
+    const int t = t0 + e / kcv;
+    const int r = e - (t - t0) * kcv;
+    const int j = r / cv, c = 8 * (r - j * cv);
+    st16(cols + (row0 + t) * ld_cols + (long)j * C + c, joined8<DT>(st, x, ld_x, row0, pad, t + j * dil, c, C, use_elu));
+  }
+  if (!pad || blockIdx.y) return;
+  u16x8 keep[CODEC_KEEP / 8];
+  int n = 0;
+  for (int e = threadIdx.x; e < pad * cv; e += CODEC_THREADS)
+    keep[n++] = joined8<DT>(st, x, ld_x, row0, pad, T + e / cv, 8 * (e % cv), C, use_elu);
+  __syncthreads();
+  n = 0;
+  for (int e = threadIdx.x; e < pad * cv; e += CODEC_THREADS) st16(st + 8 * e, keep[n++]);
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// Row op: out = act(res + scale * (g + bias)); bias, scale, res may be NULL; act = ELU (alpha 1) when use_elu.
+// Serves the conv biases (with the resnet shortcut and the ELU that follows it) and the transformer's
+// layer-scaled residuals. C % 8 == 0, 16-byte rows.
+template <int DT>
+__global__ __launch_bounds__(256) void rows_op_kernel(const uint16_t* __restrict__ g, long ld_g,
+                                                      const uint16_t* __restrict__ bias,
+                                                      const uint16_t* __restrict__ scale, const uint16_t* res,
+                                                      long ld_res, uint16_t* out, long ld_out, int rows, int C,
+                                                      int use_elu) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int cv = C / 8;
+  if (i >= (long)rows * cv) return;
+  const long r = i / cv;
+  const int c = 8 * (int)(i - r * cv);
+  const u16x8 gv = ld16(g + r * ld_g + c);
+  u16x8 bv = {}, sv = {}, rv = {}, ov;
+  if (bias) bv = ld16(bias + c);
+  if (scale) sv = ld16(scale + c);
+  if (res) rv = ld16(res + r * ld_res + c);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float v = E<DT>::to_f(gv.v[e]);
+    if (bias) v = v + E<DT>::to_f(bv.v[e]);
+    if (scale) v = E<DT>::to_f(sv.v[e]) * v;
+    if (res) v = E<DT>::to_f(rv.v[e]) + v;
+    if (use_elu) v = elu1(v);
+    ov.v[e] = E<DT>::from_f(v);
+  }
+  st16(out + r * ld_out + c, ov);
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// Transposed conv overlap-add (:112-130). cols[b * Tin + t, j * C + c] = x[b, t] . W[:, c, j] comes from the GEMM;
+// output frame o < Tin * s of seat b is the sum of its contributions (t, j = o - t s, 0 <= j < k) + tail[slot, o, c]
+// (o < k - s) + bias[c]; the new tail[slot, i, c] = the contributions to frame Tin * s + i, without bias (the
+// reference stores its tail bias-free). Grid (B, ceil(Tin * s / chunk)), chunk >= k - s; 8 channels per thread.
+template <int DT>
+__device__ __forceinline__ void convt_frame8(const uint16_t* cols, long ld_cols, long row0, int o, int c, int Tin,
+                                             int C, int k, int s, float (&v)[8]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = 0.f;
+  for (int t = min(o / s, Tin - 1); t >= 0 && o - t * s < k; --t) {
+    const u16x8 w = ld16(cols + (row0 + t) * ld_cols + (long)(o - t * s) * C + c);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] += E<DT>::to_f(w.v[e]);
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(CODEC_THREADS) void convt_overlap_kernel(const uint16_t* __restrict__ cols, long ld_cols,
+                                                                      uint16_t* tail, long ld_tail,
+                                                                      const int64_t* __restrict__ slots,
+                                                                      const uint16_t* __restrict__ bias,
+                                                                      uint16_t* __restrict__ out, long ld_out, int Tin,
+                                                                      int C, int k, int s, int chunk) {
+  const int b = blockIdx.x;
+  const int nout = Tin * s, ov = k - s;
+  const int o0 = blockIdx.y * chunk, o1 = min(nout, o0 + chunk);
+  const long row0 = (long)b * Tin;
+  uint16_t* tl = tail + slots[b] * ld_tail;  // [k - s][C]
+  const int cv = C / 8;
+  for (int e = threadIdx.x; e < (o1 - o0) * cv; e += CODEC_THREADS) {
+    const int o = o0 + e / cv, c = 8 * (e % cv);
+    float v[8];
+    convt_frame8<DT>(cols, ld_cols, row0, o, c, Tin, C, k, s, v);
+    u16x8 tv = {}, bv = {}, r;
+    if (o < ov) tv = ld16(tl + (long)o * C + c);
+    if (bias) bv = ld16(bias + c);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float y = v[i];
+      if (o < ov) y += E<DT>::to_f(tv.v[i]);
+      if (bias) y += E<DT>::to_f(bv.v[i]);
+      r.v[i] = E<DT>::from_f(y);
+    }
+    st16(out + ((long)b * nout + o) * ld_out + c, r);
+  }
+  if (blockIdx.y) return;
+  u16x8 keep[CODEC_KEEP / 8];
+  int n = 0;
+  for (int e = threadIdx.x; e < ov * cv; e += CODEC_THREADS) {
+    float v[8];
+    convt_frame8<DT>(cols, ld_cols, row0, nout + e / cv, 8 * (e % cv), Tin, C, k, s, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) keep[n].v[i] = E<DT>::from_f(v[i]);
+    ++n;
+  }
+  __syncthreads();
+  n = 0;
+  for (int e = threadIdx.x; e < ov * cv; e += CODEC_THREADS) st16(tl + 8 * e, keep[n++]);
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// Decoder transformer attention (:151-184) for T new tokens per seat at positions p = tokens[slot] + t: q and k
+// get RoPE (rotate_half; angle p * inv_freq[i] in fp32, cos and sin times rope_scale), k (post-RoPE) and v go to
+// the slot's ring entry p % ring with key_pos[slot, p % ring] = p; query p attends the entries with
+// p - window < key_pos <= p, softmax at scale 1/sqrt(64). qkv rows [q heads | k heads | v heads] (as many kv heads
+// as heads), head_dim 64.
+// One wave per (seat, head): lanes own ring entries for the scores (each key row read once for all T queries);
+// for P.V lane l takes keys j = l / 8 (mod 8) and dims 8 (l % 8) .. + 7, and the 8 key groups are summed by
+// shuffles. The head-0 wave records key_pos; every wave knows the positions of the entries this call writes, so
+// no wave depends on another's key_pos write.
+constexpr int RA_HD = 64;
+constexpr int RA_RING = 256;
+constexpr int RA_T = 8;
+template <int DT>
+__global__ __launch_bounds__(64) void ring_attn_kernel(const uint16_t* __restrict__ qkv, long ld_qkv,
+                                                       uint16_t* kring, uint16_t* vring, int64_t* key_pos,
+                                                       const int64_t* __restrict__ tokens,
+                                                       const int64_t* __restrict__ slots,
+                                                       const float* __restrict__ inv_freq, float rope_scale,
+                                                       uint16_t* __restrict__ out, long ld_out, int T, int H, int ring,
+                                                       int window) {
+  __shared__ float qs[RA_T][RA_HD];
+  __shared__ float pw[RA_T][RA_RING];
+  const int b = blockIdx.x, h = blockIdx.y;
+  const int l = threadIdx.x;
+  const long slot = slots[b];
+  const long p0 = tokens[slot];
+  uint16_t* kr = kring + slot * (long)ring * H * RA_HD;  // [ring][H][hd]
+  uint16_t* vr = vring + slot * (long)ring * H * RA_HD;
+  int64_t* kp = key_pos + slot * (long)ring;
+  const int half = RA_HD / 2;
+  const int partner = l < half ? l + half : l - half;
+  const float sgn = l < half ? -1.f : 1.f;
+  const float f = inv_freq[l < half ? l : l - half];
+  for (int t = 0; t < T; ++t) {
+    const long pos = p0 + t;
+    const float ang = (float)pos * f;
+    const float cs = cosf(ang) * rope_scale, sn = sinf(ang) * rope_scale;
+    const uint16_t* r = qkv + ((long)b * T + t) * ld_qkv;
+    qs[t][l] = E<DT>::to_f(r[h * RA_HD + l]) * cs + sgn * E<DT>::to_f(r[h * RA_HD + partner]) * sn;
+    const float kv = E<DT>::to_f(r[(H + h) * RA_HD + l]) * cs + sgn * E<DT>::to_f(r[(H + h) * RA_HD + partner]) * sn;
+    const long e = pos % ring;
+    kr[(e * H + h) * RA_HD + l] = E<DT>::from_f(kv);
+    vr[(e * H + h) * RA_HD + l] = r[(2 * H + h) * RA_HD + l];
+    if (h == 0 && l == 0) kp[e] = pos;
+  }
+  __syncthreads();  // the wave's queries (LDS) and new ring rows (global) are visible to all its lanes
+  const long new_lo = p0 % ring;
+  float sc[RA_T][RA_RING / 64];
+#pragma unroll
+  for (int u = 0; u < RA_RING / 64; ++u) {
+    const int j = l + 64 * u;
+    long kj = NEVER_POS;
+    if (j < ring) {
+      const long d = ((long)j - new_lo + ring) % ring;  // entries written by this call hold p0 + d
+      kj = d < T ? p0 + d : kp[j];
+    }
+    float acc[RA_T];
+#pragma unroll
+    for (int t = 0; t < RA_T; ++t) acc[t] = 0.f;
+    if (kj > p0 - window && kj < p0 + T) {  // visible to at least one of the T queries
+      const uint16_t* krow = kr + ((long)j * H + h) * RA_HD;
+#pragma unroll
+      for (int d = 0; d < RA_HD; d += 8) {
+        const u16x8 kv = ld16(krow + d);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float kf = E<DT>::to_f(kv.v[e]);
+#pragma unroll
+          for (int t = 0; t < RA_T; ++t)
+            if (t < T) acc[t] += qs[t][d + e] * kf;
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < RA_T; ++t) {
+      const long pos = p0 + t;
+      sc[t][u] = (t < T && kj <= pos && kj > pos - window) ? acc[t] * 0.125f : -INFINITY;
+    }
+  }
+  float inv_sum[RA_T];
+#pragma unroll
+  for (int t = 0; t < RA_T; ++t) {
+    if (t >= T) break;
+    float mx = sc[t][0];
+#pragma unroll
+    for (int u = 1; u < RA_RING / 64; ++u) mx = fmaxf(mx, sc[t][u]);
+    mx = wave_max_xor(mx, 64);  // finite: query t sees its own key
+    float sum = 0.f;
+#pragma unroll
+    for (int u = 0; u < RA_RING / 64; ++u) {
+      const float pe = sc[t][u] == -INFINITY ? 0.f : expf(sc[t][u] - mx);
+      sum += pe;
+      if (l + 64 * u < ring) pw[t][l + 64 * u] = pe;
+    }
+    inv_sum[t] = 1.f / wave_sum_xor(sum, 64);
+  }
+  __syncthreads();
+  const int g = l >> 3, dc = 8 * (l & 7);
+  float o[RA_T][8];
+#pragma unroll
+  for (int t = 0; t < RA_T; ++t)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[t][e] = 0.f;
+  for (int j = g; j < ring; j += 8) {
+    float pj[RA_T];
+    bool any = false;
+#pragma unroll
+    for (int t = 0; t < RA_T; ++t) {
+      pj[t] = t < T ? pw[t][j] : 0.f;
+      any |= pj[t] != 0.f;
+    }
+    if (!any) continue;
+    const u16x8 vv = ld16(vr + ((long)j * H + h) * RA_HD + dc);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float vf = E<DT>::to_f(vv.v[e]);
+#pragma unroll
+      for (int t = 0; t < RA_T; ++t) o[t][e] += pj[t] * vf;
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < RA_T; ++t) {
+    if (t >= T) break;
+    u16x8 ov;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float v = o[t][e];
+      v += __shfl_xor(v, 8, 64);
+      v += __shfl_xor(v, 16, 64);
+      v += __shfl_xor(v, 32, 64);
+      ov.v[e] = E<DT>::from_f(v * inv_sum[t]);
+    }
+    if (g == 0) st16(out + ((long)b * T + t) * ld_out + h * RA_HD + dc, ov);
+  }
+}
+
+// Seats' token counters advance by T after the transformer (:183-184); the dummy slot's counter returns to 0.
+__global__ void advance_tokens_kernel(int64_t* tokens, const int64_t* __restrict__ slots, int B, int T, int dummy) {
+  if (threadIdx.x) return;
+  for (int b = 0; b < B; ++b)
+    if (slots[b] != dummy) tokens[slots[b]] += T;
+  tokens[dummy] = 0;
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// Last conv to PCM (decoder.layers[-1], C -> 1 channel, kernel k, causal) in fp32 with fp32 weights:
+// pcm[b, t] = bias + sum_j sum_c w[j * C + c] joined[t + j][c], joined = the slot's k - 1 stored frames then x
+// (ELU already applied by the producing row op); the state becomes joined's last k - 1 frames.
+// Grid (B, ceil(T / chunk)), chunk >= k - 1; one wave per output sample.
+template <int DT>
+__global__ __launch_bounds__(CODEC_THREADS) void final_conv_kernel(const uint16_t* __restrict__ x, long ld_x,
+                                                                   uint16_t* state, long ld_state,
+                                                                   const int64_t* __restrict__ slots,
+                                                                   const float* __restrict__ w, float bias,
+                                                                   float* __restrict__ pcm, long ld_pcm, int T, int C,
+                                                                   int k, int chunk) {
+  const int b = blockIdx.x;
+  const int t0 = blockIdx.y * chunk, t1 = min(T, t0 + chunk);
+  const int pad = k - 1;
+  const long row0 = (long)b * T;
+  uint16_t* st = pad ? state + slots[b] * ld_state : nullptr;
+  const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
+  for (int t = t0 + wave; t < t1; t += CODEC_THREADS / 64) {
+    float acc = 0.f;
+    for (int e = l; e < k * C; e += 64) {
+      const int j = e / C, c = e - j * C;
+      const int i = t + j;
+      acc += w[e] * E<DT>::to_f(i < pad ? st[(long)i * C + c] : x[(row0 + i - pad) * ld_x + c]);
+    }
+    acc = wave_sum_xor(acc, 64);
+    if (l == 0) pcm[(long)b * ld_pcm + t] = acc + bias;
+  }
+  if (!pad || blockIdx.y) return;
+  const int cv = C / 8;
+  u16x8 keep[CODEC_KEEP / 8];
+  int n = 0;
+  for (int e = threadIdx.x; e < pad * cv; e += CODEC_THREADS)
+    keep[n++] = joined8<DT>(st, x, ld_x, row0, pad, T + e / cv, 8 * (e % cv), C, 0);
+  __syncthreads();
+  n = 0;
+  for (int e = threadIdx.x; e < pad * cv; e += CODEC_THREADS) st16(st + 8 * e, keep[n++]);
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// C ABI
+#define CODEC_LAUNCH(KERNEL, GRID, BLOCK, ...)                                                 \
+  do {                                                                                         \
+    if (dtype == M3X_BF16)                                                                     \
+      hipLaunchKernelGGL(KERNEL<M3X_BF16>, GRID, BLOCK, 0, (hipStream_t)stream, __VA_ARGS__);  \
+    else if (dtype == M3X_F16)                                                                 \
+      hipLaunchKernelGGL(KERNEL<M3X_F16>, GRID, BLOCK, 0, (hipStream_t)stream, __VA_ARGS__);   \
+    else                                                                                       \
+      return M3X_EUNSUPPORTED;                                                                 \
+    M3X_CHECK_LAUNCH();                                                                        \
+  } while (0)
+
+M3X_API int m3x_rvq_decode(const int64_t* codes, long ld_codes, const void* tables, void* out, long ld_out, int B,
+                           int nq, int n_codes, int dim, int dtype, void* stream) {
+  if (B < 0 || nq < 1 || n_codes < 1 || dim < 1 || ld_codes < nq || ld_out < 2L * dim) return M3X_EINVAL;
+  if (B == 0) return M3X_OK;
+  if (!codes || !tables || !out) return M3X_ENULL;
+  CODEC_LAUNCH(rvq_decode_kernel, dim3(B), dim3(256), codes, ld_codes, (const uint16_t*)tables, (uint16_t*)out,
+               ld_out, nq, n_codes, dim);
+  return M3X_OK;
+}
+
+M3X_API int m3x_dwconvt(const void* x, long ld_x, const void* w, void* tail, long ld_tail, const int64_t* slots,
+                        void* out, int B, int C, int k, int s, int dtype, void* stream) {
+  if (B < 0 || C < 1 || s < 1 || k < s || k > 2 * s || ld_x < C || ld_tail < (long)(k - s) * C) return M3X_EINVAL;
+  if (B == 0) return M3X_OK;
+  if (!x || !w || !tail || !slots || !out) return M3X_ENULL;
+  CODEC_LAUNCH(dwconvt_kernel, dim3(B), dim3(256), (const uint16_t*)x, ld_x, (const uint16_t*)w, (uint16_t*)tail,
+               ld_tail, slots, (uint16_t*)out, C, k, s);
+  return M3X_OK;
+}
+
+M3X_API int m3x_conv_gather(const void* x, long ld_x, void* state, long ld_state, const int64_t* slots, void* cols,
+                            long ld_cols, int B, int T, int C, int k, int dil, int use_elu, int chunk, int dtype,
+                            void* stream) {
+  const int pad = (k - 1) * dil;
+  if (B < 0 || T < 1 || C < 8 || C % 8 || k < 1 || dil < 1 || ld_x < C || ld_cols < (long)k * C ||
+      chunk < max(pad, 1) || ((ld_x | ld_cols | (pad ? ld_state : 0)) & 7))
+    return M3X_EINVAL;
+  if (!m3x_aligned16(x) || !m3x_aligned16(cols) || (pad && !m3x_aligned16(state))) return M3X_EINVAL;
+  if (pad && (ld_state < (long)pad * C || pad * C > CODEC_KEEP * CODEC_THREADS)) return M3X_EINVAL;
+  if (B == 0) return M3X_OK;
+  if (!x || !cols || !slots || (pad && !state)) return M3X_ENULL;
+  CODEC_LAUNCH(conv_gather_kernel, dim3(B, m3x_ceil_div(T, chunk)), dim3(CODEC_THREADS), (const uint16_t*)x, ld_x,
+               (uint16_t*)state, ld_state, slots, (uint16_t*)cols, ld_cols, T, C, k, dil, use_elu, chunk);
+  return M3X_OK;
+}
+
+M3X_API int m3x_rows_op(const void* g, long ld_g, const void* bias, const void* scale, const void* res, long ld_res,
+                        void* out, long ld_out, int rows, int C, int use_elu, int dtype, void* stream) {
+  if (rows < 0 || C < 8 || C % 8 || ld_g < C || ld_out < C || (res && ld_res < C)) return M3X_EINVAL;
+  if ((ld_g | ld_out | (res ? ld_res : 0)) & 7) return M3X_EINVAL;
+  if (rows == 0) return M3X_OK;
+  if (!g || !out) return M3X_ENULL;
+  if (!m3x_aligned16(g) || !m3x_aligned16(out) || (bias && !m3x_aligned16(bias)) ||
+      (scale && !m3x_aligned16(scale)) || (res && !m3x_aligned16(res)))
+    return M3X_EINVAL;
+  CODEC_LAUNCH(rows_op_kernel, dim3(m3x_ceil_div((long)rows * (C / 8), 256)), dim3(256), (const uint16_t*)g, ld_g,
+               (const uint16_t*)bias, (const uint16_t*)scale, (const uint16_t*)res, ld_res, (uint16_t*)out, ld_out,
+               rows, C, use_elu);
+  return M3X_OK;
+}
+
+M3X_API int m3x_convt_overlap(const void* cols, long ld_cols, void* tail, long ld_tail, const int64_t* slots,
+                              const void* bias, void* out, long ld_out, int B, int Tin, int C, int k, int s, int chunk,
+                              int dtype, void* stream) {
+  if (B < 0 || Tin < 1 || C < 8 || C % 8 || s < 1 || k <= s || k > 2 * s || ld_cols < (long)k * C || ld_out < C ||
+      chunk < k - s || ((ld_cols | ld_tail | ld_out) & 7))
+    return M3X_EINVAL;
+  if (!m3x_aligned16(cols) || !m3x_aligned16(tail) || !m3x_aligned16(out) || (bias && !m3x_aligned16(bias)))
+    return M3X_EINVAL;
+  if (ld_tail < (long)(k - s) * C || (k - s) * C > CODEC_KEEP * CODEC_THREADS) return M3X_EINVAL;
+  if (B == 0) return M3X_OK;
+  if (!cols || !tail || !slots || !out) return M3X_ENULL;
+  CODEC_LAUNCH(convt_overlap_kernel, dim3(B, m3x_ceil_div((long)Tin * s, chunk)), dim3(CODEC_THREADS),
+               (const uint16_t*)cols, ld_cols, (uint16_t*)tail, ld_tail, slots, (const uint16_t*)bias, (uint16_t*)out,
+               ld_out, Tin, C, k, s, chunk);
+  return M3X_OK;
+}
+
+M3X_API int m3x_ring_attn(const void* qkv, long ld_qkv, void* kring, void* vring, int64_t* key_pos,
+                          const int64_t* tokens, const int64_t* slots, const float* inv_freq, float rope_scale,
+                          void* out, long ld_out, int B, int T, int H, int head_dim, int ring, int window, int dtype,
+                          void* stream) {
+  if (B < 0 || T < 1 || T > RA_T || H < 1 || H > 8 || head_dim != RA_HD || ring < 1 || ring > RA_RING ||
+      window < 1 || ring < window + T - 1 || ring < T || ld_qkv < 3L * H * RA_HD || ld_out < (long)H * RA_HD || (ld_qkv & 7))
+    return M3X_EINVAL;
+  if (B == 0) return M3X_OK;
+  if (!qkv || !kring || !vring || !key_pos || !tokens || !slots || !inv_freq || !out) return M3X_ENULL;
+  if (!m3x_aligned16(qkv) || !m3x_aligned16(kring)) return M3X_EINVAL;
+  if (!m3x_aligned16(out) || (ld_out & 7)) return M3X_EINVAL;
+  CODEC_LAUNCH(ring_attn_kernel, dim3(B, H), dim3(64), (const uint16_t*)qkv, ld_qkv, (uint16_t*)kring,
+               (uint16_t*)vring, key_pos, tokens, slots, inv_freq, rope_scale, (uint16_t*)out, ld_out, T, H, ring,
+               window);
+  return M3X_OK;
+}
+
+M3X_API int m3x_advance_tokens(int64_t* tokens, const int64_t* slots, int B, int T, int dummy, void* stream) {
+  if (B < 0 || T < 0 || dummy < 0) return M3X_EINVAL;
+  if (!tokens || (B && !slots)) return M3X_ENULL;
+  hipLaunchKernelGGL(advance_tokens_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, tokens, slots, B, T, dummy);
+  M3X_CHECK_LAUNCH();
+  return M3X_OK;
+}
+
+M3X_API int m3x_final_conv(const void* x, long ld_x, void* state, long ld_state, const int64_t* slots, const float* w,
+                           float bias, float* pcm, long ld_pcm, int B, int T, int C, int k, int chunk, int dtype,
+                           void* stream) {
+  if (B < 0 || T < 1 || C < 8 || C % 8 || k < 1 || ld_x < C || ld_pcm < T || chunk < max(k - 1, 1) ||
+      ((ld_x | (k > 1 ? ld_state : 0)) & 7))
+    return M3X_EINVAL;
+  if (!m3x_aligned16(x) || (k > 1 && !m3x_aligned16(state))) return M3X_EINVAL;
+  if (k > 1 && (ld_state < (long)(k - 1) * C || (k - 1) * C > CODEC_KEEP * CODEC_THREADS)) return M3X_EINVAL;
+  if (B == 0) return M3X_OK;
+  if (!x || !slots || !w || !pcm || (k > 1 && !state)) return M3X_ENULL;
+  CODEC_LAUNCH(final_conv_kernel, dim3(B, m3x_ceil_div(T, chunk)), dim3(CODEC_THREADS), (const uint16_t*)x, ld_x,
+               (uint16_t*)state, ld_state, slots, w, bias, pcm, ld_pcm, T, C, k, chunk);
+  return M3X_OK;
+}

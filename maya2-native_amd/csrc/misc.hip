@@ -281,4 +281,4 @@ M3X_API int m3x_tick_pack(const int64_t* stop, const int64_t* cb0, const int32_t
 }
 
 // The library's version, so a host binding can check it loaded the build it expects.
-M3X_API int m3x_version(void) { return 7; }
+M3X_API int m3x_version(void) { return 8; }

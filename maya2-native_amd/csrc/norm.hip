@@ -384,7 +384,9 @@ M3X_API int m3x_add_norm(const void* x, long sxb, long sxt, const void* a, long 
 #define M3X_ADD_NORM_LAUNCH(NN, DTT)                                                                               \
   hipLaunchKernelGGL((add_norm_kernel<NN / 8, DTT>), dim3(m3x_ceil_div(rows, 256 / (NN / 8))), dim3(256), 0, st, X, \
                      sxb, sxt, A, sab, sat, C, s_c, XO, Y, Wt, Bt, eps, rows, T, kind)
-  if (dtype == M3X_BF16 && n == 1024) M3X_ADD_NORM_LAUNCH(1024, M3X_BF16);
+  if (dtype == M3X_BF16 && n == 512) M3X_ADD_NORM_LAUNCH(512, M3X_BF16);
+  else if (dtype == M3X_F16 && n == 512) M3X_ADD_NORM_LAUNCH(512, M3X_F16);
+  else if (dtype == M3X_BF16 && n == 1024) M3X_ADD_NORM_LAUNCH(1024, M3X_BF16);
   else if (dtype == M3X_F16 && n == 1024) M3X_ADD_NORM_LAUNCH(1024, M3X_F16);
   else if (dtype == M3X_BF16 && n == 2048) M3X_ADD_NORM_LAUNCH(2048, M3X_BF16);
   else if (dtype == M3X_F16 && n == 2048) M3X_ADD_NORM_LAUNCH(2048, M3X_F16);

@@ -12,7 +12,7 @@ import os
 import torch  # noqa: F401  (must precede the CDLL load, see above)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libm3x.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -56,6 +56,14 @@ SIGNATURES = {
     "m3x_loop_guard": (_I, [_P, _L, _P, _P, _P, _I, _I, _I, _I, ctypes.c_double, _I, _I, _P]),
     "m3x_tick_pack_width": (_I, [_I, _I, _I]),
     "m3x_tick_pack": (_I, [_P, _P, _P, _P, _L, _I, _P, _L, _I, _P, _L, _I, _P]),
+    "m3x_rvq_decode": (_I, [_P, _L, _P, _P, _L, _I, _I, _I, _I, _I, _P]),
+    "m3x_dwconvt": (_I, [_P, _L, _P, _P, _L, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "m3x_conv_gather": (_I, [_P, _L, _P, _L, _P, _P, _L, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "m3x_rows_op": (_I, [_P, _L, _P, _P, _P, _L, _P, _L, _I, _I, _I, _I, _P]),
+    "m3x_convt_overlap": (_I, [_P, _L, _P, _L, _P, _P, _P, _L, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "m3x_ring_attn": (_I, [_P, _L, _P, _P, _P, _P, _P, _P, _F, _P, _L, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "m3x_advance_tokens": (_I, [_P, _P, _I, _I, _I, _P]),
+    "m3x_final_conv": (_I, [_P, _L, _P, _L, _P, _P, _F, _P, _L, _I, _I, _I, _I, _I, _I, _P]),
 }
 
 STATUS = {0: "ok", -1: "invalid argument", -2: "null pointer", -3: "workspace too small", -4: "launch failed",

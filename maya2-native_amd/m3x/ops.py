@@ -398,3 +398,63 @@ def code_ring_write(codes, ring, head, B):
     _dev(codes, ring, head)
     check(lib().m3x_code_ring_write(_p(codes), codes.stride(0), _p(ring), _p(head), ring.shape[0], ring.shape[1],
                                     ring.shape[2], int(B), _stream()), "code_ring_write")
+
+
+# ---------------------------------------------------------------- Mimi decode (serve/fast_codec.py)
+def rvq_decode(codes, tables, out):
+    """out[b] = [table_0[codes[b, 0]] | sum over q >= 1 of table_q[codes[b, q]]]; tables [nq, n_codes, dim]."""
+    _dev(codes, tables, out)
+    nq, n_codes, dim = tables.shape
+    check(lib().m3x_rvq_decode(_p(codes), codes.stride(0), _p(tables), _p(out), out.stride(0), codes.shape[0], nq,
+                               n_codes, dim, _dt(tables), _stream()), "rvq_decode")
+
+
+def dwconvt(x, w, tail, slots, out, k, s):
+    """Depthwise transposed conv of one frame per seat with per-slot overlap tails; out [B * s, C]."""
+    _dev(x, w, tail, slots, out)
+    check(lib().m3x_dwconvt(_p(x), x.stride(0), _p(w), _p(tail), tail.stride(0), _p(slots), _p(out), x.shape[0],
+                            x.shape[1], k, s, _dt(x), _stream()), "dwconvt")
+
+
+def conv_gather(x, state, slots, cols, B, T, C, k, dil, use_elu, chunk):
+    """GEMM rows of a causal conv with per-slot input history (state [slots, pad * C] or None when pad = 0)."""
+    _dev(x, state, slots, cols)
+    check(lib().m3x_conv_gather(_p(x), x.stride(0), _p(state), 0 if state is None else state.stride(0), _p(slots),
+                                _p(cols), cols.stride(0), B, T, C, k, dil, int(use_elu), chunk, _dt(x), _stream()),
+          "conv_gather")
+
+
+def rows_op(g, out, bias=None, scale=None, res=None, use_elu=False):
+    """out = act(res + scale * (g + bias)), act = ELU when use_elu; rows of g and out [rows, C]."""
+    _dev(g, out, bias, scale, res)
+    check(lib().m3x_rows_op(_p(g), g.stride(0), _p(bias), _p(scale), _p(res), 0 if res is None else res.stride(0),
+                            _p(out), out.stride(0), out.shape[0], out.shape[1], int(use_elu), _dt(g), _stream()),
+          "rows_op")
+
+
+def convt_overlap(cols, tail, slots, bias, out, B, Tin, C, k, s, chunk):
+    """Overlap-add of a transposed conv's GEMM columns with per-slot tails; out [B * Tin * s, C]."""
+    _dev(cols, tail, slots, bias, out)
+    check(lib().m3x_convt_overlap(_p(cols), cols.stride(0), _p(tail), tail.stride(0), _p(slots), _p(bias), _p(out),
+                                  out.stride(0), B, Tin, C, k, s, chunk, _dt(cols), _stream()), "convt_overlap")
+
+
+def ring_attn(qkv, kring, vring, key_pos, tokens, slots, inv_freq, rope_scale, out, B, T, H, ring, window):
+    """Sliding-window attention of T new tokens per seat over per-slot rings of post-RoPE keys."""
+    _dev(qkv, kring, vring, key_pos, tokens, slots, inv_freq, out)
+    check(lib().m3x_ring_attn(_p(qkv), qkv.stride(0), _p(kring), _p(vring), _p(key_pos), _p(tokens), _p(slots),
+                              _p(inv_freq), float(rope_scale), _p(out), out.stride(0), B, T, H, 64, ring, window,
+                              _dt(qkv), _stream()), "ring_attn")
+
+
+def advance_tokens(tokens, slots, B, T, dummy):
+    _dev(tokens, slots)
+    check(lib().m3x_advance_tokens(_p(tokens), _p(slots), B, T, dummy, _stream()), "advance_tokens")
+
+
+def final_conv(x, state, slots, w, bias, pcm, B, T, C, k, chunk):
+    """fp32 PCM of the last causal conv (C -> 1 channel) with per-slot history; pcm [B, >= T] float32."""
+    _dev(x, state, slots, w, pcm)
+    check(lib().m3x_final_conv(_p(x), x.stride(0), _p(state), 0 if state is None else state.stride(0), _p(slots),
+                               _p(w), float(bias), _p(pcm), pcm.stride(0), B, T, C, k, chunk, _dt(x), _stream()),
+          "final_conv")

@@ -1,0 +1,363 @@
+"""Slot-based, static-state, graphed one-frame Mimi decoder on m3x kernels.
+
+Drop-in for serve/fast_codec.py StaticMimi (:32-277): same constructor arguments (plus the compute dtype), the
+same public calls (decode, reset, warmup, state_bytes_per_slot, samples_per_frame) and the same streaming
+semantics: causal-conv input history, transposed-conv overlap tails stored without bias, sliding-window attention
+at absolute RoPE positions (a query at position p sees keys with p - window < key_pos <= p), one row of every
+state per slot plus the dummy row max_slots that pads a batch to its bucket.
+
+The frame runs as m3x launches on time-major activations [seat * T + t, channels] in 16-bit with fp32
+accumulation: the codebook sum (m3x_rvq_decode) and its 1x1 projections as one GEMM, the depthwise upsample with
+its tail (m3x_dwconvt), per transformer layer LayerNorm, q|k|v GEMM, ring attention (m3x_ring_attn), o GEMM,
+layer-scaled residual, LayerNorm, fc1 GEMM + GELU, fc2 GEMM, layer-scaled residual; every SEANet conv as
+history gather (m3x_conv_gather, ELU fused) + GEMM + bias/residual/ELU row op (m3x_rows_op), every transposed
+conv as GEMM + overlap-add with tail (m3x_convt_overlap), and the last conv to fp32 PCM (m3x_final_conv).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .. import ops
+
+NEVER = -(1 << 40)  # key_pos of an empty ring entry; outside every window
+
+
+class _Bucket:
+    __slots__ = ("graph", "slots", "codes", "out", "bufs", "pinned", "events", "turn")
+
+
+def _chunk(rows, B, depth, target=2048):
+    """Rows per workgroup of a stateful kernel over `rows` rows per seat: about `target` workgroups for the batch,
+    at least the state's depth (only the first chunk of a seat may read its state)."""
+    return max(depth, 1, -(-rows * B // target))
+
+
+class StaticMimi:
+    def __init__(self, mimi, max_slots, batch_buckets=(1, 2, 4, 8, 16, 24, 32, 48, 64, 80, 96), ring=256,
+                 dtype=torch.float16, use_graphs=True):
+        from transformers.models.mimi.modeling_mimi import MimiConv1d, MimiConvTranspose1d, MimiResnetBlock
+        cfg = mimi.config
+        if not cfg.use_causal_conv or cfg.pad_mode != "constant" or cfg.trim_right_ratio != 1:
+            raise ValueError("Static decoder requires causal constant padding and trim_right_ratio=1")
+        if mimi.upsample is None:
+            raise ValueError("Static decoder expects the Mimi upsample layer")
+        if dtype not in (torch.float16, torch.bfloat16):
+            raise ValueError("StaticMimi computes in float16 or bfloat16")
+        param = next(mimi.parameters())
+        if not param.is_cuda:
+            raise ValueError("StaticMimi runs on the GPU: move the Mimi model to a cuda device first")
+        self.m = mimi
+        self.device, self.dtype = param.device, dtype
+        self.max_slots = int(max_slots)
+        self.dummy = self.max_slots
+        self.batch_buckets = tuple(sorted(set(int(b) for b in batch_buckets)))
+        self.window = int(cfg.sliding_window)
+        self.frame_tokens = int(mimi.upsample.conv.stride[0])
+        self.ring = int(ring)
+        if self.ring < self.window + self.frame_tokens:
+            raise ValueError("ring must hold sliding_window + frame_tokens entries")
+        if self.ring > 256 or self.frame_tokens > 8:
+            raise ValueError("ring attention holds at most 256 ring entries and 8 tokens per frame")
+        self.codebooks = int(cfg.num_quantizers)
+        self.use_graphs = use_graphs
+        rows = self.max_slots + 1
+        dt = dtype
+
+        def w16(t):
+            return t.detach().to(self.device, dt).contiguous()
+
+        with torch.inference_mode():
+            # quantizer: tables [semantic rows | acoustic rows], output projections side by side
+            q = mimi.quantizer
+            sem, ac = q.semantic_residual_vector_quantizer, q.acoustic_residual_vector_quantizer
+            if q.num_semantic_quantizers != 1 or sem.output_proj is None or ac.output_proj is None:
+                raise ValueError("expected one semantic codebook and 1x1 output projections")
+            if sem.output_proj.bias is not None or ac.output_proj.bias is not None:
+                raise ValueError("quantizer output projections carry no bias")
+            self.tables = w16(torch.stack([l.codebook.embed for l in list(sem.layers) + list(ac.layers)]))
+            self.n_codes, self.cb_dim = self.tables.shape[1], self.tables.shape[2]
+            self.w_quant = ops.pack_weight(w16(torch.cat([sem.output_proj.weight[:, :, 0],
+                                                          ac.output_proj.weight[:, :, 0]], 1)))
+            self.hidden = self.w_quant.N
+            up = mimi.upsample.conv
+            if up.groups != up.in_channels or up.bias is not None or up.dilation != (1,):
+                raise ValueError("expected a depthwise bias-free upsample")
+            self.up_k, self.up_s = up.kernel_size[0], up.stride[0]
+            self.w_up = w16(up.weight[:, 0, :])
+            # transformer
+            self.layers = []
+            for L in mimi.decoder_transformer.layers:
+                a = L.self_attn
+                if any(p.bias is not None for p in (a.q_proj, a.k_proj, a.v_proj, a.o_proj, L.mlp.fc1, L.mlp.fc2)):
+                    raise ValueError("expected bias-free attention and MLP projections")
+                if a.num_key_value_groups != 1 or a.head_dim != 64:
+                    raise ValueError("ring attention takes head_dim 64 and as many kv heads as heads")
+                self.layers.append(dict(
+                    ln1=(w16(L.input_layernorm.weight), w16(L.input_layernorm.bias), L.input_layernorm.eps),
+                    qkv=ops.pack_weight(w16(torch.cat([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight]))),
+                    o=ops.pack_weight(w16(a.o_proj.weight)), s1=w16(L.self_attn_layer_scale.scale),
+                    ln2=(w16(L.post_attention_layernorm.weight), w16(L.post_attention_layernorm.bias),
+                         L.post_attention_layernorm.eps),
+                    fc1=ops.pack_weight(w16(L.mlp.fc1.weight)), fc2=ops.pack_weight(w16(L.mlp.fc2.weight)),
+                    s2=w16(L.mlp_layer_scale.scale)))
+            self.heads = mimi.decoder_transformer.layers[0].self_attn.num_heads
+            rot = mimi.decoder_transformer.rotary_emb
+            self.inv_freq = rot.inv_freq.detach().float().to(self.device).contiguous()
+            self.rope_scale = float(rot.attention_scaling)
+            # SEANet decoder: conv, (ELU, conv-T, resnet)*, ELU, conv
+            mods = list(mimi.decoder.layers)
+            self.plan = []
+            state_sizes = [("upsample", (self.up_k - self.up_s) * self.hidden)]
+            first = mods[0]
+            if not isinstance(first, MimiConv1d):
+                raise ValueError("decoder must start with a conv")
+            self.plan.append(self._conv_step("decoder.0", first, pre_elu=False, post_elu=True))
+            state_sizes.append(("decoder.0", self.plan[-1]["pad"] * self.plan[-1]["cin"]))
+            i = 1
+            while i < len(mods) - 2:
+                elu, ct, res = mods[i], mods[i + 1], mods[i + 2]
+                if not (isinstance(elu, torch.nn.ELU) and elu.alpha == 1.0 and isinstance(ct, MimiConvTranspose1d)
+                        and isinstance(res, MimiResnetBlock) and isinstance(res.shortcut, torch.nn.Identity)):
+                    raise ValueError(f"unexpected decoder layers at {i}")
+                c = ct.conv
+                if ct.padding_left != 0 or c.dilation != (1,) or c.groups != 1 or ct.padding_right != c.kernel_size[0] - c.stride[0]:
+                    raise ValueError("unsupported transpose-convolution geometry")
+                k, s, cin, cout = c.kernel_size[0], c.stride[0], c.in_channels, c.out_channels
+                self.plan.append(dict(kind="convt", key=f"decoder.{i + 1}", k=k, s=s, cin=cin, cout=cout,
+                                      w=ops.pack_weight(w16(c.weight.permute(2, 1, 0).reshape(k * cout, cin))),
+                                      bias=None if c.bias is None else w16(c.bias)))
+                state_sizes.append((f"decoder.{i + 1}", (k - s) * cout))
+                blk = list(res.block)
+                if len(blk) != 4 or not all(isinstance(b, torch.nn.ELU) and b.alpha == 1.0 for b in blk[::2]):
+                    raise ValueError("resnet block must be ELU, conv, ELU, conv")
+                ca = self._conv_step(f"decoder.{i + 2}.block.1", blk[1], pre_elu=True, post_elu=True)
+                cb = self._conv_step(f"decoder.{i + 2}.block.3", blk[3], pre_elu=False, post_elu=True)
+                if cb["pad"] or cb["k"] != 1:
+                    raise ValueError("the resnet block's second conv must be 1x1")
+                self.plan.append(dict(kind="resnet", a=ca, b=cb))
+                state_sizes.append((ca["key"], ca["pad"] * ca["cin"]))
+                i += 3
+            elu, last = mods[i], mods[i + 1] if i + 1 < len(mods) else None
+            if not (isinstance(elu, torch.nn.ELU) and isinstance(last, MimiConv1d) and last.conv.out_channels == 1):
+                raise ValueError("decoder must end with ELU and a conv to one channel")
+            lc = last.conv
+            k = lc.kernel_size[0]
+            if lc.dilation != (1,) or lc.stride != (1,):
+                raise ValueError("the last conv must have stride and dilation 1")
+            self.final = dict(key=f"decoder.{i + 1}", k=k, cin=lc.in_channels,
+                              w=lc.weight[0].t().contiguous().reshape(-1).float().to(self.device),
+                              bias=float(lc.bias[0]) if lc.bias is not None else 0.0)
+            state_sizes.append((self.final["key"], (k - 1) * lc.in_channels))
+            # per-slot state: one flat row per slot, one column range per stateful layer ([frames][channels])
+            total = sum(n for _, n in state_sizes)
+            self.conv_flat = torch.zeros(rows, total, device=self.device, dtype=dt)
+            self.state, off = {}, 0
+            for key, n in state_sizes:
+                self.state[key] = self.conv_flat[:, off:off + n] if n else None
+                off += n
+            self.kv = torch.zeros(len(self.layers), 2, rows, self.ring, self.heads, 64, device=self.device, dtype=dt)
+            self.key_pos = torch.full((rows, self.ring), NEVER, device=self.device, dtype=torch.long)
+            self.tokens = torch.zeros(rows, device=self.device, dtype=torch.long)
+            # samples per frame: the SEANet's strides times the upsample's tokens
+            t = self.frame_tokens
+            for st in self.plan:
+                if st["kind"] == "convt":
+                    t *= st["s"]
+            self.samples_per_frame = t
+        self._pool = None
+        self._buckets = {}
+
+    def _conv_step(self, key, mod, pre_elu, post_elu):
+        c = mod.conv
+        if c.stride != (1,) or c.groups != 1:
+            raise ValueError("Only stride-one dense decoder convolutions are supported")
+        k, dil = c.kernel_size[0], c.dilation[0]
+        return dict(kind="conv", key=key, k=k, dil=dil, pad=(k - 1) * dil, cin=c.in_channels, cout=c.out_channels,
+                    pre_elu=pre_elu, post_elu=post_elu,
+                    w=ops.pack_weight(c.weight.detach().to(self.device, self.dtype).permute(0, 2, 1)
+                                      .reshape(c.out_channels, k * c.in_channels).contiguous()),
+                    bias=None if c.bias is None else c.bias.detach().to(self.device, self.dtype).contiguous())
+
+    def state_bytes_per_slot(self):
+        return {"conv": self.conv_flat[0].numel() * self.conv_flat.element_size(),
+                "attention_kv": self.kv[:, :, 0].numel() * self.kv.element_size(),
+                "attention_index": self.key_pos[0].numel() * 8 + 8}
+
+    # ---- buffers and the frame body ---------------------------------------------------------------
+    def _buffers(self, B):
+        T0, D = self.frame_tokens, self.hidden
+        act = cols = inner = B * T0 * 2 * D
+        t = T0
+        for st in self.plan:
+            if st["kind"] == "conv":
+                cols = max(cols, B * t * st["k"] * st["cin"])
+                act = max(act, B * t * st["cout"])
+            elif st["kind"] == "convt":
+                cols = max(cols, B * t * st["k"] * st["cout"])
+                t *= st["s"]
+                act = max(act, B * t * st["cout"])
+            elif st["kind"] == "resnet":
+                a = st["a"]
+                cols = max(cols, B * t * a["k"] * a["cin"])
+                inner = max(inner, B * t * a["cout"])
+        z = lambda n: torch.zeros(n, device=self.device, dtype=self.dtype)  # noqa: E731
+        R = B * T0
+        return dict(e=z(B * 2 * self.cb_dim).view(B, 2 * self.cb_dim), u=z(B * D).view(B, D), h=z(R * D).view(R, D),
+                    y=z(R * D).view(R, D), qkv=z(R * 3 * D).view(R, 3 * D), o=z(R * D).view(R, D),
+                    a=z(R * D).view(R, D), f=z(R * 4 * D).view(R, 4 * D), X=z(act), G=z(act), I=z(inner),
+                    C=z(cols), pcm=torch.zeros(B, self.samples_per_frame, device=self.device, dtype=torch.float32))
+
+    def _forward(self, slots, codes, bf, B):
+        T0, D, H = self.frame_tokens, self.hidden, self.heads
+        R = B * T0
+        ops.rvq_decode(codes, self.tables, bf["e"])
+        ops.linear(bf["e"], self.w_quant, bf["u"])
+        h, y = bf["h"], bf["y"]
+        ops.dwconvt(bf["u"], self.w_up, self.state["upsample"], slots, h, self.up_k, self.up_s)
+        for li, L in enumerate(self.layers):
+            w, b, eps = L["ln1"]
+            ops.add_norm(h, None, None, None, y, w, b, eps, 1, ops.NORM_LAYER)
+            ops.linear(y, L["qkv"], bf["qkv"])
+            ops.ring_attn(bf["qkv"], self.kv[li, 0], self.kv[li, 1], self.key_pos, self.tokens, slots, self.inv_freq,
+                          self.rope_scale, bf["o"], B, T0, H, self.ring, self.window)
+            ops.linear(bf["o"], L["o"], bf["a"])
+            ops.rows_op(bf["a"], h, scale=L["s1"], res=h)
+            w, b, eps = L["ln2"]
+            ops.add_norm(h, None, None, None, y, w, b, eps, 1, ops.NORM_LAYER)
+            ops.linear_act(y, L["fc1"], None, ops.ACT_GELU, bf["f"])
+            ops.linear(bf["f"], L["fc2"], bf["a"])
+            ops.rows_op(bf["a"], h, scale=L["s2"], res=h)
+        ops.advance_tokens(self.tokens, slots, B, T0, self.dummy)
+        # SEANet: x is the current activation [B * t, C]
+        x, t = h, T0
+        for st in self.plan:
+            if st["kind"] == "conv":
+                x = self._conv(st, x, slots, B, t, out=bf["X"])
+            elif st["kind"] == "convt":
+                cols = bf["C"][:B * t * st["k"] * st["cout"]].view(B * t, st["k"] * st["cout"])
+                ops.linear(x, st["w"], cols)
+                out = bf["X"][:B * t * st["s"] * st["cout"]].view(B * t * st["s"], st["cout"])
+                ops.convt_overlap(cols, self.state[st["key"]], slots, st["bias"], out, B, t, st["cout"], st["k"],
+                                  st["s"], _chunk(t * st["s"], B, st["k"] - st["s"]))
+                x, t = out, t * st["s"]
+            else:
+                a, b = st["a"], st["b"]
+                inner = self._conv(a, x, slots, B, t, out=bf["I"])
+                g = bf["G"][:B * t * b["cout"]].view(B * t, b["cout"])
+                ops.linear(inner, b["w"], g)
+                ops.rows_op(g, x, bias=b["bias"], res=x, use_elu=True)  # shortcut + block, then the next ELU
+        f = self.final
+        ops.final_conv(x, self.state[f["key"]], slots, f["w"], f["bias"], bf["pcm"], B, t, f["cin"], f["k"],
+                       _chunk(t, B, f["k"] - 1))
+        return bf["pcm"]
+
+    def _conv(self, st, x, slots, B, t, out):
+        """Causal conv of x [B * t, cin] -> act(out) [B * t, cout] (bias, ELU when post_elu)."""
+        k, cin, cout = st["k"], st["cin"], st["cout"]
+        if k == 1 and not st["pre_elu"]:
+            src = x
+        else:
+            src = self._bf["C"][:B * t * k * cin].view(B * t, k * cin)
+            ops.conv_gather(x, self.state[st["key"]], slots, src, B, t, cin, k, st["dil"], st["pre_elu"],
+                            _chunk(t, B, st["pad"]))
+        y = out[:B * t * cout].view(B * t, cout)
+        g = self._bf["G"][:B * t * cout].view(B * t, cout) if out is not self._bf["G"] else y
+        ops.linear(src, st["w"], g)
+        ops.rows_op(g, y, bias=st["bias"], use_elu=st["post_elu"])
+        return y
+
+    def _run(self, bucket, B):
+        self._bf = bucket.bufs
+        return self._forward(bucket.slots, bucket.codes, bucket.bufs, B)
+
+    # ---- capture ----------------------------------------------------------------------------------
+    def _capture(self, size):
+        bucket = _Bucket()
+        bucket.slots = torch.full((size,), self.dummy, device=self.device, dtype=torch.long)
+        bucket.codes = torch.zeros(size, self.codebooks, device=self.device, dtype=torch.long)
+        bucket.pinned = [torch.full((size,), self.dummy, dtype=torch.long).pin_memory() for _ in range(8)]
+        bucket.events = [None] * len(bucket.pinned)
+        bucket.turn = 0
+        bucket.bufs = self._buffers(size)
+        bucket.graph = None
+        if self.use_graphs:
+            # warmup and capture touch only the dummy slot, so live seats are never disturbed
+            side = torch.cuda.Stream(device=self.device)
+            side.wait_stream(torch.cuda.current_stream(self.device))
+            with torch.cuda.stream(side):
+                self._run(bucket, size)
+            torch.cuda.current_stream(self.device).wait_stream(side)
+            torch.cuda.synchronize(self.device)
+            if self._pool is None:
+                self._pool = torch.cuda.graph_pool_handle()
+            bucket.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(bucket.graph, pool=self._pool):
+                bucket.out = self._run(bucket, size)
+            self._reset_row(self.dummy)
+        else:
+            bucket.out = bucket.bufs["pcm"]
+        self._buckets[size] = bucket
+        return bucket
+
+    @torch.inference_mode()
+    def warmup(self, batch_buckets=None):
+        sizes = self.batch_buckets if batch_buckets is None else tuple(sorted(set(int(b) for b in batch_buckets)))
+        for size in sorted(sizes, reverse=True):
+            if size not in self._buckets:
+                self._capture(size)
+        self.batch_buckets = tuple(sorted(set(self.batch_buckets) | set(sizes)))
+
+    # ---- public -----------------------------------------------------------------------------------
+    def _reset_row(self, row):
+        self.conv_flat[row].zero_()
+        self.key_pos[row].fill_(NEVER)
+        self.tokens[row].zero_()
+
+    @torch.inference_mode()
+    def reset(self, slot, zero_kv=False):
+        """Fill kernels only, no host sync. Ring entries are unreachable once key_pos is NEVER; zero_kv=True also
+        clears them."""
+        if not 0 <= slot < self.max_slots:
+            raise IndexError(f"slot {slot} outside [0,{self.max_slots})")
+        self._reset_row(slot)
+        if zero_kv:
+            self.kv[:, :, slot].zero_()
+
+    @torch.inference_mode()
+    def decode(self, slots, codes):
+        """slots: distinct ints in [0, max_slots) (or a CUDA long tensor of them); codes: [B, K] long CUDA, one
+        frame per seat. Returns an owned float32 [B, samples_per_frame] tensor."""
+        count = len(slots)
+        if codes.dim() != 2 or codes.shape[0] != count or codes.shape[1] != self.codebooks:
+            raise ValueError(f"codes must be [{count},{self.codebooks}], got {tuple(codes.shape)}")
+        size = next((b for b in self.batch_buckets if b >= count), None)
+        if size is None:
+            raise ValueError(f"batch {count} exceeds largest bucket {self.batch_buckets[-1]}")
+        bucket = self._buckets.get(size) or self._capture(size)
+        if torch.is_tensor(slots):
+            bucket.slots[:count].copy_(slots)
+            bucket.slots[count:].fill_(self.dummy)
+        else:
+            if len(set(slots)) != count or (count and (min(slots) < 0 or max(slots) >= self.max_slots)):
+                raise ValueError("slots must be distinct and inside [0,max_slots)")
+            turn = bucket.turn
+            bucket.turn = (turn + 1) % len(bucket.pinned)
+            if bucket.events[turn] is not None:
+                bucket.events[turn].synchronize()
+            staging = bucket.pinned[turn]
+            staging[:count] = torch.tensor(slots, dtype=torch.long)
+            staging[count:] = self.dummy
+            bucket.slots.copy_(staging, non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record()
+            bucket.events[turn] = ev
+        bucket.codes[:count].copy_(codes)
+        if count < size:
+            bucket.codes[count:].zero_()
+        if bucket.graph is not None:
+            bucket.graph.replay()
+        else:
+            self._run(bucket, size)
+        return bucket.out[:count].clone()

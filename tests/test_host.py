@@ -111,6 +111,9 @@ def test_surfaces_reject_host_models():
     small = synth.swiglu_depth(d=1024, n_q=16)
     with pytest.raises(ValueError):
         FastDepth(small, 2)
+    from m3x.serve.fast_codec import StaticMimi
+    with pytest.raises(ValueError):  # a host-resident Mimi: the product path has no CPU fallback
+        StaticMimi(synth.mimi(seed=1), 2)
 
 
 def test_bench_refuses_multi_gpu():
