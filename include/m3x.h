@@ -257,6 +257,12 @@ int m3x_conv_gather(const void* x, long ld_x, void* state, long ld_state, const 
 int m3x_rows_op(const void* g, long ld_g, const void* bias, const void* scale, const void* res, long ld_res,
                 void* out, long ld_out, int rows, int C, int use_elu, int dtype, void* stream);
 
+/* h = dt(h + scale * a) (m3x_rows_op's arithmetic), then y = LayerNorm(h) (w, b, eps; fp32 statistics) over rows of
+ * n = 512. Replaces `h = h + layer.self_attn_layer_scale(a)` / `h + layer.mlp_layer_scale(...)` followed by the
+ * next `post_attention_layernorm` / `input_layernorm` (serve/fast_codec.py:172,181-182). */
+int m3x_resid_ln(void* h, long ld_h, const void* a, long ld_a, const void* scale, const void* w, const void* b,
+                 void* y, long ld_y, float eps, int rows, int n, int dtype, void* stream);
+
 /* Overlap-add of a transposed conv (kernel k, stride s, s < k <= 2 s) from its GEMM columns cols[b*Tin + t,
  * j*C + c]: out [B * Tin * s, C] with the slot's tail added to the first k - s frames and bias; the new tail is the
  * overflow without bias. Replaces the MimiConvTranspose1d branch of `_layer` (serve/fast_codec.py:112-126). */

@@ -132,6 +132,47 @@ __global__ __launch_bounds__(256) void rows_op_kernel(const uint16_t* __restrict
 }
 
 // ---------------------------------------------------------------------------------------------------------
+// Layer-scaled residual then LayerNorm over rows of 512: h = dt(h + scale * a) (the arithmetic of m3x_rows_op),
+// y = dt((h - mean) / sqrt(var + eps) * w + b) with fp32 statistics. One wave per row. Serves the decoder
+// transformer's `h = h + layer_scale(a)` followed by the next LayerNorm (serve/fast_codec.py:181-182,172,182).
+constexpr int RLN_N = 512;
+template <int DT>
+__global__ __launch_bounds__(256) void resid_ln_kernel(uint16_t* h, long ld_h, const uint16_t* __restrict__ a,
+                                                       long ld_a, const uint16_t* __restrict__ scale,
+                                                       const uint16_t* __restrict__ w, const uint16_t* __restrict__ b,
+                                                       uint16_t* __restrict__ y, long ld_y, float eps, int rows) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // a whole wave; the kernel has no block barrier
+  const int c = 8 * (threadIdx.x & 63);
+  const u16x8 hv = ld16(h + row * ld_h + c), av = ld16(a + row * ld_a + c), sv = ld16(scale + c);
+  float v[8];
+  u16x8 ho;
+  float sum = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float t = E<DT>::to_f(sv.v[e]) * E<DT>::to_f(av.v[e]);
+    t = E<DT>::to_f(hv.v[e]) + t;
+    ho.v[e] = E<DT>::from_f(t);
+    v[e] = E<DT>::to_f(ho.v[e]);
+    sum += v[e];
+  }
+  st16(h + row * ld_h + c, ho);
+  const float mean = wave_sum_xor(sum, 64) / (float)RLN_N;
+  float sq = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    v[e] = v[e] - mean;
+    sq += v[e] * v[e];
+  }
+  const float inv = 1.f / sqrtf(wave_sum_xor(sq, 64) / (float)RLN_N + eps);
+  const u16x8 wv = ld16(w + c), bv = ld16(b + c);
+  u16x8 yo;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) yo.v[e] = E<DT>::from_f(v[e] * inv * E<DT>::to_f(wv.v[e]) + E<DT>::to_f(bv.v[e]));
+  st16(y + row * ld_y + c, yo);
+}
+
+// ---------------------------------------------------------------------------------------------------------
 // Transposed conv overlap-add (:112-130). cols[b * Tin + t, j * C + c] = x[b, t] . W[:, c, j] comes from the GEMM;
 // output frame o < Tin * s of seat b is the sum of its contributions (t, j = o - t s, 0 <= j < k) + tail[slot, o, c]
 // (o < k - s) + bias[c]; the new tail[slot, i, c] = the contributions to frame Tin * s + i, without bias (the
@@ -198,134 +239,149 @@ __global__ __launch_bounds__(CODEC_THREADS) void convt_overlap_kernel(const uint
 // the slot's ring entry p % ring with key_pos[slot, p % ring] = p; query p attends the entries with
 // p - window < key_pos <= p, softmax at scale 1/sqrt(64). qkv rows [q heads | k heads | v heads] (as many kv heads
 // as heads), head_dim 64.
-// One wave per (seat, head): lanes own ring entries for the scores (each key row read once for all T queries);
-// for P.V lane l takes keys j = l / 8 (mod 8) and dims 8 (l % 8) .. + 7, and the 8 key groups are summed by
-// shuffles. The head-0 wave records key_pos; every wave knows the positions of the entries this call writes, so
-// no wave depends on another's key_pos write.
+// One 4-wave workgroup per (seat, head). Thread j owns ring entry j for the scores (its key row read whole, the
+// queries read from LDS as broadcasts); the softmax is block-wide; for P.V wave w sums entries 64 w .. 64 w + 63
+// with lane (g, d8) taking keys g (mod 8) and dims 8 d8 .. + 7, all loads in flight at once and no branch around
+// them (masked entries have probability 0); the 8 key groups meet by shuffles and the 4 waves in LDS. Each key
+// and value row is read once for all T queries. The head-0 workgroup records key_pos; every workgroup knows the
+// positions of the entries this call writes, so none depends on another's key_pos write.
 constexpr int RA_HD = 64;
 constexpr int RA_RING = 256;
 constexpr int RA_T = 8;
 template <int DT>
-__global__ __launch_bounds__(64) void ring_attn_kernel(const uint16_t* __restrict__ qkv, long ld_qkv,
-                                                       uint16_t* kring, uint16_t* vring, int64_t* key_pos,
-                                                       const int64_t* __restrict__ tokens,
-                                                       const int64_t* __restrict__ slots,
-                                                       const float* __restrict__ inv_freq, float rope_scale,
-                                                       uint16_t* __restrict__ out, long ld_out, int T, int H, int ring,
-                                                       int window) {
+__global__ __launch_bounds__(256) void ring_attn_kernel(const uint16_t* __restrict__ qkv, long ld_qkv,
+                                                        uint16_t* kring, uint16_t* vring, int64_t* key_pos,
+                                                        const int64_t* __restrict__ tokens,
+                                                        const int64_t* __restrict__ slots,
+                                                        const float* __restrict__ inv_freq, float rope_scale,
+                                                        uint16_t* __restrict__ out, long ld_out, int T, int H, int ring,
+                                                        int window) {
   __shared__ float qs[RA_T][RA_HD];
   __shared__ float pw[RA_T][RA_RING];
+  __shared__ float red[2][RA_T][4];
+  __shared__ float part[4][RA_T][RA_HD];
   const int b = blockIdx.x, h = blockIdx.y;
-  const int l = threadIdx.x;
+  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
   const long slot = slots[b];
   const long p0 = tokens[slot];
   uint16_t* kr = kring + slot * (long)ring * H * RA_HD;  // [ring][H][hd]
   uint16_t* vr = vring + slot * (long)ring * H * RA_HD;
   int64_t* kp = key_pos + slot * (long)ring;
-  const int half = RA_HD / 2;
-  const int partner = l < half ? l + half : l - half;
-  const float sgn = l < half ? -1.f : 1.f;
-  const float f = inv_freq[l < half ? l : l - half];
-  for (int t = 0; t < T; ++t) {
-    const long pos = p0 + t;
-    const float ang = (float)pos * f;
-    const float cs = cosf(ang) * rope_scale, sn = sinf(ang) * rope_scale;
-    const uint16_t* r = qkv + ((long)b * T + t) * ld_qkv;
-    qs[t][l] = E<DT>::to_f(r[h * RA_HD + l]) * cs + sgn * E<DT>::to_f(r[h * RA_HD + partner]) * sn;
-    const float kv = E<DT>::to_f(r[(H + h) * RA_HD + l]) * cs + sgn * E<DT>::to_f(r[(H + h) * RA_HD + partner]) * sn;
-    const long e = pos % ring;
-    kr[(e * H + h) * RA_HD + l] = E<DT>::from_f(kv);
-    vr[(e * H + h) * RA_HD + l] = r[(2 * H + h) * RA_HD + l];
-    if (h == 0 && l == 0) kp[e] = pos;
-  }
-  __syncthreads();  // the wave's queries (LDS) and new ring rows (global) are visible to all its lanes
-  const long new_lo = p0 % ring;
-  float sc[RA_T][RA_RING / 64];
-#pragma unroll
-  for (int u = 0; u < RA_RING / 64; ++u) {
-    const int j = l + 64 * u;
-    long kj = NEVER_POS;
-    if (j < ring) {
-      const long d = ((long)j - new_lo + ring) % ring;  // entries written by this call hold p0 + d
-      kj = d < T ? p0 + d : kp[j];
-    }
-    float acc[RA_T];
-#pragma unroll
-    for (int t = 0; t < RA_T; ++t) acc[t] = 0.f;
-    if (kj > p0 - window && kj < p0 + T) {  // visible to at least one of the T queries
-      const uint16_t* krow = kr + ((long)j * H + h) * RA_HD;
-#pragma unroll
-      for (int d = 0; d < RA_HD; d += 8) {
-        const u16x8 kv = ld16(krow + d);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float kf = E<DT>::to_f(kv.v[e]);
-#pragma unroll
-          for (int t = 0; t < RA_T; ++t)
-            if (t < T) acc[t] += qs[t][d + e] * kf;
-        }
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < RA_T; ++t) {
+  {  // RoPE and ring writes: wave w takes tokens w, w + 4
+    const int half = RA_HD / 2;
+    const int partner = l < half ? l + half : l - half;
+    const float sgn = l < half ? -1.f : 1.f;
+    const float f = inv_freq[l < half ? l : l - half];
+    for (int t = wave; t < T; t += 4) {
       const long pos = p0 + t;
-      sc[t][u] = (t < T && kj <= pos && kj > pos - window) ? acc[t] * 0.125f : -INFINITY;
+      const float ang = (float)pos * f;
+      const float cs = cosf(ang) * rope_scale, sn = sinf(ang) * rope_scale;
+      const uint16_t* r = qkv + ((long)b * T + t) * ld_qkv;
+      qs[t][l] = E<DT>::to_f(r[h * RA_HD + l]) * cs + sgn * E<DT>::to_f(r[h * RA_HD + partner]) * sn;
+      const float kv = E<DT>::to_f(r[(H + h) * RA_HD + l]) * cs + sgn * E<DT>::to_f(r[(H + h) * RA_HD + partner]) * sn;
+      const long e = pos % ring;
+      kr[(e * H + h) * RA_HD + l] = E<DT>::from_f(kv);
+      vr[(e * H + h) * RA_HD + l] = r[(2 * H + h) * RA_HD + l];
+      if (h == 0 && l == 0) kp[e] = pos;
     }
   }
-  float inv_sum[RA_T];
+  __syncthreads();  // queries (LDS) and this call's ring rows (global) are visible to the whole workgroup
+  // scores: thread j owns entry j; entries this call wrote hold p0 + d, d = (j - p0 % ring) mod ring < T
+  const int j = tid;
+  long kj = NEVER_POS;
+  u16x8 k8[RA_HD / 8];
+#pragma unroll
+  for (int d = 0; d < RA_HD / 8; ++d) k8[d] = u16x8{};
+  if (j < ring) {
+    const uint16_t* krow = kr + ((long)j * H + h) * RA_HD;
+#pragma unroll
+    for (int d = 0; d < RA_HD / 8; ++d) k8[d] = ld16(krow + 8 * d);
+    const long dd = ((long)j - p0 % ring + ring) % ring;
+    kj = dd < T ? p0 + dd : kp[j];
+  }
+  float sc[RA_T];
+#pragma unroll
+  for (int t = 0; t < RA_T; ++t) {
+    sc[t] = -INFINITY;
+    if (t >= T) continue;
+    float acc = 0.f;
+#pragma unroll
+    for (int d = 0; d < RA_HD / 8; ++d) {
+      const float4 qa = *reinterpret_cast<const float4*>(&qs[t][8 * d]);
+      const float4 qb = *reinterpret_cast<const float4*>(&qs[t][8 * d + 4]);
+      acc += qa.x * E<DT>::to_f(k8[d].v[0]) + qa.y * E<DT>::to_f(k8[d].v[1]) + qa.z * E<DT>::to_f(k8[d].v[2]) +
+             qa.w * E<DT>::to_f(k8[d].v[3]) + qb.x * E<DT>::to_f(k8[d].v[4]) + qb.y * E<DT>::to_f(k8[d].v[5]) +
+             qb.z * E<DT>::to_f(k8[d].v[6]) + qb.w * E<DT>::to_f(k8[d].v[7]);
+    }
+    const long pos = p0 + t;
+    if (kj <= pos && kj > pos - window) sc[t] = acc * 0.125f;  // NEVER_POS and j >= ring never qualify
+  }
+  // block-wide softmax per query
 #pragma unroll
   for (int t = 0; t < RA_T; ++t) {
     if (t >= T) break;
-    float mx = sc[t][0];
-#pragma unroll
-    for (int u = 1; u < RA_RING / 64; ++u) mx = fmaxf(mx, sc[t][u]);
-    mx = wave_max_xor(mx, 64);  // finite: query t sees its own key
-    float sum = 0.f;
-#pragma unroll
-    for (int u = 0; u < RA_RING / 64; ++u) {
-      const float pe = sc[t][u] == -INFINITY ? 0.f : expf(sc[t][u] - mx);
-      sum += pe;
-      if (l + 64 * u < ring) pw[t][l + 64 * u] = pe;
-    }
-    inv_sum[t] = 1.f / wave_sum_xor(sum, 64);
+    const float m = wave_max_xor(sc[t], 64);
+    if (l == 0) red[0][t][wave] = m;
   }
   __syncthreads();
+  float mx[RA_T];
+#pragma unroll
+  for (int t = 0; t < RA_T; ++t) {
+    if (t >= T) break;
+    mx[t] = fmaxf(fmaxf(red[0][t][0], red[0][t][1]), fmaxf(red[0][t][2], red[0][t][3]));  // finite: own key
+    const float pe = sc[t] == -INFINITY ? 0.f : expf(sc[t] - mx[t]);
+    if (j < ring) pw[t][j] = pe;
+    const float sm = wave_sum_xor(pe, 64);
+    if (l == 0) red[1][t][wave] = sm;
+  }
+  __syncthreads();
+  // P.V over this wave's 64 entries
   const int g = l >> 3, dc = 8 * (l & 7);
   float o[RA_T][8];
 #pragma unroll
   for (int t = 0; t < RA_T; ++t)
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[t][e] = 0.f;
-  for (int j = g; j < ring; j += 8) {
-    float pj[RA_T];
-    bool any = false;
+  u16x8 vv[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int jj = 64 * wave + g + 8 * i;
+    vv[i] = u16x8{};
+    if (jj < ring) vv[i] = ld16(vr + ((long)jj * H + h) * RA_HD + dc);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int jj = 64 * wave + g + 8 * i;
 #pragma unroll
     for (int t = 0; t < RA_T; ++t) {
-      pj[t] = t < T ? pw[t][j] : 0.f;
-      any |= pj[t] != 0.f;
-    }
-    if (!any) continue;
-    const u16x8 vv = ld16(vr + ((long)j * H + h) * RA_HD + dc);
+      if (t >= T) continue;
+      const float pj = jj < ring ? pw[t][jj] : 0.f;  // 0 for masked entries, whose values are finite
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float vf = E<DT>::to_f(vv.v[e]);
-#pragma unroll
-      for (int t = 0; t < RA_T; ++t) o[t][e] += pj[t] * vf;
+      for (int e = 0; e < 8; ++e) o[t][e] += pj * E<DT>::to_f(vv[i].v[e]);
     }
   }
 #pragma unroll
   for (int t = 0; t < RA_T; ++t) {
     if (t >= T) break;
-    u16x8 ov;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       float v = o[t][e];
       v += __shfl_xor(v, 8, 64);
       v += __shfl_xor(v, 16, 64);
       v += __shfl_xor(v, 32, 64);
-      ov.v[e] = E<DT>::from_f(v * inv_sum[t]);
+      o[t][e] = v;
     }
-    if (g == 0) st16(out + ((long)b * T + t) * ld_out + h * RA_HD + dc, ov);
+    if (g == 0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part[wave][t][dc + e] = o[t][e];
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < T * RA_HD; i += 256) {
+    const int t = i / RA_HD, d = i % RA_HD;
+    const float sum = red[1][t][0] + red[1][t][1] + red[1][t][2] + red[1][t][3];
+    const float v = part[0][t][d] + part[1][t][d] + part[2][t][d] + part[3][t][d];
+    out[((long)b * T + t) * ld_out + h * RA_HD + d] = E<DT>::from_f(v / sum);
   }
 }
 
@@ -468,7 +524,7 @@ M3X_API int m3x_ring_attn(const void* qkv, long ld_qkv, void* kring, void* vring
   if (!qkv || !kring || !vring || !key_pos || !tokens || !slots || !inv_freq || !out) return M3X_ENULL;
   if (!m3x_aligned16(qkv) || !m3x_aligned16(kring)) return M3X_EINVAL;
   if (!m3x_aligned16(out) || (ld_out & 7)) return M3X_EINVAL;
-  CODEC_LAUNCH(ring_attn_kernel, dim3(B, H), dim3(64), (const uint16_t*)qkv, ld_qkv, (uint16_t*)kring,
+  CODEC_LAUNCH(ring_attn_kernel, dim3(B, H), dim3(256), (const uint16_t*)qkv, ld_qkv, (uint16_t*)kring,
                (uint16_t*)vring, key_pos, tokens, slots, inv_freq, rope_scale, (uint16_t*)out, ld_out, T, H, ring,
                window);
   return M3X_OK;
@@ -494,5 +550,18 @@ M3X_API int m3x_final_conv(const void* x, long ld_x, void* state, long ld_state,
   if (!x || !slots || !w || !pcm || (k > 1 && !state)) return M3X_ENULL;
   CODEC_LAUNCH(final_conv_kernel, dim3(B, m3x_ceil_div(T, chunk)), dim3(CODEC_THREADS), (const uint16_t*)x, ld_x,
                (uint16_t*)state, ld_state, slots, w, bias, pcm, ld_pcm, T, C, k, chunk);
+  return M3X_OK;
+}
+
+M3X_API int m3x_resid_ln(void* h, long ld_h, const void* a, long ld_a, const void* scale, const void* w,
+                         const void* b, void* y, long ld_y, float eps, int rows, int n, int dtype, void* stream) {
+  if (rows < 0 || n != RLN_N || ld_h < n || ld_a < n || ld_y < n || ((ld_h | ld_a | ld_y) & 7)) return M3X_EINVAL;
+  if (rows == 0) return M3X_OK;
+  if (!h || !a || !scale || !w || !b || !y) return M3X_ENULL;
+  if (!m3x_aligned16(h) || !m3x_aligned16(a) || !m3x_aligned16(scale) || !m3x_aligned16(w) || !m3x_aligned16(b) ||
+      !m3x_aligned16(y))
+    return M3X_EINVAL;
+  CODEC_LAUNCH(resid_ln_kernel, dim3(m3x_ceil_div(rows, 4)), dim3(256), (uint16_t*)h, ld_h, (const uint16_t*)a, ld_a,
+               (const uint16_t*)scale, (const uint16_t*)w, (const uint16_t*)b, (uint16_t*)y, ld_y, eps, rows);
   return M3X_OK;
 }

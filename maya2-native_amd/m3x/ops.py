@@ -432,6 +432,13 @@ def rows_op(g, out, bias=None, scale=None, res=None, use_elu=False):
           "rows_op")
 
 
+def resid_ln(h, a, scale, w, b, eps, y):
+    """h = h + scale * a in place (16-bit rounding once), then y = LayerNorm(h) with (w, b, eps); rows of 512."""
+    _dev(h, a, scale, w, b, y)
+    check(lib().m3x_resid_ln(_p(h), h.stride(0), _p(a), a.stride(0), _p(scale), _p(w), _p(b), _p(y), y.stride(0),
+                             float(eps), h.shape[0], h.shape[1], _dt(h), _stream()), "resid_ln")
+
+
 def convt_overlap(cols, tail, slots, bias, out, B, Tin, C, k, s, chunk):
     """Overlap-add of a transposed conv's GEMM columns with per-slot tails; out [B * Tin * s, C]."""
     _dev(cols, tail, slots, bias, out)

@@ -8,8 +8,9 @@ state per slot plus the dummy row max_slots that pads a batch to its bucket.
 
 The frame runs as m3x launches on time-major activations [seat * T + t, channels] in 16-bit with fp32
 accumulation: the codebook sum (m3x_rvq_decode) and its 1x1 projections as one GEMM, the depthwise upsample with
-its tail (m3x_dwconvt), per transformer layer LayerNorm, q|k|v GEMM, ring attention (m3x_ring_attn), o GEMM,
-layer-scaled residual, LayerNorm, fc1 GEMM + GELU, fc2 GEMM, layer-scaled residual; every SEANet conv as
+its tail (m3x_dwconvt), per transformer layer q|k|v GEMM, ring attention (m3x_ring_attn), o GEMM, layer-scaled
+residual fused with the next LayerNorm (m3x_resid_ln), fc1 GEMM + GELU, fc2 GEMM, layer-scaled residual fused with
+the next layer's LayerNorm; every SEANet conv as
 history gather (m3x_conv_gather, ELU fused) + GEMM + bias/residual/ELU row op (m3x_rows_op), every transposed
 conv as GEMM + overlap-add with tail (m3x_convt_overlap), and the last conv to fp32 PCM (m3x_final_conv).
 """
@@ -216,19 +217,23 @@ class StaticMimi:
         ops.linear(bf["e"], self.w_quant, bf["u"])
         h, y = bf["h"], bf["y"]
         ops.dwconvt(bf["u"], self.w_up, self.state["upsample"], slots, h, self.up_k, self.up_s)
+        w, b, eps = self.layers[0]["ln1"]
+        ops.add_norm(h, None, None, None, y, w, b, eps, 1, ops.NORM_LAYER)
         for li, L in enumerate(self.layers):
-            w, b, eps = L["ln1"]
-            ops.add_norm(h, None, None, None, y, w, b, eps, 1, ops.NORM_LAYER)
+            # y = input_layernorm(h) here
             ops.linear(y, L["qkv"], bf["qkv"])
             ops.ring_attn(bf["qkv"], self.kv[li, 0], self.kv[li, 1], self.key_pos, self.tokens, slots, self.inv_freq,
                           self.rope_scale, bf["o"], B, T0, H, self.ring, self.window)
             ops.linear(bf["o"], L["o"], bf["a"])
-            ops.rows_op(bf["a"], h, scale=L["s1"], res=h)
             w, b, eps = L["ln2"]
-            ops.add_norm(h, None, None, None, y, w, b, eps, 1, ops.NORM_LAYER)
+            ops.resid_ln(h, bf["a"], L["s1"], w, b, eps, y)  # h += s1 * attn; y = post_attention_layernorm(h)
             ops.linear_act(y, L["fc1"], None, ops.ACT_GELU, bf["f"])
             ops.linear(bf["f"], L["fc2"], bf["a"])
-            ops.rows_op(bf["a"], h, scale=L["s2"], res=h)
+            if li + 1 < len(self.layers):
+                w, b, eps = self.layers[li + 1]["ln1"]
+                ops.resid_ln(h, bf["a"], L["s2"], w, b, eps, y)  # h += s2 * mlp; y = next input_layernorm(h)
+            else:
+                ops.rows_op(bf["a"], h, scale=L["s2"], res=h)
         ops.advance_tokens(self.tokens, slots, B, T0, self.dummy)
         # SEANet: x is the current activation [B * t, C]
         x, t = h, T0
