@@ -109,7 +109,7 @@ int m3x_act(const void* in, long ld_in, void* out, long ld_out, int rows, int I,
 
 /* Row r = (b, t) = (r / T, r % T): x_out = dt(x + a) [then dt(x_out + c[b])]; y = norm(x_out) with LayerNorm
  * (w, b) or RMSNorm (w). x and a are read at base + b*s?b + t*s?t; x_out and y are contiguous [rows, n]; c rows
- * have stride s_c (0 broadcasts); a, c, x_out may be NULL; n in {1024, 2048}.
+ * have stride s_c (0 broadcasts); a, c, x_out may be NULL; n in {512, 1024, 2048}.
  * Replaces `_add_ln`/`add_ln` (serve/fast_depth_kernels.py:14-45) and the first-layer `n1` (serve/fast_depth.py:164). */
 int m3x_add_norm(const void* x, long sxb, long sxt, const void* a, long sab, long sat, const void* c, long s_c,
                  void* x_out, void* y, const void* w, const void* b, float eps, int rows, int T, int n, int kind,
