@@ -263,6 +263,13 @@ int m3x_rows_op(const void* g, long ld_g, const void* bias, const void* scale, c
 int m3x_resid_ln(void* h, long ld_h, const void* a, long ld_a, const void* scale, const void* w, const void* b,
                  void* y, long ld_y, float eps, int rows, int n, int dtype, void* stream);
 
+/* y = act(res + (dt(x . w^T) + bias)) for N in {16, 32, 64, 128} output channels, w packed by m3x_pack_weight,
+ * K % 32 == 0; bias and res optional; act = ELU when use_elu. The product of m3x_linear followed by the arithmetic
+ * of m3x_rows_op in one launch. Replaces a SEANet MimiConv1d's `module.conv(x)` with its bias, the resnet
+ * `shortcut + x` and the next ELU (serve/fast_codec.py:104-111,127-130) when the conv has at most 128 outputs. */
+int m3x_conv_gemm(const void* x, long ldx, const void* w_packed, const void* bias, const void* res, long ld_res,
+                  void* y, long ldy, int M, int N, int K, int use_elu, int dtype, void* stream);
+
 /* Overlap-add of a transposed conv (kernel k, stride s, s < k <= 2 s) from its GEMM columns cols[b*Tin + t,
  * j*C + c]: out [B * Tin * s, C] with the slot's tail added to the first k - s frames and bias; the new tail is the
  * overflow without bias. Replaces the MimiConvTranspose1d branch of `_layer` (serve/fast_codec.py:112-126). */
@@ -282,7 +289,8 @@ int m3x_ring_attn(const void* qkv, long ld_qkv, void* kring, void* vring, int64_
  * Replaces `self.tokens.index_copy_(0, slots, start + count); self.tokens[self.dummy].zero_()` (:183-184). */
 int m3x_advance_tokens(int64_t* tokens, const int64_t* slots, int B, int T, int dummy, void* stream);
 
-/* Last conv (C -> 1 channel, kernel k, causal) to fp32 PCM [B, T] with fp32 weights w[j*C + c] and the slot's
+/* Last conv (C -> 1 channel, kernel k, causal; C % 8 == 0, k * C <= 4096) to fp32 PCM [B, T] with fp32 weights
+ * w[j*C + c] and the slot's
  * k - 1 stored input frames. Replaces the final MimiConv1d of `_forward` (serve/fast_codec.py:189-191). */
 int m3x_final_conv(const void* x, long ld_x, void* state, long ld_state, const int64_t* slots, const float* w,
                    float bias, float* pcm, long ld_pcm, int B, int T, int C, int k, int chunk, int dtype,

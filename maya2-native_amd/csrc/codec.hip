@@ -173,6 +173,86 @@ __global__ __launch_bounds__(256) void resid_ln_kernel(uint16_t* h, long ld_h, c
 }
 
 // ---------------------------------------------------------------------------------------------------------
+// Thin GEMM with the conv epilogue, for the SEANet convs with at most 128 output channels:
+// y[m, n] = act(res[m, n] + (dt(x[m, :] . w[n, :]) + bias[n])) (m3x_linear's product, then m3x_rows_op's
+// arithmetic), w packed by m3x_pack_weight, N = 16 NT, K % 32 == 0; bias and res optional, act = ELU when use_elu.
+// Each wave owns 16 MT rows and all N columns: the activation fragments are loaded straight into the MFMA's B
+// operand (each activation element is read once), the weight fragments (K * N * 2 bytes, cache resident) into A.
+template <int DT, int NT, int MT>
+__global__ __launch_bounds__(256) void conv_gemm_kernel(const uint16_t* __restrict__ X, long ldx,
+                                                        const uint16_t* __restrict__ Wp,
+                                                        const uint16_t* __restrict__ bias, const uint16_t* res,
+                                                        long ld_res, uint16_t* Y, long ldy, int M, int K,
+                                                        int use_elu) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = threadIdx.x & 63, li = l & 15, lg = l >> 4;
+  const long m0 = ((long)blockIdx.x * 4 + wave) * (16 * MT);
+  if (m0 >= M) return;  // wave-uniform
+  f32x4_t acc[NT][MT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int j = 0; j < MT; ++j) acc[t][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const int ks = K / 32;
+  // the fragments of step s + 1 are in flight while step s multiplies
+  u16x8 a[2][NT], b[2][MT];
+  auto load = [&](int s, int buf) {
+#pragma unroll
+    for (int j = 0; j < MT; ++j) {
+      const long row = m0 + 16 * j + li;
+      b[buf][j] = u16x8{};
+      if (row < M) b[buf][j] = ld16(X + row * ldx + 32 * s + 8 * lg);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) a[buf][t] = ld16(Wp + ((long)t * ks + s) * 512 + 8 * l);
+  };
+  load(0, 0);
+  for (int s = 0; s < ks; s += 2) {
+    if (s + 1 < ks) load(s + 1, 1);
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int j = 0; j < MT; ++j) acc[t][j] = mfma16x16x32<DT>(a[0][t], b[0][j], acc[t][j]);
+    if (s + 1 >= ks) break;
+    if (s + 2 < ks) load(s + 2, 0);
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int j = 0; j < MT; ++j) acc[t][j] = mfma16x16x32<DT>(a[1][t], b[1][j], acc[t][j]);
+  }
+  // lane (li, lg) holds columns 16 t + 4 lg + r of row m0 + 16 j + li. res may be y itself (in place): every
+  // residual and bias value of the lane is read before its first store.
+#pragma unroll
+  for (int j = 0; j < MT; ++j) {
+    const long m = m0 + 16 * j + li;
+    if (m >= M) continue;
+    uint2 bb[NT], rr[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int n = 16 * t + 4 * lg;
+      bb[t] = bias ? *reinterpret_cast<const uint2*>(bias + n) : uint2{0, 0};
+      rr[t] = res ? *reinterpret_cast<const uint2*>(res + m * ld_res + n) : uint2{0, 0};
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int n = 16 * t + 4 * lg;
+      const uint16_t* bv = reinterpret_cast<const uint16_t*>(&bb[t]);
+      const uint16_t* rv = reinterpret_cast<const uint16_t*>(&rr[t]);
+      uint16_t o[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float v = rnd<DT>(acc[t][j][r]);
+        if (bias) v = v + E<DT>::to_f(bv[r]);
+        if (res) v = E<DT>::to_f(rv[r]) + v;
+        if (use_elu) v = elu1(v);
+        o[r] = E<DT>::from_f(v);
+      }
+      *reinterpret_cast<uint2*>(Y + m * ldy + n) = *reinterpret_cast<const uint2*>(o);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------
 // Transposed conv overlap-add (:112-130). cols[b * Tin + t, j * C + c] = x[b, t] . W[:, c, j] comes from the GEMM;
 // output frame o < Tin * s of seat b is the sum of its contributions (t, j = o - t s, 0 <= j < k) + tail[slot, o, c]
 // (o < k - s) + bias[c]; the new tail[slot, i, c] = the contributions to frame Tin * s + i, without bias (the
@@ -397,7 +477,9 @@ __global__ void advance_tokens_kernel(int64_t* tokens, const int64_t* __restrict
 // Last conv to PCM (decoder.layers[-1], C -> 1 channel, kernel k, causal) in fp32 with fp32 weights:
 // pcm[b, t] = bias + sum_j sum_c w[j * C + c] joined[t + j][c], joined = the slot's k - 1 stored frames then x
 // (ELU already applied by the producing row op); the state becomes joined's last k - 1 frames.
-// Grid (B, ceil(T / chunk)), chunk >= k - 1; one wave per output sample.
+// Grid (B, ceil(T / chunk)), chunk >= k - 1; one thread per output sample (rows read as 16-byte vectors,
+// weights from LDS); k * C <= 4096.
+constexpr int FC_W = 4096;
 template <int DT>
 __global__ __launch_bounds__(CODEC_THREADS) void final_conv_kernel(const uint16_t* __restrict__ x, long ld_x,
                                                                    uint16_t* state, long ld_state,
@@ -405,24 +487,30 @@ __global__ __launch_bounds__(CODEC_THREADS) void final_conv_kernel(const uint16_
                                                                    const float* __restrict__ w, float bias,
                                                                    float* __restrict__ pcm, long ld_pcm, int T, int C,
                                                                    int k, int chunk) {
+  __shared__ float ws[FC_W];
   const int b = blockIdx.x;
   const int t0 = blockIdx.y * chunk, t1 = min(T, t0 + chunk);
   const int pad = k - 1;
   const long row0 = (long)b * T;
   uint16_t* st = pad ? state + slots[b] * ld_state : nullptr;
-  const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
-  for (int t = t0 + wave; t < t1; t += CODEC_THREADS / 64) {
+  for (int i = threadIdx.x; i < k * C; i += CODEC_THREADS) ws[i] = w[i];
+  __syncthreads();
+  const int cv = C / 8;
+  for (int t = t0 + threadIdx.x; t < t1; t += CODEC_THREADS) {
     float acc = 0.f;
-    for (int e = l; e < k * C; e += 64) {
-      const int j = e / C, c = e - j * C;
+    for (int j = 0; j < k; ++j) {
       const int i = t + j;
-      acc += w[e] * E<DT>::to_f(i < pad ? st[(long)i * C + c] : x[(row0 + i - pad) * ld_x + c]);
+      const uint16_t* row = i < pad ? st + (long)i * C : x + (row0 + i - pad) * ld_x;
+      const float* wj = ws + j * C;
+      for (int c8 = 0; c8 < cv; ++c8) {
+        const u16x8 v = ld16(row + 8 * c8);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc += wj[8 * c8 + e] * E<DT>::to_f(v.v[e]);
+      }
     }
-    acc = wave_sum_xor(acc, 64);
-    if (l == 0) pcm[(long)b * ld_pcm + t] = acc + bias;
+    pcm[(long)b * ld_pcm + t] = acc + bias;
   }
   if (!pad || blockIdx.y) return;
-  const int cv = C / 8;
   u16x8 keep[CODEC_KEEP / 8];
   int n = 0;
   for (int e = threadIdx.x; e < pad * cv; e += CODEC_THREADS)
@@ -546,6 +634,7 @@ M3X_API int m3x_final_conv(const void* x, long ld_x, void* state, long ld_state,
     return M3X_EINVAL;
   if (!m3x_aligned16(x) || (k > 1 && !m3x_aligned16(state))) return M3X_EINVAL;
   if (k > 1 && (ld_state < (long)(k - 1) * C || (k - 1) * C > CODEC_KEEP * CODEC_THREADS)) return M3X_EINVAL;
+  if ((long)k * C > FC_W) return M3X_EINVAL;
   if (B == 0) return M3X_OK;
   if (!x || !slots || !w || !pcm || (k > 1 && !state)) return M3X_ENULL;
   CODEC_LAUNCH(final_conv_kernel, dim3(B, m3x_ceil_div(T, chunk)), dim3(CODEC_THREADS), (const uint16_t*)x, ld_x,
@@ -564,4 +653,34 @@ M3X_API int m3x_resid_ln(void* h, long ld_h, const void* a, long ld_a, const voi
   CODEC_LAUNCH(resid_ln_kernel, dim3(m3x_ceil_div(rows, 4)), dim3(256), (uint16_t*)h, ld_h, (const uint16_t*)a, ld_a,
                (const uint16_t*)scale, (const uint16_t*)w, (const uint16_t*)b, (uint16_t*)y, ld_y, eps, rows);
   return M3X_OK;
+}
+
+M3X_API int m3x_conv_gemm(const void* x, long ldx, const void* w_packed, const void* bias, const void* res,
+                          long ld_res, void* y, long ldy, int M, int N, int K, int use_elu, int dtype, void* stream) {
+  if (M < 0 || K < 32 || K % 32 || (N != 16 && N != 32 && N != 64 && N != 128) || ldx < K || ldy < N || (res && ld_res < N) || ((ldx | ldy | (res ? ld_res : 0)) & 7))
+    return M3X_EINVAL;
+  if (M == 0) return M3X_OK;
+  if (!x || !w_packed || !y) return M3X_ENULL;
+  if (!m3x_aligned16(x) || !m3x_aligned16(w_packed) || !m3x_aligned16(y) || (res && !m3x_aligned16(res)) ||
+      (bias && (((uintptr_t)bias) & 7)))
+    return M3X_EINVAL;
+  const int mt = M >= 64 * 1024 ? 2 : 1;  // two row tiles per wave once the grid fills the chip anyway
+  const dim3 grid(m3x_ceil_div(M, 4 * 16 * mt));
+  const uint16_t *X = (const uint16_t*)x, *W = (const uint16_t*)w_packed, *Bi = (const uint16_t*)bias,
+                 *R = (const uint16_t*)res;
+  uint16_t* Yp = (uint16_t*)y;
+  hipStream_t st = (hipStream_t)stream;
+#define CG_CASE(DTT, NTT, MTT)                                                                                     \
+  if (dtype == DTT && N == 16 * NTT && mt == MTT) {                                                                \
+    hipLaunchKernelGGL((conv_gemm_kernel<DTT, NTT, MTT>), grid, dim3(256), 0, st, X, ldx, W, Bi, R, ld_res, Yp, ldy, \
+                       M, K, use_elu);                                                                             \
+    M3X_CHECK_LAUNCH();                                                                                            \
+    return M3X_OK;                                                                                                 \
+  }
+  CG_CASE(M3X_F16, 1, 1) CG_CASE(M3X_F16, 2, 1) CG_CASE(M3X_F16, 4, 1) CG_CASE(M3X_F16, 8, 1)
+  CG_CASE(M3X_F16, 1, 2) CG_CASE(M3X_F16, 2, 2) CG_CASE(M3X_F16, 4, 2) CG_CASE(M3X_F16, 8, 2)
+  CG_CASE(M3X_BF16, 1, 1) CG_CASE(M3X_BF16, 2, 1) CG_CASE(M3X_BF16, 4, 1) CG_CASE(M3X_BF16, 8, 1)
+  CG_CASE(M3X_BF16, 1, 2) CG_CASE(M3X_BF16, 2, 2) CG_CASE(M3X_BF16, 4, 2) CG_CASE(M3X_BF16, 8, 2)
+#undef CG_CASE
+  return M3X_EUNSUPPORTED;
 }

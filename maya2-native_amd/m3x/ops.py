@@ -432,6 +432,16 @@ def rows_op(g, out, bias=None, scale=None, res=None, use_elu=False):
           "rows_op")
 
 
+def conv_gemm(x, w, y, bias=None, res=None, use_elu=False):
+    """y = act(res + (x @ W.T + bias)) for a packed W with N in {16, 32, 64, 128}; act = ELU when use_elu."""
+    if not isinstance(w, PackedWeight):
+        raise TypeError("conv_gemm: the weight must be packed with ops.pack_weight")
+    _dev(x, w.data, y, bias, res)
+    check(lib().m3x_conv_gemm(_p(x), x.stride(0), _p(w.data), _p(bias), _p(res), 0 if res is None else res.stride(0),
+                              _p(y), y.stride(0), x.shape[0], w.N, w.K, int(use_elu), _dt(x), _stream()), "conv_gemm")
+    return y
+
+
 def resid_ln(h, a, scale, w, b, eps, y):
     """h = h + scale * a in place (16-bit rounding once), then y = LayerNorm(h) with (w, b, eps); rows of 512."""
     _dev(h, a, scale, w, b, y)

@@ -29,6 +29,12 @@ class _Bucket:
     __slots__ = ("graph", "slots", "codes", "out", "bufs", "pinned", "events", "turn")
 
 
+def _thin(n, k):
+    """Convs that go to the fused conv GEMM (m3x_conv_gemm): up to 128 outputs over a short reduction (a wave
+    walks K alone, so a long K with few rows is faster on the tiled GEMM + row op)."""
+    return n in (16, 32, 64, 128) and k <= 384
+
+
 def _chunk(rows, B, depth, target=2048):
     """Rows per workgroup of a stateful kernel over `rows` rows per seat: about `target` workgroups for the batch,
     at least the state's depth (only the first chunk of a seat may read its state)."""
@@ -250,12 +256,15 @@ class StaticMimi:
             else:
                 a, b = st["a"], st["b"]
                 inner = self._conv(a, x, slots, B, t, out=bf["I"])
-                g = bf["G"][:B * t * b["cout"]].view(B * t, b["cout"])
-                ops.linear(inner, b["w"], g)
-                ops.rows_op(g, x, bias=b["bias"], res=x, use_elu=True)  # shortcut + block, then the next ELU
+                if _thin(b["cout"], b["cin"]):  # shortcut + block, then the next ELU
+                    ops.conv_gemm(inner, b["w"], x, bias=b["bias"], res=x, use_elu=True)
+                else:
+                    g = bf["G"][:B * t * b["cout"]].view(B * t, b["cout"])
+                    ops.linear(inner, b["w"], g)
+                    ops.rows_op(g, x, bias=b["bias"], res=x, use_elu=True)
         f = self.final
         ops.final_conv(x, self.state[f["key"]], slots, f["w"], f["bias"], bf["pcm"], B, t, f["cin"], f["k"],
-                       _chunk(t, B, f["k"] - 1))
+                       max(f["k"] - 1, 256))  # one thread per sample
         return bf["pcm"]
 
     def _conv(self, st, x, slots, B, t, out):
@@ -268,7 +277,10 @@ class StaticMimi:
             ops.conv_gather(x, self.state[st["key"]], slots, src, B, t, cin, k, st["dil"], st["pre_elu"],
                             _chunk(t, B, st["pad"]))
         y = out[:B * t * cout].view(B * t, cout)
-        g = self._bf["G"][:B * t * cout].view(B * t, cout) if out is not self._bf["G"] else y
+        if _thin(cout, k * cin):
+            ops.conv_gemm(src, st["w"], y, bias=st["bias"], use_elu=st["post_elu"])
+            return y
+        g = self._bf["G"][:B * t * cout].view(B * t, cout)
         ops.linear(src, st["w"], g)
         ops.rows_op(g, y, bias=st["bias"], use_elu=st["post_elu"])
         return y
