@@ -340,6 +340,8 @@ __global__ __launch_bounds__(256) void ring_attn_kernel(const uint16_t* __restri
   __shared__ float pw[RA_T][RA_RING];
   __shared__ float red[2][RA_T][4];
   __shared__ float part[4][RA_T][RA_HD];
+  __shared__ __align__(16) uint16_t knew[RA_T][RA_HD];  // this call's keys (post-RoPE) and values, stored to the
+  __shared__ __align__(16) uint16_t vnew[RA_T][RA_HD];  // ring only at the end: reads of them come from here
   const int b = blockIdx.x, h = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
   const long slot = slots[b];
@@ -347,37 +349,53 @@ __global__ __launch_bounds__(256) void ring_attn_kernel(const uint16_t* __restri
   uint16_t* kr = kring + slot * (long)ring * H * RA_HD;  // [ring][H][hd]
   uint16_t* vr = vring + slot * (long)ring * H * RA_HD;
   int64_t* kp = key_pos + slot * (long)ring;
-  {  // RoPE and ring writes: wave w takes tokens w, w + 4
+  const int lo = (int)(p0 % ring);  // ring entry of token 0; token t sits at (lo + t) % ring
+  {  // RoPE: wave w takes tokens w, w + 4
     const int half = RA_HD / 2;
     const int partner = l < half ? l + half : l - half;
     const float sgn = l < half ? -1.f : 1.f;
     const float f = inv_freq[l < half ? l : l - half];
     for (int t = wave; t < T; t += 4) {
-      const long pos = p0 + t;
-      const float ang = (float)pos * f;
+      const float ang = (float)(p0 + t) * f;
       const float cs = cosf(ang) * rope_scale, sn = sinf(ang) * rope_scale;
       const uint16_t* r = qkv + ((long)b * T + t) * ld_qkv;
       qs[t][l] = E<DT>::to_f(r[h * RA_HD + l]) * cs + sgn * E<DT>::to_f(r[h * RA_HD + partner]) * sn;
-      const float kv = E<DT>::to_f(r[(H + h) * RA_HD + l]) * cs + sgn * E<DT>::to_f(r[(H + h) * RA_HD + partner]) * sn;
-      const long e = pos % ring;
-      kr[(e * H + h) * RA_HD + l] = E<DT>::from_f(kv);
-      vr[(e * H + h) * RA_HD + l] = r[(2 * H + h) * RA_HD + l];
-      if (h == 0 && l == 0) kp[e] = pos;
+      knew[t][l] = E<DT>::from_f(E<DT>::to_f(r[(H + h) * RA_HD + l]) * cs +
+                                 sgn * E<DT>::to_f(r[(H + h) * RA_HD + partner]) * sn);
+      vnew[t][l] = r[(2 * H + h) * RA_HD + l];
     }
   }
-  __syncthreads();  // queries (LDS) and this call's ring rows (global) are visible to the whole workgroup
-  // scores: thread j owns entry j; entries this call wrote hold p0 + d, d = (j - p0 % ring) mod ring < T
+  __syncthreads();  // queries and this call's rows are in LDS
+  // the values this wave multiplies in P.V: lane (g, d8) takes entries 64 w + g + 8 i, dims 8 d8 .. + 7; issued
+  // now so that they arrive while the scores and the softmax run
+  const int g = l >> 3, dc = 8 * (l & 7);
+  u16x8 vv[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int jj = 64 * wave + g + 8 * i;
+    const int dn = (jj - lo + ring) % ring;
+    vv[i] = u16x8{};
+    if (jj < ring) vv[i] = dn < T ? *reinterpret_cast<const u16x8*>(&vnew[dn][dc])
+                                  : ld16(vr + ((long)jj * H + h) * RA_HD + dc);
+  }
+  // scores: thread j owns entry j; entries this call writes hold p0 + d, d = (j - lo) mod ring < T
   const int j = tid;
   long kj = NEVER_POS;
   u16x8 k8[RA_HD / 8];
 #pragma unroll
   for (int d = 0; d < RA_HD / 8; ++d) k8[d] = u16x8{};
   if (j < ring) {
-    const uint16_t* krow = kr + ((long)j * H + h) * RA_HD;
+    const int dd = (j - lo + ring) % ring;
+    if (dd < T) {
+      kj = p0 + dd;
 #pragma unroll
-    for (int d = 0; d < RA_HD / 8; ++d) k8[d] = ld16(krow + 8 * d);
-    const long dd = ((long)j - p0 % ring + ring) % ring;
-    kj = dd < T ? p0 + dd : kp[j];
+      for (int d = 0; d < RA_HD / 8; ++d) k8[d] = *reinterpret_cast<const u16x8*>(&knew[dd][8 * d]);
+    } else {
+      const uint16_t* krow = kr + ((long)j * H + h) * RA_HD;
+#pragma unroll
+      for (int d = 0; d < RA_HD / 8; ++d) k8[d] = ld16(krow + 8 * d);
+      kj = kp[j];
+    }
   }
   float sc[RA_T];
 #pragma unroll
@@ -415,20 +433,12 @@ __global__ __launch_bounds__(256) void ring_attn_kernel(const uint16_t* __restri
     if (l == 0) red[1][t][wave] = sm;
   }
   __syncthreads();
-  // P.V over this wave's 64 entries
-  const int g = l >> 3, dc = 8 * (l & 7);
+  // P.V over this wave's 64 entries (values loaded above)
   float o[RA_T][8];
 #pragma unroll
   for (int t = 0; t < RA_T; ++t)
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[t][e] = 0.f;
-  u16x8 vv[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int jj = 64 * wave + g + 8 * i;
-    vv[i] = u16x8{};
-    if (jj < ring) vv[i] = ld16(vr + ((long)jj * H + h) * RA_HD + dc);
-  }
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int jj = 64 * wave + g + 8 * i;
@@ -462,6 +472,11 @@ __global__ __launch_bounds__(256) void ring_attn_kernel(const uint16_t* __restri
     const float sum = red[1][t][0] + red[1][t][1] + red[1][t][2] + red[1][t][3];
     const float v = part[0][t][d] + part[1][t][d] + part[2][t][d] + part[3][t][d];
     out[((long)b * T + t) * ld_out + h * RA_HD + d] = E<DT>::from_f(v / sum);
+    // this call's rows into the ring (no thread of this workgroup reads them from global memory)
+    const long e = (lo + t) % ring;
+    kr[(e * H + h) * RA_HD + d] = knew[t][d];
+    vr[(e * H + h) * RA_HD + d] = vnew[t][d];
+    if (h == 0 && d == 0) kp[e] = p0 + t;
   }
 }
 
