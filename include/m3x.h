@@ -277,7 +277,7 @@ int m3x_convt_overlap(const void* cols, long ld_cols, void* tail, long ld_tail, 
                       const void* bias, void* out, long ld_out, int B, int Tin, int C, int k, int s, int chunk,
                       int dtype, void* stream);
 
-/* Sliding-window attention of T <= 8 new tokens per seat at positions tokens[slot] + t over the slot's ring
+/* Sliding-window attention of T <= 2 new tokens per seat at positions tokens[slot] + t over the slot's ring
  * (kring/vring [slots, ring, H, 64] post-RoPE, key_pos [slots, ring]); RoPE angle pos * inv_freq[i] (fp32),
  * cos/sin times rope_scale; ring <= 256, ring >= window + T - 1. Replaces the ring writes, mask, RoPE and SDPA of
  * `_transformer` (serve/fast_codec.py:157-180). */

@@ -319,6 +319,7 @@ __global__ __launch_bounds__(CODEC_THREADS) void convt_overlap_kernel(const uint
 // the slot's ring entry p % ring with key_pos[slot, p % ring] = p; query p attends the entries with
 // p - window < key_pos <= p, softmax at scale 1/sqrt(64). qkv rows [q heads | k heads | v heads] (as many kv heads
 // as heads), head_dim 64.
+// TM bounds T at compile time, which keeps the unrolled code small.
 // One 4-wave workgroup per (seat, head). Thread j owns ring entry j for the scores (its key row read whole, the
 // queries read from LDS as broadcasts); the softmax is block-wide; for P.V wave w sums entries 64 w .. 64 w + 63
 // with lane (g, d8) taking keys g (mod 8) and dims 8 d8 .. + 7, all loads in flight at once and no branch around
@@ -327,8 +328,8 @@ __global__ __launch_bounds__(CODEC_THREADS) void convt_overlap_kernel(const uint
 // positions of the entries this call writes, so none depends on another's key_pos write.
 constexpr int RA_HD = 64;
 constexpr int RA_RING = 256;
-constexpr int RA_T = 8;
-template <int DT>
+constexpr int RA_T = 2;  // tokens per call: Mimi's upsample makes 2 per frame
+template <int DT, int TM>
 __global__ __launch_bounds__(256) void ring_attn_kernel(const uint16_t* __restrict__ qkv, long ld_qkv,
                                                         uint16_t* kring, uint16_t* vring, int64_t* key_pos,
                                                         const int64_t* __restrict__ tokens,
@@ -336,12 +337,12 @@ __global__ __launch_bounds__(256) void ring_attn_kernel(const uint16_t* __restri
                                                         const float* __restrict__ inv_freq, float rope_scale,
                                                         uint16_t* __restrict__ out, long ld_out, int T, int H, int ring,
                                                         int window) {
-  __shared__ float qs[RA_T][RA_HD];
-  __shared__ float pw[RA_T][RA_RING];
-  __shared__ float red[2][RA_T][4];
-  __shared__ float part[4][RA_T][RA_HD];
-  __shared__ __align__(16) uint16_t knew[RA_T][RA_HD];  // this call's keys (post-RoPE) and values, stored to the
-  __shared__ __align__(16) uint16_t vnew[RA_T][RA_HD];  // ring only at the end: reads of them come from here
+  __shared__ float qs[TM][RA_HD];
+  __shared__ float pw[TM][RA_RING];
+  __shared__ float red[2][TM][4];
+  __shared__ float part[4][TM][RA_HD];
+  __shared__ __align__(16) uint16_t knew[TM][RA_HD];  // this call's keys (post-RoPE) and values, stored to the
+  __shared__ __align__(16) uint16_t vnew[TM][RA_HD];  // ring only at the end: reads of them come from here
   const int b = blockIdx.x, h = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
   const long slot = slots[b];
@@ -397,9 +398,9 @@ __global__ __launch_bounds__(256) void ring_attn_kernel(const uint16_t* __restri
       kj = kp[j];
     }
   }
-  float sc[RA_T];
+  float sc[TM];
 #pragma unroll
-  for (int t = 0; t < RA_T; ++t) {
+  for (int t = 0; t < TM; ++t) {
     sc[t] = -INFINITY;
     if (t >= T) continue;
     float acc = 0.f;
@@ -416,15 +417,15 @@ __global__ __launch_bounds__(256) void ring_attn_kernel(const uint16_t* __restri
   }
   // block-wide softmax per query
 #pragma unroll
-  for (int t = 0; t < RA_T; ++t) {
+  for (int t = 0; t < TM; ++t) {
     if (t >= T) break;
     const float m = wave_max_xor(sc[t], 64);
     if (l == 0) red[0][t][wave] = m;
   }
   __syncthreads();
-  float mx[RA_T];
+  float mx[TM];
 #pragma unroll
-  for (int t = 0; t < RA_T; ++t) {
+  for (int t = 0; t < TM; ++t) {
     if (t >= T) break;
     mx[t] = fmaxf(fmaxf(red[0][t][0], red[0][t][1]), fmaxf(red[0][t][2], red[0][t][3]));  // finite: own key
     const float pe = sc[t] == -INFINITY ? 0.f : expf(sc[t] - mx[t]);
@@ -434,16 +435,16 @@ __global__ __launch_bounds__(256) void ring_attn_kernel(const uint16_t* __restri
   }
   __syncthreads();
   // P.V over this wave's 64 entries (values loaded above)
-  float o[RA_T][8];
+  float o[TM][8];
 #pragma unroll
-  for (int t = 0; t < RA_T; ++t)
+  for (int t = 0; t < TM; ++t)
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[t][e] = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int jj = 64 * wave + g + 8 * i;
 #pragma unroll
-    for (int t = 0; t < RA_T; ++t) {
+    for (int t = 0; t < TM; ++t) {
       if (t >= T) continue;
       const float pj = jj < ring ? pw[t][jj] : 0.f;  // 0 for masked entries, whose values are finite
 #pragma unroll
@@ -451,7 +452,7 @@ __global__ __launch_bounds__(256) void ring_attn_kernel(const uint16_t* __restri
     }
   }
 #pragma unroll
-  for (int t = 0; t < RA_T; ++t) {
+  for (int t = 0; t < TM; ++t) {
     if (t >= T) break;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -627,9 +628,15 @@ M3X_API int m3x_ring_attn(const void* qkv, long ld_qkv, void* kring, void* vring
   if (!qkv || !kring || !vring || !key_pos || !tokens || !slots || !inv_freq || !out) return M3X_ENULL;
   if (!m3x_aligned16(qkv) || !m3x_aligned16(kring)) return M3X_EINVAL;
   if (!m3x_aligned16(out) || (ld_out & 7)) return M3X_EINVAL;
-  CODEC_LAUNCH(ring_attn_kernel, dim3(B, H), dim3(256), (const uint16_t*)qkv, ld_qkv, (uint16_t*)kring,
-               (uint16_t*)vring, key_pos, tokens, slots, inv_freq, rope_scale, (uint16_t*)out, ld_out, T, H, ring,
-               window);
+#define RA_LAUNCH(DTT, TMM)                                                                                    \
+  hipLaunchKernelGGL((ring_attn_kernel<DTT, TMM>), dim3(B, H), dim3(256), 0, (hipStream_t)stream,                  \
+                     (const uint16_t*)qkv, ld_qkv, (uint16_t*)kring, (uint16_t*)vring, key_pos, tokens, slots,      \
+                     inv_freq, rope_scale, (uint16_t*)out, ld_out, T, H, ring, window)
+  if (dtype == M3X_F16) RA_LAUNCH(M3X_F16, RA_T);
+  else if (dtype == M3X_BF16) RA_LAUNCH(M3X_BF16, RA_T);
+  else return M3X_EUNSUPPORTED;
+#undef RA_LAUNCH
+  M3X_CHECK_LAUNCH();
   return M3X_OK;
 }
 

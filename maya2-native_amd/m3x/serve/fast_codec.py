@@ -65,8 +65,8 @@ class StaticMimi:
         self.ring = int(ring)
         if self.ring < self.window + self.frame_tokens:
             raise ValueError("ring must hold sliding_window + frame_tokens entries")
-        if self.ring > 256 or self.frame_tokens > 8:
-            raise ValueError("ring attention holds at most 256 ring entries and 8 tokens per frame")
+        if self.ring > 256 or self.frame_tokens > 2:
+            raise ValueError("ring attention holds at most 256 ring entries and 2 tokens per frame")
         self.codebooks = int(cfg.num_quantizers)
         self.use_graphs = use_graphs
         rows = self.max_slots + 1
