@@ -329,6 +329,7 @@ __global__ __launch_bounds__(CODEC_THREADS) void convt_overlap_kernel(const uint
 constexpr int RA_HD = 64;
 constexpr int RA_RING = 256;
 constexpr int RA_T = 2;  // tokens per call: Mimi's upsample makes 2 per frame
+static_assert(RA_T <= 4, "one wave of the 4-wave workgroup per token");
 template <int DT, int TM>
 __global__ __launch_bounds__(256) void ring_attn_kernel(const uint16_t* __restrict__ qkv, long ld_qkv,
                                                         uint16_t* kring, uint16_t* vring, int64_t* key_pos,
@@ -346,57 +347,67 @@ __global__ __launch_bounds__(256) void ring_attn_kernel(const uint16_t* __restri
   const int b = blockIdx.x, h = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
   const long slot = slots[b];
+  // wave w < T handles token w: its q, k, v elements do not depend on the position, so they load first
+  const int half = RA_HD / 2;
+  const int partner = l < half ? l + half : l - half;
+  float q_l = 0.f, q_p = 0.f, k_l = 0.f, k_p = 0.f;
+  uint16_t v_l = 0;
+  if (wave < T) {
+    const uint16_t* r = qkv + ((long)b * T + wave) * ld_qkv;
+    q_l = E<DT>::to_f(r[h * RA_HD + l]);
+    q_p = E<DT>::to_f(r[h * RA_HD + partner]);
+    k_l = E<DT>::to_f(r[(H + h) * RA_HD + l]);
+    k_p = E<DT>::to_f(r[(H + h) * RA_HD + partner]);
+    v_l = r[(2 * H + h) * RA_HD + l];
+  }
   const long p0 = tokens[slot];
   uint16_t* kr = kring + slot * (long)ring * H * RA_HD;  // [ring][H][hd]
   uint16_t* vr = vring + slot * (long)ring * H * RA_HD;
   int64_t* kp = key_pos + slot * (long)ring;
   const int lo = (int)(p0 % ring);  // ring entry of token 0; token t sits at (lo + t) % ring
-  {  // RoPE: wave w takes tokens w, w + 4
-    const int half = RA_HD / 2;
-    const int partner = l < half ? l + half : l - half;
-    const float sgn = l < half ? -1.f : 1.f;
-    const float f = inv_freq[l < half ? l : l - half];
-    for (int t = wave; t < T; t += 4) {
-      const float ang = (float)(p0 + t) * f;
-      const float cs = cosf(ang) * rope_scale, sn = sinf(ang) * rope_scale;
-      const uint16_t* r = qkv + ((long)b * T + t) * ld_qkv;
-      qs[t][l] = E<DT>::to_f(r[h * RA_HD + l]) * cs + sgn * E<DT>::to_f(r[h * RA_HD + partner]) * sn;
-      knew[t][l] = E<DT>::from_f(E<DT>::to_f(r[(H + h) * RA_HD + l]) * cs +
-                                 sgn * E<DT>::to_f(r[(H + h) * RA_HD + partner]) * sn);
-      vnew[t][l] = r[(2 * H + h) * RA_HD + l];
-    }
+  // the older entries' keys, positions and values load now, while RoPE runs; this call's own rows come from LDS
+  // after the barrier. Thread j owns entry j for the scores; for P.V lane (g, d8) of wave w takes entries
+  // 64 w + g + 8 i, dims 8 d8 .. + 7.
+  const int j = tid;
+  const int dd = (j - lo + ring) % ring;  // entries this call writes hold p0 + dd, dd < T
+  long kj = NEVER_POS;
+  u16x8 k8[RA_HD / 8];
+#pragma unroll
+  for (int d = 0; d < RA_HD / 8; ++d) k8[d] = u16x8{};
+  if (j < ring && dd >= T) {
+    const uint16_t* krow = kr + ((long)j * H + h) * RA_HD;
+#pragma unroll
+    for (int d = 0; d < RA_HD / 8; ++d) k8[d] = ld16(krow + 8 * d);
+    kj = kp[j];
   }
-  __syncthreads();  // queries and this call's rows are in LDS
-  // the values this wave multiplies in P.V: lane (g, d8) takes entries 64 w + g + 8 i, dims 8 d8 .. + 7; issued
-  // now so that they arrive while the scores and the softmax run
   const int g = l >> 3, dc = 8 * (l & 7);
   u16x8 vv[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int jj = 64 * wave + g + 8 * i;
-    const int dn = (jj - lo + ring) % ring;
     vv[i] = u16x8{};
-    if (jj < ring) vv[i] = dn < T ? *reinterpret_cast<const u16x8*>(&vnew[dn][dc])
-                                  : ld16(vr + ((long)jj * H + h) * RA_HD + dc);
+    if (jj < ring && (jj - lo + ring) % ring >= T) vv[i] = ld16(vr + ((long)jj * H + h) * RA_HD + dc);
   }
-  // scores: thread j owns entry j; entries this call writes hold p0 + d, d = (j - lo) mod ring < T
-  const int j = tid;
-  long kj = NEVER_POS;
-  u16x8 k8[RA_HD / 8];
+  if (wave < T) {  // RoPE of token `wave`
+    const float f = inv_freq[l < half ? l : l - half];
+    const float sgn = l < half ? -1.f : 1.f;
+    const float ang = (float)(p0 + wave) * f;
+    const float cs = cosf(ang) * rope_scale, sn = sinf(ang) * rope_scale;
+    qs[wave][l] = q_l * cs + sgn * q_p * sn;
+    knew[wave][l] = E<DT>::from_f(k_l * cs + sgn * k_p * sn);
+    vnew[wave][l] = v_l;
+  }
+  __syncthreads();  // queries and this call's rows are in LDS
+  if (j < ring && dd < T) {
+    kj = p0 + dd;
 #pragma unroll
-  for (int d = 0; d < RA_HD / 8; ++d) k8[d] = u16x8{};
-  if (j < ring) {
-    const int dd = (j - lo + ring) % ring;
-    if (dd < T) {
-      kj = p0 + dd;
+    for (int d = 0; d < RA_HD / 8; ++d) k8[d] = *reinterpret_cast<const u16x8*>(&knew[dd][8 * d]);
+  }
 #pragma unroll
-      for (int d = 0; d < RA_HD / 8; ++d) k8[d] = *reinterpret_cast<const u16x8*>(&knew[dd][8 * d]);
-    } else {
-      const uint16_t* krow = kr + ((long)j * H + h) * RA_HD;
-#pragma unroll
-      for (int d = 0; d < RA_HD / 8; ++d) k8[d] = ld16(krow + 8 * d);
-      kj = kp[j];
-    }
+  for (int i = 0; i < 8; ++i) {
+    const int jj = 64 * wave + g + 8 * i;
+    const int dn = (jj - lo + ring) % ring;
+    if (jj < ring && dn < T) vv[i] = *reinterpret_cast<const u16x8*>(&vnew[dn][dc]);
   }
   float sc[TM];
 #pragma unroll
