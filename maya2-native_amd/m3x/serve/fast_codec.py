@@ -16,7 +16,6 @@ conv as GEMM + overlap-add with tail (m3x_convt_overlap), and the last conv to f
 """
 from __future__ import annotations
 
-import math
 
 import torch
 

@@ -6,6 +6,7 @@ Tolerance: the product stores activations in float16 and accumulates in fp32, th
 Rounding every stage of the oracle itself to float16 moves its PCM by 0.12% RMS, so every frame of every seat must
 have relative RMS error <= 5e-3 and max abs error <= 1e-2 of the frame's peak (an attention that dropped a
 query lane's broadcast was 1.4% off and fails)."""
+import numpy as np
 import pytest
 import torch
 
@@ -104,3 +105,31 @@ def test_surface_errors(gpu):
         StaticMimi(synth.mimi(seed=37, device=gpu), 2, ring=200)
     b = sm.state_bytes_per_slot()
     assert b["attention_kv"] == 8 * 2 * 256 * 512 * 2 and b["attention_index"] == 256 * 8 + 8
+
+
+def test_tick_frame_codes_through_codec_to_readout(gpu):
+    """The tick on the device: a frame graph's codes go to StaticMimi.decode, whose PCM (checked against the
+    streaming oracle on the same codes) the tick readout packs beside the codes in one host copy."""
+    from m3x.serve.fast_codec import StaticMimi
+    from m3x.tick import TickReadout
+    from test_gpu_frame import _frame
+    fs = _frame(gpu, seed=93)
+    mc = synth.mimi(seed=94)
+    sm = StaticMimi(synth.mimi(seed=94, device=gpu), 8, batch_buckets=(4,))
+    rd = TickReadout(4, frame=1920, nq=32, with_loop=False, device=gpu)
+    seats = [1, 6]
+    streams = {s: MimiStream(mc, 1) for s in seats}
+    with torch.inference_mode():
+        g = fs.capture(4, 256)
+        fs.set_slots(g, seats)
+        for frame in range(3):
+            fs.replay(g)
+            codes = fs.codes(g)[:2]
+            pcm = sm.decode(seats, codes)
+            fs.readout(g, rd, B=2, pcm=pcm)
+            got = rd.wait()
+            assert np.array_equal(got["codes"], codes.cpu().numpy())
+            want16 = (pcm.cpu().clamp(-1, 1) * 32767).round().to(torch.int16).numpy()
+            assert np.array_equal(got["pcm"], want16)
+            for i, s in enumerate(seats):
+                _check(pcm[i:i + 1].cpu(), streams[s].decode_frame(codes[i:i + 1].cpu().long()), f"tick {frame} {s}")
