@@ -245,7 +245,8 @@ int m3x_dwconvt(const void* x, long ld_x, const void* w, void* tail, long ld_tai
                 int B, int C, int k, int s, int dtype, void* stream);
 
 /* GEMM rows of a causal conv: cols[b*T + t, j*C + c] = joined[t + j*dil][c], joined = the slot's (k-1)*dil stored
- * frames then ELU(x) (use_elu) or x; the state becomes joined's last (k-1)*dil frames.
+ * frames then ELU(x) (use_elu) or x; the state becomes joined's last (k-1)*dil frames. cols = NULL only advances
+ * the state.
  * Replaces the MimiConv1d branch of `_layer` (serve/fast_codec.py:104-111) with the ELU in front of it. */
 int m3x_conv_gather(const void* x, long ld_x, void* state, long ld_state, const int64_t* slots, void* cols,
                     long ld_cols, int B, int T, int C, int k, int dil, int use_elu, int chunk, int dtype,
@@ -266,9 +267,13 @@ int m3x_resid_ln(void* h, long ld_h, const void* a, long ld_a, const void* scale
 /* y = act(res + (dt(x . w^T) + bias)) for N in {16, 32, 64, 128} output channels, w packed by m3x_pack_weight,
  * K % 32 == 0; bias and res optional; act = ELU when use_elu. The product of m3x_linear followed by the arithmetic
  * of m3x_rows_op in one launch. Replaces a SEANet MimiConv1d's `module.conv(x)` with its bias, the resnet
- * `shortcut + x` and the next ELU (serve/fast_codec.py:104-111,127-130) when the conv has at most 128 outputs. */
+ * `shortcut + x` and the next ELU (serve/fast_codec.py:104-111,127-130) when the conv has at most 128 outputs.
+ * With C > 0 the product's rows are m3x_conv_gather's (K = k * C; x [M, C], M = B * T; the slot's history
+ * `state`, the ELU in front when pre_elu) read in place of a gathered copy; the caller then advances the history
+ * with m3x_conv_gather(cols = NULL). C = 0: x is the [M, K] product input itself. */
 int m3x_conv_gemm(const void* x, long ldx, const void* w_packed, const void* bias, const void* res, long ld_res,
-                  void* y, long ldy, int M, int N, int K, int use_elu, int dtype, void* stream);
+                  void* y, long ldy, int M, int N, int K, int use_elu, const void* state, long ld_state,
+                  const int64_t* slots, int T, int C, int dil, int pre_elu, int dtype, void* stream);
 
 /* Overlap-add of a transposed conv (kernel k, stride s, s < k <= 2 s) from its GEMM columns cols[b*Tin + t,
  * j*C + c]: out [B * Tin * s, C] with the slot's tail added to the first k - s frames and bias; the new tail is the

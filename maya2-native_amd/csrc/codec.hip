@@ -11,7 +11,9 @@ constexpr int CODEC_THREADS = 256;
 constexpr int CODEC_KEEP = 16;
 constexpr long NEVER_POS = -(1L << 40);  // key_pos of an empty ring entry
 
-__device__ __forceinline__ float elu1(float v) { return v > 0.f ? v : expm1f(v); }
+// ELU (alpha 1) with the hardware exp: exp(v) - 1 for v <= 0, absolute error ~1e-7, below the 16-bit storage step
+// of every value it produces.
+__device__ __forceinline__ float elu1(float v) { return v > 0.f ? v : __expf(v) - 1.f; }
 
 // ---------------------------------------------------------------------------------------------------------
 // RVQ decode (:134-149; transformers MimiSplitResidualVectorQuantizer.decode): out[b, :dim] = table_0[code_0]
@@ -59,6 +61,7 @@ __global__ __launch_bounds__(256) void dwconvt_kernel(const uint16_t* __restrict
 // the slot's pad = (k - 1) * dil stored frames followed by act(x[b * T + 0 .. T)), act = ELU (alpha 1) when
 // use_elu, the ELU module in front of the conv. The slot's state becomes joined's last pad frames (post-ELU, as
 // the reference stores the conv's own input). Grid (B, ceil(T / chunk)), chunk >= pad; 8 channels per thread.
+// cols == NULL only advances the history (after an m3x_conv_gemm that read it in place of the gathered rows).
 template <int DT>
 __device__ __forceinline__ u16x8 joined8(const uint16_t* st, const uint16_t* x, long ld_x, long row0, int pad, int i,
                                          int c, int C, int use_elu) {
@@ -83,7 +86,7 @@ __global__ __launch_bounds__(CODEC_THREADS) void conv_gather_kernel(const uint16
   const long row0 = (long)b * T;
   uint16_t* st = pad ? state + slots[b] * ld_state : nullptr;  // [pad][C]
   const int cv = C / 8, kcv = k * cv;
-  for (int e = threadIdx.x; e < (t1 - t0) * kcv; e += CODEC_THREADS) {
+  for (int e = threadIdx.x; cols && e < (t1 - t0) * kcv; e += CODEC_THREADS) {
     const int t = t0 + e / kcv;
     const int r = e - (t - t0) * kcv;
     const int j = r / cv, c = 8 * (r - j * cv);
@@ -178,12 +181,22 @@ __global__ __launch_bounds__(256) void resid_ln_kernel(uint16_t* h, long ld_h, c
 // arithmetic), w packed by m3x_pack_weight, N = 16 NT, K % 32 == 0; bias and res optional, act = ELU when use_elu.
 // Each wave owns 16 MT rows and all N columns: the activation fragments are loaded straight into the MFMA's B
 // operand (each activation element is read once), the weight fragments (K * N * 2 bytes, cache resident) into A.
-template <int DT, int NT, int MT>
+// Gathered form (G = 1): the conv's rows are read in place of a gathered copy. Row m = b * T + t, column
+// kk = j * C + c of the product is joined[t + j * dil][c] (m3x_conv_gather's rows: the slot's pad stored frames,
+// then x with ELU when pre_elu); the caller advances the history afterwards.
+struct ConvSrc {
+  const uint16_t* state;
+  long ld_state;
+  const int64_t* slots;
+  int T, C, dil, pad, pre_elu;
+};
+
+template <int DT, int NT, int MT, int G>
 __global__ __launch_bounds__(256) void conv_gemm_kernel(const uint16_t* __restrict__ X, long ldx,
                                                         const uint16_t* __restrict__ Wp,
                                                         const uint16_t* __restrict__ bias, const uint16_t* res,
                                                         long ld_res, uint16_t* Y, long ldy, int M, int K,
-                                                        int use_elu) {
+                                                        int use_elu, ConvSrc cs) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, li = l & 15, lg = l >> 4;
   const long m0 = ((long)blockIdx.x * 4 + wave) * (16 * MT);
@@ -196,12 +209,44 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(const uint16_t* __restri
   const int ks = K / 32;
   // the fragments of step s + 1 are in flight while step s multiplies
   u16x8 a[2][NT], b[2][MT];
+  // gathered form: each row's seat, time and history row
+  long xrow0[MT];
+  int tt[MT];
+  const uint16_t* hist[MT];
+#pragma unroll
+  for (int j = 0; j < MT; ++j) {
+    const long row = m0 + 16 * j + li;
+    xrow0[j] = 0, tt[j] = 0, hist[j] = nullptr;
+    if (G && row < M) {
+      const long bs = row / cs.T;
+      tt[j] = (int)(row - bs * cs.T);
+      xrow0[j] = bs * cs.T;
+      hist[j] = cs.pad ? cs.state + cs.slots[bs] * cs.ld_state : nullptr;
+    }
+  }
   auto load = [&](int s, int buf) {
+    const int kk = 32 * s + 8 * lg;
+    const int tap = G ? kk / cs.C : 0, c = G ? kk - tap * cs.C : 0;
 #pragma unroll
     for (int j = 0; j < MT; ++j) {
       const long row = m0 + 16 * j + li;
       b[buf][j] = u16x8{};
-      if (row < M) b[buf][j] = ld16(X + row * ldx + 32 * s + 8 * lg);
+      if (row < M) {
+        if (!G) {
+          b[buf][j] = ld16(X + row * ldx + kk);
+        } else {
+          const int i = tt[j] + tap * cs.dil;
+          if (i < cs.pad) {
+            b[buf][j] = ld16(hist[j] + (long)i * cs.C + c);
+          } else {
+            b[buf][j] = ld16(X + (xrow0[j] + i - cs.pad) * ldx + c);
+            if (cs.pre_elu) {
+#pragma unroll
+              for (int e = 0; e < 8; ++e) b[buf][j].v[e] = E<DT>::from_f(elu1(E<DT>::to_f(b[buf][j].v[e])));
+            }
+          }
+        }
+      }
     }
 #pragma unroll
     for (int t = 0; t < NT; ++t) a[buf][t] = ld16(Wp + ((long)t * ks + s) * 512 + 8 * l);
@@ -584,13 +629,14 @@ M3X_API int m3x_conv_gather(const void* x, long ld_x, void* state, long ld_state
                             long ld_cols, int B, int T, int C, int k, int dil, int use_elu, int chunk, int dtype,
                             void* stream) {
   const int pad = (k - 1) * dil;
-  if (B < 0 || T < 1 || C < 8 || C % 8 || k < 1 || dil < 1 || ld_x < C || ld_cols < (long)k * C ||
-      chunk < max(pad, 1) || ((ld_x | ld_cols | (pad ? ld_state : 0)) & 7))
+  if (B < 0 || T < 1 || C < 8 || C % 8 || k < 1 || dil < 1 || ld_x < C || (cols && ld_cols < (long)k * C) ||
+      chunk < max(pad, 1) || ((ld_x | (cols ? ld_cols : 0) | (pad ? ld_state : 0)) & 7))
     return M3X_EINVAL;
-  if (!m3x_aligned16(x) || !m3x_aligned16(cols) || (pad && !m3x_aligned16(state))) return M3X_EINVAL;
+  if (!m3x_aligned16(x) || (cols && !m3x_aligned16(cols)) || (pad && !m3x_aligned16(state))) return M3X_EINVAL;
   if (pad && (ld_state < (long)pad * C || pad * C > CODEC_KEEP * CODEC_THREADS)) return M3X_EINVAL;
   if (B == 0) return M3X_OK;
-  if (!x || !cols || !slots || (pad && !state)) return M3X_ENULL;
+  if (!x || !slots || (pad && !state)) return M3X_ENULL;
+  if (!cols && !pad) return M3X_OK;
   CODEC_LAUNCH(conv_gather_kernel, dim3(B, m3x_ceil_div(T, chunk)), dim3(CODEC_THREADS), (const uint16_t*)x, ld_x,
                (uint16_t*)state, ld_state, slots, (uint16_t*)cols, ld_cols, T, C, k, dil, use_elu, chunk);
   return M3X_OK;
@@ -689,8 +735,19 @@ M3X_API int m3x_resid_ln(void* h, long ld_h, const void* a, long ld_a, const voi
 }
 
 M3X_API int m3x_conv_gemm(const void* x, long ldx, const void* w_packed, const void* bias, const void* res,
-                          long ld_res, void* y, long ldy, int M, int N, int K, int use_elu, int dtype, void* stream) {
-  if (M < 0 || K < 32 || K % 32 || (N != 16 && N != 32 && N != 64 && N != 128) || ldx < K || ldy < N || (res && ld_res < N) || ((ldx | ldy | (res ? ld_res : 0)) & 7))
+                          long ld_res, void* y, long ldy, int M, int N, int K, int use_elu, const void* state,
+                          long ld_state, const int64_t* slots, int T, int C, int dil, int pre_elu, int dtype,
+                          void* stream) {
+  // gathered form when C > 0: K = k * C, x rows [M, C], the slot's history of pad = (k - 1) * dil frames
+  ConvSrc cs{(const uint16_t*)state, ld_state, slots, T, C, dil, 0, pre_elu};
+  const int G = C > 0;
+  if (G) {
+    if (T < 1 || C % 8 || K % C || M % T || dil < 1 || ldx < C || (ldx & 7)) return M3X_EINVAL;
+    cs.pad = (K / C - 1) * dil;
+    if (cs.pad && (!state || !slots)) return M3X_ENULL;
+    if (cs.pad && (ld_state < (long)cs.pad * C || (ld_state & 7) || !m3x_aligned16(state))) return M3X_EINVAL;
+  }
+  if (M < 0 || K < 32 || K % 32 || (N != 16 && N != 32 && N != 64 && N != 128) || (!G && ldx < K) || ldy < N || (res && ld_res < N) || ((ldx | ldy | (res ? ld_res : 0)) & 7))
     return M3X_EINVAL;
   if (M == 0) return M3X_OK;
   if (!x || !w_packed || !y) return M3X_ENULL;
@@ -705,8 +762,12 @@ M3X_API int m3x_conv_gemm(const void* x, long ldx, const void* w_packed, const v
   hipStream_t st = (hipStream_t)stream;
 #define CG_CASE(DTT, NTT, MTT)                                                                                     \
   if (dtype == DTT && N == 16 * NTT && mt == MTT) {                                                                \
-    hipLaunchKernelGGL((conv_gemm_kernel<DTT, NTT, MTT>), grid, dim3(256), 0, st, X, ldx, W, Bi, R, ld_res, Yp, ldy, \
-                       M, K, use_elu);                                                                             \
+    if (G)                                                                                                         \
+      hipLaunchKernelGGL((conv_gemm_kernel<DTT, NTT, MTT, 1>), grid, dim3(256), 0, st, X, ldx, W, Bi, R, ld_res, Yp, \
+                         ldy, M, K, use_elu, cs);                                                                  \
+    else                                                                                                           \
+      hipLaunchKernelGGL((conv_gemm_kernel<DTT, NTT, MTT, 0>), grid, dim3(256), 0, st, X, ldx, W, Bi, R, ld_res, Yp, \
+                         ldy, M, K, use_elu, cs);                                                                  \
     M3X_CHECK_LAUNCH();                                                                                            \
     return M3X_OK;                                                                                                 \
   }

@@ -63,7 +63,7 @@ SIGNATURES = {
     "m3x_convt_overlap": (_I, [_P, _L, _P, _L, _P, _P, _P, _L, _I, _I, _I, _I, _I, _I, _I, _P]),
     "m3x_ring_attn": (_I, [_P, _L, _P, _P, _P, _P, _P, _P, _F, _P, _L, _I, _I, _I, _I, _I, _I, _I, _P]),
     "m3x_advance_tokens": (_I, [_P, _P, _I, _I, _I, _P]),
-    "m3x_conv_gemm": (_I, [_P, _L, _P, _P, _P, _L, _P, _L, _I, _I, _I, _I, _I, _P]),
+    "m3x_conv_gemm": (_I, [_P, _L, _P, _P, _P, _L, _P, _L, _I, _I, _I, _I, _P, _L, _P, _I, _I, _I, _I, _I, _P]),
     "m3x_resid_ln": (_I, [_P, _L, _P, _L, _P, _P, _P, _P, _L, _F, _I, _I, _I, _P]),
     "m3x_final_conv": (_I, [_P, _L, _P, _L, _P, _P, _F, _P, _L, _I, _I, _I, _I, _I, _I, _P]),
 }

@@ -417,10 +417,12 @@ def dwconvt(x, w, tail, slots, out, k, s):
 
 
 def conv_gather(x, state, slots, cols, B, T, C, k, dil, use_elu, chunk):
-    """GEMM rows of a causal conv with per-slot input history (state [slots, pad * C] or None when pad = 0)."""
+    """GEMM rows of a causal conv with per-slot input history (state [slots, pad * C] or None when pad = 0);
+    cols None only advances the history."""
     _dev(x, state, slots, cols)
     check(lib().m3x_conv_gather(_p(x), x.stride(0), _p(state), 0 if state is None else state.stride(0), _p(slots),
-                                _p(cols), cols.stride(0), B, T, C, k, dil, int(use_elu), chunk, _dt(x), _stream()),
+                                _p(cols), 0 if cols is None else cols.stride(0), B, T, C, k, dil, int(use_elu), chunk,
+                                _dt(x), _stream()),
           "conv_gather")
 
 
@@ -432,13 +434,18 @@ def rows_op(g, out, bias=None, scale=None, res=None, use_elu=False):
           "rows_op")
 
 
-def conv_gemm(x, w, y, bias=None, res=None, use_elu=False):
-    """y = act(res + (x @ W.T + bias)) for a packed W with N in {16, 32, 64, 128}; act = ELU when use_elu."""
+def conv_gemm(x, w, y, bias=None, res=None, use_elu=False, gather=None):
+    """y = act(res + (x @ W.T + bias)) for a packed W with N in {16, 32, 64, 128}; act = ELU when use_elu.
+    gather = (state, slots, T, C, dil, pre_elu): x is the conv's input [B * T, C] and the product reads
+    m3x_conv_gather's rows in place (the history is not advanced here)."""
     if not isinstance(w, PackedWeight):
         raise TypeError("conv_gemm: the weight must be packed with ops.pack_weight")
-    _dev(x, w.data, y, bias, res)
+    st, slots, T, C, dil, pre = gather if gather is not None else (None, None, 0, 0, 1, False)
+    _dev(x, w.data, y, bias, res, st, slots)
     check(lib().m3x_conv_gemm(_p(x), x.stride(0), _p(w.data), _p(bias), _p(res), 0 if res is None else res.stride(0),
-                              _p(y), y.stride(0), x.shape[0], w.N, w.K, int(use_elu), _dt(x), _stream()), "conv_gemm")
+                              _p(y), y.stride(0), y.shape[0], w.N, w.K, int(use_elu), _p(st),
+                              0 if st is None else st.stride(0), _p(slots), T, C, dil, int(pre), _dt(x), _stream()),
+          "conv_gemm")
     return y
 
 

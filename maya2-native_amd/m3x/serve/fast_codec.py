@@ -269,6 +269,14 @@ class StaticMimi:
     def _conv(self, st, x, slots, B, t, out):
         """Causal conv of x [B * t, cin] -> act(out) [B * t, cout] (bias, ELU when post_elu)."""
         k, cin, cout = st["k"], st["cin"], st["cout"]
+        if _thin(cout, k * cin) and (k > 1 or st["pre_elu"]):
+            # the conv GEMM reads the input and the slot's history in place, then the history advances
+            y = out[:B * t * cout].view(B * t, cout)
+            ops.conv_gemm(x, st["w"], y, bias=st["bias"], use_elu=st["post_elu"],
+                          gather=(self.state[st["key"]], slots, t, cin, st["dil"], st["pre_elu"]))
+            if st["pad"]:
+                ops.conv_gather(x, self.state[st["key"]], slots, None, B, t, cin, k, st["dil"], st["pre_elu"], t)
+            return y
         if k == 1 and not st["pre_elu"]:
             src = x
         else:
