@@ -28,10 +28,11 @@ class _Bucket:
     __slots__ = ("graph", "slots", "codes", "out", "bufs", "pinned", "events", "turn")
 
 
-def _thin(n, k):
-    """Convs that go to the fused conv GEMM (m3x_conv_gemm): up to 128 outputs over a short reduction (a wave
-    walks K alone, so a long K with few rows is faster on the tiled GEMM + row op)."""
-    return n in (16, 32, 64, 128) and k <= 384
+def _thin(n, k, rows):
+    """Convs that go to the fused conv GEMM (m3x_conv_gemm): up to 128 outputs over a short reduction, or a
+    reduction of up to 768 over at least 4096 rows (a wave walks K alone, so a long K over few rows is faster on
+    the tiled GEMM + row op; measured on the 96-row and 21504-row cases of the 128-output conv)."""
+    return n in (16, 32, 64, 128) and (k <= 384 or (k <= 768 and rows >= 4096))
 
 
 def _chunk(rows, B, depth, target=2048):
@@ -255,7 +256,7 @@ class StaticMimi:
             else:
                 a, b = st["a"], st["b"]
                 inner = self._conv(a, x, slots, B, t, out=bf["I"])
-                if _thin(b["cout"], b["cin"]):  # shortcut + block, then the next ELU
+                if _thin(b["cout"], b["cin"], B * t):  # shortcut + block, then the next ELU
                     ops.conv_gemm(inner, b["w"], x, bias=b["bias"], res=x, use_elu=True)
                 else:
                     g = bf["G"][:B * t * b["cout"]].view(B * t, b["cout"])
@@ -269,7 +270,7 @@ class StaticMimi:
     def _conv(self, st, x, slots, B, t, out):
         """Causal conv of x [B * t, cin] -> act(out) [B * t, cout] (bias, ELU when post_elu)."""
         k, cin, cout = st["k"], st["cin"], st["cout"]
-        if _thin(cout, k * cin) and (k > 1 or st["pre_elu"]):
+        if _thin(cout, k * cin, B * t) and (k > 1 or st["pre_elu"]):
             # the conv GEMM reads the input and the slot's history in place, then the history advances
             y = out[:B * t * cout].view(B * t, cout)
             ops.conv_gemm(x, st["w"], y, bias=st["bias"], use_elu=st["post_elu"],
@@ -284,7 +285,7 @@ class StaticMimi:
             ops.conv_gather(x, self.state[st["key"]], slots, src, B, t, cin, k, st["dil"], st["pre_elu"],
                             _chunk(t, B, st["pad"]))
         y = out[:B * t * cout].view(B * t, cout)
-        if _thin(cout, k * cin):
+        if _thin(cout, k * cin, B * t):
             ops.conv_gemm(src, st["w"], y, bias=st["bias"], use_elu=st["post_elu"])
             return y
         g = self._bf["G"][:B * t * cout].view(B * t, cout)
