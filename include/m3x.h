@@ -21,7 +21,7 @@ extern "C" {
 #endif
 
 enum { M3X_OK = 0, M3X_EINVAL = -1, M3X_ENULL = -2, M3X_EWORKSPACE = -3, M3X_ELAUNCH = -4, M3X_EUNSUPPORTED = -5 };
-enum { M3X_BF16 = 0, M3X_F16 = 1 };
+enum { M3X_BF16 = 0, M3X_F16 = 1, M3X_F32 = 2 };
 enum { M3X_NORM_LAYER = 0, M3X_NORM_RMS = 1 };
 enum { M3X_ACT_SWIGLU = 0, M3X_ACT_GELU = 1 };
 
@@ -188,6 +188,12 @@ int m3x_feedback(const void* table, const int32_t* codes, long s_codes, void* ou
  * `self.feedback[idx]` gather / `self.feedback[idx] = fb` scatter (maya3/engine.py:542,556). */
 int m3x_copy_rows(const void* src, long ld_src, const void* src_idx, long src_off, long src_rows, void* dst,
                   long ld_dst, const int64_t* dst_idx, int rows, int n, int idx_i32, long ld_idx, void* stream);
+
+/* dst[r, :n] = src[r, :n] converted between M3X_BF16, M3X_F16 and M3X_F32 (round to nearest even).
+ * Replaces the dtype casts around the depth when it runs in another dtype than the backbone: the engine builds
+ * FastDepth in `depth_dtype` (fp16 by default, maya3/engine.py:53,192-199) and feeds it the bf16 hidden state. */
+int m3x_cast_rows(const void* src, long ld_src, int src_dtype, void* dst, long ld_dst, int dst_dtype, int rows, int n,
+                  void* stream);
 
 /* ring[(*head) % depth, b, :] = codes[b, :nq] for b < B, then *head += 1 (int32 [depth, seats, nq] ring).
  * Replaces the per-tick code readout (serve/fast_depth.py:137,257; maya3/engine.py:559-563) with a device ring. */

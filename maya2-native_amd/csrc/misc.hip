@@ -280,5 +280,45 @@ M3X_API int m3x_tick_pack(const int64_t* stop, const int64_t* cb0, const int32_t
   return M3X_OK;
 }
 
+// dst[r][c] = convert(src[r][c]) between bf16, fp16 and fp32 (round to nearest even). The frame step hands the
+// backbone's bf16 hidden state to a depth that computes in another dtype (maya3/engine.py:192-199 builds the depth
+// in fp16 by default) and takes the result back.
+template <int SDT, int DDT>
+__device__ __forceinline__ void cast_one(const void* src, void* dst, long si, long di) {
+  float v;
+  if constexpr (SDT == M3X_F32) v = ((const float*)src)[si];
+  else v = E<SDT>::to_f(((const uint16_t*)src)[si]);
+  if constexpr (DDT == M3X_F32) ((float*)dst)[di] = v;
+  else ((uint16_t*)dst)[di] = E<DDT>::from_f(v);
+}
+
+template <int SDT, int DDT>
+__global__ void cast_rows_kernel(const void* __restrict__ src, long ld_src, void* __restrict__ dst, long ld_dst,
+                                 int rows, int n) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long)rows * n) return;
+  const long r = i / n, c = i % n;
+  cast_one<SDT, DDT>(src, dst, r * ld_src + c, r * ld_dst + c);
+}
+
+M3X_API int m3x_cast_rows(const void* src, long ld_src, int src_dtype, void* dst, long ld_dst, int dst_dtype,
+                          int rows, int n, void* stream) {
+  if (rows < 0 || n <= 0 || ld_src < n || ld_dst < n) return M3X_EINVAL;
+  if (src_dtype < 0 || src_dtype > 2 || dst_dtype < 0 || dst_dtype > 2) return M3X_EUNSUPPORTED;
+  if (rows == 0) return M3X_OK;
+  if (!src || !dst) return M3X_ENULL;
+  const dim3 grid(m3x_ceil_div((long)rows * n, 256));
+  hipStream_t st = (hipStream_t)stream;
+#define M3X_CAST(S, D)                                                                                  \
+  if (src_dtype == S && dst_dtype == D)                                                                 \
+    hipLaunchKernelGGL((cast_rows_kernel<S, D>), grid, dim3(256), 0, st, src, ld_src, dst, ld_dst, rows, n);
+  M3X_CAST(M3X_BF16, M3X_BF16) M3X_CAST(M3X_BF16, M3X_F16) M3X_CAST(M3X_BF16, M3X_F32)
+  M3X_CAST(M3X_F16, M3X_BF16) M3X_CAST(M3X_F16, M3X_F16) M3X_CAST(M3X_F16, M3X_F32)
+  M3X_CAST(M3X_F32, M3X_BF16) M3X_CAST(M3X_F32, M3X_F16) M3X_CAST(M3X_F32, M3X_F32)
+#undef M3X_CAST
+  M3X_CHECK_LAUNCH();
+  return M3X_OK;
+}
+
 // The library's version, so a host binding can check it loaded the build it expects.
-M3X_API int m3x_version(void) { return 8; }
+M3X_API int m3x_version(void) { return 9; }

@@ -12,7 +12,7 @@ import os
 import torch  # noqa: F401  (must precede the CDLL load, see above)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libm3x.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -51,6 +51,7 @@ SIGNATURES = {
     "m3x_ctr_add": (_I, [_P, _P, _I, _P]),
     "m3x_feedback": (_I, [_P, _P, _L, _P, _L, _P, _F, _F, _I, _I, _I, _I, _I, _P]),
     "m3x_copy_rows": (_I, [_P, _L, _P, _L, _L, _P, _L, _P, _I, _I, _I, _L, _P]),
+    "m3x_cast_rows": (_I, [_P, _L, _I, _P, _L, _I, _I, _I, _P]),
     "m3x_code_ring_write": (_I, [_P, _L, _P, _P, _I, _I, _I, _I, _P]),
     "m3x_hist_push": (_I, [_P, _L, _P, _P, _P, _L, _I, _I, _P]),
     "m3x_loop_guard": (_I, [_P, _L, _P, _P, _P, _I, _I, _I, _I, ctypes.c_double, _I, _I, _P]),

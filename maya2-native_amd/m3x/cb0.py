@@ -33,11 +33,12 @@ class Cb0Sampler:
         dev = head_weight.device
         m = max_seats + 1
         self.max_seats = max_seats
-        self.temp_t = torch.full((m,), float(temp), device=dev, dtype=torch.float32)
-        self.topk_t = torch.full((m,), int(top_k), device=dev, dtype=torch.long)
         if not 0.0 < float(top_p) <= 1.0:
             raise ValueError("top_p must be in (0, 1]")
-        self.top_p = float(top_p)
+        # the configuration defaults a seat gets back when its request leaves a setting unset
+        self.temp, self.top_k, self.top_p, self.rep = float(temp), int(top_k), float(top_p), float(rep)
+        self.temp_t = torch.full((m,), self.temp, device=dev, dtype=torch.float32)
+        self.topk_t = torch.full((m,), self.top_k, device=dev, dtype=torch.long)
         self.topp_t = torch.full((m,), self.top_p, device=dev, dtype=torch.float32)
         self.rep_t = torch.full((m,), float(rep), device=dev, dtype=torch.float32)
         self.seed_t = torch.zeros(m, device=dev, dtype=torch.int32)
@@ -47,11 +48,12 @@ class Cb0Sampler:
         self.min_t = torch.zeros(m, device=dev, dtype=torch.long)
         self.hazard_t = torch.zeros(m, device=dev, dtype=torch.float32)
         self.aeos_bias = torch.zeros(m, device=dev, dtype=torch.float32)
-        self.any_rep = float(rep) > 0 and self.rep_win > 0
 
     @torch.inference_mode()
     def bind(self, slot, seed, temperature=None, top_k=None, top_p=None, repetition_penalty=None, min_frames=0):
-        """Per-seat settings at admission (maya3/engine.py:429-444)."""
+        """Per-seat settings at admission (maya3/engine.py:429-444): a setting left unset (None, or 0 where the
+        engine's `x or default` reads it so) takes the sampler's configured default, so a reused slot never
+        inherits its previous seat's settings."""
         if top_p is not None and not 0.0 < float(top_p) <= 1.0:
             raise ValueError("top_p must be in (0, 1]")
         self.seed_t[slot] = int(seed)
@@ -61,14 +63,10 @@ class Cb0Sampler:
         self.hazard_t[slot] = 0
         self.aeos_bias[slot] = 0
         self.hist_t[slot] = -1
-        if temperature is not None:
-            self.temp_t[slot] = float(temperature)
-        if top_k is not None:
-            self.topk_t[slot] = int(top_k)
-        self.topp_t[slot] = float(top_p) if top_p else self.top_p
-        if repetition_penalty is not None:
-            self.rep_t[slot] = float(repetition_penalty)
-            self.any_rep = self.any_rep or float(repetition_penalty) > 0
+        self.temp_t[slot] = float(temperature or self.temp)
+        self.topk_t[slot] = int(top_k or self.top_k)
+        self.topp_t[slot] = float(top_p or self.top_p)
+        self.rep_t[slot] = float(self.rep if repetition_penalty is None else repetition_penalty)
 
     def make_buffers(self, B, h=None, codes=None):
         dev = self.w.device
@@ -87,11 +85,13 @@ class Cb0Sampler:
         ops.linear(b.h, self.pw, b.logits)
         if uniforms:
             ops.philox_uniforms(self.seed_t, self.ctr_t, b.slots, b.u, 0)
-        rep = self.any_rep and self.rep_win > 0
+        # with a history window the penalty always runs: a seat with penalty 0 subtracts exactly 0, so a graph
+        # captured before any seat asked for a penalty still applies one bound later
+        win = self.rep_win > 0
         ops.cb0_sample(b.logits, self.aeos, b.slots, b.u[:, 0], temp_t=self.temp_t, topk_t=self.topk_t,
                        topp_t=self.topp_t,
-                       aeos_bias=self.aeos_bias if self.aeos >= 0 else None, rep_t=self.rep_t if rep else None,
-                       hist_t=self.hist_t if self.rep_win > 0 else None,
+                       aeos_bias=self.aeos_bias if self.aeos >= 0 else None, rep_t=self.rep_t if win else None,
+                       hist_t=self.hist_t if win else None,
                        frames_t=self.frames_t if self.stop else None, min_t=self.min_t if self.stop else None,
                        hazard_t=self.hazard_t if self.stop else None, ctr_t=self.ctr_t, cb0_out=b.cb0,
                        cb0_i32=None if b.codes is None else b.codes[:, 0], stop_out=b.stop)

@@ -20,6 +20,7 @@ from ._lib import check, lib
 NORM_LAYER, NORM_RMS = 0, 1
 ACT_SWIGLU, ACT_GELU = 0, 1
 _DT = {torch.bfloat16: 0, torch.float16: 1}
+_DT_ANY = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 
 
 def _p(t):
@@ -392,6 +393,18 @@ def copy_rows(src, dst, src_idx=None, src_off=0, dst_idx=None, rows=None):
         _need(dst_idx, torch.long, "dst_idx")
     check(lib().m3x_copy_rows(_p(src), src.stride(-2), _p(src_idx), int(src_off), src.shape[-2], _p(dst),
                               dst.stride(-2), _p(dst_idx), int(rows), n, idx_i32, ld_idx, _stream()), "copy_rows")
+
+
+def cast_rows(src, dst):
+    """dst = src converted to dst's dtype (bf16 / fp16 / fp32 rows with a contiguous last dimension)."""
+    _dev(src, dst)
+    _rows2d(src, "src")
+    _rows2d(dst, "dst")
+    if src.shape != dst.shape or src.dtype not in _DT_ANY or dst.dtype not in _DT_ANY:
+        raise ValueError(f"cast_rows: {tuple(src.shape)} {src.dtype} -> {tuple(dst.shape)} {dst.dtype}")
+    check(lib().m3x_cast_rows(_p(src), src.stride(0), _DT_ANY[src.dtype], _p(dst), dst.stride(0),
+                              _DT_ANY[dst.dtype], src.shape[0], src.shape[1], _stream()), "cast_rows")
+    return dst
 
 
 def code_ring_write(codes, ring, head, B):

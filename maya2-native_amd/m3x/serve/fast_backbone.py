@@ -1,16 +1,28 @@
-"""Static-KV single-token decode of the Qwen3 backbone with per-seat positions, on m3x gfx950 kernels.
+"""Static-KV decode of the Qwen3 backbone with per-seat positions, on m3x gfx950 kernels.
 
-Drop-in for serve/fast_backbone.py (StaticBackbone, :111-362): same constructor, methods, attributes, errors and
-static KV layout — per layer `k[i], v[i]: [max_slots+1, kv_heads, capacity, head_dim]` in the model dtype, slot
-`max_slots` a dummy whose length stays 0 and pads a batch up to its bucket (:3-4,146-150). One hipGraph per
-(row bucket, context bucket), all graphs in one memory pool; q|k|v and gate|up are concatenated once and the HF
-weights re-viewed into them (:130-141), and every projection weight gets one packed copy in MFMA fragment order
-(ops.pack_weight) that the projection kernels stream with fully contiguous loads.
+Drop-in for serve/fast_backbone.py (StaticBackbone, :111-362). The surface is the reference's: constructor
+arguments, `step`, `step_mixed`, `load_slot`, `load_prefix`, `free`, `warmup`, `memory_bytes`, the attributes the
+engine and its tests read (`k`, `v`, `lengths`, `lengths_cpu`, `kv_heads`, `head_dim`, `layers`, `max_slots`,
+`capacity`, `dummy`), and its exception types. The KV layout is the reference's contract: per layer
+`k[i], v[i]: [max_slots + 1, kv_heads, capacity, head_dim]` in the model dtype, slot `max_slots` a dummy whose
+length stays 0 and that pads a step up to its row bucket (:3-4,146-150).
 
-Per layer the step runs: [add+]RMSNorm -> q|k|v GEMM -> q/k-norm + RoPE + K/V cache write -> decode attention
-over the cache in place -> o GEMM -> add+RMSNorm -> gate|up GEMM -> SwiGLU -> down GEMM (deferred into the next
-layer's add+RMSNorm), i.e. the reference's fuse_rope path (:187-203). `attention`, `fuse_proj`, `fuse_rope` and
-`fused_norm` are accepted for construction-site compatibility; there is one kernel path.
+How a step runs here:
+  - A step is a list of rows. Decoding seats give one row each; an inline prefill of T tokens gives T rows of
+    one slot at offsets 0..T-1 from the slot's length. The row layout (slot, real-row flag, offset) is one
+    int64 table staged in a single async copy (m3x.staging.RowTable); a decode step with the same seats as the
+    previous one on its graph stages nothing.
+  - Each (row bucket, context bucket) has one hipGraph over its own buffers; steps with inline prefills use a
+    separate graph whose attention walks a host-built list of work items (prefill rows of one slot share one
+    pass over its keys).
+  - The graph body per layer: [add+]RMSNorm -> q|k|v GEMM -> q/k-norm + RoPE + K/V cache write -> decode
+    attention in place over the cache -> o GEMM -> add+RMSNorm -> gate|up GEMM with SwiGLU -> down GEMM, whose
+    output the next layer's add+RMSNorm consumes (the reference's fuse_rope path, :187-203).
+  - q|k|v and gate|up are joined into one weight each, with the model's modules re-pointed at row views of
+    the joined tensors (no second copy of the HF weights, as the reference's fuse_proj does, :130-141), and every
+    projection also gets a copy in MFMA fragment order (ops.pack_weight).
+`attention`, `fuse_proj`, `fuse_rope` and `fused_norm` are accepted for construction-site compatibility; there is
+one kernel path.
 """
 from __future__ import annotations
 
@@ -20,6 +32,9 @@ import torch
 
 from .. import ops
 from .._lib import lib
+from ..staging import Buckets, RowTable, Upload, capture, check_slots
+
+TILE = 32  # keys per attention tile: the per-slot extent of the cache allocation is a multiple of this
 
 
 def attn_chunk(rows: int, kv_heads: int, ctx: int) -> int:
@@ -35,9 +50,32 @@ def attn_chunk(rows: int, kv_heads: int, ctx: int) -> int:
     return c
 
 
-class _Graph:
-    __slots__ = ('graph', 'slots', 'slots_cpu', 'x', 'real', 'real_cpu', 'out', 'last', 'offset', 'offset_cpu',
-                 'offset_dirty', 'evt', 'bufs', 'items_cpu')
+def _retarget(module, view):
+    """Point a Linear-like module's weight at `view` (nn.Parameter .data or a plain holder attribute)."""
+    w = module.weight
+    if isinstance(w, torch.nn.Parameter):
+        w.data = view
+    else:
+        module.weight = view
+
+
+def _join(modules):
+    """One contiguous [sum of outs, in] tensor of the modules' weights, each module re-pointed at its rows."""
+    joint = torch.cat([m.weight for m in modules]).contiguous()
+    at = 0
+    for m in modules:
+        n = m.weight.shape[0]
+        _retarget(m, joint[at:at + n])
+        at += n
+    return joint
+
+
+class _StepGraph:
+    """One (row bucket, context bucket[, inline prefills]) step: buffers, row table, item upload, graph."""
+    __slots__ = ("bufs", "items", "graph")
+
+    def __init__(self, bufs):
+        self.bufs, self.items, self.graph = bufs, None, None
 
 
 class StaticBackbone:
@@ -47,118 +85,113 @@ class StaticBackbone:
         if attention not in ('gather', 'triton'):
             raise ValueError('attention must be gather or triton')
         lib()  # the kernels are the only path: fail here if the library is missing
+        self.attention, self.fused_norm, self.use_graphs = attention, fused_norm, use_graphs
+        self.fuse_proj = self.fuse_rope = True
         with torch.inference_mode():
-            self.backbone = backbone
-            self.lm = backbone.lm.model
-            cfg = backbone.lm.config
-            self.layers = list(self.lm.layers)
-            self.norm = self.lm.norm
-            p = next(self.lm.parameters())
-            self.dtype = p.dtype
-            self.device = p.device
-            if self.dtype != torch.bfloat16:
-                raise ValueError('fused add+norm kernel is bf16-only')
-            if self.device.type != 'cuda':
-                raise ValueError('StaticBackbone runs on the GPU; the model is on ' + str(self.device))
-            self.heads = cfg.num_attention_heads
-            self.kv_heads = cfg.num_key_value_heads
-            self.head_dim = getattr(cfg, 'head_dim', None) or cfg.hidden_size // cfg.num_attention_heads
-            self.groups = self.heads // self.kv_heads
-            self.hidden = cfg.hidden_size
-            self.scaling = self.head_dim ** -0.5
-            self.eps = cfg.rms_norm_eps
-            self.max_slots = max_slots
-            self.capacity = capacity
-            self.dummy = max_slots
-            self.attention = attention
-            self.fused_norm = fused_norm
-            self.use_graphs = use_graphs
-            self.fuse_proj = True
-            self.fuse_rope = True
-            self.wqkv = []
-            self.wgu = []
-            for layer in self.layers:
-                a = layer.self_attn
-                m = layer.mlp
-                if a.q_proj.bias is not None or getattr(m.gate_proj, 'bias', None) is not None:
-                    raise ValueError('fuse_proj expects bias-free projections')
-                w = torch.cat([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight]).contiguous()
-                nq, nk = a.q_proj.weight.shape[0], a.k_proj.weight.shape[0]
-                _reweight(a.q_proj, w[:nq])
-                _reweight(a.k_proj, w[nq:nq + nk])
-                _reweight(a.v_proj, w[nq + nk:])
-                self.wqkv.append(w)
-                g = torch.cat([m.gate_proj.weight, m.up_proj.weight]).contiguous()
-                ng = m.gate_proj.weight.shape[0]
-                _reweight(m.gate_proj, g[:ng])
-                _reweight(m.up_proj, g[ng:])
-                self.wgu.append(g)
-            self.inter = self.wgu[0].shape[0] // 2
-            # MFMA fragment-order copies for the projection kernels (the module weights stay as they are)
-            I = self.inter
-            self.pqkv = [ops.pack_weight(w) for w in self.wqkv]
-            pgu = [ops.pack_weight(g) for g in self.wgu]
-            self.pgate = [p.rows(0, I) for p in pgu]
-            self.pup = [p.rows(I, 2 * I) for p in pgu]
-            self.po = [ops.pack_weight(layer.self_attn.o_proj.weight) for layer in self.layers]
-            self.pdown = [ops.pack_weight(layer.mlp.down_proj.weight) for layer in self.layers]
-            torch.cuda.current_stream(self.device).synchronize()
-            self.batch_buckets = tuple(sorted(set(batch_buckets)))
-            if self.batch_buckets[-1] < max_slots:
-                self.batch_buckets += (max_slots,)
-            self.ctx_buckets = tuple(sorted({min(c, capacity) for c in ctx_buckets} | {capacity}))
-            # the kernels read 32-key tiles: the slot extent is the capacity rounded up to a multiple of 32
-            cap_alloc = -(-capacity // 32) * 32
-            shape = (max_slots + 1, self.kv_heads, cap_alloc, self.head_dim)
-            self.k = [torch.zeros(shape, dtype=self.dtype, device=self.device) for _ in self.layers]
-            self.v = [torch.zeros(shape, dtype=self.dtype, device=self.device) for _ in self.layers]
-            self.lengths = torch.zeros(max_slots + 1, dtype=torch.long, device=self.device)
-            self.lengths_cpu = [0] * (max_slots + 1)
-            positions = torch.arange(cap_alloc, device=self.device)[None]
-            cos, sin = self.lm.rotary_emb(torch.zeros(1, 1, self.hidden, dtype=self.dtype, device=self.device),
-                                          positions)
-            self.cos = cos[0].contiguous()  # [cap, head_dim], model dtype (as HF)
-            self.sin = sin[0].contiguous()
-            self.graphs = {}
-            self.pool = None
+            self._read_model(backbone)
+            self.max_slots, self.capacity, self.dummy = int(max_slots), int(capacity), int(max_slots)
+            self._pack_weights()
+            rows = Buckets(batch_buckets)
+            if rows.sizes[-1] < self.max_slots:  # a step of every seat must have a row bucket
+                rows = Buckets(rows.sizes + (self.max_slots,))
+            self._rows = rows
+            self._ctx = Buckets({min(int(c), self.capacity) for c in ctx_buckets} | {self.capacity})
+            self.batch_buckets, self.ctx_buckets = rows.sizes, self._ctx.sizes
+            self._alloc_cache()
+        self.graphs = {}
+        self.pool = None
+
+    # ---------------------------------------------------------------- construction
+    def _read_model(self, backbone):
+        self.backbone = backbone
+        self.lm = backbone.lm.model
+        cfg = backbone.lm.config
+        self.layers = list(self.lm.layers)
+        self.norm = self.lm.norm
+        p = next(self.lm.parameters())
+        self.dtype, self.device = p.dtype, p.device
+        if self.dtype != torch.bfloat16:
+            raise ValueError('fused add+norm kernel is bf16-only')
+        if self.device.type != 'cuda':
+            raise ValueError('StaticBackbone runs on the GPU; the model is on ' + str(self.device))
+        self.heads, self.kv_heads = cfg.num_attention_heads, cfg.num_key_value_heads
+        self.head_dim = getattr(cfg, 'head_dim', None) or cfg.hidden_size // cfg.num_attention_heads
+        self.groups = self.heads // self.kv_heads
+        self.hidden = cfg.hidden_size
+        self.scaling = self.head_dim ** -0.5
+        self.eps = cfg.rms_norm_eps
+
+    def _pack_weights(self):
+        self.wqkv, self.wgu = [], []
+        self.pqkv, self.pgate, self.pup, self.po, self.pdown = [], [], [], [], []
+        for layer in self.layers:
+            a, m = layer.self_attn, layer.mlp
+            if a.q_proj.bias is not None or getattr(m.gate_proj, 'bias', None) is not None:
+                raise ValueError('fuse_proj expects bias-free projections')
+            self.wqkv.append(_join([a.q_proj, a.k_proj, a.v_proj]))
+            self.wgu.append(_join([m.gate_proj, m.up_proj]))
+            inter = m.gate_proj.weight.shape[0]
+            self.pqkv.append(ops.pack_weight(self.wqkv[-1]))
+            gu = ops.pack_weight(self.wgu[-1])
+            self.pgate.append(gu.rows(0, inter))
+            self.pup.append(gu.rows(inter, 2 * inter))
+            self.po.append(ops.pack_weight(a.o_proj.weight))
+            self.pdown.append(ops.pack_weight(m.down_proj.weight))
+        self.inter = self.pgate[0].N
+        torch.cuda.current_stream(self.device).synchronize()  # packing ran on the current stream
+
+    def _alloc_cache(self):
+        # the allocation's per-slot extent is a whole number of attention tiles; k[i] / v[i] are views of exactly
+        # `capacity` positions, as the reference's tensors are
+        self._extent = -(-self.capacity // TILE) * TILE
+        full = (self.max_slots + 1, self.kv_heads, self._extent, self.head_dim)
+        self._kfull = [torch.zeros(full, dtype=self.dtype, device=self.device) for _ in self.layers]
+        self._vfull = [torch.zeros(full, dtype=self.dtype, device=self.device) for _ in self.layers]
+        self.k = [t[:, :, :self.capacity] for t in self._kfull]
+        self.v = [t[:, :, :self.capacity] for t in self._vfull]
+        self.lengths = torch.zeros(self.max_slots + 1, dtype=torch.long, device=self.device)
+        self.lengths_cpu = [0] * (self.max_slots + 1)
+        cos, sin = self.lm.rotary_emb(torch.zeros(1, 1, self.hidden, dtype=self.dtype, device=self.device),
+                                      torch.arange(self._extent, device=self.device)[None])
+        self.cos, self.sin = cos[0].contiguous(), sin[0].contiguous()  # [extent, head_dim], model dtype (as HF)
 
     # ---------------------------------------------------------------- slots
-    @torch.inference_mode()
-    def load_slot(self, slot, hf_cache, length):
-        if not 0 <= slot < self.max_slots:
-            raise IndexError(slot)
+    def _set_length(self, slot, n):
+        self.lengths[slot] = n
+        self.lengths_cpu[slot] = n
+
+    def _install(self, slot, length, pairs):
+        """Copy the first `length` positions of per-layer (keys, values) [kv_heads, >= length, head_dim]."""
+        check_slots([slot], self.max_slots)
         if length > self.capacity:
             raise ValueError(f'length {length} exceeds capacity {self.capacity}')
-        for i in range(len(self.layers)):
-            layer = hf_cache.layers[i]
-            self.k[i][slot, :, :length].copy_(layer.keys[0, :, :length])
-            self.v[i][slot, :, :length].copy_(layer.values[0, :, :length])
-        self.lengths[slot] = length
-        self.lengths_cpu[slot] = length
+        for i, (keys, values) in enumerate(pairs):
+            self.k[i][slot, :, :length].copy_(keys[:, :length])
+            self.v[i][slot, :, :length].copy_(values[:, :length])
+        self._set_length(slot, length)
+
+    @torch.inference_mode()
+    def load_slot(self, slot, hf_cache, length):
+        """Install an HF cache's first `length` positions (serve/fast_backbone.py:158-165; m3x.serve.cache builds
+        such caches)."""
+        self._install(slot, length, [(hf_cache.layers[i].keys[0], hf_cache.layers[i].values[0])
+                                     for i in range(len(self.layers))])
 
     @torch.inference_mode()
     def free(self, slot):
-        self.lengths[slot] = 0
-        self.lengths_cpu[slot] = 0
+        self._set_length(slot, 0)
 
     @torch.inference_mode()
     def load_prefix(self, slot, kv, length):
-        """Install a stored reference-prefix KV (list of per-layer (k,v) [1,KV,length,D]) into a slot."""
-        if not 0 <= slot < self.max_slots:
-            raise IndexError(slot)
-        for i, (k, v) in enumerate(kv):
-            self.k[i][slot, :, :length].copy_(k[0])
-            self.v[i][slot, :, :length].copy_(v[0])
-        self.lengths[slot] = length
-        self.lengths_cpu[slot] = length
+        """Install a stored reference-prefix KV (list of per-layer (k, v) [1, KV, length, D]) into a slot."""
+        self._install(slot, length, [(k[0], v[0]) for k, v in kv])
 
     @torch.inference_mode()
     def export_prefix(self, slot, length=None):
         """The slot's first `length` (default: all) cached positions in load_prefix's format: a list of per-layer
         (k, v) [1, kv_heads, length, head_dim] copies, e.g. a voice prefix computed once and installed into other
         slots (the `voice.kv` of maya3/engine.py:276-277)."""
-        if not 0 <= slot < self.max_slots:
-            raise IndexError(slot)
+        check_slots([slot], self.max_slots)
         n = self.lengths_cpu[slot] if length is None else int(length)
         if not 0 <= n <= self.lengths_cpu[slot]:
             raise ValueError(f'length {n} outside the slot\'s {self.lengths_cpu[slot]} cached positions')
@@ -171,8 +204,7 @@ class StaticBackbone:
         (step_mixed with no decoding seats) in pieces of at most the largest row bucket; returns the last position's
         hidden state [hidden]. Replaces the eager HF prefill that the engine falls back to for prompts longer than a
         tick's row budget and that computes a voice's prefix KV (maya3/engine.py:270-279,497-506)."""
-        if not 0 <= slot < self.max_slots:
-            raise IndexError(slot)
+        check_slots([slot], self.max_slots)
         if x.dim() != 2 or x.shape[1] != self.hidden or x.shape[0] == 0:
             raise ValueError(f'x must be [T>0, {self.hidden}], got {tuple(x.shape)}')
         if self.lengths_cpu[slot] + x.shape[0] > self.capacity:
@@ -180,42 +212,35 @@ class StaticBackbone:
         piece = self.batch_buckets[-1]
         last = None
         for t0 in range(0, x.shape[0], piece):
-            _, out = self.step_mixed([], None, [(slot, x[t0:t0 + piece])])
-            last = out[0]
+            last = self.step_mixed([], None, [(slot, x[t0:t0 + piece])])[1][0]
         return last
 
     # ---------------------------------------------------------------- math
     def make_buffers(self, rows, ctx, mixed=False):
         """Static buffers of one (row bucket, context bucket) step; reused by every replay of its graph.
+        b.table holds the per-row columns slot / real / offset (b.slots, b.real, b.offset are its device columns).
         mixed: the step may hold inline prefill rows (step_mixed), whose attention runs in blocks of consecutive
         rows; a decode-only step (step, the frame step) leaves that launch out."""
         dev, dt = self.device, self.dtype
         H, KV, D, hid, I = self.heads, self.kv_heads, self.head_dim, self.hidden, self.inter
         b = SimpleNamespace(rows=rows, ctx=ctx, mixed=mixed)
-        b.slots = torch.full((rows,), self.dummy, dtype=torch.long, device=dev)
-        b.real = torch.zeros(rows, dtype=torch.long, device=dev)
-        b.offset = torch.zeros(rows, dtype=torch.long, device=dev)
-        b.items = None
+        b.table = RowTable(('slot', 'real', 'offset'), rows, dev, pad=dict(slot=self.dummy))
+        b.slots, b.real, b.offset = b.table['slot'], b.table['real'], b.table['offset']
         b.pos = torch.zeros(rows, dtype=torch.int32, device=dev)
         b.x = torch.zeros(rows, hid, dtype=dt, device=dev)
-        b.h = torch.empty(rows, hid, dtype=dt, device=dev)
-        b.y = torch.empty(rows, hid, dtype=dt, device=dev)
-        b.qkv = torch.empty(rows, (H + 2 * KV) * D, dtype=dt, device=dev)
+        for name, width in (('h', hid), ('y', hid), ('qkv', (H + 2 * KV) * D), ('o', H * D), ('a', hid),
+                            ('act', I), ('pend', hid), ('out', hid)):
+            setattr(b, name, torch.empty(rows, width, dtype=dt, device=dev))
         b.q = torch.empty(rows, H, D, dtype=dt, device=dev)
-        b.o = torch.empty(rows, H * D, dtype=dt, device=dev)
-        b.a = torch.empty(rows, hid, dtype=dt, device=dev)
-        b.act = torch.empty(rows, I, dtype=dt, device=dev)
-        b.pend = torch.empty(rows, hid, dtype=dt, device=dev)
-        b.out = torch.empty(rows, hid, dtype=dt, device=dev)
         b.chunk = attn_chunk(rows, KV, ctx)
+        b.items = None
         if mixed:
-            # attention work items of a mixed step (ops.attn_items): prefill rows attended 16 // G at a time; until
-            # a step stages its own, every row is an item of its own
+            # work items of a mixed step (ops.attn_items): until a step stages its own, every row is its own item
             b.item_bins = ops.attn_item_bins(rows, KV, ctx, b.chunk)
-            items = ops.attn_items([(r, 1, 0) for r in range(rows)], H, KV, b.item_bins, b.chunk)
-            b.items = torch.zeros(2 + b.item_bins + rows * ((ctx + b.chunk - 1) // b.chunk), dtype=torch.int32,
-                                  device=dev)
-            b.items[:len(items)] = torch.from_numpy(items)
+            cap_items = 2 + b.item_bins + rows * -(-ctx // b.chunk)
+            b.items = torch.zeros(cap_items, dtype=torch.int32, device=dev)
+            first = ops.attn_items([(r, 1, 0) for r in range(rows)], H, KV, b.item_bins, b.chunk)
+            b.items[:len(first)] = torch.from_numpy(first).to(dev)
         ws = ops.decode_attn_workspace(rows, KV, ctx, b.chunk)
         b.attn_ws = torch.empty(max(ws, 16) // 4, dtype=torch.float32, device=dev)
         return b
@@ -223,20 +248,19 @@ class StaticBackbone:
     def forward(self, b):
         """One decode step over the rows of buffer set `b` (positions from lengths[slots] + offset); returns b.out."""
         H, KV, D, eps = self.heads, self.kv_heads, self.head_dim, self.eps
-        R = b.rows
         ops.positions(self.lengths, b.slots, b.offset, b.pos)
-        o3 = b.o.view(R, H, D)
+        o3 = b.o.view(b.rows, H, D)
         for i, layer in enumerate(self.layers):
-            attn = layer.self_attn
+            attn, kc, vc = layer.self_attn, self._kfull[i], self._vfull[i]
             if i == 0:
                 ops.add_rms(b.x, None, layer.input_layernorm.weight, eps, y=b.y)
-            else:
+            else:  # the previous layer's down projection joins the residual here
                 ops.add_rms(b.h, b.pend, layer.input_layernorm.weight, eps, h_out=b.h, y=b.y)
             ops.linear(b.y, self.pqkv[i], b.qkv)
-            ops.qk_norm_rope_cache(b.qkv, b.q, self.k[i], self.v[i], b.slots, b.pos, self.cos, self.sin,
-                                   attn.q_norm.weight, attn.k_norm.weight, eps, H, KV)
-            ops.decode_attn(b.q, self.k[i], self.v[i], o3, b.slots, b.pos, self.scaling, b.ctx, b.chunk, b.attn_ws,
-                            H, KV, items=b.items)
+            ops.qk_norm_rope_cache(b.qkv, b.q, kc, vc, b.slots, b.pos, self.cos, self.sin, attn.q_norm.weight,
+                                   attn.k_norm.weight, eps, H, KV)
+            ops.decode_attn(b.q, kc, vc, o3, b.slots, b.pos, self.scaling, b.ctx, b.chunk, b.attn_ws, H, KV,
+                            items=b.items)
             ops.linear(b.o, self.po[i], b.a)
             ops.add_rms(b.x if i == 0 else b.h, b.a, layer.post_attention_layernorm.weight, eps, h_out=b.h, y=b.y)
             ops.linear_act(b.y, self.pgate[i], self.pup[i], ops.ACT_SWIGLU, b.act)
@@ -246,185 +270,112 @@ class StaticBackbone:
         return b.out
 
     # ---------------------------------------------------------------- graphs
-    def _bucket(self, values, need, what):
-        for b in values:
-            if b >= need:
-                return b
-        raise ValueError(f'{what} {need} exceeds largest bucket {values[-1]}')
-
     @torch.inference_mode()
-    def _capture(self, bb, cb, mixed=False):
-        g = _Graph()
-        g.bufs = self.make_buffers(bb, cb, mixed)
-        g.slots, g.real, g.offset, g.x = g.bufs.slots, g.bufs.real, g.bufs.offset, g.bufs.x
-        g.offset_cpu = torch.zeros(bb, dtype=torch.long, pin_memory=True)
-        g.offset_dirty = False
-        g.slots_cpu = torch.full((bb,), self.dummy, dtype=torch.long, pin_memory=True)
-        g.real_cpu = torch.zeros(bb, dtype=torch.long, pin_memory=True)
-        g.items_cpu = torch.zeros_like(g.bufs.items, device='cpu').pin_memory() if mixed else None
-        g.last = None
-        g.graph = None
-        g.evt = None
-        g.out = g.bufs.out
+    def _graph(self, rows, ctx, mixed=False):
+        key = (rows, ctx, 'mixed') if mixed else (rows, ctx)
+        g = self.graphs.get(key)
+        if g is not None:
+            return g
+        g = _StepGraph(self.make_buffers(rows, ctx, mixed))
+        if mixed:
+            g.items = Upload(g.bufs.items, ring=2)
         if self.use_graphs:
-            stream = torch.cuda.Stream()
-            stream.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(stream):
-                for _ in range(2):
-                    self.forward(g.bufs)  # all-dummy rows: touches only the dummy slot
-            torch.cuda.current_stream().wait_stream(stream)
             if self.pool is None:
                 self.pool = torch.cuda.graph_pool_handle()
-            g.graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g.graph, pool=self.pool):
-                self.forward(g.bufs)
-        self.graphs[(bb, cb, 'mixed') if mixed else (bb, cb)] = g
+            # warm-up and capture see all-dummy rows: only the dummy slot's cache rows and length are touched,
+            # and the dummy's length is put back
+            g.graph = capture(lambda: self.forward(g.bufs), self.pool, warm=2, keep=(self.lengths,))
+        self.graphs[key] = g
         return g
 
     @torch.inference_mode()
     def warmup(self, batch_buckets=None, ctx_buckets=None, mixed=False):
-        """Captures the decode graphs of the buckets (and with mixed=True also the graphs step_mixed uses for steps
-        with inline prefills; otherwise those are captured on their first use)."""
-        # largest first so later (smaller) captures reuse the shared pool's blocks
-        for bb in sorted(batch_buckets or self.batch_buckets, reverse=True):
-            for cb in sorted(ctx_buckets or self.ctx_buckets, reverse=True):
-                cb = min(cb, self.capacity)
-                if (bb, cb) not in self.graphs:
-                    self._capture(bb, cb)
-                if mixed and (bb, cb, 'mixed') not in self.graphs:
-                    self._capture(bb, cb, True)
+        """Captures the decode graphs of the buckets (with mixed=True also the graphs of steps with inline
+        prefills; otherwise those are captured on first use)."""
+        for rows in self._rows.largest_first(batch_buckets):
+            for ctx in self._ctx.largest_first({min(int(c), self.capacity) for c in (ctx_buckets or self.ctx_buckets)}):
+                self._graph(rows, ctx)
+                if mixed:
+                    self._graph(rows, ctx, True)
         torch.cuda.synchronize()
 
-    def _run(self, g):
+    def _rows_of(self, slots, prefills):
+        """The step's rows: one per decoding seat, then T per prefill (same slot, offsets 0..T-1). Validates the
+        slots and the context; returns (row slots, row offsets, runs for the attention items, context needed)."""
+        check_slots(list(slots) + [s for s, _ in prefills], self.max_slots)
+        row_slot, row_off = list(slots), [0] * len(slots)
+        runs = [(r, 1, self.lengths_cpu[s]) for r, s in enumerate(slots)]
+        need = max([self.lengths_cpu[s] + 1 for s in slots], default=0)
+        for s, t in prefills:
+            n = t.shape[0]
+            runs.append((len(row_slot), n, self.lengths_cpu[s]))
+            row_slot += [s] * n
+            row_off += range(n)
+            need = max(need, self.lengths_cpu[s] + n)
+        if need > self.capacity:
+            raise ValueError(f'context {need} exceeds capacity {self.capacity}')
+        return row_slot, row_off, runs, need
+
+    def _replay(self, slots, x, prefills):
+        """Stage and run one step; returns the step's output rows (a view of the graph's buffer)."""
+        row_slot, row_off, runs, need = self._rows_of(slots, prefills)
+        n = len(row_slot)
+        g = self._graph(self._rows.pick(n, 'batch'), self._ctx.pick(need, 'context'), bool(prefills))
+        b = g.bufs
+        # a decode step keyed by its seats restages nothing when they repeat
+        b.table.stage(dict(slot=row_slot, real=[1] * n, offset=row_off),
+                      key=None if prefills else ('decode', tuple(slots)))
+        if prefills:
+            runs += [(r, 1, 0) for r in range(n, b.rows)]  # padding rows on the dummy slot
+            items = ops.attn_items(runs, self.heads, self.kv_heads, b.item_bins, b.chunk)
+            g.items.buffer()[:len(items)] = items
+            g.items.send(len(items))
+        at = 0
+        if slots:
+            b.x[:len(slots)].copy_(x)
+            at = len(slots)
+        for _, t in prefills:
+            b.x[at:at + t.shape[0]].copy_(t)
+            at += t.shape[0]
         if g.graph is not None:
             g.graph.replay()
         else:
-            self.forward(g.bufs)
-        return g.out
+            self.forward(b)
+        for s in slots:
+            self.lengths_cpu[s] += 1
+        for s, t in prefills:
+            self.lengths_cpu[s] += t.shape[0]
+        return b.out
 
     @torch.inference_mode()
     def step(self, slots, x):
+        """Decode one token for each seat; x [B, hidden] -> the final-normed hidden states [B, hidden] (owned)."""
         B = len(slots)
         if B == 0:
             return x.new_zeros(0, self.hidden)
-        if len(set(slots)) != B:
-            raise ValueError('duplicate slots in one step')
-        need = 0
-        for s in slots:
-            if not 0 <= s < self.max_slots:
-                raise IndexError(s)
-            need = max(need, self.lengths_cpu[s] + 1)
-        if need > self.capacity:
-            raise ValueError(f'context {need} exceeds capacity {self.capacity}')
         if tuple(x.shape) != (B, self.hidden):
+            check_slots(slots, self.max_slots)
             raise ValueError(f'x must be [{B}, {self.hidden}], got {tuple(x.shape)}')
-        bb = self._bucket(self.batch_buckets, B, 'batch')
-        cb = self._bucket(self.ctx_buckets, need, 'context')
-        g = self.graphs.get((bb, cb)) or self._capture(bb, cb)
-        key = tuple(slots)
-        if g.offset_dirty:
-            g.offset.zero_()
-            g.offset_dirty = False
-            g.last = None
-        if g.last != key:
-            if g.evt is not None:
-                g.evt.synchronize()  # pinned staging may still feed an earlier async copy
-            g.slots_cpu[:B] = torch.tensor(slots, dtype=torch.long)
-            g.slots_cpu[B:] = self.dummy
-            g.real_cpu[:B] = 1
-            g.real_cpu[B:] = 0
-            g.slots.copy_(g.slots_cpu, non_blocking=True)
-            g.real.copy_(g.real_cpu, non_blocking=True)
-            g.evt = torch.cuda.Event()
-            g.evt.record()
-            g.last = key
-        g.x[:B].copy_(x)
-        out = self._run(g)[:B].clone()
-        for s in slots:
-            self.lengths_cpu[s] += 1
-        return out
+        return self._replay(list(slots), x, ())[:B].clone()
 
     @torch.inference_mode()
     def step_mixed(self, slots, x, prefills):
         """One graphed step for decoding seats plus inline prefills.
 
-        prefills: list of (slot, x_tokens [T,hidden]); the slot must already hold its prefix. Each prefill
-        contributes T rows of the same slot at consecutive positions: every layer writes all rows' K/V before
-        attention, and row i only reads keys <= its own position, so this is an exact causal prefill.
-        Returns (decode hidden [B,hidden], [last hidden per prefill]) (serve/fast_backbone.py:326-359).
-        """
+        prefills: list of (slot, tokens [T, hidden]) for slots that already hold their prefix. A prefill's T rows
+        sit at consecutive positions of its slot; every layer writes all rows' K/V before its attention and each
+        row attends to keys up to its own position, so the rows form an exact causal prefill.
+        Returns (decoding seats' hidden states [B, hidden], [last position's hidden state per prefill])
+        (serve/fast_backbone.py:326-359)."""
         B = len(slots)
-        rows = B + sum(t.shape[0] for _, t in prefills)
-        if rows == 0:
+        if B + sum(t.shape[0] for _, t in prefills) == 0:
             return x.new_zeros(0, self.hidden), []
-        if len(set(slots) | {s for s, _ in prefills}) != B + len(prefills):
-            raise ValueError('duplicate slots in one step')
-        for s in list(slots) + [s for s, _ in prefills]:
-            if not 0 <= s < self.max_slots:
-                raise IndexError(s)
-        need = max([self.lengths_cpu[s] + 1 for s in slots] + [self.lengths_cpu[s] + t.shape[0] for s, t in prefills])
-        if need > self.capacity:
-            raise ValueError(f'context {need} exceeds capacity {self.capacity}')
-        bb = self._bucket(self.batch_buckets, rows, 'batch')
-        cb = self._bucket(self.ctx_buckets, need, 'context')
-        key = (bb, cb, 'mixed') if prefills else (bb, cb)
-        g = self.graphs.get(key) or self._capture(bb, cb, bool(prefills))
-        if g.evt is not None:
-            g.evt.synchronize()
-        index = list(slots)
-        offsets = [0] * B
-        for s, t in prefills:
-            index += [s] * t.shape[0]
-            offsets += range(t.shape[0])
-        g.slots_cpu[:rows] = torch.tensor(index, dtype=torch.long)
-        g.slots_cpu[rows:] = self.dummy
-        g.offset_cpu[:rows] = torch.tensor(offsets, dtype=torch.long)
-        g.offset_cpu[rows:] = 0
-        g.real_cpu[:rows] = 1
-        g.real_cpu[rows:] = 0
-        g.slots.copy_(g.slots_cpu, non_blocking=True)
-        g.real.copy_(g.real_cpu, non_blocking=True)
-        g.offset.copy_(g.offset_cpu, non_blocking=True)
-        if g.items_cpu is not None:
-            runs = [(i, 1, self.lengths_cpu[s]) for i, s in enumerate(slots)]
-            at = B
-            for s, t in prefills:
-                runs.append((at, t.shape[0], self.lengths_cpu[s]))
-                at += t.shape[0]
-            runs += [(r, 1, 0) for r in range(rows, bb)]  # padding rows on the dummy slot
-            items = ops.attn_items(runs, self.heads, self.kv_heads, g.bufs.item_bins, g.bufs.chunk)
-            g.items_cpu[:len(items)] = torch.from_numpy(items)
-            g.bufs.items.copy_(g.items_cpu, non_blocking=True)
-        g.last = None
-        g.offset_dirty = bool(prefills)
-        g.evt = torch.cuda.Event()
-        g.evt.record()
-        if B:
-            g.x[:B].copy_(x)
-        at = B
+        out = self._replay(list(slots), x, list(prefills))
+        ends, at = [], B
         for _, t in prefills:
-            g.x[at:at + t.shape[0]].copy_(t)
             at += t.shape[0]
-        out = self._run(g)
-        decoded = out[:B].clone()
-        last = []
-        at = B
-        for s, t in prefills:
-            at += t.shape[0]
-            last.append(out[at - 1].clone())
-            self.lengths_cpu[s] += t.shape[0]
-        for s in slots:
-            self.lengths_cpu[s] += 1
-        return decoded, last
+            ends.append(at - 1)
+        return out[:B].clone(), [out[e].clone() for e in ends]
 
     def memory_bytes(self):
-        return sum(t.numel() * t.element_size() for t in self.k + self.v)
-
-
-def _reweight(module, view):
-    """Point a Linear-like module's weight at `view` (nn.Parameter .data or a plain holder attribute)."""
-    w = module.weight
-    if isinstance(w, torch.nn.Parameter):
-        w.data = view
-    else:
-        module.weight = view
+        return sum(t.numel() * t.element_size() for t in self._kfull + self._vfull)

