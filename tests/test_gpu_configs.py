@@ -139,6 +139,7 @@ def _cb0_exact(logits, u, temp, top_k):
 
 
 # ---------------------------------------------------------------- C1
+@torch.inference_mode()
 def test_c1_layer_vs_hf_golden(gpu):
     """C1 on the HIP path: one layer (bf16 weights and cache from the fixture's seeds), B=1, 256 cached keys,
     against HF transformers' fp32 Qwen3Model output (tests/golden/c1_qwen3_layer.npz) within the bf16 floor of the
@@ -170,6 +171,7 @@ def test_c1_layer_vs_hf_golden(gpu):
 
 
 # ---------------------------------------------------------------- C2
+@torch.inference_mode()
 def test_c2_depth_16_seats(gpu, models):
     """C2: FastDepth.__call__ over 16 seats (one graph replay); an eager rerun of the same frame traces every
     level's logits and gives the same codes; every code of every seat equals the oracle sampler on those logits
@@ -214,6 +216,7 @@ def test_c2_depth_16_seats(gpu, models):
 
 
 # ---------------------------------------------------------------- C3
+@torch.inference_mode()
 def test_c3_backbone_64_seats(gpu, models):
     """C3: StaticBackbone.step over 64 seats (28 layers, capacity 4096, lengths U[64, 2048]) + cb0: three sampled
     seats (shortest, median, longest) against the oracle, properties on all 64, cb0 bit-exact on all 64."""
@@ -223,6 +226,7 @@ def test_c3_backbone_64_seats(gpu, models):
     B = 64
     sb = StaticBackbone(bb, B, capacity=CAP, batch_buckets=(B,), ctx_buckets=(2048, 3072, CAP), attention="triton",
                         fuse_rope=True)
+    sb.warmup()  # capture first: the warm-up runs write the dummy slot's position 0, the step must not
     _fill_cache(sb, 303)
     lengths = synth.c3_lengths(B)
     _set_lengths(sb, lengths)
@@ -256,6 +260,7 @@ def test_c3_backbone_64_seats(gpu, models):
 
 
 # ---------------------------------------------------------------- C4
+@torch.inference_mode()
 def test_c4_mixed_step_2264_rows(gpu, models):
     """C4: step_mixed with 216 decoding seats (lengths log-uniform in [128, 4096)) and 8 inline prefills of 256
     embedding rows (uniform ids over a 151,936-row table) from length 0 = 2264 rows in one graph replay: two
@@ -268,6 +273,7 @@ def test_c4_mixed_step_2264_rows(gpu, models):
     S = nd + npf
     sb = StaticBackbone(bb, S, capacity=CAP, batch_buckets=(nd + npf * T,), ctx_buckets=(CAP,), attention="triton",
                         fuse_rope=True)
+    sb.warmup(mixed=True)  # capture first: the warm-up runs write the dummy slot's position 0, the step must not
     _fill_cache(sb, 404)
     lengths = torch.cat([synth.c4_decode_lengths(nd), torch.zeros(npf, dtype=torch.long)])
     _set_lengths(sb, lengths)
@@ -315,6 +321,7 @@ def test_c4_mixed_step_2264_rows(gpu, models):
 
 
 # ---------------------------------------------------------------- C5
+@torch.inference_mode()
 def test_c5_frame_224_seats(gpu, models):
     """C5: the whole frame graph at 224 seats (lengths Poisson(2048) capped at 4096): backbone rows of three sampled
     seats against the oracle; cb0 of all 224 seats bit-exact against the oracle sampler on the graph's logits and

@@ -38,7 +38,7 @@ def test_row_exponential_matches_philox(gpu):
             u = (w >> 8).astype(np.float64) * 2.0 ** -24
             ref = (-np.log(np.maximum(u, 1e-12))).astype(np.float32)
             ulp = np.spacing(np.abs(ref)).astype(np.float64)
-            assert np.all(np.abs(E[b].astype(np.float64) - ref) <= ulp), (level, b)
+            assert np.all(np.abs(E[b].astype(np.float64) - ref) <= 2 * ulp), (level, b)
     big = row_exponential(64, 4096, torch.arange(1, 65, dtype=torch.int32, device=gpu),
                           torch.zeros(64, dtype=torch.int32, device=gpu)).cpu()
     assert abs(big.mean().item() - 1.0) < 0.01 and abs((big > 1).float().mean().item() - math.exp(-1)) < 0.005
@@ -203,7 +203,8 @@ def test_frame_with_fp16_depth(gpu):
     dp2.h.copy_(dp.h)
     dp2.codes.copy_(codes)
     ctr = a.depth.row_ctr.clone()
-    a.depth.row_ctr.sub_(torch.isin(torch.arange(9, device=gpu), torch.tensor(slots, device=gpu)).int())
+    # the frame moved each row's counter once, the padding row's (the dummy slot) included
+    a.depth.row_ctr.sub_(torch.bincount(bb.slots, minlength=9).int())
     trace = []
     a.depth.run(dp2, trace=trace)
     torch.cuda.synchronize()
