@@ -77,6 +77,18 @@ int m3x_decode_attn(const void* q, long sq_b, long sq_h, const void* k_cache, co
  * and split, ~3 workgroups per CU. */
 int m3x_decode_attn_item_bins(int rows, int kv_heads, int max_ctx, int chunk);
 
+/* m3x_decode_attn without a workspace argument, allocating nothing. No counterpart in the reference: it is for
+ * callers that cannot allocate (code under graph capture, tight serving loops, harnesses that forbid allocation).
+ * The split partials live in a file-scope device array of M3X_DECODE_ATTN_NOALLOC_SCRATCH bytes that each GPU holds
+ * until the process ends; its address is taken on a device's first call (hipGetSymbolAddress, with the device
+ * current). Returns M3X_EWORKSPACE when m3x_decode_attn_workspace(rows, kv_heads, max_ctx, chunk) exceeds that size
+ * (nothing is launched). Calls that overlap on one GPU share the array and race. Results are m3x_decode_attn's. */
+#define M3X_DECODE_ATTN_NOALLOC_SCRATCH (4u << 20)
+int m3x_decode_attn_noalloc(const void* q, long sq_b, long sq_h, const void* k_cache, const void* v_cache, long sk_s,
+                            long sk_h, long sk_t, int cap, void* out, long so_b, long so_h, const int64_t* slots,
+                            const int32_t* pos, const int32_t* items, float scale, int rows, int heads, int kv_heads,
+                            int head_dim, int max_ctx, int chunk, void* stream);
+
 /* Elements of the packed form of an [N, K] weight (N rounded up to a multiple of 16, times K); -1 if K % 32. */
 long m3x_packed_weight_elems(int N, int K);
 

@@ -18,6 +18,7 @@
 #include "m3x_common.h"
 
 #include <algorithm>
+#include <mutex>
 
 // K rows through a wave-private LDS tile (coalesced loads; bit-identical results): 1-2 % faster at 224 rows and
 // 7 % at one row than loading the MFMA A layout straight from memory (KL = 0).
@@ -560,6 +561,53 @@ M3X_API int m3x_decode_attn(const void* q, long sq_b, long sq_h, const void* k_c
 #undef M3X_ATTN_LAUNCH
   M3X_CHECK_LAUNCH();
   return M3X_OK;
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// Allocation-free decode attention for callers that cannot allocate (code under graph capture, tight serving
+// loops): the split partials go to `scratch`, a file-scope device array of M3X_NOALLOC_SCRATCH_BYTES that every
+// GPU the library runs on holds until the process ends. In host code the array's name is only a stand-in: its
+// device address is taken once per device with hipGetSymbolAddress, on that device's first call, and only that
+// address reaches a kernel. Calls that overlap on one GPU share the array and race; the partials need no clearing
+// (the combine reads only the splits the same call wrote).
+#define M3X_NOALLOC_SCRATCH_BYTES (4u << 20)
+#define M3X_NOALLOC_MAX_DEVICES 64
+static __device__ __align__(256) unsigned char scratch[M3X_NOALLOC_SCRATCH_BYTES];
+static void* g_scratch_addr[M3X_NOALLOC_MAX_DEVICES];
+static std::mutex g_scratch_mu;
+
+static int scratch_address(void** addr) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return M3X_ELAUNCH;
+  if (dev < 0 || dev >= M3X_NOALLOC_MAX_DEVICES) return M3X_EUNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_addr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return M3X_ELAUNCH;
+    g_scratch_addr[dev] = p;
+  }
+  *addr = g_scratch_addr[dev];
+  return M3X_OK;
+}
+
+M3X_API int m3x_decode_attn_noalloc(const void* q, long sq_b, long sq_h, const void* k_cache, const void* v_cache,
+                                    long sk_s, long sk_h, long sk_t, int cap, void* out, long so_b, long so_h,
+                                    const int64_t* slots, const int32_t* pos, const int32_t* items, float scale,
+                                    int rows, int heads, int kv_heads, int head_dim, int max_ctx, int chunk,
+                                    void* stream) {
+  if (rows < 0 || kv_heads <= 0 || max_ctx <= 0 || chunk <= 0) return M3X_EINVAL;
+  if (rows == 0) return M3X_OK;
+  const bool split = (max_ctx + chunk - 1) / chunk > 1;
+  const size_t need = split ? m3x_decode_attn_workspace(rows, kv_heads, max_ctx, chunk) : 0;
+  if (need > M3X_NOALLOC_SCRATCH_BYTES) return M3X_EWORKSPACE;
+  void* ws = nullptr;
+  if (split) {
+    const int st = scratch_address(&ws);
+    if (st != M3X_OK) return st;
+  }
+  return m3x_decode_attn(q, sq_b, sq_h, k_cache, v_cache, sk_s, sk_h, sk_t, cap, out, so_b, so_h, slots, pos, items,
+                         scale, rows, heads, kv_heads, head_dim, max_ctx, chunk, ws, split ? M3X_NOALLOC_SCRATCH_BYTES : 0,
+                         stream);
 }
 
 // ---------------------------------------------------------------------------------------------------------

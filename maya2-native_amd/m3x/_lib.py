@@ -32,6 +32,8 @@ SIGNATURES = {
     "m3x_decode_attn_item_bins": (_I, [_I, _I, _I, _I]),
     "m3x_decode_attn": (_I, [_P, _L, _L, _P, _P, _L, _L, _L, _I, _P, _L, _L, _P, _P, _P, _F, _I, _I, _I, _I, _I, _I,
                              _P, _Z, _P]),
+    "m3x_decode_attn_noalloc": (_I, [_P, _L, _L, _P, _P, _L, _L, _L, _I, _P, _L, _L, _P, _P, _P, _F, _I, _I, _I, _I,
+                                     _I, _I, _P]),
     "m3x_packed_weight_elems": (_L, [_I, _I]),
     "m3x_pack_weight": (_I, [_P, _L, _I, _I, _P, _P]),
     "m3x_linear": (_I, [_P, _L, _P, _P, _L, _I, _I, _I, _I, _P]),
