@@ -319,6 +319,64 @@ int m3x_final_conv(const void* x, long ld_x, void* state, long ld_state, const i
                    float bias, float* pcm, long ld_pcm, int B, int T, int C, int k, int chunk, int dtype,
                    void* stream);
 
+/* ---- the depth frame over a run of continuing levels as one persistent kernel (serve/fast_depth.py:143-203) -- */
+
+/* Arguments of m3x_depth_run: levels L0 .. L1-1, each continuing the weight group of level L0 - 1 (one position
+ * per seat per level, T = 1), for B <= 16 seats. Trunk geometry: width 1024, H heads of hd in {128 (SwiGLU, act
+ * M3X_ACT_SWIGLU, F 2816), 64 (GELU, act M3X_ACT_GELU, F 3072)}, `layers` <= 4 layers, codebooks of 2048 codes.
+ * Weights are packed (m3x_pack_weight): per layer q|k|v [3*1024, 1024], o [1024, 1024], gate (or f1) [F, 1024],
+ * up [F, 1024] (SwiGLU only), down [1024, F]; heads[L-1] [2048, 1024] for each level L of the run. Norms: kind
+ * M3X_NORM_RMS (weights) or M3X_NORM_LAYER (weights and biases) with per-layer eps, and the final norm.
+ * State: prefix[b * ld_prefix + p * 1024 ...] holds position L0's input row; the sampled code of level L goes to
+ * codes[b * ld_codes + L] and, for L < 31, the next prefix row embed[L][code] to prefix position L + 1. kd/vd
+ * [B][H][32][hd] per layer hold the group's K/V at positions < L0. u[b * ld_u + L - 1] is the uniform of level L.
+ * xchg: m3x_depth_run_xchg_bytes() of device memory, zeroed before the first run and then left to the kernel;
+ * sync: 4 int32, zeroed before the first run (the kernel keeps an epoch in [0], a counter in [1] and sets [2]
+ * to 1 if a step's input never arrived, in which case the run's outputs are void). nwg must equal 256 (the
+ * workgroups are resident together: one per CU). logits_out (nullable): [31][B][2048] copy of the head outputs. */
+typedef struct M3xDepthRun {
+  int B, L0, L1, layers, H, hd, F, V, act, norm_kind, dtype, nwg;
+  float inv_temp;
+  int top_k, greedy;
+  float eps1[4], eps2[4], eps_f;
+  const void* n1w[4];
+  const void* n1b[4];
+  const void* n2w[4];
+  const void* n2b[4];
+  const void* fw;
+  const void* fb;
+  const void* wqkv[4];
+  const void* wo[4];
+  const void* wg[4];
+  const void* wu[4];
+  const void* wd[4];
+  const void* heads[31];
+  const void* embed;
+  const void* cross;
+  long ld_cross;
+  void* prefix;
+  long ld_prefix;
+  int32_t* codes;
+  long ld_codes;
+  const float* u;
+  long ld_u;
+  const void* kd[4];
+  const void* vd[4];
+  long kv_sb, kv_sh;
+  uint64_t* xchg;
+  int32_t* sync;
+  void* logits_out;
+} M3xDepthRun;
+
+/* Bytes of the exchange area and of M3xDepthRun (a binding checks its layout against the latter). */
+size_t m3x_depth_run_xchg_bytes(void);
+size_t m3x_depth_run_args_bytes(void);
+
+/* Launch the run described by *args (read on the host during the call; the kernel gets a copy).
+ * Replaces the per-level loop of `_compute_fused` for continuing levels (serve/fast_depth.py:150-155 attention
+ * over the within-group K/V, :179-190 the layers, :191-198 head, sampling and next prefix). */
+int m3x_depth_run(const M3xDepthRun* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

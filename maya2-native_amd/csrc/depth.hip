@@ -1,0 +1,669 @@
+// The depth frame over a run of levels that continue one weight group, as ONE persistent kernel
+// (serve/fast_depth.py:143-203: the incremental levels, :150-155, with their sampling, :191-198).
+//
+// A level is a chain of ~22 dependent steps: per trunk layer q|k|v, attention, o, gate|up (+SwiGLU or GELU) and
+// down, then the codebook head and the sampler. Launched one kernel per step, each step pays a launch and a cold
+// memory round trip (~3.5 us per step at one seat, ~107 us per level). Here one workgroup per CU stays resident
+// for the whole run:
+//   - the first 192 workgroups project the residual stream (q|k|v, gate|up and head tiles): each keeps that stream,
+//     and its norm, in LDS across the layers and the codebooks; each of them also owns up to one (seat, head)
+//     pair, whose depth K/V history it keeps in LDS across the codebooks;
+//   - the last 64 workgroups own the o and down tiles; the down tile's input (16 rows x the FFN width) lands in
+//     their LDS, which holds nothing else;
+//   - a step's weights are loaded before the step waits for its input, so the weight stream overlaps the chain;
+//   - steps hand their outputs over through global memory in LL form: an 8-byte word carries 4 bytes of payload
+//     (two 16-bit values, one code, ...) and a 4-byte tag, written and read with device-scope (sc1) accesses that
+//     stay coherent across the XCDs' L2s. A consumer polls exactly the words it needs until each carries the
+//     step's tag (the launch's epoch << 12 | the step's number). A word is its own flag, so no barrier, fence or
+//     cache flush is needed, and a word read before its producer wrote it is simply read again.
+// Every wait is bounded: a workgroup whose input does not arrive within SPIN_LIMIT polls sets the error word and
+// skips the rest of the run, so the grid always drains. The grid is at most one workgroup per CU (LDS use
+// forces one per CU), so every workgroup is resident and every wait can be satisfied.
+//
+// Numerics follow the launch path step for step: norms in the add+norm kernels' reduction order (bit-identical
+// rows), GEMM tiles accumulate in fp32 over four K slices summed in slice order with one rounding, the gated
+// epilogues round where the reference rounds (serve/fast_backbone.py:201-202, serve/fast_depth.py:123,186),
+// attention in fp32 with one rounding of the output, the sampler is m3x_sample.h's.
+#include "m3x_sample.h"
+
+namespace dk {
+constexpr int NT = 256;     // threads per workgroup
+constexpr int RB = 16;      // seats per run (one MFMA row block)
+constexpr int DM = 1024;    // trunk width
+constexpr int XS = DM + 8;  // LDS row stride of the residual and its norm: a 16-byte offset per row
+constexpr int NPOS = 32;    // positions of a frame
+constexpr int MAXL = 4;     // trunk layers
+constexpr int VMAX = 2048;  // codebook size
+constexpr int FMAX = 3072;  // FFN width
+constexpr int HDMAX = 128;  // head dim
+constexpr unsigned SPIN_LIMIT = 1u << 19;
+constexpr int SC1 = 16;     // cache-policy bit of a device-scope access (gfx950 SC1)
+
+// exchange buffers, in 8-byte words; two copies of each, alternating by layer (by level for head and codes)
+constexpr long W_QKV = (long)RB * 3 * DM / 2, W_ATT = (long)RB * DM / 2, W_GU = (long)RB * FMAX / 2,
+               W_LOG = (long)RB * VMAX / 2, W_CODE = RB;
+constexpr long O_QKV = 0, O_ATT = O_QKV + 2 * W_QKV, O_O = O_ATT + 2 * W_ATT, O_GU = O_O + 2 * W_ATT,
+               O_DN = O_GU + 2 * W_GU, O_LOG = O_DN + 2 * W_ATT, O_CODE = O_LOG + 2 * W_LOG,
+               O_DUMMY = O_CODE + 2 * W_CODE, X_WORDS = O_DUMMY + 8;
+}  // namespace dk
+
+// Arguments of one run (a plain struct of pointers and sizes; the host fills it from m3x_depth_run's caller).
+struct M3xDepthRun {
+  int B, L0, L1, layers, H, hd, F, V, act, norm_kind, dtype, nwg;
+  float inv_temp;
+  int top_k, greedy;
+  float eps1[dk::MAXL], eps2[dk::MAXL], eps_f;
+  const void* n1w[dk::MAXL];
+  const void* n1b[dk::MAXL];
+  const void* n2w[dk::MAXL];
+  const void* n2b[dk::MAXL];
+  const void* fw;
+  const void* fb;
+  const void* wqkv[dk::MAXL];
+  const void* wo[dk::MAXL];
+  const void* wg[dk::MAXL];
+  const void* wu[dk::MAXL];
+  const void* wd[dk::MAXL];
+  const void* heads[31];
+  const void* embed;  // [31][V][DM]: prefix row of level L+1 = embed[L][code]
+  const void* cross;  // [B][layers * DM] speaker constants, or null
+  long ld_cross;
+  void* prefix;       // row b, position p at prefix + b * ld_prefix + p * DM
+  long ld_prefix;
+  int32_t* codes;
+  long ld_codes;
+  const float* u;     // u[b * ld_u + L - 1]
+  long ld_u;
+  const void* kd[dk::MAXL];  // [B][H][32][hd] per layer: the group's K/V at positions < L0
+  const void* vd[dk::MAXL];
+  long kv_sb, kv_sh;
+  uint64_t* xchg;     // dk::X_WORDS words, zeroed once
+  int32_t* sync;      // [0] epoch, [1] workgroups done, [2] error
+  void* logits_out;   // optional [31][B][V] copy of every level's head output (tests)
+};
+
+namespace dk {
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int NXM = 3 * DM / 16;  // workgroups that keep the residual stream (one q|k|v tile each)
+constexpr int NOD = DM / 16;      // workgroups of the o and down tiles
+constexpr int AS = FMAX + 8;      // LDS row stride of the down tile's input
+
+struct SmemXM {
+  uint16_t x[RB][XS];                 // the residual stream of every seat
+  union {
+    uint16_t y[RB][XS];               // its norm: the B operand of the q|k|v, gate|up and head tiles
+    SampleSmemT<VMAX> smp;            // the sampler's candidates (the head's input is dead by then)
+  } u;
+  uint16_t kv[MAXL][2][NPOS][HDMAX];  // this workgroup's (seat, head) K and V history
+};
+struct Smem {
+  union {
+    SmemXM m;
+    uint16_t act[RB][AS];             // o/down workgroups: the down tile's input
+  };
+  float part[2][4][256];              // per-wave partial tiles (gate, up)
+  float qv[HDMAX];
+  float pr[NPOS];
+  int codes[RB];
+};
+
+__device__ __forceinline__ u32x4 ll_ld16(__amdgpu_buffer_rsrc_t r, int word) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, word * 8, 0, SC1);
+}
+__device__ __forceinline__ u32x2 ll_ld8(__amdgpu_buffer_rsrc_t r, int word) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, word * 8, 0, SC1);
+}
+__device__ __forceinline__ void ll_st16(__amdgpu_buffer_rsrc_t r, int word, uint32_t p0, uint32_t p1, uint32_t tag) {
+  const u32x4 v = {p0, tag, p1, tag};
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, word * 8, 0, SC1);
+}
+__device__ __forceinline__ void ll_st8(__amdgpu_buffer_rsrc_t r, int word, uint32_t p, uint32_t tag) {
+  const u32x2 v = {p, tag};
+  __builtin_amdgcn_raw_buffer_store_b64(v, r, word * 8, 0, SC1);
+}
+
+// Poll this thread's N 16-byte chunks (two words each) until both words of every live chunk carry `tag`, handing
+// each chunk's two payloads to sink(i, p0, p1) once. Chunk i sits at word base + U(i), base per thread and U(i) a
+// constant, so the loads take one address register and constant offsets. A finished (or dead) chunk's load is
+// pushed past the end of the buffer, where it returns zeros without touching memory, so every load of a round is
+// issued before the first check and only in-flight loads occupy registers. Workgroup-collective (every thread
+// calls it); false after SPIN_LIMIT rounds.
+constexpr int OOB = 1 << 30;  // a byte offset past every exchange buffer
+template <int N, class U, class Live, class Sink>
+__device__ __forceinline__ bool ll_poll16(__amdgpu_buffer_rsrc_t r, int base, U uoff, Live live, uint32_t tag,
+                                          Sink sink) {
+  static_assert(N <= 64, "chunks per thread");
+  uint64_t pending = 0;
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    if (live(i)) pending |= 1ull << i;
+  for (unsigned it = 0;; ++it) {
+    u32x4 v[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      v[i] = __builtin_amdgcn_raw_buffer_load_b128(r, base * 8 + (((pending >> i) & 1) ? 0 : OOB), uoff(i) * 8, SC1);
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      if (((pending >> i) & 1) && v[i].y == tag && v[i].w == tag) {
+        sink(i, v[i].x, v[i].z);
+        pending &= ~(1ull << i);
+      }
+    }
+    if (__syncthreads_and(pending == 0)) return true;
+    if (it >= SPIN_LIMIT) return false;
+  }
+}
+
+// the same for N single words (8-byte loads); sink(i, payload)
+template <int N, class U, class Live, class Sink>
+__device__ __forceinline__ bool ll_poll8(__amdgpu_buffer_rsrc_t r, int base, U uoff, Live live, uint32_t tag,
+                                         Sink sink) {
+  static_assert(N <= 32, "words per thread");
+  uint32_t pending = 0;
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    if (live(i)) pending |= 1u << i;
+  for (unsigned it = 0;; ++it) {
+    u32x2 v[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      v[i] = __builtin_amdgcn_raw_buffer_load_b64(r, base * 8 + (((pending >> i) & 1) ? 0 : OOB), uoff(i) * 8, SC1);
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      if (((pending >> i) & 1) && v[i].y == tag) {
+        sink(i, v[i].x);
+        pending &= ~(1u << i);
+      }
+    }
+    if (__syncthreads_and(pending == 0)) return true;
+    if (it >= SPIN_LIMIT) return false;
+  }
+}
+
+__device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) { return (uint32_t)lo | ((uint32_t)hi << 16); }
+
+// ---- norms of the resident stream: 16 threads per seat row, thread j of a row holds the 8-element groups
+// g = j + 16 i (i < 8); the partial sums fold as the add+norm kernels' tree (s = 64, 32, 16 inside the thread,
+// 8, 4, 2, 1 across the row's 16 lanes), so the rows are those kernels' bits.
+__device__ __forceinline__ float row16_fold(const float (&p)[8]) {
+  float q[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) q[i] = p[i];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) q[i] = q[i] + q[i + 4];  // s = 64
+#pragma unroll
+  for (int i = 0; i < 2; ++i) q[i] = q[i] + q[i + 2];  // s = 32
+  q[0] = q[0] + q[1];                                  // s = 16
+  const float v = fold_half_sum<16>(q[0]);             // s = 8, 4, 2, 1 across the row's lanes
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), DPP_ROW_NEWBCAST(0), 0xF,
+                                                             0xF, false));
+}
+
+// y[r] = norm(x[r]) for the rows r < B (x, y in LDS; w, b the norm's affine terms in global memory)
+template <int DT>
+__device__ __forceinline__ void norm_rows(Smem& sm, int B, int kind, const uint16_t* w, const uint16_t* b, float eps) {
+  const int r = threadIdx.x >> 4, j = threadIdx.x & 15;
+  float v[8][8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const u16x8 xv = *reinterpret_cast<const u16x8*>(&sm.m.x[r][8 * (j + 16 * i)]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[i][e] = E<DT>::to_f(xv.v[e]);
+  }
+  float p[8];
+  if (kind == M3X_NORM_LAYER) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      p[i] = v[i][0];
+#pragma unroll
+      for (int e = 1; e < 8; ++e) p[i] = p[i] + v[i][e];
+    }
+    const float mean = row16_fold(p) / (float)DM;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[i][e] = v[i][e] - mean;
+      p[i] = v[i][0] * v[i][0];
+#pragma unroll
+      for (int e = 1; e < 8; ++e) p[i] = p[i] + v[i][e] * v[i][e];
+    }
+    const float sd = sqrtf(row16_fold(p) / (float)DM + eps);
+    if (r < B) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int c = 8 * (j + 16 * i);
+        const u16x8 wv = ld16(w + c), bv = ld16(b + c);
+        u16x8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o.v[e] = E<DT>::from_f(v[i][e] / sd * E<DT>::to_f(wv.v[e]) + E<DT>::to_f(bv.v[e]));
+        *reinterpret_cast<u16x8*>(&sm.m.u.y[r][c]) = o;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      p[i] = v[i][0] * v[i][0];
+#pragma unroll
+      for (int e = 1; e < 8; ++e) p[i] = p[i] + v[i][e] * v[i][e];
+    }
+    const float inv = 1.0f / sqrtf(row16_fold(p) / (float)DM + eps);
+    if (r < B) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int c = 8 * (j + 16 * i);
+        const u16x8 wv = ld16(w + c);
+        u16x8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o.v[e] = E<DT>::from_f(rnd<DT>(v[i][e] * inv) * E<DT>::to_f(wv.v[e]));
+        *reinterpret_cast<u16x8*>(&sm.m.u.y[r][c]) = o;
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// x[r] = dt(dt(x[r] + a[r]) + c[r]) for r < B with a from an LL buffer [RB][DM] (c optional, global [B][ld_c])
+template <int DT>
+__device__ __forceinline__ bool add_rows(Smem& sm, __amdgpu_buffer_rsrc_t rs, int base, uint32_t tag, int B,
+                                         const uint16_t* c, long ld_c) {
+  const int r = threadIdx.x >> 4, j = threadIdx.x & 15;
+  // chunk i: columns 8 (j + 16 (i / 2)) + 4 (i % 2) .. + 3 of row r, at word r DM / 2 + col / 2
+  const int w0 = base + r * (DM / 2) + 4 * j;
+  const bool live = r < B;
+  const bool ok = ll_poll16<16>(
+      rs, w0, [](int i) { return 64 * (i >> 1) + 2 * (i & 1); }, [&](int) { return live; }, tag,
+      [&](int i, uint32_t p0, uint32_t p1) {
+        const int col = 8 * (j + 16 * (i >> 1)) + 4 * (i & 1);
+        uint16_t* xp = &sm.m.x[r][col];
+        const uint16_t av[4] = {(uint16_t)(p0 & 0xffff), (uint16_t)(p0 >> 16), (uint16_t)(p1 & 0xffff),
+                                (uint16_t)(p1 >> 16)};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float t = rnd<DT>(E<DT>::to_f(xp[e]) + E<DT>::to_f(av[e]));
+          if (c) t = rnd<DT>(t + E<DT>::to_f(c[(long)r * ld_c + col + e]));
+          xp[e] = E<DT>::from_f(t);
+        }
+      });
+  __syncthreads();
+  return ok;
+}
+
+// rows [RB][K] of an LL buffer into sm.act (rows >= B stay as they are): chunk c = tid + NT i holds columns
+// 4 (c % (K / 4)) .. + 3 of row c / (K / 4), at word 2 c
+template <int K>
+__device__ __forceinline__ bool stage_act(Smem& sm, __amdgpu_buffer_rsrc_t rs, int base, uint32_t tag, int B) {
+  constexpr int CPR = K / 4, N = RB * CPR / NT;
+  static_assert(RB * CPR % NT == 0, "chunks per thread");
+  const bool ok = ll_poll16<N>(
+      rs, base + 2 * (int)threadIdx.x, [](int i) { return 2 * NT * i; },
+      [&](int i) { return (int)(threadIdx.x + NT * i) / CPR < B; }, tag, [&](int i, uint32_t p0, uint32_t p1) {
+        const int cc = threadIdx.x + NT * i;
+        *reinterpret_cast<uint2*>(&sm.act[cc / CPR][4 * (cc % CPR)]) = uint2{p0, p1};
+      });
+  __syncthreads();
+  return ok;
+}
+
+// ---- GEMM tiles: 16 output columns x 16 seat rows; wave w reduces K slice w of 4 (NF fragments of 32)
+template <int NF>
+struct WTile {
+  u16x8 f[NF];
+};
+template <int NF>
+__device__ __forceinline__ void load_tile(WTile<NF>& t, const uint16_t* w, int tile, int K) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint16_t* p = w + (long)tile * 16 * K + (long)wave * NF * 512 + 8 * lane;
+#pragma unroll
+  for (int f = 0; f < NF; ++f) t.f[f] = ld16(p + (long)f * 512);
+}
+// W tile x y^T, y the residual's norm in LDS
+template <int DT, int NF>
+__device__ __forceinline__ f32x4_t mma_y(const WTile<NF>& t, const Smem& sm) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int row = lane & 15, kg = lane >> 4;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int f = 0; f < NF; ++f) {
+    const int k = (wave * NF + f) * 32 + 8 * kg;
+    acc = mfma16x16x32<DT>(t.f[f], *reinterpret_cast<const u16x8*>(&sm.m.u.y[row][k]), acc);
+  }
+  return acc;
+}
+// W tile x act^T, act staged in LDS
+template <int DT, int NF>
+__device__ __forceinline__ f32x4_t mma_act(const WTile<NF>& t, const Smem& sm) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int row = lane & 15, kg = lane >> 4;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int f = 0; f < NF; ++f) {
+    const int k = (wave * NF + f) * 32 + 8 * kg;
+    acc = mfma16x16x32<DT>(t.f[f], *reinterpret_cast<const u16x8*>(&sm.act[row][k]), acc);
+  }
+  return acc;
+}
+
+// Sum the four waves' partial tiles (slice order, one rounding) and store the 16 x 16 tile to an LL buffer
+// row-major [RB][N] at column tile `tile`: EPI 0 plain, 1 SwiGLU (acc = gate, acc2 = up), 2 GELU. dbg (optional):
+// a plain row-major copy [B][ld_dbg].
+template <int DT, int EPI>
+__device__ __forceinline__ void finish_tile(Smem& sm, f32x4_t acc, f32x4_t acc2, __amdgpu_buffer_rsrc_t rs, int base,
+                                            int N, int tile, uint32_t tag, int B, uint16_t* dbg, long ld_dbg) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int row = lane & 15, kg = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    sm.part[0][wave][(4 * kg + i) * 16 + row] = acc[i];
+    if constexpr (EPI == 1) sm.part[1][wave][(4 * kg + i) * 16 + row] = acc2[i];
+  }
+  __syncthreads();
+  if (wave == 0 && row < B) {
+    uint16_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = (4 * kg + i) * 16 + row;
+      float v = rnd<DT>(((sm.part[0][0][idx] + sm.part[0][1][idx]) + sm.part[0][2][idx]) + sm.part[0][3][idx]);
+      if constexpr (EPI == 1) {
+        const float g = v;
+        const float uu =
+            rnd<DT>(((sm.part[1][0][idx] + sm.part[1][1][idx]) + sm.part[1][2][idx]) + sm.part[1][3][idx]);
+        v = rnd<DT>(g / (1.0f + expf(-g))) * uu;
+      } else if constexpr (EPI == 2) {
+        v = 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+      }
+      o[i] = E<DT>::from_f(v);
+    }
+    const int col = 16 * tile + 4 * kg;
+    ll_st16(rs, base + row * (N / 2) + col / 2, pack2(o[0], o[1]), pack2(o[2], o[3]), tag);
+    if (dbg) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dbg[(long)row * ld_dbg + col + i] = o[i];
+    }
+  }
+  __syncthreads();
+}
+}  // namespace dk
+
+using namespace dk;
+
+template <int DT, int ACT, int HD>
+__global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
+  __shared__ Smem sm;
+  const int wg = blockIdx.x, tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int B = a.B, H = a.H, layers = a.layers;
+  const uint32_t epoch = (uint32_t)a.sync[0];
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(a.xchg, 0, (int)(X_WORDS * 8), 0x00020000);
+  // roles: workgroup w < NXM keeps the residual stream and owns q|k|v tile w, gate|up tile w (if any), head tile
+  // w (if any) and the (seat, head) pair NXM - 1 - w (if any); workgroup NXM + t owns o tile t and down tile t
+  const int U_GU = a.F / 16, U_HEAD = a.V / 16;
+  const bool xm = wg < NXM;
+  const bool do_gu = xm && wg < U_GU, do_head = xm && wg < U_HEAD;
+  const int u_od = wg - NXM;
+  const bool do_od = u_od >= 0 && u_od < NOD;
+  const int pair = NXM - 1 - wg;
+  const bool has_pair = xm && pair < B * H;
+  const int pb = has_pair ? pair / H : 0, ph = has_pair ? pair % H : 0;
+  const int steps_per_level = 5 * layers + 2;
+  const float scale = 1.0f / sqrtf((float)HD);
+  bool ok = true;
+
+  // ---- set-up: zeroed LDS rows, the residual at L0 from the prefix, the pair's K/V history
+  if (xm) {
+    for (int i = tid; i < RB * XS / 8; i += NT) {
+      reinterpret_cast<u16x8*>(&sm.m.x[0][0])[i] = u16x8{};
+      reinterpret_cast<u16x8*>(&sm.m.u.y[0][0])[i] = u16x8{};
+    }
+  } else {
+    for (int i = tid; i < RB * AS / 8; i += NT) reinterpret_cast<u16x8*>(&sm.act[0][0])[i] = u16x8{};
+  }
+  __syncthreads();
+  if (xm) {
+    const uint16_t* pre = (const uint16_t*)a.prefix;
+    for (int i = tid; i < B * DM / 8; i += NT) {
+      const int r = i / (DM / 8), c = 8 * (i % (DM / 8));
+      *reinterpret_cast<u16x8*>(&sm.m.x[r][c]) = ld16(pre + (long)r * a.ld_prefix + (long)a.L0 * DM + c);
+    }
+  }
+  if (has_pair) {
+    for (int l = 0; l < layers; ++l) {
+      const uint16_t* kb = (const uint16_t*)a.kd[l] + (long)pb * a.kv_sb + (long)ph * a.kv_sh;
+      const uint16_t* vb = (const uint16_t*)a.vd[l] + (long)pb * a.kv_sb + (long)ph * a.kv_sh;
+      for (int i = tid; i < a.L0 * HD / 8; i += NT) {
+        const int p = i / (HD / 8), c = 8 * (i % (HD / 8));
+        *reinterpret_cast<u16x8*>(&sm.m.kv[l][0][p][c]) = ld16(kb + (long)p * HD + c);
+        *reinterpret_cast<u16x8*>(&sm.m.kv[l][1][p][c]) = ld16(vb + (long)p * HD + c);
+      }
+    }
+  }
+  __syncthreads();
+
+  for (int L = a.L0; L < a.L1 && ok; ++L) {
+    const int li = L - a.L0;
+    const uint32_t lvl_seq = 1u + (uint32_t)(li * steps_per_level);
+    const int lpar = li & 1;
+    for (int l = 0; l < layers && ok; ++l) {
+      const int par = (li * layers + l) & 1;
+      const uint32_t s0 = lvl_seq + 5u * l;  // steps q|k|v .. down of this layer: s0 .. s0 + 4
+      const uint32_t t_qkv = (epoch << 12) | s0, t_att = t_qkv + 1, t_o = t_qkv + 2, t_gu = t_qkv + 3,
+                     t_dn = t_qkv + 4;
+      const int b_qkv = O_QKV + par * W_QKV, b_att = O_ATT + par * W_ATT, b_o = O_O + par * W_ATT,
+                b_gu = O_GU + par * W_GU, b_dn = O_DN + par * W_ATT;
+      // ---- step 1: the layer's input (the level's prefix row, or x + f + c of the previous layer) -> norm -> q|k|v
+      if (xm) {
+        WTile<8> wt;
+        load_tile<8>(wt, (const uint16_t*)a.wqkv[l], wg, DM);
+        if (l == 0 && L > a.L0) {
+          // the previous level's codes; this level's input rows are their prefix rows
+          const uint32_t t_code = (epoch << 12) | (lvl_seq - 1);
+          const int b_code = O_CODE + (1 - lpar) * W_CODE;
+          ok = ll_poll8<1>(rs, b_code + tid, [](int) { return 0; }, [&](int) { return tid < B; }, t_code,
+                           [&](int, uint32_t p) { sm.codes[tid] = (int)p; });
+          __syncthreads();
+          const uint16_t* emb = (const uint16_t*)a.embed + (long)(L - 1) * a.V * DM;
+          for (int i = tid; i < B * DM / 8; i += NT) {
+            const int r = i / (DM / 8), c = 8 * (i % (DM / 8));
+            const long code = min(max(sm.codes[r], 0), a.V - 1);
+            *reinterpret_cast<u16x8*>(&sm.m.x[r][c]) = ld16(emb + code * DM + c);
+          }
+          __syncthreads();
+        } else if (l > 0) {
+          const int b_prev = O_DN + ((li * layers + l - 1) & 1) * W_ATT;
+          const uint16_t* c = a.cross ? (const uint16_t*)a.cross + (long)(l - 1) * DM : nullptr;
+          ok = add_rows<DT>(sm, rs, b_prev, t_qkv - 1, B, c, a.ld_cross);
+        }
+        norm_rows<DT>(sm, B, a.norm_kind, (const uint16_t*)a.n1w[l], (const uint16_t*)a.n1b[l], a.eps1[l]);
+        if (ok) finish_tile<DT, 0>(sm, mma_y<DT, 8>(wt, sm), f32x4_t{}, rs, b_qkv, 3 * DM, wg, t_qkv, B, nullptr, 0);
+      }
+      // ---- step 2: attention of this workgroup's (seat, head) at position L over the group's keys 0..L
+      if (ok && has_pair) {
+        constexpr int per = HD / 4;  // 16-byte chunks of each of q, k and v of one head
+        const int part = tid / per, c = tid % per;
+        const int w0 = b_qkv + pb * (3 * DM / 2) + (part * DM + ph * HD) / 2 + 2 * c;
+        ok = ll_poll16<1>(rs, w0, [](int) { return 0; }, [&](int) { return tid < 3 * per; }, t_qkv,
+                          [&](int, uint32_t p0, uint32_t p1) {
+                            const uint16_t v4[4] = {(uint16_t)(p0 & 0xffff), (uint16_t)(p0 >> 16),
+                                                    (uint16_t)(p1 & 0xffff), (uint16_t)(p1 >> 16)};
+                            if (part == 0) {
+#pragma unroll
+                              for (int e = 0; e < 4; ++e) sm.qv[4 * c + e] = E<DT>::to_f(v4[e]);
+                            } else {
+#pragma unroll
+                              for (int e = 0; e < 4; ++e) sm.m.kv[l][part - 1][L][4 * c + e] = v4[e];
+                            }
+                          });
+        if (wave == 0) {
+          // lane j <= L: the score of key j
+          float sj = -INFINITY;
+          if (lane <= L) {
+            float d = 0.f;
+            for (int cc = 0; cc < HD; cc += 8) {
+              const u16x8 k8 = *reinterpret_cast<const u16x8*>(&sm.m.kv[l][0][lane][cc]);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) d = fmaf(sm.qv[cc + e], E<DT>::to_f(k8.v[e]), d);
+            }
+            sj = d * scale;
+          }
+          float m = sj;
+          for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+          const float e = lane <= L ? expf(sj - m) : 0.f;
+          float sum = e;
+          for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+          if (lane < NPOS) sm.pr[lane] = e / sum;
+        }
+        __syncthreads();
+        if (tid < HD / 4) {
+          // thread t: output dims 4t .. 4t + 3
+          float o4[4] = {0.f, 0.f, 0.f, 0.f};
+          for (int j = 0; j <= L; ++j) {
+            const float pj = sm.pr[j];
+            const uint16_t* vr = &sm.m.kv[l][1][j][4 * tid];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o4[e] = fmaf(pj, E<DT>::to_f(vr[e]), o4[e]);
+          }
+          ll_st16(rs, b_att + pb * (DM / 2) + (ph * HD + 4 * tid) / 2,
+                  pack2(E<DT>::from_f(o4[0]), E<DT>::from_f(o4[1])), pack2(E<DT>::from_f(o4[2]), E<DT>::from_f(o4[3])),
+                  t_att);
+        }
+        __syncthreads();
+      }
+      // ---- step 3: o projection of the attention rows
+      if (ok && do_od) {
+        WTile<8> wt;
+        load_tile<8>(wt, (const uint16_t*)a.wo[l], u_od, DM);
+        ok = stage_act<DM>(sm, rs, b_att, t_att, B);
+        if (ok) finish_tile<DT, 0>(sm, mma_act<DT, 8>(wt, sm), f32x4_t{}, rs, b_o, DM, u_od, t_o, B, nullptr, 0);
+      }
+      // ---- step 4: x += o -> norm -> gate|up with the activation
+      if (ok && xm) {
+        WTile<8> wg_, wu_;
+        if (do_gu) {
+          load_tile<8>(wg_, (const uint16_t*)a.wg[l], wg, DM);
+          if constexpr (ACT == 1) load_tile<8>(wu_, (const uint16_t*)a.wu[l], wg, DM);
+        }
+        ok = add_rows<DT>(sm, rs, b_o, t_o, B, nullptr, 0);
+        norm_rows<DT>(sm, B, a.norm_kind, (const uint16_t*)a.n2w[l], (const uint16_t*)a.n2b[l], a.eps2[l]);
+        if (ok && do_gu) {
+          if constexpr (ACT == 1)
+            finish_tile<DT, 1>(sm, mma_y<DT, 8>(wg_, sm), mma_y<DT, 8>(wu_, sm), rs, b_gu, a.F, wg, t_gu, B, nullptr,
+                               0);
+          else
+            finish_tile<DT, 2>(sm, mma_y<DT, 8>(wg_, sm), f32x4_t{}, rs, b_gu, a.F, wg, t_gu, B, nullptr, 0);
+        }
+      }
+      // ---- step 5: down projection of the activation (staged in LDS)
+      if (ok && do_od) {
+        f32x4_t acc;
+        if constexpr (ACT == 1) {
+          WTile<22> wt;
+          load_tile<22>(wt, (const uint16_t*)a.wd[l], u_od, 2816);
+          ok = stage_act<2816>(sm, rs, b_gu, t_gu, B);
+          acc = mma_act<DT, 22>(wt, sm);
+        } else {
+          WTile<24> wt;
+          load_tile<24>(wt, (const uint16_t*)a.wd[l], u_od, 3072);
+          ok = stage_act<3072>(sm, rs, b_gu, t_gu, B);
+          acc = mma_act<DT, 24>(wt, sm);
+        }
+        if (ok) finish_tile<DT, 0>(sm, acc, f32x4_t{}, rs, b_dn, DM, u_od, t_dn, B, nullptr, 0);
+      }
+    }
+    if (!ok) break;
+    // ---- the codebook head of level L over the final norm of x + f + c
+    const uint32_t t_log = (epoch << 12) | (lvl_seq + 5u * layers), t_code = t_log + 1;
+    const int b_log = O_LOG + lpar * W_LOG, b_code = O_CODE + lpar * W_CODE;
+    if (xm) {
+      WTile<8> wt;
+      if (do_head) load_tile<8>(wt, (const uint16_t*)a.heads[L - 1], wg, DM);
+      const int b_prev = O_DN + ((li * layers + layers - 1) & 1) * W_ATT;
+      const uint16_t* c = a.cross ? (const uint16_t*)a.cross + (long)(layers - 1) * DM : nullptr;
+      ok = add_rows<DT>(sm, rs, b_prev, t_log - 1, B, c, a.ld_cross);
+      norm_rows<DT>(sm, B, a.norm_kind, (const uint16_t*)a.fw, (const uint16_t*)a.fb, a.eps_f);
+      if (ok && do_head) {
+        uint16_t* dbg = a.logits_out ? (uint16_t*)a.logits_out + (long)(L - 1) * B * a.V : nullptr;
+        finish_tile<DT, 0>(sm, mma_y<DT, 8>(wt, sm), f32x4_t{}, rs, b_log, a.V, wg, t_log, B, dbg, a.V);
+      }
+    }
+    // ---- sampling of seat wg's code (the launch path's sampler, on the LL copy of the head row)
+    if (ok && wg < B) {
+      const int r = wg;
+      constexpr int NE = VMAX / NT;
+      const float ur = a.greedy ? 0.f : a.u[(long)r * a.ld_u + L - 1];
+      float xv[NE];
+      ok = ll_poll8<NE>(rs, b_log + r * (VMAX / 2) + tid / 2, [](int e) { return NT / 2 * e; },
+                        [&](int) { return true; }, t_log, [&](int e, uint32_t p) {
+                          const uint16_t h16 = (uint16_t)((tid & 1) ? (p >> 16) : (p & 0xffff));
+                          xv[e] = E<DT>::to_f(h16) * a.inv_temp;
+                        });
+      topk_select<NE>(xv, VMAX, a.top_k, sm.m.u.smp);
+      if (tid < 64) {
+        int code = cand_index(sm.m.u.smp.cand[0]);
+        if (!a.greedy) {
+          const int cp = pick(sm.m.u.smp, sm.m.u.smp.nkeep, ur, -1);
+          if (cp >= 0) code = cp;
+        }
+        if (tid == 0) {
+          sm.codes[0] = code;
+          a.codes[(long)r * a.ld_codes + L] = code;
+          ll_st8(rs, b_code + r, (uint32_t)code, t_code);
+        }
+      }
+      __syncthreads();
+      if (L + 1 < NPOS && tid < DM / 8) {
+        // the next prefix row, for a later group start that recomputes the whole prefix
+        const long code = min(max(sm.codes[0], 0), VMAX - 1);
+        st16((uint16_t*)a.prefix + (long)r * a.ld_prefix + (long)(L + 1) * DM + 8 * tid,
+             ld16((const uint16_t*)a.embed + ((long)L * VMAX + code) * DM + 8 * tid));
+      }
+      __syncthreads();
+    }
+  }
+
+  // ---- the run's end: failures are recorded, and the last workgroup out advances the epoch
+  if (!ok && tid == 0) atomicOr(&a.sync[2], 1);
+  __syncthreads();
+  if (tid == 0) {
+    const int prev = atomicAdd(&a.sync[1], 1);
+    if (prev == (int)gridDim.x - 1) {
+      a.sync[1] = 0;
+      a.sync[0] = (int)((epoch + 1) & 0xFFFFF);
+    }
+  }
+}
+
+M3X_API size_t m3x_depth_run_xchg_bytes(void) { return (size_t)X_WORDS * 8; }
+M3X_API size_t m3x_depth_run_args_bytes(void) { return sizeof(M3xDepthRun); }
+
+M3X_API int m3x_depth_run(const M3xDepthRun* args, void* stream) {
+  if (!args) return M3X_ENULL;
+  const M3xDepthRun& a = *args;
+  if (a.B <= 0 || a.B > RB || a.L0 < 2 || a.L1 > NPOS || a.L0 >= a.L1 || a.layers <= 0 || a.layers > MAXL)
+    return M3X_EINVAL;
+  if (a.H * a.hd != DM || (a.hd != 64 && a.hd != 128) || a.V != VMAX || a.top_k <= 0) return M3X_EUNSUPPORTED;
+  if (!((a.act == 0 && a.F == 2816) || (a.act == 1 && a.F == 3072))) return M3X_EUNSUPPORTED;
+  if (a.nwg != NXM + NOD || a.B * a.H > NXM) return M3X_EINVAL;
+  if (!a.xchg || !a.sync || !a.embed || !a.prefix || !a.codes || (!a.greedy && !a.u) || !a.fw) return M3X_ENULL;
+  if (a.norm_kind == M3X_NORM_LAYER && !a.fb) return M3X_ENULL;
+  for (int l = 0; l < a.layers; ++l) {
+    if (!a.wqkv[l] || !a.wo[l] || !a.wg[l] || !a.wd[l] || !a.n1w[l] || !a.n2w[l] || !a.kd[l] || !a.vd[l])
+      return M3X_ENULL;
+    if (a.act == 0 && !a.wu[l]) return M3X_ENULL;
+    if (a.norm_kind == M3X_NORM_LAYER && (!a.n1b[l] || !a.n2b[l])) return M3X_ENULL;
+  }
+  for (int L = a.L0; L < a.L1; ++L)
+    if (!a.heads[L - 1]) return M3X_ENULL;
+  hipStream_t st = (hipStream_t)stream;
+#define M3X_DR(DTT, ACTT, HDD) \
+  hipLaunchKernelGGL((depth_run_kernel<DTT, ACTT, HDD>), dim3(a.nwg), dim3(NT), 0, st, a)
+  // ACT template: 1 = SwiGLU pair (act 0 in the host's numbering), 2 = GELU
+  if (a.dtype == M3X_BF16 && a.act == 0 && a.hd == 128) M3X_DR(M3X_BF16, 1, 128);
+  else if (a.dtype == M3X_BF16 && a.act == 1 && a.hd == 64) M3X_DR(M3X_BF16, 2, 64);
+  else if (a.dtype == M3X_F16 && a.act == 0 && a.hd == 128) M3X_DR(M3X_F16, 1, 128);
+  else if (a.dtype == M3X_F16 && a.act == 1 && a.hd == 64) M3X_DR(M3X_F16, 2, 64);
+  else return M3X_EUNSUPPORTED;
+#undef M3X_DR
+  M3X_CHECK_LAUNCH();
+  return M3X_OK;
+}

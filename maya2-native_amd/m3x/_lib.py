@@ -59,6 +59,9 @@ SIGNATURES = {
     "m3x_loop_guard": (_I, [_P, _L, _P, _P, _P, _I, _I, _I, _I, ctypes.c_double, _I, _I, _P]),
     "m3x_tick_pack_width": (_I, [_I, _I, _I]),
     "m3x_tick_pack": (_I, [_P, _P, _P, _P, _L, _I, _P, _L, _I, _P, _L, _I, _P]),
+    "m3x_depth_run_xchg_bytes": (_Z, []),
+    "m3x_depth_run_args_bytes": (_Z, []),
+    "m3x_depth_run": (_I, [_P, _P]),
     "m3x_rvq_decode": (_I, [_P, _L, _P, _P, _L, _I, _I, _I, _I, _I, _P]),
     "m3x_dwconvt": (_I, [_P, _L, _P, _P, _L, _P, _P, _I, _I, _I, _I, _I, _P]),
     "m3x_conv_gather": (_I, [_P, _L, _P, _L, _P, _P, _L, _I, _I, _I, _I, _I, _I, _I, _I, _P]),

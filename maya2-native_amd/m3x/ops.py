@@ -413,6 +413,34 @@ def code_ring_write(codes, ring, head, B):
                                     ring.shape[2], int(B), _stream()), "code_ring_write")
 
 
+# ---------------------------------------------------------------- the depth frame as one persistent run
+class DepthRunArgs(ctypes.Structure):
+    """Mirror of M3xDepthRun (include/m3x.h); its size is checked against the library's."""
+    _P4 = ctypes.c_void_p * 4
+    _fields_ = [(n, ctypes.c_int) for n in ("B", "L0", "L1", "layers", "H", "hd", "F", "V", "act", "norm_kind",
+                                            "dtype", "nwg")] + [
+        ("inv_temp", ctypes.c_float), ("top_k", ctypes.c_int), ("greedy", ctypes.c_int),
+        ("eps1", ctypes.c_float * 4), ("eps2", ctypes.c_float * 4), ("eps_f", ctypes.c_float),
+        ("n1w", _P4), ("n1b", _P4), ("n2w", _P4), ("n2b", _P4), ("fw", ctypes.c_void_p), ("fb", ctypes.c_void_p),
+        ("wqkv", _P4), ("wo", _P4), ("wg", _P4), ("wu", _P4), ("wd", _P4), ("heads", ctypes.c_void_p * 31),
+        ("embed", ctypes.c_void_p), ("cross", ctypes.c_void_p), ("ld_cross", ctypes.c_long),
+        ("prefix", ctypes.c_void_p), ("ld_prefix", ctypes.c_long), ("codes", ctypes.c_void_p),
+        ("ld_codes", ctypes.c_long), ("u", ctypes.c_void_p), ("ld_u", ctypes.c_long), ("kd", _P4), ("vd", _P4),
+        ("kv_sb", ctypes.c_long), ("kv_sh", ctypes.c_long), ("xchg", ctypes.c_void_p), ("sync", ctypes.c_void_p),
+        ("logits_out", ctypes.c_void_p)]
+
+
+def depth_run_xchg_bytes() -> int:
+    return int(lib().m3x_depth_run_xchg_bytes())
+
+
+def depth_run(args: DepthRunArgs):
+    """Launch a persistent depth run on the current stream (args built by FastDepth)."""
+    if ctypes.sizeof(DepthRunArgs) != int(lib().m3x_depth_run_args_bytes()):
+        raise RuntimeError("DepthRunArgs does not match the library's M3xDepthRun: rebuild the library")
+    check(lib().m3x_depth_run(ctypes.byref(args), _stream()), "depth_run")
+
+
 # ---------------------------------------------------------------- Mimi decode (serve/fast_codec.py)
 def rvq_decode(codes, tables, out):
     """out[b] = [table_0[codes[b, 0]] | sum over q >= 1 of table_q[codes[b, q]]]; tables [nq, n_codes, dim]."""

@@ -91,6 +91,12 @@ class FastDepth:
         self.graphs = {}
         self.pool = None
         self._fn = self._compute
+        # the persistent run of continuing levels (m3x_depth_run): its exchange area, epoch/error words, and the
+        # workgroup count (one per CU)
+        self.persistent = True
+        self._run_xchg = torch.zeros(ops.depth_run_xchg_bytes() // 8, dtype=torch.int64, device=dev)
+        self._run_sync = torch.zeros(4, dtype=torch.int32, device=dev)
+        self._nwg = torch.cuda.get_device_properties(dev).multi_processor_count
 
     def _load(self, model):
         d, dt = model.depth, self.dtype
@@ -206,9 +212,26 @@ class FastDepth:
         ops.copy_rows(self.embed[0], b.prefix[:, 1], src_idx=b.codes[:, 0])
         inv_temp = 1.0 / self.temp
         staged = False  # the previous sampler already wrote this level's input row and its norm
-        for level in range(1, N_LEVELS):
+        level = 1
+        while level < N_LEVELS:
             group = self.group_of_level[level]
             continues = level > 1 and self.group_of_level[level - 1] == group
+            if continues and self._persistent_ok(B, group):
+                # every level that continues this group, in one persistent kernel
+                end = level
+                while end < N_LEVELS and self.group_of_level[end] == group:
+                    end += 1
+                a = self._run_args(b, level, end, group)
+                logits = None
+                if trace is not None:
+                    logits = torch.empty(N_LEVELS - 1, B, self.n_codes, dtype=self.dtype, device=self.device)
+                    a.logits_out = logits.data_ptr()
+                ops.depth_run(a)
+                a.logits_out = None
+                if trace is not None:
+                    trace.extend(logits[lv - 1].clone() for lv in range(level, end))
+                level, staged = end, False
+                continue
             T, p0 = (1, level) if continues else (level + 1, 0)
             layers = self.trunks[group]
             n1 = layers[0].n1
@@ -226,14 +249,71 @@ class FastDepth:
                 break
             # the sampler writes the drawn code's prefix row; when the next level continues this group its input
             # is exactly that one row, so the sampler also writes the row's first-layer norm
-            staged = self.group_of_level[nxt] == group
+            staged = self.group_of_level[nxt] == group and not self._persistent_ok(B, group)
             norm_out = dict(x_out=b.xw[:B], y=b.yw[:B], w=n1.w, b=n1.b, eps=n1.eps, kind=n1.kind) if staged else {}
             ops.topk_sample_embed(b.logits, u, inv_temp, self.top_k, self.greedy, b.codes[:, level],
                                   self.embed[level], b.prefix[:, nxt], **norm_out)
+            level = nxt
         ops.ctr_add(self.row_ctr, b.slots)
         ops.feedback(self.fb_table, b.codes, b.feedback, self.fb_norm.w, self.fb_norm.eps, self.feedback_scale,
                      N_LEVELS, self.n_codes)
         return b.codes, b.feedback
+
+    # ---------------------------------------------------------------- persistent run
+    PERSISTENT_SEATS = 16
+
+    def _persistent_ok(self, B, group):
+        """Whether levels continuing `group` run as one persistent kernel for B seats: at most 16 seats and one
+        (seat, head) pair per residual workgroup, one workgroup per CU on a 256-CU part, the trunk geometries the
+        kernel implements (width 1024, 2048 codes, SwiGLU 2816 with 128-wide heads or GELU 3072 with 64-wide
+        heads, one norm kind) in bf16 or fp16."""
+        if not self.persistent or B > self.PERSISTENT_SEATS or B * self.H > 192 or self._nwg != 256:
+            return False
+        layers = self.trunks[group]
+        kinds = {L.n1.kind for L in layers} | {L.n2.kind for L in layers} | {self.final_norm.kind}
+        geo = {(L.act, L.ffn) for L in layers}
+        return (self.D == 1024 and self.n_codes == 2048 and len(layers) <= 4 and len(kinds) == 1 and len(geo) == 1
+                and geo.pop() in ((ops.ACT_SWIGLU, 2816), (ops.ACT_GELU, 3072))
+                and self.hd == (128 if layers[0].act == ops.ACT_SWIGLU else 64))
+
+    def _run_args(self, b, L0, L1, group):
+        """The persistent run's arguments for buffer set b and levels L0 .. L1-1 (built once; the pointers are
+        those of b's static buffers)."""
+        runs = b.__dict__.setdefault('runs', {})
+        key = (L0, L1, group)
+        if key in runs:
+            return runs[key]
+        layers = self.trunks[group]
+        a = ops.DepthRunArgs()
+        a.B, a.L0, a.L1, a.layers, a.H, a.hd = b.B, L0, L1, len(layers), self.H, self.hd
+        a.F, a.V, a.act, a.norm_kind = layers[0].ffn, self.n_codes, layers[0].act, layers[0].n1.kind
+        a.dtype, a.nwg = ops._DT[self.dtype], self._nwg
+        a.inv_temp, a.top_k, a.greedy = 1.0 / self.temp, self.top_k, int(self.greedy)
+        p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+        for l, L in enumerate(layers):
+            a.eps1[l], a.eps2[l] = L.n1.eps, L.n2.eps
+            a.n1w[l], a.n1b[l], a.n2w[l], a.n2b[l] = p(L.n1.w), p(L.n1.b), p(L.n2.w), p(L.n2.b)
+            a.wqkv[l], a.wo[l], a.wg[l], a.wd[l] = p(L.qkv.data), p(L.o.data), p(L.wg.data), p(L.w2.data)
+            a.wu[l] = p(L.wu.data) if L.wu is not None else None
+            a.kd[l], a.vd[l] = p(b.kd[l]), p(b.vd[l])
+        a.eps_f, a.fw, a.fb = self.final_norm.eps, p(self.final_norm.w), p(self.final_norm.b)
+        for i, hw in enumerate(self.heads):
+            a.heads[i] = p(hw.data)
+        a.embed = p(self.embed)
+        if b.crossb is not None:
+            a.cross, a.ld_cross = p(b.crossb), b.crossb.stride(0)
+        a.prefix, a.ld_prefix = p(b.prefix), b.prefix.stride(0)
+        a.codes, a.ld_codes = p(b.codes), b.codes.stride(0)
+        a.u, a.ld_u = p(b.u), b.u.stride(0)
+        a.kv_sb, a.kv_sh = b.kd[0].stride(0), b.kd[0].stride(1)
+        a.xchg, a.sync = p(self._run_xchg), p(self._run_sync)
+        runs[key] = a
+        return a
+
+    def run_error(self):
+        """True when a persistent run since construction (or the last clear) lost a step's input and voided its
+        outputs (the kernel's bounded waits ran out)."""
+        return bool(self._run_sync[2].item())
 
     def _compute(self, slots_idx, h, cb0):
         """Eager frame body over fresh buffers (the reference's tests call `_fn(slots_idx, h, cb0)`)."""
