@@ -333,7 +333,8 @@ int m3x_final_conv(const void* x, long ld_x, void* state, long ld_state, const i
  * xchg: m3x_depth_run_xchg_bytes() of device memory, zeroed before the first run and then left to the kernel;
  * sync: 4 int32, zeroed before the first run (the kernel keeps an epoch in [0], a counter in [1] and sets [2]
  * to 1 if a step's input never arrived, in which case the run's outputs are void). nwg must equal 256 (the
- * workgroups are resident together: one per CU). logits_out (nullable): [31][B][2048] copy of the head outputs. */
+ * workgroups are resident together: one per CU). logits_out (nullable): [31][B][2048] copy of the head outputs.
+ * prof (nullable): [256][2048] real-time counter stamps of every workgroup's steps (profiling). */
 typedef struct M3xDepthRun {
   int B, L0, L1, layers, H, hd, F, V, act, norm_kind, dtype, nwg;
   float inv_temp;
@@ -366,6 +367,7 @@ typedef struct M3xDepthRun {
   uint64_t* xchg;
   int32_t* sync;
   void* logits_out;
+  uint64_t* prof;
 } M3xDepthRun;
 
 /* Bytes of the exchange area and of M3xDepthRun (a binding checks its layout against the latter). */

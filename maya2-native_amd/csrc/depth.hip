@@ -80,6 +80,7 @@ struct M3xDepthRun {
   uint64_t* xchg;     // dk::X_WORDS words, zeroed once
   int32_t* sync;      // [0] epoch, [1] workgroups done, [2] error
   void* logits_out;   // optional [31][B][V] copy of every level's head output (tests)
+  uint64_t* prof;     // optional [nwg][2048] real-time stamps of each workgroup's steps (profiling)
 };
 
 namespace dk {
@@ -107,7 +108,19 @@ struct Smem {
   float qv[HDMAX];
   float pr[NPOS];
   int codes[RB];
+  int vote[2][NT / 64];               // wg_all's per-wave votes, alternating buffers
 };
+
+// true in every thread iff v is true in every thread: one barrier; the two vote buffers alternate, so a wave that
+// runs ahead into the next call writes the other buffer while a slower one still reads this one
+__device__ __forceinline__ bool wg_all(Smem& sm, bool v, int& phase) {
+  const bool any_false = __ballot(!v) != 0;
+  if ((threadIdx.x & 63) == 0) sm.vote[phase][threadIdx.x >> 6] = any_false;
+  __syncthreads();
+  const bool r = !(sm.vote[phase][0] | sm.vote[phase][1] | sm.vote[phase][2] | sm.vote[phase][3]);
+  phase ^= 1;
+  return r;
+}
 
 __device__ __forceinline__ u32x4 ll_ld16(__amdgpu_buffer_rsrc_t r, int word) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, word * 8, 0, SC1);
@@ -124,60 +137,94 @@ __device__ __forceinline__ void ll_st8(__amdgpu_buffer_rsrc_t r, int word, uint3
   __builtin_amdgcn_raw_buffer_store_b64(v, r, word * 8, 0, SC1);
 }
 
+// Read-only tensors through buffer resources: the base stays in scalar registers and a load takes one 32-bit
+// offset register, so loop-invariant addressing does not pin 64-bit vector address pairs for the whole run.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t ro_rsrc(const void* p) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ u16x8 bld16(__amdgpu_buffer_rsrc_t r, int voff_bytes, int soff_bytes) {
+  return __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff_bytes, soff_bytes, 0));
+}
+
 // Poll this thread's N 16-byte chunks (two words each) until both words of every live chunk carry `tag`, handing
 // each chunk's two payloads to sink(i, p0, p1) once. Chunk i sits at word base + U(i), base per thread and U(i) a
-// constant, so the loads take one address register and constant offsets. A finished (or dead) chunk's load is
-// pushed past the end of the buffer, where it returns zeros without touching memory, so every load of a round is
-// issued before the first check and only in-flight loads occupy registers. Workgroup-collective (every thread
-// calls it); false after SPIN_LIMIT rounds.
+// constant, so the loads take one address register and constant offsets. A chunk that is not being polled has its
+// load pushed past the end of the buffer, where it returns zeros without touching memory, so every load of a round
+// is issued before the first check and only in-flight loads occupy registers.
+// Rounds first poll each thread's chunk 0 alone (a probe: a few bytes per thread while the producers still run);
+// once every probe has its tag, a round reads every chunk still missing, and later rounds only the stragglers.
+// Workgroup-collective (every thread calls it); false after SPIN_LIMIT rounds.
 constexpr int OOB = 1 << 30;  // a byte offset past every exchange buffer
 template <int N, class U, class Live, class Sink>
-__device__ __forceinline__ bool ll_poll16(__amdgpu_buffer_rsrc_t r, int base, U uoff, Live live, uint32_t tag,
-                                          Sink sink) {
+__device__ __forceinline__ bool ll_poll16(Smem& sm, int& vph, __amdgpu_buffer_rsrc_t r, int base, U uoff, Live live,
+                                          uint32_t tag, Sink sink) {
   static_assert(N <= 64, "chunks per thread");
   uint64_t pending = 0;
 #pragma unroll
   for (int i = 0; i < N; ++i)
     if (live(i)) pending |= 1ull << i;
+  uint64_t active = pending & 1ull;
+  bool probing = N > 1;
+  if (!probing) active = pending;
   for (unsigned it = 0;; ++it) {
     u32x4 v[N];
 #pragma unroll
     for (int i = 0; i < N; ++i)
-      v[i] = __builtin_amdgcn_raw_buffer_load_b128(r, base * 8 + (((pending >> i) & 1) ? 0 : OOB), uoff(i) * 8, SC1);
+      v[i] = __builtin_amdgcn_raw_buffer_load_b128(r, base * 8 + (((active >> i) & 1) ? 0 : OOB), uoff(i) * 8, SC1);
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-      if (((pending >> i) & 1) && v[i].y == tag && v[i].w == tag) {
+      if (((active >> i) & 1) && v[i].y == tag && v[i].w == tag) {
         sink(i, v[i].x, v[i].z);
         pending &= ~(1ull << i);
       }
     }
-    if (__syncthreads_and(pending == 0)) return true;
+    if (probing) {
+      active &= pending;
+      if (wg_all(sm, active == 0, vph)) {
+        probing = false;
+        active = pending;
+      }
+    } else {
+      active = pending;
+      if (wg_all(sm, pending == 0, vph)) return true;
+    }
     if (it >= SPIN_LIMIT) return false;
   }
 }
 
 // the same for N single words (8-byte loads); sink(i, payload)
 template <int N, class U, class Live, class Sink>
-__device__ __forceinline__ bool ll_poll8(__amdgpu_buffer_rsrc_t r, int base, U uoff, Live live, uint32_t tag,
-                                         Sink sink) {
+__device__ __forceinline__ bool ll_poll8(Smem& sm, int& vph, __amdgpu_buffer_rsrc_t r, int base, U uoff, Live live,
+                                         uint32_t tag, Sink sink) {
   static_assert(N <= 32, "words per thread");
   uint32_t pending = 0;
 #pragma unroll
   for (int i = 0; i < N; ++i)
     if (live(i)) pending |= 1u << i;
+  uint32_t active = N > 1 ? (pending & 1u) : pending;
+  bool probing = N > 1;
   for (unsigned it = 0;; ++it) {
     u32x2 v[N];
 #pragma unroll
     for (int i = 0; i < N; ++i)
-      v[i] = __builtin_amdgcn_raw_buffer_load_b64(r, base * 8 + (((pending >> i) & 1) ? 0 : OOB), uoff(i) * 8, SC1);
+      v[i] = __builtin_amdgcn_raw_buffer_load_b64(r, base * 8 + (((active >> i) & 1) ? 0 : OOB), uoff(i) * 8, SC1);
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-      if (((pending >> i) & 1) && v[i].y == tag) {
+      if (((active >> i) & 1) && v[i].y == tag) {
         sink(i, v[i].x);
         pending &= ~(1u << i);
       }
     }
-    if (__syncthreads_and(pending == 0)) return true;
+    if (probing) {
+      active &= pending;
+      if (wg_all(sm, active == 0, vph)) {
+        probing = false;
+        active = pending;
+      }
+    } else {
+      active = pending;
+      if (wg_all(sm, pending == 0, vph)) return true;
+    }
     if (it >= SPIN_LIMIT) return false;
   }
 }
@@ -201,9 +248,28 @@ __device__ __forceinline__ float row16_fold(const float (&p)[8]) {
                                                              0xF, false));
 }
 
-// y[r] = norm(x[r]) for the rows r < B (x, y in LDS; w, b the norm's affine terms in global memory)
+// the affine terms of a norm, as norm_rows' threads use them (loaded before a step waits for its input)
+struct NormW {
+  u16x8 w[8], b[8];
+};
+__device__ __forceinline__ void load_norm(NormW& n, const void* w, const void* b, int kind) {
+  const int voff = 16 * (threadIdx.x & 15);
+  const __amdgpu_buffer_rsrc_t rw = ro_rsrc(w);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) n.w[i] = bld16(rw, voff, 256 * i);
+  if (kind == M3X_NORM_LAYER) {
+    const __amdgpu_buffer_rsrc_t rb = ro_rsrc(b);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) n.b[i] = bld16(rb, voff, 256 * i);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) n.b[i] = u16x8{};
+  }
+}
+
+// y[r] = norm(x[r]) for the rows r < B (x, y in LDS; the affine terms preloaded)
 template <int DT>
-__device__ __forceinline__ void norm_rows(Smem& sm, int B, int kind, const uint16_t* w, const uint16_t* b, float eps) {
+__device__ __forceinline__ void norm_rows(Smem& sm, int B, int kind, const NormW& nw, float eps) {
   const int r = threadIdx.x >> 4, j = threadIdx.x & 15;
   float v[8][8];
 #pragma unroll
@@ -234,7 +300,7 @@ __device__ __forceinline__ void norm_rows(Smem& sm, int B, int kind, const uint1
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int c = 8 * (j + 16 * i);
-        const u16x8 wv = ld16(w + c), bv = ld16(b + c);
+        const u16x8 wv = nw.w[i], bv = nw.b[i];
         u16x8 o;
 #pragma unroll
         for (int e = 0; e < 8; ++e) o.v[e] = E<DT>::from_f(v[i][e] / sd * E<DT>::to_f(wv.v[e]) + E<DT>::to_f(bv.v[e]));
@@ -253,7 +319,7 @@ __device__ __forceinline__ void norm_rows(Smem& sm, int B, int kind, const uint1
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int c = 8 * (j + 16 * i);
-        const u16x8 wv = ld16(w + c);
+        const u16x8 wv = nw.w[i];
         u16x8 o;
 #pragma unroll
         for (int e = 0; e < 8; ++e) o.v[e] = E<DT>::from_f(rnd<DT>(v[i][e] * inv) * E<DT>::to_f(wv.v[e]));
@@ -266,23 +332,35 @@ __device__ __forceinline__ void norm_rows(Smem& sm, int B, int kind, const uint1
 
 // x[r] = dt(dt(x[r] + a[r]) + c[r]) for r < B with a from an LL buffer [RB][DM] (c optional, global [B][ld_c])
 template <int DT>
-__device__ __forceinline__ bool add_rows(Smem& sm, __amdgpu_buffer_rsrc_t rs, int base, uint32_t tag, int B,
-                                         const uint16_t* c, long ld_c) {
+__device__ __forceinline__ bool add_rows(Smem& sm, int& vph, __amdgpu_buffer_rsrc_t rs, int base, uint32_t tag,
+                                         int B, const uint16_t* c, long ld_c) {
   const int r = threadIdx.x >> 4, j = threadIdx.x & 15;
   // chunk i: columns 8 (j + 16 (i / 2)) + 4 (i % 2) .. + 3 of row r, at word r DM / 2 + col / 2
   const int w0 = base + r * (DM / 2) + 4 * j;
   const bool live = r < B;
+  uint2 cv[16];
+  if (c && live) {
+    const __amdgpu_buffer_rsrc_t rc = ro_rsrc(c);
+    const int voff = 2 * (r * (int)ld_c + 8 * j);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const u32x2 t = __builtin_amdgcn_raw_buffer_load_b64(rc, voff, 2 * (128 * (i >> 1) + 4 * (i & 1)), 0);
+      cv[i] = uint2{t.x, t.y};
+    }
+  }
   const bool ok = ll_poll16<16>(
-      rs, w0, [](int i) { return 64 * (i >> 1) + 2 * (i & 1); }, [&](int) { return live; }, tag,
+      sm, vph, rs, w0, [](int i) { return 64 * (i >> 1) + 2 * (i & 1); }, [&](int) { return live; }, tag,
       [&](int i, uint32_t p0, uint32_t p1) {
         const int col = 8 * (j + 16 * (i >> 1)) + 4 * (i & 1);
         uint16_t* xp = &sm.m.x[r][col];
         const uint16_t av[4] = {(uint16_t)(p0 & 0xffff), (uint16_t)(p0 >> 16), (uint16_t)(p1 & 0xffff),
                                 (uint16_t)(p1 >> 16)};
+        const uint16_t cc[4] = {(uint16_t)(cv[i].x & 0xffff), (uint16_t)(cv[i].x >> 16), (uint16_t)(cv[i].y & 0xffff),
+                                (uint16_t)(cv[i].y >> 16)};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           float t = rnd<DT>(E<DT>::to_f(xp[e]) + E<DT>::to_f(av[e]));
-          if (c) t = rnd<DT>(t + E<DT>::to_f(c[(long)r * ld_c + col + e]));
+          if (c) t = rnd<DT>(t + E<DT>::to_f(cc[e]));
           xp[e] = E<DT>::from_f(t);
         }
       });
@@ -293,11 +371,12 @@ __device__ __forceinline__ bool add_rows(Smem& sm, __amdgpu_buffer_rsrc_t rs, in
 // rows [RB][K] of an LL buffer into sm.act (rows >= B stay as they are): chunk c = tid + NT i holds columns
 // 4 (c % (K / 4)) .. + 3 of row c / (K / 4), at word 2 c
 template <int K>
-__device__ __forceinline__ bool stage_act(Smem& sm, __amdgpu_buffer_rsrc_t rs, int base, uint32_t tag, int B) {
+__device__ __forceinline__ bool stage_act(Smem& sm, int& vph, __amdgpu_buffer_rsrc_t rs, int base, uint32_t tag,
+                                          int B) {
   constexpr int CPR = K / 4, N = RB * CPR / NT;
   static_assert(RB * CPR % NT == 0, "chunks per thread");
   const bool ok = ll_poll16<N>(
-      rs, base + 2 * (int)threadIdx.x, [](int i) { return 2 * NT * i; },
+      sm, vph, rs, base + 2 * (int)threadIdx.x, [](int i) { return 2 * NT * i; },
       [&](int i) { return (int)(threadIdx.x + NT * i) / CPR < B; }, tag, [&](int i, uint32_t p0, uint32_t p1) {
         const int cc = threadIdx.x + NT * i;
         *reinterpret_cast<uint2*>(&sm.act[cc / CPR][4 * (cc % CPR)]) = uint2{p0, p1};
@@ -313,10 +392,11 @@ struct WTile {
 };
 template <int NF>
 __device__ __forceinline__ void load_tile(WTile<NF>& t, const uint16_t* w, int tile, int K) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const uint16_t* p = w + (long)tile * 16 * K + (long)wave * NF * 512 + 8 * lane;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const __amdgpu_buffer_rsrc_t r = ro_rsrc(w);
+  const int s0 = (tile * 16 * K + wave * NF * 512) * 2;  // uniform: scalar offset
 #pragma unroll
-  for (int f = 0; f < NF; ++f) t.f[f] = ld16(p + (long)f * 512);
+  for (int f = 0; f < NF; ++f) t.f[f] = bld16(r, 16 * lane, s0 + f * 1024);
 }
 // W tile x y^T, y the residual's norm in LDS
 template <int DT, int NF>
@@ -384,6 +464,25 @@ __device__ __forceinline__ void finish_tile(Smem& sm, f32x4_t acc, f32x4_t acc2,
   }
   __syncthreads();
 }
+// The draw of one seat's code from its head row (x = logits / temp as the launch path's sampler forms them, one
+// element i = tid + 256 e per thread): a separate function so that the selection's registers do not add to the
+// rest of the run's. Every thread calls it; the code is returned in every thread.
+__device__ __attribute__((noinline)) int draw_code(SampleSmemT<VMAX>& sp, int* code_slot, float x0, float x1,
+                                                   float x2, float x3, float x4, float x5, float x6, float x7,
+                                                   int top_k, int greedy, float u) {
+  const float xv[VMAX / NT] = {x0, x1, x2, x3, x4, x5, x6, x7};
+  topk_select<VMAX / NT>(xv, VMAX, top_k, sp);
+  if (threadIdx.x < 64) {
+    int code = cand_index(sp.cand[0]);
+    if (!greedy) {
+      const int cp = pick(sp, sp.nkeep, u, -1);
+      if (cp >= 0) code = cp;
+    }
+    if (threadIdx.x == 0) *code_slot = code;
+  }
+  __syncthreads();
+  return *code_slot;
+}
 }  // namespace dk
 
 using namespace dk;
@@ -409,6 +508,11 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
   const int steps_per_level = 5 * layers + 2;
   const float scale = 1.0f / sqrtf((float)HD);
   bool ok = true;
+  int vph = 0;  // wg_all's vote buffer
+  // stamp k of (level li, layer l): slot li * 64 + l * 12 + k; the level's head and sampler at li * 64 + 48 + k
+  auto stamp = [&](int slot) {
+    if (a.prof && tid == 0) a.prof[(long)wg * 2048 + slot] = __builtin_amdgcn_s_memrealtime();
+  };
 
   // ---- set-up: zeroed LDS rows, the residual at L0 from the prefix, the pair's K/V history
   if (xm) {
@@ -455,34 +559,39 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
       if (xm) {
         WTile<8> wt;
         load_tile<8>(wt, (const uint16_t*)a.wqkv[l], wg, DM);
+        NormW nw;
+        load_norm(nw, a.n1w[l], a.n1b[l], a.norm_kind);
         if (l == 0 && L > a.L0) {
           // the previous level's codes; this level's input rows are their prefix rows
           const uint32_t t_code = (epoch << 12) | (lvl_seq - 1);
           const int b_code = O_CODE + (1 - lpar) * W_CODE;
-          ok = ll_poll8<1>(rs, b_code + tid, [](int) { return 0; }, [&](int) { return tid < B; }, t_code,
+          ok = ll_poll8<1>(sm, vph, rs, b_code + tid, [](int) { return 0; }, [&](int) { return tid < B; }, t_code,
                            [&](int, uint32_t p) { sm.codes[tid] = (int)p; });
+          stamp(li * 64 + 52);
           __syncthreads();
-          const uint16_t* emb = (const uint16_t*)a.embed + (long)(L - 1) * a.V * DM;
+          const __amdgpu_buffer_rsrc_t re = ro_rsrc((const uint16_t*)a.embed + (long)(L - 1) * a.V * DM);
           for (int i = tid; i < B * DM / 8; i += NT) {
             const int r = i / (DM / 8), c = 8 * (i % (DM / 8));
-            const long code = min(max(sm.codes[r], 0), a.V - 1);
-            *reinterpret_cast<u16x8*>(&sm.m.x[r][c]) = ld16(emb + code * DM + c);
+            const int code = min(max(sm.codes[r], 0), a.V - 1);
+            *reinterpret_cast<u16x8*>(&sm.m.x[r][c]) = bld16(re, 2 * (code * DM + c), 0);
           }
           __syncthreads();
         } else if (l > 0) {
           const int b_prev = O_DN + ((li * layers + l - 1) & 1) * W_ATT;
           const uint16_t* c = a.cross ? (const uint16_t*)a.cross + (long)(l - 1) * DM : nullptr;
-          ok = add_rows<DT>(sm, rs, b_prev, t_qkv - 1, B, c, a.ld_cross);
+          ok = add_rows<DT>(sm, vph, rs, b_prev, t_qkv - 1, B, c, a.ld_cross);
         }
-        norm_rows<DT>(sm, B, a.norm_kind, (const uint16_t*)a.n1w[l], (const uint16_t*)a.n1b[l], a.eps1[l]);
+        stamp(li * 64 + l * 12 + 0);
+        norm_rows<DT>(sm, B, a.norm_kind, nw, a.eps1[l]);
         if (ok) finish_tile<DT, 0>(sm, mma_y<DT, 8>(wt, sm), f32x4_t{}, rs, b_qkv, 3 * DM, wg, t_qkv, B, nullptr, 0);
+        stamp(li * 64 + l * 12 + 1);
       }
       // ---- step 2: attention of this workgroup's (seat, head) at position L over the group's keys 0..L
       if (ok && has_pair) {
         constexpr int per = HD / 4;  // 16-byte chunks of each of q, k and v of one head
         const int part = tid / per, c = tid % per;
         const int w0 = b_qkv + pb * (3 * DM / 2) + (part * DM + ph * HD) / 2 + 2 * c;
-        ok = ll_poll16<1>(rs, w0, [](int) { return 0; }, [&](int) { return tid < 3 * per; }, t_qkv,
+        ok = ll_poll16<1>(sm, vph, rs, w0, [](int) { return 0; }, [&](int) { return tid < 3 * per; }, t_qkv,
                           [&](int, uint32_t p0, uint32_t p1) {
                             const uint16_t v4[4] = {(uint16_t)(p0 & 0xffff), (uint16_t)(p0 >> 16),
                                                     (uint16_t)(p1 & 0xffff), (uint16_t)(p1 >> 16)};
@@ -494,6 +603,7 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
                               for (int e = 0; e < 4; ++e) sm.m.kv[l][part - 1][L][4 * c + e] = v4[e];
                             }
                           });
+        stamp(li * 64 + l * 12 + 2);
         if (wave == 0) {
           // lane j <= L: the score of key j
           float sj = -INFINITY;
@@ -528,13 +638,16 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
                   t_att);
         }
         __syncthreads();
+        stamp(li * 64 + l * 12 + 3);
       }
       // ---- step 3: o projection of the attention rows
       if (ok && do_od) {
         WTile<8> wt;
         load_tile<8>(wt, (const uint16_t*)a.wo[l], u_od, DM);
-        ok = stage_act<DM>(sm, rs, b_att, t_att, B);
+        ok = stage_act<DM>(sm, vph, rs, b_att, t_att, B);
+        stamp(li * 64 + l * 12 + 4);
         if (ok) finish_tile<DT, 0>(sm, mma_act<DT, 8>(wt, sm), f32x4_t{}, rs, b_o, DM, u_od, t_o, B, nullptr, 0);
+        stamp(li * 64 + l * 12 + 5);
       }
       // ---- step 4: x += o -> norm -> gate|up with the activation
       if (ok && xm) {
@@ -543,8 +656,11 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
           load_tile<8>(wg_, (const uint16_t*)a.wg[l], wg, DM);
           if constexpr (ACT == 1) load_tile<8>(wu_, (const uint16_t*)a.wu[l], wg, DM);
         }
-        ok = add_rows<DT>(sm, rs, b_o, t_o, B, nullptr, 0);
-        norm_rows<DT>(sm, B, a.norm_kind, (const uint16_t*)a.n2w[l], (const uint16_t*)a.n2b[l], a.eps2[l]);
+        NormW nw;
+        load_norm(nw, a.n2w[l], a.n2b[l], a.norm_kind);
+        ok = add_rows<DT>(sm, vph, rs, b_o, t_o, B, nullptr, 0);
+        stamp(li * 64 + l * 12 + 6);
+        norm_rows<DT>(sm, B, a.norm_kind, nw, a.eps2[l]);
         if (ok && do_gu) {
           if constexpr (ACT == 1)
             finish_tile<DT, 1>(sm, mma_y<DT, 8>(wg_, sm), mma_y<DT, 8>(wu_, sm), rs, b_gu, a.F, wg, t_gu, B, nullptr,
@@ -552,6 +668,7 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
           else
             finish_tile<DT, 2>(sm, mma_y<DT, 8>(wg_, sm), f32x4_t{}, rs, b_gu, a.F, wg, t_gu, B, nullptr, 0);
         }
+        stamp(li * 64 + l * 12 + 7);
       }
       // ---- step 5: down projection of the activation (staged in LDS)
       if (ok && do_od) {
@@ -559,15 +676,17 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
         if constexpr (ACT == 1) {
           WTile<22> wt;
           load_tile<22>(wt, (const uint16_t*)a.wd[l], u_od, 2816);
-          ok = stage_act<2816>(sm, rs, b_gu, t_gu, B);
+          ok = stage_act<2816>(sm, vph, rs, b_gu, t_gu, B);
+          stamp(li * 64 + l * 12 + 8);
           acc = mma_act<DT, 22>(wt, sm);
         } else {
           WTile<24> wt;
           load_tile<24>(wt, (const uint16_t*)a.wd[l], u_od, 3072);
-          ok = stage_act<3072>(sm, rs, b_gu, t_gu, B);
+          ok = stage_act<3072>(sm, vph, rs, b_gu, t_gu, B);
           acc = mma_act<DT, 24>(wt, sm);
         }
         if (ok) finish_tile<DT, 0>(sm, acc, f32x4_t{}, rs, b_dn, DM, u_od, t_dn, B, nullptr, 0);
+        stamp(li * 64 + l * 12 + 9);
       }
     }
     if (!ok) break;
@@ -577,14 +696,18 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
     if (xm) {
       WTile<8> wt;
       if (do_head) load_tile<8>(wt, (const uint16_t*)a.heads[L - 1], wg, DM);
+      NormW nw;
+      load_norm(nw, a.fw, a.fb, a.norm_kind);
       const int b_prev = O_DN + ((li * layers + layers - 1) & 1) * W_ATT;
       const uint16_t* c = a.cross ? (const uint16_t*)a.cross + (long)(layers - 1) * DM : nullptr;
-      ok = add_rows<DT>(sm, rs, b_prev, t_log - 1, B, c, a.ld_cross);
-      norm_rows<DT>(sm, B, a.norm_kind, (const uint16_t*)a.fw, (const uint16_t*)a.fb, a.eps_f);
+      ok = add_rows<DT>(sm, vph, rs, b_prev, t_log - 1, B, c, a.ld_cross);
+      stamp(li * 64 + 48);
+      norm_rows<DT>(sm, B, a.norm_kind, nw, a.eps_f);
       if (ok && do_head) {
         uint16_t* dbg = a.logits_out ? (uint16_t*)a.logits_out + (long)(L - 1) * B * a.V : nullptr;
         finish_tile<DT, 0>(sm, mma_y<DT, 8>(wt, sm), f32x4_t{}, rs, b_log, a.V, wg, t_log, B, dbg, a.V);
       }
+      stamp(li * 64 + 49);
     }
     // ---- sampling of seat wg's code (the launch path's sampler, on the LL copy of the head row)
     if (ok && wg < B) {
@@ -592,30 +715,24 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
       constexpr int NE = VMAX / NT;
       const float ur = a.greedy ? 0.f : a.u[(long)r * a.ld_u + L - 1];
       float xv[NE];
-      ok = ll_poll8<NE>(rs, b_log + r * (VMAX / 2) + tid / 2, [](int e) { return NT / 2 * e; },
+      ok = ll_poll8<NE>(sm, vph, rs, b_log + r * (VMAX / 2) + tid / 2, [](int e) { return NT / 2 * e; },
                         [&](int) { return true; }, t_log, [&](int e, uint32_t p) {
                           const uint16_t h16 = (uint16_t)((tid & 1) ? (p >> 16) : (p & 0xffff));
                           xv[e] = E<DT>::to_f(h16) * a.inv_temp;
                         });
-      topk_select<NE>(xv, VMAX, a.top_k, sm.m.u.smp);
-      if (tid < 64) {
-        int code = cand_index(sm.m.u.smp.cand[0]);
-        if (!a.greedy) {
-          const int cp = pick(sm.m.u.smp, sm.m.u.smp.nkeep, ur, -1);
-          if (cp >= 0) code = cp;
-        }
-        if (tid == 0) {
-          sm.codes[0] = code;
-          a.codes[(long)r * a.ld_codes + L] = code;
-          ll_st8(rs, b_code + r, (uint32_t)code, t_code);
-        }
+      stamp(li * 64 + 50);
+      const int code = draw_code(sm.m.u.smp, &sm.codes[0], xv[0], xv[1], xv[2], xv[3], xv[4], xv[5],
+                                 xv[6], xv[7], a.top_k, a.greedy, ur);
+      if (tid == 0) {
+        a.codes[(long)r * a.ld_codes + L] = code;
+        ll_st8(rs, b_code + r, (uint32_t)code, t_code);
       }
-      __syncthreads();
+      stamp(li * 64 + 51);
       if (L + 1 < NPOS && tid < DM / 8) {
         // the next prefix row, for a later group start that recomputes the whole prefix
-        const long code = min(max(sm.codes[0], 0), VMAX - 1);
+        const long cc = min(max(code, 0), VMAX - 1);
         st16((uint16_t*)a.prefix + (long)r * a.ld_prefix + (long)(L + 1) * DM + 8 * tid,
-             ld16((const uint16_t*)a.embed + ((long)L * VMAX + code) * DM + 8 * tid));
+             ld16((const uint16_t*)a.embed + ((long)L * VMAX + cc) * DM + 8 * tid));
       }
       __syncthreads();
     }
