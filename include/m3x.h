@@ -326,7 +326,8 @@ int m3x_final_conv(const void* x, long ld_x, void* state, long ld_state, const i
  * M3X_ACT_SWIGLU, F 2816), 64 (GELU, act M3X_ACT_GELU, F 3072)}, `layers` <= 4 layers, codebooks of 2048 codes.
  * Weights are packed (m3x_pack_weight): per layer q|k|v [3*1024, 1024], o [1024, 1024], gate (or f1) [F, 1024],
  * up [F, 1024] (SwiGLU only), down [1024, F]; heads[L-1] [2048, 1024] for each level L of the run. Norms: kind
- * M3X_NORM_RMS (weights) or M3X_NORM_LAYER (weights and biases) with per-layer eps, and the final norm.
+ * M3X_NORM_RMS (weights) with SwiGLU, M3X_NORM_LAYER (weights and biases) with GELU (other pairings:
+ * M3X_EUNSUPPORTED), per-layer eps, and the final norm.
  * State: prefix[b * ld_prefix + p * 1024 ...] holds position L0's input row; the sampled code of level L goes to
  * codes[b * ld_codes + L] and, for L < 31, the next prefix row embed[L][code] to prefix position L + 1. kd/vd
  * [B][H][32][hd] per layer hold the group's K/V at positions < L0. u[b * ld_u + L - 1] is the uniform of level L.

@@ -117,9 +117,9 @@ __device__ __forceinline__ bool wg_all(Smem& sm, bool v, int& phase) {
   const bool any_false = __ballot(!v) != 0;
   if ((threadIdx.x & 63) == 0) sm.vote[phase][threadIdx.x >> 6] = any_false;
   __syncthreads();
-  const bool r = !(sm.vote[phase][0] | sm.vote[phase][1] | sm.vote[phase][2] | sm.vote[phase][3]);
+  const int r = !(sm.vote[phase][0] | sm.vote[phase][1] | sm.vote[phase][2] | sm.vote[phase][3]);
   phase ^= 1;
-  return r;
+  return __builtin_amdgcn_readfirstlane(r) != 0;
 }
 
 __device__ __forceinline__ u32x4 ll_ld16(__amdgpu_buffer_rsrc_t r, int word) {
@@ -146,241 +146,309 @@ __device__ __forceinline__ u16x8 bld16(__amdgpu_buffer_rsrc_t r, int voff_bytes,
   return __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff_bytes, soff_bytes, 0));
 }
 
-// Poll this thread's N 16-byte chunks (two words each) until both words of every live chunk carry `tag`, handing
-// each chunk's two payloads to sink(i, p0, p1) once. Chunk i sits at word base + U(i), base per thread and U(i) a
-// constant, so the loads take one address register and constant offsets. A chunk that is not being polled has its
-// load pushed past the end of the buffer, where it returns zeros without touching memory, so every load of a round
-// is issued before the first check and only in-flight loads occupy registers.
-// Rounds first poll each thread's chunk 0 alone (a probe: a few bytes per thread while the producers still run);
-// once every probe has its tag, a round reads every chunk still missing, and later rounds only the stragglers.
-// Workgroup-collective (every thread calls it); false after SPIN_LIMIT rounds.
-constexpr int OOB = 1 << 30;  // a byte offset past every exchange buffer
+// Polling. A consumer reads exactly the words it needs until each carries the step's tag. Each wave polls its own
+// threads' chunks, with no workgroup barrier per round; the workgroup meets once at the end (which also makes the
+// sinks' LDS writes visible). A compiler-only memory clobber in every polling round keeps identical polls from
+// being merged or hoisted out of the loop (the loads stay device-scope, sc1).
+constexpr int OOB = 1 << 30;  // a byte offset past every exchange buffer: such a load returns zeros, no traffic
+constexpr int VOL = SC1;
+#define M3X_POLL_CLOBBER() asm volatile("" ::: "memory")
+
+// One 16-byte chunk per lane (live lanes at byte offset `off`) until both words of every live lane of the wave
+// carry `tag` (a lane that has its chunk polls out of bounds). The chunk's value lands in `out`; false after
+// SPIN_LIMIT rounds.
+__device__ __forceinline__ bool wave_poll1(__amdgpu_buffer_rsrc_t r, int off, bool live, uint32_t tag, u32x4& out) {
+  bool got = !live;
+  for (unsigned it = 0; it < SPIN_LIMIT; ++it) {
+    M3X_POLL_CLOBBER();
+    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, got ? OOB : off, 0, VOL);
+    if (!got && a.y == tag && a.w == tag) {
+      out = a;
+      got = true;
+    }
+    if (__builtin_amdgcn_ballot_w64(!got) == 0) return true;
+  }
+  return false;
+}
+// the same for one 8-byte word per lane (payload in out.x)
+__device__ __forceinline__ bool wave_poll1w(__amdgpu_buffer_rsrc_t r, int off, bool live, uint32_t tag, u32x2& out) {
+  bool got = !live;
+  for (unsigned it = 0; it < SPIN_LIMIT; ++it) {
+    M3X_POLL_CLOBBER();
+    const u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(r, got ? OOB : off, 0, VOL);
+    if (!got && a.y == tag) {
+      out = a;
+      got = true;
+    }
+    if (__builtin_amdgcn_ballot_w64(!got) == 0) return true;
+  }
+  return false;
+}
+
+// This thread's chunks i < nit (16 bytes, two words each; nit uniform across the workgroup, at most N), handing
+// each live chunk's two payloads to sink(i, p0, p1) once. Chunk i sits at word base + U(i), base per thread and
+// U(i) a constant, so the loads take one address register and constant offsets. Chunk 0 is polled first (a probe:
+// one chunk per thread while the producers still run, which then mostly finds the rest already there); then rounds
+// read the chunks still missing, skipping chunks i >= nit by uniform branches and pushing arrived ones out of
+// bounds. Workgroup-collective (every thread calls it); false if any wave gave up after SPIN_LIMIT rounds.
 template <int N, class U, class Live, class Sink>
-__device__ __forceinline__ bool ll_poll16(Smem& sm, int& vph, __amdgpu_buffer_rsrc_t r, int base, U uoff, Live live,
-                                          uint32_t tag, Sink sink) {
+__device__ __forceinline__ bool ll_poll16(Smem& sm, int& vph, __amdgpu_buffer_rsrc_t r, int base, U uoff, int nit,
+                                          Live live, uint32_t tag, Sink sink) {
   static_assert(N <= 64, "chunks per thread");
   uint64_t pending = 0;
 #pragma unroll
   for (int i = 0; i < N; ++i)
-    if (live(i)) pending |= 1ull << i;
-  uint64_t active = pending & 1ull;
-  bool probing = N > 1;
-  if (!probing) active = pending;
-  for (unsigned it = 0;; ++it) {
-    u32x4 v[N];
-#pragma unroll
-    for (int i = 0; i < N; ++i)
-      v[i] = __builtin_amdgcn_raw_buffer_load_b128(r, base * 8 + (((active >> i) & 1) ? 0 : OOB), uoff(i) * 8, SC1);
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-      if (((active >> i) & 1) && v[i].y == tag && v[i].w == tag) {
-        sink(i, v[i].x, v[i].z);
-        pending &= ~(1ull << i);
-      }
+    if (i < nit && live(i)) pending |= 1ull << i;
+  bool ok = true;
+  if (nit > 0) {
+    const bool l0 = pending & 1ull;
+    u32x4 v0;
+    ok = wave_poll1(r, base * 8 + uoff(0) * 8, l0, tag, v0);
+    if (ok && l0) {
+      sink(0, v0.x, v0.z);
+      pending &= ~1ull;
     }
-    if (probing) {
-      active &= pending;
-      if (wg_all(sm, active == 0, vph)) {
-        probing = false;
-        active = pending;
-      }
-    } else {
-      active = pending;
-      if (wg_all(sm, pending == 0, vph)) return true;
-    }
-    if (it >= SPIN_LIMIT) return false;
   }
+  if constexpr (N > 1) {
+    for (unsigned it = 0; ok && nit > 1; ++it) {
+      if (__builtin_amdgcn_ballot_w64(pending != 0) == 0) break;
+      if (it >= SPIN_LIMIT) {
+        ok = false;
+        break;
+      }
+      M3X_POLL_CLOBBER();
+      u32x4 v[N];
+#pragma unroll
+      for (int i = 1; i < N; ++i)
+        if (i < nit)
+          v[i] = __builtin_amdgcn_raw_buffer_load_b128(r, base * 8 + (((pending >> i) & 1) ? 0 : OOB), uoff(i) * 8,
+                                                       VOL);
+#pragma unroll
+      for (int i = 1; i < N; ++i) {
+        if (i < nit && ((pending >> i) & 1) && v[i].y == tag && v[i].w == tag) {
+          sink(i, v[i].x, v[i].z);
+          pending &= ~(1ull << i);
+        }
+      }
+    }
+  }
+  return wg_all(sm, ok, vph);
 }
 
-// the same for N single words (8-byte loads); sink(i, payload)
+// the same for single words (8-byte loads); sink(i, payload)
 template <int N, class U, class Live, class Sink>
-__device__ __forceinline__ bool ll_poll8(Smem& sm, int& vph, __amdgpu_buffer_rsrc_t r, int base, U uoff, Live live,
-                                         uint32_t tag, Sink sink) {
+__device__ __forceinline__ bool ll_poll8(Smem& sm, int& vph, __amdgpu_buffer_rsrc_t r, int base, U uoff, int nit,
+                                         Live live, uint32_t tag, Sink sink) {
   static_assert(N <= 32, "words per thread");
   uint32_t pending = 0;
 #pragma unroll
   for (int i = 0; i < N; ++i)
-    if (live(i)) pending |= 1u << i;
-  uint32_t active = N > 1 ? (pending & 1u) : pending;
-  bool probing = N > 1;
-  for (unsigned it = 0;; ++it) {
-    u32x2 v[N];
-#pragma unroll
-    for (int i = 0; i < N; ++i)
-      v[i] = __builtin_amdgcn_raw_buffer_load_b64(r, base * 8 + (((active >> i) & 1) ? 0 : OOB), uoff(i) * 8, SC1);
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-      if (((active >> i) & 1) && v[i].y == tag) {
-        sink(i, v[i].x);
-        pending &= ~(1u << i);
-      }
+    if (i < nit && live(i)) pending |= 1u << i;
+  bool ok = true;
+  if (nit > 0) {
+    const bool l0 = pending & 1u;
+    u32x2 v0;
+    ok = wave_poll1w(r, base * 8 + uoff(0) * 8, l0, tag, v0);
+    if (ok && l0) {
+      sink(0, v0.x);
+      pending &= ~1u;
     }
-    if (probing) {
-      active &= pending;
-      if (wg_all(sm, active == 0, vph)) {
-        probing = false;
-        active = pending;
-      }
-    } else {
-      active = pending;
-      if (wg_all(sm, pending == 0, vph)) return true;
-    }
-    if (it >= SPIN_LIMIT) return false;
   }
+  if constexpr (N > 1) {
+    for (unsigned it = 0; ok && nit > 1; ++it) {
+      if (__builtin_amdgcn_ballot_w64(pending != 0) == 0) break;
+      if (it >= SPIN_LIMIT) {
+        ok = false;
+        break;
+      }
+      M3X_POLL_CLOBBER();
+      u32x2 v[N];
+#pragma unroll
+      for (int i = 1; i < N; ++i)
+        if (i < nit)
+          v[i] = __builtin_amdgcn_raw_buffer_load_b64(r, base * 8 + (((pending >> i) & 1) ? 0 : OOB), uoff(i) * 8,
+                                                      VOL);
+#pragma unroll
+      for (int i = 1; i < N; ++i) {
+        if (i < nit && ((pending >> i) & 1) && v[i].y == tag) {
+          sink(i, v[i].x);
+          pending &= ~(1u << i);
+        }
+      }
+    }
+  }
+  return wg_all(sm, ok, vph);
 }
 
 __device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) { return (uint32_t)lo | ((uint32_t)hi << 16); }
 
-// ---- norms of the resident stream: 16 threads per seat row, thread j of a row holds the 8-element groups
-// g = j + 16 i (i < 8); the partial sums fold as the add+norm kernels' tree (s = 64, 32, 16 inside the thread,
-// 8, 4, 2, 1 across the row's 16 lanes), so the rows are those kernels' bits.
-__device__ __forceinline__ float row16_fold(const float (&p)[8]) {
-  float q[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) q[i] = p[i];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) q[i] = q[i] + q[i + 4];  // s = 64
-#pragma unroll
-  for (int i = 0; i < 2; ++i) q[i] = q[i] + q[i + 2];  // s = 32
-  q[0] = q[0] + q[1];                                  // s = 16
-  const float v = fold_half_sum<16>(q[0]);             // s = 8, 4, 2, 1 across the row's lanes
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), DPP_ROW_NEWBCAST(0), 0xF,
-                                                             0xF, false));
+// ---- norms of the resident stream. A row's 1024 elements are 128 groups of 8 (group g = columns 8 g .. 8 g + 7);
+// the add+norm kernels sum each group left to right and fold the 128 partials in half (p[g] + p[g + s] for
+// s = 64, 32, ..., 1). Here a row has one wave: lane t holds the groups t and t + 64, folds them (s = 64), and
+// the wave folds the rest with fold_half_sum<64> (lane 0 ends with the tree's sum), so the rows are those kernels'
+// bits. Wave w takes the rows w, w + 4, ... below B, interleaved.
+__device__ __forceinline__ float row_fold(float p0, float p1) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, fold_half_sum<64>(p0 + p1))));
 }
+__device__ __forceinline__ int norm_group(int m) { return (threadIdx.x & 63) + 64 * m; }
 
-// the affine terms of a norm, as norm_rows' threads use them (loaded before a step waits for its input)
+// the affine terms of a norm, as norm_rows' threads use them (loaded before a step waits for its input; the kind
+// is a compile-time constant of the kernel, so an RMS norm holds no bias registers)
+template <int NK>
 struct NormW {
-  u16x8 w[8], b[8];
+  u16x8 w[2], b[NK == M3X_NORM_LAYER ? 2 : 1];
 };
-__device__ __forceinline__ void load_norm(NormW& n, const void* w, const void* b, int kind) {
-  const int voff = 16 * (threadIdx.x & 15);
+template <int NK>
+__device__ __forceinline__ void load_norm(NormW<NK>& n, const void* w, const void* b) {
   const __amdgpu_buffer_rsrc_t rw = ro_rsrc(w);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) n.w[i] = bld16(rw, voff, 256 * i);
-  if (kind == M3X_NORM_LAYER) {
+  for (int m = 0; m < 2; ++m) n.w[m] = bld16(rw, 16 * norm_group(m), 0);
+  if constexpr (NK == M3X_NORM_LAYER) {
     const __amdgpu_buffer_rsrc_t rb = ro_rsrc(b);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) n.b[i] = bld16(rb, voff, 256 * i);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) n.b[i] = u16x8{};
+    for (int m = 0; m < 2; ++m) n.b[m] = bld16(rb, 16 * norm_group(m), 0);
   }
 }
 
-// y[r] = norm(x[r]) for the rows r < B (x, y in LDS; the affine terms preloaded)
-template <int DT>
-__device__ __forceinline__ void norm_rows(Smem& sm, int B, int kind, const NormW& nw, float eps) {
-  const int r = threadIdx.x >> 4, j = threadIdx.x & 15;
-  float v[8][8];
+// y[r] = norm(x[r]) for the rows r < B (x, y in LDS; the affine terms preloaded): wave w takes rows w + 4 k, k < R
+template <int DT, int NK, int R>
+__device__ __forceinline__ void norm_rows_r(Smem& sm, int B, const NormW<NK>& nw, float eps) {
+  const int w = threadIdx.x >> 6, g0 = norm_group(0), g1 = norm_group(1);
+  float v[R][2][8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const u16x8 xv = *reinterpret_cast<const u16x8*>(&sm.m.x[r][8 * (j + 16 * i)]);
+  for (int k = 0; k < R; ++k) {
+    const u16x8 x0 = *reinterpret_cast<const u16x8*>(&sm.m.x[w + 4 * k][8 * g0]);
+    const u16x8 x1 = *reinterpret_cast<const u16x8*>(&sm.m.x[w + 4 * k][8 * g1]);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[i][e] = E<DT>::to_f(xv.v[e]);
+    for (int e = 0; e < 8; ++e) {
+      v[k][0][e] = E<DT>::to_f(x0.v[e]);
+      v[k][1][e] = E<DT>::to_f(x1.v[e]);
+    }
   }
-  float p[8];
-  if (kind == M3X_NORM_LAYER) {
+  float sc[R];  // LayerNorm: the standard deviation; RMSNorm: 1 / rms
+  if constexpr (NK == M3X_NORM_LAYER) {
+    float mean[R];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      p[i] = v[i][0];
+    for (int k = 0; k < R; ++k) {
+      float p[2];
 #pragma unroll
-      for (int e = 1; e < 8; ++e) p[i] = p[i] + v[i][e];
-    }
-    const float mean = row16_fold(p) / (float)DM;
+      for (int m = 0; m < 2; ++m) {
+        p[m] = v[k][m][0];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[i][e] = v[i][e] - mean;
-      p[i] = v[i][0] * v[i][0];
-#pragma unroll
-      for (int e = 1; e < 8; ++e) p[i] = p[i] + v[i][e] * v[i][e];
-    }
-    const float sd = sqrtf(row16_fold(p) / (float)DM + eps);
-    if (r < B) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int c = 8 * (j + 16 * i);
-        const u16x8 wv = nw.w[i], bv = nw.b[i];
-        u16x8 o;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o.v[e] = E<DT>::from_f(v[i][e] / sd * E<DT>::to_f(wv.v[e]) + E<DT>::to_f(bv.v[e]));
-        *reinterpret_cast<u16x8*>(&sm.m.u.y[r][c]) = o;
+        for (int e = 1; e < 8; ++e) p[m] = p[m] + v[k][m][e];
       }
+      mean[k] = row_fold(p[0], p[1]) / (float)DM;
+    }
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      float p[2];
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[k][m][e] = v[k][m][e] - mean[k];
+        p[m] = v[k][m][0] * v[k][m][0];
+#pragma unroll
+        for (int e = 1; e < 8; ++e) p[m] = p[m] + v[k][m][e] * v[k][m][e];
+      }
+      sc[k] = sqrtf(row_fold(p[0], p[1]) / (float)DM + eps);
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      p[i] = v[i][0] * v[i][0];
+    for (int k = 0; k < R; ++k) {
+      float p[2];
 #pragma unroll
-      for (int e = 1; e < 8; ++e) p[i] = p[i] + v[i][e] * v[i][e];
+      for (int m = 0; m < 2; ++m) {
+        p[m] = v[k][m][0] * v[k][m][0];
+#pragma unroll
+        for (int e = 1; e < 8; ++e) p[m] = p[m] + v[k][m][e] * v[k][m][e];
+      }
+      sc[k] = 1.0f / sqrtf(row_fold(p[0], p[1]) / (float)DM + eps);
     }
-    const float inv = 1.0f / sqrtf(row16_fold(p) / (float)DM + eps);
+  }
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const int r = w + 4 * k;
     if (r < B) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int c = 8 * (j + 16 * i);
-        const u16x8 wv = nw.w[i];
+      for (int m = 0; m < 2; ++m) {
         u16x8 o;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o.v[e] = E<DT>::from_f(rnd<DT>(v[i][e] * inv) * E<DT>::to_f(wv.v[e]));
-        *reinterpret_cast<u16x8*>(&sm.m.u.y[r][c]) = o;
+        for (int e = 0; e < 8; ++e) {
+          if constexpr (NK == M3X_NORM_LAYER)
+            o.v[e] = E<DT>::from_f(v[k][m][e] / sc[k] * E<DT>::to_f(nw.w[m].v[e]) + E<DT>::to_f(nw.b[m].v[e]));
+          else
+            o.v[e] = E<DT>::from_f(rnd<DT>(v[k][m][e] * sc[k]) * E<DT>::to_f(nw.w[m].v[e]));
+        }
+        *reinterpret_cast<u16x8*>(&sm.m.u.y[r][8 * (m ? g1 : g0)]) = o;
       }
     }
   }
   __syncthreads();
 }
+template <int DT, int NK>
+__device__ __forceinline__ void norm_rows(Smem& sm, int B, const NormW<NK>& nw, float eps) {
+  if (B <= 4) norm_rows_r<DT, NK, 1>(sm, B, nw, eps);
+  else if (B <= 8) norm_rows_r<DT, NK, 2>(sm, B, nw, eps);
+  else if (B <= 12) norm_rows_r<DT, NK, 3>(sm, B, nw, eps);
+  else norm_rows_r<DT, NK, 4>(sm, B, nw, eps);
+}
 
-// x[r] = dt(dt(x[r] + a[r]) + c[r]) for r < B with a from an LL buffer [RB][DM] (c optional, global [B][ld_c])
+// x[r] = dt(dt(x[r] + a[r]) + c[r]) for r < B with a from an LL buffer [RB][DM] (c optional, global [B][ld_c]):
+// thread t takes columns 4 t .. 4 t + 3 of every row, so a row is one 16-byte chunk per thread
 template <int DT>
 __device__ __forceinline__ bool add_rows(Smem& sm, int& vph, __amdgpu_buffer_rsrc_t rs, int base, uint32_t tag,
                                          int B, const uint16_t* c, long ld_c) {
-  const int r = threadIdx.x >> 4, j = threadIdx.x & 15;
-  // chunk i: columns 8 (j + 16 (i / 2)) + 4 (i % 2) .. + 3 of row r, at word r DM / 2 + col / 2
-  const int w0 = base + r * (DM / 2) + 4 * j;
-  const bool live = r < B;
-  uint2 cv[16];
-  if (c && live) {
+  const int t = threadIdx.x;
+  uint2 cv[RB];
+  if (c) {
     const __amdgpu_buffer_rsrc_t rc = ro_rsrc(c);
-    const int voff = 2 * (r * (int)ld_c + 8 * j);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const u32x2 t = __builtin_amdgcn_raw_buffer_load_b64(rc, voff, 2 * (128 * (i >> 1) + 4 * (i & 1)), 0);
-      cv[i] = uint2{t.x, t.y};
-    }
+    for (int i = 0; i < RB; ++i)
+      if (i < B) {
+        const u32x2 q = __builtin_amdgcn_raw_buffer_load_b64(rc, 8 * t, 2 * i * (int)ld_c, 0);
+        cv[i] = uint2{q.x, q.y};
+      }
   }
-  const bool ok = ll_poll16<16>(
-      sm, vph, rs, w0, [](int i) { return 64 * (i >> 1) + 2 * (i & 1); }, [&](int) { return live; }, tag,
+  const bool ok = ll_poll16<RB>(
+      sm, vph, rs, base + 2 * t, [](int i) { return i * (DM / 2); }, B, [](int) { return true; }, tag,
       [&](int i, uint32_t p0, uint32_t p1) {
-        const int col = 8 * (j + 16 * (i >> 1)) + 4 * (i & 1);
-        uint16_t* xp = &sm.m.x[r][col];
+        uint16_t* xp = &sm.m.x[i][4 * t];
         const uint16_t av[4] = {(uint16_t)(p0 & 0xffff), (uint16_t)(p0 >> 16), (uint16_t)(p1 & 0xffff),
                                 (uint16_t)(p1 >> 16)};
         const uint16_t cc[4] = {(uint16_t)(cv[i].x & 0xffff), (uint16_t)(cv[i].x >> 16), (uint16_t)(cv[i].y & 0xffff),
                                 (uint16_t)(cv[i].y >> 16)};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float t = rnd<DT>(E<DT>::to_f(xp[e]) + E<DT>::to_f(av[e]));
-          if (c) t = rnd<DT>(t + E<DT>::to_f(cc[e]));
-          xp[e] = E<DT>::from_f(t);
+          float v = rnd<DT>(E<DT>::to_f(xp[e]) + E<DT>::to_f(av[e]));
+          if (c) v = rnd<DT>(v + E<DT>::to_f(cc[e]));
+          xp[e] = E<DT>::from_f(v);
         }
       });
   __syncthreads();
   return ok;
 }
 
-// rows [RB][K] of an LL buffer into sm.act (rows >= B stay as they are): chunk c = tid + NT i holds columns
-// 4 (c % (K / 4)) .. + 3 of row c / (K / 4), at word 2 c
+// rows [RB][K] of an LL buffer into sm.act (rows >= B stay as they are), in two halves of RB / 2 rows so that at
+// most half the chunks are in flight beside the down tile's prefetched weights: chunk c = tid + NT i of half h
+// holds columns 4 (c % (K / 4)) .. + 3 of row h RB / 2 + c / (K / 4), at word 2 c of the half; a half's first
+// (its live rows) K / 4 chunks are live, and a half with no live row is skipped
 template <int K>
 __device__ __forceinline__ bool stage_act(Smem& sm, int& vph, __amdgpu_buffer_rsrc_t rs, int base, uint32_t tag,
                                           int B) {
-  constexpr int CPR = K / 4, N = RB * CPR / NT;
-  static_assert(RB * CPR % NT == 0, "chunks per thread");
-  const bool ok = ll_poll16<N>(
-      sm, vph, rs, base + 2 * (int)threadIdx.x, [](int i) { return 2 * NT * i; },
-      [&](int i) { return (int)(threadIdx.x + NT * i) / CPR < B; }, tag, [&](int i, uint32_t p0, uint32_t p1) {
-        const int cc = threadIdx.x + NT * i;
-        *reinterpret_cast<uint2*>(&sm.act[cc / CPR][4 * (cc % CPR)]) = uint2{p0, p1};
-      });
+  constexpr int CPR = K / 4, HR = RB / 2, N = HR * CPR / NT;
+  static_assert(HR * CPR % NT == 0, "chunks per thread");
+  bool ok = true;
+  for (int h = 0; h < 2 && ok; ++h) {
+    const int rows = min(max(B - h * HR, 0), HR), nlive = rows * CPR;
+    if (rows == 0) break;
+    ok = ll_poll16<N>(
+        sm, vph, rs, base + h * HR * CPR * 2 + 2 * (int)threadIdx.x, [](int i) { return 2 * NT * i; },
+        (nlive + NT - 1) / NT, [&](int i) { return (int)threadIdx.x + NT * i < nlive; }, tag,
+        [&](int i, uint32_t p0, uint32_t p1) {
+          const int cc = threadIdx.x + NT * i;
+          *reinterpret_cast<uint2*>(&sm.act[h * HR + cc / CPR][4 * (cc % CPR)]) = uint2{p0, p1};
+        });
+  }
   __syncthreads();
   return ok;
 }
@@ -490,6 +558,8 @@ using namespace dk;
 template <int DT, int ACT, int HD>
 __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
   __shared__ Smem sm;
+  // the norm kind goes with the activation: RMSNorm in the SwiGLU trunks, LayerNorm in the GELU ones
+  constexpr int NK = ACT == 1 ? M3X_NORM_RMS : M3X_NORM_LAYER;
   const int wg = blockIdx.x, tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int B = a.B, H = a.H, layers = a.layers;
@@ -559,13 +629,13 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
       if (xm) {
         WTile<8> wt;
         load_tile<8>(wt, (const uint16_t*)a.wqkv[l], wg, DM);
-        NormW nw;
-        load_norm(nw, a.n1w[l], a.n1b[l], a.norm_kind);
+        NormW<NK> nw;
+        load_norm<NK>(nw, a.n1w[l], a.n1b[l]);
         if (l == 0 && L > a.L0) {
           // the previous level's codes; this level's input rows are their prefix rows
           const uint32_t t_code = (epoch << 12) | (lvl_seq - 1);
           const int b_code = O_CODE + (1 - lpar) * W_CODE;
-          ok = ll_poll8<1>(sm, vph, rs, b_code + tid, [](int) { return 0; }, [&](int) { return tid < B; }, t_code,
+          ok = ll_poll8<1>(sm, vph, rs, b_code + tid, [](int) { return 0; }, 1, [&](int) { return tid < B; }, t_code,
                            [&](int, uint32_t p) { sm.codes[tid] = (int)p; });
           stamp(li * 64 + 52);
           __syncthreads();
@@ -582,7 +652,8 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
           ok = add_rows<DT>(sm, vph, rs, b_prev, t_qkv - 1, B, c, a.ld_cross);
         }
         stamp(li * 64 + l * 12 + 0);
-        norm_rows<DT>(sm, B, a.norm_kind, nw, a.eps1[l]);
+        norm_rows<DT, NK>(sm, B, nw, a.eps1[l]);
+        stamp(li * 64 + l * 12 + 10);
         if (ok) finish_tile<DT, 0>(sm, mma_y<DT, 8>(wt, sm), f32x4_t{}, rs, b_qkv, 3 * DM, wg, t_qkv, B, nullptr, 0);
         stamp(li * 64 + l * 12 + 1);
       }
@@ -591,7 +662,7 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
         constexpr int per = HD / 4;  // 16-byte chunks of each of q, k and v of one head
         const int part = tid / per, c = tid % per;
         const int w0 = b_qkv + pb * (3 * DM / 2) + (part * DM + ph * HD) / 2 + 2 * c;
-        ok = ll_poll16<1>(sm, vph, rs, w0, [](int) { return 0; }, [&](int) { return tid < 3 * per; }, t_qkv,
+        ok = ll_poll16<1>(sm, vph, rs, w0, [](int) { return 0; }, 1, [&](int) { return tid < 3 * per; }, t_qkv,
                           [&](int, uint32_t p0, uint32_t p1) {
                             const uint16_t v4[4] = {(uint16_t)(p0 & 0xffff), (uint16_t)(p0 >> 16),
                                                     (uint16_t)(p1 & 0xffff), (uint16_t)(p1 >> 16)};
@@ -604,40 +675,67 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
                             }
                           });
         stamp(li * 64 + l * 12 + 2);
-        if (wave == 0) {
-          // lane j <= L: the score of key j
-          float sj = -INFINITY;
-          if (lane <= L) {
-            float d = 0.f;
-            for (int cc = 0; cc < HD; cc += 8) {
-              const u16x8 k8 = *reinterpret_cast<const u16x8*>(&sm.m.kv[l][0][lane][cc]);
+        // scores: thread t takes key j = t / 8 and dims (t % 8) HD / 8 .. + HD / 8 - 1, summed over the 8 lanes
+        {
+          constexpr int DS = HD / 8;
+          const int j = tid >> 3, s8 = tid & 7;
+          float d = 0.f;
+          if (j <= L) {
 #pragma unroll
-              for (int e = 0; e < 8; ++e) d = fmaf(sm.qv[cc + e], E<DT>::to_f(k8.v[e]), d);
+            for (int g = 0; g < DS / 8; ++g) {
+              const u16x8 k8 = *reinterpret_cast<const u16x8*>(&sm.m.kv[l][0][j][s8 * DS + 8 * g]);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) d = fmaf(sm.qv[s8 * DS + 8 * g + e], E<DT>::to_f(k8.v[e]), d);
             }
-            sj = d * scale;
           }
+          d += __shfl_xor(d, 1, 64);
+          d += __shfl_xor(d, 2, 64);
+          d += __shfl_xor(d, 4, 64);
+          if (s8 == 0) sm.pr[j] = j <= L ? d * scale : -INFINITY;
+        }
+        __syncthreads();
+        {
+          // the softmax's max and sum, in every wave (lane j < NPOS holds key j's score)
+          const float sj = lane < NPOS ? sm.pr[lane] : -INFINITY;
           float m = sj;
           for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-          const float e = lane <= L ? expf(sj - m) : 0.f;
-          float sum = e;
+          float sum = lane <= L ? expf(sj - m) : 0.f;
           for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
-          if (lane < NPOS) sm.pr[lane] = e / sum;
-        }
-        __syncthreads();
-        if (tid < HD / 4) {
-          // thread t: output dims 4t .. 4t + 3
+          // P V: thread t takes dims 4 (t % DG) .. + 3 over the keys j = t / DG + PG i, then the PG partial
+          // rows are summed, first across the lanes of a wave, then across the four waves
+          constexpr int DG = HD / 4, PG = NT / DG;
+          const int dg = tid % DG;
           float o4[4] = {0.f, 0.f, 0.f, 0.f};
-          for (int j = 0; j <= L; ++j) {
-            const float pj = sm.pr[j];
-            const uint16_t* vr = &sm.m.kv[l][1][j][4 * tid];
+          for (int j = tid / DG; j <= L; j += PG) {
+            const float pj = expf(sm.pr[j] - m) / sum;
+            const uint2 vv = *reinterpret_cast<const uint2*>(&sm.m.kv[l][1][j][4 * dg]);
+            const uint16_t v4[4] = {(uint16_t)(vv.x & 0xffff), (uint16_t)(vv.x >> 16), (uint16_t)(vv.y & 0xffff),
+                                    (uint16_t)(vv.y >> 16)};
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o4[e] = fmaf(pj, E<DT>::to_f(vr[e]), o4[e]);
+            for (int e = 0; e < 4; ++e) o4[e] = fmaf(pj, E<DT>::to_f(v4[e]), o4[e]);
           }
-          ll_st16(rs, b_att + pb * (DM / 2) + (ph * HD + 4 * tid) / 2,
-                  pack2(E<DT>::from_f(o4[0]), E<DT>::from_f(o4[1])), pack2(E<DT>::from_f(o4[2]), E<DT>::from_f(o4[3])),
-                  t_att);
+#pragma unroll
+          for (int o = DG; o < 64; o <<= 1)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o4[e] += __shfl_xor(o4[e], o, 64);
+          if (lane < DG) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sm.part[0][wave][4 * lane + e] = o4[e];
+          }
+          __syncthreads();
+          if (tid < DG) {
+            float r4[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int i = 4 * tid + e;
+              r4[e] = ((sm.part[0][0][i] + sm.part[0][1][i]) + sm.part[0][2][i]) + sm.part[0][3][i];
+            }
+            ll_st16(rs, b_att + pb * (DM / 2) + (ph * HD + 4 * tid) / 2,
+                    pack2(E<DT>::from_f(r4[0]), E<DT>::from_f(r4[1])),
+                    pack2(E<DT>::from_f(r4[2]), E<DT>::from_f(r4[3])), t_att);
+          }
+          __syncthreads();
         }
-        __syncthreads();
         stamp(li * 64 + l * 12 + 3);
       }
       // ---- step 3: o projection of the attention rows
@@ -656,11 +754,12 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
           load_tile<8>(wg_, (const uint16_t*)a.wg[l], wg, DM);
           if constexpr (ACT == 1) load_tile<8>(wu_, (const uint16_t*)a.wu[l], wg, DM);
         }
-        NormW nw;
-        load_norm(nw, a.n2w[l], a.n2b[l], a.norm_kind);
+        NormW<NK> nw;
+        load_norm<NK>(nw, a.n2w[l], a.n2b[l]);
         ok = add_rows<DT>(sm, vph, rs, b_o, t_o, B, nullptr, 0);
         stamp(li * 64 + l * 12 + 6);
-        norm_rows<DT>(sm, B, a.norm_kind, nw, a.eps2[l]);
+        norm_rows<DT, NK>(sm, B, nw, a.eps2[l]);
+        stamp(li * 64 + l * 12 + 11);
         if (ok && do_gu) {
           if constexpr (ACT == 1)
             finish_tile<DT, 1>(sm, mma_y<DT, 8>(wg_, sm), mma_y<DT, 8>(wu_, sm), rs, b_gu, a.F, wg, t_gu, B, nullptr,
@@ -696,13 +795,13 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
     if (xm) {
       WTile<8> wt;
       if (do_head) load_tile<8>(wt, (const uint16_t*)a.heads[L - 1], wg, DM);
-      NormW nw;
-      load_norm(nw, a.fw, a.fb, a.norm_kind);
+      NormW<NK> nw;
+      load_norm<NK>(nw, a.fw, a.fb);
       const int b_prev = O_DN + ((li * layers + layers - 1) & 1) * W_ATT;
       const uint16_t* c = a.cross ? (const uint16_t*)a.cross + (long)(layers - 1) * DM : nullptr;
       ok = add_rows<DT>(sm, vph, rs, b_prev, t_log - 1, B, c, a.ld_cross);
       stamp(li * 64 + 48);
-      norm_rows<DT>(sm, B, a.norm_kind, nw, a.eps_f);
+      norm_rows<DT, NK>(sm, B, nw, a.eps_f);
       if (ok && do_head) {
         uint16_t* dbg = a.logits_out ? (uint16_t*)a.logits_out + (long)(L - 1) * B * a.V : nullptr;
         finish_tile<DT, 0>(sm, mma_y<DT, 8>(wt, sm), f32x4_t{}, rs, b_log, a.V, wg, t_log, B, dbg, a.V);
@@ -715,7 +814,7 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
       constexpr int NE = VMAX / NT;
       const float ur = a.greedy ? 0.f : a.u[(long)r * a.ld_u + L - 1];
       float xv[NE];
-      ok = ll_poll8<NE>(sm, vph, rs, b_log + r * (VMAX / 2) + tid / 2, [](int e) { return NT / 2 * e; },
+      ok = ll_poll8<NE>(sm, vph, rs, b_log + r * (VMAX / 2) + tid / 2, [](int e) { return NT / 2 * e; }, NE,
                         [&](int) { return true; }, t_log, [&](int e, uint32_t p) {
                           const uint16_t h16 = (uint16_t)((tid & 1) ? (p >> 16) : (p & 0xffff));
                           xv[e] = E<DT>::to_f(h16) * a.inv_temp;
@@ -759,7 +858,9 @@ M3X_API int m3x_depth_run(const M3xDepthRun* args, void* stream) {
   if (a.B <= 0 || a.B > RB || a.L0 < 2 || a.L1 > NPOS || a.L0 >= a.L1 || a.layers <= 0 || a.layers > MAXL)
     return M3X_EINVAL;
   if (a.H * a.hd != DM || (a.hd != 64 && a.hd != 128) || a.V != VMAX || a.top_k <= 0) return M3X_EUNSUPPORTED;
-  if (!((a.act == 0 && a.F == 2816) || (a.act == 1 && a.F == 3072))) return M3X_EUNSUPPORTED;
+  if (!((a.act == 0 && a.F == 2816 && a.norm_kind == M3X_NORM_RMS) ||
+        (a.act == 1 && a.F == 3072 && a.norm_kind == M3X_NORM_LAYER)))
+    return M3X_EUNSUPPORTED;
   if (a.nwg != NXM + NOD || a.B * a.H > NXM) return M3X_EINVAL;
   if (!a.xchg || !a.sync || !a.embed || !a.prefix || !a.codes || (!a.greedy && !a.u) || !a.fw) return M3X_ENULL;
   if (a.norm_kind == M3X_NORM_LAYER && !a.fb) return M3X_ENULL;

@@ -260,21 +260,24 @@ class FastDepth:
         return b.codes, b.feedback
 
     # ---------------------------------------------------------------- persistent run
-    PERSISTENT_SEATS = 16
+    # The kernel takes up to 16 seats; past 8 its handovers (every residual workgroup reads the whole rows of each
+    # step's output) cost more than the launch path's kernels on MI355X, so larger batches take the launch path.
+    PERSISTENT_SEATS = 8
 
     def _persistent_ok(self, B, group):
-        """Whether levels continuing `group` run as one persistent kernel for B seats: at most 16 seats and one
-        (seat, head) pair per residual workgroup, one workgroup per CU on a 256-CU part, the trunk geometries the
+        """Whether levels continuing `group` run as one persistent kernel for B seats: at most PERSISTENT_SEATS and
+        one (seat, head) pair per residual workgroup, one workgroup per CU on a 256-CU part, the trunk geometries the
         kernel implements (width 1024, 2048 codes, SwiGLU 2816 with 128-wide heads or GELU 3072 with 64-wide
-        heads, one norm kind) in bf16 or fp16."""
+        heads; RMSNorm with SwiGLU, LayerNorm with GELU) in bf16 or fp16."""
         if not self.persistent or B > self.PERSISTENT_SEATS or B * self.H > 192 or self._nwg != 256:
             return False
         layers = self.trunks[group]
         kinds = {L.n1.kind for L in layers} | {L.n2.kind for L in layers} | {self.final_norm.kind}
         geo = {(L.act, L.ffn) for L in layers}
-        return (self.D == 1024 and self.n_codes == 2048 and len(layers) <= 4 and len(kinds) == 1 and len(geo) == 1
+        swiglu = layers[0].act == ops.ACT_SWIGLU
+        return (self.D == 1024 and self.n_codes == 2048 and len(layers) <= 4 and len(geo) == 1
                 and geo.pop() in ((ops.ACT_SWIGLU, 2816), (ops.ACT_GELU, 3072))
-                and self.hd == (128 if layers[0].act == ops.ACT_SWIGLU else 64))
+                and kinds == {ops.NORM_RMS if swiglu else ops.NORM_LAYER} and self.hd == (128 if swiglu else 64))
 
     def _run_args(self, b, L0, L1, group):
         """The persistent run's arguments for buffer set b and levels L0 .. L1-1 (built once; the pointers are

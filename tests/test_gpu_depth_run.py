@@ -51,6 +51,7 @@ def test_swiglu_run_matches_oracle_and_launch_path(gpu, B):
     model_g = synth.swiglu_depth(seed=611, device=gpu)
     model_c = synth.swiglu_depth(seed=611, device="cpu")
     fd = FastDepth(model_g, 20, dtype=torch.bfloat16, temp=0.9, top_k=50, batch_buckets=(B,))
+    fd.PERSISTENT_SEATS = 16  # the kernel's own limit (serving switches to the launch path above 8 seats)
     fd.row_seed.copy_(torch.arange(21, dtype=torch.int32, device=gpu) * 7777 + 3)
     g = torch.Generator().manual_seed(612 + B)
     h = torch.randn(B, 1024, generator=g).to(torch.bfloat16)
