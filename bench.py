@@ -437,6 +437,26 @@ def _traffic_ratio():
     return None
 
 
+def b1_latency(torch, replays, bb=None, dm=None):
+    """Median latency (us) of the frame graph at one seat (KV length 2048), over `replays` replays."""
+    log("B=1 frame latency (length 2048)")
+    stream = torch.cuda.current_stream()
+    fs1, _, _ = build_frame(torch, 1, torch.tensor([2048]), seed_base=1, backbone=bb, depth_model=dm)
+    g1 = fs1.capture(1, CAP)
+    fs1.set_slots(g1, [0])
+    for _ in range(5):
+        fs1.replay(g1)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(replays)]
+    for a, b in ev:
+        a.record(stream)
+        fs1.replay(g1)
+        b.record(stream)
+    torch.cuda.synchronize()
+    lat = sorted(a.elapsed_time(b) * 1e3 for a, b in ev)
+    log(f"B=1: median {lat[len(lat) // 2]:.0f} us over {len(lat)} replays")
+    return lat[len(lat) // 2]
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -452,6 +472,7 @@ def main():
     ap.add_argument("--no-secondary", action="store_true", help="skip the C3 / C4 backbone-step lines")
     ap.add_argument("--secondary-steps", type=int, default=5)
     ap.add_argument("--mimi-only", action="store_true", help="print only the Mimi decode line (for profiling)")
+    ap.add_argument("--b1-only", action="store_true", help="print only the B=1 frame latency (for profiling)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -470,6 +491,10 @@ def main():
     B = args.batch
     K, W = args.steps, args.warmup
     dev = torch.device("cuda:0")
+    if args.b1_only:
+        with torch.inference_mode():
+            print(json.dumps({"b1_frame_us": round(b1_latency(torch, args.b1_replays), 1)}), flush=True)
+        return
     log(f"device {torch.cuda.get_device_name(0)}; building the B={B} frame (KV {B + 1} slots x {CAP})")
     lengths = synth.c5_lengths(B)
     if int(lengths.max()) + W + K + 1 > CAP:
@@ -570,23 +595,7 @@ def main():
 
         b1_us = None
         if not args.no_b1:
-            log("B=1 frame latency (length 2048)")
-            fs1, _, _ = build_frame(torch, 1, torch.tensor([2048]), seed_base=1, backbone=bb, depth_model=dm)
-            g1 = fs1.capture(1, CAP)
-            fs1.set_slots(g1, [0])
-            for _ in range(5):
-                fs1.replay(g1)
-            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                  for _ in range(args.b1_replays)]
-            for a, b in ev:
-                a.record(stream)
-                fs1.replay(g1)
-                b.record(stream)
-            torch.cuda.synchronize()
-            lat = sorted(a.elapsed_time(b) * 1e3 for a, b in ev)
-            b1_us = lat[len(lat) // 2]
-            log(f"B=1: median {b1_us:.0f} us over {len(lat)} replays")
-            del fs1, g1
+            b1_us = b1_latency(torch, args.b1_replays, bb, dm)
         sec = None
         if not args.no_secondary:
             sec = secondary(torch, bb, dm, args.secondary_steps)

@@ -335,7 +335,8 @@ int m3x_final_conv(const void* x, long ld_x, void* state, long ld_state, const i
  * sync: 4 int32, zeroed before the first run (the kernel keeps an epoch in [0], a counter in [1] and sets [2]
  * to 1 if a step's input never arrived, in which case the run's outputs are void). nwg must equal 256 (the
  * workgroups are resident together: one per CU). logits_out (nullable): [31][B][2048] copy of the head outputs.
- * prof (nullable): [256][2048] real-time counter stamps of every workgroup's steps (profiling). */
+ * prof (nullable): [256][2048] real-time counter stamps of every workgroup's steps (profiling). probe: a poll of
+ * more 16-byte chunks per thread than this first waits on one chunk per thread (fewer: every chunk each round). */
 typedef struct M3xDepthRun {
   int B, L0, L1, layers, H, hd, F, V, act, norm_kind, dtype, nwg;
   float inv_temp;
@@ -369,6 +370,7 @@ typedef struct M3xDepthRun {
   int32_t* sync;
   void* logits_out;
   uint64_t* prof;
+  int probe;
 } M3xDepthRun;
 
 /* Bytes of the exchange area and of M3xDepthRun (a binding checks its layout against the latter). */

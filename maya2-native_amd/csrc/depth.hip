@@ -81,6 +81,7 @@ struct M3xDepthRun {
   int32_t* sync;      // [0] epoch, [1] workgroups done, [2] error
   void* logits_out;   // optional [31][B][V] copy of every level's head output (tests)
   uint64_t* prof;     // optional [nwg][2048] real-time stamps of each workgroup's steps (profiling)
+  int probe;          // a poll with more chunks per thread than this waits on one chunk first
 };
 
 namespace dk {
@@ -108,6 +109,7 @@ struct Smem {
   float qv[HDMAX];
   float pr[NPOS];
   int codes[RB];
+  int seat_codes[NPOS];               // a sampler workgroup's codes of its seat, for the prefix rows at the end
   int vote[2][NT / 64];               // wg_all's per-wave votes, alternating buffers
 };
 
@@ -187,20 +189,21 @@ __device__ __forceinline__ bool wave_poll1w(__amdgpu_buffer_rsrc_t r, int off, b
 
 // This thread's chunks i < nit (16 bytes, two words each; nit uniform across the workgroup, at most N), handing
 // each live chunk's two payloads to sink(i, p0, p1) once. Chunk i sits at word base + U(i), base per thread and
-// U(i) a constant, so the loads take one address register and constant offsets. Chunk 0 is polled first (a probe:
-// one chunk per thread while the producers still run, which then mostly finds the rest already there); then rounds
-// read the chunks still missing, skipping chunks i >= nit by uniform branches and pushing arrived ones out of
-// bounds. Workgroup-collective (every thread calls it); false if any wave gave up after SPIN_LIMIT rounds.
+// U(i) a constant, so the loads take one address register and constant offsets. With more than `probe` chunks per
+// thread, chunk 0 is polled first (a probe: one chunk per thread while the producers still run, which then mostly
+// finds the rest already there); rounds read the chunks still missing, skipping chunks i >= nit by uniform
+// branches and pushing arrived ones out of bounds. Workgroup-collective (every thread calls it); false if any wave
+// gave up after SPIN_LIMIT rounds.
 template <int N, class U, class Live, class Sink>
 __device__ __forceinline__ bool ll_poll16(Smem& sm, int& vph, __amdgpu_buffer_rsrc_t r, int base, U uoff, int nit,
-                                          Live live, uint32_t tag, Sink sink) {
+                                          int probe, Live live, uint32_t tag, Sink sink) {
   static_assert(N <= 64, "chunks per thread");
   uint64_t pending = 0;
 #pragma unroll
   for (int i = 0; i < N; ++i)
     if (i < nit && live(i)) pending |= 1ull << i;
   bool ok = true;
-  if (nit > 0) {
+  if (nit > probe) {
     const bool l0 = pending & 1ull;
     u32x4 v0;
     ok = wave_poll1(r, base * 8 + uoff(0) * 8, l0, tag, v0);
@@ -209,8 +212,8 @@ __device__ __forceinline__ bool ll_poll16(Smem& sm, int& vph, __amdgpu_buffer_rs
       pending &= ~1ull;
     }
   }
-  if constexpr (N > 1) {
-    for (unsigned it = 0; ok && nit > 1; ++it) {
+  {
+    for (unsigned it = 0; ok; ++it) {
       if (__builtin_amdgcn_ballot_w64(pending != 0) == 0) break;
       if (it >= SPIN_LIMIT) {
         ok = false;
@@ -219,12 +222,12 @@ __device__ __forceinline__ bool ll_poll16(Smem& sm, int& vph, __amdgpu_buffer_rs
       M3X_POLL_CLOBBER();
       u32x4 v[N];
 #pragma unroll
-      for (int i = 1; i < N; ++i)
+      for (int i = 0; i < N; ++i)
         if (i < nit)
           v[i] = __builtin_amdgcn_raw_buffer_load_b128(r, base * 8 + (((pending >> i) & 1) ? 0 : OOB), uoff(i) * 8,
                                                        VOL);
 #pragma unroll
-      for (int i = 1; i < N; ++i) {
+      for (int i = 0; i < N; ++i) {
         if (i < nit && ((pending >> i) & 1) && v[i].y == tag && v[i].w == tag) {
           sink(i, v[i].x, v[i].z);
           pending &= ~(1ull << i);
@@ -238,14 +241,14 @@ __device__ __forceinline__ bool ll_poll16(Smem& sm, int& vph, __amdgpu_buffer_rs
 // the same for single words (8-byte loads); sink(i, payload)
 template <int N, class U, class Live, class Sink>
 __device__ __forceinline__ bool ll_poll8(Smem& sm, int& vph, __amdgpu_buffer_rsrc_t r, int base, U uoff, int nit,
-                                         Live live, uint32_t tag, Sink sink) {
+                                         int probe, Live live, uint32_t tag, Sink sink) {
   static_assert(N <= 32, "words per thread");
   uint32_t pending = 0;
 #pragma unroll
   for (int i = 0; i < N; ++i)
     if (i < nit && live(i)) pending |= 1u << i;
   bool ok = true;
-  if (nit > 0) {
+  if (nit > probe) {
     const bool l0 = pending & 1u;
     u32x2 v0;
     ok = wave_poll1w(r, base * 8 + uoff(0) * 8, l0, tag, v0);
@@ -254,26 +257,23 @@ __device__ __forceinline__ bool ll_poll8(Smem& sm, int& vph, __amdgpu_buffer_rsr
       pending &= ~1u;
     }
   }
-  if constexpr (N > 1) {
-    for (unsigned it = 0; ok && nit > 1; ++it) {
-      if (__builtin_amdgcn_ballot_w64(pending != 0) == 0) break;
-      if (it >= SPIN_LIMIT) {
-        ok = false;
-        break;
-      }
-      M3X_POLL_CLOBBER();
-      u32x2 v[N];
+  for (unsigned it = 0; ok; ++it) {
+    if (__builtin_amdgcn_ballot_w64(pending != 0) == 0) break;
+    if (it >= SPIN_LIMIT) {
+      ok = false;
+      break;
+    }
+    M3X_POLL_CLOBBER();
+    u32x2 v[N];
 #pragma unroll
-      for (int i = 1; i < N; ++i)
-        if (i < nit)
-          v[i] = __builtin_amdgcn_raw_buffer_load_b64(r, base * 8 + (((pending >> i) & 1) ? 0 : OOB), uoff(i) * 8,
-                                                      VOL);
+    for (int i = 0; i < N; ++i)
+      if (i < nit)
+        v[i] = __builtin_amdgcn_raw_buffer_load_b64(r, base * 8 + (((pending >> i) & 1) ? 0 : OOB), uoff(i) * 8, VOL);
 #pragma unroll
-      for (int i = 1; i < N; ++i) {
-        if (i < nit && ((pending >> i) & 1) && v[i].y == tag) {
-          sink(i, v[i].x);
-          pending &= ~(1u << i);
-        }
+    for (int i = 0; i < N; ++i) {
+      if (i < nit && ((pending >> i) & 1) && v[i].y == tag) {
+        sink(i, v[i].x);
+        pending &= ~(1u << i);
       }
     }
   }
@@ -397,7 +397,7 @@ __device__ __forceinline__ void norm_rows(Smem& sm, int B, const NormW<NK>& nw, 
 // thread t takes columns 4 t .. 4 t + 3 of every row, so a row is one 16-byte chunk per thread
 template <int DT>
 __device__ __forceinline__ bool add_rows(Smem& sm, int& vph, __amdgpu_buffer_rsrc_t rs, int base, uint32_t tag,
-                                         int B, const uint16_t* c, long ld_c) {
+                                         int B, const uint16_t* c, long ld_c, int probe) {
   const int t = threadIdx.x;
   uint2 cv[RB];
   if (c) {
@@ -410,7 +410,7 @@ __device__ __forceinline__ bool add_rows(Smem& sm, int& vph, __amdgpu_buffer_rsr
       }
   }
   const bool ok = ll_poll16<RB>(
-      sm, vph, rs, base + 2 * t, [](int i) { return i * (DM / 2); }, B, [](int) { return true; }, tag,
+      sm, vph, rs, base + 2 * t, [](int i) { return i * (DM / 2); }, B, probe, [](int) { return true; }, tag,
       [&](int i, uint32_t p0, uint32_t p1) {
         uint16_t* xp = &sm.m.x[i][4 * t];
         const uint16_t av[4] = {(uint16_t)(p0 & 0xffff), (uint16_t)(p0 >> 16), (uint16_t)(p1 & 0xffff),
@@ -434,7 +434,7 @@ __device__ __forceinline__ bool add_rows(Smem& sm, int& vph, __amdgpu_buffer_rsr
 // (its live rows) K / 4 chunks are live, and a half with no live row is skipped
 template <int K>
 __device__ __forceinline__ bool stage_act(Smem& sm, int& vph, __amdgpu_buffer_rsrc_t rs, int base, uint32_t tag,
-                                          int B) {
+                                          int B, int probe) {
   constexpr int CPR = K / 4, HR = RB / 2, N = HR * CPR / NT;
   static_assert(HR * CPR % NT == 0, "chunks per thread");
   bool ok = true;
@@ -443,7 +443,7 @@ __device__ __forceinline__ bool stage_act(Smem& sm, int& vph, __amdgpu_buffer_rs
     if (rows == 0) break;
     ok = ll_poll16<N>(
         sm, vph, rs, base + h * HR * CPR * 2 + 2 * (int)threadIdx.x, [](int i) { return 2 * NT * i; },
-        (nlive + NT - 1) / NT, [&](int i) { return (int)threadIdx.x + NT * i < nlive; }, tag,
+        (nlive + NT - 1) / NT, probe, [&](int i) { return (int)threadIdx.x + NT * i < nlive; }, tag,
         [&](int i, uint32_t p0, uint32_t p1) {
           const int cc = threadIdx.x + NT * i;
           *reinterpret_cast<uint2*>(&sm.act[h * HR + cc / CPR][4 * (cc % CPR)]) = uint2{p0, p1};
@@ -635,8 +635,9 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
           // the previous level's codes; this level's input rows are their prefix rows
           const uint32_t t_code = (epoch << 12) | (lvl_seq - 1);
           const int b_code = O_CODE + (1 - lpar) * W_CODE;
-          ok = ll_poll8<1>(sm, vph, rs, b_code + tid, [](int) { return 0; }, 1, [&](int) { return tid < B; }, t_code,
-                           [&](int, uint32_t p) { sm.codes[tid] = (int)p; });
+          ok = ll_poll8<1>(
+              sm, vph, rs, b_code + tid, [](int) { return 0; }, 1, a.probe, [&](int) { return tid < B; }, t_code,
+              [&](int, uint32_t p) { sm.codes[tid] = (int)p; });
           stamp(li * 64 + 52);
           __syncthreads();
           const __amdgpu_buffer_rsrc_t re = ro_rsrc((const uint16_t*)a.embed + (long)(L - 1) * a.V * DM);
@@ -649,7 +650,7 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
         } else if (l > 0) {
           const int b_prev = O_DN + ((li * layers + l - 1) & 1) * W_ATT;
           const uint16_t* c = a.cross ? (const uint16_t*)a.cross + (long)(l - 1) * DM : nullptr;
-          ok = add_rows<DT>(sm, vph, rs, b_prev, t_qkv - 1, B, c, a.ld_cross);
+          ok = add_rows<DT>(sm, vph, rs, b_prev, t_qkv - 1, B, c, a.ld_cross, a.probe);
         }
         stamp(li * 64 + l * 12 + 0);
         norm_rows<DT, NK>(sm, B, nw, a.eps1[l]);
@@ -662,7 +663,7 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
         constexpr int per = HD / 4;  // 16-byte chunks of each of q, k and v of one head
         const int part = tid / per, c = tid % per;
         const int w0 = b_qkv + pb * (3 * DM / 2) + (part * DM + ph * HD) / 2 + 2 * c;
-        ok = ll_poll16<1>(sm, vph, rs, w0, [](int) { return 0; }, 1, [&](int) { return tid < 3 * per; }, t_qkv,
+        ok = ll_poll16<1>(sm, vph, rs, w0, [](int) { return 0; }, 1, a.probe, [&](int) { return tid < 3 * per; }, t_qkv,
                           [&](int, uint32_t p0, uint32_t p1) {
                             const uint16_t v4[4] = {(uint16_t)(p0 & 0xffff), (uint16_t)(p0 >> 16),
                                                     (uint16_t)(p1 & 0xffff), (uint16_t)(p1 >> 16)};
@@ -742,7 +743,7 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
       if (ok && do_od) {
         WTile<8> wt;
         load_tile<8>(wt, (const uint16_t*)a.wo[l], u_od, DM);
-        ok = stage_act<DM>(sm, vph, rs, b_att, t_att, B);
+        ok = stage_act<DM>(sm, vph, rs, b_att, t_att, B, a.probe);
         stamp(li * 64 + l * 12 + 4);
         if (ok) finish_tile<DT, 0>(sm, mma_act<DT, 8>(wt, sm), f32x4_t{}, rs, b_o, DM, u_od, t_o, B, nullptr, 0);
         stamp(li * 64 + l * 12 + 5);
@@ -756,7 +757,7 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
         }
         NormW<NK> nw;
         load_norm<NK>(nw, a.n2w[l], a.n2b[l]);
-        ok = add_rows<DT>(sm, vph, rs, b_o, t_o, B, nullptr, 0);
+        ok = add_rows<DT>(sm, vph, rs, b_o, t_o, B, nullptr, 0, a.probe);
         stamp(li * 64 + l * 12 + 6);
         norm_rows<DT, NK>(sm, B, nw, a.eps2[l]);
         stamp(li * 64 + l * 12 + 11);
@@ -775,13 +776,13 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
         if constexpr (ACT == 1) {
           WTile<22> wt;
           load_tile<22>(wt, (const uint16_t*)a.wd[l], u_od, 2816);
-          ok = stage_act<2816>(sm, vph, rs, b_gu, t_gu, B);
+          ok = stage_act<2816>(sm, vph, rs, b_gu, t_gu, B, a.probe);
           stamp(li * 64 + l * 12 + 8);
           acc = mma_act<DT, 22>(wt, sm);
         } else {
           WTile<24> wt;
           load_tile<24>(wt, (const uint16_t*)a.wd[l], u_od, 3072);
-          ok = stage_act<3072>(sm, vph, rs, b_gu, t_gu, B);
+          ok = stage_act<3072>(sm, vph, rs, b_gu, t_gu, B, a.probe);
           acc = mma_act<DT, 24>(wt, sm);
         }
         if (ok) finish_tile<DT, 0>(sm, acc, f32x4_t{}, rs, b_dn, DM, u_od, t_dn, B, nullptr, 0);
@@ -799,7 +800,7 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
       load_norm<NK>(nw, a.fw, a.fb);
       const int b_prev = O_DN + ((li * layers + layers - 1) & 1) * W_ATT;
       const uint16_t* c = a.cross ? (const uint16_t*)a.cross + (long)(layers - 1) * DM : nullptr;
-      ok = add_rows<DT>(sm, vph, rs, b_prev, t_log - 1, B, c, a.ld_cross);
+      ok = add_rows<DT>(sm, vph, rs, b_prev, t_log - 1, B, c, a.ld_cross, a.probe);
       stamp(li * 64 + 48);
       norm_rows<DT, NK>(sm, B, nw, a.eps_f);
       if (ok && do_head) {
@@ -814,7 +815,7 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
       constexpr int NE = VMAX / NT;
       const float ur = a.greedy ? 0.f : a.u[(long)r * a.ld_u + L - 1];
       float xv[NE];
-      ok = ll_poll8<NE>(sm, vph, rs, b_log + r * (VMAX / 2) + tid / 2, [](int e) { return NT / 2 * e; }, NE,
+      ok = ll_poll8<NE>(sm, vph, rs, b_log + r * (VMAX / 2) + tid / 2, [](int e) { return NT / 2 * e; }, NE, a.probe,
                         [&](int) { return true; }, t_log, [&](int e, uint32_t p) {
                           const uint16_t h16 = (uint16_t)((tid & 1) ? (p >> 16) : (p & 0xffff));
                           xv[e] = E<DT>::to_f(h16) * a.inv_temp;
@@ -825,15 +826,22 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
       if (tid == 0) {
         a.codes[(long)r * a.ld_codes + L] = code;
         ll_st8(rs, b_code + r, (uint32_t)code, t_code);
+        sm.seat_codes[L] = code;
       }
       stamp(li * 64 + 51);
-      if (L + 1 < NPOS && tid < DM / 8) {
-        // the next prefix row, for a later group start that recomputes the whole prefix
-        const long cc = min(max(code, 0), VMAX - 1);
-        st16((uint16_t*)a.prefix + (long)r * a.ld_prefix + (long)(L + 1) * DM + 8 * tid,
-             ld16((const uint16_t*)a.embed + ((long)L * VMAX + cc) * DM + 8 * tid));
-      }
       __syncthreads();
+    }
+  }
+
+  // ---- the prefix rows of the levels sampled here (prefix position L + 1 = embed[L][code of level L]), for a
+  // later group start that recomputes the whole prefix; written once at the end, off the levels' chain
+  if (ok && wg < B) {
+    const int nl = min(a.L1, NPOS - 1) - a.L0;
+    for (int i = tid; i < nl * (DM / 8); i += NT) {
+      const int L = a.L0 + i / (DM / 8), c = 8 * (i % (DM / 8));
+      const long cc = min(max(sm.seat_codes[L], 0), VMAX - 1);
+      st16((uint16_t*)a.prefix + (long)wg * a.ld_prefix + (long)(L + 1) * DM + c,
+           ld16((const uint16_t*)a.embed + ((long)L * VMAX + cc) * DM + c));
     }
   }
 

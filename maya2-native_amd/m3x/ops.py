@@ -427,7 +427,7 @@ class DepthRunArgs(ctypes.Structure):
         ("prefix", ctypes.c_void_p), ("ld_prefix", ctypes.c_long), ("codes", ctypes.c_void_p),
         ("ld_codes", ctypes.c_long), ("u", ctypes.c_void_p), ("ld_u", ctypes.c_long), ("kd", _P4), ("vd", _P4),
         ("kv_sb", ctypes.c_long), ("kv_sh", ctypes.c_long), ("xchg", ctypes.c_void_p), ("sync", ctypes.c_void_p),
-        ("logits_out", ctypes.c_void_p), ("prof", ctypes.c_void_p)]
+        ("logits_out", ctypes.c_void_p), ("prof", ctypes.c_void_p), ("probe", ctypes.c_int)]
 
 
 def depth_run_xchg_bytes() -> int:

@@ -263,6 +263,9 @@ class FastDepth:
     # The kernel takes up to 16 seats; past 8 its handovers (every residual workgroup reads the whole rows of each
     # step's output) cost more than the launch path's kernels on MI355X, so larger batches take the launch path.
     PERSISTENT_SEATS = 8
+    # a handover poll with more 16-byte chunks per thread than this first waits on one chunk per thread (0: every
+    # poll does; measured best at 1-4 seats and within 1.5 % of the best at 8 and 16 on MI355X)
+    POLL_PROBE = 0
 
     def _persistent_ok(self, B, group):
         """Whether levels continuing `group` run as one persistent kernel for B seats: at most PERSISTENT_SEATS and
@@ -290,7 +293,7 @@ class FastDepth:
         a = ops.DepthRunArgs()
         a.B, a.L0, a.L1, a.layers, a.H, a.hd = b.B, L0, L1, len(layers), self.H, self.hd
         a.F, a.V, a.act, a.norm_kind = layers[0].ffn, self.n_codes, layers[0].act, layers[0].n1.kind
-        a.dtype, a.nwg = ops._DT[self.dtype], self._nwg
+        a.dtype, a.nwg, a.probe = ops._DT[self.dtype], self._nwg, self.POLL_PROBE
         a.inv_temp, a.top_k, a.greedy = 1.0 / self.temp, self.top_k, int(self.greedy)
         p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
         for l, L in enumerate(layers):
