@@ -12,7 +12,7 @@ import os
 import torch  # noqa: F401  (must precede the CDLL load, see above)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libm3x.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
