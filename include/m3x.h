@@ -92,13 +92,14 @@ int m3x_decode_attn_noalloc(const void* q, long sq_b, long sq_h, const void* k_c
 /* Elements of the packed form of an [N, K] weight (N rounded up to a multiple of 16, times K); -1 if K % 32. */
 long m3x_packed_weight_elems(int N, int K);
 
-/* Packs w[N, K] (row stride ldw, 16-bit) into MFMA fragment order for m3x_linear / m3x_linear_act: the 16 x 32
- * fragment (row tile t, k step s) is 1 KB at element (t * K/32 + s) * 512, lane l's 8 values at + 8 l holding
- * w[16 t + l % 16][32 s + 8 (l / 16) + e]; rows past N are zero. Done once per weight at load time.
- * Replaces nothing at run time: the reference multiplies nn.Linear weights in place (F.linear). */
-int m3x_pack_weight(const void* w, long ldw, int N, int K, void* out, void* stream);
+/* Packs w[N, K] (row stride ldw; bf16, fp16 or fp32 per dtype) into MFMA fragment order for m3x_linear /
+ * m3x_linear_act: the 16 x 32 fragment (row tile t, k step s) sits at element (t * K/32 + s) * 512, lane l's 8
+ * values at + 8 l holding w[16 t + l % 16][32 s + 8 (l / 16) + e]; rows past N are zero. Done once per weight at
+ * load time. Replaces nothing at run time: the reference multiplies nn.Linear weights in place (F.linear). */
+int m3x_pack_weight(const void* w, long ldw, int N, int K, void* out, int dtype, void* stream);
 
-/* y[M,N] = x[M,K] · w[N,K]^T with w packed by m3x_pack_weight; 16-bit in/out, fp32 accumulation (MFMA);
+/* y[M,N] = x[M,K] · w[N,K]^T with w packed by m3x_pack_weight; bf16/fp16 in and out with fp32 accumulation
+ * (MFMA 16x16x32), or fp32 throughout (dtype M3X_F32: MFMA 16x16x4 f32, the fp32 depth and codec paths);
  * K % 32 == 0. Deterministic (K slices are summed in a fixed order inside the workgroup), one launch, no workspace.
  * Replaces `F.linear` / `nn.Linear` on the path: q|k|v, o, down (serve/fast_backbone.py:193,200,202),
  * cb0 head (tts/model/backbone.py:135-136), depth trunk and heads (serve/fast_depth.py:104,122,125,185-191). */

@@ -627,8 +627,8 @@ M3X_API int m3x_decode_attn_noalloc(const void* q, long sq_b, long sq_h, const v
 // With write_kv the keys and values of this call's own positions are read from qkv, and the last query's
 // registers, which hold every one of them, are what is stored to the scratch.
 template <int DT, int HD, int NG>
-__global__ __launch_bounds__(64) void depth_attn_kernel(const uint16_t* __restrict__ qkv, long sqb, long sqt,
-                                                        uint16_t* kd, uint16_t* vd, uint16_t* __restrict__ out,
+__global__ __launch_bounds__(64) void depth_attn_kernel(const Elt<DT>* __restrict__ qkv, long sqb, long sqt,
+                                                        Elt<DT>* kd, Elt<DT>* vd, Elt<DT>* __restrict__ out,
                                                         long sob, long sot, int T, int p0, int tq0, int H, int np,
                                                         float scale, int write_kv) {
   constexpr int PPR = HD / 8;   // 16-byte pieces per row
@@ -637,9 +637,9 @@ __global__ __launch_bounds__(64) void depth_attn_kernel(const uint16_t* __restri
   const int h = blockIdx.y;
   const int lane = threadIdx.x;
   const int r = lane / PPR, c = lane % PPR;
-  uint16_t* kb = kd + ((long)b * H + h) * np * HD;
-  uint16_t* vb = vd + ((long)b * H + h) * np * HD;
-  const uint16_t* qb = qkv + (long)b * sqb + (long)h * HD;  // q of row t at qb + t*sqt; k at +H*HD; v at +2*H*HD
+  Elt<DT>* kb = kd + ((long)b * H + h) * np * HD;
+  Elt<DT>* vb = vd + ((long)b * H + h) * np * HD;
+  const Elt<DT>* qb = qkv + (long)b * sqb + (long)h * HD;  // q of row t at qb + t*sqt; k at +H*HD; v at +2*H*HD
   // key/value row j of this (b, h): the scratch below p0 (or always without write_kv), else this call's qkv row
   const int own = write_kv ? p0 : np;
   auto krow = [&](int j) { return j < own ? kb + (long)j * HD : qb + (long)(j - p0) * sqt + (long)H * HD; };
@@ -647,13 +647,13 @@ __global__ __launch_bounds__(64) void depth_attn_kernel(const uint16_t* __restri
   for (int t = tq0; t < T; ++t) {
     const int nk = p0 + t + 1;
     const int ng = (nk + RPI - 1) / RPI;
-    const u16x8 qv = ld16(qb + (long)t * sqt + 8 * c);
-    u16x8 kv[NG], vv[NG];
+    const V8<DT> qv = ldv<DT>(qb + (long)t * sqt + 8 * c);
+    V8<DT> kv[NG], vv[NG];
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       const int j = min(g * RPI + r, nk - 1);
-      kv[g] = ld16(krow(j) + 8 * c);
-      vv[g] = ld16(vrow(j) + 8 * c);
+      kv[g] = ldv<DT>(krow(j) + 8 * c);
+      vv[g] = ldv<DT>(vrow(j) + 8 * c);
     }
     float qf[8];
 #pragma unroll
@@ -690,10 +690,10 @@ __global__ __launch_bounds__(64) void depth_attn_kernel(const uint16_t* __restri
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] = across_sum<PPR>(acc[e]);
     if (r == 0) {
-      u16x8 ov;
+      V8<DT> ov;
 #pragma unroll
       for (int e = 0; e < 8; ++e) ov.v[e] = E<DT>::from_f(acc[e] / l);
-      st16(out + (long)b * sob + (long)(t - tq0) * sot + (long)h * HD + 8 * c, ov);
+      stv<DT>(out + (long)b * sob + (long)(t - tq0) * sot + (long)h * HD + 8 * c, ov);
     }
     // the last query has loaded every new row (keys p0..p0+T-1, from qkv): store them to the scratch
     if (write_kv && t == T - 1) {
@@ -701,8 +701,8 @@ __global__ __launch_bounds__(64) void depth_attn_kernel(const uint16_t* __restri
       for (int g = 0; g < NG; ++g) {
         const int j = g * RPI + r;
         if (j >= p0 && j < nk) {
-          st16(kb + (long)j * HD + 8 * c, kv[g]);
-          st16(vb + (long)j * HD + 8 * c, vv[g]);
+          stv<DT>(kb + (long)j * HD + 8 * c, kv[g]);
+          stv<DT>(vb + (long)j * HD + 8 * c, vv[g]);
         }
       }
     }
@@ -722,8 +722,8 @@ M3X_API int m3x_depth_attn(const void* qkv, long sqb, long sqt, void* kd, void* 
     return M3X_EINVAL;
   hipStream_t st = (hipStream_t)stream;
 #define M3X_DA(DTT, HDD, NGG)                                                                                     \
-  hipLaunchKernelGGL((depth_attn_kernel<DTT, HDD, NGG>), dim3(B, heads), dim3(64), 0, st, (const uint16_t*)qkv,   \
-                     sqb, sqt, (uint16_t*)kd, (uint16_t*)vd, (uint16_t*)out, sob, sot, T, p0, tq0, heads, np,     \
+  hipLaunchKernelGGL((depth_attn_kernel<DTT, HDD, NGG>), dim3(B, heads), dim3(64), 0, st, (const Elt<DTT>*)qkv,    \
+                     sqb, sqt, (Elt<DTT>*)kd, (Elt<DTT>*)vd, (Elt<DTT>*)out, sob, sot, T, p0, tq0, heads, np,        \
                      scale, write_kv)
 #define M3X_DA_NG(DTT, HDD)                                                        \
   do {                                                                             \
@@ -738,6 +738,8 @@ M3X_API int m3x_depth_attn(const void* qkv, long sqb, long sqt, void* kd, void* 
   else if (dtype == M3X_BF16) M3X_DA_NG(M3X_BF16, 64);
   else if (dtype == M3X_F16 && head_dim == 128) M3X_DA_NG(M3X_F16, 128);
   else if (dtype == M3X_F16) M3X_DA_NG(M3X_F16, 64);
+  else if (dtype == M3X_F32 && head_dim == 128) M3X_DA_NG(M3X_F32, 128);
+  else if (dtype == M3X_F32) M3X_DA_NG(M3X_F32, 64);
   else return M3X_EUNSUPPORTED;
 #undef M3X_DA_NG
 #undef M3X_DA

@@ -38,7 +38,7 @@ __device__ __forceinline__ uint16_t f2bf(float f) { return __builtin_bit_cast(ui
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 
-// Element-type traits: DT = M3X_BF16 or M3X_F16.
+// Element-type traits: DT = M3X_BF16 or M3X_F16 (16-bit storage); M3X_F32 below.
 template <int DT> struct E;
 template <> struct E<M3X_BF16> {
   static __device__ __forceinline__ float to_f(uint16_t v) { return bf2f(v); }
@@ -49,8 +49,20 @@ template <> struct E<M3X_F16> {
   static __device__ __forceinline__ uint16_t from_f(float f) { return f2h(f); }
 };
 
+// fp32 storage (the fp32 compute paths): conversions are the identity, so every rnd<M3X_F32> is a no-op and a
+// kernel instantiated for it computes the same fp32 expression without intermediate roundings.
+template <> struct E<M3X_F32> {
+  static __device__ __forceinline__ float to_f(float v) { return v; }
+  static __device__ __forceinline__ float from_f(float f) { return f; }
+};
+
 // round a float through the storage type
 template <int DT> __device__ __forceinline__ float rnd(float f) { return E<DT>::to_f(E<DT>::from_f(f)); }
+
+// storage element of DT: uint16_t bit patterns for bf16 / fp16, float for fp32
+template <int DT> struct Store { using T = uint16_t; };
+template <> struct Store<M3X_F32> { using T = float; };
+template <int DT> using Elt = typename Store<DT>::T;
 
 // ------------------------------------------------------------------ 16-byte vectors
 struct __align__(16) u16x8 { uint16_t v[8]; };
@@ -67,6 +79,43 @@ __device__ __forceinline__ u16x8 ld16_nt(const uint16_t* p) {
 }
 __device__ __forceinline__ void st16(uint16_t* p, const u16x8& x) {
   *reinterpret_cast<uint4*>(p) = __builtin_bit_cast(uint4, x);
+}
+
+// Eight consecutive elements of storage type DT: one 16-byte vector for 16-bit types, two for fp32. Kernels that
+// move rows in groups of 8 elements use V8 / ldv / stv and so serve every dtype with one body; for 16-bit types
+// they are exactly u16x8 / ld16 / st16.
+struct __align__(16) f32x8 { float v[8]; };
+template <int DT> struct V8T { using T = u16x8; };
+template <> struct V8T<M3X_F32> { using T = f32x8; };
+template <int DT> using V8 = typename V8T<DT>::T;
+template <int DT> __device__ __forceinline__ V8<DT> ldv(const Elt<DT>* p) {
+  if constexpr (DT == M3X_F32) {
+    const uint4 a = reinterpret_cast<const uint4*>(p)[0];
+    const uint4 b = reinterpret_cast<const uint4*>(p)[1];
+    f32x8 r;
+    r.v[0] = __uint_as_float(a.x), r.v[1] = __uint_as_float(a.y), r.v[2] = __uint_as_float(a.z);
+    r.v[3] = __uint_as_float(a.w), r.v[4] = __uint_as_float(b.x), r.v[5] = __uint_as_float(b.y);
+    r.v[6] = __uint_as_float(b.z), r.v[7] = __uint_as_float(b.w);
+    return r;
+  } else {
+    return ld16(p);
+  }
+}
+template <int DT> __device__ __forceinline__ void stv(Elt<DT>* p, const V8<DT>& x) {
+  if constexpr (DT == M3X_F32) {
+    reinterpret_cast<uint4*>(p)[0] = make_uint4(__float_as_uint(x.v[0]), __float_as_uint(x.v[1]),
+                                                __float_as_uint(x.v[2]), __float_as_uint(x.v[3]));
+    reinterpret_cast<uint4*>(p)[1] = make_uint4(__float_as_uint(x.v[4]), __float_as_uint(x.v[5]),
+                                                __float_as_uint(x.v[6]), __float_as_uint(x.v[7]));
+  } else {
+    st16(p, x);
+  }
+}
+template <int DT> __device__ __forceinline__ V8<DT> zero_v8() {
+  V8<DT> z;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) z.v[e] = 0;
+  return z;
 }
 
 // ------------------------------------------------------------------ exp for the samplers
@@ -189,6 +238,15 @@ template <> __device__ __forceinline__ f32x4_t mfma16x16x32<M3X_BF16>(const u16x
 template <> __device__ __forceinline__ f32x4_t mfma16x16x32<M3X_F16>(const u16x8& a, const u16x8& b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
                                                 0, 0, 0);
+}
+
+// fp32 operands in the same fragment layout (lane l holds A[l%16][8*(l/16)+e] and B[8*(l/16)+e][l%16], e = 0..7):
+// eight v_mfma_f32_16x16x4_f32, instruction e taking element e of each lane, whose k index l/16 then stands for
+// k = 8*(l/16)+e of the 32. Together they add the same 32 products into D (same D layout as above), in fp32.
+__device__ __forceinline__ f32x4_t mfma16x16x32_f32(const f32x8& a, const f32x8& b, f32x4_t c) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.v[e], b.v[e], c, 0, 0, 0);
+  return c;
 }
 
 static inline int m3x_ceil_div(long a, long b) { return (int)((a + b - 1) / b); }

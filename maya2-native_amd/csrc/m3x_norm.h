@@ -41,10 +41,10 @@ __device__ __forceinline__ float row_tree_sum(float p, float* red, float* bcast)
 //   RMSNorm    y = dt(dt(v * (1 / sqrt(mean(v^2) + eps))) * w)
 // Threads of inactive rows pass v = 0 and discard the result. Every thread of the block calls it.
 template <int TPR, int DT>
-__device__ __forceinline__ u16x8 norm_vec(const float (&v)[8], const u16x8& wv, const u16x8& bv, int kind, float eps,
+__device__ __forceinline__ V8<DT> norm_vec(const float (&v)[8], const V8<DT>& wv, const V8<DT>& bv, int kind, float eps,
                                           float* red, float* bcast) {
   constexpr int N = TPR * 8;
-  u16x8 yv;
+  V8<DT> yv;
   float p;
   if (kind == M3X_NORM_LAYER) {
     p = v[0];

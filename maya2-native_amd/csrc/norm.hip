@@ -61,9 +61,9 @@ __device__ __forceinline__ float wave_row_total(float p) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fold_half_sum<64>(p)), 0));
 }
 template <int DT>
-__device__ __forceinline__ void norm_pair_wave(const float (&v0)[8], const float (&v1)[8], const u16x8& w0,
-                                               const u16x8& w1, const u16x8& b0, const u16x8& b1, int kind, float eps,
-                                               u16x8& y0, u16x8& y1) {
+__device__ __forceinline__ void norm_pair_wave(const float (&v0)[8], const float (&v1)[8], const V8<DT>& w0,
+                                               const V8<DT>& w1, const V8<DT>& b0, const V8<DT>& b1, int kind, float eps,
+                                               V8<DT>& y0, V8<DT>& y1) {
   constexpr float N = 1024.0f;
   if (kind == M3X_NORM_LAYER) {
     float p0 = v0[0], p1 = v1[0];
@@ -266,11 +266,11 @@ M3X_API int m3x_qk_norm_rope_cache(const void* qkv, long s_qkv, void* q_out, lon
 // a == nullptr: x' = x (plain norm of the input, serve/fast_depth.py:164).
 
 template <int TPR, int DT>
-__global__ __launch_bounds__(256) void add_norm_kernel(const uint16_t* __restrict__ x, long sxb, long sxt,
-                                                       const uint16_t* __restrict__ a, long sab, long sat,
-                                                       const uint16_t* __restrict__ c, long s_c, uint16_t* xo,
-                                                       uint16_t* __restrict__ y, const uint16_t* __restrict__ w,
-                                                       const uint16_t* __restrict__ b, float eps, int rows, int T,
+__global__ __launch_bounds__(256) void add_norm_kernel(const Elt<DT>* __restrict__ x, long sxb, long sxt,
+                                                       const Elt<DT>* __restrict__ a, long sab, long sat,
+                                                       const Elt<DT>* __restrict__ c, long s_c, Elt<DT>* xo,
+                                                       Elt<DT>* __restrict__ y, const Elt<DT>* __restrict__ w,
+                                                       const Elt<DT>* __restrict__ b, float eps, int rows, int T,
                                                        int kind) {
   constexpr int N = TPR * 8;
   constexpr int RPB = 256 / TPR;
@@ -281,57 +281,57 @@ __global__ __launch_bounds__(256) void add_norm_kernel(const uint16_t* __restric
   const bool active = row < rows;
   const int rb = active ? row / T : 0, rt = active ? row % T : 0;
   float v[8];
-  u16x8 wv = {}, bv = {};
+  V8<DT> wv = zero_v8<DT>(), bv = zero_v8<DT>();
   if (active) {
-    u16x8 xv = ld16(x + rb * sxb + rt * sxt + 8 * t);
+    V8<DT> xv = ldv<DT>(x + rb * sxb + rt * sxt + 8 * t);
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = E<DT>::to_f(xv.v[e]);
     if (a) {
-      u16x8 av = ld16(a + rb * sab + rt * sat + 8 * t);
+      V8<DT> av = ldv<DT>(a + rb * sab + rt * sat + 8 * t);
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[e] = rnd<DT>(v[e] + E<DT>::to_f(av.v[e]));
     }
     if (c) {
-      u16x8 cv = ld16(c + (long)rb * s_c + 8 * t);
+      V8<DT> cv = ldv<DT>(c + (long)rb * s_c + 8 * t);
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[e] = rnd<DT>(v[e] + E<DT>::to_f(cv.v[e]));
     }
     // affine parameters after the row's own loads: they arrive while the reductions run
-    wv = ld16(w + 8 * t);
-    if (kind == M3X_NORM_LAYER) bv = ld16(b + 8 * t);
+    wv = ldv<DT>(w + 8 * t);
+    if (kind == M3X_NORM_LAYER) bv = ldv<DT>(b + 8 * t);
     if (xo) {
-      u16x8 ov;
+      V8<DT> ov;
 #pragma unroll
       for (int e = 0; e < 8; ++e) ov.v[e] = E<DT>::from_f(v[e]);
-      st16(xo + (long)row * N + 8 * t, ov);
+      stv<DT>(xo + (long)row * N + 8 * t, ov);
     }
   } else {
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = 0.f;
   }
-  const u16x8 yv = norm_vec<TPR, DT>(v, wv, bv, kind, eps, red, bcast);
+  const V8<DT> yv = norm_vec<TPR, DT>(v, wv, bv, kind, eps, red, bcast);
   if (!active) return;
-  st16(y + (long)row * N + 8 * t, yv);
+  stv<DT>(y + (long)row * N + 8 * t, yv);
 }
 
 // add_norm_kernel's contract for n = 1024, one 64-thread workgroup per row.
 template <int DT>
-__global__ __launch_bounds__(64) void add_norm_wave_kernel(const uint16_t* __restrict__ x, long sxb, long sxt,
-                                                           const uint16_t* __restrict__ a, long sab, long sat,
-                                                           const uint16_t* __restrict__ c, long s_c, uint16_t* xo,
-                                                           uint16_t* __restrict__ y, const uint16_t* __restrict__ w,
-                                                           const uint16_t* __restrict__ b, float eps, int T,
+__global__ __launch_bounds__(64) void add_norm_wave_kernel(const Elt<DT>* __restrict__ x, long sxb, long sxt,
+                                                           const Elt<DT>* __restrict__ a, long sab, long sat,
+                                                           const Elt<DT>* __restrict__ c, long s_c, Elt<DT>* xo,
+                                                           Elt<DT>* __restrict__ y, const Elt<DT>* __restrict__ w,
+                                                           const Elt<DT>* __restrict__ b, float eps, int T,
                                                            int kind) {
   const int row = blockIdx.x;
   const int l = threadIdx.x;
   const long rb = row / T, rt = row % T;
-  const uint16_t* xr = x + rb * sxb + rt * sxt;
-  u16x8 x0 = ld16(xr + 8 * l), x1 = ld16(xr + 8 * (l + 64));
-  u16x8 a0, a1, c0, c1, b0 = {}, b1 = {};
-  if (a) a0 = ld16(a + rb * sab + rt * sat + 8 * l), a1 = ld16(a + rb * sab + rt * sat + 8 * (l + 64));
-  if (c) c0 = ld16(c + rb * s_c + 8 * l), c1 = ld16(c + rb * s_c + 8 * (l + 64));
-  const u16x8 w0 = ld16(w + 8 * l), w1 = ld16(w + 8 * (l + 64));
-  if (kind == M3X_NORM_LAYER) b0 = ld16(b + 8 * l), b1 = ld16(b + 8 * (l + 64));
+  const Elt<DT>* xr = x + rb * sxb + rt * sxt;
+  V8<DT> x0 = ldv<DT>(xr + 8 * l), x1 = ldv<DT>(xr + 8 * (l + 64));
+  V8<DT> a0, a1, c0, c1, b0 = zero_v8<DT>(), b1 = zero_v8<DT>();
+  if (a) a0 = ldv<DT>(a + rb * sab + rt * sat + 8 * l), a1 = ldv<DT>(a + rb * sab + rt * sat + 8 * (l + 64));
+  if (c) c0 = ldv<DT>(c + rb * s_c + 8 * l), c1 = ldv<DT>(c + rb * s_c + 8 * (l + 64));
+  const V8<DT> w0 = ldv<DT>(w + 8 * l), w1 = ldv<DT>(w + 8 * (l + 64));
+  if (kind == M3X_NORM_LAYER) b0 = ldv<DT>(b + 8 * l), b1 = ldv<DT>(b + 8 * (l + 64));
   float v0[8], v1[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -341,16 +341,39 @@ __global__ __launch_bounds__(64) void add_norm_wave_kernel(const uint16_t* __res
     if (c) v0[e] = rnd<DT>(v0[e] + E<DT>::to_f(c0.v[e])), v1[e] = rnd<DT>(v1[e] + E<DT>::to_f(c1.v[e]));
   }
   if (xo) {
-    u16x8 o0, o1;
+    V8<DT> o0, o1;
 #pragma unroll
     for (int e = 0; e < 8; ++e) o0.v[e] = E<DT>::from_f(v0[e]), o1.v[e] = E<DT>::from_f(v1[e]);
-    st16(xo + (long)row * 1024 + 8 * l, o0);
-    st16(xo + (long)row * 1024 + 8 * (l + 64), o1);
+    stv<DT>(xo + (long)row * 1024 + 8 * l, o0);
+    stv<DT>(xo + (long)row * 1024 + 8 * (l + 64), o1);
   }
-  u16x8 y0, y1;
+  V8<DT> y0, y1;
   norm_pair_wave<DT>(v0, v1, w0, w1, b0, b1, kind, eps, y0, y1);
-  st16(y + (long)row * 1024 + 8 * l, y0);
-  st16(y + (long)row * 1024 + 8 * (l + 64), y1);
+  stv<DT>(y + (long)row * 1024 + 8 * l, y0);
+  stv<DT>(y + (long)row * 1024 + 8 * (l + 64), y1);
+}
+
+template <int DT>
+static bool launch_add_norm(const void* x, long sxb, long sxt, const void* a, long sab, long sat, const void* c,
+                            long s_c, void* x_out, void* y, const void* w, const void* b, float eps, int rows, int T,
+                            int n, int kind, hipStream_t st) {
+  const Elt<DT> *X = (const Elt<DT>*)x, *A = (const Elt<DT>*)a, *C = (const Elt<DT>*)c;
+  const Elt<DT> *Wt = (const Elt<DT>*)w, *Bt = (const Elt<DT>*)b;
+  Elt<DT> *XO = (Elt<DT>*)x_out, *Y = (Elt<DT>*)y;
+  if (n == 1024 && rows <= WAVE_ROWS_MAX) {
+    hipLaunchKernelGGL(add_norm_wave_kernel<DT>, dim3(rows), dim3(64), 0, st, X, sxb, sxt, A, sab, sat, C, s_c, XO, Y,
+                       Wt, Bt, eps, T, kind);
+    return true;
+  }
+#define M3X_ADD_NORM_LAUNCH(NN)                                                                                  \
+  hipLaunchKernelGGL((add_norm_kernel<NN / 8, DT>), dim3(m3x_ceil_div(rows, 256 / (NN / 8))), dim3(256), 0, st, X, \
+                     sxb, sxt, A, sab, sat, C, s_c, XO, Y, Wt, Bt, eps, rows, T, kind)
+  if (n == 512) M3X_ADD_NORM_LAUNCH(512);
+  else if (n == 1024) M3X_ADD_NORM_LAUNCH(1024);
+  else if (n == 2048) M3X_ADD_NORM_LAUNCH(2048);
+  else return false;
+#undef M3X_ADD_NORM_LAUNCH
+  return true;
 }
 
 // Row r = (b, t) = (r / T, r % T) of x is read at x + b*sxb + t*sxt (likewise a); x_out and y are contiguous
@@ -368,30 +391,16 @@ M3X_API int m3x_add_norm(const void* x, long sxb, long sxt, const void* a, long 
       (c && !m3x_aligned16(c)) || (x_out && !m3x_aligned16(x_out)) || (b && !m3x_aligned16(b)))
     return M3X_EINVAL;
   hipStream_t st = (hipStream_t)stream;
-  const uint16_t *X = (const uint16_t*)x, *A = (const uint16_t*)a, *C = (const uint16_t*)c;
-  const uint16_t *Wt = (const uint16_t*)w, *Bt = (const uint16_t*)b;
-  uint16_t *XO = (uint16_t*)x_out, *Y = (uint16_t*)y;
-  if (n == 1024 && rows <= WAVE_ROWS_MAX && (dtype == M3X_BF16 || dtype == M3X_F16)) {
-    if (dtype == M3X_BF16)
-      hipLaunchKernelGGL(add_norm_wave_kernel<M3X_BF16>, dim3(rows), dim3(64), 0, st, X, sxb, sxt, A, sab, sat, C, s_c,
-                         XO, Y, Wt, Bt, eps, T, kind);
-    else
-      hipLaunchKernelGGL(add_norm_wave_kernel<M3X_F16>, dim3(rows), dim3(64), 0, st, X, sxb, sxt, A, sab, sat, C, s_c,
-                         XO, Y, Wt, Bt, eps, T, kind);
-    M3X_CHECK_LAUNCH();
-    return M3X_OK;
-  }
-#define M3X_ADD_NORM_LAUNCH(NN, DTT)                                                                               \
-  hipLaunchKernelGGL((add_norm_kernel<NN / 8, DTT>), dim3(m3x_ceil_div(rows, 256 / (NN / 8))), dim3(256), 0, st, X, \
-                     sxb, sxt, A, sab, sat, C, s_c, XO, Y, Wt, Bt, eps, rows, T, kind)
-  if (dtype == M3X_BF16 && n == 512) M3X_ADD_NORM_LAUNCH(512, M3X_BF16);
-  else if (dtype == M3X_F16 && n == 512) M3X_ADD_NORM_LAUNCH(512, M3X_F16);
-  else if (dtype == M3X_BF16 && n == 1024) M3X_ADD_NORM_LAUNCH(1024, M3X_BF16);
-  else if (dtype == M3X_F16 && n == 1024) M3X_ADD_NORM_LAUNCH(1024, M3X_F16);
-  else if (dtype == M3X_BF16 && n == 2048) M3X_ADD_NORM_LAUNCH(2048, M3X_BF16);
-  else if (dtype == M3X_F16 && n == 2048) M3X_ADD_NORM_LAUNCH(2048, M3X_F16);
-  else return M3X_EUNSUPPORTED;
-#undef M3X_ADD_NORM_LAUNCH
+  bool ok;
+  if (dtype == M3X_BF16)
+    ok = launch_add_norm<M3X_BF16>(x, sxb, sxt, a, sab, sat, c, s_c, x_out, y, w, b, eps, rows, T, n, kind, st);
+  else if (dtype == M3X_F16)
+    ok = launch_add_norm<M3X_F16>(x, sxb, sxt, a, sab, sat, c, s_c, x_out, y, w, b, eps, rows, T, n, kind, st);
+  else if (dtype == M3X_F32)
+    ok = launch_add_norm<M3X_F32>(x, sxb, sxt, a, sab, sat, c, s_c, x_out, y, w, b, eps, rows, T, n, kind, st);
+  else
+    return M3X_EUNSUPPORTED;
+  if (!ok) return M3X_EUNSUPPORTED;
   M3X_CHECK_LAUNCH();
   return M3X_OK;
 }
@@ -399,16 +408,16 @@ M3X_API int m3x_add_norm(const void* x, long sxb, long sxt, const void* a, long 
 // out[r] = dt(x[r] + bias[r * ld_bias]) for rows of n elements (ld_bias = 0 broadcasts one vector).
 // Replaces `d.in_proj(h) + self.level0` (serve/fast_depth.py:150).
 template <int DT>
-__global__ __launch_bounds__(256) void add_rows_kernel(const uint16_t* __restrict__ x, long ld_x,
-                                                       const uint16_t* __restrict__ bias, long ld_b,
-                                                       uint16_t* __restrict__ out, long ld_o, int rows, int nvec) {
+__global__ __launch_bounds__(256) void add_rows_kernel(const Elt<DT>* __restrict__ x, long ld_x,
+                                                       const Elt<DT>* __restrict__ bias, long ld_b,
+                                                       Elt<DT>* __restrict__ out, long ld_o, int rows, int nvec) {
   const long i = (long)blockIdx.x * 256 + threadIdx.x;
   if (i >= (long)rows * nvec) return;
   const int r = (int)(i / nvec), v = (int)(i % nvec);
-  u16x8 xv = ld16(x + r * ld_x + 8 * v), bv = ld16(bias + r * ld_b + 8 * v), ov;
+  V8<DT> xv = ldv<DT>(x + r * ld_x + 8 * v), bv = ldv<DT>(bias + r * ld_b + 8 * v), ov;
 #pragma unroll
   for (int e = 0; e < 8; ++e) ov.v[e] = E<DT>::from_f(E<DT>::to_f(xv.v[e]) + E<DT>::to_f(bv.v[e]));
-  st16(out + r * ld_o + 8 * v, ov);
+  stv<DT>(out + r * ld_o + 8 * v, ov);
 }
 
 M3X_API int m3x_add_rows(const void* x, long ld_x, const void* bias, long ld_bias, void* out, long ld_out, int rows,
@@ -419,14 +428,14 @@ M3X_API int m3x_add_rows(const void* x, long ld_x, const void* bias, long ld_bia
   if (!m3x_aligned16(x) || !m3x_aligned16(bias) || !m3x_aligned16(out)) return M3X_EINVAL;
   const long total = (long)rows * (n / 8);
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == M3X_BF16)
-    hipLaunchKernelGGL(add_rows_kernel<M3X_BF16>, dim3(m3x_ceil_div(total, 256)), dim3(256), 0, st,
-                       (const uint16_t*)x, ld_x, (const uint16_t*)bias, ld_bias, (uint16_t*)out, ld_out, rows, n / 8);
-  else if (dtype == M3X_F16)
-    hipLaunchKernelGGL(add_rows_kernel<M3X_F16>, dim3(m3x_ceil_div(total, 256)), dim3(256), 0, st,
-                       (const uint16_t*)x, ld_x, (const uint16_t*)bias, ld_bias, (uint16_t*)out, ld_out, rows, n / 8);
-  else
-    return M3X_EUNSUPPORTED;
+#define M3X_ADD_ROWS(DTT)                                                                                 \
+  hipLaunchKernelGGL(add_rows_kernel<DTT>, dim3(m3x_ceil_div(total, 256)), dim3(256), 0, st, (const Elt<DTT>*)x, \
+                     ld_x, (const Elt<DTT>*)bias, ld_bias, (Elt<DTT>*)out, ld_out, rows, n / 8)
+  if (dtype == M3X_BF16) M3X_ADD_ROWS(M3X_BF16);
+  else if (dtype == M3X_F16) M3X_ADD_ROWS(M3X_F16);
+  else if (dtype == M3X_F32) M3X_ADD_ROWS(M3X_F32);
+  else return M3X_EUNSUPPORTED;
+#undef M3X_ADD_ROWS
   M3X_CHECK_LAUNCH();
   return M3X_OK;
 }
@@ -438,10 +447,10 @@ M3X_API int m3x_add_rows(const void* x, long ld_x, const void* bias, long ld_bia
 // (nn.RMSNorm with eps = finfo(dtype).eps when the module was built with eps=None).
 // Codes outside [0, n_codes) are clamped (the reference trusts its sampler; a clamp keeps the gather in bounds).
 template <int TPR, int DT>
-__global__ __launch_bounds__(256) void feedback_kernel(const uint16_t* __restrict__ table,
+__global__ __launch_bounds__(256) void feedback_kernel(const Elt<DT>* __restrict__ table,
                                                        const int32_t* __restrict__ codes, long s_codes,
-                                                       uint16_t* __restrict__ out, long s_out,
-                                                       const uint16_t* __restrict__ w, float eps, float scale, int B,
+                                                       Elt<DT>* __restrict__ out, long s_out,
+                                                       const Elt<DT>* __restrict__ w, float eps, float scale, int B,
                                                        int n_q, int n_codes) {
   constexpr int N = TPR * 8;
   constexpr int RPB = 256 / TPR;
@@ -466,10 +475,10 @@ __global__ __launch_bounds__(256) void feedback_kernel(const uint16_t* __restric
       }
 #pragma unroll
       for (int h = 0; h < 32; h += 16) {
-        u16x8 tv[16];
+        V8<DT> tv[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i)
-          if (l0 + h + i < n_q) tv[i] = ld16(table + ((long)cd[h + i] + (long)n_codes * (l0 + h + i)) * N + 8 * t);
+          if (l0 + h + i < n_q) tv[i] = ldv<DT>(table + ((long)cd[h + i] + (long)n_codes * (l0 + h + i)) * N + 8 * t);
 #pragma unroll
         for (int i = 0; i < 16; ++i)
           if (l0 + h + i < n_q) {
@@ -487,10 +496,10 @@ __global__ __launch_bounds__(256) void feedback_kernel(const uint16_t* __restric
   const float ss = row_tree_sum<TPR>(p, red, bcast);
   if (!active) return;
   const float inv = 1.0f / sqrtf(ss / (float)N + eps);
-  u16x8 wv = ld16(w + 8 * t), yv;
+  V8<DT> wv = ldv<DT>(w + 8 * t), yv;
 #pragma unroll
   for (int e = 0; e < 8; ++e) yv.v[e] = E<DT>::from_f(v[e] * inv * E<DT>::to_f(wv.v[e]));
-  st16(out + (long)row * s_out + 8 * t, yv);
+  stv<DT>(out + (long)row * s_out + 8 * t, yv);
 }
 
 M3X_API int m3x_feedback(const void* table, const int32_t* codes, long s_codes, void* out, long s_out, const void* w,
@@ -503,12 +512,14 @@ M3X_API int m3x_feedback(const void* table, const int32_t* codes, long s_codes, 
   hipStream_t st = (hipStream_t)stream;
 #define M3X_FB_LAUNCH(NN, DTT)                                                                                   \
   hipLaunchKernelGGL((feedback_kernel<NN / 8, DTT>), dim3(m3x_ceil_div(B, 256 / (NN / 8))), dim3(256), 0, st,   \
-                     (const uint16_t*)table, codes, s_codes, (uint16_t*)out, s_out, (const uint16_t*)w, eps, scale, \
+                     (const Elt<DTT>*)table, codes, s_codes, (Elt<DTT>*)out, s_out, (const Elt<DTT>*)w, eps, scale,    \
                      B, n_q, n_codes)
   if (dtype == M3X_BF16 && n == 1024) M3X_FB_LAUNCH(1024, M3X_BF16);
   else if (dtype == M3X_F16 && n == 1024) M3X_FB_LAUNCH(1024, M3X_F16);
   else if (dtype == M3X_BF16 && n == 2048) M3X_FB_LAUNCH(2048, M3X_BF16);
   else if (dtype == M3X_F16 && n == 2048) M3X_FB_LAUNCH(2048, M3X_F16);
+  else if (dtype == M3X_F32 && n == 1024) M3X_FB_LAUNCH(1024, M3X_F32);
+  else if (dtype == M3X_F32 && n == 2048) M3X_FB_LAUNCH(2048, M3X_F32);
   else return M3X_EUNSUPPORTED;
 #undef M3X_FB_LAUNCH
   M3X_CHECK_LAUNCH();

@@ -27,21 +27,22 @@
 // 137-138 and the first norm of the next level, :164): e = table[code] is written to prefix[b]; with y given,
 // xo[b] = e and y[b] = norm(e) (norm_vec over 8*TPR elements, the add+norm kernel's arithmetic with no addend),
 // which replaces a row copy and a norm launch per codebook.
+// Rows of the kernel's storage type (Elt<DT>); kept untyped here so one struct serves every dtype.
 struct EmbedArgs {
-  const uint16_t* table;
+  const void* table;
   long ld_table, table_rows;
-  uint16_t* prefix;
+  void* prefix;
   long ld_prefix;
-  uint16_t* xo;
-  uint16_t* y;
-  const uint16_t* w;
-  const uint16_t* b;
+  void* xo;
+  void* y;
+  const void* w;
+  const void* b;
   float eps;
   int kind;
 };
 
 template <int DT, int TPR, int NE>
-__global__ __launch_bounds__(ST) void topk_sample_kernel(const uint16_t* __restrict__ logits, long ld_l, int V,
+__global__ __launch_bounds__(ST) void topk_sample_kernel(const Elt<DT>* __restrict__ logits, long ld_l, int V,
                                                          const float* __restrict__ u, long ld_u, float inv_temp,
                                                          int top_k, int greedy, void* out, long ld_out, int out_i64,
                                                          EmbedArgs ea) {
@@ -80,23 +81,24 @@ __global__ __launch_bounds__(ST) void topk_sample_kernel(const uint16_t* __restr
     long cr = sm.code;
     cr = cr < 0 ? 0 : (cr >= ea.table_rows ? ea.table_rows - 1 : cr);
     float v[8];
-    u16x8 wv = {}, bv = {};
+    using T = Elt<DT>;
+    V8<DT> wv = zero_v8<DT>(), bv = zero_v8<DT>();
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = 0.f;
     if (act) {
-      const u16x8 ev = ld16(ea.table + cr * ea.ld_table + 8 * t);
+      const V8<DT> ev = ldv<DT>((const T*)ea.table + cr * ea.ld_table + 8 * t);
       if (ea.y) {
-        wv = ld16(ea.w + 8 * t);
-        if (ea.kind == M3X_NORM_LAYER) bv = ld16(ea.b + 8 * t);
+        wv = ldv<DT>((const T*)ea.w + 8 * t);
+        if (ea.kind == M3X_NORM_LAYER) bv = ldv<DT>((const T*)ea.b + 8 * t);
       }
-      st16(ea.prefix + (long)row * ea.ld_prefix + 8 * t, ev);
-      if (ea.xo) st16(ea.xo + (long)row * N + 8 * t, ev);
+      stv<DT>((T*)ea.prefix + (long)row * ea.ld_prefix + 8 * t, ev);
+      if (ea.xo) stv<DT>((T*)ea.xo + (long)row * N + 8 * t, ev);
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[e] = E<DT>::to_f(ev.v[e]);
     }
     if (ea.y) {
-      const u16x8 yv = norm_vec<TPR, DT>(v, wv, bv, ea.kind, ea.eps, red, bcast);
-      if (act) st16(ea.y + (long)row * N + 8 * t, yv);
+      const V8<DT> yv = norm_vec<TPR, DT>(v, wv, bv, ea.kind, ea.eps, red, bcast);
+      if (act) stv<DT>((T*)ea.y + (long)row * N + 8 * t, yv);
     }
   }
 }
@@ -110,12 +112,14 @@ M3X_API int m3x_topk_sample(const void* logits, long ld_l, int V, const float* u
   hipStream_t st = (hipStream_t)stream;
   const EmbedArgs ea{};
 #define M3X_TS(DTT, NEE)                                                                                             \
-  hipLaunchKernelGGL((topk_sample_kernel<DTT, 0, NEE>), dim3(B), dim3(ST), 0, st, (const uint16_t*)logits, ld_l, V, \
+  hipLaunchKernelGGL((topk_sample_kernel<DTT, 0, NEE>), dim3(B), dim3(ST), 0, st, (const Elt<DTT>*)logits, ld_l, V, \
                      u, ld_u, inv_temp, top_k, greedy, out, ld_out, out_i64, ea)
   if (dtype == M3X_BF16 && V <= 2048) M3X_TS(M3X_BF16, 8);
   else if (dtype == M3X_BF16) M3X_TS(M3X_BF16, 16);
   else if (dtype == M3X_F16 && V <= 2048) M3X_TS(M3X_F16, 8);
   else if (dtype == M3X_F16) M3X_TS(M3X_F16, 16);
+  else if (dtype == M3X_F32 && V <= 2048) M3X_TS(M3X_F32, 8);
+  else if (dtype == M3X_F32) M3X_TS(M3X_F32, 16);
   else return M3X_EUNSUPPORTED;
 #undef M3X_TS
   M3X_CHECK_LAUNCH();
@@ -140,21 +144,22 @@ M3X_API int m3x_topk_sample_embed(const void* logits, long ld_l, int V, const fl
       (y && !m3x_aligned16(y)) || (w && !m3x_aligned16(w)) || (b && !m3x_aligned16(b)))
     return M3X_EINVAL;
   hipStream_t st = (hipStream_t)stream;
-  const EmbedArgs ea{(const uint16_t*)table, ld_table, table_rows, (uint16_t*)prefix, ld_prefix,
-                     y ? (uint16_t*)x_out : nullptr, (uint16_t*)y, (const uint16_t*)w, (const uint16_t*)b, eps, kind};
+  const EmbedArgs ea{table, ld_table, table_rows, prefix, ld_prefix, y ? x_out : nullptr, y, w, b, eps, kind};
 #define M3X_TSE(DTT, TT)                                                                                      \
   do {                                                                                                     \
     if (V <= 2048)                                                                                         \
-      hipLaunchKernelGGL((topk_sample_kernel<DTT, TT, 8>), dim3(B), dim3(ST), 0, st, (const uint16_t*)logits, \
+      hipLaunchKernelGGL((topk_sample_kernel<DTT, TT, 8>), dim3(B), dim3(ST), 0, st, (const Elt<DTT>*)logits,  \
                          ld_l, V, u, ld_u, inv_temp, top_k, greedy, out, ld_out, out_i64, ea);               \
     else                                                                                                   \
-      hipLaunchKernelGGL((topk_sample_kernel<DTT, TT, 16>), dim3(B), dim3(ST), 0, st, (const uint16_t*)logits, \
+      hipLaunchKernelGGL((topk_sample_kernel<DTT, TT, 16>), dim3(B), dim3(ST), 0, st, (const Elt<DTT>*)logits, \
                          ld_l, V, u, ld_u, inv_temp, top_k, greedy, out, ld_out, out_i64, ea);               \
   } while (0)
   if (dtype == M3X_BF16 && n == 1024) M3X_TSE(M3X_BF16, 128);
   else if (dtype == M3X_F16 && n == 1024) M3X_TSE(M3X_F16, 128);
   else if (dtype == M3X_BF16 && n == 2048) M3X_TSE(M3X_BF16, 256);
   else if (dtype == M3X_F16 && n == 2048) M3X_TSE(M3X_F16, 256);
+  else if (dtype == M3X_F32 && n == 1024) M3X_TSE(M3X_F32, 128);
+  else if (dtype == M3X_F32 && n == 2048) M3X_TSE(M3X_F32, 256);
   else return M3X_EUNSUPPORTED;
 #undef M3X_TSE
   M3X_CHECK_LAUNCH();

@@ -37,6 +37,14 @@ def _dt(t: torch.Tensor) -> int:
     return _DT[t.dtype]
 
 
+def _dt3(t: torch.Tensor) -> int:
+    """dtype code for the entry points that also have an fp32 instance (projections, depth norms / attention /
+    sampler / feedback, and the codec's kernels)."""
+    if t.dtype not in _DT_ANY:
+        raise ValueError(f"m3x kernels take bfloat16, float16 or float32 tensors, got {t.dtype}")
+    return _DT_ANY[t.dtype]
+
+
 def _dev(*ts):
     for t in ts:
         if t is not None and not t.is_cuda:
@@ -163,7 +171,8 @@ def attn_items(runs, heads, kv_heads, bins, chunk):
 
 
 class PackedWeight:
-    """An [N, K] 16-bit weight in MFMA fragment order (see m3x_pack_weight): `data` holds ceil(N/16)*16*K elements."""
+    """An [N, K] weight (bf16, fp16 or fp32) in MFMA fragment order (see m3x_pack_weight): `data` holds
+    ceil(N/16)*16*K elements."""
     __slots__ = ("data", "N", "K")
 
     def __init__(self, data, N, K):
@@ -193,7 +202,7 @@ def pack_weight(w):
     if n < 0:
         raise ValueError(f"pack_weight: K={K} must be a multiple of 32")
     out = torch.empty(n, dtype=w.dtype, device=w.device)
-    check(lib().m3x_pack_weight(_p(w), w.stride(0), N, K, _p(out), _stream()), "pack_weight")
+    check(lib().m3x_pack_weight(_p(w), w.stride(0), N, K, _p(out), _dt3(w), _stream()), "pack_weight")
     return PackedWeight(out, N, K)
 
 
@@ -216,7 +225,7 @@ def _lin_args(x, w, y, N):
 def linear(x, w, y=None):
     """y = x @ W.T with x [M, K] and W [N, K] packed by pack_weight (same dtype); returns y [M, N]."""
     M, K, y = _lin_args(x, w, y, w.N)
-    check(lib().m3x_linear(_p(x), x.stride(0), _p(w.data), _p(y), y.stride(0), M, w.N, K, _dt(x), _stream()),
+    check(lib().m3x_linear(_p(x), x.stride(0), _p(w.data), _p(y), y.stride(0), M, w.N, K, _dt3(x), _stream()),
           "linear")
     return y
 
@@ -230,7 +239,7 @@ def linear_act(x, w_gate, w_up, kind, y=None):
             raise ValueError("linear_act: w_up must be a packed weight of w_gate's shape")
         _dev(w_up.data)
     check(lib().m3x_linear_act(_p(x), x.stride(0), _p(w_gate.data), _p(w_up.data if kind == ACT_SWIGLU else None),
-                               _p(y), y.stride(0), M, I, K, kind, _dt(x), _stream()), "linear_act")
+                               _p(y), y.stride(0), M, I, K, kind, _dt3(x), _stream()), "linear_act")
     return y
 
 
@@ -263,7 +272,7 @@ def add_norm(x, a, c, x_out, y, w, b, eps, T, kind):
     sxb, sxt = _bt_strides(x, T)
     sab, sat = _bt_strides(a, T) if a is not None else (0, 0)
     check(lib().m3x_add_norm(_p(x), sxb, sxt, _p(a), sab, sat, _p(c), 0 if c is None else c.stride(0), _p(x_out),
-                             _p(y), _p(w), _p(b), float(eps), rows, T, n, kind, _dt(y), _stream()), "add_norm")
+                             _p(y), _p(w), _p(b), float(eps), rows, T, n, kind, _dt3(y), _stream()), "add_norm")
 
 
 def add_rows(x, bias, out):
@@ -271,7 +280,7 @@ def add_rows(x, bias, out):
     _dev(x, bias, out)
     ldb = 0 if bias.dim() == 1 else bias.stride(0)
     check(lib().m3x_add_rows(_p(x), x.stride(0), _p(bias), ldb, _p(out), out.stride(0), x.shape[0], x.shape[-1],
-                             _dt(x), _stream()), "add_rows")
+                             _dt3(x), _stream()), "add_rows")
 
 
 def depth_attn(qkv, kd, vd, out, B, T, p0, tq0, heads, head_dim, scale, write_kv=True):
@@ -279,7 +288,7 @@ def depth_attn(qkv, kd, vd, out, B, T, p0, tq0, heads, head_dim, scale, write_kv
     sqb, sqt = _bt_strides(qkv, T)
     sob, sot = _bt_strides(out, T - tq0)
     check(lib().m3x_depth_attn(_p(qkv), sqb, sqt, _p(kd), _p(vd), _p(out), sob, sot, B, T, p0, tq0, heads, head_dim,
-                               kd.shape[2], float(scale), int(write_kv), _dt(qkv), _stream()), "depth_attn")
+                               kd.shape[2], float(scale), int(write_kv), _dt3(qkv), _stream()), "depth_attn")
 
 
 def topk_sample(logits, u, inv_temp, top_k, greedy, out, out_i64=False):
@@ -289,7 +298,7 @@ def topk_sample(logits, u, inv_temp, top_k, greedy, out, out_i64=False):
     B, V = logits.shape
     check(lib().m3x_topk_sample(_p(logits), logits.stride(0), V, _p(u), 0 if u is None else u.stride(0),
                                 float(inv_temp), int(top_k), int(greedy), _p(out), out.stride(0), int(out_i64), B,
-                                _dt(logits), _stream()), "topk_sample")
+                                _dt3(logits), _stream()), "topk_sample")
 
 
 def topk_sample_embed(logits, u, inv_temp, top_k, greedy, out, table, prefix, x_out=None, y=None, w=None, b=None,
@@ -314,7 +323,7 @@ def topk_sample_embed(logits, u, inv_temp, top_k, greedy, out, table, prefix, x_
     check(lib().m3x_topk_sample_embed(
         _p(logits), logits.stride(0), V, _p(u), 0 if u is None else u.stride(0), float(inv_temp), int(top_k),
         int(greedy), _p(out), out.stride(0), int(out_i64), B, _p(table), table.stride(0), table.shape[0], _p(prefix),
-        prefix.stride(0), _p(x_out), _p(y), _p(w), _p(b), float(eps), int(kind), n, _dt(logits), _stream()),
+        prefix.stride(0), _p(x_out), _p(y), _p(w), _p(b), float(eps), int(kind), n, _dt3(logits), _stream()),
         "topk_sample_embed")
 
 
@@ -369,15 +378,19 @@ def feedback(table, codes, out, w, eps, scale, n_q, n_codes):
     _dev(table, codes, out, w)
     _need(codes, torch.int32, "codes")
     check(lib().m3x_feedback(_p(table), _p(codes), codes.stride(0), _p(out), out.stride(0), _p(w), float(eps),
-                             float(scale), out.shape[0], out.shape[1], int(n_q), int(n_codes), _dt(table),
+                             float(scale), out.shape[0], out.shape[1], int(n_q), int(n_codes), _dt3(table),
                              _stream()), "feedback")
 
 
 def copy_rows(src, dst, src_idx=None, src_off=0, dst_idx=None, rows=None):
-    """dst[dst_idx[r] or r] = src[src_idx[r] + src_off or r] for r < rows (16-bit rows, width % 8 == 0)."""
+    """dst[dst_idx[r] or r] = src[src_idx[r] + src_off or r] for r < rows (rows of 16-bit elements with
+    width % 8 == 0, or of fp32 elements with width % 4 == 0, moved as pairs of 16-bit halves)."""
     _dev(src, dst, src_idx, dst_idx)
-    n = src.shape[-1]
-    if dst.shape[-1] != n:
+    if src.dtype != dst.dtype or src.element_size() not in (2, 4):
+        raise ValueError(f"copy_rows: {src.dtype} -> {dst.dtype}")
+    w = src.element_size() // 2  # 16-bit units per element
+    n = src.shape[-1] * w
+    if dst.shape[-1] * w != n:
         raise ValueError("copy_rows: row widths differ")
     if rows is None:
         rows = src_idx.numel() if src_idx is not None else (dst_idx.numel() if dst_idx is not None else src.shape[0])
@@ -391,8 +404,8 @@ def copy_rows(src, dst, src_idx=None, src_off=0, dst_idx=None, rows=None):
         ld_idx = src_idx.stride(0)
     if dst_idx is not None:
         _need(dst_idx, torch.long, "dst_idx")
-    check(lib().m3x_copy_rows(_p(src), src.stride(-2), _p(src_idx), int(src_off), src.shape[-2], _p(dst),
-                              dst.stride(-2), _p(dst_idx), int(rows), n, idx_i32, ld_idx, _stream()), "copy_rows")
+    check(lib().m3x_copy_rows(_p(src), src.stride(-2) * w, _p(src_idx), int(src_off), src.shape[-2], _p(dst),
+                              dst.stride(-2) * w, _p(dst_idx), int(rows), n, idx_i32, ld_idx, _stream()), "copy_rows")
 
 
 def cast_rows(src, dst):

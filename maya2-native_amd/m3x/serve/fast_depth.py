@@ -72,8 +72,8 @@ class FastDepth:
                  fused=False):
         if model.depth.n_q != N_LEVELS:
             raise ValueError('FastDepth expects the 32-codebook depth stack')
-        if dtype not in (torch.bfloat16, torch.float16):
-            raise ValueError(f'FastDepth computes in bfloat16 or float16, got {dtype}')
+        if dtype not in (torch.bfloat16, torch.float16, torch.float32):
+            raise ValueError(f'FastDepth computes in bfloat16, float16 or float32, got {dtype}')
         lib()
         self.max_slots, self.dtype = int(max_slots), dtype
         self.temp, self.top_k, self.greedy, self.fused = float(temp), int(top_k), bool(greedy), bool(fused)
@@ -127,7 +127,7 @@ class FastDepth:
                                                        for c in self.cross]
         self.audio_in = model.audio_in  # shared and read-only, in the engine's dtype
         table = model.audio_in.table.weight
-        if table.dtype not in (torch.bfloat16, torch.float16):
+        if table.dtype not in (torch.bfloat16, torch.float16, torch.float32):
             table = table.detach().to(torch.bfloat16).contiguous()  # the serving dtype of the feedback table
         self.fb_table = table
         self.fb_norm = _norm_spec(model.audio_in.norm, table.dtype, dev)
@@ -272,7 +272,8 @@ class FastDepth:
         one (seat, head) pair per residual workgroup, one workgroup per CU on a 256-CU part, the trunk geometries the
         kernel implements (width 1024, 2048 codes, SwiGLU 2816 with 128-wide heads or GELU 3072 with 64-wide
         heads; RMSNorm with SwiGLU, LayerNorm with GELU) in bf16 or fp16."""
-        if not self.persistent or B > self.PERSISTENT_SEATS or B * self.H > 192 or self._nwg != 256:
+        if (not self.persistent or self.dtype == torch.float32 or B > self.PERSISTENT_SEATS or B * self.H > 192
+                or self._nwg != 256):
             return False
         layers = self.trunks[group]
         kinds = {L.n1.kind for L in layers} | {L.n2.kind for L in layers} | {self.final_norm.kind}

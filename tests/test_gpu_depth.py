@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import bf16_bits, close, convert, floor_check
+from helpers import bf16_bits, close, convert, floor_check, rel_l2, report
 from m3x import synth
 from oracle import coracle as C
 from oracle import torch_oracle as O
@@ -41,10 +41,16 @@ def _check(fd, model_c, h, cb0, gpu, dt, temp, top_k, cross=None, logit_tol=None
     assert (fd.row_ctr.cpu() - ctr0).tolist() == [1 if s in SLOTS else 0 for s in range(fd.max_slots + 1)]
     # sampling: bit-exact given the kernel's logits and uniforms
     for lv in range(1, 32):
-        ref = C.topk_sample_rows(bf16_bits(logits[:, lv - 1]), 1.0 / temp, top_k, u[:, lv - 1].numpy(),
-                                 is_f16=dt == torch.float16)
+        if dt == torch.float32:
+            xs = logits[:, lv - 1].numpy() * np.float32(1.0 / temp)
+            ref = np.array([C.topk_sample(xs[r], top_k, float(u[r, lv - 1])) for r in range(B)])
+        else:
+            ref = C.topk_sample_rows(bf16_bits(logits[:, lv - 1]), 1.0 / temp, top_k, u[:, lv - 1].numpy(),
+                                     is_f16=dt == torch.float16)
         assert np.array_equal(codes[:, lv].numpy(), ref), lv
     assert torch.equal(codes[:, 0], cb0)
+    if dt == torch.float32:
+        return _check_f32(model_c, h, cb0, u, temp, top_k, codes, fb, logits, cross)
     # logits: teacher-forced CPU oracle on the same codes, against the fp32 evaluation's noise floor
     _, ref_logits = O.depth_frame(model_c, h, cb0, u, temp, top_k, forced=codes, cross=cross, dt=dt)
     m32 = convert(model_c, torch.float32)
@@ -53,6 +59,26 @@ def _check(fd, model_c, h, cb0, gpu, dt, temp, top_k, cross=None, logit_tol=None
     ok, info = floor_check(logits, ref_logits, truth)
     assert ok, info
     ok, info = close(fb, O.feedback(model_c.audio_in, codes).float())
+    assert ok, info
+    return codes, fb
+
+
+# fp32 bar: the kernel and the oracle evaluate the same fp32 math in different summation orders (MFMA 16x16x4
+# f32 blocks against torch's CPU matmul), so they differ by fp32 rounding alone, ~sqrt(K) * 2^-24 relative per
+# projection over 4 layers x 31 levels; the reference's fp32 FastDepth is its own precision baseline
+# (maya3/tests/test_depth_fused.py:30-31).
+F32_REL_L2, F32_MAX_ABS = 1e-5, 1e-5
+
+
+def _check_f32(model_c, h, cb0, u, temp, top_k, codes, fb, logits, cross):
+    _, ref_logits = O.depth_frame(model_c, h, cb0, u, temp, top_k, forced=codes, cross=cross, dt=torch.float32)
+    err = rel_l2(logits, ref_logits)
+    max_abs = (logits.float() - ref_logits.float()).abs().max().item()
+    scale = ref_logits.abs().max().item()
+    report("fastdepth fp32 logits", dict(rel_l2=err, max_abs=max_abs, max_logit=scale))
+    assert err <= F32_REL_L2 and max_abs <= F32_MAX_ABS * max(1.0, scale), (err, max_abs, scale)
+    ref_fb = O.feedback(model_c.audio_in, codes).float()
+    ok, info = close(fb, ref_fb)
     assert ok, info
     return codes, fb
 
@@ -90,6 +116,42 @@ def test_depthv2_geometry_fp16_with_speaker(gpu):
     cb0 = torch.randint(0, 2048, (B,), generator=g)
     cross = fd.cross_const[SLOTS].cpu()
     _check(fd, model_c, h, cb0, gpu, torch.float16, 0.7, 64, cross=cross)
+
+
+def test_swiglu_depth_frame_fp32(gpu):
+    """FastDepth(dtype=torch.float32): the engine's depth_dtype="fp32" (maya3/engine.py:53,192-199) and the
+    reference's own fp32 FastDepth (maya3/tests/test_depth_fused.py:30-31). Launch path, fp32 kernels throughout."""
+    from m3x.serve.fast_depth import FastDepth
+    model_g = convert(synth.swiglu_depth(seed=33, device=gpu), torch.float32)
+    model_c = convert(synth.swiglu_depth(seed=33, device="cpu"), torch.float32)
+    fd = FastDepth(model_g, 8, dtype=torch.float32, temp=0.9, top_k=50, batch_buckets=(B,), fused=True)
+    assert not fd._persistent_ok(B, 0)
+    g = torch.Generator().manual_seed(34)
+    h = torch.randn(B, 1024, generator=g)
+    cb0 = torch.randint(0, 2048, (B,), generator=g)
+    _check(fd, model_c, h, cb0, gpu, torch.float32, 0.9, 50)
+
+
+def test_depthv2_geometry_fp32_with_speaker(gpu):
+    """The reference's DepthV2 shape (LayerNorm + GELU, 16 x 64 heads, weight groups with group starts and
+    incremental levels, speaker constants) in fp32, as the reference's fp32 FastDepth runs it."""
+    from m3x.serve.fast_depth import FastDepth
+    gol = [None] + [0] * 3 + [1] * 8 + [2] * 20
+    mk = lambda dev: synth.depthv2_like(group_of_level=gol, seed=43, device=dev, affine_std=0.1)  # noqa: E731
+    model_g, model_c = mk(gpu), mk("cpu")
+    fd = FastDepth(model_g, 8, dtype=torch.float32, temp=0.7, top_k=64, batch_buckets=(B,), fused=True)
+    g = torch.Generator().manual_seed(44)
+    mems = torch.randn(8, 1, 1, 1024, generator=g)
+    for s in range(8):
+        fd.set_speaker(s, mems[s].to(gpu), torch.ones(1, 1, device=gpu))
+    d = model_c.depth
+    ref_cross = torch.stack([torch.stack([O.lin(O.lin(mems[s, 0], c.kv.weight)[:, 1024:], c.o.weight)[0]
+                                          for c in d.cross]) for s in range(8)])
+    assert rel_l2(fd.cross_const[:8], ref_cross) <= F32_REL_L2
+    h = torch.randn(B, 1024, generator=g)
+    cb0 = torch.randint(0, 2048, (B,), generator=g)
+    cross = fd.cross_const[SLOTS].cpu()
+    _check(fd, model_c, h, cb0, gpu, torch.float32, 0.7, 64, cross=cross)
 
 
 def test_graph_replay_equals_eager(gpu):
