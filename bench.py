@@ -265,12 +265,34 @@ def secondary(torch, bb, dm, steps):
 def mimi_decode(torch, dev, steps):
     """One 80 ms Mimi frame per seat (32 codes -> 1920 PCM samples) through StaticMimi's graph at 1, 64 and 224
     seats (HIP-event time of the replay, and the wall time of decode() with its slot/code uploads and the owned
-    output), beside one frame of the fp32 streaming oracle on the host at one seat."""
+    output), beside one frame of the fp32 streaming oracle on the host at one seat. The headline figures compute in
+    float32, the Mimi module's dtype and so the reference's precision (serve/fast_codec.py:47-49,
+    maya3/engine.py:165,201); the `fp16` object is the opt-in float16 variant."""
+    from m3x import synth
+    from oracle.mimi_oracle import MimiStream
+    res = _mimi_variant(torch, dev, steps, torch.float32)
+    res["fp16"] = _mimi_variant(torch, dev, steps, torch.float16)
+    mc = synth.mimi(seed=7)
+    st = MimiStream(mc, 1)
+    c = synth.mimi_codes(1, 4, seed=8)
+    with torch.no_grad():
+        st.decode_frame(c[:, :, 0])
+        t0 = time.perf_counter()
+        for t in range(1, 4):
+            st.decode_frame(c[:, :, t])
+    res["cpu_oracle_ms_b1"] = round((time.perf_counter() - t0) / 3 * 1e3, 2)
+    res["cpu_cores"] = torch.get_num_threads()
+    res["note"] = ("StaticMimi in float32 (the reference's precision; the fp16 object: float16 storage with fp32 "
+                   "accumulation); realtime_x = seconds of audio per second of GPU time; CPU: the fp32 streaming "
+                   "oracle, one seat")
+    return res
+
+
+def _mimi_variant(torch, dev, steps, dtype):
     from m3x import synth
     from m3x.serve.fast_codec import StaticMimi
-    from oracle.mimi_oracle import MimiStream
-    sm = StaticMimi(synth.mimi(seed=7, device=dev), 224, batch_buckets=(1, 64, 224))
-    res = {}
+    sm = StaticMimi(synth.mimi(seed=7, device=dev), 224, batch_buckets=(1, 64, 224), dtype=dtype)
+    res = {"dtype": str(dtype).replace("torch.", "")}
     stream = torch.cuda.current_stream()
     with torch.inference_mode():
         sm.warmup()
@@ -299,21 +321,10 @@ def mimi_decode(torch, dev, steps):
             res[f"b{B}"] = {"seats": B, "graph_ms": round(gpu_ms, 4), "decode_wall_ms": round(wall_ms, 4),
                             "frames_per_s": round(B / gpu_ms * 1e3, 1),
                             "realtime_x": round(B * 80.0 / gpu_ms, 1)}
-            log(f"Mimi decode, {B} seats: {gpu_ms:.3f} ms per frame in the graph, decode() {wall_ms:.3f} ms wall")
+            log(f"Mimi decode ({res['dtype']}), {B} seats: {gpu_ms:.3f} ms per frame in the graph, "
+                f"decode() {wall_ms:.3f} ms wall")
     del sm
     torch.cuda.empty_cache()
-    mc = synth.mimi(seed=7)
-    st = MimiStream(mc, 1)
-    c = synth.mimi_codes(1, 4, seed=8)
-    with torch.no_grad():
-        st.decode_frame(c[:, :, 0])
-        t0 = time.perf_counter()
-        for t in range(1, 4):
-            st.decode_frame(c[:, :, t])
-    res["cpu_oracle_ms_b1"] = round((time.perf_counter() - t0) / 3 * 1e3, 2)
-    res["cpu_cores"] = torch.get_num_threads()
-    res["note"] = ("StaticMimi computes in float16 with fp32 accumulation (the reference runs Mimi in float32); "
-                   "realtime_x = seconds of audio per second of GPU time; CPU: the fp32 streaming oracle, one seat")
     return res
 
 

@@ -11,9 +11,12 @@ constexpr int CODEC_THREADS = 256;
 constexpr int CODEC_KEEP = 16;
 constexpr long NEVER_POS = -(1L << 40);  // key_pos of an empty ring entry
 
-// ELU (alpha 1) with the hardware exp: exp(v) - 1 for v <= 0, absolute error ~1e-7, below the 16-bit storage step
-// of every value it produces.
-__device__ __forceinline__ float elu1(float v) { return v > 0.f ? v : __expf(v) - 1.f; }
+// ELU (alpha 1). 16-bit storage: the hardware exp, exp(v) - 1 for v <= 0, absolute error ~1e-7, below the storage
+// step of every value it produces. fp32 storage: expm1f, accurate to an ulp of the result near 0 as well.
+template <int DT> __device__ __forceinline__ float elu(float v) {
+  if constexpr (DT == M3X_F32) return v > 0.f ? v : expm1f(v);
+  else return v > 0.f ? v : __expf(v) - 1.f;
+}
 
 // ---------------------------------------------------------------------------------------------------------
 // RVQ decode (:134-149; transformers MimiSplitResidualVectorQuantizer.decode): out[b, :dim] = table_0[code_0]
@@ -22,7 +25,7 @@ __device__ __forceinline__ float elu1(float v) { return v > 0.f ? v : __expf(v) 
 // Codes outside [0, n_codes) are clamped into it (the reference's embedding lookup raises on them).
 template <int DT>
 __global__ __launch_bounds__(256) void rvq_decode_kernel(const int64_t* __restrict__ codes, long ld_codes,
-                                                         const uint16_t* __restrict__ tables, uint16_t* __restrict__ out,
+                                                         const Elt<DT>* __restrict__ tables, Elt<DT>* __restrict__ out,
                                                          long ld_out, int nq, int n_codes, int dim) {
   const int b = blockIdx.x;
   const int64_t* c = codes + (long)b * ld_codes;
@@ -40,12 +43,12 @@ __global__ __launch_bounds__(256) void rvq_decode_kernel(const int64_t* __restri
 // frame per seat: out[b * s + j, c] = x[b, c] w[c, j] + tail[slot, j, c] (j < k - s); the new tail[slot, j - s, c]
 // = x[b, c] w[c, j] for j >= s. Each thread owns channels, so its tail reads precede its tail writes.
 template <int DT>
-__global__ __launch_bounds__(256) void dwconvt_kernel(const uint16_t* __restrict__ x, long ld_x,
-                                                      const uint16_t* __restrict__ w, uint16_t* tail, long ld_tail,
-                                                      const int64_t* __restrict__ slots, uint16_t* __restrict__ out,
+__global__ __launch_bounds__(256) void dwconvt_kernel(const Elt<DT>* __restrict__ x, long ld_x,
+                                                      const Elt<DT>* __restrict__ w, Elt<DT>* tail, long ld_tail,
+                                                      const int64_t* __restrict__ slots, Elt<DT>* __restrict__ out,
                                                       int C, int k, int s) {
   const int b = blockIdx.x;
-  uint16_t* tl = tail + slots[b] * ld_tail;  // [k - s][C]
+  Elt<DT>* tl = tail + slots[b] * ld_tail;  // [k - s][C]
   for (int c = threadIdx.x; c < C; c += blockDim.x) {
     const float xv = E<DT>::to_f(x[(long)b * ld_x + c]);
     for (int j = 0; j < s; ++j) {
@@ -63,43 +66,43 @@ __global__ __launch_bounds__(256) void dwconvt_kernel(const uint16_t* __restrict
 // the reference stores the conv's own input). Grid (B, ceil(T / chunk)), chunk >= pad; 8 channels per thread.
 // cols == NULL only advances the history (after an m3x_conv_gemm that read it in place of the gathered rows).
 template <int DT>
-__device__ __forceinline__ u16x8 joined8(const uint16_t* st, const uint16_t* x, long ld_x, long row0, int pad, int i,
+__device__ __forceinline__ V8<DT> joined8(const Elt<DT>* st, const Elt<DT>* x, long ld_x, long row0, int pad, int i,
                                          int c, int C, int use_elu) {
-  if (i < pad) return ld16(st + (long)i * C + c);
-  u16x8 v = ld16(x + (row0 + i - pad) * ld_x + c);
+  if (i < pad) return ldv<DT>(st + (long)i * C + c);
+  V8<DT> v = ldv<DT>(x + (row0 + i - pad) * ld_x + c);
   if (use_elu) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v.v[e] = E<DT>::from_f(elu1(E<DT>::to_f(v.v[e])));
+    for (int e = 0; e < 8; ++e) v.v[e] = E<DT>::from_f(elu<DT>(E<DT>::to_f(v.v[e])));
   }
   return v;
 }
 
 template <int DT>
-__global__ __launch_bounds__(CODEC_THREADS) void conv_gather_kernel(const uint16_t* __restrict__ x, long ld_x,
-                                                                    uint16_t* state, long ld_state,
+__global__ __launch_bounds__(CODEC_THREADS) void conv_gather_kernel(const Elt<DT>* __restrict__ x, long ld_x,
+                                                                    Elt<DT>* state, long ld_state,
                                                                     const int64_t* __restrict__ slots,
-                                                                    uint16_t* __restrict__ cols, long ld_cols, int T,
+                                                                    Elt<DT>* __restrict__ cols, long ld_cols, int T,
                                                                     int C, int k, int dil, int use_elu, int chunk) {
   const int b = blockIdx.x;
   const int t0 = blockIdx.y * chunk, t1 = min(T, t0 + chunk);
   const int pad = (k - 1) * dil;
   const long row0 = (long)b * T;
-  uint16_t* st = pad ? state + slots[b] * ld_state : nullptr;  // [pad][C]
+  Elt<DT>* st = pad ? state + slots[b] * ld_state : nullptr;  // [pad][C]
   const int cv = C / 8, kcv = k * cv;
   for (int e = threadIdx.x; cols && e < (t1 - t0) * kcv; e += CODEC_THREADS) {
     const int t = t0 + e / kcv;
     const int r = e - (t - t0) * kcv;
     const int j = r / cv, c = 8 * (r - j * cv);
-    st16(cols + (row0 + t) * ld_cols + (long)j * C + c, joined8<DT>(st, x, ld_x, row0, pad, t + j * dil, c, C, use_elu));
+    stv<DT>(cols + (row0 + t) * ld_cols + (long)j * C + c, joined8<DT>(st, x, ld_x, row0, pad, t + j * dil, c, C, use_elu));
   }
   if (!pad || blockIdx.y) return;
-  u16x8 keep[CODEC_KEEP / 8];
+  V8<DT> keep[CODEC_KEEP / 8];
   int n = 0;
   for (int e = threadIdx.x; e < pad * cv; e += CODEC_THREADS)
     keep[n++] = joined8<DT>(st, x, ld_x, row0, pad, T + e / cv, 8 * (e % cv), C, use_elu);
   __syncthreads();
   n = 0;
-  for (int e = threadIdx.x; e < pad * cv; e += CODEC_THREADS) st16(st + 8 * e, keep[n++]);
+  for (int e = threadIdx.x; e < pad * cv; e += CODEC_THREADS) stv<DT>(st + 8 * e, keep[n++]);
 }
 
 // ---------------------------------------------------------------------------------------------------------
@@ -107,31 +110,31 @@ __global__ __launch_bounds__(CODEC_THREADS) void conv_gather_kernel(const uint16
 // Serves the conv biases (with the resnet shortcut and the ELU that follows it) and the transformer's
 // layer-scaled residuals. C % 8 == 0, 16-byte rows.
 template <int DT>
-__global__ __launch_bounds__(256) void rows_op_kernel(const uint16_t* __restrict__ g, long ld_g,
-                                                      const uint16_t* __restrict__ bias,
-                                                      const uint16_t* __restrict__ scale, const uint16_t* res,
-                                                      long ld_res, uint16_t* out, long ld_out, int rows, int C,
+__global__ __launch_bounds__(256) void rows_op_kernel(const Elt<DT>* __restrict__ g, long ld_g,
+                                                      const Elt<DT>* __restrict__ bias,
+                                                      const Elt<DT>* __restrict__ scale, const Elt<DT>* res,
+                                                      long ld_res, Elt<DT>* out, long ld_out, int rows, int C,
                                                       int use_elu) {
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
   const int cv = C / 8;
   if (i >= (long)rows * cv) return;
   const long r = i / cv;
   const int c = 8 * (int)(i - r * cv);
-  const u16x8 gv = ld16(g + r * ld_g + c);
-  u16x8 bv = {}, sv = {}, rv = {}, ov;
-  if (bias) bv = ld16(bias + c);
-  if (scale) sv = ld16(scale + c);
-  if (res) rv = ld16(res + r * ld_res + c);
+  const V8<DT> gv = ldv<DT>(g + r * ld_g + c);
+  V8<DT> bv = zero_v8<DT>(), sv = zero_v8<DT>(), rv = zero_v8<DT>(), ov;
+  if (bias) bv = ldv<DT>(bias + c);
+  if (scale) sv = ldv<DT>(scale + c);
+  if (res) rv = ldv<DT>(res + r * ld_res + c);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     float v = E<DT>::to_f(gv.v[e]);
     if (bias) v = v + E<DT>::to_f(bv.v[e]);
     if (scale) v = E<DT>::to_f(sv.v[e]) * v;
     if (res) v = E<DT>::to_f(rv.v[e]) + v;
-    if (use_elu) v = elu1(v);
+    if (use_elu) v = elu<DT>(v);
     ov.v[e] = E<DT>::from_f(v);
   }
-  st16(out + r * ld_out + c, ov);
+  stv<DT>(out + r * ld_out + c, ov);
 }
 
 // ---------------------------------------------------------------------------------------------------------
@@ -140,16 +143,16 @@ __global__ __launch_bounds__(256) void rows_op_kernel(const uint16_t* __restrict
 // transformer's `h = h + layer_scale(a)` followed by the next LayerNorm (serve/fast_codec.py:181-182,172,182).
 constexpr int RLN_N = 512;
 template <int DT>
-__global__ __launch_bounds__(256) void resid_ln_kernel(uint16_t* h, long ld_h, const uint16_t* __restrict__ a,
-                                                       long ld_a, const uint16_t* __restrict__ scale,
-                                                       const uint16_t* __restrict__ w, const uint16_t* __restrict__ b,
-                                                       uint16_t* __restrict__ y, long ld_y, float eps, int rows) {
+__global__ __launch_bounds__(256) void resid_ln_kernel(Elt<DT>* h, long ld_h, const Elt<DT>* __restrict__ a,
+                                                       long ld_a, const Elt<DT>* __restrict__ scale,
+                                                       const Elt<DT>* __restrict__ w, const Elt<DT>* __restrict__ b,
+                                                       Elt<DT>* __restrict__ y, long ld_y, float eps, int rows) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;  // a whole wave; the kernel has no block barrier
   const int c = 8 * (threadIdx.x & 63);
-  const u16x8 hv = ld16(h + row * ld_h + c), av = ld16(a + row * ld_a + c), sv = ld16(scale + c);
+  const V8<DT> hv = ldv<DT>(h + row * ld_h + c), av = ldv<DT>(a + row * ld_a + c), sv = ldv<DT>(scale + c);
   float v[8];
-  u16x8 ho;
+  V8<DT> ho;
   float sum = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -159,7 +162,7 @@ __global__ __launch_bounds__(256) void resid_ln_kernel(uint16_t* h, long ld_h, c
     v[e] = E<DT>::to_f(ho.v[e]);
     sum += v[e];
   }
-  st16(h + row * ld_h + c, ho);
+  stv<DT>(h + row * ld_h + c, ho);
   const float mean = wave_sum_xor(sum, 64) / (float)RLN_N;
   float sq = 0.f;
 #pragma unroll
@@ -168,11 +171,11 @@ __global__ __launch_bounds__(256) void resid_ln_kernel(uint16_t* h, long ld_h, c
     sq += v[e] * v[e];
   }
   const float inv = 1.f / sqrtf(wave_sum_xor(sq, 64) / (float)RLN_N + eps);
-  const u16x8 wv = ld16(w + c), bv = ld16(b + c);
-  u16x8 yo;
+  const V8<DT> wv = ldv<DT>(w + c), bv = ldv<DT>(b + c);
+  V8<DT> yo;
 #pragma unroll
   for (int e = 0; e < 8; ++e) yo.v[e] = E<DT>::from_f(v[e] * inv * E<DT>::to_f(wv.v[e]) + E<DT>::to_f(bv.v[e]));
-  st16(y + row * ld_y + c, yo);
+  stv<DT>(y + row * ld_y + c, yo);
 }
 
 // ---------------------------------------------------------------------------------------------------------
@@ -185,17 +188,17 @@ __global__ __launch_bounds__(256) void resid_ln_kernel(uint16_t* h, long ld_h, c
 // kk = j * C + c of the product is joined[t + j * dil][c] (m3x_conv_gather's rows: the slot's pad stored frames,
 // then x with ELU when pre_elu); the caller advances the history afterwards.
 struct ConvSrc {
-  const uint16_t* state;
+  const void* state;  // Elt<DT> rows
   long ld_state;
   const int64_t* slots;
   int T, C, dil, pad, pre_elu;
 };
 
 template <int DT, int NT, int MT, int G>
-__global__ __launch_bounds__(256) void conv_gemm_kernel(const uint16_t* __restrict__ X, long ldx,
-                                                        const uint16_t* __restrict__ Wp,
-                                                        const uint16_t* __restrict__ bias, const uint16_t* res,
-                                                        long ld_res, uint16_t* Y, long ldy, int M, int K,
+__global__ __launch_bounds__(256) void conv_gemm_kernel(const Elt<DT>* __restrict__ X, long ldx,
+                                                        const Elt<DT>* __restrict__ Wp,
+                                                        const Elt<DT>* __restrict__ bias, const Elt<DT>* res,
+                                                        long ld_res, Elt<DT>* Y, long ldy, int M, int K,
                                                         int use_elu, ConvSrc cs) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, li = l & 15, lg = l >> 4;
@@ -208,11 +211,11 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(const uint16_t* __restri
     for (int j = 0; j < MT; ++j) acc[t][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const int ks = K / 32;
   // the fragments of step s + 1 are in flight while step s multiplies
-  u16x8 a[2][NT], b[2][MT];
+  V8<DT> a[2][NT], b[2][MT];
   // gathered form: each row's seat, time and history row
   long xrow0[MT];
   int tt[MT];
-  const uint16_t* hist[MT];
+  const Elt<DT>* hist[MT];
 #pragma unroll
   for (int j = 0; j < MT; ++j) {
     const long row = m0 + 16 * j + li;
@@ -221,7 +224,7 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(const uint16_t* __restri
       const long bs = row / cs.T;
       tt[j] = (int)(row - bs * cs.T);
       xrow0[j] = bs * cs.T;
-      hist[j] = cs.pad ? cs.state + cs.slots[bs] * cs.ld_state : nullptr;
+      hist[j] = cs.pad ? (const Elt<DT>*)cs.state + cs.slots[bs] * cs.ld_state : nullptr;
     }
   }
   auto load = [&](int s, int buf) {
@@ -230,26 +233,26 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(const uint16_t* __restri
 #pragma unroll
     for (int j = 0; j < MT; ++j) {
       const long row = m0 + 16 * j + li;
-      b[buf][j] = u16x8{};
+      b[buf][j] = zero_v8<DT>();
       if (row < M) {
         if (!G) {
-          b[buf][j] = ld16(X + row * ldx + kk);
+          b[buf][j] = ldv<DT>(X + row * ldx + kk);
         } else {
           const int i = tt[j] + tap * cs.dil;
           if (i < cs.pad) {
-            b[buf][j] = ld16(hist[j] + (long)i * cs.C + c);
+            b[buf][j] = ldv<DT>(hist[j] + (long)i * cs.C + c);
           } else {
-            b[buf][j] = ld16(X + (xrow0[j] + i - cs.pad) * ldx + c);
+            b[buf][j] = ldv<DT>(X + (xrow0[j] + i - cs.pad) * ldx + c);
             if (cs.pre_elu) {
 #pragma unroll
-              for (int e = 0; e < 8; ++e) b[buf][j].v[e] = E<DT>::from_f(elu1(E<DT>::to_f(b[buf][j].v[e])));
+              for (int e = 0; e < 8; ++e) b[buf][j].v[e] = E<DT>::from_f(elu<DT>(E<DT>::to_f(b[buf][j].v[e])));
             }
           }
         }
       }
     }
 #pragma unroll
-    for (int t = 0; t < NT; ++t) a[buf][t] = ld16(Wp + ((long)t * ks + s) * 512 + 8 * l);
+    for (int t = 0; t < NT; ++t) a[buf][t] = ldv<DT>(Wp + ((long)t * ks + s) * 512 + 8 * l);
   };
   load(0, 0);
   for (int s = 0; s < ks; s += 2) {
@@ -257,13 +260,13 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(const uint16_t* __restri
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
-      for (int j = 0; j < MT; ++j) acc[t][j] = mfma16x16x32<DT>(a[0][t], b[0][j], acc[t][j]);
+      for (int j = 0; j < MT; ++j) acc[t][j] = mfma_k32<DT>(a[0][t], b[0][j], acc[t][j]);
     if (s + 1 >= ks) break;
     if (s + 2 < ks) load(s + 2, 0);
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
-      for (int j = 0; j < MT; ++j) acc[t][j] = mfma16x16x32<DT>(a[1][t], b[1][j], acc[t][j]);
+      for (int j = 0; j < MT; ++j) acc[t][j] = mfma_k32<DT>(a[1][t], b[1][j], acc[t][j]);
   }
   // lane (li, lg) holds columns 16 t + 4 lg + r of row m0 + 16 j + li. res may be y itself (in place): every
   // residual and bias value of the lane is read before its first store.
@@ -271,28 +274,53 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(const uint16_t* __restri
   for (int j = 0; j < MT; ++j) {
     const long m = m0 + 16 * j + li;
     if (m >= M) continue;
-    uint2 bb[NT], rr[NT];
+    if constexpr (DT == M3X_F32) {
+      float4 bb[NT], rr[NT];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const int n = 16 * t + 4 * lg;
-      bb[t] = bias ? *reinterpret_cast<const uint2*>(bias + n) : uint2{0, 0};
-      rr[t] = res ? *reinterpret_cast<const uint2*>(res + m * ld_res + n) : uint2{0, 0};
-    }
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const int n = 16 * t + 4 * lg;
-      const uint16_t* bv = reinterpret_cast<const uint16_t*>(&bb[t]);
-      const uint16_t* rv = reinterpret_cast<const uint16_t*>(&rr[t]);
-      uint16_t o[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float v = rnd<DT>(acc[t][j][r]);
-        if (bias) v = v + E<DT>::to_f(bv[r]);
-        if (res) v = E<DT>::to_f(rv[r]) + v;
-        if (use_elu) v = elu1(v);
-        o[r] = E<DT>::from_f(v);
+      for (int t = 0; t < NT; ++t) {
+        const int n = 16 * t + 4 * lg;
+        bb[t] = bias ? *reinterpret_cast<const float4*>(bias + n) : make_float4(0.f, 0.f, 0.f, 0.f);
+        rr[t] = res ? *reinterpret_cast<const float4*>(res + m * ld_res + n) : make_float4(0.f, 0.f, 0.f, 0.f);
       }
-      *reinterpret_cast<uint2*>(Y + m * ldy + n) = *reinterpret_cast<const uint2*>(o);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const int n = 16 * t + 4 * lg;
+        const float bv[4] = {bb[t].x, bb[t].y, bb[t].z, bb[t].w}, rv[4] = {rr[t].x, rr[t].y, rr[t].z, rr[t].w};
+        float o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float v = acc[t][j][r];
+          if (bias) v = v + bv[r];
+          if (res) v = rv[r] + v;
+          if (use_elu) v = elu<DT>(v);
+          o[r] = v;
+        }
+        *reinterpret_cast<float4*>(Y + m * ldy + n) = make_float4(o[0], o[1], o[2], o[3]);
+      }
+    } else {
+      uint2 bb[NT], rr[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const int n = 16 * t + 4 * lg;
+        bb[t] = bias ? *reinterpret_cast<const uint2*>(bias + n) : uint2{0, 0};
+        rr[t] = res ? *reinterpret_cast<const uint2*>(res + m * ld_res + n) : uint2{0, 0};
+      }
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const int n = 16 * t + 4 * lg;
+        const uint16_t* bv = reinterpret_cast<const uint16_t*>(&bb[t]);
+        const uint16_t* rv = reinterpret_cast<const uint16_t*>(&rr[t]);
+        uint16_t o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float v = rnd<DT>(acc[t][j][r]);
+          if (bias) v = v + E<DT>::to_f(bv[r]);
+          if (res) v = E<DT>::to_f(rv[r]) + v;
+          if (use_elu) v = elu<DT>(v);
+          o[r] = E<DT>::from_f(v);
+        }
+        *reinterpret_cast<uint2*>(Y + m * ldy + n) = *reinterpret_cast<const uint2*>(o);
+      }
     }
   }
 }
@@ -303,37 +331,37 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(const uint16_t* __restri
 // (o < k - s) + bias[c]; the new tail[slot, i, c] = the contributions to frame Tin * s + i, without bias (the
 // reference stores its tail bias-free). Grid (B, ceil(Tin * s / chunk)), chunk >= k - s; 8 channels per thread.
 template <int DT>
-__device__ __forceinline__ void convt_frame8(const uint16_t* cols, long ld_cols, long row0, int o, int c, int Tin,
+__device__ __forceinline__ void convt_frame8(const Elt<DT>* cols, long ld_cols, long row0, int o, int c, int Tin,
                                              int C, int k, int s, float (&v)[8]) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) v[e] = 0.f;
   for (int t = min(o / s, Tin - 1); t >= 0 && o - t * s < k; --t) {
-    const u16x8 w = ld16(cols + (row0 + t) * ld_cols + (long)(o - t * s) * C + c);
+    const V8<DT> w = ldv<DT>(cols + (row0 + t) * ld_cols + (long)(o - t * s) * C + c);
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] += E<DT>::to_f(w.v[e]);
   }
 }
 
 template <int DT>
-__global__ __launch_bounds__(CODEC_THREADS) void convt_overlap_kernel(const uint16_t* __restrict__ cols, long ld_cols,
-                                                                      uint16_t* tail, long ld_tail,
+__global__ __launch_bounds__(CODEC_THREADS) void convt_overlap_kernel(const Elt<DT>* __restrict__ cols, long ld_cols,
+                                                                      Elt<DT>* tail, long ld_tail,
                                                                       const int64_t* __restrict__ slots,
-                                                                      const uint16_t* __restrict__ bias,
-                                                                      uint16_t* __restrict__ out, long ld_out, int Tin,
+                                                                      const Elt<DT>* __restrict__ bias,
+                                                                      Elt<DT>* __restrict__ out, long ld_out, int Tin,
                                                                       int C, int k, int s, int chunk) {
   const int b = blockIdx.x;
   const int nout = Tin * s, ov = k - s;
   const int o0 = blockIdx.y * chunk, o1 = min(nout, o0 + chunk);
   const long row0 = (long)b * Tin;
-  uint16_t* tl = tail + slots[b] * ld_tail;  // [k - s][C]
+  Elt<DT>* tl = tail + slots[b] * ld_tail;  // [k - s][C]
   const int cv = C / 8;
   for (int e = threadIdx.x; e < (o1 - o0) * cv; e += CODEC_THREADS) {
     const int o = o0 + e / cv, c = 8 * (e % cv);
     float v[8];
     convt_frame8<DT>(cols, ld_cols, row0, o, c, Tin, C, k, s, v);
-    u16x8 tv = {}, bv = {}, r;
-    if (o < ov) tv = ld16(tl + (long)o * C + c);
-    if (bias) bv = ld16(bias + c);
+    V8<DT> tv = zero_v8<DT>(), bv = zero_v8<DT>(), r;
+    if (o < ov) tv = ldv<DT>(tl + (long)o * C + c);
+    if (bias) bv = ldv<DT>(bias + c);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       float y = v[i];
@@ -341,10 +369,10 @@ __global__ __launch_bounds__(CODEC_THREADS) void convt_overlap_kernel(const uint
       if (bias) y += E<DT>::to_f(bv.v[i]);
       r.v[i] = E<DT>::from_f(y);
     }
-    st16(out + ((long)b * nout + o) * ld_out + c, r);
+    stv<DT>(out + ((long)b * nout + o) * ld_out + c, r);
   }
   if (blockIdx.y) return;
-  u16x8 keep[CODEC_KEEP / 8];
+  V8<DT> keep[CODEC_KEEP / 8];
   int n = 0;
   for (int e = threadIdx.x; e < ov * cv; e += CODEC_THREADS) {
     float v[8];
@@ -355,7 +383,7 @@ __global__ __launch_bounds__(CODEC_THREADS) void convt_overlap_kernel(const uint
   }
   __syncthreads();
   n = 0;
-  for (int e = threadIdx.x; e < ov * cv; e += CODEC_THREADS) st16(tl + 8 * e, keep[n++]);
+  for (int e = threadIdx.x; e < ov * cv; e += CODEC_THREADS) stv<DT>(tl + 8 * e, keep[n++]);
 }
 
 // ---------------------------------------------------------------------------------------------------------
@@ -376,19 +404,19 @@ constexpr int RA_RING = 256;
 constexpr int RA_T = 2;  // tokens per call: Mimi's upsample makes 2 per frame
 static_assert(RA_T <= 4, "one wave of the 4-wave workgroup per token");
 template <int DT, int TM>
-__global__ __launch_bounds__(256) void ring_attn_kernel(const uint16_t* __restrict__ qkv, long ld_qkv,
-                                                        uint16_t* kring, uint16_t* vring, int64_t* key_pos,
+__global__ __launch_bounds__(256) void ring_attn_kernel(const Elt<DT>* __restrict__ qkv, long ld_qkv,
+                                                        Elt<DT>* kring, Elt<DT>* vring, int64_t* key_pos,
                                                         const int64_t* __restrict__ tokens,
                                                         const int64_t* __restrict__ slots,
                                                         const float* __restrict__ inv_freq, float rope_scale,
-                                                        uint16_t* __restrict__ out, long ld_out, int T, int H, int ring,
+                                                        Elt<DT>* __restrict__ out, long ld_out, int T, int H, int ring,
                                                         int window) {
   __shared__ float qs[TM][RA_HD];
   __shared__ float pw[TM][RA_RING];
   __shared__ float red[2][TM][4];
   __shared__ float part[4][TM][RA_HD];
-  __shared__ __align__(16) uint16_t knew[TM][RA_HD];  // this call's keys (post-RoPE) and values, stored to the
-  __shared__ __align__(16) uint16_t vnew[TM][RA_HD];  // ring only at the end: reads of them come from here
+  __shared__ __align__(16) Elt<DT> knew[TM][RA_HD];  // this call's keys (post-RoPE) and values, stored to the
+  __shared__ __align__(16) Elt<DT> vnew[TM][RA_HD];  // ring only at the end: reads of them come from here
   const int b = blockIdx.x, h = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
   const long slot = slots[b];
@@ -396,9 +424,9 @@ __global__ __launch_bounds__(256) void ring_attn_kernel(const uint16_t* __restri
   const int half = RA_HD / 2;
   const int partner = l < half ? l + half : l - half;
   float q_l = 0.f, q_p = 0.f, k_l = 0.f, k_p = 0.f;
-  uint16_t v_l = 0;
+  Elt<DT> v_l = 0;
   if (wave < T) {
-    const uint16_t* r = qkv + ((long)b * T + wave) * ld_qkv;
+    const Elt<DT>* r = qkv + ((long)b * T + wave) * ld_qkv;
     q_l = E<DT>::to_f(r[h * RA_HD + l]);
     q_p = E<DT>::to_f(r[h * RA_HD + partner]);
     k_l = E<DT>::to_f(r[(H + h) * RA_HD + l]);
@@ -406,8 +434,8 @@ __global__ __launch_bounds__(256) void ring_attn_kernel(const uint16_t* __restri
     v_l = r[(2 * H + h) * RA_HD + l];
   }
   const long p0 = tokens[slot];
-  uint16_t* kr = kring + slot * (long)ring * H * RA_HD;  // [ring][H][hd]
-  uint16_t* vr = vring + slot * (long)ring * H * RA_HD;
+  Elt<DT>* kr = kring + slot * (long)ring * H * RA_HD;  // [ring][H][hd]
+  Elt<DT>* vr = vring + slot * (long)ring * H * RA_HD;
   int64_t* kp = key_pos + slot * (long)ring;
   const int lo = (int)(p0 % ring);  // ring entry of token 0; token t sits at (lo + t) % ring
   // the older entries' keys, positions and values load now, while RoPE runs; this call's own rows come from LDS
@@ -416,22 +444,22 @@ __global__ __launch_bounds__(256) void ring_attn_kernel(const uint16_t* __restri
   const int j = tid;
   const int dd = (j - lo + ring) % ring;  // entries this call writes hold p0 + dd, dd < T
   long kj = NEVER_POS;
-  u16x8 k8[RA_HD / 8];
+  V8<DT> k8[RA_HD / 8];
 #pragma unroll
-  for (int d = 0; d < RA_HD / 8; ++d) k8[d] = u16x8{};
+  for (int d = 0; d < RA_HD / 8; ++d) k8[d] = zero_v8<DT>();
   if (j < ring && dd >= T) {
-    const uint16_t* krow = kr + ((long)j * H + h) * RA_HD;
+    const Elt<DT>* krow = kr + ((long)j * H + h) * RA_HD;
 #pragma unroll
-    for (int d = 0; d < RA_HD / 8; ++d) k8[d] = ld16(krow + 8 * d);
+    for (int d = 0; d < RA_HD / 8; ++d) k8[d] = ldv<DT>(krow + 8 * d);
     kj = kp[j];
   }
   const int g = l >> 3, dc = 8 * (l & 7);
-  u16x8 vv[8];
+  V8<DT> vv[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int jj = 64 * wave + g + 8 * i;
-    vv[i] = u16x8{};
-    if (jj < ring && (jj - lo + ring) % ring >= T) vv[i] = ld16(vr + ((long)jj * H + h) * RA_HD + dc);
+    vv[i] = zero_v8<DT>();
+    if (jj < ring && (jj - lo + ring) % ring >= T) vv[i] = ldv<DT>(vr + ((long)jj * H + h) * RA_HD + dc);
   }
   if (wave < T) {  // RoPE of token `wave`
     const float f = inv_freq[l < half ? l : l - half];
@@ -446,13 +474,13 @@ __global__ __launch_bounds__(256) void ring_attn_kernel(const uint16_t* __restri
   if (j < ring && dd < T) {
     kj = p0 + dd;
 #pragma unroll
-    for (int d = 0; d < RA_HD / 8; ++d) k8[d] = *reinterpret_cast<const u16x8*>(&knew[dd][8 * d]);
+    for (int d = 0; d < RA_HD / 8; ++d) k8[d] = *reinterpret_cast<const V8<DT>*>(&knew[dd][8 * d]);
   }
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int jj = 64 * wave + g + 8 * i;
     const int dn = (jj - lo + ring) % ring;
-    if (jj < ring && dn < T) vv[i] = *reinterpret_cast<const u16x8*>(&vnew[dn][dc]);
+    if (jj < ring && dn < T) vv[i] = *reinterpret_cast<const V8<DT>*>(&vnew[dn][dc]);
   }
   float sc[TM];
 #pragma unroll
@@ -553,8 +581,8 @@ __global__ void advance_tokens_kernel(int64_t* tokens, const int64_t* __restrict
 // weights from LDS); k * C <= 4096.
 constexpr int FC_W = 4096;
 template <int DT>
-__global__ __launch_bounds__(CODEC_THREADS) void final_conv_kernel(const uint16_t* __restrict__ x, long ld_x,
-                                                                   uint16_t* state, long ld_state,
+__global__ __launch_bounds__(CODEC_THREADS) void final_conv_kernel(const Elt<DT>* __restrict__ x, long ld_x,
+                                                                   Elt<DT>* state, long ld_state,
                                                                    const int64_t* __restrict__ slots,
                                                                    const float* __restrict__ w, float bias,
                                                                    float* __restrict__ pcm, long ld_pcm, int T, int C,
@@ -564,7 +592,7 @@ __global__ __launch_bounds__(CODEC_THREADS) void final_conv_kernel(const uint16_
   const int t0 = blockIdx.y * chunk, t1 = min(T, t0 + chunk);
   const int pad = k - 1;
   const long row0 = (long)b * T;
-  uint16_t* st = pad ? state + slots[b] * ld_state : nullptr;
+  Elt<DT>* st = pad ? state + slots[b] * ld_state : nullptr;
   for (int i = threadIdx.x; i < k * C; i += CODEC_THREADS) ws[i] = w[i];
   __syncthreads();
   const int cv = C / 8;
@@ -572,10 +600,10 @@ __global__ __launch_bounds__(CODEC_THREADS) void final_conv_kernel(const uint16_
     float acc = 0.f;
     for (int j = 0; j < k; ++j) {
       const int i = t + j;
-      const uint16_t* row = i < pad ? st + (long)i * C : x + (row0 + i - pad) * ld_x;
+      const Elt<DT>* row = i < pad ? st + (long)i * C : x + (row0 + i - pad) * ld_x;
       const float* wj = ws + j * C;
       for (int c8 = 0; c8 < cv; ++c8) {
-        const u16x8 v = ld16(row + 8 * c8);
+        const V8<DT> v = ldv<DT>(row + 8 * c8);
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc += wj[8 * c8 + e] * E<DT>::to_f(v.v[e]);
       }
@@ -583,26 +611,33 @@ __global__ __launch_bounds__(CODEC_THREADS) void final_conv_kernel(const uint16_
     pcm[(long)b * ld_pcm + t] = acc + bias;
   }
   if (!pad || blockIdx.y) return;
-  u16x8 keep[CODEC_KEEP / 8];
+  V8<DT> keep[CODEC_KEEP / 8];
   int n = 0;
   for (int e = threadIdx.x; e < pad * cv; e += CODEC_THREADS)
     keep[n++] = joined8<DT>(st, x, ld_x, row0, pad, T + e / cv, 8 * (e % cv), C, 0);
   __syncthreads();
   n = 0;
-  for (int e = threadIdx.x; e < pad * cv; e += CODEC_THREADS) st16(st + 8 * e, keep[n++]);
+  for (int e = threadIdx.x; e < pad * cv; e += CODEC_THREADS) stv<DT>(st + 8 * e, keep[n++]);
 }
 
 // ---------------------------------------------------------------------------------------------------------
 // C ABI
-#define CODEC_LAUNCH(KERNEL, GRID, BLOCK, ...)                                                 \
-  do {                                                                                         \
-    if (dtype == M3X_BF16)                                                                     \
-      hipLaunchKernelGGL(KERNEL<M3X_BF16>, GRID, BLOCK, 0, (hipStream_t)stream, __VA_ARGS__);  \
-    else if (dtype == M3X_F16)                                                                 \
-      hipLaunchKernelGGL(KERNEL<M3X_F16>, GRID, BLOCK, 0, (hipStream_t)stream, __VA_ARGS__);   \
-    else                                                                                       \
-      return M3X_EUNSUPPORTED;                                                                 \
-    M3X_CHECK_LAUNCH();                                                                        \
+// The arguments name the element type ET, which each branch binds to its dtype's storage type.
+#define CODEC_LAUNCH(KERNEL, GRID, BLOCK, ...)                                                   \
+  do {                                                                                           \
+    if (dtype == M3X_BF16) {                                                                     \
+      using ET = uint16_t;                                                                        \
+      hipLaunchKernelGGL(KERNEL<M3X_BF16>, GRID, BLOCK, 0, (hipStream_t)stream, __VA_ARGS__);    \
+    } else if (dtype == M3X_F16) {                                                               \
+      using ET = uint16_t;                                                                        \
+      hipLaunchKernelGGL(KERNEL<M3X_F16>, GRID, BLOCK, 0, (hipStream_t)stream, __VA_ARGS__);     \
+    } else if (dtype == M3X_F32) {                                                               \
+      using ET = float;                                                                            \
+      hipLaunchKernelGGL(KERNEL<M3X_F32>, GRID, BLOCK, 0, (hipStream_t)stream, __VA_ARGS__);     \
+    } else {                                                                                     \
+      return M3X_EUNSUPPORTED;                                                                   \
+    }                                                                                            \
+    M3X_CHECK_LAUNCH();                                                                          \
   } while (0)
 
 M3X_API int m3x_rvq_decode(const int64_t* codes, long ld_codes, const void* tables, void* out, long ld_out, int B,
@@ -610,7 +645,7 @@ M3X_API int m3x_rvq_decode(const int64_t* codes, long ld_codes, const void* tabl
   if (B < 0 || nq < 1 || n_codes < 1 || dim < 1 || ld_codes < nq || ld_out < 2L * dim) return M3X_EINVAL;
   if (B == 0) return M3X_OK;
   if (!codes || !tables || !out) return M3X_ENULL;
-  CODEC_LAUNCH(rvq_decode_kernel, dim3(B), dim3(256), codes, ld_codes, (const uint16_t*)tables, (uint16_t*)out,
+  CODEC_LAUNCH(rvq_decode_kernel, dim3(B), dim3(256), codes, ld_codes, (const ET*)tables, (ET*)out,
                ld_out, nq, n_codes, dim);
   return M3X_OK;
 }
@@ -620,8 +655,8 @@ M3X_API int m3x_dwconvt(const void* x, long ld_x, const void* w, void* tail, lon
   if (B < 0 || C < 1 || s < 1 || k < s || k > 2 * s || ld_x < C || ld_tail < (long)(k - s) * C) return M3X_EINVAL;
   if (B == 0) return M3X_OK;
   if (!x || !w || !tail || !slots || !out) return M3X_ENULL;
-  CODEC_LAUNCH(dwconvt_kernel, dim3(B), dim3(256), (const uint16_t*)x, ld_x, (const uint16_t*)w, (uint16_t*)tail,
-               ld_tail, slots, (uint16_t*)out, C, k, s);
+  CODEC_LAUNCH(dwconvt_kernel, dim3(B), dim3(256), (const ET*)x, ld_x, (const ET*)w, (ET*)tail,
+               ld_tail, slots, (ET*)out, C, k, s);
   return M3X_OK;
 }
 
@@ -637,8 +672,8 @@ M3X_API int m3x_conv_gather(const void* x, long ld_x, void* state, long ld_state
   if (B == 0) return M3X_OK;
   if (!x || !slots || (pad && !state)) return M3X_ENULL;
   if (!cols && !pad) return M3X_OK;
-  CODEC_LAUNCH(conv_gather_kernel, dim3(B, m3x_ceil_div(T, chunk)), dim3(CODEC_THREADS), (const uint16_t*)x, ld_x,
-               (uint16_t*)state, ld_state, slots, (uint16_t*)cols, ld_cols, T, C, k, dil, use_elu, chunk);
+  CODEC_LAUNCH(conv_gather_kernel, dim3(B, m3x_ceil_div(T, chunk)), dim3(CODEC_THREADS), (const ET*)x, ld_x,
+               (ET*)state, ld_state, slots, (ET*)cols, ld_cols, T, C, k, dil, use_elu, chunk);
   return M3X_OK;
 }
 
@@ -651,8 +686,8 @@ M3X_API int m3x_rows_op(const void* g, long ld_g, const void* bias, const void* 
   if (!m3x_aligned16(g) || !m3x_aligned16(out) || (bias && !m3x_aligned16(bias)) ||
       (scale && !m3x_aligned16(scale)) || (res && !m3x_aligned16(res)))
     return M3X_EINVAL;
-  CODEC_LAUNCH(rows_op_kernel, dim3(m3x_ceil_div((long)rows * (C / 8), 256)), dim3(256), (const uint16_t*)g, ld_g,
-               (const uint16_t*)bias, (const uint16_t*)scale, (const uint16_t*)res, ld_res, (uint16_t*)out, ld_out,
+  CODEC_LAUNCH(rows_op_kernel, dim3(m3x_ceil_div((long)rows * (C / 8), 256)), dim3(256), (const ET*)g, ld_g,
+               (const ET*)bias, (const ET*)scale, (const ET*)res, ld_res, (ET*)out, ld_out,
                rows, C, use_elu);
   return M3X_OK;
 }
@@ -669,7 +704,7 @@ M3X_API int m3x_convt_overlap(const void* cols, long ld_cols, void* tail, long l
   if (B == 0) return M3X_OK;
   if (!cols || !tail || !slots || !out) return M3X_ENULL;
   CODEC_LAUNCH(convt_overlap_kernel, dim3(B, m3x_ceil_div((long)Tin * s, chunk)), dim3(CODEC_THREADS),
-               (const uint16_t*)cols, ld_cols, (uint16_t*)tail, ld_tail, slots, (const uint16_t*)bias, (uint16_t*)out,
+               (const ET*)cols, ld_cols, (ET*)tail, ld_tail, slots, (const ET*)bias, (ET*)out,
                ld_out, Tin, C, k, s, chunk);
   return M3X_OK;
 }
@@ -687,10 +722,11 @@ M3X_API int m3x_ring_attn(const void* qkv, long ld_qkv, void* kring, void* vring
   if (!m3x_aligned16(out) || (ld_out & 7)) return M3X_EINVAL;
 #define RA_LAUNCH(DTT, TMM)                                                                                    \
   hipLaunchKernelGGL((ring_attn_kernel<DTT, TMM>), dim3(B, H), dim3(256), 0, (hipStream_t)stream,                  \
-                     (const uint16_t*)qkv, ld_qkv, (uint16_t*)kring, (uint16_t*)vring, key_pos, tokens, slots,      \
-                     inv_freq, rope_scale, (uint16_t*)out, ld_out, T, H, ring, window)
+                     (const Elt<DTT>*)qkv, ld_qkv, (Elt<DTT>*)kring, (Elt<DTT>*)vring, key_pos, tokens, slots,      \
+                     inv_freq, rope_scale, (Elt<DTT>*)out, ld_out, T, H, ring, window)
   if (dtype == M3X_F16) RA_LAUNCH(M3X_F16, RA_T);
   else if (dtype == M3X_BF16) RA_LAUNCH(M3X_BF16, RA_T);
+  else if (dtype == M3X_F32) RA_LAUNCH(M3X_F32, RA_T);
   else return M3X_EUNSUPPORTED;
 #undef RA_LAUNCH
   M3X_CHECK_LAUNCH();
@@ -716,8 +752,8 @@ M3X_API int m3x_final_conv(const void* x, long ld_x, void* state, long ld_state,
   if ((long)k * C > FC_W) return M3X_EINVAL;
   if (B == 0) return M3X_OK;
   if (!x || !slots || !w || !pcm || (k > 1 && !state)) return M3X_ENULL;
-  CODEC_LAUNCH(final_conv_kernel, dim3(B, m3x_ceil_div(T, chunk)), dim3(CODEC_THREADS), (const uint16_t*)x, ld_x,
-               (uint16_t*)state, ld_state, slots, w, bias, pcm, ld_pcm, T, C, k, chunk);
+  CODEC_LAUNCH(final_conv_kernel, dim3(B, m3x_ceil_div(T, chunk)), dim3(CODEC_THREADS), (const ET*)x, ld_x,
+               (ET*)state, ld_state, slots, w, bias, pcm, ld_pcm, T, C, k, chunk);
   return M3X_OK;
 }
 
@@ -729,8 +765,8 @@ M3X_API int m3x_resid_ln(void* h, long ld_h, const void* a, long ld_a, const voi
   if (!m3x_aligned16(h) || !m3x_aligned16(a) || !m3x_aligned16(scale) || !m3x_aligned16(w) || !m3x_aligned16(b) ||
       !m3x_aligned16(y))
     return M3X_EINVAL;
-  CODEC_LAUNCH(resid_ln_kernel, dim3(m3x_ceil_div(rows, 4)), dim3(256), (uint16_t*)h, ld_h, (const uint16_t*)a, ld_a,
-               (const uint16_t*)scale, (const uint16_t*)w, (const uint16_t*)b, (uint16_t*)y, ld_y, eps, rows);
+  CODEC_LAUNCH(resid_ln_kernel, dim3(m3x_ceil_div(rows, 4)), dim3(256), (ET*)h, ld_h, (const ET*)a, ld_a,
+               (const ET*)scale, (const ET*)w, (const ET*)b, (ET*)y, ld_y, eps, rows);
   return M3X_OK;
 }
 
@@ -739,7 +775,7 @@ M3X_API int m3x_conv_gemm(const void* x, long ldx, const void* w_packed, const v
                           long ld_state, const int64_t* slots, int T, int C, int dil, int pre_elu, int dtype,
                           void* stream) {
   // gathered form when C > 0: K = k * C, x rows [M, C], the slot's history of pad = (k - 1) * dil frames
-  ConvSrc cs{(const uint16_t*)state, ld_state, slots, T, C, dil, 0, pre_elu};
+  ConvSrc cs{state, ld_state, slots, T, C, dil, 0, pre_elu};
   const int G = C > 0;
   if (G) {
     if (T < 1 || C % 8 || K % C || M % T || dil < 1 || ldx < C || (ldx & 7)) return M3X_EINVAL;
@@ -756,25 +792,27 @@ M3X_API int m3x_conv_gemm(const void* x, long ldx, const void* w_packed, const v
     return M3X_EINVAL;
   const int mt = M >= 64 * 1024 ? 2 : 1;  // two row tiles per wave once the grid fills the chip anyway
   const dim3 grid(m3x_ceil_div(M, 4 * 16 * mt));
-  const uint16_t *X = (const uint16_t*)x, *W = (const uint16_t*)w_packed, *Bi = (const uint16_t*)bias,
-                 *R = (const uint16_t*)res;
-  uint16_t* Yp = (uint16_t*)y;
+  if (dtype == M3X_F32 && bias && !m3x_aligned16(bias)) return M3X_EINVAL;
   hipStream_t st = (hipStream_t)stream;
-#define CG_CASE(DTT, NTT, MTT)                                                                                     \
-  if (dtype == DTT && N == 16 * NTT && mt == MTT) {                                                                \
-    if (G)                                                                                                         \
-      hipLaunchKernelGGL((conv_gemm_kernel<DTT, NTT, MTT, 1>), grid, dim3(256), 0, st, X, ldx, W, Bi, R, ld_res, Yp, \
-                         ldy, M, K, use_elu, cs);                                                                  \
-    else                                                                                                           \
-      hipLaunchKernelGGL((conv_gemm_kernel<DTT, NTT, MTT, 0>), grid, dim3(256), 0, st, X, ldx, W, Bi, R, ld_res, Yp, \
-                         ldy, M, K, use_elu, cs);                                                                  \
-    M3X_CHECK_LAUNCH();                                                                                            \
-    return M3X_OK;                                                                                                 \
+#define CG_CASE(DTT, NTT, MTT)                                                                                   \
+  if (dtype == DTT && N == 16 * NTT && mt == MTT) {                                                              \
+    using ET = Elt<DTT>;                                                                                         \
+    const ET *X = (const ET*)x, *W = (const ET*)w_packed, *Bi = (const ET*)bias, *R = (const ET*)res;                 \
+    if (G)                                                                                                       \
+      hipLaunchKernelGGL((conv_gemm_kernel<DTT, NTT, MTT, 1>), grid, dim3(256), 0, st, X, ldx, W, Bi, R, ld_res, \
+                         (ET*)y, ldy, M, K, use_elu, cs);                                                         \
+    else                                                                                                         \
+      hipLaunchKernelGGL((conv_gemm_kernel<DTT, NTT, MTT, 0>), grid, dim3(256), 0, st, X, ldx, W, Bi, R, ld_res, \
+                         (ET*)y, ldy, M, K, use_elu, cs);                                                         \
+    M3X_CHECK_LAUNCH();                                                                                          \
+    return M3X_OK;                                                                                               \
   }
   CG_CASE(M3X_F16, 1, 1) CG_CASE(M3X_F16, 2, 1) CG_CASE(M3X_F16, 4, 1) CG_CASE(M3X_F16, 8, 1)
   CG_CASE(M3X_F16, 1, 2) CG_CASE(M3X_F16, 2, 2) CG_CASE(M3X_F16, 4, 2) CG_CASE(M3X_F16, 8, 2)
   CG_CASE(M3X_BF16, 1, 1) CG_CASE(M3X_BF16, 2, 1) CG_CASE(M3X_BF16, 4, 1) CG_CASE(M3X_BF16, 8, 1)
   CG_CASE(M3X_BF16, 1, 2) CG_CASE(M3X_BF16, 2, 2) CG_CASE(M3X_BF16, 4, 2) CG_CASE(M3X_BF16, 8, 2)
+  CG_CASE(M3X_F32, 1, 1) CG_CASE(M3X_F32, 2, 1) CG_CASE(M3X_F32, 4, 1) CG_CASE(M3X_F32, 8, 1)
+  CG_CASE(M3X_F32, 1, 2) CG_CASE(M3X_F32, 2, 2) CG_CASE(M3X_F32, 4, 2) CG_CASE(M3X_F32, 8, 2)
 #undef CG_CASE
   return M3X_EUNSUPPORTED;
 }

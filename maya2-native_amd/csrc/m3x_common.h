@@ -249,5 +249,11 @@ __device__ __forceinline__ f32x4_t mfma16x16x32_f32(const f32x8& a, const f32x8&
   return c;
 }
 
+// one 32-deep k step of the fragment layout for any storage type
+template <int DT> __device__ __forceinline__ f32x4_t mfma_k32(const V8<DT>& a, const V8<DT>& b, f32x4_t c) {
+  if constexpr (DT == M3X_F32) return mfma16x16x32_f32(a, b, c);
+  else return mfma16x16x32<DT>(a, b, c);
+}
+
 static inline int m3x_ceil_div(long a, long b) { return (int)((a + b - 1) / b); }
 static inline bool m3x_aligned16(const void* p) { return (((uintptr_t)p) & 15u) == 0; }

@@ -460,14 +460,14 @@ def rvq_decode(codes, tables, out):
     _dev(codes, tables, out)
     nq, n_codes, dim = tables.shape
     check(lib().m3x_rvq_decode(_p(codes), codes.stride(0), _p(tables), _p(out), out.stride(0), codes.shape[0], nq,
-                               n_codes, dim, _dt(tables), _stream()), "rvq_decode")
+                               n_codes, dim, _dt3(tables), _stream()), "rvq_decode")
 
 
 def dwconvt(x, w, tail, slots, out, k, s):
     """Depthwise transposed conv of one frame per seat with per-slot overlap tails; out [B * s, C]."""
     _dev(x, w, tail, slots, out)
     check(lib().m3x_dwconvt(_p(x), x.stride(0), _p(w), _p(tail), tail.stride(0), _p(slots), _p(out), x.shape[0],
-                            x.shape[1], k, s, _dt(x), _stream()), "dwconvt")
+                            x.shape[1], k, s, _dt3(x), _stream()), "dwconvt")
 
 
 def conv_gather(x, state, slots, cols, B, T, C, k, dil, use_elu, chunk):
@@ -476,7 +476,7 @@ def conv_gather(x, state, slots, cols, B, T, C, k, dil, use_elu, chunk):
     _dev(x, state, slots, cols)
     check(lib().m3x_conv_gather(_p(x), x.stride(0), _p(state), 0 if state is None else state.stride(0), _p(slots),
                                 _p(cols), 0 if cols is None else cols.stride(0), B, T, C, k, dil, int(use_elu), chunk,
-                                _dt(x), _stream()),
+                                _dt3(x), _stream()),
           "conv_gather")
 
 
@@ -484,7 +484,7 @@ def rows_op(g, out, bias=None, scale=None, res=None, use_elu=False):
     """out = act(res + scale * (g + bias)), act = ELU when use_elu; rows of g and out [rows, C]."""
     _dev(g, out, bias, scale, res)
     check(lib().m3x_rows_op(_p(g), g.stride(0), _p(bias), _p(scale), _p(res), 0 if res is None else res.stride(0),
-                            _p(out), out.stride(0), out.shape[0], out.shape[1], int(use_elu), _dt(g), _stream()),
+                            _p(out), out.stride(0), out.shape[0], out.shape[1], int(use_elu), _dt3(g), _stream()),
           "rows_op")
 
 
@@ -498,7 +498,7 @@ def conv_gemm(x, w, y, bias=None, res=None, use_elu=False, gather=None):
     _dev(x, w.data, y, bias, res, st, slots)
     check(lib().m3x_conv_gemm(_p(x), x.stride(0), _p(w.data), _p(bias), _p(res), 0 if res is None else res.stride(0),
                               _p(y), y.stride(0), y.shape[0], w.N, w.K, int(use_elu), _p(st),
-                              0 if st is None else st.stride(0), _p(slots), T, C, dil, int(pre), _dt(x), _stream()),
+                              0 if st is None else st.stride(0), _p(slots), T, C, dil, int(pre), _dt3(x), _stream()),
           "conv_gemm")
     return y
 
@@ -507,14 +507,14 @@ def resid_ln(h, a, scale, w, b, eps, y):
     """h = h + scale * a in place (16-bit rounding once), then y = LayerNorm(h) with (w, b, eps); rows of 512."""
     _dev(h, a, scale, w, b, y)
     check(lib().m3x_resid_ln(_p(h), h.stride(0), _p(a), a.stride(0), _p(scale), _p(w), _p(b), _p(y), y.stride(0),
-                             float(eps), h.shape[0], h.shape[1], _dt(h), _stream()), "resid_ln")
+                             float(eps), h.shape[0], h.shape[1], _dt3(h), _stream()), "resid_ln")
 
 
 def convt_overlap(cols, tail, slots, bias, out, B, Tin, C, k, s, chunk):
     """Overlap-add of a transposed conv's GEMM columns with per-slot tails; out [B * Tin * s, C]."""
     _dev(cols, tail, slots, bias, out)
     check(lib().m3x_convt_overlap(_p(cols), cols.stride(0), _p(tail), tail.stride(0), _p(slots), _p(bias), _p(out),
-                                  out.stride(0), B, Tin, C, k, s, chunk, _dt(cols), _stream()), "convt_overlap")
+                                  out.stride(0), B, Tin, C, k, s, chunk, _dt3(cols), _stream()), "convt_overlap")
 
 
 def ring_attn(qkv, kring, vring, key_pos, tokens, slots, inv_freq, rope_scale, out, B, T, H, ring, window):
@@ -522,7 +522,7 @@ def ring_attn(qkv, kring, vring, key_pos, tokens, slots, inv_freq, rope_scale, o
     _dev(qkv, kring, vring, key_pos, tokens, slots, inv_freq, out)
     check(lib().m3x_ring_attn(_p(qkv), qkv.stride(0), _p(kring), _p(vring), _p(key_pos), _p(tokens), _p(slots),
                               _p(inv_freq), float(rope_scale), _p(out), out.stride(0), B, T, H, 64, ring, window,
-                              _dt(qkv), _stream()), "ring_attn")
+                              _dt3(qkv), _stream()), "ring_attn")
 
 
 def advance_tokens(tokens, slots, B, T, dummy):
@@ -534,5 +534,5 @@ def final_conv(x, state, slots, w, bias, pcm, B, T, C, k, chunk):
     """fp32 PCM of the last causal conv (C -> 1 channel) with per-slot history; pcm [B, >= T] float32."""
     _dev(x, state, slots, w, pcm)
     check(lib().m3x_final_conv(_p(x), x.stride(0), _p(state), 0 if state is None else state.stride(0), _p(slots),
-                               _p(w), float(bias), _p(pcm), pcm.stride(0), B, T, C, k, chunk, _dt(x), _stream()),
+                               _p(w), float(bias), _p(pcm), pcm.stride(0), B, T, C, k, chunk, _dt3(x), _stream()),
           "final_conv")

@@ -1,13 +1,14 @@
 """Slot-based, static-state, graphed one-frame Mimi decoder on m3x kernels.
 
-Drop-in for serve/fast_codec.py StaticMimi (:32-277): same constructor arguments (plus the compute dtype), the
-same public calls (decode, reset, warmup, state_bytes_per_slot, samples_per_frame) and the same streaming
+Drop-in for serve/fast_codec.py StaticMimi (:32-277): same constructor arguments (plus an optional compute dtype;
+by default the Mimi module's own dtype, as the reference computes, :47-49, i.e. float32 for the engine's codec,
+maya3/engine.py:165,201), the same public calls (decode, reset, warmup, state_bytes_per_slot, samples_per_frame) and the same streaming
 semantics: causal-conv input history, transposed-conv overlap tails stored without bias, sliding-window attention
 at absolute RoPE positions (a query at position p sees keys with p - window < key_pos <= p), one row of every
 state per slot plus the dummy row max_slots that pads a batch to its bucket.
 
-The frame runs as m3x launches on time-major activations [seat * T + t, channels] in 16-bit with fp32
-accumulation: the codebook sum (m3x_rvq_decode) and its 1x1 projections as one GEMM, the depthwise upsample with
+The frame runs as m3x launches on time-major activations [seat * T + t, channels] in the compute dtype (fp32, or
+16-bit with fp32 accumulation): the codebook sum (m3x_rvq_decode) and its 1x1 projections as one GEMM, the depthwise upsample with
 its tail (m3x_dwconvt), per transformer layer q|k|v GEMM, ring attention (m3x_ring_attn), o GEMM, layer-scaled
 residual fused with the next LayerNorm (m3x_resid_ln), fc1 GEMM + GELU, fc2 GEMM, layer-scaled residual fused with
 the next layer's LayerNorm; every SEANet conv as
@@ -41,8 +42,9 @@ def _chunk(rows, B, depth, target=2048):
 
 class StaticMimi:
     def __init__(self, mimi, max_slots, batch_buckets=(1, 2, 4, 8, 16, 24, 32, 48, 64, 80, 96), ring=256,
-                 dtype=torch.float16, use_graphs=True):
+                 dtype=None, use_graphs=True):
         from transformers.models.mimi.modeling_mimi import MimiConv1d, MimiConvTranspose1d, MimiResnetBlock
+        dtype = next(mimi.parameters()).dtype if dtype is None else dtype
         _check_codec(mimi, dtype)
         cfg = mimi.config
         self.m = mimi
@@ -60,7 +62,7 @@ class StaticMimi:
         rows = self.max_slots + 1
         dt = dtype
 
-        def w16(t):
+        def cvt(t):
             return t.detach().to(self.device, dt).contiguous()
 
         with torch.inference_mode():
@@ -71,16 +73,16 @@ class StaticMimi:
                 raise ValueError("expected one semantic codebook and 1x1 output projections")
             if sem.output_proj.bias is not None or ac.output_proj.bias is not None:
                 raise ValueError("quantizer output projections carry no bias")
-            self.tables = w16(torch.stack([l.codebook.embed for l in list(sem.layers) + list(ac.layers)]))
+            self.tables = cvt(torch.stack([l.codebook.embed for l in list(sem.layers) + list(ac.layers)]))
             self.n_codes, self.cb_dim = self.tables.shape[1], self.tables.shape[2]
-            self.w_quant = ops.pack_weight(w16(torch.cat([sem.output_proj.weight[:, :, 0],
+            self.w_quant = ops.pack_weight(cvt(torch.cat([sem.output_proj.weight[:, :, 0],
                                                           ac.output_proj.weight[:, :, 0]], 1)))
             self.hidden = self.w_quant.N
             up = mimi.upsample.conv
             if up.groups != up.in_channels or up.bias is not None or up.dilation != (1,):
                 raise ValueError("expected a depthwise bias-free upsample")
             self.up_k, self.up_s = up.kernel_size[0], up.stride[0]
-            self.w_up = w16(up.weight[:, 0, :])
+            self.w_up = cvt(up.weight[:, 0, :])
             # transformer
             self.layers = []
             for L in mimi.decoder_transformer.layers:
@@ -90,13 +92,13 @@ class StaticMimi:
                 if a.num_key_value_groups != 1 or a.head_dim != 64:
                     raise ValueError("ring attention takes head_dim 64 and as many kv heads as heads")
                 self.layers.append(dict(
-                    ln1=(w16(L.input_layernorm.weight), w16(L.input_layernorm.bias), L.input_layernorm.eps),
-                    qkv=ops.pack_weight(w16(torch.cat([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight]))),
-                    o=ops.pack_weight(w16(a.o_proj.weight)), s1=w16(L.self_attn_layer_scale.scale),
-                    ln2=(w16(L.post_attention_layernorm.weight), w16(L.post_attention_layernorm.bias),
+                    ln1=(cvt(L.input_layernorm.weight), cvt(L.input_layernorm.bias), L.input_layernorm.eps),
+                    qkv=ops.pack_weight(cvt(torch.cat([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight]))),
+                    o=ops.pack_weight(cvt(a.o_proj.weight)), s1=cvt(L.self_attn_layer_scale.scale),
+                    ln2=(cvt(L.post_attention_layernorm.weight), cvt(L.post_attention_layernorm.bias),
                          L.post_attention_layernorm.eps),
-                    fc1=ops.pack_weight(w16(L.mlp.fc1.weight)), fc2=ops.pack_weight(w16(L.mlp.fc2.weight)),
-                    s2=w16(L.mlp_layer_scale.scale)))
+                    fc1=ops.pack_weight(cvt(L.mlp.fc1.weight)), fc2=ops.pack_weight(cvt(L.mlp.fc2.weight)),
+                    s2=cvt(L.mlp_layer_scale.scale)))
             self.heads = mimi.decoder_transformer.layers[0].self_attn.num_heads
             rot = mimi.decoder_transformer.rotary_emb
             self.inv_freq = rot.inv_freq.detach().float().to(self.device).contiguous()
@@ -121,8 +123,8 @@ class StaticMimi:
                     raise ValueError("unsupported transpose-convolution geometry")
                 k, s, cin, cout = c.kernel_size[0], c.stride[0], c.in_channels, c.out_channels
                 self.plan.append(dict(kind="convt", key=f"decoder.{i + 1}", k=k, s=s, cin=cin, cout=cout,
-                                      w=ops.pack_weight(w16(c.weight.permute(2, 1, 0).reshape(k * cout, cin))),
-                                      bias=None if c.bias is None else w16(c.bias)))
+                                      w=ops.pack_weight(cvt(c.weight.permute(2, 1, 0).reshape(k * cout, cin))),
+                                      bias=None if c.bias is None else cvt(c.bias)))
                 state_sizes.append((f"decoder.{i + 1}", (k - s) * cout))
                 blk = list(res.block)
                 if len(blk) != 4 or not all(isinstance(b, torch.nn.ELU) and b.alpha == 1.0 for b in blk[::2]):
@@ -357,13 +359,13 @@ class StaticMimi:
 
 def _check_codec(mimi, dtype):
     """The codec shapes this decoder implements: causal constant-padded convs without right trim, an upsample
-    layer, 16-bit compute, weights on the GPU."""
+    layer, fp32 / fp16 / bf16 compute, weights on the GPU."""
     cfg = mimi.config
     if not cfg.use_causal_conv or cfg.pad_mode != "constant" or cfg.trim_right_ratio != 1:
         raise ValueError("Static decoder requires causal constant padding and trim_right_ratio=1")
     if mimi.upsample is None:
         raise ValueError("Static decoder expects the Mimi upsample layer")
-    if dtype not in (torch.float16, torch.bfloat16):
-        raise ValueError("StaticMimi computes in float16 or bfloat16")
+    if dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise ValueError("StaticMimi computes in float32, float16 or bfloat16")
     if not next(mimi.parameters()).is_cuda:
         raise ValueError("StaticMimi runs on the GPU: move the Mimi model to a cuda device first")
