@@ -23,7 +23,7 @@ extern "C" {
 enum { M3X_OK = 0, M3X_EINVAL = -1, M3X_ENULL = -2, M3X_EWORKSPACE = -3, M3X_ELAUNCH = -4, M3X_EUNSUPPORTED = -5 };
 enum { M3X_BF16 = 0, M3X_F16 = 1, M3X_F32 = 2 };
 enum { M3X_NORM_LAYER = 0, M3X_NORM_RMS = 1 };
-enum { M3X_ACT_SWIGLU = 0, M3X_ACT_GELU = 1 };
+enum { M3X_ACT_NONE = -1, M3X_ACT_SWIGLU = 0, M3X_ACT_GELU = 1 };
 
 int m3x_version(void);
 
@@ -112,6 +112,28 @@ int m3x_linear(const void* x, long ldx, const void* w_packed, void* y, long ldy,
  * `F.gelu(block.f1(y2))` (serve/fast_depth.py:123,186). */
 int m3x_linear_act(const void* x, long ldx, const void* wg_packed, const void* wu_packed, void* y, long ldy, int M,
                    int I, int K, int kind, int dtype, void* stream);
+
+/* Projection that joins the residual stream: h_out[m, :] = dt(h[m, :] + dt(x[m, :] . w^T)), then, when c is not
+ * NULL, h_out[m, :] = dt(h_out[m, :] + c[(m / tc) * ldc + :]) (a per-seat constant such as the depth trunk's
+ * speaker term). The same launch writes part[m * (N / 16) + j] (float2) for every 16-column tile j of the stored
+ * row: (sum, sum of squares) for norm_kind M3X_NORM_RMS, (sum, sum of squared deviations from the tile mean) for
+ * M3X_NORM_LAYER, which m3x_linear_normed turns into the norm that follows. bf16/fp16; K % 32 == 0, N % 16 == 0;
+ * h_out may equal h. Replaces `F.linear(...)` followed by the add of `_add_rms` (serve/fast_backbone.py:95-104,
+ * 200,202,236-240) and of `add_ln` (serve/fast_depth_kernels.py:14-45; serve/fast_depth.py:122,125,185,191). */
+int m3x_linear_resid(const void* x, long ldx, const void* w_packed, const void* h, long ldh, const void* c, long ldc,
+                     int tc, void* h_out, long ld_out, void* part, int M, int N, int K, int norm_kind, int dtype,
+                     void* stream);
+
+/* Projection of normed rows: y = act(norm(x) . w^T) with norm(x) the RMSNorm (nw) or LayerNorm (nw, nb) of each
+ * row of x [M, K = 1024], computed from the tile statistics `part` that m3x_linear_resid wrote for x, with the
+ * add+norm kernels' formulas and roundings (only the order of the row sums differs). act as m3x_linear_act
+ * (M3X_ACT_SWIGLU with wg/wu, M3X_ACT_GELU with wg) or M3X_ACT_NONE (plain, wu NULL). Replaces the norm of
+ * `_add_rms` / `add_ln` and the projection it feeds: q|k|v and gate|up (serve/fast_backbone.py:186,193,199-202),
+ * the depth trunk's q|k|v, f1 / gate|up and the codebook head after the final norm (serve/fast_depth.py:104,
+ * 122-125,165-191). */
+int m3x_linear_normed(const void* x, long ldx, const void* part, const void* nw, const void* nb, float eps,
+                      int norm_kind, const void* wg_packed, const void* wu_packed, void* y, long ldy, int M, int N,
+                      int K, int act, int dtype, void* stream);
 
 /* out[r, :I] = act(in[r, :]): M3X_ACT_SWIGLU: bf16(silu(g)) * u with in = [g | u] (2*I wide);
  * M3X_ACT_GELU: gelu(in[r, :I]) (erf form), for callers that already hold the projection output.

@@ -12,7 +12,7 @@ import os
 import torch  # noqa: F401  (must precede the CDLL load, see above)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libm3x.so")
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -38,6 +38,8 @@ SIGNATURES = {
     "m3x_pack_weight": (_I, [_P, _L, _I, _I, _P, _I, _P]),
     "m3x_linear": (_I, [_P, _L, _P, _P, _L, _I, _I, _I, _I, _P]),
     "m3x_linear_act": (_I, [_P, _L, _P, _P, _P, _L, _I, _I, _I, _I, _I, _P]),
+    "m3x_linear_resid": (_I, [_P, _L, _P, _P, _L, _P, _L, _I, _P, _L, _P, _I, _I, _I, _I, _I, _P]),
+    "m3x_linear_normed": (_I, [_P, _L, _P, _P, _P, _F, _I, _P, _P, _P, _L, _I, _I, _I, _I, _I, _P]),
     "m3x_act": (_I, [_P, _L, _P, _L, _I, _I, _I, _I, _P]),
     "m3x_add_norm": (_I, [_P, _L, _L, _P, _L, _L, _P, _L, _P, _P, _P, _P, _F, _I, _I, _I, _I, _I, _P]),
     "m3x_add_rows": (_I, [_P, _L, _P, _L, _P, _L, _I, _I, _I, _P]),

@@ -18,7 +18,7 @@ import torch
 from ._lib import check, lib
 
 NORM_LAYER, NORM_RMS = 0, 1
-ACT_SWIGLU, ACT_GELU = 0, 1
+ACT_NONE, ACT_SWIGLU, ACT_GELU = -1, 0, 1
 _DT = {torch.bfloat16: 0, torch.float16: 1}
 _DT_ANY = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 
@@ -240,6 +240,48 @@ def linear_act(x, w_gate, w_up, kind, y=None):
         _dev(w_up.data)
     check(lib().m3x_linear_act(_p(x), x.stride(0), _p(w_gate.data), _p(w_up.data if kind == ACT_SWIGLU else None),
                                _p(y), y.stride(0), M, I, K, kind, _dt3(x), _stream()), "linear_act")
+    return y
+
+
+def tile_stats_elems(rows, n):
+    """float32 elements of the tile statistics linear_resid writes for `rows` rows of width n (2 per 16 columns)."""
+    return rows * (n // 16) * 2
+
+
+def linear_resid(x, w, h, h_out, part, kind, c=None, tc=1):
+    """h_out = dt(h + dt(x @ W.T)) [then dt(h_out + c[m // tc])], and the 16-column tile statistics of h_out into
+    `part` (float32, >= tile_stats_elems(M, N)) for a following norm of `kind` (NORM_RMS or NORM_LAYER).
+    h may be a strided row view (row stride h.stride(0)); h_out may be h."""
+    M, K, h_out = _lin_args(x, w, h_out, w.N)
+    _dev(h, c, part)
+    for t, name in ((h, "h"), (c, "c")):
+        if t is not None and (t.dim() != 2 or t.stride(-1) != 1 or t.dtype != x.dtype or t.shape[1] < w.N):
+            raise ValueError(f"linear_resid: {name} must be a row-strided [rows, >= {w.N}] {x.dtype} view")
+    if h.shape[0] < M or (c is not None and c.shape[0] * tc < M):
+        raise ValueError("linear_resid: h / c have too few rows")
+    if part.dtype != torch.float32 or not part.is_contiguous() or part.numel() < tile_stats_elems(M, w.N):
+        raise ValueError("linear_resid: part must be a contiguous float32 buffer of tile_stats_elems(M, N)")
+    check(lib().m3x_linear_resid(_p(x), x.stride(0), _p(w.data), _p(h), h.stride(0), _p(c),
+                                 0 if c is None else c.stride(0), tc, _p(h_out), h_out.stride(0), _p(part), M, w.N, K,
+                                 kind, _dt(x), _stream()), "linear_resid")
+    return h_out
+
+
+def linear_normed(x, part, nw, nb, eps, kind, w_gate, w_up=None, act_kind=ACT_NONE, y=None):
+    """y = act(norm(x) @ W.T) with the row norm of x (width 1024) taken from the tile statistics `part` that
+    linear_resid wrote with x; act_kind ACT_NONE (w_up None), ACT_SWIGLU (w_up) or ACT_GELU."""
+    M, K, y = _lin_args(x, w_gate, y, w_gate.N)
+    _dev(part, nw, nb)
+    if act_kind == ACT_SWIGLU and (not isinstance(w_up, PackedWeight) or (w_up.N, w_up.K) != (w_gate.N, w_gate.K)):
+        raise ValueError("linear_normed: w_up must be a packed weight of w_gate's shape")
+    if part.dtype != torch.float32 or not part.is_contiguous() or part.numel() < tile_stats_elems(M, K):
+        raise ValueError("linear_normed: part must hold the tile statistics of x")
+    for t, name in ((nw, "nw"), (nb, "nb")):
+        if t is not None and (t.dtype != x.dtype or not t.is_contiguous() or t.numel() != K):
+            raise ValueError(f"linear_normed: {name} must be a contiguous [{K}] {x.dtype} vector")
+    check(lib().m3x_linear_normed(_p(x), x.stride(0), _p(part), _p(nw), _p(nb), eps, kind, _p(w_gate.data),
+                                  _p(w_up.data if act_kind == ACT_SWIGLU else None), _p(y), y.stride(0), M,
+                                  w_gate.N, K, act_kind, _dt(x), _stream()), "linear_normed")
     return y
 
 

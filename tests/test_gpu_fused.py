@@ -1,0 +1,137 @@
+"""Projections fused with the residual stream (m3x_linear_resid) and with the norm that follows it
+(m3x_linear_normed), against the two-launch chain they replace (projection, then add+norm, then projection) and
+against fp32 torch references."""
+import pytest
+import torch
+
+from helpers import close
+
+pytestmark = pytest.mark.gpu
+
+
+def _g(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _tile_stats(v, kind):
+    """fp32 (sum, second moment) per 16-column tile of rows v [M, N]: sum of squares (RMS) or of squared deviations
+    from the tile mean (LayerNorm)."""
+    t = v.float().view(v.shape[0], -1, 16)
+    s = t.sum(-1)
+    q = (t * t).sum(-1) if kind == 1 else ((t - t.mean(-1, keepdim=True)) ** 2).sum(-1)
+    return torch.stack([s, q], -1)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1024, 1024), (5, 1024, 2816), (16, 1024, 3072), (64, 1024, 1024),
+                                   (224, 1024, 1024), (224, 1024, 2816), (224, 1024, 3072), (250, 1024, 2048),
+                                   (100, 2048, 1024), (600, 1024, 3072), (2264, 1024, 1024), (2264, 1024, 3072)])
+@pytest.mark.parametrize("kind", [0, 1])
+def test_linear_resid_bf16(gpu, M, N, K, kind):
+    """h_out = dt(h + dt(x W^T)) bit for bit against the plain projection plus a bf16 add (same plan, same sums);
+    h read through a strided view and updated in place; tile statistics against fp32 sums of the stored row."""
+    from m3x import ops
+    g = _g(M * 13 + K + kind)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(gpu)
+    w = ops.pack_weight((torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).to(gpu))
+    big = torch.randn(M, 3 * N, generator=g).to(torch.bfloat16).to(gpu)
+    h = big[:, N:2 * N]
+    h0, big0 = h.clone(), big.clone()
+    part = torch.full((ops.tile_stats_elems(M, N),), float("nan"), device=gpu)
+    ops.linear_resid(x, w, h, h, part, kind)
+    ref = (h0.float() + ops.linear(x, w).float()).to(torch.bfloat16)
+    assert torch.equal(h.cpu(), ref.cpu())
+    assert torch.equal(big[:, :N].cpu(), big0[:, :N].cpu()) and torch.equal(big[:, 2 * N:].cpu(), big0[:, 2 * N:].cpu())
+    st = part.view(M, N // 16, 2).cpu()
+    exp = _tile_stats(ref.cpu(), kind)
+    assert torch.allclose(st, exp, rtol=1e-5, atol=1e-4), (st - exp).abs().max()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("B,T", [(4, 3), (224, 1), (16, 31)])
+def test_linear_resid_cross_term(gpu, dtype, B, T):
+    """The per-seat constant c[m // T] (the depth trunk's speaker term) is added after the residual, rounded once
+    more, as add_norm does with its c."""
+    from m3x import ops
+    g = _g(B * 7 + T)
+    M, N, K = B * T, 1024, 2816
+    x = torch.randn(M, K, generator=g).to(dtype).to(gpu)
+    w = ops.pack_weight((torch.randn(N, K, generator=g) * 0.02).to(dtype).to(gpu))
+    h = torch.randn(M, N, generator=g).to(dtype).to(gpu)
+    cross = torch.randn(B, 4 * N, generator=g).to(dtype).to(gpu)
+    c = cross[:, 2 * N:3 * N]
+    out = torch.empty(M, N, dtype=dtype, device=gpu)
+    part = torch.empty(ops.tile_stats_elems(M, N), device=gpu)
+    ops.linear_resid(x, w, h, out, part, 0, c=c, tc=T)
+    lin = ops.linear(x, w).float()
+    ref = ((h.float() + lin).to(dtype).float() + c.repeat_interleave(T, 0).float()).to(dtype)
+    assert torch.equal(out.cpu(), ref.cpu())
+    exp = _tile_stats(ref.cpu(), 0)
+    assert torch.allclose(part.view(M, N // 16, 2).cpu(), exp, rtol=1e-5, atol=1e-4)
+
+
+def _norm_ref(h, w, b, eps, kind):
+    """fp32 evaluation of the norm with the add+norm kernels' roundings (LayerNorm: one rounding; RMSNorm: the
+    product x * inv rounded, then the weight)."""
+    x = h.float()
+    if kind == 0:
+        return torch.nn.functional.layer_norm(x, (x.shape[1],), w.float(), b.float(), eps).to(h.dtype)
+    inv = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps)
+    return ((x * inv).to(h.dtype).float() * w.float()).to(h.dtype)
+
+
+@pytest.mark.parametrize("M", [1, 3, 16, 64, 130, 224, 600, 2264])
+@pytest.mark.parametrize("act,kind", [(-1, 1), (0, 1), (1, 0), (-1, 0)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_linear_normed(gpu, M, act, kind, dtype):
+    """norm(h) . W^T with the norm from linear_resid's tile statistics, against the add+norm kernel's y fed to the
+    plain / gated projection (the row sums fold in another order, so a normed input may sit one ulp apart) and
+    against an fp32 reference."""
+    from m3x import ops
+    if dtype == torch.float16 and M not in (3, 224, 2264):
+        pytest.skip("fp16: a subset of the row plans")
+    g = _g(M * 31 + act * 5 + kind)
+    D = 1024
+    N = {-1: 3072, 0: 2816, 1: 3072}[act]
+    eps = 1e-6 if kind == 1 else 1e-5
+    x = torch.randn(M, 2816, generator=g).to(dtype).to(gpu)
+    wd = ops.pack_weight((torch.randn(D, 2816, generator=g) * 0.02).to(dtype).to(gpu))
+    h = (2 * torch.randn(M, D, generator=g)).to(dtype).to(gpu)
+    nw = (1 + 0.1 * torch.randn(D, generator=g)).to(dtype).to(gpu)
+    nb = (0.1 * torch.randn(D, generator=g)).to(dtype).to(gpu) if kind == 0 else None
+    part = torch.empty(ops.tile_stats_elems(M, D), device=gpu)
+    hn = ops.linear_resid(x, wd, h, torch.empty_like(h), part, kind)
+    wg_full = (torch.randn(2 * N, D, generator=g) * 0.02).to(dtype).to(gpu)
+    pw = ops.pack_weight(wg_full)
+    wg, wu = pw.rows(0, N), pw.rows(N, 2 * N)
+    got = ops.linear_normed(hn, part, nw, nb, eps, kind, wg, wu if act == 0 else None, act)
+    # the two-launch chain: add+norm kernel, then the projection
+    y = torch.empty_like(hn)
+    ops.add_norm(hn, None, None, None, y, nw, nb, eps, 1, kind)
+    two = ops.linear(y, wg) if act == -1 else ops.linear_act(y, wg, wu if act == 0 else None, act)
+    ok, info = close(got, two.float(), atol=2e-3, rel_ulps=2)
+    assert ok, info
+    yr = _norm_ref(hn.cpu(), nw.cpu(), None if nb is None else nb.cpu(), eps, kind).float()
+    a = (yr @ wg_full[:N].float().cpu().t()).to(dtype).float()
+    if act == 0:
+        u = (yr @ wg_full[N:].float().cpu().t()).to(dtype).float()
+        ref = torch.nn.functional.silu(a).to(dtype).float() * u
+    elif act == 1:
+        ref = torch.nn.functional.gelu(a)
+    else:
+        ref = a
+    ok, info = close(got, ref, atol=1e-2)
+    assert ok, info
+
+
+def test_linear_normed_rejects_bad_args(gpu):
+    from m3x import ops
+    x = torch.zeros(4, 1024, dtype=torch.bfloat16, device=gpu)
+    w = ops.pack_weight(torch.zeros(64, 1024, dtype=torch.bfloat16, device=gpu))
+    nw = torch.ones(1024, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(ValueError):
+        ops.linear_normed(x, torch.zeros(10, device=gpu), nw, None, 1e-6, 1, w)
+    w2 = ops.pack_weight(torch.zeros(64, 2048, dtype=torch.bfloat16, device=gpu))
+    x2 = torch.zeros(4, 2048, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(RuntimeError):  # the norm prologue covers rows of width 1024 only
+        ops.linear_normed(x2, torch.zeros(ops.tile_stats_elems(4, 2048), device=gpu),
+                          torch.ones(2048, dtype=torch.bfloat16, device=gpu), None, 1e-6, 1, w2)
