@@ -124,14 +124,17 @@ int m3x_linear_resid(const void* x, long ldx, const void* w_packed, const void* 
                      int tc, void* h_out, long ld_out, void* part, int M, int N, int K, int norm_kind, int dtype,
                      void* stream);
 
-/* Projection of normed rows: y = act(norm(x) . w^T) with norm(x) the RMSNorm (nw) or LayerNorm (nw, nb) of each
- * row of x [M, K = 1024], computed from the tile statistics `part` that m3x_linear_resid wrote for x, with the
- * add+norm kernels' formulas and roundings (only the order of the row sums differs). act as m3x_linear_act
- * (M3X_ACT_SWIGLU with wg/wu, M3X_ACT_GELU with wg) or M3X_ACT_NONE (plain, wu NULL). Replaces the norm of
- * `_add_rms` / `add_ln` and the projection it feeds: q|k|v and gate|up (serve/fast_backbone.py:186,193,199-202),
- * the depth trunk's q|k|v, f1 / gate|up and the codebook head after the final norm (serve/fast_depth.py:104,
- * 122-125,165-191). */
-int m3x_linear_normed(const void* x, long ldx, const void* part, const void* nw, const void* nb, float eps,
+/* Projection of normed rows: y = act(norm(x) . W^T) for x [M, K = 1024] whose rows m3x_linear_resid wrote with
+ * their tile statistics `part`, norm RMSNorm (weight nw) or LayerNorm (nw, nb; eps for both). The norm is folded:
+ * the weights are packed from Wf = dt(W * nw) (per input column), and the product of the raw rows is scaled per row,
+ * RMSNorm inv_rms * (x . Wf^T), LayerNorm rstd * (x . Wf^T) - rstd * mean * u + v with the fp32 column vectors
+ * u[n] = sum_k Wf[n, k], v[n] = sum_k nb[k] W[n, k] (NULL for RMSNorm; 2N entries, gate then up, for SwiGLU). act as
+ * m3x_linear_act (M3X_ACT_SWIGLU with wg/wu, M3X_ACT_GELU with wg) or M3X_ACT_NONE (plain, wu NULL). Against the
+ * reference's order the one rounding to the storage type moves from the normed activation to the folded weight.
+ * Replaces the norm of `_add_rms` / `add_ln` and the projection it feeds: q|k|v and gate|up
+ * (serve/fast_backbone.py:186,193,199-202), the depth trunk's q|k|v, f1 / gate|up and the codebook head after the
+ * final norm (serve/fast_depth.py:104,122-125,165-191). */
+int m3x_linear_normed(const void* x, long ldx, const void* part, const float* u, const float* v, float eps,
                       int norm_kind, const void* wg_packed, const void* wu_packed, void* y, long ldy, int M, int N,
                       int K, int act, int dtype, void* stream);
 

@@ -1,7 +1,8 @@
 // Projections fused with the residual stream: the producer of a residual add (o and down projections) adds its
 // output into the stream and writes the statistics of each 16-column tile of the new row; the consumer (the
-// q|k|v, gate|up and head projections) normalises its input rows from those statistics while staging them. The
-// separate add+norm launch between the two disappears (serve/fast_backbone.py:95-104,236-240 _add_rms;
+// q|k|v, gate|up and head projections) multiplies the raw rows by a weight with the norm's affine terms folded in
+// and applies each row's scale (and shift) from those statistics in its epilogue. The separate add+norm launch
+// between the two disappears (serve/fast_backbone.py:95-104,236-240 _add_rms;
 // serve/fast_depth_kernels.py:14-45 _add_ln). Kernels and plans: m3x_gemm.h.
 #include "m3x_gemm.h"
 
@@ -52,24 +53,24 @@ M3X_API int m3x_linear_resid(const void* x, long ldx, const void* w_packed, cons
   return M3X_OK;
 }
 
-M3X_API int m3x_linear_normed(const void* x, long ldx, const void* part, const void* nw, const void* nb, float eps,
+M3X_API int m3x_linear_normed(const void* x, long ldx, const void* part, const float* u, const float* v, float eps,
                               int norm_kind, const void* wg_packed, const void* wu_packed, void* y, long ldy, int M,
                               int N, int K, int act, int dtype, void* stream) {
   if (M < 0 || N <= 0) return M3X_EINVAL;
   if (M == 0) return M3X_OK;
-  if (!x || !part || !nw || !wg_packed || !y) return M3X_ENULL;
-  if (norm_kind == M3X_NORM_LAYER && !nb) return M3X_ENULL;
+  if (!x || !part || !wg_packed || !y) return M3X_ENULL;
+  if (norm_kind == M3X_NORM_LAYER && (!u || !v)) return M3X_ENULL;
   if (act == M3X_ACT_SWIGLU && !wu_packed) return M3X_ENULL;
   if (norm_kind != M3X_NORM_LAYER && norm_kind != M3X_NORM_RMS) return M3X_EINVAL;
   if (act != M3X_ACT_NONE && act != M3X_ACT_SWIGLU && act != M3X_ACT_GELU) return M3X_EINVAL;
   if (K != PRO_K || (ldx & 7) || ldx < K || ldy < N) return M3X_EINVAL;
-  if (!aligned(x, 16) || !aligned(part, 16) || !aligned(nw, 16) || (nb && !aligned(nb, 16)) ||
+  if (!aligned(x, 16) || !aligned(part, 16) ||
       !aligned(wg_packed, 16) || (wu_packed && !aligned(wu_packed, 16)) || !aligned(y, 2))
     return M3X_EINVAL;
   if (dtype != M3X_BF16 && dtype != M3X_F16) return M3X_EUNSUPPORTED;
   const LinearPlan p = linear_plan(M, N, K, act == M3X_ACT_SWIGLU, ldx);
   if ((long)m3x_ceil_div(p.nblk, 8) * 8 * p.mblk > 0x7fffffffL) return M3X_EINVAL;
-  const NormIn ni{(const float2*)part, (const uint16_t*)nw, (const uint16_t*)nb, eps, norm_kind};
+  const NormIn ni{(const float2*)part, u, v, eps, norm_kind};
   hipStream_t st = (hipStream_t)stream;
   const bool ok = dtype == M3X_BF16
                       ? normed_launch<M3X_BF16>(p, st, x, ldx, wg_packed, wu_packed, y, ldy, M, N, K, act, ni)

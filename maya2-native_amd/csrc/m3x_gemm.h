@@ -28,12 +28,20 @@
 //   EPI_RESID   y = dt(h + dt(acc)) [then dt(y + c[m / tc])]: the projection joins the residual stream, and the
 //               workgroup also writes the statistics of every 16-column tile of the stored row for the norm that
 //               follows (the add of _add_rms / _add_ln, serve/fast_backbone.py:95-104, serve/fast_depth_kernels.py:
-//               14-45; the norm itself runs in the consumer's prologue, below)
+//               14-45; the norm itself is folded into the consumer, below)
 //
-// Norm prologue (PRO): the consumer of a residual row normalises it while staging it, from the producer's tile
-// statistics: (sum, sum of squares) per 16 columns for RMSNorm, (sum, squared deviations from the tile mean) for
-// LayerNorm, merged in a fixed order (Chan's pairwise combination for the LayerNorm variance). The norm's formulas
-// and roundings are the add+norm kernels' (m3x_norm.h norm_vec); only the order of the row sums differs.
+// Folded norm (PRO): the consumer of a residual row multiplies the raw row and applies the norm to the product.
+// A norm's elementwise weight w (and LayerNorm bias b) is folded into the consumer's weight when it is packed:
+// Wf[n, k] = dt(W[n, k] * w[k]), u[n] = sum_k Wf[n, k], v[n] = sum_k b[k] W[n, k] (fp32). Then
+//   RMSNorm:   norm(x) . W[n]^T = inv_rms * (x . Wf[n]^T)
+//   LayerNorm: norm(x) . W[n]^T = rstd * (x . Wf[n]^T) - rstd * mean * u[n] + v[n]
+// with the row's inv_rms, or mean and rstd = 1 / sqrt(var + eps), merged from the producer's tile statistics
+// ((sum, sum of squares) per 16 columns for RMSNorm, (sum, squared deviations from the tile mean) for LayerNorm,
+// combined in a fixed order: Chan's pairwise combination for the variance). The prologue only loads and merges the
+// statistics of the workgroup's rows; the activations go to the MFMAs as stored, and the epilogue applies the row
+// scale (and shift) before its own rounding. Against the reference's order (normalised row rounded to the storage
+// type, then multiplied) this moves the rounding from the normalised activation to the folded weight: the same
+// one-rounding error at the storage precision, on the other operand.
 #pragma once
 #include "m3x_common.h"
 #include "m3x_norm.h"
@@ -41,12 +49,13 @@
 enum { EPI_NONE = 0, EPI_SWIGLU = 1, EPI_GELU = 2, EPI_RESID = 3 };
 enum { M3X_ACT_NONE = -1, M3X_ACT_SWIGLU = 0, M3X_ACT_GELU = 1 };  // the C ABI's gated-activation kinds
 
-// Input norm of a PRO projection: row m of x is normalised with the statistics part[m * (K / 16) + j] of its
-// 16-column tiles j and the affine vectors w (and b for LayerNorm) of length K.
+// Folded input norm of a PRO projection: the statistics part[m * (K / 16) + j] of row m's 16-column tiles j, and
+// for LayerNorm the column vectors u, v of the folded weight (N entries; with SwiGLU 2N: the gate's, then the
+// up projection's).
 struct NormIn {
   const float2* part;
-  const uint16_t* w;
-  const uint16_t* b;
+  const float* u;
+  const float* v;
   float eps;
   int kind;  // M3X_NORM_LAYER or M3X_NORM_RMS
 };
@@ -63,9 +72,9 @@ struct ResidOut {
   int kind;
 };
 
-// Tile statistics of a PRO row: 8 consecutive lanes per row, TPT tiles per lane (K = 128 TPT). Every lane of the
-// row's group returns (mean, sd) for LayerNorm and (0, 1 / rms) for RMSNorm; the sums over the group's lanes are
-// group_sum<8> butterflies, so all eight lanes hold the same bits.
+// Row scale and shift of a PRO row from its tile statistics: 8 consecutive lanes per row, TPT tiles per lane
+// (K = 128 TPT). Every lane of the row's group returns (rstd, -mean * rstd) for LayerNorm and (1 / rms, 0) for
+// RMSNorm; the sums over the group's lanes are group_sum<8> butterflies, so all eight lanes hold the same bits.
 template <int TPT>
 __device__ __forceinline__ float2 norm_row_stats(const float2 (&p)[TPT], int K, int kind, float eps) {
   if (kind == M3X_NORM_RMS) {
@@ -73,7 +82,7 @@ __device__ __forceinline__ float2 norm_row_stats(const float2 (&p)[TPT], int K, 
 #pragma unroll
     for (int j = 1; j < TPT; ++j) q = q + p[j].y;
     q = group_sum<8>(q);
-    return make_float2(0.f, 1.0f / sqrtf(q / (float)K + eps));
+    return make_float2(1.0f / sqrtf(q / (float)K + eps), 0.f);
   }
   float s = p[0].x;
 #pragma unroll
@@ -86,35 +95,18 @@ __device__ __forceinline__ float2 norm_row_stats(const float2 (&p)[TPT], int K, 
     m2 = m2 + (p[j].y + 16.0f * d * d);
   }
   m2 = group_sum<8>(m2);
-  return make_float2(mean, sqrtf(m2 / (float)K + eps));
+  const float rstd = 1.0f / sqrtf(m2 / (float)K + eps);
+  return make_float2(rstd, -mean * rstd);
 }
 
-// The norm of 8 consecutive elements of a row with statistics st (norm_row_stats) and affine vectors w, b:
-// LayerNorm dt((x - mean) / sd * w + b), RMSNorm dt(dt(x * inv) * w) (m3x_norm.h norm_vec).
-template <int DT>
-__device__ __forceinline__ u16x8 norm_granule(const u16x8& x, float2 st, const u16x8& w, const u16x8& b, int kind) {
-  u16x8 y;
-  if (kind == M3X_NORM_LAYER) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      y.v[e] = E<DT>::from_f((E<DT>::to_f(x.v[e]) - st.x) / st.y * E<DT>::to_f(w.v[e]) + E<DT>::to_f(b.v[e]));
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) y.v[e] = E<DT>::from_f(rnd<DT>(E<DT>::to_f(x.v[e]) * st.y) * E<DT>::to_f(w.v[e]));
-  }
-  return y;
-}
-
-// PRO prologue, in two halves around the kernel's own loads. norm_part_load issues the loads of the tile
-// statistics of rows m0 .. m0 + ROWS - 1 (8 threads per row, NT threads, PASSES rounds) and of the affine vectors
-// (threads below K / 8); norm_part_finish, once the kernel's activation and weight loads are in flight, reduces
-// the statistics to st[ROWS] and stores the affine vectors to aw / ab in LDS. The caller then waits at a barrier.
-// Rows past M get (0, 0) and are never stored.
+// PRO prologue, in two halves around the kernel's own loads. load issues the loads of the tile statistics of rows
+// m0 .. m0 + ROWS - 1 (8 threads per row, NT threads, PASSES rounds); finish, once the kernel's activation and
+// weight loads are in flight, merges them into the row scale and shift st[ROWS] in LDS. The caller then waits at a
+// barrier before the epilogue reads them. Rows past M get (0, 0) and are never stored.
 template <int ROWS, int NT, int TPT>
 struct NormStage {
   static constexpr int PASSES = (ROWS * 8 + NT - 1) / NT;
   float2 p[PASSES][TPT];
-  u16x8 w, b;
   __device__ __forceinline__ void load(const NormIn& ni, int m0, int M, int K) {
     const int tid = threadIdx.x;
 #pragma unroll
@@ -133,14 +125,8 @@ struct NormStage {
         }
       }
     }
-    if (tid < (K >> 3)) {
-      w = ld16(ni.w + 8 * tid);
-      if (ni.kind == M3X_NORM_LAYER) b = ld16(ni.b + 8 * tid);
-    }
   }
-  template <int DT>
-  __device__ __forceinline__ void finish(const NormIn& ni, int m0, int M, int K, float2* st, uint16_t* aw,
-                                         uint16_t* ab) {
+  __device__ __forceinline__ void finish(const NormIn& ni, int m0, int M, int K, float2* st) {
     const int tid = threadIdx.x;
 #pragma unroll
     for (int ps = 0; ps < PASSES; ++ps) {
@@ -148,12 +134,27 @@ struct NormStage {
       const float2 v = norm_row_stats<TPT>(p[ps], K, ni.kind, ni.eps);
       if (r < ROWS && (tid & 7) == 0) st[r] = m0 + r < M ? v : make_float2(0.f, 0.f);
     }
-    if (tid < (K >> 3)) {
-      st16(aw + 8 * tid, w);
-      if (ni.kind == M3X_NORM_LAYER) st16(ab + 8 * tid, b);
-    }
   }
 };
+
+// The folded norm on one lane's 4 accumulators of row slot `row` (columns n .. n + 3 of weight a: 0 = W, 1 = W2):
+// acc = scale * acc [+ shift * u[n] + v[n]].
+__device__ __forceinline__ void norm_apply(f32x4_t& acc, const float2* pst, int row, const NormIn& ni, int n, int N,
+                                           int a) {
+  const float2 st = pst[row];
+  if (ni.kind == M3X_NORM_LAYER) {
+    const float* u = ni.u + a * N;
+    const float* v = ni.v + a * N;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int c = min(n + r, N - 1);  // columns past N: any finite value, never stored
+      acc[r] = st.x * acc[r] + (st.y * u[c] + v[c]);
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] = st.x * acc[r];
+  }
+}
 
 // EPI_RESID for one lane's 4 outputs (columns n .. n + 3 of row m, acc as accumulated): stores the residual row's
 // values and, with the other 3 lanes of the 16-column tile (lanes li + 16 lg'), the tile's statistics
@@ -196,10 +197,11 @@ __device__ __forceinline__ void resid_quad(const f32x4_t& acc, int m, int n, int
 // The KW K-slice partials of one weight tile meet in LDS (`red`, free when this runs) and are added in slice
 // order by slice 0, which then applies the epilogue. Lane (li, lg) holds weight rows n0 + 4*lg + r of
 // activation row m0 + 16*t + li.
-template <int DT, int MT, int NW, int KW, int EPI>
+template <int DT, int MT, int NW, int KW, int EPI, bool PRO>
 __device__ __forceinline__ void linear_finish(f32x4_t (&acc)[EPI == EPI_SWIGLU ? 2 : 1][MT], f32x4_t* red, int wn,
                                               int wk, int lane, int n0, int m0, uint16_t* __restrict__ Y, long ldy,
-                                              int M, int N, const ResidOut& ro) {
+                                              int M, int N, const ResidOut& ro, const float2* pst,
+                                              const NormIn& ni) {
   constexpr int NA = EPI == EPI_SWIGLU ? 2 : 1;
   const int li = lane & 15;
   const int lg = lane >> 4;
@@ -224,6 +226,12 @@ __device__ __forceinline__ void linear_finish(f32x4_t (&acc)[EPI == EPI_SWIGLU ?
         }
   }
   const int n = n0 + 4 * lg;
+  if constexpr (PRO) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int a = 0; a < NA; ++a) norm_apply(acc[a][t], pst, 16 * t + li, ni, n, N, a);
+  }
   if constexpr (EPI == EPI_RESID) {
 #pragma unroll
     for (int t = 0; t < MT; ++t) resid_quad<DT>(acc[0][t], m0 + 16 * t + li, n, n0 >> 4, M, N, lg, ro, Y, ldy);
@@ -261,7 +269,7 @@ __device__ __forceinline__ void linear_finish(f32x4_t (&acc)[EPI == EPI_SWIGLU ?
   }
 }
 
-// PRO: the input rows are normalised while staged (NormIn; K == PRO_K).
+// PRO: the input rows' folded norm (NormIn; K == PRO_K): statistics loaded in the prologue, applied in the epilogue.
 constexpr int PRO_K = 1024;
 
 template <int DT, int MT, int NW, int EPI, bool PRO>
@@ -282,7 +290,6 @@ __global__ __launch_bounds__(256) void linear_kernel(const uint16_t* __restrict_
   constexpr int NA = DUAL ? 2 : 1;
   __shared__ __align__(16) uint16_t xs[2][KW * ROWS * LDR];
   __shared__ float2 pst[PRO ? ROWS : 1];
-  __shared__ __align__(16) uint16_t paw[PRO ? PRO_K : 8], pab[PRO ? PRO_K : 8];
 
   const int xcd = blockIdx.x & 7;
   const int slot = blockIdx.x >> 3;
@@ -345,15 +352,7 @@ __global__ __launch_bounds__(256) void linear_kernel(const uint16_t* __restrict_
         const int rem = v - q * (ROWS * VPR);
         const int r = rem / VPR;
         const int c16 = rem - r * VPR;
-        u16x8 x = Xr[j];
-        if constexpr (PRO) {
-          const int step = q * span + c * U + (c16 >> 2);
-          const int col = step * 32 + (c16 & 3) * 8;
-          if (col < PRO_K)  // past K: a step no slice multiplies
-            x = norm_granule<DT>(x, pst[r], *reinterpret_cast<const u16x8*>(paw + col),
-                                 *reinterpret_cast<const u16x8*>(pab + col), ni.kind);
-        }
-        st16(&xs[buf][(q * ROWS + r) * LDR + c16 * 8], x);
+        st16(&xs[buf][(q * ROWS + r) * LDR + c16 * 8], Xr[j]);
       }
     }
   };
@@ -394,7 +393,7 @@ __global__ __launch_bounds__(256) void linear_kernel(const uint16_t* __restrict_
     wload(1, W1);
   }
   if constexpr (PRO) {
-    ns.template finish<DT>(ni, m0, M, PRO_K, pst, paw, pab);
+    ns.finish(ni, m0, M, PRO_K, pst);
     __syncthreads();
   }
   xstore(0, 0, X0);
@@ -414,8 +413,8 @@ __global__ __launch_bounds__(256) void linear_kernel(const uint16_t* __restrict_
     __syncthreads();
   }
 
-  linear_finish<DT, MT, NW, KW, EPI>(acc, reinterpret_cast<f32x4_t*>(&xs[0][0]), wn, wk, lane, n0, m0, Y, ldy, M,
-                                     N, ro);
+  linear_finish<DT, MT, NW, KW, EPI, PRO>(acc, reinterpret_cast<f32x4_t*>(&xs[0][0]), wn, wk, lane, n0, m0, Y,
+                                          ldy, M, N, ro, pst, ni);
 }
 
 // One-shot variant: every weight fragment of the wave's K slice (S steps of 32) and the workgroup's whole
@@ -425,8 +424,8 @@ __global__ __launch_bounds__(256) void linear_kernel(const uint16_t* __restrict_
 // once. The block sits in LDS unpadded when a slice row is a multiple of 16 granules of 16 bytes, with granule
 // g of row r stored at g ^ (r % 16), so the 16 rows a fragment read touches fall in 16 different bank groups;
 // otherwise rows are padded by 16 bytes.
-// PRO (K == PRO_K): the tile statistics and affine vectors are requested before the activation block, reduced
-// once the weight fragments are in flight, and the block is normalised on its way to LDS.
+// PRO (K == PRO_K): the tile statistics are requested before the activation block and merged into the rows' scale
+// and shift once the weight fragments are in flight; the epilogue applies them.
 template <int DT, int MT, int NW, int NWAVES, int EPI, int S, bool PRO>
 __global__ __launch_bounds__(64 * NWAVES) void linear_oneshot_kernel(const uint16_t* __restrict__ X, long ldx,
                                                                      const uint16_t* __restrict__ Wp,
@@ -450,7 +449,6 @@ __global__ __launch_bounds__(64 * NWAVES) void linear_oneshot_kernel(const uint1
   static_assert(!PRO || KW * KS == PRO_K, "the norm prologue covers K = PRO_K");
   __shared__ __align__(16) uint16_t xs[KW * ROWS * LDR];
   __shared__ float2 pst[PRO ? ROWS : 1];
-  __shared__ __align__(16) uint16_t paw[PRO ? PRO_K : 8], pab[PRO ? PRO_K : 8];
 
   const int xcd = blockIdx.x & 7;
   const int slot = blockIdx.x >> 3;
@@ -503,7 +501,7 @@ __global__ __launch_bounds__(64 * NWAVES) void linear_oneshot_kernel(const uint1
     }
   }
   if constexpr (PRO) {
-    ns.template finish<DT>(ni, m0, M, PRO_K, pst, paw, pab);
+    ns.finish(ni, m0, M, PRO_K, pst);
     __syncthreads();
   }
 #pragma unroll
@@ -513,13 +511,7 @@ __global__ __launch_bounds__(64 * NWAVES) void linear_oneshot_kernel(const uint1
     const int rem = v - q * (ROWS * GR);
     const int r = rem / GR;
     const int g = rem - r * GR;
-    u16x8 x = Xr[j];
-    if constexpr (PRO) {
-      const int col = q * KS + g * 8;
-      x = norm_granule<DT>(x, pst[r], *reinterpret_cast<const u16x8*>(paw + col),
-                           *reinterpret_cast<const u16x8*>(pab + col), ni.kind);
-    }
-    if (NVEC % NT == 0 || v < NVEC) st16(&xs[(q * ROWS + r) * LDR + ((SWZ ? g ^ (r & 15) : g) << 3)], x);
+    if (NVEC % NT == 0 || v < NVEC) st16(&xs[(q * ROWS + r) * LDR + ((SWZ ? g ^ (r & 15) : g) << 3)], Xr[j]);
   }
   __syncthreads();
 
@@ -540,7 +532,8 @@ __global__ __launch_bounds__(64 * NWAVES) void linear_oneshot_kernel(const uint1
     }
   }
   __syncthreads();  // every wave is done with the block before it holds the slice partials
-  linear_finish<DT, MT, NW, KW, EPI>(acc, reinterpret_cast<f32x4_t*>(xs), wn, wk, lane, n0, m0, Y, ldy, M, N, ro);
+  linear_finish<DT, MT, NW, KW, EPI, PRO>(acc, reinterpret_cast<f32x4_t*>(xs), wn, wk, lane, n0, m0, Y, ldy, M, N, ro,
+                                          pst, ni);
 }
 
 // Large-M projections (M > 512 rows: steps with inline prefills). A workgroup of 8 waves owns a 2-D tile of 128
@@ -553,7 +546,7 @@ __global__ __launch_bounds__(64 * NWAVES) void linear_oneshot_kernel(const uint1
 // global loads are in flight while the current one multiplies, with one barrier per stage. Every weight byte is
 // read by ceil(M / 128) workgroups and every activation byte by ceil(N / 128), against 36 and 64 for the 64 x 64
 // chunked tiles at 2264 rows.
-// PRO (K == PRO_K): each stage's activation rows are normalised on their way to LDS.
+// PRO (K == PRO_K): the rows' folded norm, applied in the epilogue.
 template <int DT, int EPI, bool PRO>
 __global__ __launch_bounds__(512, 2) void linear_tiled_kernel(const uint16_t* __restrict__ X, long ldx,
                                                               const uint16_t* __restrict__ Wp,
@@ -566,7 +559,6 @@ __global__ __launch_bounds__(512, 2) void linear_tiled_kernel(const uint16_t* __
   __shared__ __align__(16) uint16_t lw[2][16 * 512];
   __shared__ __align__(16) uint16_t la[2][BM * LDA];
   __shared__ float2 pst[PRO ? BM : 1];
-  __shared__ __align__(16) uint16_t paw[PRO ? PRO_K : 8], pab[PRO ? PRO_K : 8];
 
   const int xcd = blockIdx.x & 7;
   const int slot = blockIdx.x >> 3;
@@ -619,26 +611,20 @@ __global__ __launch_bounds__(512, 2) void linear_tiled_kernel(const uint16_t* __
       ra[j] = ld16(X + ga[j] + stg * 64);
     }
   };
-  auto lstore = [&](int buf, int stg) {
+  auto lstore = [&](int buf) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       st16(&lw[buf][tid * 8 + 4096 * j], rw[j]);
-      u16x8 x = ra[j];
-      if constexpr (PRO) {
-        const int col = stg * 64 + 8 * (tid & 7);
-        x = norm_granule<DT>(x, pst[(tid >> 3) + 64 * j], *reinterpret_cast<const u16x8*>(paw + col),
-                             *reinterpret_cast<const u16x8*>(pab + col), ni.kind);
-      }
-      st16(&la[buf][la0 + 64 * j * LDA], x);
+      st16(&la[buf][la0 + 64 * j * LDA], ra[j]);
     }
   };
   const int nst = K >> 6;
   gload(0);
   if constexpr (PRO) {
-    ns.template finish<DT>(ni, m0, M, PRO_K, pst, paw, pab);
+    ns.finish(ni, m0, M, PRO_K, pst);
     __syncthreads();
   }
-  lstore(0, 0);
+  lstore(0);
   __syncthreads();
   for (int stg = 0; stg < nst; ++stg) {
     const int buf = stg & 1;
@@ -656,10 +642,18 @@ __global__ __launch_bounds__(512, 2) void linear_tiled_kernel(const uint16_t* __
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = mfma16x16x32<DT>(a[i], b[j], acc[i][j]);
     }
-    if (stg + 1 < nst) lstore(buf ^ 1, stg + 1);
+    if (stg + 1 < nst) lstore(buf ^ 1);
     __syncthreads();
   }
 
+  if constexpr (PRO) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int n = DUAL ? (nb * 4 + wn) * 16 + 4 * lg : (nb * 8 + wt[i]) * 16 + 4 * lg;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) norm_apply(acc[i][j], pst, 16 * (4 * wm + j) + li, ni, n, N, DUAL ? i : 0);
+    }
+  }
   if constexpr (EPI == EPI_RESID) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {

@@ -267,19 +267,37 @@ def linear_resid(x, w, h, h_out, part, kind, c=None, tc=1):
     return h_out
 
 
-def linear_normed(x, part, nw, nb, eps, kind, w_gate, w_up=None, act_kind=ACT_NONE, y=None):
-    """y = act(norm(x) @ W.T) with the row norm of x (width 1024) taken from the tile statistics `part` that
-    linear_resid wrote with x; act_kind ACT_NONE (w_up None), ACT_SWIGLU (w_up) or ACT_GELU."""
+def fold_norm(w, nw, nb=None):
+    """Load-time preparation of a projection w [N, K] that consumes normed rows (linear_normed): the norm's weight
+    nw [K] (and LayerNorm bias nb [K]) folded in. Returns (packed dt(w * nw), u, v): for LayerNorm the fp32 column
+    vectors u[n] = sum_k dt(w * nw)[n, k] and v[n] = sum_k nb[k] w[n, k]; None for RMSNorm. A joined gate|up weight
+    [2I, K] gives u, v in the same [gate | up] order that linear_normed takes with ACT_SWIGLU."""
+    _dev(w, nw, nb)
+    if w.dim() != 2 or nw.numel() != w.shape[1] or (nb is not None and nb.numel() != w.shape[1]):
+        raise ValueError("fold_norm: w [N, K] with nw (and nb) of K elements")
+    wf = (w.float() * nw.float()[None]).to(w.dtype).contiguous()
+    packed = pack_weight(wf)
+    if nb is None:
+        return packed, None, None
+    return packed, wf.float().sum(1).contiguous(), (w.float() @ nb.float()).contiguous()
+
+
+def linear_normed(x, part, eps, kind, w_gate, w_up=None, act_kind=ACT_NONE, u=None, v=None, y=None):
+    """y = act(norm(x) @ W.T) for rows x of width 1024 whose tile statistics linear_resid left in `part`, with the
+    weights prepared by fold_norm (u, v: its column vectors, LayerNorm only; [2N] for ACT_SWIGLU). act_kind
+    ACT_NONE (w_up None), ACT_SWIGLU (w_up) or ACT_GELU."""
     M, K, y = _lin_args(x, w_gate, y, w_gate.N)
-    _dev(part, nw, nb)
+    _dev(part, u, v)
     if act_kind == ACT_SWIGLU and (not isinstance(w_up, PackedWeight) or (w_up.N, w_up.K) != (w_gate.N, w_gate.K)):
         raise ValueError("linear_normed: w_up must be a packed weight of w_gate's shape")
     if part.dtype != torch.float32 or not part.is_contiguous() or part.numel() < tile_stats_elems(M, K):
         raise ValueError("linear_normed: part must hold the tile statistics of x")
-    for t, name in ((nw, "nw"), (nb, "nb")):
-        if t is not None and (t.dtype != x.dtype or not t.is_contiguous() or t.numel() != K):
-            raise ValueError(f"linear_normed: {name} must be a contiguous [{K}] {x.dtype} vector")
-    check(lib().m3x_linear_normed(_p(x), x.stride(0), _p(part), _p(nw), _p(nb), eps, kind, _p(w_gate.data),
+    ncol = w_gate.N * (2 if act_kind == ACT_SWIGLU else 1)
+    if kind == NORM_LAYER:
+        for t, name in ((u, "u"), (v, "v")):
+            if t is None or t.dtype != torch.float32 or not t.is_contiguous() or t.numel() != ncol:
+                raise ValueError(f"linear_normed: LayerNorm needs fold_norm's {name} ({ncol} float32)")
+    check(lib().m3x_linear_normed(_p(x), x.stride(0), _p(part), _p(u), _p(v), eps, kind, _p(w_gate.data),
                                   _p(w_up.data if act_kind == ACT_SWIGLU else None), _p(y), y.stride(0), M,
                                   w_gate.N, K, act_kind, _dt(x), _stream()), "linear_normed")
     return y

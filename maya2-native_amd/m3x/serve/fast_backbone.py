@@ -15,9 +15,13 @@ How a step runs here:
   - Each (row bucket, context bucket) has one hipGraph over its own buffers; steps with inline prefills use a
     separate graph whose attention walks a host-built list of work items (prefill rows of one slot share one
     pass over its keys).
-  - The graph body per layer: [add+]RMSNorm -> q|k|v GEMM -> q/k-norm + RoPE + K/V cache write -> decode
-    attention in place over the cache -> o GEMM -> add+RMSNorm -> gate|up GEMM with SwiGLU -> down GEMM, whose
-    output the next layer's add+RMSNorm consumes (the reference's fuse_rope path, :187-203).
+  - The graph body per layer (the reference's fuse_rope path, :187-203): q|k|v GEMM with the input RMSNorm
+    folded in (the norm weight in the packed weight, each row's 1 / rms in the epilogue) -> q/k-norm + RoPE + K/V
+    cache write -> decode attention in place over the cache -> o GEMM that adds into the residual and leaves the
+    row's tile statistics -> gate|up GEMM with the post-attention RMSNorm folded in and SwiGLU behind -> down GEMM
+    that adds into the residual. Only the first
+    layer's input norm and the final norm run as add+norm kernels (widths other than 1024 keep the separate
+    add+RMSNorm launches).
   - q|k|v and gate|up are joined into one weight each, with the model's modules re-pointed at row views of
     the joined tensors (no second copy of the HF weights, as the reference's fuse_proj does, :130-141), and every
     projection also gets a copy in MFMA fragment order (ops.pack_weight).
@@ -120,19 +124,31 @@ class StaticBackbone:
         self.hidden = cfg.hidden_size
         self.scaling = self.head_dim ** -0.5
         self.eps = cfg.rms_norm_eps
+        # width 1024 (Qwen3-0.6B): the o and down projections add into the residual and leave its tile statistics,
+        # and the q|k|v and gate|up projections, whose packed weights carry the RMSNorm weight, scale each row of
+        # their product by the row's 1 / rms (no add+norm launch)
+        self.fused_norms = self.hidden == 1024
 
     def _pack_weights(self):
         self.wqkv, self.wgu = [], []
         self.pqkv, self.pgate, self.pup, self.po, self.pdown = [], [], [], [], []
-        for layer in self.layers:
+        for i, layer in enumerate(self.layers):
             a, m = layer.self_attn, layer.mlp
             if a.q_proj.bias is not None or getattr(m.gate_proj, 'bias', None) is not None:
                 raise ValueError('fuse_proj expects bias-free projections')
             self.wqkv.append(_join([a.q_proj, a.k_proj, a.v_proj]))
             self.wgu.append(_join([m.gate_proj, m.up_proj]))
             inter = m.gate_proj.weight.shape[0]
-            self.pqkv.append(ops.pack_weight(self.wqkv[-1]))
-            gu = ops.pack_weight(self.wgu[-1])
+            # with fused norms the RMSNorm weight in front of q|k|v (after the first layer) and of gate|up is folded
+            # into the packed copy; the HF modules keep their own weights
+            if self.fused_norms and i > 0:
+                self.pqkv.append(ops.fold_norm(self.wqkv[-1], layer.input_layernorm.weight)[0])
+            else:
+                self.pqkv.append(ops.pack_weight(self.wqkv[-1]))
+            if self.fused_norms:
+                gu = ops.fold_norm(self.wgu[-1], layer.post_attention_layernorm.weight)[0]
+            else:
+                gu = ops.pack_weight(self.wgu[-1])
             self.pgate.append(gu.rows(0, inter))
             self.pup.append(gu.rows(inter, 2 * inter))
             self.po.append(ops.pack_weight(a.o_proj.weight))
@@ -231,6 +247,8 @@ class StaticBackbone:
         for name, width in (('h', hid), ('y', hid), ('qkv', (H + 2 * KV) * D), ('o', H * D), ('a', hid),
                             ('act', I), ('pend', hid), ('out', hid)):
             setattr(b, name, torch.empty(rows, width, dtype=dt, device=dev))
+        # the 16-column tile statistics the residual projections leave for the next norm
+        b.part = torch.empty(ops.tile_stats_elems(rows, hid), dtype=torch.float32, device=dev)
         b.q = torch.empty(rows, H, D, dtype=dt, device=dev)
         b.chunk = attn_chunk(rows, KV, ctx)
         b.items = None
@@ -250,22 +268,36 @@ class StaticBackbone:
         H, KV, D, eps = self.heads, self.kv_heads, self.head_dim, self.eps
         ops.positions(self.lengths, b.slots, b.offset, b.pos)
         o3 = b.o.view(b.rows, H, D)
+        fused = self.fused_norms
+        rms = ops.NORM_RMS
         for i, layer in enumerate(self.layers):
             attn, kc, vc = layer.self_attn, self._kfull[i], self._vfull[i]
+            w_in, w_post = layer.input_layernorm.weight, layer.post_attention_layernorm.weight
             if i == 0:
-                ops.add_rms(b.x, None, layer.input_layernorm.weight, eps, y=b.y)
-            else:  # the previous layer's down projection joins the residual here
-                ops.add_rms(b.h, b.pend, layer.input_layernorm.weight, eps, h_out=b.h, y=b.y)
-            ops.linear(b.y, self.pqkv[i], b.qkv)
+                ops.add_rms(b.x, None, w_in, eps, y=b.y)
+                ops.linear(b.y, self.pqkv[i], b.qkv)
+            elif fused:  # the norm of the residual the previous down projection left, folded into the projection
+                ops.linear_normed(b.h, b.part, eps, rms, self.pqkv[i], y=b.qkv)
+            else:
+                ops.add_rms(b.h, b.pend, w_in, eps, h_out=b.h, y=b.y)
+                ops.linear(b.y, self.pqkv[i], b.qkv)
             ops.qk_norm_rope_cache(b.qkv, b.q, kc, vc, b.slots, b.pos, self.cos, self.sin, attn.q_norm.weight,
                                    attn.k_norm.weight, eps, H, KV)
             ops.decode_attn(b.q, kc, vc, o3, b.slots, b.pos, self.scaling, b.ctx, b.chunk, b.attn_ws, H, KV,
                             items=b.items)
-            ops.linear(b.o, self.po[i], b.a)
-            ops.add_rms(b.x if i == 0 else b.h, b.a, layer.post_attention_layernorm.weight, eps, h_out=b.h, y=b.y)
-            ops.linear_act(b.y, self.pgate[i], self.pup[i], ops.ACT_SWIGLU, b.act)
-            ops.linear(b.act, self.pdown[i], b.pend)
-        ops.add_rms(b.h, b.pend, self.norm.weight, eps, h_out=b.h, y=b.out)
+            if fused:
+                ops.linear_resid(b.o, self.po[i], b.x if i == 0 else b.h, b.h, b.part, rms)
+                ops.linear_normed(b.h, b.part, eps, rms, self.pgate[i], self.pup[i], ops.ACT_SWIGLU, y=b.act)
+                ops.linear_resid(b.act, self.pdown[i], b.h, b.h, b.part, rms)
+            else:
+                ops.linear(b.o, self.po[i], b.a)
+                ops.add_rms(b.x if i == 0 else b.h, b.a, w_post, eps, h_out=b.h, y=b.y)
+                ops.linear_act(b.y, self.pgate[i], self.pup[i], ops.ACT_SWIGLU, b.act)
+                ops.linear(b.act, self.pdown[i], b.pend)
+        if fused:
+            ops.add_rms(b.h, None, self.norm.weight, eps, y=b.out)
+        else:
+            ops.add_rms(b.h, b.pend, self.norm.weight, eps, h_out=b.h, y=b.out)
         ops.lengths_add(self.lengths, b.slots, b.real)
         return b.out
 

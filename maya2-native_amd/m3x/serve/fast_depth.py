@@ -53,7 +53,14 @@ def _norm_spec(mod, dtype, device):
                            eps=float(torch.finfo(dtype).eps if eps is None else eps))
 
 
-def _block(blk, dtype, device):
+def _folded(mod, norm, dtype, device):
+    """(packed, u, v) of a projection consuming rows normed by `norm`, the norm folded in (ops.fold_norm)."""
+    return ops.fold_norm(_dev_copy(mod.weight, dtype, device), norm.w, norm.b)
+
+
+def _block(blk, dtype, device, fold):
+    """A trunk block's norms and packed weights. fold: also the copies with the norms folded in for the fused-norm
+    launch path (fq: q|k|v after n1; fg, fu: gate and up (or f1) after n2, with their column vectors)."""
     L = SimpleNamespace(n1=_norm_spec(blk.n1, dtype, device), n2=_norm_spec(blk.n2, dtype, device),
                         qkv=_packed(blk.qkv, dtype, device), o=_packed(blk.o, dtype, device))
     if hasattr(blk, 'gate_up'):
@@ -63,6 +70,14 @@ def _block(blk, dtype, device):
     else:
         L.act, L.wg, L.wu, L.w2 = ops.ACT_GELU, _packed(blk.f1, dtype, device), None, _packed(blk.f2, dtype, device)
         L.ffn = L.wg.N
+    if fold:
+        L.fq = _folded(blk.qkv, L.n1, dtype, device)
+        if L.act == ops.ACT_SWIGLU:
+            p, u, v = _folded(blk.gate_up, L.n2, dtype, device)
+            L.fg, L.fu, L.fuv = p.rows(0, L.ffn), p.rows(L.ffn, p.N), (u, v)
+        else:
+            p, u, v = _folded(blk.f1, L.n2, dtype, device)
+            L.fg, L.fu, L.fuv = p, None, (u, v)
     return L
 
 
@@ -118,10 +133,16 @@ class FastDepth:
             lvl = _dev_copy(d.level_emb.weight, dt, dev)
             self.embed = ((lo @ up.t()).view(N_LEVELS - 1, self.n_codes, self.D) + lvl[1:N_LEVELS, None]).contiguous()
             self.level0 = lvl[0].clone()
-        self.trunks = [[_block(blk, dt, dev) for blk in blocks] for blocks in d.groups]
+        # 16-bit trunks of width 1024 take the fused-norm launch path: the o and down projections add into the
+        # residual and leave its tile statistics; the next q|k|v, gate|up (f1) and the codebook head carry the norm
+        # folded into their weights and apply each row's scale (and shift) in their epilogue
+        self.fused_norms = dt != torch.float32 and self.D == 1024
+        self.trunks = [[_block(blk, dt, dev, self.fused_norms) for blk in blocks] for blocks in d.groups]
         self.layers = len(self.trunks[0])
         self.final_norm = _norm_spec(d.norm, dt, dev)
         self.heads = [_packed(h, dt, dev) for h in d.heads]  # 31 x [n_codes, D]
+        # the heads with the final norm folded in (fused-norm launch path)
+        self.fheads = [_folded(h, self.final_norm, dt, dev) for h in d.heads] if self.fused_norms else None
         self.cross = getattr(d, 'cross', None)
         self.cross_w = None if self.cross is None else [(_packed(c.kv, dt, dev), _packed(c.o, dt, dev))
                                                        for c in self.cross]
@@ -166,6 +187,7 @@ class FastDepth:
         for name in ('xw', 'xw2', 'yw', 'y2', 'att', 'a', 'f'):
             setattr(b, name, torch.empty(R, D, dtype=dt, device=dev))
         b.qkv = torch.empty(R, 3 * D, dtype=dt, device=dev)
+        b.part = torch.empty(ops.tile_stats_elems(R, D), dtype=torch.float32, device=dev)
         b.ffn_act = torch.empty(R, max(L.ffn for t in self.trunks for L in t), dtype=dt, device=dev)
         b.kd = [torch.zeros(B, self.H, N_LEVELS, self.hd, dtype=dt, device=dev) for _ in range(self.layers)]
         b.vd = [torch.zeros(B, self.H, N_LEVELS, self.hd, dtype=dt, device=dev) for _ in range(self.layers)]
@@ -176,27 +198,51 @@ class FastDepth:
 
     def _trunk(self, b, layers, T, p0):
         """The trunk over T positions from p0 per seat (rows b.yw: the first layer's normed input, b.xw: the
-        residual). On return b.yw[:B] holds the final-normed last position."""
+        residual). On return b.xw[:B] holds the last position's residual; with fused norms (self.fused_norms)
+        b.part holds its tile statistics for the final norm (applied by the head projection), else b.yw[:B] holds
+        the final-normed row."""
         B, D = b.B, self.D
         R = B * T
         incremental = T == 1
+        fused = self.fused_norms
         for li, L in enumerate(layers):
             # at a group start the last layer is evaluated at the last position only
             tq0 = T - 1 if (li == self.layers - 1 and not incremental) else 0
             Tq = T - tq0
             R2 = B * Tq
-            ops.linear(b.yw[:R], L.qkv, b.qkv[:R])
+            if li > 0 and fused:  # the layer's input norm, from the residual's tile statistics
+                w, u, v = L.fq
+                ops.linear_normed(b.xw[:R], b.part, L.n1.eps, L.n1.kind, w, u=u, v=v, y=b.qkv[:R])
+            else:
+                ops.linear(b.yw[:R], L.qkv, b.qkv[:R])
             ops.depth_attn(b.qkv[:R], b.kd[li], b.vd[li], b.att[:R2], B, T, p0, tq0, self.H, self.hd,
                            self.hd ** -0.5, True)
-            ops.linear(b.att[:R2], L.o, b.a[:R2])
-            ops.add_norm(b.xw[:R].view(B, T, D)[:, tq0:], b.a[:R2], None, b.xw2[:R2], b.y2[:R2], L.n2.w, L.n2.b,
-                         L.n2.eps, Tq, L.n2.kind)
-            ops.linear_act(b.y2[:R2], L.wg, L.wu, L.act, b.ffn_act[:R2, :L.ffn])
-            ops.linear(b.ffn_act[:R2, :L.ffn], L.w2, b.f[:R2])
             nxt = layers[li + 1].n1 if li + 1 < self.layers else self.final_norm
             c = None if b.crossb is None else b.crossb[:, li * D:(li + 1) * D]
-            ops.add_norm(b.xw2[:R2], b.f[:R2], c, b.xw[:R2], b.yw[:R2], nxt.w, nxt.b, nxt.eps, Tq, nxt.kind)
+            if fused:
+                # residual rows of the attended positions: all rows, or each seat's last one (row stride T * D)
+                res = b.xw[:R] if tq0 == 0 else b.xw[:R].view(B, T * D)[:, tq0 * D:]
+                ops.linear_resid(b.att[:R2], L.o, res, b.xw2[:R2], b.part, L.n2.kind)
+                ops.linear_normed(b.xw2[:R2], b.part, L.n2.eps, L.n2.kind, L.fg, L.fu, L.act, u=L.fuv[0], v=L.fuv[1],
+                                  y=b.ffn_act[:R2, :L.ffn])
+                ops.linear_resid(b.ffn_act[:R2, :L.ffn], L.w2, b.xw2[:R2], b.xw[:R2], b.part, nxt.kind, c=c, tc=Tq)
+            else:
+                ops.linear(b.att[:R2], L.o, b.a[:R2])
+                ops.add_norm(b.xw[:R].view(B, T, D)[:, tq0:], b.a[:R2], None, b.xw2[:R2], b.y2[:R2], L.n2.w,
+                             L.n2.b, L.n2.eps, Tq, L.n2.kind)
+                ops.linear_act(b.y2[:R2], L.wg, L.wu, L.act, b.ffn_act[:R2, :L.ffn])
+                ops.linear(b.ffn_act[:R2, :L.ffn], L.w2, b.f[:R2])
+                ops.add_norm(b.xw2[:R2], b.f[:R2], c, b.xw[:R2], b.yw[:R2], nxt.w, nxt.b, nxt.eps, Tq, nxt.kind)
             R, T, p0 = R2, Tq, p0 + tq0
+
+    def _head(self, b, level):
+        """Logits of `level` from the trunk's last rows: the final norm and the codebook head."""
+        fn = self.final_norm
+        if self.fused_norms:
+            w, u, v = self.fheads[level - 1]
+            ops.linear_normed(b.xw[:b.B], b.part, fn.eps, fn.kind, w, u=u, v=v, y=b.logits)
+        else:
+            ops.linear(b.yw[:b.B], self.heads[level - 1], b.logits)
 
     def run(self, b, uniforms=True, trace=None):
         """The frame body over buffer set `b` (inputs b.slots, b.h, b.codes[:, 0]); fills b.codes and b.feedback.
@@ -239,7 +285,7 @@ class FastDepth:
                 ops.add_norm(b.prefix[:, p0:p0 + T], None, None, b.xw[:B * T], b.yw[:B * T], n1.w, n1.b, n1.eps, T,
                              n1.kind)
             self._trunk(b, layers, T, p0)
-            ops.linear(b.yw[:B], self.heads[level - 1], b.logits)
+            self._head(b, level)
             if trace is not None:
                 trace.append(b.logits.clone())
             u = b.u[:, level - 1]
