@@ -99,34 +99,39 @@ __device__ __forceinline__ float2 norm_row_stats(const float2 (&p)[TPT], int K, 
   return make_float2(rstd, -mean * rstd);
 }
 
-// PRO prologue, in two halves around the kernel's own loads. load issues the loads of the tile statistics of rows
-// m0 .. m0 + ROWS - 1 (8 threads per row, NT threads, PASSES rounds); finish, once the kernel's activation and
-// weight loads are in flight, merges them into the row scale and shift st[ROWS] in LDS. The caller then waits at a
-// barrier before the epilogue reads them. Rows past M get (0, 0) and are never stored.
+// PRO statistics, in two halves around the kernel's main loop. load issues the loads of the tile statistics of rows
+// m0 .. m0 + ROWS - 1 (8 threads per row, NT threads, PASSES rounds) before the kernel's own loads; finish, after
+// the main loop, merges them into the row scale and shift st[ROWS] in LDS. The caller then waits at a barrier
+// before the epilogue reads them. Rows past M get (0, 0) and are never stored.
 template <int ROWS, int NT, int TPT>
 struct NormStage {
   static constexpr int PASSES = (ROWS * 8 + NT - 1) / NT;
   float2 p[PASSES][TPT];
+  // with fewer rows than 8 lanes per row need, only the first ROWS / 8 waves hold statistics (a wave-uniform test:
+  // the other waves issue no loads)
+  static __device__ __forceinline__ bool active() {
+    return ROWS * 8 >= NT || __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) < ROWS / 8;
+  }
   __device__ __forceinline__ void load(const NormIn& ni, int m0, int M, int K) {
+    if (!active()) return;
     const int tid = threadIdx.x;
 #pragma unroll
     for (int ps = 0; ps < PASSES; ++ps) {
-      const int r = (tid + ps * NT) >> 3;
-      const int m = m0 + r;
+      // clamped to a valid row: no branch around the loads (a divergent join would wait for every load in
+      // flight); rows past M and threads past the block are never stored
+      const int r = min((tid + ps * NT) >> 3, ROWS - 1);
+      const int m = min(m0 + r, M - 1);
+      const float4* src = reinterpret_cast<const float4*>(ni.part + (long)m * (K >> 4) + (tid & 7) * TPT);
 #pragma unroll
-      for (int j = 0; j < TPT; ++j) p[ps][j] = make_float2(0.f, 0.f);
-      if (r < ROWS && m < M) {
-        const float4* src = reinterpret_cast<const float4*>(ni.part + (long)m * (K >> 4) + (tid & 7) * TPT);
-#pragma unroll
-        for (int j = 0; j < TPT / 2; ++j) {
-          const float4 v = src[j];
-          p[ps][2 * j] = make_float2(v.x, v.y);
-          p[ps][2 * j + 1] = make_float2(v.z, v.w);
-        }
+      for (int j = 0; j < TPT / 2; ++j) {
+        const float4 v = src[j];
+        p[ps][2 * j] = make_float2(v.x, v.y);
+        p[ps][2 * j + 1] = make_float2(v.z, v.w);
       }
     }
   }
   __device__ __forceinline__ void finish(const NormIn& ni, int m0, int M, int K, float2* st) {
+    if (!active()) return;
     const int tid = threadIdx.x;
 #pragma unroll
     for (int ps = 0; ps < PASSES; ++ps) {
@@ -156,21 +161,36 @@ __device__ __forceinline__ void norm_apply(f32x4_t& acc, const float2* pst, int 
   }
 }
 
-// EPI_RESID for one lane's 4 outputs (columns n .. n + 3 of row m, acc as accumulated): stores the residual row's
-// values and, with the other 3 lanes of the 16-column tile (lanes li + 16 lg'), the tile's statistics
-// part[m * (N / 16) + tile]. Every lane of the wave calls it (cross-lane sums); rows past M store nothing.
+// The residual operands of one lane's 4 outputs (columns n .. n + 3 of row m), loaded when the kernel starts so
+// that the epilogue does not wait on them: h[m, n ..] and, with a per-seat constant, c[m / tc, n ..].
+struct ResidPre {
+  uint2 h, c;
+};
+// Addresses are clamped to valid elements (values of rows past M or columns past N are never stored), and the
+// constant falls back to h's element when absent, so the loads sit in no branch.
+__device__ __forceinline__ ResidPre resid_prefetch(const ResidOut& ro, int m, int n, int M, int N) {
+  const int mc = min(m, M - 1), nc = min(n, N - 4);
+  const uint16_t* hp = ro.h + (long)mc * ro.ldh + nc;
+  const uint16_t* cp = ro.c ? ro.c + (long)(mc / ro.tc) * ro.ldc + nc : hp;
+  return ResidPre{*reinterpret_cast<const uint2*>(hp), *reinterpret_cast<const uint2*>(cp)};
+}
+
+// EPI_RESID for one lane's 4 outputs (columns n .. n + 3 of row m, acc as accumulated, pre its prefetched
+// operands): stores the residual row's values and, with the other 3 lanes of the 16-column tile (lanes
+// li + 16 lg'), the tile's statistics part[m * (N / 16) + tile]. Every lane of the wave calls it (cross-lane
+// sums); rows past M store nothing.
 template <int DT>
-__device__ __forceinline__ void resid_quad(const f32x4_t& acc, int m, int n, int tile, int M, int N, int lg,
-                                           const ResidOut& ro, uint16_t* __restrict__ Y, long ldy) {
+__device__ __forceinline__ void resid_quad(const f32x4_t& acc, const ResidPre& pre, int m, int n, int tile, int M,
+                                           int N, int lg, const ResidOut& ro, uint16_t* __restrict__ Y, long ldy) {
   const bool valid = m < M && n < N;  // N % 16 == 0: a tile is wholly inside or wholly past N
   float v[4] = {0.f, 0.f, 0.f, 0.f};
   if (valid) {
-    const uint2 hh = *reinterpret_cast<const uint2*>(ro.h + (long)m * ro.ldh + n);
+    const uint2 hh = pre.h;
     const uint16_t h4[4] = {(uint16_t)hh.x, (uint16_t)(hh.x >> 16), (uint16_t)hh.y, (uint16_t)(hh.y >> 16)};
 #pragma unroll
     for (int r = 0; r < 4; ++r) v[r] = rnd<DT>(E<DT>::to_f(h4[r]) + rnd<DT>(acc[r]));
     if (ro.c) {
-      const uint2 cc = *reinterpret_cast<const uint2*>(ro.c + (long)(m / ro.tc) * ro.ldc + n);
+      const uint2 cc = pre.c;
       const uint16_t c4[4] = {(uint16_t)cc.x, (uint16_t)(cc.x >> 16), (uint16_t)cc.y, (uint16_t)(cc.y >> 16)};
 #pragma unroll
       for (int r = 0; r < 4; ++r) v[r] = rnd<DT>(v[r] + E<DT>::to_f(c4[r]));
@@ -200,8 +220,8 @@ __device__ __forceinline__ void resid_quad(const f32x4_t& acc, int m, int n, int
 template <int DT, int MT, int NW, int KW, int EPI, bool PRO>
 __device__ __forceinline__ void linear_finish(f32x4_t (&acc)[EPI == EPI_SWIGLU ? 2 : 1][MT], f32x4_t* red, int wn,
                                               int wk, int lane, int n0, int m0, uint16_t* __restrict__ Y, long ldy,
-                                              int M, int N, const ResidOut& ro, const float2* pst,
-                                              const NormIn& ni) {
+                                              int M, int N, const ResidOut& ro, const ResidPre* pre,
+                                              const float2* pst, const NormIn& ni) {
   constexpr int NA = EPI == EPI_SWIGLU ? 2 : 1;
   const int li = lane & 15;
   const int lg = lane >> 4;
@@ -234,7 +254,8 @@ __device__ __forceinline__ void linear_finish(f32x4_t (&acc)[EPI == EPI_SWIGLU ?
   }
   if constexpr (EPI == EPI_RESID) {
 #pragma unroll
-    for (int t = 0; t < MT; ++t) resid_quad<DT>(acc[0][t], m0 + 16 * t + li, n, n0 >> 4, M, N, lg, ro, Y, ldy);
+    for (int t = 0; t < MT; ++t)
+      resid_quad<DT>(acc[0][t], pre[t], m0 + 16 * t + li, n, n0 >> 4, M, N, lg, ro, Y, ldy);
     return;
   }
   const bool vec = (ldy & 3) == 0 && (((uintptr_t)Y) & 7) == 0 && n + 3 < N;
@@ -320,40 +341,33 @@ __global__ __launch_bounds__(256) void linear_kernel(const uint16_t* __restrict_
   wp[0] = Wp + ((long)nt * ksteps * 64 + lane) * 8;
   if constexpr (DUAL) wp[NA - 1] = W2p + ((long)nt * ksteps * 64 + lane) * 8;
 
-  // Activation vectors: v = tid + 256 j -> slice q, row r, 16-byte column c16 of the chunk. Rows past M and
-  // steps past a slice are not loaded: their registers keep finite earlier values, whose products are never
-  // stored.
+  // Activation vectors: v = tid + 256 j -> slice q, row r, 16-byte column c16 of the chunk.
   u16x8 X0[VPT], X1[VPT];
-#pragma unroll
-  for (int j = 0; j < VPT; ++j)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) X0[j].v[e] = X1[j].v[e] = 0;
   auto xload = [&](int c, u16x8(&Xr)[VPT]) {
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-      const int v = tid + 256 * j;
-      if (NVEC % 256 == 0 || v < NVEC) {
-        const int q = v / (ROWS * VPR);
-        const int rem = v - q * (ROWS * VPR);
-        const int r = rem / VPR;
-        const int c16 = rem - r * VPR;
-        const int m = m0 + r;
-        const int step = q * span + c * U + (c16 >> 2);
-        if (m < M && step < min(ksteps, (q + 1) * span)) Xr[j] = ld16(X + (long)m * ldx + step * 32 + (c16 & 3) * 8);
-      }
+      // clamped addresses, no branch (rows past M re-read row M - 1, steps past K the last step: never stored or
+      // never multiplied)
+      const int v = NVEC % 256 == 0 ? tid + 256 * j : min(tid + 256 * j, NVEC - 1);
+      const int q = v / (ROWS * VPR);
+      const int rem = v - q * (ROWS * VPR);
+      const int r = rem / VPR;
+      const int c16 = rem - r * VPR;
+      const int m = min(m0 + r, M - 1);
+      const int step = min(q * span + c * U + (c16 >> 2), ksteps - 1);
+      Xr[j] = ld16(X + (long)m * ldx + step * 32 + (c16 & 3) * 8);
     }
   };
   auto xstore = [&](int buf, int c, const u16x8(&Xr)[VPT]) {
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-      const int v = tid + 256 * j;
-      if (NVEC % 256 == 0 || v < NVEC) {
-        const int q = v / (ROWS * VPR);
-        const int rem = v - q * (ROWS * VPR);
-        const int r = rem / VPR;
-        const int c16 = rem - r * VPR;
-        st16(&xs[buf][(q * ROWS + r) * LDR + c16 * 8], Xr[j]);
-      }
+      // threads past the block repeat the last vector's store (same value, same place): no branch
+      const int v = NVEC % 256 == 0 ? tid + 256 * j : min(tid + 256 * j, NVEC - 1);
+      const int q = v / (ROWS * VPR);
+      const int rem = v - q * (ROWS * VPR);
+      const int r = rem / VPR;
+      const int c16 = rem - r * VPR;
+      st16(&xs[buf][(q * ROWS + r) * LDR + c16 * 8], Xr[j]);
     }
   };
   u16x8 W0[U][NA], W1[U][NA];
@@ -392,9 +406,12 @@ __global__ __launch_bounds__(256) void linear_kernel(const uint16_t* __restrict_
     xload(1, X1);
     wload(1, W1);
   }
-  if constexpr (PRO) {
-    ns.finish(ni, m0, M, PRO_K, pst);
-    __syncthreads();
+  ResidPre pre[MT];
+  if constexpr (EPI == EPI_RESID) {
+    if (wk == 0) {
+#pragma unroll
+      for (int t = 0; t < MT; ++t) pre[t] = resid_prefetch(ro, m0 + 16 * t + li, n0 + 4 * lg, M, N);
+    }
   }
   xstore(0, 0, X0);
   if (nch > 2) xload(2, X0);
@@ -413,8 +430,12 @@ __global__ __launch_bounds__(256) void linear_kernel(const uint16_t* __restrict_
     __syncthreads();
   }
 
+  if constexpr (PRO) {  // the rows' scale and shift, from statistics that arrived long ago
+    ns.finish(ni, m0, M, PRO_K, pst);
+    __syncthreads();
+  }
   linear_finish<DT, MT, NW, KW, EPI, PRO>(acc, reinterpret_cast<f32x4_t*>(&xs[0][0]), wn, wk, lane, n0, m0, Y,
-                                          ldy, M, N, ro, pst, ni);
+                                          ldy, M, N, ro, pre, pst, ni);
 }
 
 // One-shot variant: every weight fragment of the wave's K slice (S steps of 32) and the workgroup's whole
@@ -425,7 +446,8 @@ __global__ __launch_bounds__(256) void linear_kernel(const uint16_t* __restrict_
 // g of row r stored at g ^ (r % 16), so the 16 rows a fragment read touches fall in 16 different bank groups;
 // otherwise rows are padded by 16 bytes.
 // PRO (K == PRO_K): the tile statistics are requested before the activation block and merged into the rows' scale
-// and shift once the weight fragments are in flight; the epilogue applies them.
+// and shift after the products; the epilogue applies them. EPI_RESID: the residual operands are requested after the
+// weight fragments.
 template <int DT, int MT, int NW, int NWAVES, int EPI, int S, bool PRO>
 __global__ __launch_bounds__(64 * NWAVES) void linear_oneshot_kernel(const uint16_t* __restrict__ X, long ldx,
                                                                      const uint16_t* __restrict__ Wp,
@@ -477,18 +499,18 @@ __global__ __launch_bounds__(64 * NWAVES) void linear_oneshot_kernel(const uint1
   // returns in issue order), so the products run while the rest of the slab is still arriving. Measured at
   // 224 rows: 5-24 % faster than weights first (224 x 1024 x 3072: 9.2 -> 7.0 us).
   // activation vector v = tid + NT j -> slice q, row r, granule g
+  // Loads come from addresses clamped into the block and below M (rows past M re-read row M - 1, whose products
+  // in those columns are never stored): no branch around them, so no join waits for the loads in flight.
   u16x8 Xr[VPT];
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int v = tid + NT * j;
+    const int v = NVEC % NT == 0 ? tid + NT * j : min(tid + NT * j, NVEC - 1);
     const int q = v / (ROWS * GR);
     const int rem = v - q * (ROWS * GR);
     const int r = rem / GR;
     const int g = rem - r * GR;
-    const int m = m0 + r;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) Xr[j].v[e] = 0;
-    if ((NVEC % NT == 0 || v < NVEC) && m < M) Xr[j] = ld16(X + (long)m * ldx + q * KS + g * 8);
+    const int m = min(m0 + r, M - 1);
+    Xr[j] = ld16(X + (long)m * ldx + q * KS + g * 8);
   }
   u16x8 Wr[S][NA];
   {
@@ -500,18 +522,25 @@ __global__ __launch_bounds__(64 * NWAVES) void linear_oneshot_kernel(const uint1
       if constexpr (DUAL) Wr[s][NA - 1] = ld16(w1 + (long)(s0 + s) * 512);
     }
   }
-  if constexpr (PRO) {
-    ns.finish(ni, m0, M, PRO_K, pst);
-    __syncthreads();
+  // the 16-wave plans over K >= 2816 have no registers to spare for the residual operands before the products:
+  // they load them after
+  constexpr bool EARLY = !(NWAVES == 16 && S > 16);
+  ResidPre pre[MT];
+  if constexpr (EPI == EPI_RESID && EARLY) {
+    if (wk == 0) {
+#pragma unroll
+      for (int t = 0; t < MT; ++t) pre[t] = resid_prefetch(ro, m0 + 16 * t + li, n0 + 4 * lg, M, N);
+    }
   }
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int v = tid + NT * j;
+    // threads past the block repeat the last vector's store (same value, same place): no branch
+    const int v = NVEC % NT == 0 ? tid + NT * j : min(tid + NT * j, NVEC - 1);
     const int q = v / (ROWS * GR);
     const int rem = v - q * (ROWS * GR);
     const int r = rem / GR;
     const int g = rem - r * GR;
-    if (NVEC % NT == 0 || v < NVEC) st16(&xs[(q * ROWS + r) * LDR + ((SWZ ? g ^ (r & 15) : g) << 3)], Xr[j]);
+    st16(&xs[(q * ROWS + r) * LDR + ((SWZ ? g ^ (r & 15) : g) << 3)], Xr[j]);
   }
   __syncthreads();
 
@@ -531,9 +560,16 @@ __global__ __launch_bounds__(64 * NWAVES) void linear_oneshot_kernel(const uint1
       for (int a = 0; a < NA; ++a) acc[a][t] = mfma16x16x32<DT>(Wr[s][a], b, acc[a][t]);
     }
   }
+  if constexpr (PRO) ns.finish(ni, m0, M, PRO_K, pst);  // the rows' scale and shift, read after the barrier
+  if constexpr (EPI == EPI_RESID && !EARLY) {
+    if (wk == 0) {
+#pragma unroll
+      for (int t = 0; t < MT; ++t) pre[t] = resid_prefetch(ro, m0 + 16 * t + li, n0 + 4 * lg, M, N);
+    }
+  }
   __syncthreads();  // every wave is done with the block before it holds the slice partials
   linear_finish<DT, MT, NW, KW, EPI, PRO>(acc, reinterpret_cast<f32x4_t*>(xs), wn, wk, lane, n0, m0, Y, ldy, M, N, ro,
-                                          pst, ni);
+                                          pre, pst, ni);
 }
 
 // Large-M projections (M > 512 rows: steps with inline prefills). A workgroup of 8 waves owns a 2-D tile of 128
@@ -620,9 +656,13 @@ __global__ __launch_bounds__(512, 2) void linear_tiled_kernel(const uint16_t* __
   };
   const int nst = K >> 6;
   gload(0);
-  if constexpr (PRO) {
-    ns.finish(ni, m0, M, PRO_K, pst);
-    __syncthreads();
+  ResidPre pre[2][4];
+  if constexpr (EPI == EPI_RESID) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        pre[i][j] = resid_prefetch(ro, m0 + 16 * (4 * wm + j) + li, (nb * 8 + wt[i]) * 16 + 4 * lg, M, N);
   }
   lstore(0);
   __syncthreads();
@@ -647,6 +687,8 @@ __global__ __launch_bounds__(512, 2) void linear_tiled_kernel(const uint16_t* __
   }
 
   if constexpr (PRO) {
+    ns.finish(ni, m0, M, PRO_K, pst);  // the rows' scale and shift, from statistics that arrived long ago
+    __syncthreads();
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int n = DUAL ? (nb * 4 + wn) * 16 + 4 * lg : (nb * 8 + wt[i]) * 16 + 4 * lg;
@@ -660,7 +702,8 @@ __global__ __launch_bounds__(512, 2) void linear_tiled_kernel(const uint16_t* __
       const int tile = nb * 8 + wt[i];
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        resid_quad<DT>(acc[i][j], m0 + 16 * (4 * wm + j) + li, tile * 16 + 4 * lg, tile, M, N, lg, ro, Y, ldy);
+        resid_quad<DT>(acc[i][j], pre[i][j], m0 + 16 * (4 * wm + j) + li, tile * 16 + 4 * lg, tile, M, N, lg, ro, Y,
+                       ldy);
     }
     return;
   }
