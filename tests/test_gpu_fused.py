@@ -147,4 +147,3 @@ def test_linear_normed_rejects_bad_args(gpu):
     x2 = torch.zeros(4, 2048, dtype=torch.bfloat16, device=gpu)
     with pytest.raises(RuntimeError):  # the norm prologue covers rows of width 1024 only
         ops.linear_normed(x2, torch.zeros(ops.tile_stats_elems(4, 2048), device=gpu), 1e-6, 1, w2)
-
