@@ -22,8 +22,8 @@ struct SampleSmemT {
   float w[CAP];
   unsigned int hist[256];
   float red[ST / 64];
-  int wtot[ST / 64];  // candidates per wave, for the compaction offsets
-  int nkeep, bstar;
+  int nkeep;
+  int ncand;  // candidates placed so far
   int code;  // the drawn code, for the waves that build the next level's input
 };
 using SampleSmem = SampleSmemT<SMAXV>;
@@ -51,15 +51,97 @@ __device__ __forceinline__ unsigned int wave_incl_scan(unsigned int x) {
   return v;
 }
 
-__device__ float block_max(float v, float* red) {
-  v = wave_max_dpp(v);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  float r = red[0];
+// The first of 256 bins (lane l holds the counts c[0..3] of its 4 bins, in the order they are scanned) at which the
+// running count reaches kk, with the count before that bin; every lane of the wave gets the result. (-1, 0) when
+// the total stays below kk (or kk is 0).
+__device__ __forceinline__ void wave_find_bin(const unsigned int (&c)[4], unsigned int kk, int& idx, unsigned int& before) {
+  const int lane = threadIdx.x & 63;
+  const unsigned int s = c[0] + c[1] + c[2] + c[3];
+  const unsigned int incl = wave_incl_scan(s);
+  unsigned int run = incl - s;
+  int found = -1;
+  unsigned int bef = 0;
 #pragma unroll
-  for (int i = 1; i < ST / 64; ++i) r = fmaxf(r, red[i]);
+  for (int i = 0; i < 4; ++i) {
+    if (found < 0 && kk > 0 && run + c[i] >= kk) {
+      found = 4 * lane + i;
+      bef = run;
+    }
+    run += c[i];
+  }
+  const unsigned long long mk = __ballot(found >= 0);
+  const int fl = mk ? __ffsll((long long)mk) - 1 : 0;
+  idx = mk ? __builtin_amdgcn_readlane(found, fl) : -1;
+  before = mk ? (unsigned int)__builtin_amdgcn_readlane((int)bef, fl) : 0u;
+}
+
+// The k-th largest of the valid elements (i < V, not NaN) of a row, counting repeats, by an MSB-first radix select
+// over their ordered keys, 8 bits a pass: each pass histograms the next byte of the keys that share the bytes fixed
+// so far, and every wave finds the bin where the count from the top reaches the remaining rank. With fewer than k
+// valid elements it returns the smallest; with none, NaN. Called by every thread with a block-uniform k, before
+// the candidates are placed: the three histograms (used in turn, each cleared two passes ahead, so one barrier a
+// pass) live in sm.cand after the coarse histogram of topk_select.
+template <int NE, class SM>
+__device__ float radix_kth(const float (&x)[NE], int V, int k, SM& sm) {
+  static_assert(sizeof(sm.cand) >= 4 * 256 * sizeof(unsigned int), "histograms in sm.cand");
+  unsigned int* hb = reinterpret_cast<unsigned int*>(sm.cand) + 256;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  uint32_t key[NE];
+  bool ok[NE];
+#pragma unroll
+  for (int e = 0; e < NE; ++e) {
+    ok[e] = tid + ST * e < V && x[e] == x[e];
+    key[e] = ordkey(x[e]);
+  }
+  hb[tid] = 0;
+  hb[256 + tid] = 0;
   __syncthreads();
-  return r;
+  uint32_t pre = 0;
+  unsigned int kr = (unsigned int)k;
+#pragma unroll
+  for (int pass = 0; pass < 4; ++pass) {
+    const int sh = 24 - 8 * pass;
+    const uint32_t hm = pass == 0 ? 0u : ~0u << (sh + 8);
+    unsigned int* h = hb + 256 * (pass % 3);
+#pragma unroll
+    for (int e = 0; e < NE; ++e) {
+      const bool in = ok[e] && (key[e] & hm) == pre;
+      const uint32_t d = (key[e] >> sh) & 255u;
+      // the keys of a row mostly share their top bytes: the lanes holding the wave's first live digit add their
+      // count with one atomic, the others one each
+      const unsigned long long live = __ballot(in);
+      if (live) {
+        const int first = __ffsll((long long)live) - 1;
+        const uint32_t d0 = (uint32_t)__builtin_amdgcn_readlane((int)d, first);
+        const unsigned long long same = __ballot(in && d == d0);
+        if (lane == first) atomicAdd(&h[d0], (unsigned int)__popcll(same));
+        if (in && d != d0) atomicAdd(&h[d], 1u);
+      }
+    }
+    __syncthreads();
+    if (pass < 2) hb[256 * ((pass + 2) % 3) + tid] = 0;  // last read two passes back, next written after a barrier
+    // lane l scans bins 255 - 4 l .. 252 - 4 l: descending key order
+    unsigned int c[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) c[i] = h[255 - 4 * lane - i];
+    int idx;
+    unsigned int before;
+    if (pass == 0) {
+      const unsigned int total = (unsigned int)__builtin_amdgcn_readlane(
+          (int)wave_incl_scan(c[0] + c[1] + c[2] + c[3]), 63);
+      if (total < kr) kr = total;  // fewer valid elements than k: the smallest of them
+    }
+    wave_find_bin(c, kr, idx, before);
+    if (idx < 0) {  // no valid element (block-uniform)
+      __syncthreads();
+      return __uint_as_float(0x7fc00000u);
+    }
+    pre |= (uint32_t)(255 - idx) << sh;
+    kr -= before;
+  }
+  __syncthreads();  // every wave's last scan precedes the candidate stores into sm.cand
+  return ordkey_inv(pre);
 }
 
 // After this returns, sm.cand[0 .. sm.nkeep) holds the kept candidates in sampling order and sm.w their weights.
@@ -68,13 +150,25 @@ template <int NE, class SM>
 __device__ void topk_select(const float (&x)[NE], int V, int k, SM& sm) {
   const int tid = threadIdx.x;
   const float NEG = -INFINITY;
-  sm.hist[tid] = 0;  // ordered before the histogram by block_max's barriers
-  if (tid == 0) sm.nkeep = 0;
+  sm.hist[tid] = 0;  // ordered before the histograms by the max's barrier
+  unsigned int* h2 = reinterpret_cast<unsigned int*>(sm.cand);  // the coarse histogram (candidates come later)
+  h2[tid] = 0;
+  if (tid == 0) {
+    sm.nkeep = 0;
+    sm.ncand = 0;
+  }
   float lm = NEG;
 #pragma unroll
   for (int e = 0; e < NE; ++e)
     if (tid + ST * e < V) lm = fmaxf(lm, x[e]);
-  const float m = block_max(lm, sm.red);
+  // row max: wave maxima meet in LDS behind one barrier (sm.red is next written by a later call, after further
+  // barriers)
+  lm = wave_max_dpp(lm);
+  if ((tid & 63) == 0) sm.red[tid >> 6] = lm;
+  __syncthreads();
+  float m = sm.red[0];
+#pragma unroll
+  for (int i = 1; i < ST / 64; ++i) m = fmaxf(m, sm.red[i]);
   int bk[NE];
 #pragma unroll
   for (int e = 0; e < NE; ++e) {
@@ -86,36 +180,55 @@ __device__ void topk_select(const float (&x)[NE], int V, int k, SM& sm) {
     }
   }
   __syncthreads();
-  if (tid < 64) {
-    // lane owns bins 4*lane .. 4*lane+3 (bin 255 is excluded from the count)
-    unsigned int c[4], s = 0;
+  // every wave finds b* itself from the histogram (no barrier): lane l holds bins 4 l .. 4 l + 3; bin 255 (8 or
+  // more below the max) is not counted
+  int bstar;
+  unsigned int near = 0;  // elements within 8 of the max, when fewer than k
+  {
+    const int lane = tid & 63;
+    unsigned int c[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int bin = 4 * tid + i;
-      c[i] = bin < 255 ? sm.hist[bin] : 0u;
-      s += c[i];
-    }
-    const unsigned int incl = wave_incl_scan(s);
-    unsigned int run = incl - s;
-    int found = 255;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      run += c[i];
-      if (found == 255 && run >= (unsigned)k && 4 * tid + i < 255) found = 4 * tid + i;
-    }
-    // first lane (lowest bin) that found it
-    unsigned long long mask = __ballot(found < 255);
-    if (tid == 0) sm.bstar = mask ? 0 : 255;
-    if (mask) {
-      const int first = __ffsll((long long)mask) - 1;
-      const int b = __shfl(found, first, 64);
-      if (tid == 0) sm.bstar = b;
-    }
+    for (int i = 0; i < 4; ++i) c[i] = 4 * lane + i < 255 ? sm.hist[4 * lane + i] : 0u;
+    int idx;
+    unsigned int before;
+    wave_find_bin(c, (unsigned int)k, idx, before);
+    bstar = idx < 0 ? 255 : idx;
+    if (idx < 0) near = (unsigned int)__builtin_amdgcn_readlane((int)wave_incl_scan(c[0] + c[1] + c[2] + c[3]), 63);
   }
-  __syncthreads();
-  const int bstar = sm.bstar;
-  // compaction: each wave's count through LDS, a wave's base = the counts of the waves before it (candidates
-  // land in wave order); lanes take consecutive places by ballot rank
+  // Fewer than k elements within 8 of the max (a peaked row, the usual case for a confident model): a coarse
+  // histogram of the rest, 0.5 wide bins from 255/32 below the max (bin 255: 135 or more below, not counted), finds
+  // the bin b2 where the count reaches k; the candidates are then the near elements and those in coarse bins <= b2.
+  int b2 = 0;
+  int cb[NE];
+#pragma unroll
+  for (int e = 0; e < NE; ++e) cb[e] = 255;
+  if (bstar == 255) {
+#pragma unroll
+    for (int e = 0; e < NE; ++e) {
+      if (tid + ST * e < V && bk[e] == 255) {
+        const float d2 = ((m - x[e]) * 32.0f - 255.0f) * 0.0625f;
+        cb[e] = (d2 >= 255.0f || d2 != d2) ? 255 : (int)d2;
+        if (cb[e] < 255) atomicAdd(&h2[cb[e]], 1u);
+      }
+    }
+    __syncthreads();
+    const int lane = tid & 63;
+    unsigned int c[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) c[i] = 4 * lane + i < 255 ? h2[4 * lane + i] : 0u;
+    unsigned int before;
+    wave_find_bin(c, (unsigned int)k - near, b2, before);
+    __syncthreads();  // every wave's scan of the coarse histogram precedes the candidate stores over it
+  }
+
+  // Fewer than k elements within 135 of the max (or -inf / NaN among the top k): the candidates are the elements
+  // >= the exact k-th largest (all elements when no valid one exists), found by radix select, rather than the
+  // whole row, so the rank placement below still applies.
+  const bool radix = bstar == 255 && b2 < 0;
+  const float kth_sel = radix ? radix_kth<NE>(x, V, k, sm) : 0.f;
+  const bool all = kth_sel != kth_sel;
+  // compaction: one LDS atomic per wave reserves the wave's places (their order does not matter: the candidates
+  // are ranked by key below); lanes take consecutive places by ballot rank
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const unsigned long long below = (1ull << lane) - 1ull;
@@ -123,18 +236,13 @@ __device__ void topk_select(const float (&x)[NE], int V, int k, SM& sm) {
   int total = 0;
 #pragma unroll
   for (int e = 0; e < NE; ++e) {
-    masks[e] = __ballot(tid + ST * e < V && bk[e] <= bstar);
+    const bool near_e = bstar < 255 ? bk[e] <= bstar : (bk[e] < 255 || cb[e] <= b2);
+    masks[e] = __ballot(tid + ST * e < V && (radix ? (all || x[e] >= kth_sel) : near_e));
     total += __popcll(masks[e]);
   }
-  if (lane == 0) sm.wtot[wave] = total;
-  __syncthreads();
-  int base = 0, ncand = 0;
-#pragma unroll
-  for (int w = 0; w < ST / 64; ++w) {
-    const int c = sm.wtot[w];
-    base += w < wave ? c : 0;
-    ncand += c;
-  }
+  int base = 0;
+  if (lane == 0 && total > 0) base = (int)atomicAdd((unsigned int*)&sm.ncand, (unsigned int)total);
+  base = __builtin_amdgcn_readfirstlane(base);
 #pragma unroll
   for (int e = 0; e < NE; ++e) {
     const int i = tid + ST * e;
@@ -144,10 +252,28 @@ __device__ void topk_select(const float (&x)[NE], int V, int k, SM& sm) {
     base += __popcll(masks[e]);
   }
   __syncthreads();
-  const int nc = ncand;
+  const int nc = sm.ncand;
   int P2 = 2;
   while (P2 < nc) P2 <<= 1;
-  if (nc <= ST) {
+  if (nc <= 64) {
+    // The usual case: rank placement with the count split over the waves. Keys are distinct (the index is part
+    // of the key), so candidate l goes to position #{j : key_j > key_l}; wave w counts the keys j in
+    // [16 w, 16 w + 16) (LDS broadcast reads), the four partial counts meet in sm.hist (free by now).
+    const unsigned long long key = lane < nc ? sm.cand[lane] : 0ull;
+    const int j0 = 16 * wave;
+    int part = 0;
+    if (j0 < nc) {
+      unsigned long long c16[16];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) c16[q] = sm.cand[min(j0 + q, nc - 1)];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) part += (j0 + q < nc && c16[q] > key) ? 1 : 0;
+    }
+    sm.hist[tid] = (unsigned int)part;
+    __syncthreads();
+    if (tid < nc) sm.cand[sm.hist[lane] + sm.hist[64 + lane] + sm.hist[128 + lane] + sm.hist[192 + lane]] = key;
+    __syncthreads();
+  } else if (nc <= ST) {
     // The usual case (top-k of a peaked row): rank placement. Keys are distinct (the index is part of the key),
     // so candidate t goes to position #{j : key_j > key_t}; the reads of key_j are LDS broadcasts.
     const unsigned long long key = tid < nc ? sm.cand[tid] : 0ull;

@@ -16,7 +16,9 @@
 // Selection inside one 256-thread workgroup per row: the row max m, a 256-bin histogram of the bucket
 // floor(32*(m - x)) (bin 255 = everything 8 or more below the max, not counted), the first bin b* at which the
 // cumulative count reaches k, then every x with bucket <= b* is a candidate. The bucket is monotone in x, so
-// the candidates contain the top k and all its ties; a bitonic sort of the candidates gives the exact order.
+// the candidates contain the top k and all its ties. When fewer than k elements lie within 8 of the max (a peaked
+// row), a radix select over the ordered keys finds the exact k-th largest instead, and the candidates are the
+// elements >= it. Candidates are ordered by rank placement (at most 256) or a bitonic sort.
 #include "m3x_sample.h"
 
 // ---------------------------------------------------------------------------------------------------------

@@ -426,6 +426,56 @@ def test_topk_sample_bitexact(gpu, dtype, V, k):
     assert np.array_equal(out64.cpu().numpy(), refg)
 
 
+def _peaked_rows(g, B, V, dtype):
+    """Rows with fewer than k elements within 8 of the max (after the 1/0.9 scale), the shape of a confident
+    model's logits: a few leaders far above a wide bulk, exact ties at the k-th place, -0/+0, -inf tails, rows
+    with fewer finite elements than k, a bulk beyond the coarse histogram's reach."""
+    x = torch.randn(B, V, generator=g) * 3 - 20
+    for b in range(B):
+        lead = 1 + b % 12
+        x[b, torch.randperm(V, generator=g)[:lead]] = 10 + torch.randn(lead, generator=g) * (0.5 + b % 3)
+    x[1, 100:200] = -20.0                         # 100 ties in the bulk, at the k-th place for k = 50
+    x[2, :] = float("-inf")
+    x[2, 5:45] = torch.randn(40, generator=g)     # 40 finite elements
+    x[3, 10:20] = 0.0
+    x[3, 20:30] = -0.0
+    x[3, 30:] = -50.0                             # the k-th place among +0 / -0 ties
+    x[4, 300:] = float("-inf")
+    x[5, :3] = 200.0                              # the bulk more than 135 below the max: the radix select
+    x[6, :] = torch.randn(V, generator=g) * 40    # a wide row: the coarse histogram
+    return x.to(dtype)
+
+
+@pytest.mark.parametrize("dtype,V,k", [(torch.bfloat16, 2048, 50), (torch.float16, 2048, 64),
+                                       (torch.bfloat16, 2049, 15), (torch.bfloat16, 2048, 1)])
+def test_topk_sample_peaked_rows(gpu, dtype, V, k):
+    """The coarse-histogram and radix-select paths (fewer than k elements within 8 of the row max) draw the
+    oracle's codes bit for bit, for the depth sampler and the cb0 sampler."""
+    from m3x import ops
+    g = _g(V * 3 + k)
+    B = 96
+    logits = _peaked_rows(g, B, V, dtype)
+    u = torch.rand(B, generator=g)
+    u[0] = 0.0
+    u[1] = 0.999999
+    out = torch.empty(B, dtype=torch.int32, device=gpu)
+    ops.topk_sample(logits.to(gpu), u.to(gpu), 1 / 0.9, k, False, out)
+    ref = C.topk_sample_rows(bf16_bits(logits), 1 / 0.9, k, u.numpy(), is_f16=dtype == torch.float16)
+    assert np.array_equal(out.cpu().numpy(), ref), np.nonzero(out.cpu().numpy() != ref)
+    ops.topk_sample(logits.to(gpu), None, 1 / 0.9, k, True, out)
+    refg = C.topk_sample_rows(bf16_bits(logits), 1 / 0.9, k, None, greedy=True, is_f16=dtype == torch.float16)
+    assert np.array_equal(out.cpu().numpy(), refg)
+    if dtype != torch.bfloat16:
+        return
+    slots = torch.arange(B, dtype=torch.long)
+    cb0 = torch.zeros(B, dtype=torch.long, device=gpu)
+    ops.cb0_sample(logits.to(gpu), -1, slots.to(gpu), u.to(gpu), temp=0.9, top_k=k, cb0_out=cb0)
+    lg = bf16_bits(logits)
+    for b in range(B):
+        r, _ = C.cb0_sample(lg[b], -1, 0.9, k, 0.0, 0.0, None, None, 0, None, None, float(u[b]))
+        assert r == int(cb0[b]), b
+
+
 @pytest.mark.parametrize("dtype,n,kind", [(torch.bfloat16, 1024, 1), (torch.bfloat16, 1024, 0),
                                           (torch.float16, 2048, 0)])
 def test_topk_sample_embed(gpu, dtype, n, kind):
