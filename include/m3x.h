@@ -138,6 +138,19 @@ int m3x_linear_normed(const void* x, long ldx, const void* part, const float* u,
                       int norm_kind, const void* wg_packed, const void* wu_packed, void* y, long ldy, int M, int N,
                       int K, int act, int dtype, void* stream);
 
+/* The q|k|v projection followed by m3x_qk_norm_rope_cache on its bf16 output, head_dim 128: x . W^T with W
+ * [(heads + 2 kv_heads) * 128, K] packed, or, when part is given (K = 1024), m3x_linear_normed's RMSNorm-folded
+ * product of rows whose tile statistics are part (eps_in the input norm's epsilon, W packed from the folded
+ * weight). When the row count's plan gives each workgroup whole heads (the 8-tile one-shot plan: 193..256 rows at
+ * N = 4096) the norm, RoPE and cache writes run in the projection's epilogue and qkv is not written; otherwise the
+ * two launches run in turn through qkv [M, ld_qkv]. The outputs are the same bits either way.
+ * Replaces `F.linear(x, wqkv)` + `_qk_norm_rope_cache` (serve/fast_backbone.py:193-197, 61-92). */
+int m3x_linear_qk_rope(const void* x, long ldx, const void* part, float eps_in, const void* w_packed, void* qkv,
+                       long ld_qkv, void* q_out, long s_qo_b, long s_qo_h, void* k_cache, void* v_cache, long sk_s,
+                       long sk_h, long sk_t, const int64_t* slots, const int32_t* pos, const void* cos, const void* sin,
+                       long s_cos, const void* wq, const void* wk, float eps, int M, int K, int heads, int kv_heads,
+                       int head_dim, int cap, void* stream);
+
 /* out[r, :I] = act(in[r, :]): M3X_ACT_SWIGLU: bf16(silu(g)) * u with in = [g | u] (2*I wide);
  * M3X_ACT_GELU: gelu(in[r, :I]) (erf form), for callers that already hold the projection output.
  * Replaces `F.silu(g_)*u_` (serve/fast_backbone.py:201-202) and `F.gelu` (serve/fast_depth.py:123,186). */

@@ -79,3 +79,57 @@ M3X_API int m3x_linear_normed(const void* x, long ldx, const void* part, const f
   M3X_CHECK_LAUNCH();
   return M3X_OK;
 }
+
+// norm.hip
+M3X_API int m3x_qk_norm_rope_cache(const void* qkv, long s_qkv, void* q_out, long s_qo_b, long s_qo_h, void* k_cache,
+                                   void* v_cache, long sk_s, long sk_h, long sk_t, const int64_t* slots,
+                                   const int32_t* pos, const void* cos, const void* sin, long s_cos, const void* wq,
+                                   const void* wk, float eps, int rows, int heads, int kv_heads, int head_dim,
+                                   int cap, void* stream);
+
+// The q|k|v projection (plain, or with the input norm folded in when part is given: m3x_linear_normed with
+// RMSNorm) followed by m3x_qk_norm_rope_cache on its output, in one launch when the row count's plan holds whole
+// heads per workgroup (the 8-tile one-shot plan, 193..256 rows at N = 4096); otherwise the two launches in turn,
+// through qkv. Same bits either way.
+M3X_API int m3x_linear_qk_rope(const void* x, long ldx, const void* part, float eps_in, const void* w_packed, void* qkv,
+                               long ld_qkv, void* q_out, long s_qo_b, long s_qo_h, void* k_cache, void* v_cache,
+                               long sk_s, long sk_h, long sk_t, const int64_t* slots, const int32_t* pos,
+                               const void* cos, const void* sin, long s_cos, const void* wq, const void* wk, float eps,
+                               int M, int K, int heads, int kv_heads, int head_dim, int cap, void* stream) {
+  if (M < 0 || K <= 0 || heads <= 0 || kv_heads <= 0 || cap <= 0) return M3X_EINVAL;
+  if (M == 0) return M3X_OK;
+  if (!x || !w_packed || !qkv || !q_out || !k_cache || !v_cache || !slots || !pos || !cos || !sin || !wq || !wk)
+    return M3X_ENULL;
+  if (head_dim != 128) return M3X_EUNSUPPORTED;
+  const int N = (heads + 2 * kv_heads) * head_dim;
+  if (K % 32 || (ldx & 7) || ldx < K || ld_qkv < N || (ld_qkv & 7) || (part && K != PRO_K)) return M3X_EINVAL;
+  if ((s_qo_b | s_qo_h | sk_s | sk_h | sk_t | s_cos) & 7) return M3X_EINVAL;
+  if (!aligned(x, 16) || !aligned(w_packed, 16) || !aligned(qkv, 16) || !aligned(q_out, 16) ||
+      !aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(cos, 16) || !aligned(sin, 16) || !aligned(wq, 16) ||
+      !aligned(wk, 16) || (part && !aligned(part, 16)))
+    return M3X_EINVAL;
+  const LinearPlan p = linear_plan(M, N, K, false, ldx);
+  if ((long)m3x_ceil_div(p.nblk, 8) * 8 * p.mblk > 0x7fffffffL) return M3X_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+  const NormIn ni{(const float2*)part, nullptr, nullptr, eps_in, M3X_NORM_RMS};
+  const QkOut qk{(uint16_t*)q_out, s_qo_b, s_qo_h, (uint16_t*)k_cache, (uint16_t*)v_cache, sk_s, sk_h, sk_t, slots, pos,
+                 (const uint16_t*)cos, (const uint16_t*)sin, s_cos, (const uint16_t*)wq, (const uint16_t*)wk, eps,
+                 heads, kv_heads, cap};
+  const uint16_t* X = (const uint16_t*)x;
+  const uint16_t* W = (const uint16_t*)w_packed;
+  uint16_t* Y = (uint16_t*)qkv;
+  const bool fused = part ? launch_linear<M3X_BF16, EPI_QKR, true>(p, st, X, ldx, W, nullptr, Y, ld_qkv, M, N, K, ni,
+                                                                   ResidOut{}, qk)
+                          : launch_linear<M3X_BF16, EPI_QKR, false>(p, st, X, ldx, W, nullptr, Y, ld_qkv, M, N, K,
+                                                                    ni, ResidOut{}, qk);
+  if (fused) {
+    M3X_CHECK_LAUNCH();
+    return M3X_OK;
+  }
+  const bool ok = part ? launch_linear<M3X_BF16, EPI_NONE, true>(p, st, X, ldx, W, nullptr, Y, ld_qkv, M, N, K, ni)
+                       : launch_linear<M3X_BF16, EPI_NONE, false>(p, st, X, ldx, W, nullptr, Y, ld_qkv, M, N, K);
+  if (!ok) return M3X_EUNSUPPORTED;
+  M3X_CHECK_LAUNCH();
+  return m3x_qk_norm_rope_cache(qkv, ld_qkv, q_out, s_qo_b, s_qo_h, k_cache, v_cache, sk_s, sk_h, sk_t, slots, pos, cos,
+                                sin, s_cos, wq, wk, eps, M, heads, kv_heads, head_dim, cap, stream);
+}

@@ -29,6 +29,10 @@
 //               workgroup also writes the statistics of every 16-column tile of the stored row for the norm that
 //               follows (the add of _add_rms / _add_ln, serve/fast_backbone.py:95-104, serve/fast_depth_kernels.py:
 //               14-45; the norm itself is folded into the consumer, below)
+//   EPI_QKR     the q|k|v projection's values (rounded to bf16 as EPI_NONE stores them) go through the per-head
+//               q/k RMSNorm + RoPE and into the caches (m3x_qk_norm_rope_cache's arithmetic, qk_norm_rope8):
+//               query heads to q_out, key and value heads into the static cache at [slot, head, pos]. Needs whole
+//               heads per workgroup: the one-shot plans with NW = 8 and one K slice (128 columns).
 //
 // Folded norm (PRO): the consumer of a residual row multiplies the raw row and applies the norm to the product.
 // A norm's elementwise weight w (and LayerNorm bias b) is folded into the consumer's weight when it is packed:
@@ -46,7 +50,7 @@
 #include "m3x_common.h"
 #include "m3x_norm.h"
 
-enum { EPI_NONE = 0, EPI_SWIGLU = 1, EPI_GELU = 2, EPI_RESID = 3 };
+enum { EPI_NONE = 0, EPI_SWIGLU = 1, EPI_GELU = 2, EPI_RESID = 3, EPI_QKR = 4 };
 enum { M3X_ACT_NONE = -1, M3X_ACT_SWIGLU = 0, M3X_ACT_GELU = 1 };  // the C ABI's gated-activation kinds
 
 // Folded input norm of a PRO projection: the statistics part[m * (K / 16) + j] of row m's 16-column tiles j, and
@@ -70,6 +74,25 @@ struct ResidOut {
   int tc;
   float2* part;
   int kind;
+};
+
+// EPI_QKR's outputs: q_out rows [m * s_qb + head * s_qh], the caches at [slot * sk_s + head * sk_h + pos * sk_t]
+// (slots[m], pos[m] < cap), cos/sin rows of s_cos halfwords, the q/k norm weights wq/wk (D = 128).
+struct QkOut {
+  uint16_t* q;
+  long s_qb, s_qh;
+  uint16_t* kc;
+  uint16_t* vc;
+  long sk_s, sk_h, sk_t;
+  const int64_t* slots;
+  const int32_t* pos;
+  const uint16_t* cosb;
+  const uint16_t* sinb;
+  long s_cos;
+  const uint16_t* wq;
+  const uint16_t* wk;
+  float eps;
+  int H, KV, cap;
 };
 
 // Row scale and shift of a PRO row from its tile statistics: 8 consecutive lanes per row, TPT tiles per lane
@@ -290,6 +313,59 @@ __device__ __forceinline__ void linear_finish(f32x4_t (&acc)[EPI == EPI_SWIGLU ?
   }
 }
 
+// EPI_QKR epilogue of a one-shot workgroup with one K slice and NW = 8 HPW weight tiles (HPW whole heads of 128
+// columns): the wave's tiles, with the folded norm applied, are rounded to bf16 and staged in LDS (`tile`, free
+// when this runs), then each 16-lane DPP row takes one (row, head) item at a time: a query or key head through
+// qk_norm_rope8 into q_out or the key cache, a value head into the value cache as is.
+template <int MT, int NW, int NT, bool PRO>
+__device__ __forceinline__ void qk_finish(f32x4_t (&acc)[1][MT], uint16_t* tile, int wn, int lane, int nb, int m0,
+                                          int M, int N, const float2* pst, const NormIn& ni, const QkOut& qk) {
+  constexpr int HD = 128;
+  constexpr int HPW = NW / 8;
+  constexpr int ROWS = 16 * MT;
+  constexpr int LDT = 16 * NW + 8;  // staged row stride, halfwords
+  static_assert(NW % 8 == 0, "whole heads per workgroup");
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+  const int n = (nb * NW + wn) * 16 + 4 * lg;
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    if constexpr (PRO) norm_apply(acc[0][t], pst, 16 * t + li, ni, n, N, 0);
+    uint2 pk;
+    pk.x = (uint32_t)f2bf(acc[0][t][0]) | ((uint32_t)f2bf(acc[0][t][1]) << 16);
+    pk.y = (uint32_t)f2bf(acc[0][t][2]) | ((uint32_t)f2bf(acc[0][t][3]) << 16);
+    *reinterpret_cast<uint2*>(&tile[(16 * t + li) * LDT + 16 * wn + 4 * lg]) = pk;
+  }
+  __syncthreads();
+  const int tid = threadIdx.x;
+  const int t = tid & 15;
+  for (int it = tid >> 4; it < ROWS * HPW; it += NT / 16) {
+    const int r = it / HPW;
+    const int hh = it - r * HPW;
+    const int j = nb * HPW + hh;  // head of q|k|v (uniform in the DPP row)
+    const int m = min(m0 + r, M - 1);
+    const int ps = min(qk.pos[m], qk.cap - 1);  // the host guarantees pos < cap; the clamp keeps the write in the slot
+    const long slot = qk.slots[m];
+    const u16x8 xv = *reinterpret_cast<const u16x8*>(&tile[r * LDT + HD * hh + 8 * t]);
+    if (j >= qk.H + qk.KV) {
+      if (m0 + r < M) st16(qk.vc + slot * qk.sk_s + (long)(j - qk.H - qk.KV) * qk.sk_h + (long)ps * qk.sk_t + 8 * t, xv);
+      continue;
+    }
+    const u16x8 wv = ld16((j < qk.H ? qk.wq : qk.wk) + 8 * t);
+    const u16x8 cv = ld16(qk.cosb + (long)ps * qk.s_cos + 8 * t);
+    const u16x8 sv = ld16(qk.sinb + (long)ps * qk.s_cos + 8 * t);
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = bf2f(xv.v[e]);
+    const u16x8 ov = qk_norm_rope8<HD>(x, wv, cv, sv, qk.eps, t);
+    if (m0 + r >= M) continue;
+    if (j < qk.H)
+      st16(qk.q + (long)(m0 + r) * qk.s_qb + (long)j * qk.s_qh + 8 * t, ov);
+    else
+      st16(qk.kc + slot * qk.sk_s + (long)(j - qk.H) * qk.sk_h + (long)ps * qk.sk_t + 8 * t, ov);
+  }
+}
+
 // PRO: the input rows' folded norm (NormIn; K == PRO_K): statistics loaded in the prologue, applied in the epilogue.
 constexpr int PRO_K = 1024;
 
@@ -454,7 +530,7 @@ __global__ __launch_bounds__(64 * NWAVES) void linear_oneshot_kernel(const uint1
                                                                      const uint16_t* __restrict__ W2p,
                                                                      uint16_t* __restrict__ Y, long ldy, int M, int N,
                                                                      int K, int mblk, int nblk, NormIn ni,
-                                                                     ResidOut ro) {
+                                                                     ResidOut ro, QkOut qk) {
   constexpr int NT = 64 * NWAVES;
   constexpr int KW = NWAVES / NW;
   constexpr int ROWS = 16 * MT;
@@ -568,8 +644,14 @@ __global__ __launch_bounds__(64 * NWAVES) void linear_oneshot_kernel(const uint1
     }
   }
   __syncthreads();  // every wave is done with the block before it holds the slice partials
-  linear_finish<DT, MT, NW, KW, EPI, PRO>(acc, reinterpret_cast<f32x4_t*>(xs), wn, wk, lane, n0, m0, Y, ldy, M, N, ro,
-                                          pre, pst, ni);
+  if constexpr (EPI == EPI_QKR) {
+    static_assert(KW == 1 && DT == M3X_BF16, "one K slice, bf16");
+    static_assert(ROWS * (16 * NW + 8) <= KW * ROWS * LDR, "the staged tile fits the block");
+    qk_finish<MT, NW, NT, PRO>(acc, xs, wn, lane, nb, m0, M, N, pst, ni, qk);
+  } else {
+    linear_finish<DT, MT, NW, KW, EPI, PRO>(acc, reinterpret_cast<f32x4_t*>(xs), wn, wk, lane, n0, m0, Y, ldy, M, N,
+                                            ro, pre, pst, ni);
+  }
 }
 
 // Large-M projections (M > 512 rows: steps with inline prefills). A workgroup of 8 waves owns a 2-D tile of 128
@@ -886,9 +968,16 @@ static LinearPlan linear_plan(int M, int N, int K, bool dual, long ldx) {
 template <int DT, int EPI, bool PRO = false>
 static bool launch_linear(const LinearPlan& p, hipStream_t st, const uint16_t* X, long ldx, const uint16_t* W,
                           const uint16_t* W2, uint16_t* Y, long ldy, int M, int N, int K, const NormIn& ni = NormIn{},
-                          const ResidOut& ro = ResidOut{}) {
+                          const ResidOut& ro = ResidOut{}, const QkOut& qk = QkOut{}) {
   static_assert(!(PRO && EPI == EPI_RESID), "a residual projection takes its input as is");
   const dim3 grid(m3x_ceil_div(p.nblk, 8) * 8 * p.mblk);
+  if constexpr (EPI == EPI_QKR) {
+    // whole heads per workgroup: only the plan of 8 weight tiles in one K slice
+    if (!p.oneshot || p.tiled || p.mt != 2 || p.nw != 8 || p.nwaves != 8 || p.oneshot != 32) return false;
+    hipLaunchKernelGGL((linear_oneshot_kernel<DT, 2, 8, 8, EPI_QKR, 32, PRO>), grid, dim3(512), 0, st, X, ldx, W, W2,
+                       Y, ldy, M, N, K, p.mblk, p.nblk, ni, ro, qk);
+    return true;
+  } else {
   if (p.tiled) {
     hipLaunchKernelGGL((linear_tiled_kernel<DT, EPI, PRO>), grid, dim3(512), 0, st, X, ldx, W, W2, Y, ldy, M, N, K,
                        p.mblk, p.nblk, ni, ro);
@@ -897,7 +986,7 @@ static bool launch_linear(const LinearPlan& p, hipStream_t st, const uint16_t* X
 #define M3X_ONE(MTT, NWW, NWV, SS)                                                                              \
   if constexpr (!PRO || (NWV / NWW) * SS * 32 == PRO_K) {                                                     \
     hipLaunchKernelGGL((linear_oneshot_kernel<DT, MTT, NWW, NWV, EPI, SS, PRO>), grid, dim3(64 * NWV), 0, st, X, \
-                       ldx, W, W2, Y, ldy, M, N, K, p.mblk, p.nblk, ni, ro);                                  \
+                       ldx, W, W2, Y, ldy, M, N, K, p.mblk, p.nblk, ni, ro, qk);                              \
     return true;                                                                                              \
   }                                                                                                           \
   return false
@@ -950,4 +1039,5 @@ static bool launch_linear(const LinearPlan& p, hipStream_t st, const uint16_t* X
     default: return false;
   }
 #undef M3X_LIN
+  }
 }

@@ -72,3 +72,39 @@ __device__ __forceinline__ V8<DT> norm_vec(const float (&v)[8], const V8<DT>& wv
   }
   return yv;
 }
+
+// Per-head q/k RMSNorm + RoPE of one head row (serve/fast_backbone.py:61-92, rounding points :77-81), for the D/8
+// threads that hold it, thread t holding elements 8t .. 8t+7 (x: the bf16 values of the projection, as floats):
+//   y = bf16(bf16(x * inv) * w);  first half: o = y*c - y'*s;  second half: o = y*c + y'*s  (y' = rotate partner)
+// For D = 128 the 16 threads must be one DPP row (lanes 16k .. 16k+15); for D = 64, 8 adjacent lanes. Every
+// thread of those lanes calls it (the reductions are lane exchanges).
+template <int D>
+__device__ __forceinline__ u16x8 qk_norm_rope8(const float (&x)[8], const u16x8& wv, const u16x8& cv, const u16x8& sv,
+                                               float eps, int t) {
+  constexpr int TPI = D / 8;
+  float p = x[0] * x[0];
+#pragma unroll
+  for (int e = 1; e < 8; ++e) p = p + x[e] * x[e];
+  if constexpr (TPI == 16) {
+    p = dppf<DPP_ROW_NEWBCAST(0)>(fold_half_sum<16>(p));  // one DPP row per head: its total, from its first lane
+  } else {
+#pragma unroll
+    for (int s = TPI / 2; s > 0; s >>= 1) p = p + __shfl_xor(p, s, 64);
+  }
+  const float inv = 1.0f / sqrtf(p / (float)D + eps);
+  float yv[8], yp[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) yv[e] = bf2f(f2bf(bf2f(f2bf(x[e] * inv)) * bf2f(wv.v[e])));
+#pragma unroll
+  for (int e = 0; e < 8; ++e)  // the rotate partner, lane t ^ TPI/2
+    yp[e] = TPI == 16 ? dppf<DPP_ROW_ROR(8)>(yv[e]) : __shfl_xor(yv[e], TPI / 2, 64);
+  const bool first = t < TPI / 2;
+  u16x8 ov;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float a1 = yv[e] * bf2f(cv.v[e]);
+    float a2 = yp[e] * bf2f(sv.v[e]);
+    ov.v[e] = f2bf(first ? a1 - a2 : a1 + a2);
+  }
+  return ov;
+}

@@ -164,8 +164,7 @@ M3X_API int m3x_add_rms(const void* h, long s_h, const void* a, long s_a, void* 
 // ---------------------------------------------------------------------------------------------------------
 // K2: per-head q/k RMSNorm + RoPE, query heads to q_out, key heads into the static cache at [slot, kh, pos],
 // value heads copied verbatim. serve/fast_backbone.py:61-92 (_qk_norm_rope_cache), rounding points :77-81.
-// One item = (row, j) with j < H a query head and H <= j < H+KV a key head; D/8 threads per item.
-//   y = bf16(bf16(x*inv) * w);  first half:  o = y*c - y'*s;  second half: o = y*c + y'*s  (y' = rotate partner)
+// One item = (row, j) with j < H a query head and H <= j < H+KV a key head; D/8 threads per item (qk_norm_rope8).
 template <int D>
 __global__ __launch_bounds__(256) void qk_norm_rope_cache_kernel(
     const uint16_t* __restrict__ qkv, long s_qkv, uint16_t* __restrict__ qo, long s_qo_b, long s_qo_h,
@@ -192,34 +191,11 @@ __global__ __launch_bounds__(256) void qk_norm_rope_cache_kernel(
   const u16x8 vv = ld16(qkv + (long)r * s_qkv + (long)(H + KV + kh) * D + 8 * t);
   const u16x8 cv = ld16(cosb + (long)ps * s_cos + 8 * t);
   const u16x8 sv = ld16(sinb + (long)ps * s_cos + 8 * t);
-  float x[8], yv[8];
+  float x[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) x[e] = bf2f(xv.v[e]);
-  float p = x[0] * x[0];
-#pragma unroll
-  for (int e = 1; e < 8; ++e) p = p + x[e] * x[e];
-  if constexpr (TPI == 16) {
-    p = dppf<DPP_ROW_NEWBCAST(0)>(fold_half_sum<16>(p));  // one DPP row per head: its total, from its first lane
-  } else {
-#pragma unroll
-    for (int s = TPI / 2; s > 0; s >>= 1) p = p + __shfl_xor(p, s, 64);
-  }
-  const float inv = 1.0f / sqrtf(p / (float)D + eps);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) yv[e] = bf2f(f2bf(bf2f(f2bf(x[e] * inv)) * bf2f(wv.v[e])));
-  float yp[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e)  // the rotate partner, lane t ^ TPI/2
-    yp[e] = TPI == 16 ? dppf<DPP_ROW_ROR(8)>(yv[e]) : __shfl_xor(yv[e], TPI / 2, 64);
+  const u16x8 ov = qk_norm_rope8<D>(x, wv, cv, sv, eps, t);
   if (!active) return;
-  const bool first = t < TPI / 2;
-  u16x8 ov;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    float a1 = yv[e] * bf2f(cv.v[e]);
-    float a2 = yp[e] * bf2f(sv.v[e]);
-    ov.v[e] = f2bf(first ? a1 - a2 : a1 + a2);
-  }
   if (j < H) {
     st16(qo + (long)row * s_qo_b + (long)j * s_qo_h + 8 * t, ov);
   } else {

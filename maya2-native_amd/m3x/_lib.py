@@ -12,7 +12,7 @@ import os
 import torch  # noqa: F401  (must precede the CDLL load, see above)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libm3x.so")
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -26,6 +26,8 @@ SIGNATURES = {
     "m3x_positions": (_I, [_P, _P, _P, _P, _I, _P]),
     "m3x_lengths_add": (_I, [_P, _P, _P, _I, _P]),
     "m3x_add_rms": (_I, [_P, _L, _P, _L, _P, _L, _P, _L, _P, _F, _I, _I, _P]),
+    "m3x_linear_qk_rope": (_I, [_P, _L, _P, _F, _P, _P, _L, _P, _L, _L, _P, _P, _L, _L, _L, _P, _P, _P, _P, _L, _P, _P,
+                                _F, _I, _I, _I, _I, _I, _I, _P]),
     "m3x_qk_norm_rope_cache": (_I, [_P, _L, _P, _L, _L, _P, _P, _L, _L, _L, _P, _P, _P, _P, _L, _P, _P, _F, _I, _I,
                                     _I, _I, _I, _P]),
     "m3x_decode_attn_workspace": (_Z, [_I, _I, _I, _I]),

@@ -110,6 +110,29 @@ def qk_norm_rope_cache(qkv, q_out, k_cache, v_cache, slots, pos, cos, sin, wq, w
         _p(wq), _p(wk), float(eps), rows, heads, kv_heads, D, k_cache.shape[2], _stream()), "qk_norm_rope_cache")
 
 
+def linear_qk_rope(x, w, qkv, q_out, k_cache, v_cache, slots, pos, cos, sin, wq, wk, eps, heads, kv_heads,
+                   part=None, eps_in=0.0):
+    """The q|k|v projection (x @ W.T, or with part given linear_normed's RMSNorm-folded product, W from fold_norm)
+    followed by qk_norm_rope_cache on its output, in one launch when the row count's plan holds whole heads per
+    workgroup (then qkv is not written), else two through qkv. Same bits as linear / linear_normed +
+    qk_norm_rope_cache."""
+    M, K, qkv = _lin_args(x, w, qkv, w.N)
+    _dev(q_out, k_cache, v_cache, slots, pos, cos, sin, wq, wk, part)
+    D = k_cache.shape[-1]
+    if w.N != (heads + 2 * kv_heads) * D:
+        raise ValueError(f"linear_qk_rope: weight rows {w.N} != (heads + 2*kv_heads)*head_dim")
+    if x.dtype != torch.bfloat16:
+        raise ValueError("linear_qk_rope: bf16 only")
+    if part is not None and (part.dtype != torch.float32 or not part.is_contiguous()
+                             or part.numel() < tile_stats_elems(M, K)):
+        raise ValueError("linear_qk_rope: part must hold the tile statistics of x")
+    check(lib().m3x_linear_qk_rope(
+        _p(x), x.stride(0), _p(part), float(eps_in), _p(w.data), _p(qkv), qkv.stride(0), _p(q_out), q_out.stride(0),
+        q_out.stride(1), _p(k_cache), _p(v_cache), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), _p(slots),
+        _p(pos), _p(cos), _p(sin), cos.stride(0), _p(wq), _p(wk), float(eps), M, K, heads, kv_heads, D,
+        k_cache.shape[2], _stream()), "linear_qk_rope")
+
+
 def decode_attn_workspace(rows, kv_heads, max_ctx, chunk) -> int:
     return int(lib().m3x_decode_attn_workspace(rows, kv_heads, max_ctx, chunk))
 

@@ -273,16 +273,17 @@ class StaticBackbone:
         for i, layer in enumerate(self.layers):
             attn, kc, vc = layer.self_attn, self._kfull[i], self._vfull[i]
             w_in, w_post = layer.input_layernorm.weight, layer.post_attention_layernorm.weight
+            qk = (b.qkv, b.q, kc, vc, b.slots, b.pos, self.cos, self.sin, attn.q_norm.weight, attn.k_norm.weight,
+                  eps, H, KV)
             if i == 0:
                 ops.add_rms(b.x, None, w_in, eps, y=b.y)
-                ops.linear(b.y, self.pqkv[i], b.qkv)
+                ops.linear_qk_rope(b.y, self.pqkv[i], *qk)
             elif fused:  # the norm of the residual the previous down projection left, folded into the projection
-                ops.linear_normed(b.h, b.part, eps, rms, self.pqkv[i], y=b.qkv)
+                ops.linear_qk_rope(b.h, self.pqkv[i], *qk, part=b.part, eps_in=eps)
             else:
                 ops.add_rms(b.h, b.pend, w_in, eps, h_out=b.h, y=b.y)
                 ops.linear(b.y, self.pqkv[i], b.qkv)
-            ops.qk_norm_rope_cache(b.qkv, b.q, kc, vc, b.slots, b.pos, self.cos, self.sin, attn.q_norm.weight,
-                                   attn.k_norm.weight, eps, H, KV)
+                ops.qk_norm_rope_cache(*qk)
             ops.decode_attn(b.q, kc, vc, o3, b.slots, b.pos, self.scaling, b.ctx, b.chunk, b.attn_ws, H, KV,
                             items=b.items)
             if fused:

@@ -147,3 +147,57 @@ def test_linear_normed_rejects_bad_args(gpu):
     x2 = torch.zeros(4, 2048, dtype=torch.bfloat16, device=gpu)
     with pytest.raises(RuntimeError):  # the norm prologue covers rows of width 1024 only
         ops.linear_normed(x2, torch.zeros(ops.tile_stats_elems(4, 2048), device=gpu), 1e-6, 1, w2)
+
+
+@pytest.mark.parametrize("M", [3, 100, 200, 224, 256, 300])
+@pytest.mark.parametrize("normed", [False, True])
+def test_linear_qk_rope(gpu, M, normed):
+    """The q|k|v projection with the q/k norm, RoPE and cache writes: the same bits as the projection
+    (linear / linear_normed) followed by qk_norm_rope_cache, in one launch where the plan holds whole heads
+    (193..256 rows: qkv left untouched) and through qkv elsewhere; cache entries other than the rows' own
+    (slot, pos) unchanged."""
+    from m3x import ops
+    g = _g(M * 3 + normed)
+    H, KV, D, K, eps = 16, 8, 128, 1024, 1e-6
+    N = (H + 2 * KV) * D
+    S, cap = 40, 64
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(gpu)
+    W = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).to(gpu)
+    part = None
+    if normed:
+        # rows with tile statistics, as the previous layer's down projection leaves them
+        wd = ops.pack_weight((torch.randn(K, 2816, generator=g) * 0.02).to(torch.bfloat16).to(gpu))
+        a = torch.randn(M, 2816, generator=g).to(torch.bfloat16).to(gpu)
+        part = torch.empty(ops.tile_stats_elems(M, K), device=gpu)
+        x = ops.linear_resid(a, wd, x, torch.empty_like(x), part, ops.NORM_RMS)
+        nw = (1 + 0.1 * torch.randn(K, generator=g)).to(torch.bfloat16).to(gpu)
+        w, u, v = ops.fold_norm(W, nw)
+    else:
+        w = ops.pack_weight(W)
+    rows = torch.arange(M)
+    slots = (rows % S).to(gpu)                          # distinct (slot, pos) per row
+    pos = ((rows // S) * 3 + rows % 5).int().to(gpu)
+    cosb = torch.randn(cap, D, generator=g).to(torch.bfloat16).to(gpu)
+    sinb = torch.randn(cap, D, generator=g).to(torch.bfloat16).to(gpu)
+    wq = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).to(gpu)
+    wk = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).to(gpu)
+    kc0 = torch.randn(S + 1, KV, cap, D, generator=g).to(torch.bfloat16).to(gpu)
+    vc0 = torch.randn(S + 1, KV, cap, D, generator=g).to(torch.bfloat16).to(gpu)
+    # the two-launch chain
+    qkv_ref = ops.linear_normed(x, part, eps, ops.NORM_RMS, w, u=u, v=v) if normed else ops.linear(x, w)
+    q_ref = torch.empty(M, H, D, dtype=torch.bfloat16, device=gpu)
+    kc_ref, vc_ref = kc0.clone(), vc0.clone()
+    ops.qk_norm_rope_cache(qkv_ref, q_ref, kc_ref, vc_ref, slots, pos, cosb, sinb, wq, wk, eps, H, KV)
+    # fused
+    qkv = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu)
+    q = torch.full((M, H, D), float("nan"), dtype=torch.bfloat16, device=gpu)
+    kc, vc = kc0.clone(), vc0.clone()
+    ops.linear_qk_rope(x, w, qkv, q, kc, vc, slots, pos, cosb, sinb, wq, wk, eps, H, KV, part=part, eps_in=eps)
+    torch.cuda.synchronize()
+    assert torch.equal(q.cpu(), q_ref.cpu())
+    assert torch.equal(kc.cpu(), kc_ref.cpu()) and torch.equal(vc.cpu(), vc_ref.cpu())
+    fused = 192 < M <= 256
+    if fused:
+        assert bool(torch.isnan(qkv.float()).all()), "the fused plan leaves qkv untouched"
+    else:
+        assert torch.equal(qkv.cpu(), qkv_ref.cpu())
