@@ -32,7 +32,8 @@
 //   EPI_QKR     the q|k|v projection's values (rounded to bf16 as EPI_NONE stores them) go through the per-head
 //               q/k RMSNorm + RoPE and into the caches (m3x_qk_norm_rope_cache's arithmetic, qk_norm_rope8):
 //               query heads to q_out, key and value heads into the static cache at [slot, head, pos]. Needs whole
-//               heads per workgroup: the one-shot plans with NW = 8 and one K slice (128 columns).
+//               heads per workgroup: the large-M tiled plan (128 x 128 tiles) and the one-shot plan with NW = 8 and
+//               one K slice (128 columns).
 //
 // Folded norm (PRO): the consumer of a residual row multiplies the raw row and applies the norm to the product.
 // A norm's elementwise weight w (and LayerNorm bias b) is folded into the consumer's weight when it is packed:
@@ -313,30 +314,13 @@ __device__ __forceinline__ void linear_finish(f32x4_t (&acc)[EPI == EPI_SWIGLU ?
   }
 }
 
-// EPI_QKR epilogue of a one-shot workgroup with one K slice and NW = 8 HPW weight tiles (HPW whole heads of 128
-// columns): the wave's tiles, with the folded norm applied, are rounded to bf16 and staged in LDS (`tile`, free
-// when this runs), then each 16-lane DPP row takes one (row, head) item at a time: a query or key head through
+// EPI_QKR's second half: the workgroup's ROWS rows x HPW whole heads of the projection, rounded to bf16, sit in LDS
+// (`tile`, row stride LDT halfwords, head hh of the workgroup at column 128 hh; workgroup nb holds heads
+// nb * HPW ..). Each 16-lane DPP row takes one (row, head) item at a time: a query or key head through
 // qk_norm_rope8 into q_out or the key cache, a value head into the value cache as is.
-template <int MT, int NW, int NT, bool PRO>
-__device__ __forceinline__ void qk_finish(f32x4_t (&acc)[1][MT], uint16_t* tile, int wn, int lane, int nb, int m0,
-                                          int M, int N, const float2* pst, const NormIn& ni, const QkOut& qk) {
+template <int ROWS, int HPW, int NT>
+__device__ __forceinline__ void qk_items(const uint16_t* tile, int LDT, int nb, int m0, int M, const QkOut& qk) {
   constexpr int HD = 128;
-  constexpr int HPW = NW / 8;
-  constexpr int ROWS = 16 * MT;
-  constexpr int LDT = 16 * NW + 8;  // staged row stride, halfwords
-  static_assert(NW % 8 == 0, "whole heads per workgroup");
-  const int li = lane & 15;
-  const int lg = lane >> 4;
-  const int n = (nb * NW + wn) * 16 + 4 * lg;
-#pragma unroll
-  for (int t = 0; t < MT; ++t) {
-    if constexpr (PRO) norm_apply(acc[0][t], pst, 16 * t + li, ni, n, N, 0);
-    uint2 pk;
-    pk.x = (uint32_t)f2bf(acc[0][t][0]) | ((uint32_t)f2bf(acc[0][t][1]) << 16);
-    pk.y = (uint32_t)f2bf(acc[0][t][2]) | ((uint32_t)f2bf(acc[0][t][3]) << 16);
-    *reinterpret_cast<uint2*>(&tile[(16 * t + li) * LDT + 16 * wn + 4 * lg]) = pk;
-  }
-  __syncthreads();
   const int tid = threadIdx.x;
   const int t = tid & 15;
   for (int it = tid >> 4; it < ROWS * HPW; it += NT / 16) {
@@ -364,6 +348,34 @@ __device__ __forceinline__ void qk_finish(f32x4_t (&acc)[1][MT], uint16_t* tile,
     else
       st16(qk.kc + slot * qk.sk_s + (long)(j - qk.H) * qk.sk_h + (long)ps * qk.sk_t + 8 * t, ov);
   }
+}
+
+// One lane's 4 outputs (columns c .. c + 3 of the workgroup, row r) rounded to bf16 into the staged tile.
+__device__ __forceinline__ void qk_stage(uint16_t* tile, int LDT, int r, int c, const f32x4_t& acc) {
+  uint2 pk;
+  pk.x = (uint32_t)f2bf(acc[0]) | ((uint32_t)f2bf(acc[1]) << 16);
+  pk.y = (uint32_t)f2bf(acc[2]) | ((uint32_t)f2bf(acc[3]) << 16);
+  *reinterpret_cast<uint2*>(&tile[r * LDT + c]) = pk;
+}
+
+// EPI_QKR epilogue of a one-shot workgroup with one K slice and NW = 8 HPW weight tiles (HPW whole heads of 128
+// columns): the wave's tiles, with the folded norm applied, are staged in LDS (`tile`, free when this runs), then
+// qk_items.
+template <int MT, int NW, int NT, bool PRO>
+__device__ __forceinline__ void qk_finish(f32x4_t (&acc)[1][MT], uint16_t* tile, int wn, int lane, int nb, int m0,
+                                          int M, int N, const float2* pst, const NormIn& ni, const QkOut& qk) {
+  static_assert(NW % 8 == 0, "whole heads per workgroup");
+  constexpr int LDT = 16 * NW + 8;  // staged row stride, halfwords
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+  const int n = (nb * NW + wn) * 16 + 4 * lg;
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    if constexpr (PRO) norm_apply(acc[0][t], pst, 16 * t + li, ni, n, N, 0);
+    qk_stage(tile, LDT, 16 * t + li, 16 * wn + 4 * lg, acc[0][t]);
+  }
+  __syncthreads();
+  qk_items<16 * MT, NW / 8, NT>(tile, LDT, nb, m0, M, qk);
 }
 
 // PRO: the input rows' folded norm (NormIn; K == PRO_K): statistics loaded in the prologue, applied in the epilogue.
@@ -668,11 +680,11 @@ __global__ __launch_bounds__(64 * NWAVES) void linear_oneshot_kernel(const uint1
 // PRO (K == PRO_K): the rows' folded norm, applied in the epilogue; its statistics (and EPI_RESID's operands) load
 // after the products.
 template <int DT, int EPI, bool PRO>
-__global__ __launch_bounds__(512, 2) void linear_tiled_kernel(const uint16_t* __restrict__ X, long ldx,
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void linear_tiled_kernel(const uint16_t* __restrict__ X, long ldx,
                                                               const uint16_t* __restrict__ Wp,
                                                               const uint16_t* __restrict__ W2p,
                                                               uint16_t* __restrict__ Y, long ldy, int M, int N, int K,
-                                                              int mblk, int nblk, NormIn ni, ResidOut ro) {
+                                                              int mblk, int nblk, NormIn ni, ResidOut ro, QkOut qk) {
   constexpr bool DUAL = EPI == EPI_SWIGLU;
   constexpr int BM = 128;
   constexpr int LDA = 72;  // activation row stride in LDS, halfwords
@@ -811,6 +823,20 @@ __global__ __launch_bounds__(512, 2) void linear_tiled_kernel(const uint16_t* __
         resid_quad<DT>(acc[i][j], pre[i][j], m0 + 16 * (4 * wm + j) + li, tile * 16 + 4 * lg, tile, M, N, lg, ro, Y,
                        ldy);
     }
+    return;
+  }
+  if constexpr (EPI == EPI_QKR) {
+    // the workgroup's 128 columns are one head: stage the 128 x 128 tile in the activation buffers (free after the
+    // loop's last barrier), then the per-head norm, RoPE and cache writes
+    static_assert(DT == M3X_BF16 && BM * (128 + 8) <= 2 * BM * LDA, "the staged tile fits the activation buffers");
+    constexpr int LDT = 128 + 8;
+    uint16_t* tile = &la[0][0];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) qk_stage(tile, LDT, 16 * (4 * wm + j) + li, 16 * wt[i] + 4 * lg, acc[i][j]);
+    __syncthreads();
+    qk_items<BM, 1, 512>(tile, LDT, nb, m0, M, qk);
     return;
   }
 
@@ -972,15 +998,20 @@ static bool launch_linear(const LinearPlan& p, hipStream_t st, const uint16_t* X
   static_assert(!(PRO && EPI == EPI_RESID), "a residual projection takes its input as is");
   const dim3 grid(m3x_ceil_div(p.nblk, 8) * 8 * p.mblk);
   if constexpr (EPI == EPI_QKR) {
-    // whole heads per workgroup: only the plan of 8 weight tiles in one K slice
-    if (!p.oneshot || p.tiled || p.mt != 2 || p.nw != 8 || p.nwaves != 8 || p.oneshot != 32) return false;
+    // whole heads per workgroup: the tiled plan (128 columns) or the one-shot plan of 8 weight tiles in one K slice
+    if (p.tiled) {
+      hipLaunchKernelGGL((linear_tiled_kernel<DT, EPI_QKR, PRO>), grid, dim3(512), 0, st, X, ldx, W, W2, Y, ldy, M, N,
+                         K, p.mblk, p.nblk, ni, ro, qk);
+      return true;
+    }
+    if (!p.oneshot || p.mt != 2 || p.nw != 8 || p.nwaves != 8 || p.oneshot != 32) return false;
     hipLaunchKernelGGL((linear_oneshot_kernel<DT, 2, 8, 8, EPI_QKR, 32, PRO>), grid, dim3(512), 0, st, X, ldx, W, W2,
                        Y, ldy, M, N, K, p.mblk, p.nblk, ni, ro, qk);
     return true;
   } else {
   if (p.tiled) {
     hipLaunchKernelGGL((linear_tiled_kernel<DT, EPI, PRO>), grid, dim3(512), 0, st, X, ldx, W, W2, Y, ldy, M, N, K,
-                       p.mblk, p.nblk, ni, ro);
+                       p.mblk, p.nblk, ni, ro, qk);
     return true;
   }
 #define M3X_ONE(MTT, NWW, NWV, SS)                                                                              \

@@ -149,18 +149,18 @@ def test_linear_normed_rejects_bad_args(gpu):
         ops.linear_normed(x2, torch.zeros(ops.tile_stats_elems(4, 2048), device=gpu), 1e-6, 1, w2)
 
 
-@pytest.mark.parametrize("M", [3, 100, 200, 224, 256, 300])
+@pytest.mark.parametrize("M", [3, 100, 200, 224, 256, 300, 513, 700, 2264])
 @pytest.mark.parametrize("normed", [False, True])
 def test_linear_qk_rope(gpu, M, normed):
     """The q|k|v projection with the q/k norm, RoPE and cache writes: the same bits as the projection
     (linear / linear_normed) followed by qk_norm_rope_cache, in one launch where the plan holds whole heads
-    (193..256 rows: qkv left untouched) and through qkv elsewhere; cache entries other than the rows' own
-    (slot, pos) unchanged."""
+    (193..256 rows and above 512: qkv left untouched) and through qkv elsewhere; cache entries other than the
+    rows' own (slot, pos) unchanged."""
     from m3x import ops
     g = _g(M * 3 + normed)
     H, KV, D, K, eps = 16, 8, 128, 1024, 1e-6
     N = (H + 2 * KV) * D
-    S, cap = 40, 64
+    S, cap = 40, 192
     x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(gpu)
     W = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).to(gpu)
     part = None
@@ -196,7 +196,7 @@ def test_linear_qk_rope(gpu, M, normed):
     torch.cuda.synchronize()
     assert torch.equal(q.cpu(), q_ref.cpu())
     assert torch.equal(kc.cpu(), kc_ref.cpu()) and torch.equal(vc.cpu(), vc_ref.cpu())
-    fused = 192 < M <= 256
+    fused = 192 < M <= 256 or M > 512
     if fused:
         assert bool(torch.isnan(qkv.float()).all()), "the fused plan leaves qkv untouched"
     else:
