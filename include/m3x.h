@@ -141,8 +141,8 @@ int m3x_linear_normed(const void* x, long ldx, const void* part, const float* u,
 /* The q|k|v projection followed by m3x_qk_norm_rope_cache on its bf16 output, head_dim 128: x . W^T with W
  * [(heads + 2 kv_heads) * 128, K] packed, or, when part is given (K = 1024), m3x_linear_normed's RMSNorm-folded
  * product of rows whose tile statistics are part (eps_in the input norm's epsilon, W packed from the folded
- * weight). When the row count's plan gives each workgroup whole heads (the 8-tile one-shot plan: 193..256 rows at
- * N = 4096) the norm, RoPE and cache writes run in the projection's epilogue and qkv is not written; otherwise the
+ * weight). When the row count's plan gives each workgroup whole heads (193..256 rows and above 512 at N = 4096,
+ * K = 1024) the norm, RoPE and cache writes run in the projection's epilogue and qkv is not written; otherwise the
  * two launches run in turn through qkv [M, ld_qkv]. The outputs are the same bits either way.
  * Replaces `F.linear(x, wqkv)` + `_qk_norm_rope_cache` (serve/fast_backbone.py:193-197, 61-92). */
 int m3x_linear_qk_rope(const void* x, long ldx, const void* part, float eps_in, const void* w_packed, void* qkv,

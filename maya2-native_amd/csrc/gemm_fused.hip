@@ -89,8 +89,8 @@ M3X_API int m3x_qk_norm_rope_cache(const void* qkv, long s_qkv, void* q_out, lon
 
 // The q|k|v projection (plain, or with the input norm folded in when part is given: m3x_linear_normed with
 // RMSNorm) followed by m3x_qk_norm_rope_cache on its output, in one launch when the row count's plan holds whole
-// heads per workgroup (the 8-tile one-shot plan, 193..256 rows at N = 4096); otherwise the two launches in turn,
-// through qkv. Same bits either way.
+// heads per workgroup (193..256 rows and above 512 at N = 4096); otherwise the two launches in turn, through qkv.
+// Same bits either way.
 M3X_API int m3x_linear_qk_rope(const void* x, long ldx, const void* part, float eps_in, const void* w_packed, void* qkv,
                                long ld_qkv, void* q_out, long s_qo_b, long s_qo_h, void* k_cache, void* v_cache,
                                long sk_s, long sk_h, long sk_t, const int64_t* slots, const int32_t* pos,

@@ -149,7 +149,7 @@ def test_linear_normed_rejects_bad_args(gpu):
         ops.linear_normed(x2, torch.zeros(ops.tile_stats_elems(4, 2048), device=gpu), 1e-6, 1, w2)
 
 
-@pytest.mark.parametrize("M", [3, 100, 200, 224, 256, 300, 513, 700, 2264])
+@pytest.mark.parametrize("M", [1, 3, 16, 17, 100, 200, 224, 256, 300, 513, 700, 2264])
 @pytest.mark.parametrize("normed", [False, True])
 def test_linear_qk_rope(gpu, M, normed):
     """The q|k|v projection with the q/k norm, RoPE and cache writes: the same bits as the projection
