@@ -517,7 +517,7 @@ __device__ __forceinline__ void finish_tile(Smem& sm, f32x4_t acc, f32x4_t acc2,
         const float g = v;
         const float uu =
             rnd<DT>(((sm.part[1][0][idx] + sm.part[1][1][idx]) + sm.part[1][2][idx]) + sm.part[1][3][idx]);
-        v = rnd<DT>(g / (1.0f + expf(-g))) * uu;
+        v = rnd<DT>(silu16(g)) * uu;
       } else if constexpr (EPI == 2) {
         v = 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
       }

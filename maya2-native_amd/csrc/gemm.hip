@@ -327,7 +327,7 @@ __global__ __launch_bounds__(256) void act_kernel(const uint16_t* __restrict__ i
   float y;
   if (kind == M3X_ACT_SWIGLU) {
     const float u = E<DT>::to_f(in[(long)r * ld_in + I + c]);
-    const float sg = rnd<DT>(g / (1.0f + expf(-g)));
+    const float sg = rnd<DT>(silu16(g));
     y = sg * u;
   } else {
     y = 0.5f * g * (1.0f + erff(g * 0.70710678118654752f));

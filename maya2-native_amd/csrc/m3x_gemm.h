@@ -294,7 +294,7 @@ __device__ __forceinline__ void linear_finish(f32x4_t (&acc)[EPI == EPI_SWIGLU ?
       if constexpr (EPI == EPI_SWIGLU) {
         const float g = v;
         const float u = rnd<DT>(acc[NA - 1][t][r]);
-        v = rnd<DT>(g / (1.0f + expf(-g))) * u;
+        v = rnd<DT>(silu16(g)) * u;
       } else if constexpr (EPI == EPI_GELU) {
         v = 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
       }
@@ -858,7 +858,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
         if constexpr (DUAL) {
           const float g = v;
           const float u = rnd<DT>(acc[1][j][r]);
-          v = rnd<DT>(g / (1.0f + expf(-g))) * u;
+          v = rnd<DT>(silu16(g)) * u;
         } else if constexpr (EPI == EPI_GELU) {
           v = 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
         }
