@@ -314,6 +314,134 @@ __device__ __forceinline__ void linear_finish(f32x4_t (&acc)[EPI == EPI_SWIGLU ?
   }
 }
 
+// linear_finish for the one-shot plans with several K slices and a plain, gated or GELU epilogue, with the work
+// spread over every wave of the weight tile: each of the KW waves stores its partial tiles to LDS (`red`, free when
+// this runs), then lane T = 64 wk + lane of the tile's waves takes elements e = T + 64 KW j of the MT x 16 x 16
+// block (row-major, so a row's 16 columns sit in 16 adjacent lanes), adds their KW partials in slice order (the sum
+// linear_finish forms), and applies the epilogue and a 2-byte store. Instead of one wave per tile doing all 4 MT
+// elements per lane while the others wait, every wave does 4 MT / KW (rounded up; past the block, whole waves
+// skip).
+template <int DT, int MT, int NW, int KW, int EPI, bool PRO>
+__device__ __forceinline__ void linear_finish_spread(f32x4_t (&acc)[EPI == EPI_SWIGLU ? 2 : 1][MT], float* red,
+                                                     int wn, int wk, int lane, int n0, int m0,
+                                                     uint16_t* __restrict__ Y, long ldy, int M, int N,
+                                                     const float2* pst, const NormIn& ni) {
+  constexpr int NA = EPI == EPI_SWIGLU ? 2 : 1;
+  constexpr int EPL = (4 * MT + KW - 1) / KW;  // elements per lane (with KW > 4 MT, waves 4 MT.. have none)
+  static_assert(KW > 1, "several K slices");
+  static_assert(EPI == EPI_NONE || EPI == EPI_SWIGLU || EPI == EPI_GELU, "plain, gated or GELU epilogue");
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+  // partial (slice q, weight a, row tile t) of tile wn: element (row, col) at red[base(q, a, t) + 16 row + col]
+  auto base = [&](int q, int a, int t) { return (((wn * KW + q) * NA + a) * MT + t) * 256; };
+#pragma unroll
+  for (int a = 0; a < NA; ++a)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) *reinterpret_cast<f32x4_t*>(&red[base(wk, a, t) + 16 * li + 4 * lg]) = acc[a][t];
+  __syncthreads();
+  const int T = 64 * wk + lane;
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int e = T + 64 * KW * j;
+    if (e >= 256 * MT) break;  // wave-uniform: 256 MT is a multiple of 64
+    const int t = e >> 8;
+    const int row = (e >> 4) & 15;
+    const int n = n0 + (e & 15);
+    const int m = m0 + 16 * t + row;
+    float v[NA];
+#pragma unroll
+    for (int a = 0; a < NA; ++a) {
+      float x = red[base(0, a, t) + (e & 255)];
+#pragma unroll
+      for (int q = 1; q < KW; ++q) x = x + red[base(q, a, t) + (e & 255)];
+      if constexpr (PRO) {
+        const float2 st = pst[16 * t + row];
+        if (ni.kind == M3X_NORM_LAYER) {
+          const int c = min(n, N - 1);  // columns past N: any finite value, never stored
+          x = st.x * x + (st.y * ni.u[a * N + c] + ni.v[a * N + c]);
+        } else {
+          x = st.x * x;
+        }
+      }
+      v[a] = x;
+    }
+    float o = rnd<DT>(v[0]);
+    if constexpr (EPI == EPI_SWIGLU) {
+      o = rnd<DT>(silu16(o)) * rnd<DT>(v[NA - 1]);
+    } else if constexpr (EPI == EPI_GELU) {
+      o = 0.5f * o * (1.0f + erff(o * 0.70710678118654752f));
+    }
+    if (m < M && n < N) Y[(long)m * ldy + n] = E<DT>::from_f(o);
+  }
+}
+
+// linear_finish for the one-shot plans with 2 <= KW <= MT and a plain, gated or GELU epilogue: row tile t is finished
+// by the waves of K slice t % KW, so every wave of the weight tile takes MT / KW of the tiles instead of slice 0
+// taking all MT. The other slices' partials of a tile meet in LDS (`red`, free when this runs) and are added in
+// slice order with the finishing wave's own (the sum linear_finish forms); the epilogue and stores are
+// linear_finish's.
+template <int DT, int MT, int NW, int KW, int EPI, bool PRO>
+__device__ __forceinline__ void linear_finish_tiles(f32x4_t (&acc)[EPI == EPI_SWIGLU ? 2 : 1][MT], f32x4_t* red,
+                                                    int wn, int wk, int lane, int n0, int m0,
+                                                    uint16_t* __restrict__ Y, long ldy, int M, int N,
+                                                    const float2* pst, const NormIn& ni) {
+  constexpr int NA = EPI == EPI_SWIGLU ? 2 : 1;
+  static_assert(KW > 1 && KW <= MT, "a row tile per slice");
+  static_assert(EPI == EPI_NONE || EPI == EPI_SWIGLU || EPI == EPI_GELU, "plain, gated or GELU epilogue");
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+  auto slot = [&](int q, int a, int t) { return (((wn * KW + q) * NA + a) * MT + t) * 64 + lane; };
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+    if (t % KW != wk) {
+#pragma unroll
+      for (int a = 0; a < NA; ++a) red[slot(wk, a, t)] = acc[a][t];
+    }
+  __syncthreads();
+  const int n = n0 + 4 * lg;
+  const bool vec = (ldy & 3) == 0 && (((uintptr_t)Y) & 7) == 0 && n + 3 < N;
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    if (t % KW != wk) continue;  // wave-uniform
+    f32x4_t sum[NA];
+#pragma unroll
+    for (int a = 0; a < NA; ++a) {
+      sum[a] = wk == 0 ? acc[a][t] : red[slot(0, a, t)];
+#pragma unroll
+      for (int q = 1; q < KW; ++q) {
+        const f32x4_t v = q == wk ? acc[a][t] : red[slot(q, a, t)];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sum[a][r] = sum[a][r] + v[r];
+      }
+      if constexpr (PRO) norm_apply(sum[a], pst, 16 * t + li, ni, n, N, a);
+    }
+    const int m = m0 + 16 * t + li;
+    if (m >= M) continue;
+    uint16_t o[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v = rnd<DT>(sum[0][r]);
+      if constexpr (EPI == EPI_SWIGLU) {
+        v = rnd<DT>(silu16(v)) * rnd<DT>(sum[NA - 1][r]);
+      } else if constexpr (EPI == EPI_GELU) {
+        v = 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+      }
+      o[r] = E<DT>::from_f(v);
+    }
+    uint16_t* yp = Y + (long)m * ldy + n;
+    if (vec) {
+      uint2 pk;
+      pk.x = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
+      pk.y = (uint32_t)o[2] | ((uint32_t)o[3] << 16);
+      *reinterpret_cast<uint2*>(yp) = pk;
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (n + r < N) yp[r] = o[r];
+    }
+  }
+}
+
 // EPI_QKR's second half: the workgroup's ROWS rows x HPW whole heads of the projection, rounded to bf16, sit in LDS
 // (`tile`, row stride LDT halfwords, head hh of the workgroup at column 128 hh; workgroup nb holds heads
 // nb * HPW ..). Each 16-lane DPP row takes one (row, head) item at a time: a query or key head through
@@ -660,6 +788,14 @@ __global__ __launch_bounds__(64 * NWAVES) void linear_oneshot_kernel(const uint1
     static_assert(KW == 1 && DT == M3X_BF16, "one K slice, bf16");
     static_assert(ROWS * (16 * NW + 8) <= KW * ROWS * LDR, "the staged tile fits the block");
     qk_finish<MT, NW, NT, PRO>(acc, xs, wn, lane, nb, m0, M, N, pst, ni, qk);
+  } else if constexpr (KW > 1 && KW <= MT && EPI != EPI_RESID) {
+    static_assert(NW * KW * NA * MT * 1024 <= KW * ROWS * LDR * 2, "the partial tiles fit the block");
+    linear_finish_tiles<DT, MT, NW, KW, EPI, PRO>(acc, reinterpret_cast<f32x4_t*>(xs), wn, wk, lane, n0, m0, Y, ldy, M,
+                                                  N, pst, ni);
+  } else if constexpr (KW >= 4 && EPI != EPI_RESID) {
+    static_assert(NW * KW * NA * MT * 1024 <= KW * ROWS * LDR * 2, "the partial tiles fit the block");
+    linear_finish_spread<DT, MT, NW, KW, EPI, PRO>(acc, reinterpret_cast<float*>(xs), wn, wk, lane, n0, m0, Y, ldy, M,
+                                                   N, pst, ni);
   } else {
     linear_finish<DT, MT, NW, KW, EPI, PRO>(acc, reinterpret_cast<f32x4_t*>(xs), wn, wk, lane, n0, m0, Y, ldy, M, N,
                                             ro, pre, pst, ni);
