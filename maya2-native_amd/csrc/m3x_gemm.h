@@ -802,27 +802,28 @@ __global__ __launch_bounds__(64 * NWAVES) void linear_oneshot_kernel(const uint1
   }
 }
 
-// Large-M projections (M > 512 rows: steps with inline prefills). A workgroup of 8 waves owns a 2-D tile of 128
-// activation rows x 128 weight rows (for SwiGLU: 64 gate rows from W and the same 64 up rows from W2, i.e. 64
+// Large-M projections (M > 512 rows: steps with inline prefills). A workgroup of 8 waves owns a 2-D tile of 128 (or
+// 96: RT = 3) activation rows x 128 weight rows (for SwiGLU: 64 gate rows from W and the same 64 up rows from W2, i.e. 64
 // output columns) and walks K in stages of 64. The packed weight fragments of a stage are copied to LDS as they are
 // (16 fragments of 1 KB: every fragment read is one contiguous 1 KB); the activation rows sit row-major with a
 // 144-byte row stride, so the 16 rows of a fragment read fall in 16 different bank groups and a row's 8 stores in
-// distinct banks. The waves are 2 x 4 blocks of 64 activation rows x 32 weight rows (4 x 2 MFMA tiles; with
+// distinct banks. The waves are 2 x 4 blocks of 16 RT activation rows x 32 weight rows (RT x 2 MFMA tiles; with
 // SwiGLU a wave holds one gate tile and the matching up tile). Stages are double-buffered in LDS: the next stage's
 // global loads are in flight while the current one multiplies, with one barrier per stage. Every weight byte is
-// read by ceil(M / 128) workgroups and every activation byte by ceil(N / 128), against 36 and 64 for the 64 x 64
+// read by ceil(M / 32 RT) workgroups and every activation byte by ceil(N / 128), against 36 and 64 for the 64 x 64
 // chunked tiles at 2264 rows. Global loads run two stages ahead of the products (three register sets in turn):
 // measured 2-10 % faster than one stage ahead, most on the N = 1024 shapes whose grid has one workgroup per CU.
 // PRO (K == PRO_K): the rows' folded norm, applied in the epilogue; its statistics (and EPI_RESID's operands) load
 // after the products.
-template <int DT, int EPI, bool PRO>
+template <int DT, int EPI, bool PRO, int RT>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void linear_tiled_kernel(const uint16_t* __restrict__ X, long ldx,
                                                               const uint16_t* __restrict__ Wp,
                                                               const uint16_t* __restrict__ W2p,
                                                               uint16_t* __restrict__ Y, long ldy, int M, int N, int K,
                                                               int mblk, int nblk, NormIn ni, ResidOut ro, QkOut qk) {
   constexpr bool DUAL = EPI == EPI_SWIGLU;
-  constexpr int BM = 128;
+  constexpr int BM = 32 * RT;  // activation rows: 2 wave rows x RT tiles of 16
+  static_assert(RT == 3 || RT == 4, "96- or 128-row blocks");
   constexpr int LDA = 72;  // activation row stride in LDS, halfwords
   __shared__ __align__(16) uint16_t lw[2][16 * 512];
   __shared__ __align__(16) uint16_t la[2][BM * LDA];
@@ -839,7 +840,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
   const int lane = tid & 63;
   const int li = lane & 15;
   const int lg = lane >> 4;
-  const int wm = wave & 1;   // activation tiles 4 wm .. 4 wm + 3
+  const int wm = wave & 1;   // activation tiles RT wm .. RT wm + RT - 1
   const int wn = wave >> 1;  // weight tiles (below)
   const int ksteps = K >> 5;
   const int ntiles = (N + 15) >> 4;
@@ -856,19 +857,23 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     const int t = f >> 1, st = f & 1;
     const int tt = min(DUAL ? nb * 4 + (t & 3) : nb * 8 + t, ntiles - 1);  // tiles past N: valid, never stored
     gw[j] = (tt * ksteps + st) * 512 + (tid & 63) * 8;
-    ga[j] = min(m0 + (tid >> 3) + 64 * j, M - 1) * (int)ldx + 8 * (tid & 7);  // rows past M: re-read, never stored
+    // rows past M: re-read, never stored; with 96-row blocks the second slot's rows past the block repeat its
+    // last row (the same value to the same LDS place)
+    ga[j] = min(m0 + min((tid >> 3) + 64 * j, BM - 1), M - 1) * (int)ldx + 8 * (tid & 7);
   }
-  const int la0 = (tid >> 3) * LDA + 8 * (tid & 7);
+  int la0[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) la0[j] = min((tid >> 3) + 64 * j, BM - 1) * LDA + 8 * (tid & 7);
   // the wave's 2 weight tiles: plain 2 wn + i; SwiGLU gate wn and up 4 + wn
   int wt[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) wt[i] = DUAL ? (i == 0 ? wn : 4 + wn) : 2 * wn + i;
 
-  f32x4_t acc[2][4];
+  f32x4_t acc[2][RT];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < RT; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   // a stage's loads in r[0..1] (weight fragments) and r[2..3] (activation rows); stages past the end re-read the
   // last stage (valid addresses, never stored)
@@ -885,22 +890,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       st16(&lw[buf][tid * 8 + 4096 * j], r[j]);
-      st16(&la[buf][la0 + 64 * j * LDA], r[2 + j]);
+      st16(&la[buf][la0[j]], r[2 + j]);
     }
   };
   auto compute = [&](int buf) {
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      u16x8 a[2], b[4];
+      u16x8 a[2], b[RT];
 #pragma unroll
       for (int i = 0; i < 2; ++i) a[i] = *reinterpret_cast<const u16x8*>(&lw[buf][(wt[i] * 2 + s) * 512 + lane * 8]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        b[j] = *reinterpret_cast<const u16x8*>(&la[buf][(16 * (4 * wm + j) + li) * LDA + 32 * s + 8 * lg]);
+      for (int j = 0; j < RT; ++j)
+        b[j] = *reinterpret_cast<const u16x8*>(&la[buf][(16 * (RT * wm + j) + li) * LDA + 32 * s + 8 * lg]);
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16x16x32<DT>(a[i], b[j], acc[i][j]);
+        for (int j = 0; j < RT; ++j) acc[i][j] = mfma16x16x32<DT>(a[i], b[j], acc[i][j]);
     }
   };
   u16x8 R0[4], R1[4], R2[4];
@@ -930,13 +935,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
 
   // the epilogue's operands load after the products: held across the long K loop they would cost the registers
   // of a second workgroup per CU
-  ResidPre pre[2][4];
+  ResidPre pre[2][RT];
   if constexpr (EPI == EPI_RESID) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        pre[i][j] = resid_prefetch(ro, m0 + 16 * (4 * wm + j) + li, (nb * 8 + wt[i]) * 16 + 4 * lg, M, N);
+      for (int j = 0; j < RT; ++j)
+        pre[i][j] = resid_prefetch(ro, m0 + 16 * (RT * wm + j) + li, (nb * 8 + wt[i]) * 16 + 4 * lg, M, N);
   }
   if constexpr (PRO) ns.load(ni, m0, M, PRO_K);
 
@@ -947,7 +952,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     for (int i = 0; i < 2; ++i) {
       const int n = DUAL ? (nb * 4 + wn) * 16 + 4 * lg : (nb * 8 + wt[i]) * 16 + 4 * lg;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) norm_apply(acc[i][j], pst, 16 * (4 * wm + j) + li, ni, n, N, DUAL ? i : 0);
+      for (int j = 0; j < RT; ++j) norm_apply(acc[i][j], pst, 16 * (RT * wm + j) + li, ni, n, N, DUAL ? i : 0);
     }
   }
   if constexpr (EPI == EPI_RESID) {
@@ -955,8 +960,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     for (int i = 0; i < 2; ++i) {
       const int tile = nb * 8 + wt[i];
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        resid_quad<DT>(acc[i][j], pre[i][j], m0 + 16 * (4 * wm + j) + li, tile * 16 + 4 * lg, tile, M, N, lg, ro, Y,
+      for (int j = 0; j < RT; ++j)
+        resid_quad<DT>(acc[i][j], pre[i][j], m0 + 16 * (RT * wm + j) + li, tile * 16 + 4 * lg, tile, M, N, lg, ro, Y,
                        ldy);
     }
     return;
@@ -970,22 +975,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) qk_stage(tile, LDT, 16 * (4 * wm + j) + li, 16 * wt[i] + 4 * lg, acc[i][j]);
+      for (int j = 0; j < RT; ++j) qk_stage(tile, LDT, 16 * (RT * wm + j) + li, 16 * wt[i] + 4 * lg, acc[i][j]);
     __syncthreads();
     qk_items<BM, 1, 512>(tile, LDT, nb, m0, M, qk);
     return;
   }
 
   // epilogue: lane (li, lg) of tile pair (i, j) holds weight rows 4 lg + r of tile wt[i] for activation row
-  // m0 + 16 (4 wm + j) + li
+  // m0 + 16 (RT wm + j) + li
   const bool vec = (ldy & 3) == 0 && (((uintptr_t)Y) & 7) == 0;
   constexpr int NI = DUAL ? 1 : 2;
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     const int n = DUAL ? (nb * 4 + wn) * 16 + 4 * lg : (nb * 8 + wt[i]) * 16 + 4 * lg;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int m = m0 + 16 * (4 * wm + j) + li;
+    for (int j = 0; j < RT; ++j) {
+      const int m = m0 + 16 * (RT * wm + j) + li;
       if (m >= M) continue;
       uint16_t o[4];
 #pragma unroll
@@ -1087,11 +1092,14 @@ static LinearPlan linear_plan(int M, int N, int K, bool dual, long ldx) {
   // tiled: 32-bit element offsets into the packed weight and the activations
   if (M > 512 && K % 64 == 0 && (long)ntiles * 16 * K < (1L << 31) && (long)M * ldx < (1L << 31)) {
     p.tiled = 1;
-    p.mt = 8;
     p.nw = dual ? 4 : 8;
     p.oneshot = 0;
-    p.mblk = m3x_ceil_div(M, 128);
     p.nblk = m3x_ceil_div(ntiles, p.nw);
+    // 96- or 128-row blocks, whichever gives the fewer rows per CU over the rounds of two workgroups per CU
+    // (measured at 2264 rows: 96 is 9-11 % faster for q|k|v, o and down, 11 % slower for gate|up's 1,152 blocks)
+    const long w6 = (long)m3x_ceil_div(M, 96) * p.nblk, w8 = (long)m3x_ceil_div(M, 128) * p.nblk;
+    p.mt = (w6 + 511) / 512 * 96 < (w8 + 511) / 512 * 128 ? 6 : 8;
+    p.mblk = m3x_ceil_div(M, 16 * p.mt);
     return p;
   }
   if (wide_plan(M, N, K, dual, p)) {
@@ -1136,8 +1144,12 @@ static bool launch_linear(const LinearPlan& p, hipStream_t st, const uint16_t* X
   if constexpr (EPI == EPI_QKR) {
     // whole heads per workgroup: the tiled plan (128 columns) or the one-shot plan of 8 weight tiles in one K slice
     if (p.tiled) {
-      hipLaunchKernelGGL((linear_tiled_kernel<DT, EPI_QKR, PRO>), grid, dim3(512), 0, st, X, ldx, W, W2, Y, ldy, M, N,
-                         K, p.mblk, p.nblk, ni, ro, qk);
+      if (p.mt == 6)
+        hipLaunchKernelGGL((linear_tiled_kernel<DT, EPI_QKR, PRO, 3>), grid, dim3(512), 0, st, X, ldx, W, W2, Y, ldy,
+                           M, N, K, p.mblk, p.nblk, ni, ro, qk);
+      else
+        hipLaunchKernelGGL((linear_tiled_kernel<DT, EPI_QKR, PRO, 4>), grid, dim3(512), 0, st, X, ldx, W, W2, Y, ldy,
+                           M, N, K, p.mblk, p.nblk, ni, ro, qk);
       return true;
     }
     if (!p.oneshot || p.mt != 2 || p.nw != 8 || p.nwaves != 8 || p.oneshot != 32) return false;
@@ -1146,8 +1158,12 @@ static bool launch_linear(const LinearPlan& p, hipStream_t st, const uint16_t* X
     return true;
   } else {
   if (p.tiled) {
-    hipLaunchKernelGGL((linear_tiled_kernel<DT, EPI, PRO>), grid, dim3(512), 0, st, X, ldx, W, W2, Y, ldy, M, N, K,
-                       p.mblk, p.nblk, ni, ro, qk);
+    if (p.mt == 6)
+      hipLaunchKernelGGL((linear_tiled_kernel<DT, EPI, PRO, 3>), grid, dim3(512), 0, st, X, ldx, W, W2, Y, ldy, M, N,
+                         K, p.mblk, p.nblk, ni, ro, qk);
+    else
+      hipLaunchKernelGGL((linear_tiled_kernel<DT, EPI, PRO, 4>), grid, dim3(512), 0, st, X, ldx, W, W2, Y, ldy, M, N,
+                         K, p.mblk, p.nblk, ni, ro, qk);
     return true;
   }
 #define M3X_ONE(MTT, NWW, NWV, SS)                                                                              \
