@@ -77,6 +77,17 @@ int m3x_decode_attn(const void* q, long sq_b, long sq_h, const void* k_cache, co
  * and split, ~3 workgroups per CU. */
 int m3x_decode_attn_item_bins(int rows, int kv_heads, int max_ctx, int chunk);
 
+/* Host function (no GPU work): the item list of m3x_decode_attn for rows laid out as nruns runs, runs[3 i ..] =
+ * (first row, rows, first position): a decode row is a run of one row, an inline prefill of T tokens a run of T rows
+ * at consecutive positions of one slot. Each run is cut into blocks of up to 16 / (heads / kv_heads) rows and each
+ * block's keys into splits of `chunk`; an item is one split of one block, costing its keys + 64. The items are dealt
+ * into `bins` bins longest processing time first (stable on equal costs), each to the least loaded bin (lowest index
+ * on equal loads). Writes [bins, start[0..bins], codes bin by bin] into out (capacity out_cap int32) and returns the
+ * count, or a negative status. Replaces the host-side staging of `step_mixed`'s inline prefill rows
+ * (serve/fast_backbone.py:326-333). */
+long m3x_decode_attn_items(const int32_t* runs, int nruns, int heads, int kv_heads, int bins, int chunk, int32_t* out,
+                           long out_cap);
+
 /* m3x_decode_attn without a workspace argument, allocating nothing. No counterpart in the reference: it is for
  * callers that cannot allocate (code under graph capture, tight serving loops, harnesses that forbid allocation).
  * The split partials live in a file-scope device array of M3X_DECODE_ATTN_NOALLOC_SCRATCH bytes that each GPU holds

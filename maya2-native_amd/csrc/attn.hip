@@ -18,6 +18,8 @@
 #include "m3x_common.h"
 
 #include <algorithm>
+#include <queue>
+#include <vector>
 #include <mutex>
 
 // K rows through a wave-private LDS tile (coalesced loads; bit-identical results): 1-2 % faster at 224 rows and
@@ -457,6 +459,63 @@ static int attn_item_bins(int rows, int kv_heads) { return std::max(1, std::min(
 M3X_API int m3x_decode_attn_item_bins(int rows, int kv_heads, int max_ctx, int chunk) {
   if (rows <= 0 || kv_heads <= 0 || max_ctx <= 0 || chunk <= 0) return 0;
   return attn_item_bins(rows, kv_heads);
+}
+
+// Host side: the work items of an item launch for rows laid out as runs (first row, rows, first position): each run
+// cut into blocks of up to 16 / (heads / kv_heads) rows, each block's keys into splits of `chunk`; an item is one
+// split of one block, cost = its keys + 64. Items are dealt into `bins` bins longest processing time first (stable
+// by item index on equal costs), each to the least loaded bin (the lowest index on equal loads). Writes
+// [bins, start[0..bins], codes bin by bin] with code = 2048 * first_row + 32 * split + rows and returns the count.
+M3X_API long m3x_decode_attn_items(const int32_t* runs, int nruns, int heads, int kv_heads, int bins, int chunk,
+                                   int32_t* out, long out_cap) {
+  if (!runs || !out) return M3X_ENULL;
+  if (nruns < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads || bins <= 0 || chunk <= 0) return M3X_EINVAL;
+  const int qb = std::max(1, 16 / (heads / kv_heads));
+  std::vector<long> cost;
+  std::vector<int32_t> code;
+  for (int i = 0; i < nruns; ++i) {
+    const long r0 = runs[3 * i], n = runs[3 * i + 1], p0 = runs[3 * i + 2];
+    if (r0 < 0 || n < 0 || p0 < 0 || r0 + n > (1L << 20)) return M3X_EINVAL;
+    for (long s = 0; s < n; s += qb) {
+      const long m = std::min<long>(qb, n - s);
+      const long keys = p0 + s + m;  // the block's last row attends keys 0 .. keys - 1
+      const long nsp = (keys + chunk - 1) / chunk;
+      if (nsp > 64) return M3X_EINVAL;
+      for (long sp = 0; sp < nsp; ++sp) {
+        cost.push_back(std::min<long>(chunk, keys - sp * chunk) + 64);
+        code.push_back((int32_t)(2048 * (r0 + s) + 32 * sp + m));
+      }
+    }
+  }
+  const long nitems = (long)code.size();
+  if (out_cap < 2 + bins + nitems) return M3X_EINVAL;
+  std::vector<long> order(nitems);
+  for (long i = 0; i < nitems; ++i) order[i] = i;
+  std::stable_sort(order.begin(), order.end(), [&](long a, long b) { return cost[a] > cost[b]; });
+  std::vector<std::vector<int32_t>> per(bins);
+  using Load = std::pair<long, int>;
+  std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
+  const long k = std::min<long>(bins, nitems);
+  for (long b = 0; b < k; ++b) {
+    per[b].push_back(code[order[b]]);
+    heap.push(Load(cost[order[b]], (int)b));
+  }
+  for (long j = k; j < nitems; ++j) {
+    const long i = order[j];
+    const Load top = heap.top();
+    heap.pop();
+    per[top.second].push_back(code[i]);
+    heap.push(Load(top.first + cost[i], top.second));
+  }
+  out[0] = bins;
+  out[1] = 0;
+  long w = 2 + bins, acc = 0;
+  for (int b = 0; b < bins; ++b) {
+    acc += (long)per[b].size();
+    out[2 + b] = (int32_t)acc;
+    for (int32_t c : per[b]) out[w++] = c;
+  }
+  return w;
 }
 
 template <int G>

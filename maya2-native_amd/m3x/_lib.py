@@ -12,7 +12,7 @@ import os
 import torch  # noqa: F401  (must precede the CDLL load, see above)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libm3x.so")
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -32,6 +32,7 @@ SIGNATURES = {
                                     _I, _I, _I, _P]),
     "m3x_decode_attn_workspace": (_Z, [_I, _I, _I, _I]),
     "m3x_decode_attn_item_bins": (_I, [_I, _I, _I, _I]),
+    "m3x_decode_attn_items": (_L, [_P, _I, _I, _I, _I, _I, _P, _L]),
     "m3x_decode_attn": (_I, [_P, _L, _L, _P, _P, _L, _L, _L, _I, _P, _L, _L, _P, _P, _P, _F, _I, _I, _I, _I, _I, _I,
                              _P, _Z, _P]),
     "m3x_decode_attn_noalloc": (_I, [_P, _L, _L, _P, _P, _L, _L, _L, _I, _P, _L, _L, _P, _P, _P, _F, _I, _I, _I, _I,

@@ -9,7 +9,6 @@ from __future__ import annotations
 
 import ctypes
 
-import heapq
 
 import numpy as np
 
@@ -166,31 +165,18 @@ def attn_items(runs, heads, kv_heads, bins, chunk):
     slot. Each run is cut into blocks of up to 16 // (heads // kv_heads) rows and each block's keys into splits of
     `chunk` keys; an item is one split of one block. The items are dealt into `bins` bins (attn_item_bins) longest
     processing time first: each goes to the least loaded bin, its cost its keys plus a fixed 64. Returns int32
-    [bins, start[0..bins], codes bin by bin], code = 2048 * first_row + 32 * split + rows."""
-    qb = 16 // (heads // kv_heads)
-    costs, codes = [], []
-    for r0, n, p0 in runs:
-        for s in range(0, n, qb):
-            m = min(qb, n - s)
-            keys = p0 + s + m  # the block's last row attends keys 0 .. p0 + s + m - 1
-            for sp in range(0, (keys + chunk - 1) // chunk):
-                costs.append(min(chunk, keys - sp * chunk) + 64)
-                codes.append(2048 * (r0 + s) + 32 * sp + m)
-    order = np.argsort(-np.asarray(costs, dtype=np.int64), kind="stable").tolist()
-    k = min(bins, len(order))
-    per = [[codes[i]] for i in order[:k]] + [[] for _ in range(bins - k)]
-    heap = [(costs[i], b) for b, i in enumerate(order[:k])]
-    heapq.heapify(heap)
-    for i in order[k:]:
-        load, b = heap[0]
-        per[b].append(codes[i])
-        heapq.heapreplace(heap, (load + costs[i], b))
-    out = np.empty(2 + bins + len(codes), dtype=np.int32)
-    out[0] = bins
-    out[1] = 0
-    np.cumsum([len(p) for p in per], out=out[2:2 + bins])
-    out[2 + bins:] = [c for p in per for c in p]
-    return out
+    [bins, start[0..bins], codes bin by bin], code = 2048 * first_row + 32 * split + rows. Built on the host by the
+    library (m3x_decode_attn_items)."""
+    r = np.ascontiguousarray(np.asarray(runs, dtype=np.int32).reshape(-1, 3))
+    qb = max(1, 16 // (heads // kv_heads))
+    n, p0 = r[:, 1].astype(np.int64), r[:, 2].astype(np.int64)
+    bound = int((-(-n // qb) * (-(-(p0 + n) // chunk))).sum())  # blocks x the run's most splits
+    out = np.empty(2 + bins + bound, dtype=np.int32)
+    cnt = lib().m3x_decode_attn_items(r.ctypes.data, r.shape[0], heads, kv_heads, bins, chunk, out.ctypes.data,
+                                      out.size)
+    if cnt < 0:
+        raise ValueError(f"attn_items: m3x_decode_attn_items returned {cnt}")
+    return out[:cnt]
 
 
 class PackedWeight:

@@ -57,6 +57,51 @@ def test_attn_items_cover_every_row_once():
         assert max(loads) - min(loads) <= max(cost.values())
 
 
+def _items_restated(runs, heads, kv_heads, bins, chunk):
+    """The item list restated: blocks of 16 // G rows, splits of `chunk` keys, cost keys + 64, a stable longest-first
+    order and each item to the least loaded bin (lowest index on ties)."""
+    import heapq
+    qb = 16 // (heads // kv_heads)
+    costs, codes = [], []
+    for r0, n, p0 in runs:
+        for s in range(0, n, qb):
+            m = min(qb, n - s)
+            keys = p0 + s + m
+            for sp in range((keys + chunk - 1) // chunk):
+                costs.append(min(chunk, keys - sp * chunk) + 64)
+                codes.append(2048 * (r0 + s) + 32 * sp + m)
+    order = sorted(range(len(costs)), key=lambda i: -costs[i])
+    per = [[] for _ in range(bins)]
+    heap = [(0, b) for b in range(bins)]
+    for i in order:
+        load, b = heapq.heappop(heap)
+        per[b].append(codes[i])
+        heapq.heappush(heap, (load + costs[i], b))
+    start = [0]
+    for p in per:
+        start.append(start[-1] + len(p))
+    return [bins] + start + [c for p in per for c in p]
+
+
+def test_attn_items_deal_order():
+    """The library's item list is exactly the restated deal (what the GPU's bins walk), and splits past the code's
+    64 are refused."""
+    import numpy as np
+    from m3x import ops
+    rng = np.random.default_rng(5)
+    for trial in range(40):
+        runs, row = [], 0
+        for _ in range(int(rng.integers(1, 120))):
+            n = 1 if rng.random() < 0.8 else int(rng.integers(1, 300))
+            runs.append((row, n, int(rng.integers(0, 3000))))
+            row += n
+        heads, kv = (16, 8) if trial % 2 else (16, 16)
+        bins, chunk = int(rng.integers(1, 100)), int(rng.choice([128, 512, 4096]))
+        assert ops.attn_items(runs, heads, kv, bins, chunk).tolist() == _items_restated(runs, heads, kv, bins, chunk)
+    with pytest.raises(ValueError):
+        ops.attn_items([(0, 1, 65 * 128)], 16, 8, 4, 128)
+
+
 def test_roofline_matches_published_shapes():
     # BASELINE: backbone weights 880,803,840 B; 112 KiB of KV per token per seat
     assert roofline.backbone_weight_bytes() == 880_803_840
