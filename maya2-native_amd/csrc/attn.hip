@@ -412,7 +412,7 @@ __device__ __forceinline__ void attn_block_item(
 // it; the differences are the causal mask (vector j sees keys <= pos[row + j]) and the per-vector rescale (O rows
 // are vectors 4 * lg + r, whose running max lives in lane 4 * lg + r). Rows whose context spans several splits
 // write partials for decode_attn_combine_kernel.
-// The grid is one workgroup per bin per kv head, ~3 workgroups per CU whatever the item count (a workgroup
+// The grid is one workgroup per bin per kv head, 2 workgroups per CU whatever the item count (a workgroup
 // launched only to exit costs a CU slot for microseconds). An item is one split of its rows' keys, so a long
 // context is cut into several items that the bins balance. The caller deals the items into the bins (longest
 // processing time first balances them) and lists them bin by bin:

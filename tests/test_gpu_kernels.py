@@ -605,6 +605,16 @@ def test_index_kernels(gpu):
     assert pos.tolist() == [17, 5, 18, 0]
     ops.lengths_add(lengths, slots, torch.tensor([1, 1, 1, 0], device=gpu))
     assert lengths.tolist() == [6, 0, 19, 3, 0]
+    # runs of one slot across wave and workgroup boundaries, duplicates apart, zeros, a ragged tail
+    rs = np.random.default_rng(3)
+    sl = np.concatenate([np.full(300, 7), rs.integers(0, 12, 50), np.full(61, 3), [7, 7], np.full(130, 11)])
+    re = rs.integers(0, 3, sl.size)
+    re[:40] = 1
+    want = np.zeros(12, dtype=np.int64)
+    np.add.at(want, sl, re)
+    lens = torch.zeros(12, dtype=torch.int64, device=gpu)
+    ops.lengths_add(lens, torch.from_numpy(sl).to(gpu), torch.from_numpy(re).to(gpu))
+    assert lens.cpu().numpy().tolist() == want.tolist()
     table = torch.randn(50, 64, generator=g).to(torch.bfloat16).to(gpu)
     idx = torch.tensor([3, 49, 0, 7], dtype=torch.int32, device=gpu)
     dst = torch.zeros(10, 64, dtype=torch.bfloat16, device=gpu)
