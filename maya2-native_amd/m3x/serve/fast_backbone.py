@@ -363,13 +363,14 @@ class StaticBackbone:
             items = ops.attn_items(runs, self.heads, self.kv_heads, b.item_bins, b.chunk)
             g.items.buffer()[:len(items)] = items
             g.items.send(len(items))
-        at = 0
-        if slots:
-            b.x[:len(slots)].copy_(x)
-            at = len(slots)
-        for _, t in prefills:
-            b.x[at:at + t.shape[0]].copy_(t)
-            at += t.shape[0]
+        parts = ([x] if slots else []) + [t for _, t in prefills]
+        if len(parts) > 1 and all(p.dim() == 2 and p.dtype == b.x.dtype and p.device == b.x.device for p in parts):
+            torch.cat(parts, out=b.x[:n])  # one copy kernel for the decode rows and every prefill
+        else:
+            at = 0
+            for p in parts:
+                b.x[at:at + p.shape[0]].copy_(p)
+                at += p.shape[0]
         if g.graph is not None:
             g.graph.replay()
         else:
