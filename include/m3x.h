@@ -59,7 +59,7 @@ size_t m3x_decode_attn_workspace(int rows, int kv_heads, int max_ctx, int chunk)
 /* GQA decode attention in place over the static cache: out[r, h, :] = softmax(q[r,h]·K[slot,h/G,0..pos]^T * scale)
  * · V[...]; heads/kv_heads in {1, 2}; head_dim 128; chunk = keys per split (multiple of 128); max_ctx >= pos+1
  * for every row; cap % 32 == 0.
- * items (nullable) lists the step's work for one launch of ~3 workgroups per CU: an item is split s (keys
+ * items (nullable) lists the step's work for one launch of 2 workgroups per CU: an item is split s (keys
  * [s * chunk, (s + 1) * chunk)) of m rows of one slot (1 <= m <= 16 / G: a decode row, or up to 16 / G rows of an
  * inline prefill), code 2048 * first_row + 32 * s + m; every split of every row in exactly one item; rows < 2^20.
  * The items are dealt into bins = m3x_decode_attn_item_bins(...) bins, and items = [bins, start[0], ...,
@@ -74,7 +74,7 @@ int m3x_decode_attn(const void* q, long sq_b, long sq_h, const void* k_cache, co
                     int head_dim, int max_ctx, int chunk, void* workspace, size_t ws_bytes, void* stream);
 
 /* Bins of m3x_decode_attn's item launch for (rows, kv_heads, max_ctx, chunk): one workgroup per bin per kv head
- * and split, ~3 workgroups per CU. */
+ * and split, 2 workgroups per CU (512 over the kv heads). */
 int m3x_decode_attn_item_bins(int rows, int kv_heads, int max_ctx, int chunk);
 
 /* Host function (no GPU work): the item list of m3x_decode_attn for rows laid out as nruns runs, runs[3 i ..] =
