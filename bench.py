@@ -38,8 +38,8 @@ def build_frame(torch, seats, lengths, seed_base=0, backbone=None, depth_model=N
     from m3x.serve.fast_backbone import StaticBackbone
     from m3x.serve.fast_depth import FastDepth
     dev = torch.device("cuda:0")
-    bb = backbone or synth.qwen3_backbone(layers=28, seed=0, device=dev, gen="cuda")
-    dm = depth_model or synth.swiglu_depth(seed=1, device=dev, gen="cuda")
+    bb = backbone or synth.qwen3_backbone(layers=28, seed=0, device=dev, gen="cuda", affine=synth.AFFINE)
+    dm = depth_model or synth.swiglu_depth(seed=1, device=dev, gen="cuda", affine=synth.AFFINE)
     sb = StaticBackbone(bb, seats, capacity=CAP, batch_buckets=(seats,), ctx_buckets=(CAP,), attention="triton",
                         fuse_rope=True)
     g = torch.Generator(device=dev).manual_seed(100 + seed_base)
@@ -258,8 +258,63 @@ def secondary(torch, bb, dm, steps):
     log(f"prefill of {Tp} tokens: {pre_ms:.2f} ms (HF eager: {out['ttfa_prefill'].get('hf_eager_ms')})")
     del sb
     torch.cuda.empty_cache()
+    out["depthv2_geometry"] = depthv2_frame(torch, max(steps * 4, 20))
     out["mimi_decode"] = mimi_decode(torch, dev, max(steps, 20))
     return out
+
+
+def depthv2_frame(torch, steps, seat_counts=(1, 16)):
+    """The reference's own depth geometry, timed: a DepthV2-shaped trunk (LayerNorm + GELU 3072, 16 heads x 64, 4
+    layers, the 11 weight groups of GROUP_OF_LEVEL, rank-128 code embeddings, per-layer speaker cross constants set
+    for every seat) as an fp16 FastDepth (the engine's default depth dtype, maya3/engine.py:53) with the reference's
+    sampling defaults (temp 0.7, top-k 64). Graph-timed depth frame (HIP events over replays of the FastDepth graph)
+    and the wall time of __call__, at 1 and 16 seats, beside the reference's published depth stage of its
+    one-seat frame: 6.5 ms on an H100 NVL (docs/ENGINE.md:211, its real 555M decoder of this geometry)."""
+    from m3x import roofline, synth
+    from m3x.serve.fast_depth import FastDepth
+    dev = torch.device("cuda:0")
+    model = synth.depthv2_like(seed=2, device=dev, dtype=torch.float16, affine_std=0.1)
+    S = max(seat_counts)
+    fd = FastDepth(model, S, dtype=torch.float16, temp=0.7, top_k=64, batch_buckets=tuple(seat_counts), fused=True)
+    g = torch.Generator(device=dev).manual_seed(400)
+    for s in range(S):
+        fd.set_speaker(s, torch.randn(1, 1, 1024, device=dev, generator=g), torch.ones(1, 1, device=dev))
+    fd.row_seed.copy_(torch.arange(S + 1, dtype=torch.int32, device=dev) * 7919 + 3)
+    fd.warmup()
+    stream = torch.cuda.current_stream()
+    res = {"geometry": "DepthV2: LayerNorm + GELU 3072, 16 x 64 heads, 4 layers, 11 weight groups "
+                       "(GROUP_OF_LEVEL), speaker constants; fp16; temp 0.7, top-k 64",
+           "reference_b1_depth_ms": 6.5, "reference_hardware": "1x H100 NVL (docs/ENGINE.md:211)"}
+    for B in seat_counts:
+        h = torch.randn(B, 1024, device=dev, generator=g).to(torch.float16)
+        cb0 = torch.randint(0, 2048, (B,), device=dev, generator=g)
+        slots = list(range(B))
+        for _ in range(3):
+            fd(slots, h, cb0)
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(steps):
+            t0 = time.perf_counter()
+            fd(slots, h, cb0)
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+        gr = fd._graph(fd.bucket_for(B))
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            gr.graph.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        gms = e0.elapsed_time(e1) / steps
+        byt = roofline.depth_frame_bytes(ffn=3072, ffn_mats=2, seats=B)
+        res[f"b{B}"] = {"seats": B, "graph_ms": round(gms, 4), "call_wall_ms": round(sorted(ts)[len(ts) // 2] * 1e3, 4),
+                        "persistent_levels": bool(fd._persistent_ok(B, 10)), "bytes_algorithmic": byt,
+                        "hbm_fraction": round(byt / (gms * 1e-3) / 1e9 / roofline.HBM_PEAK_GBS, 4)}
+        log(f"DepthV2 geometry fp16, {B} seats: {gms:.3f} ms per depth frame in the graph "
+            f"(reference: 6.5 ms at one seat on an H100 NVL)")
+    del fd, model
+    torch.cuda.empty_cache()
+    return res
 
 
 def mimi_decode(torch, dev, steps):
@@ -364,28 +419,20 @@ def _hf_eager_prefill_ms(torch, bb, x, steps):
     return sorted(ts)[len(ts) // 2] * 1e3
 
 
-def cpu_baseline(torch, seconds, seats=8):
-    """The oracle's eager frame (backbone + cb0 + depth) on the host cores at the C5 shapes over a `seats`-seat
-    subset of the 224 seats (the full 224-seat KV cache, 106 GB, is not built on the host). The value is the
-    subset's rate in seat-frames per second; the frames/s of a 224-seat frame extrapolate from it linearly in the
-    seats, which the sample text states."""
+def _cpu_frames(torch, O, bb, dm, seats, seconds, seed):
+    """Seconds per eager oracle frame (backbone + cb0 + depth + feedback) at `seats` seats of the C5 shapes, over
+    the frames that fit in `seconds` after one untimed frame (at least 2, at most 50)."""
     from m3x import synth
-    from oracle import torch_oracle as O
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    torch.set_num_threads(threads)
-    bb = synth.qwen3_backbone(layers=28, seed=0, device="cpu")
-    dm = synth.swiglu_depth(seed=1, device="cpu")
-    lengths = synth.c5_lengths(seats)
+    lengths = synth.c5_lengths(seats, seed=seed)
     cap = int(lengths.max()) + 64
-    g = torch.Generator().manual_seed(200)
+    g = torch.Generator().manual_seed(200 + seats)
     kc = [torch.randn(seats + 1, 8, cap, 128, generator=g).to(torch.bfloat16) for _ in range(28)]
     vc = [torch.randn(seats + 1, 8, cap, 128, generator=g).to(torch.bfloat16) for _ in range(28)]
     L = torch.cat([lengths, torch.zeros(1, dtype=torch.long)])
     cos, sin = O.rope_tables(128, 1e6, cap, torch.bfloat16)
     x = torch.randn(seats, 1024, generator=g).to(torch.bfloat16)
     slots = torch.arange(seats)
-    frames = 0
-    t0 = time.perf_counter()
+    frames, t0 = -1, 0.0
     while True:
         h = O.backbone_step(bb, kc, vc, L, slots, x, cos, sin)
         u = torch.rand(seats, 32, generator=g)
@@ -393,21 +440,47 @@ def cpu_baseline(torch, seconds, seats=8):
         codes, _ = O.depth_frame(dm, h, cb0, u[:, 1:], 0.9, 50)
         x = O.feedback(dm.audio_in, codes)
         frames += 1
+        if frames == 0:
+            t0 = time.perf_counter()
+            continue
         el = time.perf_counter() - t0
-        log(f"cpu baseline frame {frames}: {el:.1f}s")
-        if el >= seconds or frames >= 50:
-            break
+        log(f"cpu baseline, {seats} seats, frame {frames}: {el:.1f}s")
+        if (el >= seconds and frames >= 2) or frames >= 50:
+            return el / frames, frames, lengths.tolist()
+
+
+def cpu_baseline(torch, seconds, sizes=(2, 10)):
+    """The oracle's eager frame (backbone + cb0 + depth) on the host cores at the C5 shapes, timed at two seat
+    counts and fitted as t(B) = a + b B: the fixed part a (weights streamed and converted once per frame, whatever
+    the seats) and the per-seat part b (the seat's KV history, its rows through every projection, its sampling)
+    both measured, then the 224-seat frame time a + 224 b. A full 224-seat frame is not run: its 106 GB cache would
+    have to be drawn on the host first, and this line bounds the CPU work to about `seconds` so that the default
+    run ends in minutes."""
+    from m3x import synth
+    from oracle import torch_oracle as O
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    bb = synth.qwen3_backbone(layers=28, seed=0, device="cpu", affine=synth.AFFINE)
+    dm = synth.swiglu_depth(seed=1, device="cpu", affine=synth.AFFINE)
+    pts = [(s,) + _cpu_frames(torch, O, bb, dm, s, seconds / len(sizes), 5) for s in sizes]
+    (s1, t1, n1, l1), (s2, t2, n2, l2) = pts
+    b = (t2 - t1) / (s2 - s1)
+    a = t1 - b * s1
+    t224 = a + 224 * b
     try:
         ram_gb = round(os.sysconf("SC_PAGE_SIZE") * os.sysconf("SC_PHYS_PAGES") / 2 ** 30, 1)
     except (ValueError, OSError):
         ram_gb = None
-    rate = seats * frames / el
-    return dict(value=round(rate, 4), unit="frames/s", cores=threads, kind="port", extrapolated=True,
+    return dict(value=round(224 / t224, 4), unit="frames/s", cores=threads, kind="port", extrapolated=True,
                 host_ram_gib=ram_gb, host_cpus=os.cpu_count(),
-                sample=f"extrapolated from a {seats}-seat subset: {frames} frame step(s) x {seats} seats of the B=224 "
-                       f"workload shapes (28 layers, KV lengths {lengths.tolist()}, depth 31 codebooks) through the "
-                       f"PyTorch-eager oracle in {el:.1f} s on {threads} host threads; a 224-seat frame at this "
-                       f"rate takes {224 / rate:.1f} s on this host")
+                fit={"fixed_s_per_frame": round(a, 4), "s_per_seat_frame": round(b, 5),
+                     "points": [{"seats": s1, "s_per_frame": round(t1, 4), "frames": n1},
+                                {"seats": s2, "s_per_frame": round(t2, 4), "frames": n2}]},
+                sample=f"the PyTorch-eager oracle's frame (28 layers, cb0, depth over 31 codebooks) on {threads} host "
+                       f"threads at {s1} seats (KV lengths {l1}: {t1:.2f} s per frame over {n1} frames) and {s2} "
+                       f"seats ({t2:.2f} s over {n2} frames), fitted as {a:.3f} s + {b:.4f} s per seat: a 224-seat "
+                       f"frame takes {t224:.1f} s on this host (not run in full: its 106 GB cache would have to be drawn "
+                       f"on the host first, and this line is bounded to about {seconds:.0f} s of CPU work)")
 
 
 def c1_cpu(torch, reps=20):

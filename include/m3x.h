@@ -383,10 +383,13 @@ int m3x_final_conv(const void* x, long ld_x, void* state, long ld_state, const i
  * [B][H][32][hd] per layer hold the group's K/V at positions < L0. u[b * ld_u + L - 1] is the uniform of level L.
  * xchg: m3x_depth_run_xchg_bytes() of device memory, zeroed before the first run and then left to the kernel;
  * sync: 4 int32, zeroed before the first run (the kernel keeps an epoch in [0], a counter in [1] and sets [2]
- * to 1 if a step's input never arrived, in which case the run's outputs are void). nwg must equal 256 (the
- * workgroups are resident together: one per CU). logits_out (nullable): [31][B][2048] copy of the head outputs.
- * prof (nullable): [256][2048] real-time counter stamps of every workgroup's steps (profiling). probe: a poll of
- * more 16-byte chunks per thread than this first waits on one chunk per thread (fewer: every chunk each round). */
+ * to 1 if a step's input never arrived, in which case the run's outputs are void; the word stays set until the
+ * caller clears it). nwg must equal 256, and the device must hold all 256 workgroups at once (its CUs times the
+ * kernel's workgroups per CU; else M3X_EUNSUPPORTED), since every workgroup waits on others. logits_out
+ * (nullable): [31][B][2048] copy of the head outputs. prof (nullable): [256][2048] real-time counter stamps of
+ * every workgroup's steps (profiling). probe: a poll of more 16-byte chunks per thread than this first waits on one
+ * chunk per thread (fewer: every chunk each round). spin_limit: polling rounds before a wait gives up (0: 2^19;
+ * a test passes a small one to make the waits give up while every workgroup still exits). */
 typedef struct M3xDepthRun {
   int B, L0, L1, layers, H, hd, F, V, act, norm_kind, dtype, nwg;
   float inv_temp;
@@ -421,6 +424,7 @@ typedef struct M3xDepthRun {
   void* logits_out;
   uint64_t* prof;
   int probe;
+  unsigned spin_limit;
 } M3xDepthRun;
 
 /* Bytes of the exchange area and of M3xDepthRun (a binding checks its layout against the latter). */
@@ -431,6 +435,11 @@ size_t m3x_depth_run_args_bytes(void);
  * Replaces the per-level loop of `_compute_fused` for continuing levels (serve/fast_depth.py:150-155 attention
  * over the within-group K/V, :179-190 the layers, :191-198 head, sampling and next prefix). */
 int m3x_depth_run(const M3xDepthRun* args, void* stream);
+
+/* After a run, in stream order: when the run's error word (sync[2]) is set, codes[b][L0 .. L1-1] = -1 for b < B.
+ * A failed run's codes are void; every consumer of codes clamps them, and the host readouts raise on the sentinel.
+ * The reference turns a GPU-side failure into an exception that fails the engine (maya3/engine.py:375-385). */
+int m3x_depth_run_void(const int32_t* sync, int32_t* codes, long ld_codes, int B, int L0, int L1, void* stream);
 
 #ifdef __cplusplus
 }

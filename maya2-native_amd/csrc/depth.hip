@@ -16,8 +16,10 @@
 //     stay coherent across the XCDs' L2s. A consumer polls exactly the words it needs until each carries the
 //     step's tag (the launch's epoch << 12 | the step's number). A word is its own flag, so no barrier, fence or
 //     cache flush is needed, and a word read before its producer wrote it is simply read again.
-// Every wait is bounded: a workgroup whose input does not arrive within SPIN_LIMIT polls sets the error word and
-// skips the rest of the run, so the grid always drains. The grid is at most one workgroup per CU (LDS use
+// Every wait is bounded: a workgroup whose input does not arrive within the run's spin limit (SPIN_LIMIT polls
+// unless the caller sets a smaller one) sets the error word and skips the rest of the run, so the grid always
+// drains; m3x_depth_run_void, launched after the run, then overwrites the run's codes with -1 so every consumer
+// of the codes sees the failure. The grid is at most one workgroup per CU (LDS use
 // forces one per CU), so every workgroup is resident and every wait can be satisfied.
 //
 // Numerics follow the launch path step for step: norms in the add+norm kernels' reduction order (bit-identical
@@ -82,6 +84,7 @@ struct M3xDepthRun {
   void* logits_out;   // optional [31][B][V] copy of every level's head output (tests)
   uint64_t* prof;     // optional [nwg][2048] real-time stamps of each workgroup's steps (profiling)
   int probe;          // a poll with more chunks per thread than this waits on one chunk first
+  unsigned spin_limit;  // polling rounds before a wait gives up (0: SPIN_LIMIT)
 };
 
 namespace dk {
@@ -111,6 +114,7 @@ struct Smem {
   int codes[RB];
   int seat_codes[NPOS];               // a sampler workgroup's codes of its seat, for the prefix rows at the end
   int vote[2][NT / 64];               // wg_all's per-wave votes, alternating buffers
+  unsigned spin;                      // the run's spin limit
 };
 
 // true in every thread iff v is true in every thread: one barrier; the two vote buffers alternate, so a wave that
@@ -158,10 +162,11 @@ constexpr int VOL = SC1;
 
 // One 16-byte chunk per lane (live lanes at byte offset `off`) until both words of every live lane of the wave
 // carry `tag` (a lane that has its chunk polls out of bounds). The chunk's value lands in `out`; false after
-// SPIN_LIMIT rounds.
-__device__ __forceinline__ bool wave_poll1(__amdgpu_buffer_rsrc_t r, int off, bool live, uint32_t tag, u32x4& out) {
+// `limit` rounds.
+__device__ __forceinline__ bool wave_poll1(__amdgpu_buffer_rsrc_t r, int off, bool live, uint32_t tag, u32x4& out,
+                                           unsigned limit) {
   bool got = !live;
-  for (unsigned it = 0; it < SPIN_LIMIT; ++it) {
+  for (unsigned it = 0; it < limit; ++it) {
     M3X_POLL_CLOBBER();
     const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, got ? OOB : off, 0, VOL);
     if (!got && a.y == tag && a.w == tag) {
@@ -173,9 +178,10 @@ __device__ __forceinline__ bool wave_poll1(__amdgpu_buffer_rsrc_t r, int off, bo
   return false;
 }
 // the same for one 8-byte word per lane (payload in out.x)
-__device__ __forceinline__ bool wave_poll1w(__amdgpu_buffer_rsrc_t r, int off, bool live, uint32_t tag, u32x2& out) {
+__device__ __forceinline__ bool wave_poll1w(__amdgpu_buffer_rsrc_t r, int off, bool live, uint32_t tag, u32x2& out,
+                                            unsigned limit) {
   bool got = !live;
-  for (unsigned it = 0; it < SPIN_LIMIT; ++it) {
+  for (unsigned it = 0; it < limit; ++it) {
     M3X_POLL_CLOBBER();
     const u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(r, got ? OOB : off, 0, VOL);
     if (!got && a.y == tag) {
@@ -193,11 +199,12 @@ __device__ __forceinline__ bool wave_poll1w(__amdgpu_buffer_rsrc_t r, int off, b
 // thread, chunk 0 is polled first (a probe: one chunk per thread while the producers still run, which then mostly
 // finds the rest already there); rounds read the chunks still missing, skipping chunks i >= nit by uniform
 // branches and pushing arrived ones out of bounds. Workgroup-collective (every thread calls it); false if any wave
-// gave up after SPIN_LIMIT rounds.
+// gave up after the run's spin limit of rounds (sm.spin).
 template <int N, class U, class Live, class Sink>
 __device__ __forceinline__ bool ll_poll16(Smem& sm, int& vph, __amdgpu_buffer_rsrc_t r, int base, U uoff, int nit,
                                           int probe, Live live, uint32_t tag, Sink sink) {
   static_assert(N <= 64, "chunks per thread");
+  const unsigned limit = __builtin_amdgcn_readfirstlane(sm.spin);
   uint64_t pending = 0;
 #pragma unroll
   for (int i = 0; i < N; ++i)
@@ -206,7 +213,7 @@ __device__ __forceinline__ bool ll_poll16(Smem& sm, int& vph, __amdgpu_buffer_rs
   if (nit > probe) {
     const bool l0 = pending & 1ull;
     u32x4 v0;
-    ok = wave_poll1(r, base * 8 + uoff(0) * 8, l0, tag, v0);
+    ok = wave_poll1(r, base * 8 + uoff(0) * 8, l0, tag, v0, limit);
     if (ok && l0) {
       sink(0, v0.x, v0.z);
       pending &= ~1ull;
@@ -215,7 +222,7 @@ __device__ __forceinline__ bool ll_poll16(Smem& sm, int& vph, __amdgpu_buffer_rs
   {
     for (unsigned it = 0; ok; ++it) {
       if (__builtin_amdgcn_ballot_w64(pending != 0) == 0) break;
-      if (it >= SPIN_LIMIT) {
+      if (it >= limit) {
         ok = false;
         break;
       }
@@ -243,6 +250,7 @@ template <int N, class U, class Live, class Sink>
 __device__ __forceinline__ bool ll_poll8(Smem& sm, int& vph, __amdgpu_buffer_rsrc_t r, int base, U uoff, int nit,
                                          int probe, Live live, uint32_t tag, Sink sink) {
   static_assert(N <= 32, "words per thread");
+  const unsigned limit = __builtin_amdgcn_readfirstlane(sm.spin);
   uint32_t pending = 0;
 #pragma unroll
   for (int i = 0; i < N; ++i)
@@ -251,7 +259,7 @@ __device__ __forceinline__ bool ll_poll8(Smem& sm, int& vph, __amdgpu_buffer_rsr
   if (nit > probe) {
     const bool l0 = pending & 1u;
     u32x2 v0;
-    ok = wave_poll1w(r, base * 8 + uoff(0) * 8, l0, tag, v0);
+    ok = wave_poll1w(r, base * 8 + uoff(0) * 8, l0, tag, v0, limit);
     if (ok && l0) {
       sink(0, v0.x);
       pending &= ~1u;
@@ -259,7 +267,7 @@ __device__ __forceinline__ bool ll_poll8(Smem& sm, int& vph, __amdgpu_buffer_rsr
   }
   for (unsigned it = 0; ok; ++it) {
     if (__builtin_amdgcn_ballot_w64(pending != 0) == 0) break;
-    if (it >= SPIN_LIMIT) {
+    if (it >= limit) {
       ok = false;
       break;
     }
@@ -585,6 +593,7 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
   };
 
   // ---- set-up: zeroed LDS rows, the residual at L0 from the prefix, the pair's K/V history
+  if (tid == 0) sm.spin = a.spin_limit ? a.spin_limit : SPIN_LIMIT;
   if (xm) {
     for (int i = tid; i < RB * XS / 8; i += NT) {
       reinterpret_cast<u16x8*>(&sm.m.x[0][0])[i] = u16x8{};
@@ -857,8 +866,56 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
   }
 }
 
+// After a run: when its error word is set, codes[b][L0 .. L1-1] = -1 for b < B (a failed run's codes are void; the
+// code consumers clamp codes, so -1 reads a valid row, and the host checks see the sentinel). One workgroup.
+__global__ __launch_bounds__(256) void depth_run_void_kernel(const int32_t* __restrict__ sync, int32_t* codes,
+                                                             long ld_codes, int B, int L0, int L1) {
+  if (sync[2] == 0) return;
+  const int n = L1 - L0;
+  for (int i = threadIdx.x; i < B * n; i += blockDim.x) codes[(long)(i / n) * ld_codes + L0 + i % n] = -1;
+}
+
 M3X_API size_t m3x_depth_run_xchg_bytes(void) { return (size_t)X_WORDS * 8; }
 M3X_API size_t m3x_depth_run_args_bytes(void) { return sizeof(M3xDepthRun); }
+
+// Every workgroup of a run waits on others, so the whole grid must be resident at once: the device's CUs times
+// the kernel instance's workgroups per CU must cover nwg (checked once per device and instance).
+template <int DT, int ACT, int HD>
+static int resident_per_cu() {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, depth_run_kernel<DT, ACT, HD>, NT, 0) != hipSuccess) return 0;
+  return n;
+}
+static bool resident_grid_ok(const M3xDepthRun& a) {
+  constexpr int MAXDEV = 64;
+  static int cus[MAXDEV], per[MAXDEV][4];  // 0: not queried yet; -1: query failed
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAXDEV) return false;
+  if (cus[dev] == 0) {
+    int n = 0;
+    cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess ? n : -1;
+  }
+  const int inst = (a.dtype == M3X_F16 ? 2 : 0) + (a.act == 1 ? 1 : 0);
+  if (per[dev][inst] == 0) {
+    int n = 0;
+    if (inst == 0) n = resident_per_cu<M3X_BF16, 1, 128>();
+    else if (inst == 1) n = resident_per_cu<M3X_BF16, 2, 64>();
+    else if (inst == 2) n = resident_per_cu<M3X_F16, 1, 128>();
+    else n = resident_per_cu<M3X_F16, 2, 64>();
+    per[dev][inst] = n > 0 ? n : -1;
+  }
+  return cus[dev] > 0 && per[dev][inst] > 0 && (long)cus[dev] * per[dev][inst] >= a.nwg;
+}
+
+M3X_API int m3x_depth_run_void(const int32_t* sync, int32_t* codes, long ld_codes, int B, int L0, int L1,
+                               void* stream) {
+  if (!sync || !codes) return M3X_ENULL;
+  if (B <= 0 || L0 < 0 || L1 <= L0 || ld_codes < L1) return M3X_EINVAL;
+  hipLaunchKernelGGL(depth_run_void_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, sync, codes, ld_codes, B,
+                     L0, L1);
+  M3X_CHECK_LAUNCH();
+  return M3X_OK;
+}
 
 M3X_API int m3x_depth_run(const M3xDepthRun* args, void* stream) {
   if (!args) return M3X_ENULL;
@@ -870,6 +927,7 @@ M3X_API int m3x_depth_run(const M3xDepthRun* args, void* stream) {
         (a.act == 1 && a.F == 3072 && a.norm_kind == M3X_NORM_LAYER)))
     return M3X_EUNSUPPORTED;
   if (a.nwg != NXM + NOD || a.B * a.H > NXM) return M3X_EINVAL;
+  if (!resident_grid_ok(a)) return M3X_EUNSUPPORTED;
   if (!a.xchg || !a.sync || !a.embed || !a.prefix || !a.codes || (!a.greedy && !a.u) || !a.fw) return M3X_ENULL;
   if (a.norm_kind == M3X_NORM_LAYER && !a.fb) return M3X_ENULL;
   for (int l = 0; l < a.layers; ++l) {

@@ -456,7 +456,9 @@ __device__ __forceinline__ void qk_items(const uint16_t* tile, int LDT, int nb, 
     const int hh = it - r * HPW;
     const int j = nb * HPW + hh;  // head of q|k|v (uniform in the DPP row)
     const int m = min(m0 + r, M - 1);
-    const int ps = min(qk.pos[m], qk.cap - 1);  // the host guarantees pos < cap; the clamp keeps the write in the slot
+    // the host guarantees 0 <= pos < cap (lengths and offsets are non-negative, contexts are checked against the
+    // capacity); the clamp keeps the write inside the slot's rows whatever pos holds
+    const int ps = min(max(qk.pos[m], 0), qk.cap - 1);
     const long slot = qk.slots[m];
     const u16x8 xv = *reinterpret_cast<const u16x8*>(&tile[r * LDT + HD * hh + 8 * t]);
     if (j >= qk.H + qk.KV) {

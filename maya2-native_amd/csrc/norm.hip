@@ -183,7 +183,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_cache_kernel(
   // Every load is issued up front from clamped (valid) addresses, so one memory latency covers them all;
   // only cos/sin wait for the position. Inactive items compute on row 0 and store nothing.
   const int r = active ? row : 0;
-  const int ps = min(pos[r], cap - 1);  // the host guarantees pos < cap; the clamp keeps the cache write in the slot
+  // the host guarantees 0 <= pos < cap; the clamp keeps the cache write inside the slot's rows whatever pos holds
+  const int ps = min(max(pos[r], 0), cap - 1);
   const long slot = slots[r];
   const u16x8 xv = ld16(qkv + (long)r * s_qkv + (long)j * D + 8 * t);
   const u16x8 wv = ld16((j < H ? wq : wk) + 8 * t);

@@ -130,7 +130,8 @@ class FrameStep:
     def readout(self, g, rd, B=None, pcm=None):
         """Starts the tick's one host copy (m3x.tick.TickReadout rd, built with nq = 32 and with_loop = whether
         this frame has a guard): stop codes, cb0, loop codes, the 32 codes of the first B rows, and the seats'
-        PCM rows if given (maya3/engine.py:558-563). B defaults to the staged seats."""
+        PCM rows if given (maya3/engine.py:558-563). B defaults to the staged seats. rd.wait() raises
+        RuntimeError when the depth's persistent run failed this frame (its codes are voided to -1)."""
         bb, cb, dp, codes = g.bufs
         B = len(g.seats) if B is None else int(B)
         if pcm is not None and pcm.shape[0] < B:

@@ -509,7 +509,8 @@ class DepthRunArgs(ctypes.Structure):
         ("prefix", ctypes.c_void_p), ("ld_prefix", ctypes.c_long), ("codes", ctypes.c_void_p),
         ("ld_codes", ctypes.c_long), ("u", ctypes.c_void_p), ("ld_u", ctypes.c_long), ("kd", _P4), ("vd", _P4),
         ("kv_sb", ctypes.c_long), ("kv_sh", ctypes.c_long), ("xchg", ctypes.c_void_p), ("sync", ctypes.c_void_p),
-        ("logits_out", ctypes.c_void_p), ("prof", ctypes.c_void_p), ("probe", ctypes.c_int)]
+        ("logits_out", ctypes.c_void_p), ("prof", ctypes.c_void_p), ("probe", ctypes.c_int),
+        ("spin_limit", ctypes.c_uint)]
 
 
 def depth_run_xchg_bytes() -> int:
@@ -521,6 +522,12 @@ def depth_run(args: DepthRunArgs):
     if ctypes.sizeof(DepthRunArgs) != int(lib().m3x_depth_run_args_bytes()):
         raise RuntimeError("DepthRunArgs does not match the library's M3xDepthRun: rebuild the library")
     check(lib().m3x_depth_run(ctypes.byref(args), _stream()), "depth_run")
+
+
+def depth_run_void(sync, codes, B, L0, L1):
+    """After a run (stream order): codes[:B, L0:L1] = -1 when the run's error word sync[2] is set."""
+    _dev(sync, codes)
+    check(lib().m3x_depth_run_void(_p(sync), _p(codes), codes.stride(0), B, L0, L1, _stream()), "depth_run_void")
 
 
 # ---------------------------------------------------------------- Mimi decode (serve/fast_codec.py)

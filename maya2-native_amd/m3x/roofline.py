@@ -44,8 +44,9 @@ def backbone_step_flops(attended, rows, layers=28, hidden=1024, heads=16, kv_hea
     return 2 * rows * params + 2 * rows * hidden * v0 + layers * decode_attn_flops(attended, heads, head_dim)
 
 
-def depth_frame_bytes(d=1024, ffn=2816, layers=4, n_codes=2048, n_q=32, d_backbone=1024, seats=1):
-    trunk = layers * (3 * d * d + d * d + 3 * ffn * d) * 2
+def depth_frame_bytes(d=1024, ffn=2816, layers=4, n_codes=2048, n_q=32, d_backbone=1024, seats=1, ffn_mats=3):
+    """ffn_mats: 3 for a gated FFN (gate, up, down), 2 for a plain one (the reference's GELU f1, f2)."""
+    trunk = layers * (3 * d * d + d * d + ffn_mats * ffn * d) * 2
     head = n_codes * d * 2
     return (n_q - 1) * (trunk + head) + d * d_backbone * 2 + seats * (n_q - 1) * d * 2
 

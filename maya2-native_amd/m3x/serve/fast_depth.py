@@ -109,6 +109,9 @@ class FastDepth:
         # the persistent run of continuing levels (m3x_depth_run): its exchange area, epoch/error words, and the
         # workgroup count (one per CU)
         self.persistent = True
+        # polling rounds before a persistent run's wait gives up (0: the kernel's default); a run whose wait gives
+        # up sets the error word, and its codes come back as -1 (run_error, clear_run_error)
+        self.spin_limit = 0
         self._run_xchg = torch.zeros(ops.depth_run_xchg_bytes() // 8, dtype=torch.int64, device=dev)
         self._run_sync = torch.zeros(4, dtype=torch.int32, device=dev)
         self._nwg = torch.cuda.get_device_properties(dev).multi_processor_count
@@ -273,6 +276,7 @@ class FastDepth:
                     logits = torch.empty(N_LEVELS - 1, B, self.n_codes, dtype=self.dtype, device=self.device)
                     a.logits_out = logits.data_ptr()
                 ops.depth_run(a)
+                ops.depth_run_void(self._run_sync, b.codes, B, level, end)
                 a.logits_out = None
                 if trace is not None:
                     trace.extend(logits[lv - 1].clone() for lv in range(level, end))
@@ -331,17 +335,23 @@ class FastDepth:
 
     def _run_args(self, b, L0, L1, group):
         """The persistent run's arguments for buffer set b and levels L0 .. L1-1 (built once; the pointers are
-        those of b's static buffers)."""
+        those of b's static buffers). The sampling settings and the spin limit are refreshed on every call, so a
+        run follows the current temp / top_k / greedy like the launch path's levels of the same frame."""
         runs = b.__dict__.setdefault('runs', {})
         key = (L0, L1, group)
-        if key in runs:
-            return runs[key]
+        a = runs.get(key)
+        if a is None:
+            a = runs[key] = self._new_run_args(b, L0, L1, group)
+        a.inv_temp, a.top_k, a.greedy = 1.0 / self.temp, self.top_k, int(self.greedy)
+        a.spin_limit = int(self.spin_limit)
+        return a
+
+    def _new_run_args(self, b, L0, L1, group):
         layers = self.trunks[group]
         a = ops.DepthRunArgs()
         a.B, a.L0, a.L1, a.layers, a.H, a.hd = b.B, L0, L1, len(layers), self.H, self.hd
         a.F, a.V, a.act, a.norm_kind = layers[0].ffn, self.n_codes, layers[0].act, layers[0].n1.kind
         a.dtype, a.nwg, a.probe = ops._DT[self.dtype], self._nwg, self.POLL_PROBE
-        a.inv_temp, a.top_k, a.greedy = 1.0 / self.temp, self.top_k, int(self.greedy)
         p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
         for l, L in enumerate(layers):
             a.eps1[l], a.eps2[l] = L.n1.eps, L.n2.eps
@@ -360,13 +370,24 @@ class FastDepth:
         a.u, a.ld_u = p(b.u), b.u.stride(0)
         a.kv_sb, a.kv_sh = b.kd[0].stride(0), b.kd[0].stride(1)
         a.xchg, a.sync = p(self._run_xchg), p(self._run_sync)
-        runs[key] = a
         return a
 
     def run_error(self):
-        """True when a persistent run since construction (or the last clear) lost a step's input and voided its
-        outputs (the kernel's bounded waits ran out)."""
+        """True when a persistent run since construction (or the last clear) lost a step's input (its bounded waits
+        ran out): that run's codes came back as -1 and the frame is void. Synchronises with the device."""
         return bool(self._run_sync[2].item())
+
+    def clear_run_error(self):
+        """Reset the error word (stream-ordered), e.g. after the caller has failed the frame's requests."""
+        self._run_sync[2].zero_()
+
+    def _check_run(self, b):
+        """Raise when buffer set b's frame ran a persistent run and a run since the last clear failed (the
+        reference fails the engine on a GPU-side error, maya3/engine.py:375-385). Synchronises with the device,
+        only for buffer sets that run persistent levels (up to PERSISTENT_SEATS seats)."""
+        if b.__dict__.get('runs') and self.run_error():
+            raise RuntimeError('FastDepth: a persistent depth run lost a step\'s input (its bounded waits ran out); '
+                               'the frame\'s codes are void (-1). clear_run_error() resets the error word')
 
     def _compute(self, slots_idx, h, cb0):
         """Eager frame body over fresh buffers (the reference's tests call `_fn(slots_idx, h, cb0)`)."""
@@ -375,6 +396,7 @@ class FastDepth:
         b.h.copy_(h)
         b.codes[:, 0].copy_(cb0)
         codes, fb = self.run(b)
+        self._check_run(b)
         return codes.long(), fb
 
     # ---------------------------------------------------------------- graphs
@@ -410,4 +432,5 @@ class FastDepth:
         g.bufs.h[:B].copy_(h)
         g.bufs.codes[:B, 0].copy_(cb0)
         g.graph.replay()
+        self._check_run(g.bufs)
         return g.bufs.codes[:B].long(), g.bufs.feedback[:B].clone()

@@ -54,10 +54,31 @@ def _normal(g, shape, std, device, dtype):
                                                                                           dtype=dtype)
 
 
+def _norm_weights(g, norms, affine, device):
+    """Draw the weights of `norms` (Norm holders, in order) from generator g: "normal:s" -> 1 + N(0, s),
+    "lognormal:s" -> exp(N(0, s)) (at s = 0.8 a 1024-wide vector spans about 0.1x to 20x, like trained
+    Qwen3 norm weights). Drawn in fp32, then cast to each holder's dtype; a LayerNorm holder also gets a bias
+    N(0, s)."""
+    kind, s = affine.split(":")
+    s = float(s)
+    if kind not in ("normal", "lognormal"):
+        raise ValueError(f"affine kind {kind!r}")
+    for n in norms:
+        d, dt = n.weight.shape[0], n.weight.dtype
+        z = _normal(g, (d,), s, "cpu", torch.float32)
+        w = 1 + z if kind == "normal" else torch.exp(z)
+        n.weight = w.to(device=device, dtype=dt)
+        if n.bias is not None:
+            n.bias = _normal(g, (d,), s, device, dt)
+
+
 def qwen3_backbone(layers=28, hidden=1024, heads=16, kv_heads=8, head_dim=128, inter=3072, v0=2048, theta=1e6,
-                   eps=1e-6, seed=0, device="cpu", dtype=torch.bfloat16, std=0.02, gen="cpu"):
-    """Qwen3-0.6B-shaped backbone (gen: the device of the generator; "cpu" reproduces across hosts). Per layer, in order: q [H*D, hid], k [KV*D, hid], v [KV*D, hid], o [hid, H*D],
-    gate [I, hid], up [I, hid], down [hid, I], all N(0, std); RMSNorm weights 1 (HF init). Then cb0 head [v0, hid]."""
+                   eps=1e-6, seed=0, device="cpu", dtype=torch.bfloat16, std=0.02, gen="cpu", affine=None):
+    """Qwen3-0.6B-shaped backbone (gen: the device of the generator; "cpu" reproduces across hosts). Per layer, in
+    order: q [H*D, hid], k [KV*D, hid], v [KV*D, hid], o [hid, H*D], gate [I, hid], up [I, hid], down [hid, I], all
+    N(0, std); then cb0 head [v0, hid]. RMSNorm weights 1 (HF init) when affine is None; otherwise ("normal:s" or
+    "lognormal:s", see _norm_weights) drawn after everything else, per layer input_layernorm,
+    post_attention_layernorm, q_norm, k_norm, then the final norm, so the other weights do not change."""
     g = torch.Generator(device=gen).manual_seed(seed)
     ones = lambda n: torch.ones(n, dtype=dtype, device=device)  # noqa: E731
     L = []
@@ -78,6 +99,10 @@ def qwen3_backbone(layers=28, hidden=1024, heads=16, kv_heads=8, head_dim=128, i
                           hidden_size=hidden, rms_norm_eps=eps, intermediate_size=inter, num_hidden_layers=layers,
                           rope_theta=theta)
     model = SimpleNamespace(layers=L, norm=Norm(ones(hidden), eps), rotary_emb=Rotary(head_dim, theta))
+    if affine:
+        _norm_weights(g, [n for layer in L for n in (layer.input_layernorm, layer.post_attention_layernorm,
+                                                     layer.self_attn.q_norm, layer.self_attn.k_norm)]
+                      + [model.norm], affine, device)
     params = [t for layer in L for t in (layer.self_attn.q_proj.weight, layer.self_attn.k_proj.weight)]
     model.parameters = lambda: iter(params)
     lm = SimpleNamespace(model=model, config=cfg)
@@ -85,11 +110,13 @@ def qwen3_backbone(layers=28, hidden=1024, heads=16, kv_heads=8, head_dim=128, i
 
 
 def swiglu_depth(layers=4, d=1024, heads=8, ffn=2816, n_q=32, n_codes=2048, d_backbone=1024, seed=1,
-                 device="cpu", dtype=torch.bfloat16, std=0.02, eps=1e-6, gen="cpu"):
+                 device="cpu", dtype=torch.bfloat16, std=0.02, eps=1e-6, gen="cpu", affine=None):
     """Depth transformer of the 4-layer SwiGLU/RMSNorm trunk shared by every level (one weight group).
     Draw order: in_proj [d, d_backbone], level0 [d], embed [n_q-1, n_codes, d] (per-codebook table, level
     embedding folded in), per layer qkv [3d, d], o [d, d], gate|up [2*ffn, d], down [d, ffn]; heads
-    [n_q-1, n_codes, d]; then the backbone-side feedback table [n_q*n_codes, d_backbone]. Norm weights 1."""
+    [n_q-1, n_codes, d]; then the backbone-side feedback table [n_q*n_codes, d_backbone]. Norm weights 1 when
+    affine is None; otherwise ("normal:s" / "lognormal:s", see _norm_weights) drawn after everything else, per
+    layer n1, n2, then the final norm, then the feedback RMSNorm."""
     g = torch.Generator(device=gen).manual_seed(seed)
     ones = lambda n: torch.ones(n, dtype=dtype, device=device)  # noqa: E731
     in_proj = Lin(_normal(g, (d, d_backbone), std, device, dtype))
@@ -110,7 +137,17 @@ def swiglu_depth(layers=4, d=1024, heads=8, ffn=2816, n_q=32, n_codes=2048, d_ba
     audio_in = SimpleNamespace(n_q=n_q, n_codes=n_codes, table=Lin(table),
                                norm=Norm(torch.ones(d_backbone, dtype=dtype, device=device),
                                          torch.finfo(dtype).eps))
+    if affine:
+        _norm_weights(g, [n for blk in blocks for n in (blk.n1, blk.n2)] + [depth.norm, audio_in.norm], affine,
+                      device)
     return SimpleNamespace(depth=depth, audio_in=audio_in)
+
+
+# the norm-weight draws of the end-to-end tests and the benchmark: every RMSNorm / q_norm / k_norm weight
+# 1 + N(0, 0.1), so that a swapped, dropped or misplaced norm weight changes the outputs
+AFFINE = "normal:0.1"
+# a wide spread (about 0.1x .. 20x over a 1024-wide vector), like trained norm weights
+AFFINE_WIDE = "lognormal:0.8"
 
 
 REFERENCE_GROUP_OF_LEVEL = [None] + list(range(8)) + [8] * 8 + [9] * 8 + [10] * 7

@@ -48,7 +48,9 @@ class TickReadout:
         self.B = B
 
     def wait(self):
-        """Waits for the copy; returns dict(stop, cb0, loop, codes, pcm) numpy views of the pinned buffer."""
+        """Waits for the copy; returns dict(stop, cb0, loop, codes, pcm) numpy views of the pinned buffer. Raises
+        RuntimeError when a carried code is negative: a depth run that lost a step's input voids its codes to -1
+        (m3x_depth_run_void), and the reference fails the engine on a GPU-side error (maya3/engine.py:375-385)."""
         self.evt.synchronize()
         hv = self.host[:self.B].numpy()
         col = 2
@@ -60,6 +62,10 @@ class TickReadout:
             w = (self.nq + 1) // 2
             out["codes"] = hv[:, col:col + w].view(np.int32)[:, :self.nq]
             col += w
+            bad = np.flatnonzero((out["codes"] < 0).any(axis=1))
+            if bad.size:
+                raise RuntimeError(f"tick readout: the depth codes of seat rows {bad.tolist()} are void (a persistent "
+                                   "depth run lost a step's input)")
         if self.frame:
             out["pcm"] = hv[:, col:col + (self.frame + 3) // 4].view(np.int16)[:, :self.frame]
         return out

@@ -1,4 +1,5 @@
 """Shared test helpers (bit views and the bf16 parity bar)."""
+import os
 
 
 def bf16_bits(t):
@@ -35,14 +36,17 @@ def rel_l2(a, b):
 
 
 MAX_ABS = 2e-2  # the per-element bar for logits and hidden states, bf16 tolerance
+# the kernel's relative L2 error against the fp32 truth may exceed the bf16 oracle's own by this factor (measured on
+# MI355X: 0.73-1.07x over the 182 checks of the GPU suite), so a 25 % precision loss fails
+REL_FLOOR_FACTOR = 1.25
 
 
 def floor_check(got, ref16, truth, min_cos=0.9995):
     """Step-level parity against the bf16 eager oracle with an fp32 truth (the fp32 evaluation of the same math on
     the same bf16 values), following the reference's fused-vs-unfused test (maya3/tests/test_backbone_fused.py:
     12-46):
-      - relative L2 error against the truth within twice the oracle's own (the bf16 noise floor) or 1e-3;
-      - cosine to the oracle >= min_cos;
+      - relative L2 error against the truth within 1.25 times the oracle's own (the bf16 noise floor) or 1e-3;
+      - cosine to the oracle >= min_cos (lowered to 1 - 1.3 floor^2 when the floor itself exceeds ~2 %);
       - max-abs error against the truth within max(2e-2, twice the oracle's own max-abs error). Where two bf16
         paths both sit at the noise floor, 2e-2 alone cannot hold over many layers: HF transformers' own bf16
         Qwen3 forward is 0.034 max-abs off its fp32 evaluation after 4 layers. The returned info carries every
@@ -56,10 +60,16 @@ def floor_check(got, ref16, truth, min_cos=0.9995):
     cos = torch.nn.functional.cosine_similarity(a[None], b[None]).item()
     max_abs = (a - t).abs().max().item()
     oracle_max_abs = (b - t).abs().max().item()
-    info = dict(rel_err=err, floor=floor, cos=cos, max_abs_vs_oracle=(a - b).abs().max().item(),
+    # the cosine two bf16 paths can keep: each sits ~floor (relative L2) off the truth with independent rounding,
+    # so their distance is ~sqrt(1 + 1.25^2) floor and the cosine ~1 - 1.3 floor^2. At one step the floor stays
+    # below 2 % and the bar is min_cos; over frames that feed their own K/V and feedback back, the floor grows.
+    cos_bar = min(min_cos, 1 - 1.3 * floor ** 2)
+    info = dict(rel_err=err, floor=floor, cos=cos, cos_bar=cos_bar, max_abs_vs_oracle=(a - b).abs().max().item(),
                 max_abs_vs_truth=max_abs, oracle_max_abs_vs_truth=oracle_max_abs,
                 max_abs_bar=max(MAX_ABS, 2 * oracle_max_abs))
-    ok = err <= max(2 * floor, 1e-3) and cos >= min_cos and max_abs <= info["max_abs_bar"]
+    ok = err <= max(REL_FLOOR_FACTOR * floor, 1e-3) and cos >= cos_bar and max_abs <= info["max_abs_bar"]
+    # every check leaves one line in the test log (pytest -s), named by the running test
+    report("floor " + os.environ.get("PYTEST_CURRENT_TEST", "").split(" ")[0] + (" PASS" if ok else " FAIL"), info)
     return ok, info
 
 

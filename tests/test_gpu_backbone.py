@@ -2,7 +2,7 @@
 import pytest
 import torch
 
-from helpers import close, convert, floor_check
+from helpers import close, convert, floor_check, report
 from m3x import synth
 from oracle import torch_oracle as O
 
@@ -12,10 +12,10 @@ LAYERS, S, CAP = 3, 6, 512
 PREFIX = [0, 1, 37, 200, 300, 0]
 
 
-def _setup(gpu, use_graphs=True):
+def _setup(gpu, use_graphs=True, affine=synth.AFFINE):
     from m3x.serve.fast_backbone import StaticBackbone
-    bb_g = synth.qwen3_backbone(layers=LAYERS, seed=21, device=gpu)
-    bb_c = synth.qwen3_backbone(layers=LAYERS, seed=21, device="cpu")
+    bb_g = synth.qwen3_backbone(layers=LAYERS, seed=21, device=gpu, affine=affine)
+    bb_c = synth.qwen3_backbone(layers=LAYERS, seed=21, device="cpu", affine=affine)
     sb = StaticBackbone(bb_g, S, capacity=CAP, batch_buckets=(1, 2, 4, 8, 64), ctx_buckets=(256, 512),
                         attention="triton", fuse_rope=True, use_graphs=use_graphs)
     g = torch.Generator().manual_seed(22)
@@ -43,8 +43,11 @@ def _truth_step(T, slots, x, offset=None):
                            offset=offset)
 
 
-def test_step_matches_oracle(gpu):
-    sb, bb_c, kc, vc, lengths, cos, sin, T = _setup(gpu)
+@pytest.mark.parametrize("affine", [synth.AFFINE, synth.AFFINE_WIDE])
+def test_step_matches_oracle(gpu, affine):
+    """Three decode steps with non-unit norm weights (1 + N(0, 0.1), and a log-normal spread of about 0.1x to 20x
+    that tests the folded input/post-attention norms and the q/k norms on weights like trained ones)."""
+    sb, bb_c, kc, vc, lengths, cos, sin, T = _setup(gpu, affine=affine)
     g = torch.Generator().manual_seed(23)
     slots = [0, 2, 3, 4]
     for t in range(3):
@@ -53,6 +56,7 @@ def test_step_matches_oracle(gpu):
         ref = O.backbone_step(bb_c, kc, vc, lengths, torch.tensor(slots), x, cos, sin)
         truth = _truth_step(T, torch.tensor(slots), x)
         ok, info = floor_check(out, ref, truth)
+        report(f"backbone step {t} ({affine})", info)
         assert ok, (t, info)
     assert sb.lengths.cpu().tolist() == lengths.tolist() and sb.lengths_cpu == lengths.tolist()
     assert sb.lengths[S].item() == 0

@@ -36,8 +36,8 @@ sys.path.insert(0, os.path.join(HERE, "golden"))
 def models(gpu):
     """The 28-layer backbone and the 4-layer SwiGLU depth of the benchmark (seeded on the GPU), with CPU copies
     for the oracle."""
-    bb = synth.qwen3_backbone(layers=28, seed=0, device=gpu, gen="cuda")
-    dm = synth.swiglu_depth(seed=1, device=gpu, gen="cuda")
+    bb = synth.qwen3_backbone(layers=28, seed=0, device=gpu, gen="cuda", affine=synth.AFFINE)
+    dm = synth.swiglu_depth(seed=1, device=gpu, gen="cuda", affine=synth.AFFINE)
     yield bb, dm, to_device(bb, "cpu"), to_device(dm, "cpu")
     gc.collect()
     torch.cuda.empty_cache()
@@ -107,12 +107,13 @@ class _Oracle:
         self.cos, self.sin = O.rope_tables(128, 1e6, ctx, torch.bfloat16)
         self.c32, self.s32 = O.rope_tables(128, 1e6, ctx, torch.float32)
 
-    def step(self, rows_slot, x, offset=None):
-        """(bf16 output, fp32 truth) of rows at compact slots rows_slot with inputs x [rows, hidden]."""
+    def step(self, rows_slot, x, offset=None, x_truth=None):
+        """(bf16 output, fp32 truth) of rows at compact slots rows_slot with inputs x [rows, hidden] (the truth's
+        own fp32 inputs x_truth if given)."""
         out16 = O.backbone_step(self.bb16, self.kc16, self.vc16, self.l16, rows_slot, x, self.cos, self.sin,
                                 offset=offset)
-        truth = O.backbone_step(self.bb32, self.kc32, self.vc32, self.l32, rows_slot, x.float(), self.c32, self.s32,
-                                offset=offset)
+        truth = O.backbone_step(self.bb32, self.kc32, self.vc32, self.l32, rows_slot,
+                                x.float() if x_truth is None else x_truth, self.c32, self.s32, offset=offset)
         return out16, truth
 
 
@@ -148,9 +149,9 @@ def test_c1_layer_vs_hf_golden(gpu):
     from make_golden import c1_inputs
     gold = np.load(os.path.join(HERE, "golden", "c1_qwen3_layer.npz"))
     _, k, v, x = c1_inputs()
-    # the fixture's weights (the same seeded draws) rounded to bf16
-    bb16 = synth.qwen3_backbone(layers=1, seed=0, dtype=torch.bfloat16)
-    sb = StaticBackbone(synth.qwen3_backbone(layers=1, seed=0, dtype=torch.bfloat16, device=gpu), 1, capacity=512,
+    # the fixture's weights (the same seeded draws, wide-spread norm weights included) rounded to bf16
+    bb16 = c1_inputs(torch.bfloat16)[0]
+    sb = StaticBackbone(c1_inputs(torch.bfloat16, gpu)[0], 1, capacity=512,
                         batch_buckets=(1,), ctx_buckets=(512,), attention="triton", fuse_rope=True)
     sb.load_prefix(0, [(k.to(torch.bfloat16).to(gpu), v.to(torch.bfloat16).to(gpu))], 256)
     out = sb.step([0], x.to(torch.bfloat16).to(gpu))[0]
@@ -328,26 +329,9 @@ def test_c5_frame_224_seats(gpu, models):
     uniforms; an eager rerun of the depth on the graph's own inputs gives the graph's codes, and all 224 x 31
     depth codes equal the oracle sampler on its traced logits; the sampled seats' depth logits against the
     teacher-forced oracle; the ring holds the frame's codes; K/V change only at each seat's position."""
-    from m3x.cb0 import Cb0Sampler
-    from m3x.frame import FrameStep
-    from m3x.serve.fast_backbone import StaticBackbone
-    from m3x.serve.fast_depth import FastDepth
     bb, dm, bb_c, dm_c = models
     B = 224
-    sb = StaticBackbone(bb, B, capacity=CAP, batch_buckets=(B,), ctx_buckets=(CAP,), attention="triton",
-                        fuse_rope=True)
-    _fill_cache(sb, 505)
-    lengths = synth.c5_lengths(B).clamp_max(CAP - 1)
-    _set_lengths(sb, lengths)
-    cb = Cb0Sampler(bb.cb0_head.weight, B, temp=0.9, top_k=50, rep=0.0)
-    for s in range(B):
-        cb.bind(s, seed=1 + s)
-    fd = FastDepth(dm, B, dtype=torch.bfloat16, temp=0.9, top_k=50, batch_buckets=(B,), fused=True)
-    fd.row_seed.copy_(torch.arange(B + 1, dtype=torch.int32, device=gpu) * 69069 + 1)
-    fs = FrameStep(sb, cb, fd, ring_depth=4)
-    fs.feedback.normal_(generator=torch.Generator(device=gpu).manual_seed(506))
-    g = fs.capture(B, CAP)
-    fs.set_slots(g, list(range(B)))
+    sb, cb, fd, fs, g, lengths = _c5_frame(gpu, bb, dm, B)
     order = torch.argsort(lengths)
     sample = [int(order[0]), int(order[B // 2]), int(order[-1])]
     kc, vc = _sample_cache(sb, sample, int(lengths[sample].max()) + 1)
@@ -371,9 +355,50 @@ def test_c5_frame_224_seats(gpu, models):
     # cb0 of every seat
     assert np.array_equal(cbuf.cb0.cpu().numpy(), _cb0_exact(cbuf.logits, cbuf.u[:, 0].cpu(), 0.9, 50))
     assert torch.equal(codes_c[:, 0], cbuf.cb0.cpu())
-    # depth: eager rerun with traced logits
+    trace, u = _depth_rerun_exact(fd, bbuf, codes, ctr_depth)
+    h_s = bbuf.out[sample].cpu()
+    logits = torch.stack([t[sample].cpu() for t in trace], 1)
+    _, ref_l = O.depth_frame(dm_c, h_s, codes_c[sample, 0], u[sample], 0.9, 50, forced=codes_c[sample])
+    _, tru_l = O.depth_frame(convert(dm_c, torch.float32), h_s.float(), codes_c[sample, 0], u[sample], 0.9, 50,
+                             forced=codes_c[sample], dt=torch.float32)
+    ok, info = floor_check(logits, ref_l, tru_l)
+    report("C5 depth logits, 3 sampled seats x 31 levels", info)
+    assert ok, info
+    del fs, sb, cb, fd, g, before
+    _free()
+
+
+def _c5_frame(gpu, bb, dm, B):
+    """The C5 frame at B seats: cache N(0, 1), lengths Poisson(2048) capped, cb0 and depth streams seeded,
+    random feedback rows, the frame graph captured with every seat staged."""
+    from m3x.cb0 import Cb0Sampler
+    from m3x.frame import FrameStep
+    from m3x.serve.fast_backbone import StaticBackbone
+    from m3x.serve.fast_depth import FastDepth
+    sb = StaticBackbone(bb, B, capacity=CAP, batch_buckets=(B,), ctx_buckets=(CAP,), attention="triton",
+                        fuse_rope=True)
+    _fill_cache(sb, 505)
+    lengths = synth.c5_lengths(B).clamp_max(CAP - 1)
+    _set_lengths(sb, lengths)
+    cb = Cb0Sampler(bb.cb0_head.weight, B, temp=0.9, top_k=50, rep=0.0)
+    for s in range(B):
+        cb.bind(s, seed=1 + s)
+    fd = FastDepth(dm, B, dtype=torch.bfloat16, temp=0.9, top_k=50, batch_buckets=(B,), fused=True)
+    fd.row_seed.copy_(torch.arange(B + 1, dtype=torch.int32, device=gpu) * 69069 + 1)
+    fs = FrameStep(sb, cb, fd, ring_depth=4)
+    fs.feedback.normal_(generator=torch.Generator(device=gpu).manual_seed(506))
+    g = fs.capture(B, CAP)
+    fs.set_slots(g, list(range(B)))
+    return sb, cb, fd, fs, g, lengths
+
+
+def _depth_rerun_exact(fd, bbuf, codes, ctr_before):
+    """Rerun the depth of the frame just replayed, eagerly, on the graph's own inputs (the depth streams put back
+    to ctr_before) with every level's logits traced: it must give the graph's codes, and every code of every seat
+    must equal the C oracle sampler on those logits and the seat's uniforms. Returns (trace, uniforms)."""
+    B = codes.shape[0]
     now = fd.row_ctr.clone()
-    fd.row_ctr.copy_(ctr_depth)
+    fd.row_ctr.copy_(ctr_before)
     d2 = fd.make_buffers(B)
     d2.slots.copy_(bbuf.slots)
     d2.h.copy_(bbuf.out)
@@ -383,16 +408,64 @@ def test_c5_frame_224_seats(gpu, models):
     torch.cuda.synchronize()
     assert torch.equal(d2.codes, codes) and torch.equal(fd.row_ctr, now)
     u = d2.u.cpu()
+    codes_c = codes.cpu().long()
     for lv in range(1, 32):
         ref = C.topk_sample_rows(bf16_bits(trace[lv - 1]), 1 / 0.9, 50, u[:, lv - 1].numpy())
         assert np.array_equal(codes_c[:, lv].numpy(), ref), lv
+    return trace, u
+
+
+FRAMES = 8
+
+
+@torch.inference_mode()
+def test_c5_frames_through_the_feedback_loop(gpu, models):
+    """C5 over FRAMES consecutive replays of the frame graph, each frame's codes feeding the next frame's input
+    through the feedback embedding, as the engine's ticks run (the multi-step check of
+    maya3/tests/test_backbone_fused.py:12-46 at full size). Three sampled seats run the same frames on the oracle,
+    which keeps its own K/V history and takes the GPU's codes (teacher forcing): every frame, their backbone
+    rows and the feedback rows the graph wrote are checked against it at the bf16 floor, so drift through the
+    cache and the feedback loop shows; every frame, cb0 and all 224 x 31 depth codes are bit-exact against the
+    oracle sampler on the frame's own logits and uniforms, the ring holds the frame's codes, and each seat's
+    length moves by one. The last frame's depth logits of the sampled seats are checked against the oracle."""
+    bb, dm, bb_c, dm_c = models
+    B = 224
+    sb, cb, fd, fs, g, lengths = _c5_frame(gpu, bb, dm, B)
+    order = torch.argsort(lengths)
+    sample = [int(order[0]), int(order[B // 2]), int(order[-1])]
+    kc, vc = _sample_cache(sb, sample, int(lengths[sample].max()) + 1 + FRAMES)
+    orc = _Oracle(bb_c, kc, vc, torch.cat([lengths[sample], torch.tensor([0])]))
+    audio32 = convert(dm_c.audio_in, torch.float32)
+    x16 = fs.feedback[sample].cpu()
+    x32 = x16.float()
+    bbuf, cbuf, dbuf, codes = g.bufs
+    for t in range(FRAMES):
+        ctr_depth = fd.row_ctr.clone()
+        fs.replay(g)
+        torch.cuda.synchronize()
+        assert sb.lengths[:B].cpu().tolist() == (lengths + t + 1).tolist() == sb.lengths_cpu[:B]
+        codes_c = codes.cpu().long()
+        assert torch.equal(fs.ring[t % 4].cpu(), codes.cpu()) and fs.ring_head.item() == t + 1
+        out16, truth = orc.step(torch.arange(3), x16, x_truth=x32)
+        ok, info = floor_check(bbuf.out[sample], out16, truth)
+        report(f"C5 frame {t}: backbone hidden, 3 sampled seats", info)
+        assert ok, (t, info)
+        assert np.array_equal(cbuf.cb0.cpu().numpy(), _cb0_exact(cbuf.logits, cbuf.u[:, 0].cpu(), 0.9, 50)), t
+        assert torch.equal(codes_c[:, 0], cbuf.cb0.cpu())
+        trace, u = _depth_rerun_exact(fd, bbuf, codes, ctr_depth)
+        # the next input: the feedback of this frame's codes, oracle (bf16) and truth (fp32) chains
+        x16 = O.feedback(dm_c.audio_in, codes_c[sample])
+        x32 = O.feedback(audio32, codes_c[sample]).float()
+        ok, info = floor_check(fs.feedback[sample], x16, x32)
+        report(f"C5 frame {t}: feedback rows, 3 sampled seats", info)
+        assert ok, (t, info)
     h_s = bbuf.out[sample].cpu()
-    logits = torch.stack([t[sample].cpu() for t in trace], 1)
+    logits = torch.stack([tr[sample].cpu() for tr in trace], 1)
     _, ref_l = O.depth_frame(dm_c, h_s, codes_c[sample, 0], u[sample], 0.9, 50, forced=codes_c[sample])
     _, tru_l = O.depth_frame(convert(dm_c, torch.float32), h_s.float(), codes_c[sample, 0], u[sample], 0.9, 50,
                              forced=codes_c[sample], dt=torch.float32)
     ok, info = floor_check(logits, ref_l, tru_l)
-    report("C5 depth logits, 3 sampled seats x 31 levels", info)
+    report(f"C5 frame {FRAMES - 1}: depth logits, 3 sampled seats x 31 levels", info)
     assert ok, info
-    del fs, sb, cb, fd, g, d2, before
+    del fs, sb, cb, fd, g
     _free()

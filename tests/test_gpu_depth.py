@@ -57,8 +57,10 @@ def _check(fd, model_c, h, cb0, gpu, dt, temp, top_k, cross=None, logit_tol=None
     _, truth = O.depth_frame(m32, h.float(), cb0, u, temp, top_k, forced=codes,
                              cross=None if cross is None else cross.float(), dt=torch.float32)
     ok, info = floor_check(logits, ref_logits, truth)
+    report(f"depth logits {dt}, {B} seats x 31 levels", info)
     assert ok, info
     ok, info = close(fb, O.feedback(model_c.audio_in, codes).float())
+    report(f"depth feedback {dt}", info)
     assert ok, info
     return codes, fb
 
@@ -83,10 +85,14 @@ def _check_f32(model_c, h, cb0, u, temp, top_k, codes, fb, logits, cross):
     return codes, fb
 
 
-def test_swiglu_depth_frame(gpu):
+@pytest.mark.parametrize("affine", [synth.AFFINE, synth.AFFINE_WIDE])
+def test_swiglu_depth_frame(gpu, affine):
+    """The SwiGLU/RMSNorm trunk with non-unit norm weights: 1 + N(0, 0.1), and a wide log-normal spread
+    (about 0.1x to 20x) that tests the folded norm's rounding (the norm weight multiplied into the packed
+    weight, then rounded) on weights like trained ones."""
     from m3x.serve.fast_depth import FastDepth
-    model_g = synth.swiglu_depth(seed=31, device=gpu)
-    model_c = synth.swiglu_depth(seed=31, device="cpu")
+    model_g = synth.swiglu_depth(seed=31, device=gpu, affine=affine)
+    model_c = synth.swiglu_depth(seed=31, device="cpu", affine=affine)
     fd = FastDepth(model_g, 8, dtype=torch.bfloat16, temp=0.9, top_k=50, batch_buckets=(B,), fused=True)
     g = torch.Generator().manual_seed(32)
     h = torch.randn(B, 1024, generator=g).to(torch.bfloat16)
@@ -99,7 +105,7 @@ def test_depthv2_geometry_fp16_with_speaker(gpu):
     incremental levels, per-slot speaker constant (set_speaker), fp16."""
     from m3x.serve.fast_depth import FastDepth
     gol = [None] + [0] * 3 + [1] * 8 + [2] * 20
-    mk = lambda dev: synth.depthv2_like(group_of_level=gol, seed=41, device=dev)  # noqa: E731
+    mk = lambda dev: synth.depthv2_like(group_of_level=gol, seed=41, device=dev, affine_std=0.1)  # noqa: E731
     model_g, model_c = mk(gpu), mk("cpu")
     fd = FastDepth(model_g, 8, dtype=torch.float16, temp=0.7, top_k=64, batch_buckets=(B,), fused=True)
     g = torch.Generator().manual_seed(42)
@@ -122,8 +128,8 @@ def test_swiglu_depth_frame_fp32(gpu):
     """FastDepth(dtype=torch.float32): the engine's depth_dtype="fp32" (maya3/engine.py:53,192-199) and the
     reference's own fp32 FastDepth (maya3/tests/test_depth_fused.py:30-31). Launch path, fp32 kernels throughout."""
     from m3x.serve.fast_depth import FastDepth
-    model_g = convert(synth.swiglu_depth(seed=33, device=gpu), torch.float32)
-    model_c = convert(synth.swiglu_depth(seed=33, device="cpu"), torch.float32)
+    model_g = convert(synth.swiglu_depth(seed=33, device=gpu, affine=synth.AFFINE), torch.float32)
+    model_c = convert(synth.swiglu_depth(seed=33, device="cpu", affine=synth.AFFINE), torch.float32)
     fd = FastDepth(model_g, 8, dtype=torch.float32, temp=0.9, top_k=50, batch_buckets=(B,), fused=True)
     assert not fd._persistent_ok(B, 0)
     g = torch.Generator().manual_seed(34)
@@ -156,7 +162,7 @@ def test_depthv2_geometry_fp32_with_speaker(gpu):
 
 def test_graph_replay_equals_eager(gpu):
     from m3x.serve.fast_depth import FastDepth
-    model_g = synth.swiglu_depth(seed=51, device=gpu)
+    model_g = synth.swiglu_depth(seed=51, device=gpu, affine=synth.AFFINE)
     fd = FastDepth(model_g, 8, dtype=torch.bfloat16, temp=0.9, top_k=50, batch_buckets=(2, 4), fused=True)
     fd.row_seed.copy_(torch.arange(9, dtype=torch.int32, device=gpu) * 7919 + 1)
     g = torch.Generator().manual_seed(52)

@@ -48,8 +48,8 @@ def test_swiglu_run_matches_oracle_and_launch_path(gpu, B):
     run's own logits and uniforms, the logits sit at the bf16 floor of the teacher-forced oracle, the feedback
     matches, no step's input went missing, and the logits agree with the launch path's within the same floor."""
     from m3x.serve.fast_depth import FastDepth
-    model_g = synth.swiglu_depth(seed=611, device=gpu)
-    model_c = synth.swiglu_depth(seed=611, device="cpu")
+    model_g = synth.swiglu_depth(seed=611, device=gpu, affine=synth.AFFINE)
+    model_c = synth.swiglu_depth(seed=611, device="cpu", affine=synth.AFFINE)
     fd = FastDepth(model_g, 20, dtype=torch.bfloat16, temp=0.9, top_k=50, batch_buckets=(B,))
     fd.PERSISTENT_SEATS = 16  # the kernel's own limit (serving switches to the launch path above 8 seats)
     fd.row_seed.copy_(torch.arange(21, dtype=torch.int32, device=gpu) * 7777 + 3)
@@ -102,7 +102,7 @@ def test_run_graph_replays_equal_eager(gpu):
     """Graph replays of a frame with a persistent run (the kernel's epoch moves every launch, so the LL tags of
     one replay never match another's) equal eager runs bit for bit, replay after replay."""
     from m3x.serve.fast_depth import FastDepth
-    model_g = synth.swiglu_depth(seed=631, device=gpu)
+    model_g = synth.swiglu_depth(seed=631, device=gpu, affine=synth.AFFINE)
     fd = FastDepth(model_g, 8, dtype=torch.bfloat16, temp=0.9, top_k=50, batch_buckets=(4,))
     fd.row_seed.copy_(torch.arange(9, dtype=torch.int32, device=gpu) * 7919 + 1)
     g = torch.Generator().manual_seed(632)
@@ -118,3 +118,53 @@ def test_run_graph_replays_equal_eager(gpu):
     for (c, f), (ce, fe) in zip(outs, eager):
         assert torch.equal(c, ce) and torch.equal(f, fe)
     assert not torch.equal(outs[0][0], outs[1][0])
+
+
+def test_run_failure_is_surfaced(gpu):
+    """A run whose bounded waits give up, forced from the host with a spin limit of one polling round (every
+    workgroup still exits normally: a failed wait skips the rest of the run), sets the error word; the run's
+    levels come back as code -1; FastDepth._fn / __call__ raise RuntimeError, and so does the tick readout that
+    carries the codes. After clear_run_error() with the default limit, the next frame equals a run that never
+    failed (the kernel's epoch moved on, so no stale handover word is taken)."""
+    from m3x.serve.fast_depth import FastDepth
+    from m3x.tick import TickReadout
+    model_g = synth.swiglu_depth(seed=641, device=gpu, affine=synth.AFFINE)
+    fd = FastDepth(model_g, 8, dtype=torch.bfloat16, temp=0.9, top_k=50, batch_buckets=(4,))
+    fd.row_seed.copy_(torch.arange(9, dtype=torch.int32, device=gpu) * 613 + 9)
+    g = torch.Generator().manual_seed(642)
+    B, slots = 3, [4, 1, 6]
+    h = torch.randn(B, 1024, generator=g).to(torch.bfloat16).to(gpu)
+    cb0 = torch.randint(0, 2048, (B,), generator=g).to(gpu)
+    assert fd._persistent_ok(B, 0)
+    ref = _eager(fd, B, slots, h, cb0, True)
+    assert not fd.run_error()
+    ctr = fd.row_ctr.clone()
+    fd.spin_limit = 1
+    with pytest.raises(RuntimeError):
+        fd._fn(torch.tensor(slots, device=gpu), h, cb0)
+    assert fd.run_error()
+    fd.row_ctr.copy_(ctr)
+    b = fd.make_buffers(B)
+    b.slots.copy_(torch.tensor(slots))
+    b.h.copy_(h)
+    b.codes[:, 0].copy_(cb0)
+    fd.run(b)
+    torch.cuda.synchronize()
+    fd.row_ctr.copy_(ctr)
+    codes = b.codes.cpu()
+    assert (codes[:, 2:] == -1).all() and torch.equal(codes[:, 0], cb0.cpu().int())
+    rd = TickReadout(8, frame=0, nq=32, device=gpu)
+    rd.pack(torch.zeros(B, dtype=torch.int64, device=gpu), cb0.long(), codes=b.codes)
+    with pytest.raises(RuntimeError):
+        rd.wait()
+    # the graph path raises too
+    fd.warmup()
+    with pytest.raises(RuntimeError):
+        fd(slots, h, cb0)
+    fd.row_ctr.copy_(ctr)
+    # recovery
+    fd.spin_limit = 0
+    fd.clear_run_error()
+    again = _eager(fd, B, slots, h, cb0, True)
+    assert not fd.run_error()
+    assert torch.equal(again[0], ref[0]) and torch.equal(again[1], ref[1]) and torch.equal(again[2], ref[2])

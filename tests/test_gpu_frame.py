@@ -19,11 +19,11 @@ def _frame(gpu, seed=61):
     from m3x.frame import FrameStep
     from m3x.serve.fast_backbone import StaticBackbone
     from m3x.serve.fast_depth import FastDepth
-    bb = synth.qwen3_backbone(layers=2, seed=seed, device=gpu)
+    bb = synth.qwen3_backbone(layers=2, seed=seed, device=gpu, affine=synth.AFFINE)
     sb = StaticBackbone(bb, S, capacity=CAP, batch_buckets=(4,), ctx_buckets=(CAP,), attention="triton",
                         fuse_rope=True)
     cb = Cb0Sampler(bb.cb0_head.weight, S, temp=0.9, top_k=50, rep=0.0)
-    fd = FastDepth(synth.swiglu_depth(seed=seed + 1, device=gpu), S, dtype=torch.bfloat16, temp=0.9, top_k=50,
+    fd = FastDepth(synth.swiglu_depth(seed=seed + 1, device=gpu, affine=synth.AFFINE), S, dtype=torch.bfloat16, temp=0.9, top_k=50,
                    batch_buckets=(4,), fused=True)
     g = torch.Generator().manual_seed(seed + 2)
     lengths = [17, 0, 120, 3, 0, 64, 0, 0]

@@ -99,7 +99,7 @@ def test_topk_sample_surface(gpu, per_row):
 
 def _small_backbone(gpu, layers=2, S=6, cap=256, use_graphs=True, buckets=(1, 2, 4, 8, 64), seed=111):
     from m3x.serve.fast_backbone import StaticBackbone
-    bb = synth.qwen3_backbone(layers=layers, seed=seed, device=gpu)
+    bb = synth.qwen3_backbone(layers=layers, seed=seed, device=gpu, affine=synth.AFFINE)
     return StaticBackbone(bb, S, capacity=cap, batch_buckets=buckets, ctx_buckets=(cap,), attention="triton",
                           fuse_rope=True, use_graphs=use_graphs)
 
@@ -158,7 +158,7 @@ def _frame(gpu, depth_dtype, use_guard=False, seed=121, S=8, cap=256):
     from m3x.serve.fast_depth import FastDepth
     sb = _small_backbone(gpu, S=S, cap=cap, buckets=(4,), seed=seed)
     cb = Cb0Sampler(sb.backbone.cb0_head.weight, S, temp=0.9, top_k=50, rep=0.0)
-    fd = FastDepth(synth.swiglu_depth(seed=seed + 1, device=gpu, dtype=depth_dtype), S, dtype=depth_dtype, temp=0.9,
+    fd = FastDepth(synth.swiglu_depth(seed=seed + 1, device=gpu, dtype=depth_dtype, affine=synth.AFFINE), S, dtype=depth_dtype, temp=0.9,
                    top_k=50, batch_buckets=(4,))
     g = _g(seed + 2)
     with torch.inference_mode():
