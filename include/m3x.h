@@ -441,6 +441,62 @@ int m3x_depth_run(const M3xDepthRun* args, void* stream);
  * The reference turns a GPU-side failure into an exception that fails the engine (maya3/engine.py:375-385). */
 int m3x_depth_run_void(const int32_t* sync, int32_t* codes, long ld_codes, int B, int L0, int L1, void* stream);
 
+/* ---- the one-row backbone decode as one persistent kernel (serve/fast_backbone.py:176-234) ------------------ */
+
+/* Per layer: the packed weights as StaticBackbone packs them (q|k|v [4096, 1024] plain at layer 0 and with the input
+ * RMSNorm weight folded in after it, o [1024, 2048], gate and up [3072, 1024] with the post-attention RMSNorm
+ * weight folded in, down [1024, 3072]), the q/k norm weights [128] and the layer's caches [slots][8][cap][128]. */
+typedef struct M3xBackboneLayer {
+  const void* wqkv;
+  const void* wo;
+  const void* wg;
+  const void* wu;
+  const void* wd;
+  const void* wq;
+  const void* wk;
+  void* kc;
+  void* vc;
+} M3xBackboneLayer;
+
+/* Arguments of m3x_backbone_run: one decode row of the Qwen3-0.6B-shaped backbone (hidden 1024, 16 q / 8 kv heads
+ * of 128, SwiGLU 3072, bf16) through `layers` layers. layer: a DEVICE array of M3xBackboneLayer. x [1024] is the
+ * row's input; the last layer's residual goes to h_out [1024] (the caller's final norm reads it). slots[0] and
+ * pos[0] (device) give the row's slot and position (0 <= pos < cap <= 4096); its key and value are written at pos
+ * of every layer's caches (strides sk_s, sk_h, sk_t in elements), RoPE from cos/sin [cap][128] (row stride s_cos),
+ * w_in0 the layer-0 input RMSNorm weight, eps the RMSNorm epsilon (also of the q/k norms), scale = 128^-0.5.
+ * xchg: m3x_backbone_run_xchg_bytes() of device memory zeroed once; sync: 4 int32 zeroed once ([0] epoch, [1] a
+ * counter, [2] set to 1 if a step's input never arrived within spin_limit polling rounds (0: 2^19), in which case
+ * h_out is not written). nwg must equal 256 and the device must hold all of them at once (else M3X_EUNSUPPORTED).
+ * probe: as M3xDepthRun's. prof (nullable): [256][512] real-time counter stamps of every workgroup's steps. */
+typedef struct M3xBackboneRun {
+  const M3xBackboneLayer* layer;
+  int layers, cap, nwg, probe;
+  unsigned spin_limit;
+  float eps, scale;
+  const void* x;
+  void* h_out;
+  const int64_t* slots;
+  const int32_t* pos;
+  const void* cos;
+  const void* sin;
+  long s_cos;
+  const void* w_in0;
+  long sk_s, sk_h, sk_t;
+  uint64_t* xchg;
+  int32_t* sync;
+  uint64_t* prof;
+} M3xBackboneRun;
+
+/* Bytes of the exchange area, of M3xBackboneRun and of M3xBackboneLayer (a binding checks its layouts). */
+size_t m3x_backbone_run_xchg_bytes(void);
+size_t m3x_backbone_run_args_bytes(void);
+size_t m3x_backbone_run_layer_bytes(void);
+
+/* Launch the run (args read on the host during the call). Replaces, for a one-row step, the layer loop of
+ * `StaticBackbone._forward` (serve/fast_backbone.py:187-203: q|k|v, `_qk_norm_rope_cache`, `_decode_attn`, o, the
+ * add+norms, gate|up, SwiGLU, down) up to the final norm. */
+int m3x_backbone_run(const M3xBackboneRun* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

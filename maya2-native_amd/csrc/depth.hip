@@ -26,6 +26,7 @@
 // rows), GEMM tiles accumulate in fp32 over four K slices summed in slice order with one rounding, the gated
 // epilogues round where the reference rounds (serve/fast_backbone.py:201-202, serve/fast_depth.py:123,186),
 // attention in fp32 with one rounding of the output, the sampler is m3x_sample.h's.
+#include "m3x_ll.h"
 #include "m3x_sample.h"
 
 namespace dk {
@@ -38,8 +39,6 @@ constexpr int MAXL = 4;     // trunk layers
 constexpr int VMAX = 2048;  // codebook size
 constexpr int FMAX = 3072;  // FFN width
 constexpr int HDMAX = 128;  // head dim
-constexpr unsigned SPIN_LIMIT = 1u << 19;
-constexpr int SC1 = 16;     // cache-policy bit of a device-scope access (gfx950 SC1)
 
 // exchange buffers, in 8-byte words; two copies of each, alternating by layer (by level for head and codes)
 constexpr long W_QKV = (long)RB * 3 * DM / 2, W_ATT = (long)RB * DM / 2, W_GU = (long)RB * FMAX / 2,
@@ -88,8 +87,16 @@ struct M3xDepthRun {
 };
 
 namespace dk {
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+using ll::u32x2;
+using ll::u32x4;
+using ll::SC1;
+using ll::SPIN_LIMIT;
+using ll::ll_poll16;
+using ll::ll_poll8;
+using ll::ll_st16;
+using ll::ll_st8;
+using ll::ro_rsrc;
+using ll::bld16;
 
 constexpr int NXM = 3 * DM / 16;  // workgroups that keep the residual stream (one q|k|v tile each)
 constexpr int NOD = DM / 16;      // workgroups of the o and down tiles
@@ -113,180 +120,8 @@ struct Smem {
   float pr[NPOS];
   int codes[RB];
   int seat_codes[NPOS];               // a sampler workgroup's codes of its seat, for the prefix rows at the end
-  int vote[2][NT / 64];               // wg_all's per-wave votes, alternating buffers
-  unsigned spin;                      // the run's spin limit
+  ll::Sync sync;                      // the polls' votes and spin limit
 };
-
-// true in every thread iff v is true in every thread: one barrier; the two vote buffers alternate, so a wave that
-// runs ahead into the next call writes the other buffer while a slower one still reads this one
-__device__ __forceinline__ bool wg_all(Smem& sm, bool v, int& phase) {
-  const bool any_false = __ballot(!v) != 0;
-  if ((threadIdx.x & 63) == 0) sm.vote[phase][threadIdx.x >> 6] = any_false;
-  __syncthreads();
-  const int r = !(sm.vote[phase][0] | sm.vote[phase][1] | sm.vote[phase][2] | sm.vote[phase][3]);
-  phase ^= 1;
-  return __builtin_amdgcn_readfirstlane(r) != 0;
-}
-
-__device__ __forceinline__ u32x4 ll_ld16(__amdgpu_buffer_rsrc_t r, int word) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, word * 8, 0, SC1);
-}
-__device__ __forceinline__ u32x2 ll_ld8(__amdgpu_buffer_rsrc_t r, int word) {
-  return __builtin_amdgcn_raw_buffer_load_b64(r, word * 8, 0, SC1);
-}
-__device__ __forceinline__ void ll_st16(__amdgpu_buffer_rsrc_t r, int word, uint32_t p0, uint32_t p1, uint32_t tag) {
-  const u32x4 v = {p0, tag, p1, tag};
-  __builtin_amdgcn_raw_buffer_store_b128(v, r, word * 8, 0, SC1);
-}
-__device__ __forceinline__ void ll_st8(__amdgpu_buffer_rsrc_t r, int word, uint32_t p, uint32_t tag) {
-  const u32x2 v = {p, tag};
-  __builtin_amdgcn_raw_buffer_store_b64(v, r, word * 8, 0, SC1);
-}
-
-// Read-only tensors through buffer resources: the base stays in scalar registers and a load takes one 32-bit
-// offset register, so loop-invariant addressing does not pin 64-bit vector address pairs for the whole run.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t ro_rsrc(const void* p) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, 0x7fffffff, 0x00020000);
-}
-__device__ __forceinline__ u16x8 bld16(__amdgpu_buffer_rsrc_t r, int voff_bytes, int soff_bytes) {
-  return __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff_bytes, soff_bytes, 0));
-}
-
-// Polling. A consumer reads exactly the words it needs until each carries the step's tag. Each wave polls its own
-// threads' chunks, with no workgroup barrier per round; the workgroup meets once at the end (which also makes the
-// sinks' LDS writes visible). A compiler-only memory clobber in every polling round keeps identical polls from
-// being merged or hoisted out of the loop (the loads stay device-scope, sc1).
-constexpr int OOB = 1 << 30;  // a byte offset past every exchange buffer: such a load returns zeros, no traffic
-constexpr int VOL = SC1;
-#define M3X_POLL_CLOBBER() asm volatile("" ::: "memory")
-
-// One 16-byte chunk per lane (live lanes at byte offset `off`) until both words of every live lane of the wave
-// carry `tag` (a lane that has its chunk polls out of bounds). The chunk's value lands in `out`; false after
-// `limit` rounds.
-__device__ __forceinline__ bool wave_poll1(__amdgpu_buffer_rsrc_t r, int off, bool live, uint32_t tag, u32x4& out,
-                                           unsigned limit) {
-  bool got = !live;
-  for (unsigned it = 0; it < limit; ++it) {
-    M3X_POLL_CLOBBER();
-    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, got ? OOB : off, 0, VOL);
-    if (!got && a.y == tag && a.w == tag) {
-      out = a;
-      got = true;
-    }
-    if (__builtin_amdgcn_ballot_w64(!got) == 0) return true;
-  }
-  return false;
-}
-// the same for one 8-byte word per lane (payload in out.x)
-__device__ __forceinline__ bool wave_poll1w(__amdgpu_buffer_rsrc_t r, int off, bool live, uint32_t tag, u32x2& out,
-                                            unsigned limit) {
-  bool got = !live;
-  for (unsigned it = 0; it < limit; ++it) {
-    M3X_POLL_CLOBBER();
-    const u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(r, got ? OOB : off, 0, VOL);
-    if (!got && a.y == tag) {
-      out = a;
-      got = true;
-    }
-    if (__builtin_amdgcn_ballot_w64(!got) == 0) return true;
-  }
-  return false;
-}
-
-// This thread's chunks i < nit (16 bytes, two words each; nit uniform across the workgroup, at most N), handing
-// each live chunk's two payloads to sink(i, p0, p1) once. Chunk i sits at word base + U(i), base per thread and
-// U(i) a constant, so the loads take one address register and constant offsets. With more than `probe` chunks per
-// thread, chunk 0 is polled first (a probe: one chunk per thread while the producers still run, which then mostly
-// finds the rest already there); rounds read the chunks still missing, skipping chunks i >= nit by uniform
-// branches and pushing arrived ones out of bounds. Workgroup-collective (every thread calls it); false if any wave
-// gave up after the run's spin limit of rounds (sm.spin).
-template <int N, class U, class Live, class Sink>
-__device__ __forceinline__ bool ll_poll16(Smem& sm, int& vph, __amdgpu_buffer_rsrc_t r, int base, U uoff, int nit,
-                                          int probe, Live live, uint32_t tag, Sink sink) {
-  static_assert(N <= 64, "chunks per thread");
-  const unsigned limit = __builtin_amdgcn_readfirstlane(sm.spin);
-  uint64_t pending = 0;
-#pragma unroll
-  for (int i = 0; i < N; ++i)
-    if (i < nit && live(i)) pending |= 1ull << i;
-  bool ok = true;
-  if (nit > probe) {
-    const bool l0 = pending & 1ull;
-    u32x4 v0;
-    ok = wave_poll1(r, base * 8 + uoff(0) * 8, l0, tag, v0, limit);
-    if (ok && l0) {
-      sink(0, v0.x, v0.z);
-      pending &= ~1ull;
-    }
-  }
-  {
-    for (unsigned it = 0; ok; ++it) {
-      if (__builtin_amdgcn_ballot_w64(pending != 0) == 0) break;
-      if (it >= limit) {
-        ok = false;
-        break;
-      }
-      M3X_POLL_CLOBBER();
-      u32x4 v[N];
-#pragma unroll
-      for (int i = 0; i < N; ++i)
-        if (i < nit)
-          v[i] = __builtin_amdgcn_raw_buffer_load_b128(r, base * 8 + (((pending >> i) & 1) ? 0 : OOB), uoff(i) * 8,
-                                                       VOL);
-#pragma unroll
-      for (int i = 0; i < N; ++i) {
-        if (i < nit && ((pending >> i) & 1) && v[i].y == tag && v[i].w == tag) {
-          sink(i, v[i].x, v[i].z);
-          pending &= ~(1ull << i);
-        }
-      }
-    }
-  }
-  return wg_all(sm, ok, vph);
-}
-
-// the same for single words (8-byte loads); sink(i, payload)
-template <int N, class U, class Live, class Sink>
-__device__ __forceinline__ bool ll_poll8(Smem& sm, int& vph, __amdgpu_buffer_rsrc_t r, int base, U uoff, int nit,
-                                         int probe, Live live, uint32_t tag, Sink sink) {
-  static_assert(N <= 32, "words per thread");
-  const unsigned limit = __builtin_amdgcn_readfirstlane(sm.spin);
-  uint32_t pending = 0;
-#pragma unroll
-  for (int i = 0; i < N; ++i)
-    if (i < nit && live(i)) pending |= 1u << i;
-  bool ok = true;
-  if (nit > probe) {
-    const bool l0 = pending & 1u;
-    u32x2 v0;
-    ok = wave_poll1w(r, base * 8 + uoff(0) * 8, l0, tag, v0, limit);
-    if (ok && l0) {
-      sink(0, v0.x);
-      pending &= ~1u;
-    }
-  }
-  for (unsigned it = 0; ok; ++it) {
-    if (__builtin_amdgcn_ballot_w64(pending != 0) == 0) break;
-    if (it >= limit) {
-      ok = false;
-      break;
-    }
-    M3X_POLL_CLOBBER();
-    u32x2 v[N];
-#pragma unroll
-    for (int i = 0; i < N; ++i)
-      if (i < nit)
-        v[i] = __builtin_amdgcn_raw_buffer_load_b64(r, base * 8 + (((pending >> i) & 1) ? 0 : OOB), uoff(i) * 8, VOL);
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-      if (i < nit && ((pending >> i) & 1) && v[i].y == tag) {
-        sink(i, v[i].x);
-        pending &= ~(1u << i);
-      }
-    }
-  }
-  return wg_all(sm, ok, vph);
-}
 
 __device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) { return (uint32_t)lo | ((uint32_t)hi << 16); }
 
@@ -418,7 +253,7 @@ __device__ __forceinline__ bool add_rows(Smem& sm, int& vph, __amdgpu_buffer_rsr
       }
   }
   const bool ok = ll_poll16<RB>(
-      sm, vph, rs, base + 2 * t, [](int i) { return i * (DM / 2); }, B, probe, [](int) { return true; }, tag,
+      sm.sync, vph, rs, base + 2 * t, [](int i) { return i * (DM / 2); }, B, probe, [](int) { return true; }, tag,
       [&](int i, uint32_t p0, uint32_t p1) {
         uint16_t* xp = &sm.m.x[i][4 * t];
         const uint16_t av[4] = {(uint16_t)(p0 & 0xffff), (uint16_t)(p0 >> 16), (uint16_t)(p1 & 0xffff),
@@ -450,7 +285,7 @@ __device__ __forceinline__ bool stage_act(Smem& sm, int& vph, __amdgpu_buffer_rs
     const int rows = min(max(B - h * HR, 0), HR), nlive = rows * CPR;
     if (rows == 0) break;
     ok = ll_poll16<N>(
-        sm, vph, rs, base + h * HR * CPR * 2 + 2 * (int)threadIdx.x, [](int i) { return 2 * NT * i; },
+        sm.sync, vph, rs, base + h * HR * CPR * 2 + 2 * (int)threadIdx.x, [](int i) { return 2 * NT * i; },
         (nlive + NT - 1) / NT, probe, [&](int i) { return (int)threadIdx.x + NT * i < nlive; }, tag,
         [&](int i, uint32_t p0, uint32_t p1) {
           const int cc = threadIdx.x + NT * i;
@@ -593,7 +428,7 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
   };
 
   // ---- set-up: zeroed LDS rows, the residual at L0 from the prefix, the pair's K/V history
-  if (tid == 0) sm.spin = a.spin_limit ? a.spin_limit : SPIN_LIMIT;
+  if (tid == 0) sm.sync.spin = a.spin_limit ? a.spin_limit : SPIN_LIMIT;
   if (xm) {
     for (int i = tid; i < RB * XS / 8; i += NT) {
       reinterpret_cast<u16x8*>(&sm.m.x[0][0])[i] = u16x8{};
@@ -645,7 +480,7 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
           const uint32_t t_code = (epoch << 12) | (lvl_seq - 1);
           const int b_code = O_CODE + (1 - lpar) * W_CODE;
           ok = ll_poll8<1>(
-              sm, vph, rs, b_code + tid, [](int) { return 0; }, 1, a.probe, [&](int) { return tid < B; }, t_code,
+              sm.sync, vph, rs, b_code + tid, [](int) { return 0; }, 1, a.probe, [&](int) { return tid < B; }, t_code,
               [&](int, uint32_t p) { sm.codes[tid] = (int)p; });
           stamp(li * 64 + 52);
           __syncthreads();
@@ -672,7 +507,7 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
         constexpr int per = HD / 4;  // 16-byte chunks of each of q, k and v of one head
         const int part = tid / per, c = tid % per;
         const int w0 = b_qkv + pb * (3 * DM / 2) + (part * DM + ph * HD) / 2 + 2 * c;
-        ok = ll_poll16<1>(sm, vph, rs, w0, [](int) { return 0; }, 1, a.probe, [&](int) { return tid < 3 * per; }, t_qkv,
+        ok = ll_poll16<1>(sm.sync, vph, rs, w0, [](int) { return 0; }, 1, a.probe, [&](int) { return tid < 3 * per; }, t_qkv,
                           [&](int, uint32_t p0, uint32_t p1) {
                             const uint16_t v4[4] = {(uint16_t)(p0 & 0xffff), (uint16_t)(p0 >> 16),
                                                     (uint16_t)(p1 & 0xffff), (uint16_t)(p1 >> 16)};
@@ -824,7 +659,7 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
       constexpr int NE = VMAX / NT;
       const float ur = a.greedy ? 0.f : a.u[(long)r * a.ld_u + L - 1];
       float xv[NE];
-      ok = ll_poll8<NE>(sm, vph, rs, b_log + r * (VMAX / 2) + tid / 2, [](int e) { return NT / 2 * e; }, NE, a.probe,
+      ok = ll_poll8<NE>(sm.sync, vph, rs, b_log + r * (VMAX / 2) + tid / 2, [](int e) { return NT / 2 * e; }, NE, a.probe,
                         [&](int) { return true; }, t_log, [&](int e, uint32_t p) {
                           const uint16_t h16 = (uint16_t)((tid & 1) ? (p >> 16) : (p & 0xffff));
                           xv[e] = E<DT>::to_f(h16) * a.inv_temp;

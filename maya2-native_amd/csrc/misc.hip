@@ -339,4 +339,4 @@ M3X_API int m3x_cast_rows(const void* src, long ld_src, int src_dtype, void* dst
 }
 
 // The library's version, so a host binding can check it loaded the build it expects.
-M3X_API int m3x_version(void) { return 15; }
+M3X_API int m3x_version(void) { return 16; }

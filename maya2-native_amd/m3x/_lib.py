@@ -12,7 +12,7 @@ import os
 import torch  # noqa: F401  (must precede the CDLL load, see above)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libm3x.so")
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -68,6 +68,10 @@ SIGNATURES = {
     "m3x_depth_run_args_bytes": (_Z, []),
     "m3x_depth_run": (_I, [_P, _P]),
     "m3x_depth_run_void": (_I, [_P, _P, _L, _I, _I, _I, _P]),
+    "m3x_backbone_run_xchg_bytes": (_Z, []),
+    "m3x_backbone_run_args_bytes": (_Z, []),
+    "m3x_backbone_run_layer_bytes": (_Z, []),
+    "m3x_backbone_run": (_I, [_P, _P]),
     "m3x_rvq_decode": (_I, [_P, _L, _P, _P, _L, _I, _I, _I, _I, _I, _P]),
     "m3x_dwconvt": (_I, [_P, _L, _P, _P, _L, _P, _P, _I, _I, _I, _I, _I, _P]),
     "m3x_conv_gather": (_I, [_P, _L, _P, _L, _P, _P, _L, _I, _I, _I, _I, _I, _I, _I, _I, _P]),

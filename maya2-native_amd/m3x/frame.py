@@ -70,6 +70,9 @@ class FrameStep:
         if dp.h is not bb.out:
             ops.cast_rows(bb.out, dp.h)
         self.depth.run(dp)
+        if self.bb._persistent_ok(bb.rows):
+            # a one-row backbone run that lost a step's input voids the frame's codes (the readout raises on them)
+            ops.depth_run_void(self.bb._run_sync, codes, bb.rows, 0, N_CODEBOOKS)
         ops.code_ring_write(codes, self.ring, self.ring_head, bb.rows)
         fb = dp.feedback if dp.fb_back is None else ops.cast_rows(dp.feedback, dp.fb_back)
         ops.copy_rows(fb, self.feedback, dst_idx=bb.slots)

@@ -530,6 +530,42 @@ def depth_run_void(sync, codes, B, L0, L1):
     check(lib().m3x_depth_run_void(_p(sync), _p(codes), codes.stride(0), B, L0, L1, _stream()), "depth_run_void")
 
 
+# ---------------------------------------------------------------- one-row backbone run (serve/fast_backbone.py)
+class BackboneLayer(ctypes.Structure):
+    """Mirror of M3xBackboneLayer (include/m3x.h); rows of a device table, one per layer."""
+    _fields_ = [(n, ctypes.c_void_p) for n in ("wqkv", "wo", "wg", "wu", "wd", "wq", "wk", "kc", "vc")]
+
+
+class BackboneRunArgs(ctypes.Structure):
+    """Mirror of M3xBackboneRun (include/m3x.h); its size is checked against the library's."""
+    _fields_ = [("layer", ctypes.c_void_p)] + [(n, ctypes.c_int) for n in ("layers", "cap", "nwg", "probe")] + [
+        ("spin_limit", ctypes.c_uint), ("eps", ctypes.c_float), ("scale", ctypes.c_float),
+        ("x", ctypes.c_void_p), ("h_out", ctypes.c_void_p), ("slots", ctypes.c_void_p), ("pos", ctypes.c_void_p),
+        ("cos", ctypes.c_void_p), ("sin", ctypes.c_void_p), ("s_cos", ctypes.c_long), ("w_in0", ctypes.c_void_p),
+        ("sk_s", ctypes.c_long), ("sk_h", ctypes.c_long), ("sk_t", ctypes.c_long), ("xchg", ctypes.c_void_p),
+        ("sync", ctypes.c_void_p), ("prof", ctypes.c_void_p)]
+
+
+def backbone_run_xchg_bytes() -> int:
+    return int(lib().m3x_backbone_run_xchg_bytes())
+
+
+def backbone_layer_table(layers, device):
+    """The device table of M3xBackboneLayer rows for `layers` (lists of BackboneLayer)."""
+    if ctypes.sizeof(BackboneLayer) != int(lib().m3x_backbone_run_layer_bytes()):
+        raise RuntimeError("BackboneLayer does not match the library's M3xBackboneLayer: rebuild the library")
+    raw = (BackboneLayer * len(layers))(*layers)
+    host = torch.frombuffer(bytearray(bytes(raw)), dtype=torch.int64).clone()
+    return host.to(device)
+
+
+def backbone_run(args: BackboneRunArgs):
+    """Launch a one-row backbone run on the current stream (args built by StaticBackbone)."""
+    if ctypes.sizeof(BackboneRunArgs) != int(lib().m3x_backbone_run_args_bytes()):
+        raise RuntimeError("BackboneRunArgs does not match the library's M3xBackboneRun: rebuild the library")
+    check(lib().m3x_backbone_run(ctypes.byref(args), _stream()), "backbone_run")
+
+
 # ---------------------------------------------------------------- Mimi decode (serve/fast_codec.py)
 def rvq_decode(codes, tables, out):
     """out[b] = [table_0[codes[b, 0]] | sum over q >= 1 of table_q[codes[b, q]]]; tables [nq, n_codes, dim]."""

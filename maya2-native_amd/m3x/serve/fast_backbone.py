@@ -36,7 +36,7 @@ import torch
 
 from .. import ops
 from .._lib import lib
-from ..staging import Buckets, RowTable, Upload, capture, check_slots
+from ..staging import Buckets, ErrorWatch, RowTable, Upload, capture, check_slots
 
 TILE = 32  # keys per attention tile: the per-slot extent of the cache allocation is a multiple of this
 
@@ -104,6 +104,15 @@ class StaticBackbone:
             self._alloc_cache()
         self.graphs = {}
         self.pool = None
+        # the one-row step as one persistent kernel (m3x_backbone_run): its exchange area and epoch / error words;
+        # spin_limit: polling rounds before a wait gives up (0: the kernel's default)
+        self.persistent = True
+        self.spin_limit = 0
+        self._run_xchg = torch.zeros(ops.backbone_run_xchg_bytes() // 8, dtype=torch.int64, device=self.device)
+        self._run_sync = torch.zeros(4, dtype=torch.int32, device=self.device)
+        self._run_table = None
+        self._nwg = torch.cuda.get_device_properties(self.device).multi_processor_count
+        self._watch = ErrorWatch(self._run_sync, 'StaticBackbone: a persistent one-row step')
 
     # ---------------------------------------------------------------- construction
     def _read_model(self, backbone):
@@ -263,10 +272,61 @@ class StaticBackbone:
         b.attn_ws = torch.empty(max(ws, 16) // 4, dtype=torch.float32, device=dev)
         return b
 
+    # ---------------------------------------------------------------- one-row persistent run
+    def _persistent_ok(self, rows):
+        """Whether a step of `rows` rows runs as one persistent kernel: one row (the one-seat frame), the
+        Qwen3-0.6B geometry the kernel implements (hidden 1024 with the folded norms, 16 q / 8 kv heads of 128,
+        SwiGLU 3072, bf16), a per-slot extent of at most 4096 positions, one workgroup per CU on a 256-CU part."""
+        return (self.persistent and rows == 1 and self.fused_norms and self.heads == 16 and self.kv_heads == 8
+                and self.head_dim == 128 and self.inter == 3072 and self._extent <= 4096 and self._nwg == 256)
+
+    def _run_args(self, b):
+        """The persistent run's arguments for buffer set b (built once per buffer set; the spin limit refreshed)."""
+        if self._run_table is None:
+            rows = []
+            for i, layer in enumerate(self.layers):
+                a = layer.self_attn
+                rows.append(ops.BackboneLayer(
+                    self.pqkv[i].data.data_ptr(), self.po[i].data.data_ptr(), self.pgate[i].data.data_ptr(),
+                    self.pup[i].data.data_ptr(), self.pdown[i].data.data_ptr(), a.q_norm.weight.data_ptr(),
+                    a.k_norm.weight.data_ptr(), self._kfull[i].data_ptr(), self._vfull[i].data_ptr()))
+            self._run_table = ops.backbone_layer_table(rows, self.device)
+        a = b.__dict__.get('run')
+        if a is None:
+            a = b.run = ops.BackboneRunArgs()
+            kc = self._kfull[0]
+            a.layer, a.layers, a.cap, a.nwg, a.probe = self._run_table.data_ptr(), len(self.layers), self._extent, \
+                self._nwg, 0
+            a.eps, a.scale = self.eps, self.scaling
+            a.x, a.h_out, a.slots, a.pos = b.x.data_ptr(), b.h.data_ptr(), b.slots.data_ptr(), b.pos.data_ptr()
+            a.cos, a.sin, a.s_cos = self.cos.data_ptr(), self.sin.data_ptr(), self.cos.stride(0)
+            a.w_in0 = self.layers[0].input_layernorm.weight.data_ptr()
+            a.sk_s, a.sk_h, a.sk_t = kc.stride(0), kc.stride(1), kc.stride(2)
+            a.xchg, a.sync = self._run_xchg.data_ptr(), self._run_sync.data_ptr()
+        a.spin_limit = int(self.spin_limit)
+        return a
+
+    def run_error(self):
+        """True when a persistent run since construction (or the last clear) lost a step's input (its bounded waits
+        ran out); that step's output rows are void. Synchronises with the device."""
+        return bool(self._run_sync[2].item())
+
+    @torch.inference_mode()
+    def clear_run_error(self):
+        """Reset the error word (stream-ordered)."""
+        self._run_sync[2].zero_()
+        self._watch.evt = None
+
     def forward(self, b):
         """One decode step over the rows of buffer set `b` (positions from lengths[slots] + offset); returns b.out."""
         H, KV, D, eps = self.heads, self.kv_heads, self.head_dim, self.eps
         ops.positions(self.lengths, b.slots, b.offset, b.pos)
+        if self._persistent_ok(b.rows) and not b.mixed:
+            # the 28 layers of the one-row step in one launch; the final norm and the lengths as the launch path
+            ops.backbone_run(self._run_args(b))
+            ops.add_rms(b.h, None, self.norm.weight, eps, y=b.out)
+            ops.lengths_add(self.lengths, b.slots, b.real)
+            return b.out
         o3 = b.o.view(b.rows, H, D)
         fused = self.fused_norms
         rms = ops.NORM_RMS
@@ -350,7 +410,10 @@ class StaticBackbone:
         return row_slot, row_off, runs, need
 
     def _replay(self, slots, x, prefills):
-        """Stage and run one step; returns the step's output rows (a view of the graph's buffer)."""
+        """Stage and run one step; returns the step's output rows (a view of the graph's buffer). Raises when an
+        earlier persistent one-row step failed (the reference fails the engine on a GPU-side error,
+        maya3/engine.py:375-385)."""
+        self._watch.raise_if_set()
         row_slot, row_off, runs, need = self._rows_of(slots, prefills)
         n = len(row_slot)
         g = self._graph(self._rows.pick(n, 'batch'), self._ctx.pick(need, 'context'), bool(prefills))
@@ -375,6 +438,8 @@ class StaticBackbone:
             g.graph.replay()
         else:
             self.forward(b)
+        if self._persistent_ok(b.rows) and not b.mixed:
+            self._watch.after()
         for s in slots:
             self.lengths_cpu[s] += 1
         for s, t in prefills:

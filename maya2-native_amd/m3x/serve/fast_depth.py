@@ -26,7 +26,7 @@ import torch
 
 from .. import ops
 from .._lib import lib
-from ..staging import Buckets, RowTable, capture, check_slots
+from ..staging import Buckets, ErrorWatch, RowTable, capture, check_slots
 
 N_LEVELS = 32
 REFERENCE_GROUP_OF_LEVEL = [None] + list(range(8)) + [8] * 8 + [9] * 8 + [10] * 7
@@ -115,6 +115,7 @@ class FastDepth:
         self._run_xchg = torch.zeros(ops.depth_run_xchg_bytes() // 8, dtype=torch.int64, device=dev)
         self._run_sync = torch.zeros(4, dtype=torch.int32, device=dev)
         self._nwg = torch.cuda.get_device_properties(dev).multi_processor_count
+        self._watch = ErrorWatch(self._run_sync, 'FastDepth: a persistent depth run')
 
     def _load(self, model):
         d, dt = model.depth, self.dtype
@@ -377,17 +378,11 @@ class FastDepth:
         ran out): that run's codes came back as -1 and the frame is void. Synchronises with the device."""
         return bool(self._run_sync[2].item())
 
+    @torch.inference_mode()
     def clear_run_error(self):
         """Reset the error word (stream-ordered), e.g. after the caller has failed the frame's requests."""
         self._run_sync[2].zero_()
-
-    def _check_run(self, b):
-        """Raise when buffer set b's frame ran a persistent run and a run since the last clear failed (the
-        reference fails the engine on a GPU-side error, maya3/engine.py:375-385). Synchronises with the device,
-        only for buffer sets that run persistent levels (up to PERSISTENT_SEATS seats)."""
-        if b.__dict__.get('runs') and self.run_error():
-            raise RuntimeError('FastDepth: a persistent depth run lost a step\'s input (its bounded waits ran out); '
-                               'the frame\'s codes are void (-1). clear_run_error() resets the error word')
+        self._watch.evt = None
 
     def _compute(self, slots_idx, h, cb0):
         """Eager frame body over fresh buffers (the reference's tests call `_fn(slots_idx, h, cb0)`)."""
@@ -395,8 +390,10 @@ class FastDepth:
         b.slots.copy_(slots_idx)
         b.h.copy_(h)
         b.codes[:, 0].copy_(cb0)
+        self._watch.raise_if_set()
         codes, fb = self.run(b)
-        self._check_run(b)
+        if b.__dict__.get('runs'):
+            self._watch.after()
         return codes.long(), fb
 
     # ---------------------------------------------------------------- graphs
@@ -429,8 +426,10 @@ class FastDepth:
         if key != g.bufs.table.key:
             check_slots(key, self.max_slots, distinct=False)
             g.bufs.table.stage(dict(slot=key), key=key)
+        self._watch.raise_if_set()
         g.bufs.h[:B].copy_(h)
         g.bufs.codes[:B, 0].copy_(cb0)
         g.graph.replay()
-        self._check_run(g.bufs)
+        if g.bufs.__dict__.get('runs'):
+            self._watch.after()
         return g.bufs.codes[:B].long(), g.bufs.feedback[:B].clone()

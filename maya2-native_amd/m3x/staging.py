@@ -102,6 +102,29 @@ class RowTable:
         self.key = None
 
 
+class ErrorWatch:
+    """The error word of a persistent kernel's sync block (sync[2]) seen by the host without a synchronisation:
+    after() enqueues its copy into pinned memory behind the step that may set it; raise_if_set() raises once that
+    copy has landed and shows the word set (a step's failure surfaces at the next call, or at the tick's readout,
+    which sees the voided outputs in its own copy)."""
+
+    def __init__(self, sync, what):
+        self.sync, self.what = sync, what
+        self.host = torch.zeros(1, dtype=sync.dtype).pin_memory()
+        self.evt = None
+
+    def after(self):
+        self.host.copy_(self.sync[2:3], non_blocking=True)
+        self.evt = torch.cuda.Event()
+        self.evt.record()
+
+    def raise_if_set(self):
+        if self.evt is not None and self.evt.query() and int(self.host[0]):
+            self.evt = None
+            raise RuntimeError(f'{self.what} lost a step\'s input (its bounded waits ran out); that step\'s outputs '
+                               'are void. clear_run_error() resets the error word')
+
+
 def capture(body, pool, warm=2, keep=()):
     """Runs body() `warm` times on a side stream, then captures one run into a hipGraph on `pool`. The tensors in
     `keep` (per-slot counters and the like that a run advances) are restored after the runs. Returns the graph."""

@@ -123,9 +123,10 @@ def test_run_graph_replays_equal_eager(gpu):
 def test_run_failure_is_surfaced(gpu):
     """A run whose bounded waits give up, forced from the host with a spin limit of one polling round (every
     workgroup still exits normally: a failed wait skips the rest of the run), sets the error word; the run's
-    levels come back as code -1; FastDepth._fn / __call__ raise RuntimeError, and so does the tick readout that
-    carries the codes. After clear_run_error() with the default limit, the next frame equals a run that never
-    failed (the kernel's epoch moved on, so no stale handover word is taken)."""
+    levels come back as code -1; the tick readout that carries the codes raises RuntimeError, and so does the next
+    call of FastDepth._fn / __call__ (the host sees the word without a synchronisation). After clear_run_error()
+    with the default limit, the next frame equals a run that never failed (the kernel's epoch moved on, so no stale
+    handover word is taken)."""
     from m3x.serve.fast_depth import FastDepth
     from m3x.tick import TickReadout
     model_g = synth.swiglu_depth(seed=641, device=gpu, affine=synth.AFFINE)
@@ -140,9 +141,11 @@ def test_run_failure_is_surfaced(gpu):
     assert not fd.run_error()
     ctr = fd.row_ctr.clone()
     fd.spin_limit = 1
+    fd._fn(torch.tensor(slots, device=gpu), h, cb0)
+    torch.cuda.synchronize()
+    assert fd.run_error()
     with pytest.raises(RuntimeError):
         fd._fn(torch.tensor(slots, device=gpu), h, cb0)
-    assert fd.run_error()
     fd.row_ctr.copy_(ctr)
     b = fd.make_buffers(B)
     b.slots.copy_(torch.tensor(slots))
@@ -157,8 +160,10 @@ def test_run_failure_is_surfaced(gpu):
     rd.pack(torch.zeros(B, dtype=torch.int64, device=gpu), cb0.long(), codes=b.codes)
     with pytest.raises(RuntimeError):
         rd.wait()
-    # the graph path raises too
+    # the graph path (captured with the limit of one round) raises at the call after a failed replay
     fd.warmup()
+    fd(slots, h, cb0)
+    torch.cuda.synchronize()
     with pytest.raises(RuntimeError):
         fd(slots, h, cb0)
     fd.row_ctr.copy_(ctr)
