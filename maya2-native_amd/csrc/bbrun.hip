@@ -4,25 +4,33 @@
 // Launched one kernel per step, a layer of the one-row backbone is 7 dependent launches (q|k|v, q/k norm + RoPE +
 // cache write, split attention, its combine, o, gate|up, down) of 3-6 us each, almost all of it launch and cold
 // memory latency. Here one workgroup per CU stays resident for all layers, and the steps hand over through LL words
-// in global memory (m3x_ll.h):
-//   S1 q|k|v     every workgroup: one 16-column tile of the 4096, from the residual row it keeps in LDS (the input
-//                RMSNorm applied explicitly at layer 0, folded into the packed weight after it, as the launch path);
-//   S2 attention every workgroup: one (kv head, split) item of 8 x 32: the two q heads and the new key of its kv head
-//                normed and rotated (qk_norm_rope8, the launch kernels' arithmetic), the new key and value written
-//                to the cache by the item that holds the row's position, fp32 scores / softmax / P.V over the
-//                split's keys; the split's partial (max, sum, 128 values per q head) goes out;
-//   S3 combine   workgroups 0..15: one q head each, its 32 partials folded in split order;
-//   S4 o         workgroups 192..255: one 16-column tile of the o projection (K = 2048);
-//   S5 residual  every workgroup: x = dt(x + o), then workgroups 0..191: one gate|up tile pair with the
-//                post-attention RMSNorm folded, SwiGLU;
-//   S6 down      workgroups 192..255: one 16-column tile of the down projection (K = 3072);
-//   S7 residual  every workgroup: x = dt(x + down), the next layer's S1.
-// A step's weights (and an attention item's cached keys and values) are loaded before the step waits for its
-// input, so the weight stream and the cache reads overlap the chain of handovers. The split size follows the row's
-// position (32 splits of ceil((pos + 1) / 32) keys rounded up to 16), so every workgroup attends about the same
-// number of keys. After the last layer workgroup 0 stores the residual row; the caller's final norm reads it.
-// Every wait is bounded by the run's spin limit: a workgroup whose input never arrives sets the error word and
-// skips the rest, so the grid always drains (the output row is then not written).
+// in global memory (m3x_ll.h). A handover costs one device-scope round trip (~0.3 us) only if nothing else is in
+// flight in the polling wave: a wave's vector memory counter retires in order, so a poll issued behind a weight
+// load waits for that load too. The waves therefore split by role:
+//   - waves 0-3 project: they hold the workgroup's weight tiles and its attention split's cached keys and values in
+//     registers, each loaded steps ahead of its use (right after the slot's previous tile is used), and run the
+//     MFMA tiles;
+//   - waves 4-7 only poll, reduce, attend and store: nothing of theirs is in flight when they poll.
+// The two roles run their own loop over the layers and meet at the same workgroup barriers.
+// Per layer (every workgroup unless said otherwise):
+//   S1 q|k|v     x += the previous layer's down (its four K-slice partials summed in order), the row's RMS; one
+//                16-column tile of the 4096 (the input RMSNorm applied explicitly at layer 0, folded into the
+//                packed weight after it, as the launch path); the 32 tiles of kv head h sit on XCD h;
+//   S2 attention item (kv head wg % 8, split wg / 8): the two q heads and the new key of its kv head normed and
+//                rotated (qk_norm_rope8, the launch kernels' arithmetic), the new key and value written to the cache
+//                by the item that holds the row's position, fp32 scores / softmax / P.V over the split's keys; the
+//                split's partial (max, sum, 128 values per q head) goes out;
+//   S3 combine   workgroups 0..15: one q head each (on its kv head's XCD), its 32 partials folded in split order;
+//   S4 o         one (16-column tile, K quarter) unit of the o projection: an fp32 partial of 16 columns;
+//   S5 gate|up   x += o (the four partials summed in order, rounded, added), the row's RMS; workgroups 0..191: one
+//                gate|up tile pair with the post-attention RMSNorm folded, SwiGLU;
+//   S6 down      one (16-column tile, K quarter) unit of the down projection: an fp32 partial.
+// The K quarters spread the o and down weights over every workgroup, so each one streams about the same bytes
+// (~136 KB at most per layer) and a consumer of a K quarter polls only that quarter of its input. The split size
+// follows the row's position (32 splits of ceil((pos + 1) / 32) keys rounded up to 16), so every workgroup attends
+// about the same number of keys. After the last layer workgroup 0 stores the residual row; the caller's final norm
+// reads it. Every wait is bounded by the run's spin limit: a workgroup whose input never arrives sets the error word
+// and skips the rest, so the grid always drains (the output row is then not written).
 #include "m3x_ll.h"
 #include "m3x_norm.h"
 
@@ -58,13 +66,15 @@ struct M3xBackboneRun {
 };
 
 namespace bb {
-using ll::ll_poll16;
-using ll::ll_poll8;
+using ll::ll_poll16_w;
+using ll::ll_poll8_w;
 using ll::ll_st8;
 using ll::ro_rsrc;
 using ll::bld16;
+using ll::wg_all;
 
-constexpr int NT = 256;                 // threads per workgroup
+constexpr int NT = 512;                 // threads per workgroup
+constexpr int NM = 256;                 // waves 0-3: the projecting waves; waves 4-7: the io waves
 constexpr int NWG = 256;                // workgroups: one per CU
 constexpr int DM = 1024, H = 16, KV = 8, HD = 128, FF = 3072;
 constexpr int NQKV = (H + 2 * KV) * HD; // 4096: one q|k|v tile per workgroup
@@ -72,53 +82,79 @@ constexpr int SPLITS = NWG / KV;        // 32 attention splits per kv head
 constexpr int SMAX = 128;               // keys per split at most (positions below 4096)
 constexpr int KS = HD + 8;              // LDS row stride of the split's keys and values: 16 lanes hit 16 bank groups
 constexpr int PW = 2 * (HD + 2);        // partial words per item: per q head its max, its sum and 128 values
-constexpr int NOD = 64;                 // workgroups 192..255 own the o and down tiles
+constexpr int KQ = 2;                   // K halves of the o and down projections
+constexpr int KO = H * HD / KQ;         // 1024: an o unit's K (workgroups 0..127)
+constexpr int KD = FF / KQ;             // 1536: a down unit's K (workgroups 128..255)
+constexpr int NOD = NWG / 2;            // o units, then down units
 constexpr int NGU = FF / 16;            // workgroups 0..191 own the gate|up tile pairs
+constexpr int KVN = SMAX * HD / 8 / NM; // 16-byte chunks of the split's keys (and of its values) per projecting thread
 
-// exchange buffers (8-byte words, 4 bytes of payload each); two copies alternating by layer
-constexpr long W_QKV = NQKV / 2, W_PART = (long)NWG * PW, W_ATT = H * HD / 2, W_O = DM / 2, W_GU = FF / 2,
-               W_DN = DM / 2;
+// exchange buffers (8-byte words, 4 bytes of payload each); two copies alternating by layer. The o and down
+// partials are fp32 words [K half][1024]; q|k|v, attention and gate|up carry two bf16 per word.
+constexpr long W_QKV = NQKV / 2, W_PART = (long)NWG * PW, W_ATT = H * HD / 2, W_O = (long)KQ * DM, W_GU = FF / 2,
+               W_DN = (long)KQ * DM;
 constexpr long O_QKV = 0, O_PART = O_QKV + 2 * W_QKV, O_ATT = O_PART + 2 * W_PART, O_O = O_ATT + 2 * W_ATT,
                O_GU = O_O + 2 * W_O, O_DN = O_GU + 2 * W_GU, X_WORDS = O_DN + 2 * W_DN;
 constexpr int STEPS = 6;                // tags per layer: q|k|v, partials, attention, o, gate|up, down
 
 struct Smem {
-  uint16_t x[DM];                       // the residual row
-  uint16_t b[FF + 8];                   // the B operand row of the step's tile
-  union {
-    struct {
-      uint16_t kt[SMAX][KS];            // the split's keys
-      uint16_t vt[SMAX][KS];            // and values
-    } kv;
-    float comb[SPLITS][HD + 2];         // a combine workgroup's 32 partials of its q head
-  } u;
-  uint16_t raw[4 * HD];                 // q heads 2h, 2h+1, then the new key and value, as projected
-  uint16_t qb[2][HD];                   // the q heads, normed and rotated
+  alignas(16) uint16_t x[DM];           // the residual row
+  alignas(16) uint16_t b[KD + 8];       // the B operand row of a K-sliced tile (layer 0's normed row, o's, down's)
+  alignas(16) uint16_t kt[SMAX][KS];    // the split's keys, a row per key
+  alignas(16) uint16_t vt[HD][KS];      // and its values, transposed: a row per dimension (the P.V B operand)
+  alignas(16) float comb[SPLITS][HD + 2];  // a combine workgroup's 32 partials of its q head
+  alignas(16) uint16_t raw[4 * HD];     // q heads 2h, 2h+1, then the new key and value, as projected
+  alignas(16) uint16_t qb[2][HD];       // the q heads, normed and rotated
+  alignas(16) uint16_t kn[HD];          // the new key, normed and rotated
+  alignas(16) uint16_t pb[4][SMAX];     // probabilities of q heads 0, 1 (bf16), then what bf16 left of them
+  alignas(16) uint16_t nw[2][HD];       // the layer's q_norm and k_norm weights
+  alignas(16) uint16_t cs[2][HD];       // cos and sin at the row's position
   float cw[SPLITS];                     // a combine workgroup's split weights exp(m_s - M)
-  uint16_t kn[HD];                      // the new key, normed and rotated
-  float sc[2][SMAX];                    // scores, then probabilities
   float part[2][4][16];                 // per-wave partial tiles (gate, up)
-  float red[2][4];                      // per-wave reductions
-  float inv;                            // the residual row's 1 / rms
+  float red[2][8];                      // per-io-wave reductions (two q heads each)
+  float rq[2][4];                       // per-io-wave sums of squares, alternating with the votes
+  int iob;                              // the io waves' own barrier: arrivals so far
   ll::Sync sync;
 };
 
-// a 16-column weight tile: wave w takes K slice w of 4 (NF fragments of 32)
-template <int NF>
-struct WT {
-  u16x8 f[NF];
-};
-template <int NF>
-__device__ __forceinline__ void load_wt(WT<NF>& t, const void* w, int tile, int K) {
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const __amdgpu_buffer_rsrc_t r = ro_rsrc(w);
-  const int s0 = (tile * 16 * K + wave * NF * 512) * 2;  // uniform: scalar offset
+// the layer table through the constant address space: scalar loads (a generic load of it would be a vector load,
+// since the kernel's own stores might alias it, and would then wait behind every weight load in flight)
+__device__ __forceinline__ M3xBackboneLayer layer_at(const M3xBackboneLayer* t, int l) {
+  typedef const uint64_t __attribute__((address_space(4)))* CW;
+  static_assert(sizeof(M3xBackboneLayer) == 9 * sizeof(uint64_t), "nine pointers");
+  const CW p = (CW)(t + l);
+  uint64_t w[9];
 #pragma unroll
-  for (int f = 0; f < NF; ++f) t.f[f] = bld16(r, 16 * lane, s0 + f * 1024);
+  for (int i = 0; i < 9; ++i) w[i] = p[i];
+  M3xBackboneLayer L;
+  __builtin_memcpy(&L, w, sizeof L);
+  return L;
+}
+
+// the q|k|v tile of workgroup wg: XCD x = wg % 8 holds q heads 2x, 2x+1 (tiles 16x ..), key head x, value head x
+__device__ __forceinline__ int qkv_tile(int wg) {
+  const int x = wg & 7, j = wg >> 3;
+  return j < 16 ? 16 * x + j : (j < 24 ? 128 + 8 * x + (j - 16) : 192 + 8 * x + (j - 24));
+}
+
+// a 16-column weight tile over fragments f0 .. f0 + 4 NF - 1 of its K (32 each): projecting wave w takes NF of them
+// A load that is not needed (no next layer, no gate|up pair) still issues, through an empty buffer resource: it
+// moves no data and returns zeros, and every path keeps the same count of loads in flight, so the compiler's wait
+// before each use stays exact (a conditional load would make it wait for everything issued since).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t opt_rsrc(const void* p, bool on) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, on ? 0x7fffffff : 0, 0x00020000);
+}
+template <int NF>
+__device__ __forceinline__ void load_wt(u16x8* t, const void* w, int tile, int K, int f0, bool on = true) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const __amdgpu_buffer_rsrc_t r = opt_rsrc(w, on);
+  const int s0 = (tile * 16 * K + (f0 + wave * NF) * 512) * 2;  // uniform: scalar offset
+#pragma unroll
+  for (int f = 0; f < NF; ++f) t[f] = bld16(r, 16 * lane, s0 + f * 1024);
 }
 // W tile x b^T for the single row b (the MFMA's other 15 rows are zero: lanes l % 16 != 0 feed zeros)
 template <int NF>
-__device__ __forceinline__ f32x4_t mma_row(const WT<NF>& t, const uint16_t* b) {
+__device__ __forceinline__ f32x4_t mma_row(const u16x8* t, const uint16_t* b) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const bool live = (lane & 15) == 0;
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
@@ -126,11 +162,11 @@ __device__ __forceinline__ f32x4_t mma_row(const WT<NF>& t, const uint16_t* b) {
   for (int f = 0; f < NF; ++f) {
     const int k = (wave * NF + f) * 32 + 8 * (lane >> 4);
     const u16x8 bv = *reinterpret_cast<const u16x8*>(&b[live ? k : 0]);
-    acc = mfma16x16x32<M3X_BF16>(t.f[f], live ? bv : u16x8{}, acc);
+    acc = mfma16x16x32<M3X_BF16>(t[f], live ? bv : u16x8{}, acc);
   }
   return acc;
 }
-// the four waves' partials of column c (slot order, fp32): thread c < 16 gets the tile's column c
+// the four projecting waves' partials of column c (slot order, fp32): io thread c < 16 gets the tile's column c
 __device__ __forceinline__ void put_part(Smem& sm, int a, f32x4_t acc) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if ((lane & 15) == 0) {
@@ -141,42 +177,127 @@ __device__ __forceinline__ void put_part(Smem& sm, int a, f32x4_t acc) {
 __device__ __forceinline__ float get_part(const Smem& sm, int a, int c) {
   return ((sm.part[a][0][c] + sm.part[a][1][c]) + sm.part[a][2][c]) + sm.part[a][3][c];
 }
-// LL store of a tile's 16 bf16 outputs (thread c < 16 holds column c): 8 words from the even threads
-__device__ __forceinline__ void st_tile(__amdgpu_buffer_rsrc_t rs, int base, int tile, uint16_t v, uint32_t tag) {
-  const int c = threadIdx.x;
-  const uint32_t nb = (uint32_t)__shfl_down((int)v, 1, 64);
-  if (c < 16 && (c & 1) == 0) ll_st8(rs, base + tile * 8 + c / 2, (uint32_t)v | (nb << 16), tag);
+// the workgroup's o unit (workgroups 0..127: 8 fragments per projecting wave, the rest read as zeros) or down unit
+// (128..255: 12 fragments), in one register slot
+constexpr int NOD_F = KD / 32 / 4;  // 12
+__device__ __forceinline__ void load_od(u16x8 (&t)[NOD_F], const M3xBackboneLayer& L, bool ow, int tu, int kh) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  constexpr int NOF = KO / 32 / 4;  // 8
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(ow ? L.wo : L.wd), 0, ow ? DM * H * HD * 2 : DM * FF * 2, 0x00020000);
+  const int s0 = ow ? (tu * 16 * (H * HD) + (kh * (KO / 32) + wave * NOF) * 512) * 2
+                    : (tu * 16 * FF + (kh * (KD / 32) + wave * NOD_F) * 512) * 2;
+#pragma unroll
+  for (int f = 0; f < NOD_F; ++f) t[f] = bld16(r, 16 * lane + (ow && f >= NOF ? ll::OOB : 0), s0 + f * 1024);
 }
 
-// x = dt(x + a) with a from an LL buffer of DM bf16 (one 16-byte chunk of 4 per thread), then sm.inv = its 1 / rms
-// (fp32 sum of squares: each thread's 4 in order, the wave's xor tree, then the 4 waves in order)
-__device__ __forceinline__ bool add_row(Smem& sm, int& vph, __amdgpu_buffer_rsrc_t rs, int base, uint32_t tag,
-                                        int probe, float eps) {
-  const int t = threadIdx.x;
-  const bool ok = ll_poll16<1>(
-      sm.sync, vph, rs, base + 2 * t, [](int) { return 0; }, 1, probe, [](int) { return true; }, tag,
-      [&](int, uint32_t p0, uint32_t p1) {
-        const uint16_t av[4] = {(uint16_t)(p0 & 0xffff), (uint16_t)(p0 >> 16), (uint16_t)(p1 & 0xffff),
-                                (uint16_t)(p1 >> 16)};
+// the split's cached keys and values: rows past the split's n keys read as zeros (an out-of-range offset: no
+// traffic), so the P.V tile's unused keys are zero times zero
+__device__ __forceinline__ void load_kv(u16x8 (&kr)[KVN], u16x8 (&vr)[KVN], const M3xBackboneLayer& L, long off,
+                                        long sk_t, int cap, int k0, int n, bool on = true) {
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((uint16_t*)L.kc + off, 0,
+                                                                      on ? (int)(cap * sk_t * 2) : 0, 0x00020000),
+                               rv = __builtin_amdgcn_make_buffer_rsrc((uint16_t*)L.vc + off, 0,
+                                                                      on ? (int)(cap * sk_t * 2) : 0, 0x00020000);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sm.x[4 * t + e] = f2bf(bf2f(sm.x[4 * t + e]) + bf2f(av[e]));
-      });
-  return ok;
+  for (int i = 0; i < KVN; ++i) {
+    const int c = threadIdx.x + NM * i, j = c / (HD / 8), d = 8 * (c % (HD / 8));
+    const int o = j < n ? (int)(((long)(k0 + j) * sk_t + d) * 2) : ll::OOB;
+    kr[i] = bld16(rk, o, 0);
+    vr[i] = bld16(rv, o, 0);
+  }
 }
-__device__ __forceinline__ void row_inv(Smem& sm, float eps) {
+// the layer's q_norm weight (8 per projecting thread 0-15) and k_norm weight (16-31); zeros elsewhere
+__device__ __forceinline__ void load_nw(u16x8& nq, u16x8& nk, const M3xBackboneLayer& L, bool on) {
   const int t = threadIdx.x;
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(L.wq), 0, on ? HD * 2 : 0,
+                                                                      0x00020000),
+                               rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(L.wk), 0, on ? HD * 2 : 0,
+                                                                      0x00020000);
+  nq = bld16(rq, t < 16 ? 16 * t : ll::OOB, 0);
+  nk = bld16(rk, t >= 16 && t < 32 ? 16 * (t - 16) : ll::OOB, 0);
+}
+
+// One barrier: every wave's vote (true iff every wave's ok) and, from the io waves, the row's sum of squares (each io
+// thread's 4 in order, the wave's xor tree, the 4 io waves in order); every thread (both roles) gets 1 / rms in inv.
+template <bool IO>
+__device__ __forceinline__ bool vote_rms(Smem& sm, int& ph, bool ok, float q, float eps, float& inv) {
+  const int w = threadIdx.x >> 6;
+  const bool bad = __ballot(!ok) != 0;
+  if (IO) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) q = q + __shfl_xor(q, o, 64);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    sm.sync.vote[ph][w] = bad;
+    if (IO) sm.rq[ph][w - NM / 64] = q;
+  }
+  __syncthreads();
+  int any = 0;
+#pragma unroll
+  for (int i = 0; i < NT / 64; ++i) any |= sm.sync.vote[ph][i];
+  inv = 1.0f / sqrtf((((sm.rq[ph][0] + sm.rq[ph][1]) + sm.rq[ph][2]) + sm.rq[ph][3]) / (float)DM + eps);
+  ph ^= 1;
+  return __builtin_amdgcn_readfirstlane(!any) != 0;
+}
+
+// The io waves' own barrier (the projecting waves take no part, so a burst of their loads never holds it up): an
+// LDS arrival counter that only grows; the call returns once all four io waves have arrived k times. LDS writes
+// before it are visible after it (each wave's writes are done before its arrival). False after `limit` rounds.
+__device__ __forceinline__ bool io_bar(Smem& sm, int& k, unsigned limit) {
+  k += NM / 64;
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  if ((threadIdx.x & 63) == 0) atomicAdd(&sm.iob, 1);
+  for (unsigned s = 0;; ++s) {
+    if (__hip_atomic_load(&sm.iob, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= k) break;
+    if (s >= limit) return false;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  asm volatile("" ::: "memory");
+  return true;
+}
+
+// io thread ti: x[4 ti .. 4 ti + 3] += dt(the K-half partials summed in order); returns their sum of squares
+__device__ __forceinline__ float add_quarters(Smem& sm, int ti, const float (&pv)[KQ][4]) {
   float q = 0.f;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const float v = bf2f(sm.x[4 * t + e]);
+    float o = pv[0][e];
+#pragma unroll
+    for (int h = 1; h < KQ; ++h) o = o + pv[h][e];
+    const uint16_t xv = f2bf(bf2f(sm.x[4 * ti + e]) + bf2f(f2bf(o)));
+    sm.x[4 * ti + e] = xv;
+    const float v = bf2f(xv);
     q = q + v * v;
   }
+  return q;
+}
+__device__ __forceinline__ float row_sq(const Smem& sm, int ti) {
+  float q = 0.f;
 #pragma unroll
-  for (int o = 1; o < 64; o <<= 1) q = q + __shfl_xor(q, o, 64);
-  if ((t & 63) == 0) sm.red[0][t >> 6] = q;
-  __syncthreads();
-  if (t == 0) sm.inv = 1.0f / sqrtf((((sm.red[0][0] + sm.red[0][1]) + sm.red[0][2]) + sm.red[0][3]) / (float)DM + eps);
-  __syncthreads();
+  for (int e = 0; e < 4; ++e) {
+    const float v = bf2f(sm.x[4 * ti + e]);
+    q = q + v * v;
+  }
+  return q;
+}
+// io wave: poll the K-half partials of columns 4 ti .. 4 ti + 3 (two 16-byte chunks per half)
+__device__ __forceinline__ bool poll_quarters(unsigned limit, __amdgpu_buffer_rsrc_t rs, int base, int ti, int probe,
+                                              uint32_t tag, float (&pv)[KQ][4]) {
+  return ll_poll16_w<2 * KQ>(
+      limit, rs, base + 4 * ti, [](int i) { return (i >> 1) * DM + 2 * (i & 1); }, 2 * KQ, probe,
+      [](int) { return true; }, tag, [&](int i, uint32_t p0, uint32_t p1) {
+        pv[i >> 1][2 * (i & 1)] = __uint_as_float(p0);
+        pv[i >> 1][2 * (i & 1) + 1] = __uint_as_float(p1);
+      });
+}
+// projecting wave 0: LL store of a tile's 16 bf16 outputs (thread c < 16 holds column c): 8 words from the even
+// threads. The tiles' outputs leave from the projecting waves, which never poll, so no poll waits behind a store.
+__device__ __forceinline__ void st_tile(__amdgpu_buffer_rsrc_t rs, int base, int tile, uint16_t v, uint32_t tag) {
+  const int t = threadIdx.x;
+  const uint32_t nb = (uint32_t)__shfl_down((int)v, 1, 64);
+  if (t < 16 && (t & 1) == 0) ll_st8(rs, base + tile * 8 + t / 2, (uint32_t)v | (nb << 16), tag);
 }
 }  // namespace bb
 
@@ -185,261 +306,100 @@ using namespace bb;
 __global__ __launch_bounds__(NT, 1) void backbone_run_kernel(const M3xBackboneRun a) {
   __shared__ Smem sm;
   const int wg = blockIdx.x, tid = threadIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const uint32_t epoch = (uint32_t)a.sync[0];
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(a.xchg, 0, (int)(X_WORDS * 8), 0x00020000);
-  const bool od = wg >= NWG - NOD;    // an o / down workgroup
-  const int t_od = wg - (NWG - NOD);  // its tile
-  const bool gu = wg < NGU;           // a gate|up workgroup
-  const int ih = wg / SPLITS, is = wg % SPLITS;  // the attention item: kv head, split
+  const bool gu = wg < NGU;              // a gate|up workgroup
+  const bool ow = wg < NOD, dw = !ow;    // an o unit's, else a down unit's workgroup
+  const int tq = qkv_tile(wg);           // its q|k|v tile
+  const int tu = (wg % NOD) >> 1, kh = wg & 1;  // its o or down unit: 16-column tile, K half
+  const int ih = wg & (KV - 1), is = wg / KV;   // its attention item: kv head (= its XCD), split
   // the row's slot and position (the host guarantees 0 <= pos < cap; the clamp keeps every access in the slot)
   const long slot = a.slots[0];
   const int pos = min(max(a.pos[0], 0), a.cap - 1);
   const int S = max(16, (((pos + 1 + SPLITS - 1) / SPLITS) + 15) / 16 * 16);
   const int k0 = is * S, n = max(min(k0 + S, pos + 1) - k0, 0);  // the item's keys k0 .. k0 + n - 1
   const bool own_pos = k0 <= pos && pos < k0 + S;
-  const float scale = a.scale;
+  const long kvoff = slot * a.sk_s + (long)ih * a.sk_h;
   bool ok = true;
   int vph = 0;
-  // stamp k of layer l at slot 16 l + k (profiling only)
-  auto stamp = [&](int slot) {
-    if (a.prof && tid == 0) a.prof[(long)wg * 512 + slot] = __builtin_amdgcn_s_memrealtime();
-  };
 
-  if (tid == 0) sm.sync.spin = a.spin_limit ? a.spin_limit : ll::SPIN_LIMIT;
-  for (int i = tid; i < DM / 8; i += NT)
-    *reinterpret_cast<u16x8*>(&sm.x[8 * i]) = ld16((const uint16_t*)a.x + 8 * i);
-  __syncthreads();
+  if (tid == 0) {
+    ll::sync_init(sm.sync, a.spin_limit);
+    sm.iob = 0;
+  }
+  if (tid >= NM) {
+    const int ti = tid - NM;
+    *reinterpret_cast<uint2*>(&sm.x[4 * ti]) = *reinterpret_cast<const uint2*>((const uint16_t*)a.x + 4 * ti);
+    if (ti < 32)  // cos and sin at the position, for every layer
+      *reinterpret_cast<u16x8*>(&sm.cs[ti >> 4][8 * (ti & 15)]) =
+          ld16((const uint16_t*)(ti < 16 ? a.cos : a.sin) + (long)pos * a.s_cos + 8 * (ti & 15));
+  }
 
-  for (int l = 0; l < a.layers && ok; ++l) {
-    const M3xBackboneLayer L = a.layer[l];
-    const int par = l & 1;
-    const uint32_t s0 = 1u + (uint32_t)(STEPS * l);
-    const uint32_t t_qkv = (epoch << 12) | s0, t_part = t_qkv + 1, t_att = t_qkv + 2, t_o = t_qkv + 3,
-                   t_gu = t_qkv + 4, t_dn = t_qkv + 5;
-    const int b_qkv = O_QKV + par * W_QKV, b_part = O_PART + par * W_PART, b_att = O_ATT + par * W_ATT,
-              b_o = O_O + par * W_O, b_gu = O_GU + par * W_GU, b_dn = O_DN + par * W_DN;
-
-    // ---- S1: the layer's input row -> q|k|v tile wg
+  if (__builtin_amdgcn_readfirstlane(tid) < NM) {
+    // ================= projecting waves: the MFMA tiles and their epilogues, the weights and the split's keys and
+    // values in registers ahead of use. Refills (each after its slot's tile is used) go right before the io waves'
+    // longest stretches, since a burst of loads holds the issuing wave until the memory system takes it:
+    //   after S1: the next layer's q|k|v and q/k norm weights, this layer's gate|up pair and o or down unit;
+    //   after S5: the next layer's keys and values, which go to LDS after S6.
+    // Registers (per projecting thread, 16 B each): q|k|v 8, the o or down unit 12, one 16-chunk slot shared by
+    // the split's keys / values (until S6) and the gate|up pair (S1..S5), the norm weights 2 (no array indexed by a
+    // thread-dependent value: that would move it to LDS).
+    u16x8 wq[8], wod[NOD_F], ka[KVN], va[KVN], nq, nk;
     {
-      WT<8> wt;
-      load_wt<8>(wt, L.wqkv, wg, DM);
-      stamp(16 * l + 0);
-      if (l > 0) {
-        const uint32_t t_prev = (epoch << 12) | (s0 - 1);
-        ok = add_row(sm, vph, rs, O_DN + (1 - par) * W_DN, t_prev, a.probe, a.eps);
-        if (!ok) break;
-      }
-      stamp(16 * l + 1);
-      row_inv(sm, a.eps);
-      const float inv = sm.inv;
-      if (l == 0) {
-        // the input RMSNorm applied to the row (the packed weight of layer 0 is the plain one)
-        const __amdgpu_buffer_rsrc_t rw = ro_rsrc(a.w_in0);
-        for (int i = tid; i < DM / 8; i += NT) {
-          const u16x8 w8 = bld16(rw, 16 * i, 0);
+      const M3xBackboneLayer L = layer_at(a.layer, 0);
+      load_kv(ka, va, L, kvoff, a.sk_t, a.cap, k0, n);
+      load_nw(nq, nk, L, true);
+      load_wt<8>(wq, L.wqkv, tq, DM, 0);
 #pragma unroll
-          for (int e = 0; e < 8; ++e)
-            sm.b[8 * i + e] = f2bf(bf2f(f2bf(bf2f(sm.x[8 * i + e]) * inv)) * bf2f(w8.v[e]));
-        }
-      } else {
-        for (int i = tid; i < DM / 8; i += NT)
-          *reinterpret_cast<u16x8*>(&sm.b[8 * i]) = *reinterpret_cast<const u16x8*>(&sm.x[8 * i]);
+      for (int i = 0; i < KVN; ++i) {
+        const int c = tid + NM * i, j = c / (HD / 8), d = 8 * (c % (HD / 8));
+        *reinterpret_cast<u16x8*>(&sm.kt[j][d]) = ka[i];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sm.vt[d + e][j] = va[i].v[e];
       }
-      __syncthreads();
-      put_part(sm, 0, mma_row<8>(wt, sm.b));
-      __syncthreads();
-      uint16_t v = 0;
-      if (tid < 16) {
-        const float s = get_part(sm, 0, tid);
-        v = f2bf(l == 0 ? s : inv * s);  // the folded norm's row scale (the plain weight at layer 0)
-      }
-      st_tile(rs, b_qkv, wg, v, t_qkv);
-      stamp(16 * l + 2);
+      if (tid < 16) *reinterpret_cast<u16x8*>(&sm.nw[0][8 * tid]) = nq;
+      else if (tid < 32) *reinterpret_cast<u16x8*>(&sm.nw[1][8 * (tid - 16)]) = nk;
     }
-
-    // ---- S2: attention item (ih, is): keys k0 .. k0 + n - 1 of the slot's kv head ih
-    {
-      // the split's cached keys and values load first (rows past the item clamp to the position: valid, unused)
-      const uint16_t* kb = (const uint16_t*)L.kc + slot * a.sk_s + (long)ih * a.sk_h;
-      const uint16_t* vb = (const uint16_t*)L.vc + slot * a.sk_s + (long)ih * a.sk_h;
-      u16x8 kr[SMAX * HD / 8 / NT], vr[SMAX * HD / 8 / NT];
-#pragma unroll
-      for (int i = 0; i < SMAX * HD / 8 / NT; ++i) {
-        const int c = tid + NT * i, j = c / (HD / 8), d = 8 * (c % (HD / 8));
-        const long p = min(k0 + j, pos);
-        kr[i] = ld16(kb + p * a.sk_t + d);
-        vr[i] = ld16(vb + p * a.sk_t + d);
-      }
-      // q heads 2 ih, 2 ih + 1, the key and the value of kv head ih, as projected
-      const int part = tid >> 5, c4 = tid & 31;  // 16-byte chunks: q 0..63, k 64..95, v 96..127
-      const int col = part < 2 ? 2 * ih * HD + 4 * tid : (part == 2 ? H * HD + ih * HD : (H + KV) * HD + ih * HD) + 4 * c4;
-      ok = ll_poll16<1>(
-          sm.sync, vph, rs, b_qkv + col / 2, [](int) { return 0; }, 1, a.probe, [&](int) { return tid < 128; }, t_qkv,
-          [&](int, uint32_t p0, uint32_t p1) {
-            *reinterpret_cast<uint2*>(&sm.raw[4 * tid]) = uint2{p0, p1};
-          });
-      if (!ok) break;
-      stamp(16 * l + 3);
-#pragma unroll
-      for (int i = 0; i < SMAX * HD / 8 / NT; ++i) {
-        const int c = tid + NT * i, j = c / (HD / 8), d = 8 * (c % (HD / 8));
-        *reinterpret_cast<u16x8*>(&sm.u.kv.kt[j][d]) = kr[i];
-        *reinterpret_cast<u16x8*>(&sm.u.kv.vt[j][d]) = vr[i];
-      }
+    __syncthreads();  // the set-up's LDS
+    float inv = 0.f;
+    for (int l = 0; l < a.layers; ++l) {
+      const bool nx = l + 1 < a.layers;
+      const M3xBackboneLayer L = layer_at(a.layer, l), N = layer_at(a.layer, nx ? l + 1 : l);
+      const int par = l & 1;
+      const uint32_t t_qkv = (epoch << 12) | (1u + (uint32_t)(STEPS * l));
+      const int b_qkv = O_QKV + par * W_QKV, b_o = O_O + par * W_O, b_gu = O_GU + par * W_GU, b_dn = O_DN + par * W_DN;
+      // S1
+      if (!(ok = vote_rms<false>(sm, vph, true, 0.f, a.eps, inv))) break;
+      if (l == 0) __syncthreads();  // the normed row in sm.b
+      put_part(sm, 0, mma_row<8>(wq, l == 0 ? sm.b : sm.x));
       __syncthreads();
-      stamp(16 * l + 13);
-      // q/k norm + RoPE: lanes 0-15 q head 2 ih, 16-31 q head 2 ih + 1, 32-47 the key (one DPP row each)
-      if (wave == 0) {
-        const int grp = lane >> 4, t16 = lane & 15;
-        const int g3 = min(grp, 2);
-        float xv[8];
-        const u16x8 r8 = *reinterpret_cast<const u16x8*>(&sm.raw[g3 * HD + 8 * t16]);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) xv[e] = bf2f(r8.v[e]);
-        const u16x8 wv = ld16((const uint16_t*)(g3 < 2 ? L.wq : L.wk) + 8 * t16);
-        const u16x8 cv = ld16((const uint16_t*)a.cos + (long)pos * a.s_cos + 8 * t16);
-        const u16x8 sv = ld16((const uint16_t*)a.sin + (long)pos * a.s_cos + 8 * t16);
-        const u16x8 ov = qk_norm_rope8<HD>(xv, wv, cv, sv, a.eps, t16);
-        if (grp < 2) {
-          *reinterpret_cast<u16x8*>(&sm.qb[grp][8 * t16]) = ov;
-        } else if (grp == 2) {
-          *reinterpret_cast<u16x8*>(&sm.kn[8 * t16]) = ov;
-        }
-      }
-      __syncthreads();
-      stamp(16 * l + 14);
-      // the new key and value into the cache, by the item that holds the position
-      if (own_pos && tid < 32) {
-        const int d = 8 * (tid & 15);
-        if (tid < 16) st16((uint16_t*)L.kc + slot * a.sk_s + (long)ih * a.sk_h + (long)pos * a.sk_t + d,
-                           *reinterpret_cast<const u16x8*>(&sm.kn[d]));
-        else st16((uint16_t*)L.vc + slot * a.sk_s + (long)ih * a.sk_h + (long)pos * a.sk_t + d,
-                  *reinterpret_cast<const u16x8*>(&sm.raw[3 * HD + d]));
-      }
-      // scores: thread t takes q head t / 128 and key t % 128 (the new key at the position)
-      const int g = tid >> 7, jl = tid & (SMAX - 1);
       {
-        float s = -INFINITY;
-        if (jl < n) {
-          const uint16_t* kp = (k0 + jl == pos) ? sm.kn : &sm.u.kv.kt[jl][0];
-          float d = 0.f;
-#pragma unroll
-          for (int c = 0; c < HD / 8; ++c) {
-            const u16x8 k8 = *reinterpret_cast<const u16x8*>(&kp[8 * c]);
-            const u16x8 q8 = *reinterpret_cast<const u16x8*>(&sm.qb[g][8 * c]);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) d = fmaf(bf2f(q8.v[e]), bf2f(k8.v[e]), d);
-          }
-          s = d * scale;
+        uint16_t v = 0;
+        if (tid < 16) {
+          const float s = get_part(sm, 0, tid);
+          v = f2bf(l == 0 ? s : inv * s);  // the folded norm's row scale (the plain weight at layer 0)
         }
-        float m = s;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-        if (lane == 0) sm.red[0][wave] = m;
-        __syncthreads();
-        m = fmaxf(sm.red[0][2 * g], sm.red[0][2 * g + 1]);
-        const float p = jl < n ? expf(s - m) : 0.f;
-        sm.sc[g][jl] = p;
-        float sum = p;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) sum = sum + __shfl_xor(sum, o, 64);
-        if (lane == 0) sm.red[1][wave] = sum;
-        __syncthreads();
-        sum = sm.red[1][2 * g] + sm.red[1][2 * g + 1];
-        // P.V: thread t takes q head t / 128 and dimension t % 128 (the new value at the position)
-        const int d = jl;
-        // the new value stands in the tile's row pos - k0 (the tile's own row there is the cache's stale entry)
-        if (own_pos && tid < HD) sm.u.kv.vt[pos - k0][tid] = sm.raw[3 * HD + tid];
-        __syncthreads();
-        stamp(16 * l + 15);
-        // four running sums over keys j = 4 i + r (a fixed order), so four loads are in flight at once
-        float ac[4] = {0.f, 0.f, 0.f, 0.f};
-        const int n4 = n & ~3;
-        for (int j = 0; j < n4; j += 4) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) ac[r] = fmaf(sm.sc[g][j + r], bf2f(sm.u.kv.vt[j + r][d]), ac[r]);
-        }
-        for (int j = n4; j < n; ++j) ac[j & 3] = fmaf(sm.sc[g][j], bf2f(sm.u.kv.vt[j][d]), ac[j & 3]);
-        const float acc = (ac[0] + ac[1]) + (ac[2] + ac[3]);
-        const int w0 = b_part + wg * PW + g * (HD + 2);
-        if (d == 0) {
-          ll_st8(rs, w0, __float_as_uint(n > 0 ? m : -INFINITY), t_part);
-          ll_st8(rs, w0 + 1, __float_as_uint(n > 0 ? sum : 0.f), t_part);
-        }
-        ll_st8(rs, w0 + 2 + d, __float_as_uint(acc), t_part);
+        st_tile(rs, b_qkv, tq, v, t_qkv);
       }
-      __syncthreads();  // the K/V area is reused by the combine
-      stamp(16 * l + 4);
-    }
-
-    // ---- S3: combine of q head wg (workgroups 0..15): its 32 partials in split order
-    if (wg < H) {
-      // thread t reads split t / 8, words t % 8 + 8 i of the q head's 130 (i < 17)
-      const int hk = wg >> 1, gq = wg & 1, sp = tid >> 3, k8 = tid & 7;
-      constexpr int NW = (HD + 2 + 7) / 8;
-      ok = ll_poll8<NW>(
-          sm.sync, vph, rs, b_part + (hk * SPLITS + sp) * PW + gq * (HD + 2) + k8, [](int i) { return 8 * i; }, NW,
-          a.probe, [&](int i) { return k8 + 8 * i < HD + 2; }, t_part,
-          [&](int i, uint32_t p) { sm.u.comb[sp][k8 + 8 * i] = __uint_as_float(p); });
-      if (!ok) break;
-      stamp(16 * l + 5);
-      // the splits' weights exp(m_s - M) once per split (M the largest m_s of the non-empty ones)
-      if (tid < SPLITS) {
-        float M = sm.u.comb[tid][0];
-#pragma unroll
-        for (int o = 1; o < SPLITS; o <<= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-        sm.cw[tid] = sm.u.comb[tid][1] > 0.f ? expf(sm.u.comb[tid][0] - M) : 0.f;
+      load_wt<8>(wq, N.wqkv, tq, DM, 0, nx);
+      load_nw(nq, nk, N, nx);
+      load_wt<8>(ka, L.wg, gu ? wg : 0, DM, 0, gu);
+      load_wt<8>(va, L.wu, gu ? wg : 0, DM, 0, gu);
+      load_od(wod, L, ow, tu, kh);
+      // S2, S3: io waves only
+      // S4 (o units)
+      if (ow) {
+        if (!(ok = wg_all(sm.sync, true, vph))) break;
+        put_part(sm, 0, mma_row<KO / 32 / 4>(wod, sm.b));
+        __syncthreads();
+        if (tid < 16) ll_st8(rs, b_o + kh * DM + 16 * tu + tid, __float_as_uint(get_part(sm, 0, tid)), t_qkv + 3);
       }
-      __syncthreads();
-      if (tid < HD) {
-        float L = 0.f, o = 0.f;
-        for (int s = 0; s < SPLITS; ++s) {
-          const float w = sm.cw[s];
-          L = L + sm.u.comb[s][1] * w;
-          o = o + sm.u.comb[s][2 + tid] * w;
-        }
-        const uint16_t v = f2bf(o / L);
-        const uint32_t nb = (uint32_t)__shfl_down((int)v, 1, 64);
-        if ((tid & 1) == 0) ll_st8(rs, b_att + (wg * HD + tid) / 2, (uint32_t)v | (nb << 16), t_att);
-      }
-      __syncthreads();
-      stamp(16 * l + 6);
-    }
-
-    // ---- S4: o projection tile (workgroups 192..255), K = 2048
-    if (od) {
-      WT<16> wt;
-      load_wt<16>(wt, L.wo, t_od, H * HD);
-      ok = ll_poll16<2>(
-          sm.sync, vph, rs, b_att + 2 * tid, [](int i) { return 2 * NT * i; }, 2, a.probe,
-          [](int) { return true; }, t_att, [&](int i, uint32_t p0, uint32_t p1) {
-            *reinterpret_cast<uint2*>(&sm.b[4 * (tid + NT * i)]) = uint2{p0, p1};
-          });
-      if (!ok) break;
-      stamp(16 * l + 7);
-      __syncthreads();
-      put_part(sm, 0, mma_row<16>(wt, sm.b));
-      __syncthreads();
-      st_tile(rs, b_o, t_od, tid < 16 ? f2bf(get_part(sm, 0, tid)) : (uint16_t)0, t_o);
-      stamp(16 * l + 8);
-    }
-
-    // ---- S5: x += o (every workgroup), gate|up tile pair wg with the folded norm and SwiGLU (0..191)
-    {
-      WT<8> wg_, wu_;
+      // S5: the gate|up pair (a workgroup without one multiplies the zeros its empty loads returned: every path
+      // then waits for the same loads); the sm.x reads end before the io waves pass the barrier below
+      if (!(ok = vote_rms<false>(sm, vph, true, 0.f, a.eps, inv))) break;
+      put_part(sm, 0, mma_row<8>(ka, sm.x));
+      put_part(sm, 1, mma_row<8>(va, sm.x));
       if (gu) {
-        load_wt<8>(wg_, L.wg, wg, DM);
-        load_wt<8>(wu_, L.wu, wg, DM);
-      }
-      ok = add_row(sm, vph, rs, b_o, t_o, a.probe, a.eps);
-      if (!ok) break;
-      stamp(16 * l + 9);
-      row_inv(sm, a.eps);
-      if (gu) {
-        const float inv = sm.inv;
-        put_part(sm, 0, mma_row<8>(wg_, sm.x));
-        put_part(sm, 1, mma_row<8>(wu_, sm.x));
         __syncthreads();
         uint16_t v = 0;
         if (tid < 16) {
@@ -447,38 +407,295 @@ __global__ __launch_bounds__(NT, 1) void backbone_run_kernel(const M3xBackboneRu
           const float u = rnd<M3X_BF16>(inv * get_part(sm, 1, tid));
           v = f2bf(rnd<M3X_BF16>(silu16(gt)) * u);
         }
-        st_tile(rs, b_gu, wg, v, t_gu);
+        st_tile(rs, b_gu, wg, v, t_qkv + 4);
+      }
+      load_kv(ka, va, N, kvoff, a.sk_t, a.cap, k0, n, nx);
+      // S6 (down units)
+      if (dw) {
+        if (!(ok = wg_all(sm.sync, true, vph))) break;
+        put_part(sm, 0, mma_row<NOD_F>(wod, sm.b));
+        __syncthreads();
+        if (tid < 16) ll_st8(rs, b_dn + kh * DM + 16 * tu + tid, __float_as_uint(get_part(sm, 0, tid)), t_qkv + 5);
+      }
+      // the next layer's keys (rows), values (transposed) and norm weights into LDS: the io waves finished this
+      // layer's attention before the S5 barrier, and start the next one after the next S1 barrier
+#pragma unroll
+      for (int i = 0; i < KVN; ++i) {
+        const int c = tid + NM * i, j = c / (HD / 8), d = 8 * (c % (HD / 8));
+        *reinterpret_cast<u16x8*>(&sm.kt[j][d]) = ka[i];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sm.vt[d + e][j] = va[i].v[e];
+      }
+      if (tid < 16) *reinterpret_cast<u16x8*>(&sm.nw[0][8 * tid]) = nq;
+      else if (tid < 32) *reinterpret_cast<u16x8*>(&sm.nw[1][8 * (tid - 16)]) = nk;
+    }
+    if (ok) ok = wg_all(sm.sync, true, vph);  // the last layer's down
+  } else {
+    // ================= io waves: polls, norms, attention, combine
+    const int ti = tid - NM, iw = ti >> 6, lane = ti & 63, l16 = lane & 15, lg = lane >> 4;
+    __syncthreads();  // the set-up's LDS
+    const unsigned limit = __builtin_amdgcn_readfirstlane(sm.sync.spin);
+    const int probe = a.probe;
+    const float scale = a.scale;
+    int kb = 0;  // io_bar arrivals
+    auto stamp = [&](int s) {  // stamp s of layer l at slot 16 l + s (profiling only)
+      if (a.prof && ti == 0) a.prof[(long)wg * 512 + s] = __builtin_amdgcn_s_memrealtime();
+    };
+    for (int l = 0; l < a.layers; ++l) {
+      const M3xBackboneLayer L = layer_at(a.layer, l);
+      const int par = l & 1;
+      const uint32_t s0 = 1u + (uint32_t)(STEPS * l);
+      const uint32_t t_qkv = (epoch << 12) | s0, t_part = t_qkv + 1, t_att = t_qkv + 2, t_o = t_qkv + 3,
+                     t_gu = t_qkv + 4;
+      const int b_qkv = O_QKV + par * W_QKV, b_part = O_PART + par * W_PART, b_att = O_ATT + par * W_ATT,
+                b_o = O_O + par * W_O, b_gu = O_GU + par * W_GU;
+      bool okc = true;  // polls and io barriers between two votes
+      stamp(16 * l + 0);
+
+      // ---- S1: x += the previous layer's down, the row's RMS (the q|k|v tile and its epilogue run in the
+      // projecting waves)
+      float inv;
+      {
+        bool okw = true;
+        float q;
+        if (l > 0) {
+          float pv[KQ][4];
+          okw = poll_quarters(limit, rs, O_DN + (1 - par) * W_DN, ti, probe, (epoch << 12) | (s0 - 1), pv);
+          q = okw ? add_quarters(sm, ti, pv) : 0.f;
+        } else {
+          q = row_sq(sm, ti);
+        }
+        if (!(ok = vote_rms<true>(sm, vph, okw, q, a.eps, inv))) break;
+      }
+      stamp(16 * l + 1);
+      if (l == 0) {
+        // the input RMSNorm applied to the row (the packed weight of layer 0 is the plain one)
+        const uint2 w4 = *reinterpret_cast<const uint2*>((const uint16_t*)a.w_in0 + 4 * ti);
+        const uint16_t wv[4] = {(uint16_t)(w4.x & 0xffff), (uint16_t)(w4.x >> 16), (uint16_t)(w4.y & 0xffff),
+                                (uint16_t)(w4.y >> 16)};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sm.b[4 * ti + e] = f2bf(bf2f(f2bf(bf2f(sm.x[4 * ti + e]) * inv)) * bf2f(wv[e]));
+        __syncthreads();
+      }
+      __syncthreads();  // the projecting waves' partials (their x and sm.b reads end here)
+
+      // ---- S2: attention item (ih, is): keys k0 .. k0 + n - 1 of the slot's kv head ih (io waves only)
+      {
+        // q heads 2 ih, 2 ih + 1, the key and the value of kv head ih, as projected
+        const int part = ti >> 5, c4 = ti & 31;  // 16-byte chunks: q 0..63, k 64..95, v 96..127
+        const int col = part < 2 ? 2 * ih * HD + 4 * ti
+                                 : (part == 2 ? H * HD + ih * HD : (H + KV) * HD + ih * HD) + 4 * c4;
+        okc = ll_poll16_w<1>(
+            limit, rs, b_qkv + col / 2, [](int) { return 0; }, 1, probe, [&](int) { return ti < 128; }, t_qkv,
+            [&](int, uint32_t p0, uint32_t p1) { *reinterpret_cast<uint2*>(&sm.raw[4 * ti]) = uint2{p0, p1}; });
+        okc = io_bar(sm, kb, limit) && okc;
+      }
+      stamp(16 * l + 3);
+      // q/k norm + RoPE: lanes 0-15 q head 2 ih, 16-31 q head 2 ih + 1, 32-47 the key (one DPP row each)
+      if (iw == 0) {
+        const int g3 = min(lg, 2);
+        float xv[8];
+        const u16x8 r8 = *reinterpret_cast<const u16x8*>(&sm.raw[g3 * HD + 8 * l16]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xv[e] = bf2f(r8.v[e]);
+        const u16x8 wv = *reinterpret_cast<const u16x8*>(&sm.nw[g3 < 2 ? 0 : 1][8 * l16]);
+        const u16x8 cv = *reinterpret_cast<const u16x8*>(&sm.cs[0][8 * l16]);
+        const u16x8 sv = *reinterpret_cast<const u16x8*>(&sm.cs[1][8 * l16]);
+        const u16x8 ov = qk_norm_rope8<HD>(xv, wv, cv, sv, a.eps, l16);
+        if (lg < 2) {
+          *reinterpret_cast<u16x8*>(&sm.qb[lg][8 * l16]) = ov;
+        } else if (lg == 2) {
+          *reinterpret_cast<u16x8*>(&sm.kn[8 * l16]) = ov;
+        }
+      }
+      // the new value stands in the tile's column pos - k0 (the tile's own entry there is the cache's stale one)
+      if (own_pos && ti < HD) sm.vt[ti][pos - k0] = sm.raw[3 * HD + ti];
+      okc = io_bar(sm, kb, limit) && okc;
+      stamp(16 * l + 13);
+      // the new key and value into the cache, by the item that holds the position
+      if (own_pos && ti < 32) {
+        const int d = 8 * (ti & 15);
+        if (ti < 16) st16((uint16_t*)L.kc + kvoff + (long)pos * a.sk_t + d, *reinterpret_cast<const u16x8*>(&sm.kn[d]));
+        else st16((uint16_t*)L.vc + kvoff + (long)pos * a.sk_t + d, *reinterpret_cast<const u16x8*>(&sm.raw[3 * HD + d]));
+      }
+      {
+        // scores on MFMA: io wave w takes key blocks w and w + 4 (16 keys each); A = the two q heads (rows 0, 1),
+        // B = the block's keys (the new key at the position); lanes 0-15 end with key l16's two scores
+        float sc[2][2];
+#pragma unroll
+        for (int bs = 0; bs < 2; ++bs) {
+          const int b = iw + 4 * bs, j = 16 * b + l16;
+          sc[bs][0] = sc[bs][1] = -INFINITY;
+          if (16 * b < n) {
+            const uint16_t* kp = (k0 + j == pos) ? sm.kn : &sm.kt[j][0];
+            f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kc = 0; kc < HD / 32; ++kc) {
+              const u16x8 qa = l16 < 2 ? *reinterpret_cast<const u16x8*>(&sm.qb[l16 & 1][32 * kc + 8 * lg]) : u16x8{};
+              const u16x8 kv8 = *reinterpret_cast<const u16x8*>(&kp[32 * kc + 8 * lg]);
+              acc = mfma16x16x32<M3X_BF16>(qa, kv8, acc);
+            }
+            if (lane < 16 && j < n) {
+              sc[bs][0] = acc[0] * scale;
+              sc[bs][1] = acc[1] * scale;
+            }
+          }
+        }
+        float m0 = fmaxf(sc[0][0], sc[1][0]), m1 = fmaxf(sc[0][1], sc[1][1]);
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) {
+          m0 = fmaxf(m0, __shfl_xor(m0, o, 64));
+          m1 = fmaxf(m1, __shfl_xor(m1, o, 64));
+        }
+        if (lane == 0) {
+          sm.red[0][2 * iw] = m0;
+          sm.red[0][2 * iw + 1] = m1;
+        }
+        okc = io_bar(sm, kb, limit) && okc;
+        const float M0 = fmaxf(fmaxf(sm.red[0][0], sm.red[0][2]), fmaxf(sm.red[0][4], sm.red[0][6]));
+        const float M1 = fmaxf(fmaxf(sm.red[0][1], sm.red[0][3]), fmaxf(sm.red[0][5], sm.red[0][7]));
+        // probabilities in fp32; the P.V operand carries each as a bf16 pair (hi, lo = what bf16 left), so P.V is
+        // the fp32 product to ~16 bits; every block 0..7 is written (zeros past the split's keys)
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int bs = 0; bs < 2; ++bs) {
+          const int j = 16 * (iw + 4 * bs) + l16;
+          const bool live = lane < 16 && j < n;
+          const float p0 = live ? expf(sc[bs][0] - M0) : 0.f, p1 = live ? expf(sc[bs][1] - M1) : 0.f;
+          if (lane < 16) {
+            const uint16_t h0 = f2bf(p0), h1 = f2bf(p1);
+            sm.pb[0][j] = h0;
+            sm.pb[1][j] = h1;
+            sm.pb[2][j] = f2bf(p0 - bf2f(h0));
+            sm.pb[3][j] = f2bf(p1 - bf2f(h1));
+          }
+          s0 = s0 + p0;
+          s1 = s1 + p1;
+        }
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) {
+          s0 = s0 + __shfl_xor(s0, o, 64);
+          s1 = s1 + __shfl_xor(s1, o, 64);
+        }
+        if (lane == 0) {
+          sm.red[1][2 * iw] = s0;
+          sm.red[1][2 * iw + 1] = s1;
+        }
+        okc = io_bar(sm, kb, limit) && okc;
+        stamp(16 * l + 15);
+        // P.V on MFMA: io wave w takes dimensions 16 w .. and 16 (w + 4) ..; A = P's four rows, B = the values'
+        // transposed tile; lanes 0-15 end with dimension l16's sums: rows 0 + 2 for head 0, 1 + 3 for head 1
+        const int w0 = b_part + wg * PW;
+        const int nk = (n + 31) & ~31;
+#pragma unroll
+        for (int ds = 0; ds < 2; ++ds) {
+          const int db = iw + 4 * ds;
+          f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+          for (int kc = 0; kc < nk; kc += 32) {
+            const u16x8 pa = l16 < 4 ? *reinterpret_cast<const u16x8*>(&sm.pb[l16 & 3][kc + 8 * lg]) : u16x8{};
+            const u16x8 vb = *reinterpret_cast<const u16x8*>(&sm.vt[16 * db + l16][kc + 8 * lg]);
+            acc = mfma16x16x32<M3X_BF16>(pa, vb, acc);
+          }
+          if (lane < 16) {
+            ll_st8(rs, w0 + 2 + 16 * db + l16, __float_as_uint(acc[0] + acc[2]), t_part);
+            ll_st8(rs, w0 + (HD + 2) + 2 + 16 * db + l16, __float_as_uint(acc[1] + acc[3]), t_part);
+          }
+        }
+        if (ti < 2) {
+          const float M = ti == 0 ? M0 : M1;
+          const float Ls = ti == 0 ? ((sm.red[1][0] + sm.red[1][2]) + sm.red[1][4]) + sm.red[1][6]
+                                   : ((sm.red[1][1] + sm.red[1][3]) + sm.red[1][5]) + sm.red[1][7];
+          ll_st8(rs, w0 + ti * (HD + 2), __float_as_uint(n > 0 ? M : -INFINITY), t_part);
+          ll_st8(rs, w0 + ti * (HD + 2) + 1, __float_as_uint(n > 0 ? Ls : 0.f), t_part);
+        }
+      }
+      stamp(16 * l + 4);
+
+      // ---- S3: combine of q head 2 hk + gq (workgroups 0..15, on kv head hk's XCD): its 32 partials
+      if (wg < H) {
+        // io thread t reads split t / 8, words t % 8 + 8 i of the q head's 130 (i < 17)
+        const int hk = wg & (KV - 1), gq = wg / KV, sp = ti >> 3, k8 = ti & 7;
+        constexpr int NW = (HD + 2 + 7) / 8;
+        okc = ll_poll8_w<NW>(
+                  limit, rs, b_part + (hk + KV * sp) * PW + gq * (HD + 2) + k8, [](int i) { return 8 * i; }, NW,
+                  probe, [&](int i) { return k8 + 8 * i < HD + 2; }, t_part,
+                  [&](int i, uint32_t p) { sm.comb[sp][k8 + 8 * i] = __uint_as_float(p); }) &&
+              okc;
+        okc = io_bar(sm, kb, limit) && okc;
+        stamp(16 * l + 5);
+        // the splits' weights exp(m_s - M) (M the largest m_s; empty splits weigh 0)
+        if (ti < SPLITS) {
+          float M = sm.comb[ti][0];
+#pragma unroll
+          for (int o = 1; o < SPLITS; o <<= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+          sm.cw[ti] = sm.comb[ti][1] > 0.f ? expf(sm.comb[ti][0] - M) : 0.f;
+        }
+        okc = io_bar(sm, kb, limit) && okc;
+        if (ti < HD) {
+          // four chains over the splits s = 4 i + r (a fixed order), so the LDS reads pipeline
+          float Lr[4] = {0.f, 0.f, 0.f, 0.f}, orr[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int s = 0; s < SPLITS; ++s) {
+            const float w = sm.cw[s];
+            Lr[s & 3] = Lr[s & 3] + sm.comb[s][1] * w;
+            orr[s & 3] = orr[s & 3] + sm.comb[s][2 + ti] * w;
+          }
+          const float Ls = (Lr[0] + Lr[1]) + (Lr[2] + Lr[3]), o = (orr[0] + orr[1]) + (orr[2] + orr[3]);
+          const uint16_t v = f2bf(o / Ls);
+          const uint32_t nb = (uint32_t)__shfl_down((int)v, 1, 64);
+          if ((ti & 1) == 0) ll_st8(rs, b_att + ((2 * hk + gq) * HD + ti) / 2, (uint32_t)v | (nb << 16), t_att);
+        }
+        stamp(16 * l + 6);
+      }
+
+      // ---- S4 (o units, workgroups 0..127): tile tu's K half kh, the half's 8 heads of the attention output
+      if (ow) {
+        okc = ll_poll16_w<1>(
+                  limit, rs, b_att + kh * (KO / 2) + 2 * ti, [](int) { return 0; }, 1, probe, [](int) { return true; },
+                  t_att, [&](int, uint32_t p0, uint32_t p1) { *reinterpret_cast<uint2*>(&sm.b[4 * ti]) = uint2{p0, p1}; }) &&
+              okc;
+        if (!(ok = wg_all(sm.sync, okc, vph))) break;
+        okc = true;
+        stamp(16 * l + 7);
+        __syncthreads();  // the projecting waves' partials
+        stamp(16 * l + 8);
+      }
+
+      // ---- S5: x += o, the row's RMS (gate|up tile pair and SwiGLU in the projecting waves)
+      {
+        float pv[KQ][4];
+        const bool okw = poll_quarters(limit, rs, b_o, ti, probe, t_o, pv);
+        const float q = okw ? add_quarters(sm, ti, pv) : 0.f;
+        if (!(ok = vote_rms<true>(sm, vph, okw && okc, q, a.eps, inv))) break;
+      }
+      stamp(16 * l + 9);
+      if (gu) {
+        __syncthreads();  // the projecting waves' partials (their sm.x reads end here)
         stamp(16 * l + 10);
       }
-    }
 
-    // ---- S6: down projection tile (workgroups 192..255), K = 3072
-    if (od) {
-      WT<24> wt;
-      load_wt<24>(wt, L.wd, t_od, FF);
-      ok = ll_poll16<3>(
-          sm.sync, vph, rs, b_gu + 2 * tid, [](int i) { return 2 * NT * i; }, 3, a.probe,
-          [](int) { return true; }, t_gu, [&](int i, uint32_t p0, uint32_t p1) {
-            *reinterpret_cast<uint2*>(&sm.b[4 * (tid + NT * i)]) = uint2{p0, p1};
-          });
-      if (!ok) break;
-      stamp(16 * l + 11);
-      __syncthreads();
-      put_part(sm, 0, mma_row<24>(wt, sm.b));
-      __syncthreads();
-      st_tile(rs, b_dn, t_od, tid < 16 ? f2bf(get_part(sm, 0, tid)) : (uint16_t)0, t_dn);
-      stamp(16 * l + 12);
+      // ---- S6 (down units, workgroups 128..255): tile tu's K half kh, the half's 1536 gate|up outputs
+      if (dw) {
+        const bool okw = ll_poll16_w<2>(
+            limit, rs, b_gu + kh * (KD / 2) + 2 * ti, [](int i) { return 2 * NT / 2 * i; }, 2, probe,
+            [&](int i) { return i == 0 || ti < (KD / 4 - NM); }, t_gu,
+            [&](int i, uint32_t p0, uint32_t p1) { *reinterpret_cast<uint2*>(&sm.b[4 * ti + 4 * NM * i]) = uint2{p0, p1}; });
+        if (!(ok = wg_all(sm.sync, okw, vph))) break;
+        stamp(16 * l + 11);
+        __syncthreads();  // the projecting waves' partials (their sm.b reads end here)
+        stamp(16 * l + 12);
+      }
     }
-  }
-
-  // ---- the last layer's x += down, and workgroup 0 stores the row
-  if (ok) {
-    const int lp = a.layers - 1;
-    ok = add_row(sm, vph, rs, O_DN + (lp & 1) * W_DN, (epoch << 12) | (uint32_t)(STEPS * lp + STEPS), a.probe,
-                 a.eps);
-    if (ok && wg == 0) {
-      for (int i = tid; i < DM / 8; i += NT)
-        st16((uint16_t*)a.h_out + 8 * i, *reinterpret_cast<const u16x8*>(&sm.x[8 * i]));
+    // ---- the last layer's x += down, and workgroup 0 stores the row
+    if (ok) {
+      const int lp = a.layers - 1;
+      float pv[KQ][4];
+      const bool okw = poll_quarters(limit, rs, O_DN + (lp & 1) * W_DN, ti, probe,
+                                     (epoch << 12) | (uint32_t)(STEPS * lp + STEPS), pv);
+      if (okw) add_quarters(sm, ti, pv);
+      ok = wg_all(sm.sync, okw, vph);
+      if (ok && wg == 0)
+        *reinterpret_cast<uint2*>((uint16_t*)a.h_out + 4 * ti) = *reinterpret_cast<const uint2*>(&sm.x[4 * ti]);
     }
   }
 

@@ -428,7 +428,7 @@ __global__ __launch_bounds__(NT, 1) void depth_run_kernel(const M3xDepthRun a) {
   };
 
   // ---- set-up: zeroed LDS rows, the residual at L0 from the prefix, the pair's K/V history
-  if (tid == 0) sm.sync.spin = a.spin_limit ? a.spin_limit : SPIN_LIMIT;
+  if (tid == 0) ll::sync_init(sm.sync, a.spin_limit);
   if (xm) {
     for (int i = tid; i < RB * XS / 8; i += NT) {
       reinterpret_cast<u16x8*>(&sm.m.x[0][0])[i] = u16x8{};

@@ -14,11 +14,17 @@ constexpr unsigned SPIN_LIMIT = 1u << 19;
 constexpr int SC1 = 16;  // cache-policy bit of a device-scope access (gfx950 SC1)
 
 // per-workgroup LDS state of the polls: wg_all's per-wave votes (alternating buffers, up to 16 waves) and the run's
-// spin limit (set once by thread 0 before the first barrier)
+// spin limit; sync_init (thread 0, before the first barrier) sets the limit and clears every vote slot, so slots of
+// waves the workgroup does not have read as "no failure"
 struct Sync {
   int vote[2][16];
   unsigned spin;
 };
+__device__ __forceinline__ void sync_init(Sync& sy, unsigned spin_limit) {
+  sy.spin = spin_limit ? spin_limit : SPIN_LIMIT;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) sy.vote[0][i] = sy.vote[1][i] = 0;
+}
 
 // true in every thread iff v is true in every thread: one barrier; the two vote buffers alternate, so a wave that
 // runs ahead into the next call writes the other buffer while a slower one still reads this one
@@ -27,7 +33,8 @@ __device__ __forceinline__ bool wg_all(Sync& sy, bool v, int& phase) {
   if ((threadIdx.x & 63) == 0) sy.vote[phase][threadIdx.x >> 6] = any_false;
   __syncthreads();
   int any = 0;
-  for (int w = 0; w < (int)(blockDim.x >> 6); ++w) any |= sy.vote[phase][w];
+#pragma unroll
+  for (int w = 0; w < 16; ++w) any |= sy.vote[phase][w];
   const int r = !any;
   phase ^= 1;
   return __builtin_amdgcn_readfirstlane(r) != 0;
@@ -98,18 +105,16 @@ __device__ __forceinline__ bool wave_poll1w(__amdgpu_buffer_rsrc_t r, int off, b
   return false;
 }
 
-// This thread's chunks i < nit (16 bytes, two words each; nit uniform across the workgroup, at most N), handing
-// each live chunk's two payloads to sink(i, p0, p1) once. Chunk i sits at word base + U(i), base per thread and
-// U(i) a constant, so the loads take one address register and constant offsets. With more than `probe` chunks per
-// thread, chunk 0 is polled first (a probe: one chunk per thread while the producers still run, which then mostly
-// finds the rest already there); rounds read the chunks still missing, skipping chunks i >= nit by uniform
-// branches and pushing arrived ones out of bounds. Workgroup-collective (every thread calls it); false if any wave
-// gave up after the run's spin limit of rounds (sy.spin).
+// This thread's chunks i < nit (16 bytes, two words each; nit uniform across the wave, at most N), handing each
+// live chunk's two payloads to sink(i, p0, p1) once. Chunk i sits at word base + U(i), base per thread and U(i) a
+// constant, so the loads take one address register and constant offsets. With more than `probe` chunks per thread,
+// chunk 0 is polled first (a probe: one chunk per thread while the producers still run, which then mostly finds the
+// rest already there); rounds read the chunks still missing, skipping chunks i >= nit by uniform branches and
+// pushing arrived ones out of bounds. Wave-level: false (in every lane) if the wave gave up after `limit` rounds.
 template <int N, class U, class Live, class Sink>
-__device__ __forceinline__ bool ll_poll16(Sync& sy, int& vph, __amdgpu_buffer_rsrc_t r, int base, U uoff, int nit,
-                                          int probe, Live live, uint32_t tag, Sink sink) {
+__device__ __forceinline__ bool ll_poll16_w(unsigned limit, __amdgpu_buffer_rsrc_t r, int base, U uoff, int nit,
+                                            int probe, Live live, uint32_t tag, Sink sink) {
   static_assert(N <= 64, "chunks per thread");
-  const unsigned limit = __builtin_amdgcn_readfirstlane(sy.spin);
   uint64_t pending = 0;
 #pragma unroll
   for (int i = 0; i < N; ++i)
@@ -124,38 +129,33 @@ __device__ __forceinline__ bool ll_poll16(Sync& sy, int& vph, __amdgpu_buffer_rs
       pending &= ~1ull;
     }
   }
-  {
-    for (unsigned it = 0; ok; ++it) {
-      if (__builtin_amdgcn_ballot_w64(pending != 0) == 0) break;
-      if (it >= limit) {
-        ok = false;
-        break;
-      }
-      M3X_POLL_CLOBBER();
-      u32x4 v[N];
+  for (unsigned it = 0; ok; ++it) {
+    if (__builtin_amdgcn_ballot_w64(pending != 0) == 0) break;
+    if (it >= limit) {
+      ok = false;
+      break;
+    }
+    M3X_POLL_CLOBBER();
+    u32x4 v[N];
 #pragma unroll
-      for (int i = 0; i < N; ++i)
-        if (i < nit)
-          v[i] = __builtin_amdgcn_raw_buffer_load_b128(r, base * 8 + (((pending >> i) & 1) ? 0 : OOB), uoff(i) * 8,
-                                                       VOL);
+    for (int i = 0; i < N; ++i)
+      if (i < nit)
+        v[i] = __builtin_amdgcn_raw_buffer_load_b128(r, base * 8 + (((pending >> i) & 1) ? 0 : OOB), uoff(i) * 8, VOL);
 #pragma unroll
-      for (int i = 0; i < N; ++i) {
-        if (i < nit && ((pending >> i) & 1) && v[i].y == tag && v[i].w == tag) {
-          sink(i, v[i].x, v[i].z);
-          pending &= ~(1ull << i);
-        }
+    for (int i = 0; i < N; ++i) {
+      if (i < nit && ((pending >> i) & 1) && v[i].y == tag && v[i].w == tag) {
+        sink(i, v[i].x, v[i].z);
+        pending &= ~(1ull << i);
       }
     }
   }
-  return wg_all(sy, ok, vph);
+  return ok;
 }
-
 // the same for single words (8-byte loads); sink(i, payload)
 template <int N, class U, class Live, class Sink>
-__device__ __forceinline__ bool ll_poll8(Sync& sy, int& vph, __amdgpu_buffer_rsrc_t r, int base, U uoff, int nit,
-                                         int probe, Live live, uint32_t tag, Sink sink) {
+__device__ __forceinline__ bool ll_poll8_w(unsigned limit, __amdgpu_buffer_rsrc_t r, int base, U uoff, int nit,
+                                           int probe, Live live, uint32_t tag, Sink sink) {
   static_assert(N <= 32, "words per thread");
-  const unsigned limit = __builtin_amdgcn_readfirstlane(sy.spin);
   uint32_t pending = 0;
 #pragma unroll
   for (int i = 0; i < N; ++i)
@@ -190,7 +190,22 @@ __device__ __forceinline__ bool ll_poll8(Sync& sy, int& vph, __amdgpu_buffer_rsr
       }
     }
   }
-  return wg_all(sy, ok, vph);
+  return ok;
+}
+
+// Workgroup-collective forms (every thread calls them): the wave-level poll, then one vote over the workgroup
+// (which also makes the sinks' LDS writes visible); false if any wave gave up after the run's spin limit (sy.spin).
+template <int N, class U, class Live, class Sink>
+__device__ __forceinline__ bool ll_poll16(Sync& sy, int& vph, __amdgpu_buffer_rsrc_t r, int base, U uoff, int nit,
+                                          int probe, Live live, uint32_t tag, Sink sink) {
+  const unsigned limit = __builtin_amdgcn_readfirstlane(sy.spin);
+  return wg_all(sy, ll_poll16_w<N>(limit, r, base, uoff, nit, probe, live, tag, sink), vph);
+}
+template <int N, class U, class Live, class Sink>
+__device__ __forceinline__ bool ll_poll8(Sync& sy, int& vph, __amdgpu_buffer_rsrc_t r, int base, U uoff, int nit,
+                                         int probe, Live live, uint32_t tag, Sink sink) {
+  const unsigned limit = __builtin_amdgcn_readfirstlane(sy.spin);
+  return wg_all(sy, ll_poll8_w<N>(limit, r, base, uoff, nit, probe, live, tag, sink), vph);
 }
 
 }  // namespace ll

@@ -277,7 +277,8 @@ class StaticBackbone:
         """Whether a step of `rows` rows runs as one persistent kernel: one row (the one-seat frame), the
         Qwen3-0.6B geometry the kernel implements (hidden 1024 with the folded norms, 16 q / 8 kv heads of 128,
         SwiGLU 3072, bf16), a per-slot extent of at most 4096 positions, one workgroup per CU on a 256-CU part."""
-        return (self.persistent and rows == 1 and self.fused_norms and self.heads == 16 and self.kv_heads == 8
+        return (self.persistent and rows == 1 and self.fused_norms and self.dtype == torch.bfloat16
+                and self.heads == 16 and self.kv_heads == 8
                 and self.head_dim == 128 and self.inter == 3072 and self._extent <= 4096 and self._nwg == 256)
 
     def _run_args(self, b):
@@ -295,8 +296,9 @@ class StaticBackbone:
         if a is None:
             a = b.run = ops.BackboneRunArgs()
             kc = self._kfull[0]
+            # probe 1: a poll of more than one chunk per thread waits on its first chunk, then reads the rest
             a.layer, a.layers, a.cap, a.nwg, a.probe = self._run_table.data_ptr(), len(self.layers), self._extent, \
-                self._nwg, 0
+                self._nwg, 1
             a.eps, a.scale = self.eps, self.scaling
             a.x, a.h_out, a.slots, a.pos = b.x.data_ptr(), b.h.data_ptr(), b.slots.data_ptr(), b.pos.data_ptr()
             a.cos, a.sin, a.s_cos = self.cos.data_ptr(), self.sin.data_ptr(), self.cos.stride(0)
