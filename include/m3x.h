@@ -467,7 +467,9 @@ typedef struct M3xBackboneLayer {
  * xchg: m3x_backbone_run_xchg_bytes() of device memory zeroed once; sync: 4 int32 zeroed once ([0] epoch, [1] a
  * counter, [2] set to 1 if a step's input never arrived within spin_limit polling rounds (0: 2^19), in which case
  * h_out is not written). nwg must equal 256 and the device must hold all of them at once (else M3X_EUNSUPPORTED).
- * probe: as M3xDepthRun's. prof (nullable): [256][512] real-time counter stamps of every workgroup's steps. */
+ * probe: as M3xDepthRun's. prof (nullable): [256][512] real-time counter stamps of every workgroup's steps.
+ * w_fin: the final RMSNorm weight [1024]; y_out [1024] receives the final norm of h_out (the add+norm kernels'
+ * arithmetic). At the run's end lengths[slots[0]] += real[0] (int64), whether or not the run failed. */
 typedef struct M3xBackboneRun {
   const M3xBackboneLayer* layer;
   int layers, cap, nwg, probe;
@@ -485,6 +487,10 @@ typedef struct M3xBackboneRun {
   uint64_t* xchg;
   int32_t* sync;
   uint64_t* prof;
+  const void* w_fin;
+  void* y_out;
+  int64_t* lengths;
+  const int64_t* real;
 } M3xBackboneRun;
 
 /* Bytes of the exchange area, of M3xBackboneRun and of M3xBackboneLayer (a binding checks its layouts). */
@@ -494,7 +500,7 @@ size_t m3x_backbone_run_layer_bytes(void);
 
 /* Launch the run (args read on the host during the call). Replaces, for a one-row step, the layer loop of
  * `StaticBackbone._forward` (serve/fast_backbone.py:187-203: q|k|v, `_qk_norm_rope_cache`, `_decode_attn`, o, the
- * add+norms, gate|up, SwiGLU, down) up to the final norm. */
+ * add+norms, gate|up, SwiGLU, down), its final norm (:229-232) and the length update (:233). */
 int m3x_backbone_run(const M3xBackboneRun* args, void* stream);
 
 #ifdef __cplusplus

@@ -8,29 +8,31 @@
 // flight in the polling wave: a wave's vector memory counter retires in order, so a poll issued behind a weight
 // load waits for that load too. The waves therefore split by role:
 //   - waves 0-3 project: they hold the workgroup's weight tiles and its attention split's cached keys and values in
-//     registers, each loaded steps ahead of its use (right after the slot's previous tile is used), and run the
-//     MFMA tiles;
-//   - waves 4-7 only poll, reduce, attend and store: nothing of theirs is in flight when they poll.
+//     registers, each loaded ahead of its use (right after the slot's previous tile is used), run the MFMA tiles
+//     and store each tile's outputs;
+//   - waves 4-7 only poll, reduce, attend and combine: nothing of theirs is in flight when they poll. The
+//     attention and the combine sync these waves alone (an LDS arrival counter), so a burst of the projecting
+//     waves' loads never holds them up.
 // The two roles run their own loop over the layers and meet at the same workgroup barriers.
 // Per layer (every workgroup unless said otherwise):
-//   S1 q|k|v     x += the previous layer's down (its four K-slice partials summed in order), the row's RMS; one
-//                16-column tile of the 4096 (the input RMSNorm applied explicitly at layer 0, folded into the
-//                packed weight after it, as the launch path); the 32 tiles of kv head h sit on XCD h;
+//   S1 q|k|v     x += the previous layer's down (its two K-half partials summed in order, rounded, added), the
+//                row's RMS; one 16-column tile of the 4096 (the input RMSNorm applied explicitly at layer 0, folded
+//                into the packed weight after it, as the launch path); the 32 tiles of kv head h sit on XCD h;
 //   S2 attention item (kv head wg % 8, split wg / 8): the two q heads and the new key of its kv head normed and
 //                rotated (qk_norm_rope8, the launch kernels' arithmetic), the new key and value written to the cache
-//                by the item that holds the row's position, fp32 scores / softmax / P.V over the split's keys; the
-//                split's partial (max, sum, 128 values per q head) goes out;
+//                by the item that holds the row's position, scores and P.V on MFMA (fp32 sums, P as a bf16 hi/lo
+//                pair), fp32 softmax; the split's partial (max, sum, 128 values per q head) goes out;
 //   S3 combine   workgroups 0..15: one q head each (on its kv head's XCD), its 32 partials folded in split order;
-//   S4 o         one (16-column tile, K quarter) unit of the o projection: an fp32 partial of 16 columns;
-//   S5 gate|up   x += o (the four partials summed in order, rounded, added), the row's RMS; workgroups 0..191: one
+//   S4 o         workgroups 0..127: one (16-column tile, K half) unit of the o projection, an fp32 partial;
+//   S5 gate|up   x += o (the two partials summed in order, rounded, added), the row's RMS; workgroups 0..191: one
 //                gate|up tile pair with the post-attention RMSNorm folded, SwiGLU;
-//   S6 down      one (16-column tile, K quarter) unit of the down projection: an fp32 partial.
-// The K quarters spread the o and down weights over every workgroup, so each one streams about the same bytes
-// (~136 KB at most per layer) and a consumer of a K quarter polls only that quarter of its input. The split size
-// follows the row's position (32 splits of ceil((pos + 1) / 32) keys rounded up to 16), so every workgroup attends
-// about the same number of keys. After the last layer workgroup 0 stores the residual row; the caller's final norm
-// reads it. Every wait is bounded by the run's spin limit: a workgroup whose input never arrives sets the error word
-// and skips the rest, so the grid always drains (the output row is then not written).
+//   S6 down      workgroups 128..255: one (16-column tile, K half) unit of the down projection, an fp32 partial.
+// The K halves spread the o and down weights, so no workgroup streams more than ~144 KB a layer, and a consumer of
+// a K half polls only that half of its input. The split size follows the row's position (32 splits of
+// ceil((pos + 1) / 32) keys rounded up to 16), so every workgroup attends about the same number of keys. After the
+// last layer workgroup 0 stores the residual row and its final RMSNorm, and the row's length moves on. Every wait
+// is bounded by the run's spin limit: a workgroup whose input never arrives sets the error word and skips the rest,
+// so the grid always drains (the output rows are then not written).
 #include "m3x_ll.h"
 #include "m3x_norm.h"
 
@@ -63,6 +65,10 @@ struct M3xBackboneRun {
   uint64_t* xchg;
   int32_t* sync;                  // [0] epoch, [1] workgroups done, [2] error
   uint64_t* prof;                 // optional [256][512] real-time stamps of each workgroup's steps (profiling)
+  const void* w_fin;              // the final RMSNorm weight [1024]
+  void* y_out;                    // [1024] the final norm of the last layer's residual
+  int64_t* lengths;               // lengths[slots[0]] += real[0] at the run's end (the step's length update)
+  const int64_t* real;
 };
 
 namespace bb {
@@ -694,13 +700,40 @@ __global__ __launch_bounds__(NT, 1) void backbone_run_kernel(const M3xBackboneRu
                                      (epoch << 12) | (uint32_t)(STEPS * lp + STEPS), pv);
       if (okw) add_quarters(sm, ti, pv);
       ok = wg_all(sm.sync, okw, vph);
-      if (ok && wg == 0)
+      if (ok && wg == 0) {
         *reinterpret_cast<uint2*>((uint16_t*)a.h_out + 4 * ti) = *reinterpret_cast<const uint2*>(&sm.x[4 * ti]);
+        if (iw == 0) {
+          // the final RMSNorm in the add+norm kernels' order: lane t sums groups t and t + 64 (8 elements each,
+          // left to right), the two partials add, then the wave's fold-in-half tree; y = dt(dt(x / rms) * w)
+          float v[2][8], p[2];
+#pragma unroll
+          for (int m = 0; m < 2; ++m) {
+            const u16x8 x8 = *reinterpret_cast<const u16x8*>(&sm.x[8 * (lane + 64 * m)]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[m][e] = bf2f(x8.v[e]);
+            p[m] = v[m][0] * v[m][0];
+#pragma unroll
+            for (int e = 1; e < 8; ++e) p[m] = p[m] + v[m][e] * v[m][e];
+          }
+          const float sum = __builtin_bit_cast(
+              float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, fold_half_sum<64>(p[0] + p[1]))));
+          const float sc = 1.0f / sqrtf(sum / (float)DM + a.eps);
+#pragma unroll
+          for (int m = 0; m < 2; ++m) {
+            const u16x8 w8 = ld16((const uint16_t*)a.w_fin + 8 * (lane + 64 * m));
+            u16x8 o;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o.v[e] = f2bf(rnd<M3X_BF16>(v[m][e] * sc) * bf2f(w8.v[e]));
+            st16((uint16_t*)a.y_out + 8 * (lane + 64 * m), o);
+          }
+        }
+      }
     }
   }
 
   // ---- the run's end: failures are recorded, and the last workgroup out advances the epoch
   if (!ok && tid == 0) atomicOr(&a.sync[2], 1);
+  if (wg == 0 && tid == 0) a.lengths[slot] += a.real[0];  // as the launch path, whether or not the run failed
   __syncthreads();
   if (tid == 0) {
     const int prev = atomicAdd(&a.sync[1], 1);
@@ -734,7 +767,8 @@ M3X_API int m3x_backbone_run(const M3xBackboneRun* args, void* stream) {
   if (!args) return M3X_ENULL;
   const M3xBackboneRun& a = *args;
   if (a.layers <= 0 || a.layers > 600 || a.cap <= 0 || a.cap > SPLITS * SMAX || a.nwg != NWG) return M3X_EINVAL;
-  if (!a.layer || !a.x || !a.h_out || !a.slots || !a.pos || !a.cos || !a.sin || !a.w_in0 || !a.xchg || !a.sync)
+  if (!a.layer || !a.x || !a.h_out || !a.slots || !a.pos || !a.cos || !a.sin || !a.w_in0 || !a.xchg || !a.sync ||
+      !a.w_fin || !a.y_out || !a.lengths || !a.real)
     return M3X_ENULL;
   if ((a.sk_s | a.sk_h | a.sk_t | a.s_cos) & 7) return M3X_EINVAL;
   if (!bb_resident_ok()) return M3X_EUNSUPPORTED;

@@ -543,7 +543,8 @@ class BackboneRunArgs(ctypes.Structure):
         ("x", ctypes.c_void_p), ("h_out", ctypes.c_void_p), ("slots", ctypes.c_void_p), ("pos", ctypes.c_void_p),
         ("cos", ctypes.c_void_p), ("sin", ctypes.c_void_p), ("s_cos", ctypes.c_long), ("w_in0", ctypes.c_void_p),
         ("sk_s", ctypes.c_long), ("sk_h", ctypes.c_long), ("sk_t", ctypes.c_long), ("xchg", ctypes.c_void_p),
-        ("sync", ctypes.c_void_p), ("prof", ctypes.c_void_p)]
+        ("sync", ctypes.c_void_p), ("prof", ctypes.c_void_p), ("w_fin", ctypes.c_void_p), ("y_out", ctypes.c_void_p),
+        ("lengths", ctypes.c_void_p), ("real", ctypes.c_void_p)]
 
 
 def backbone_run_xchg_bytes() -> int:

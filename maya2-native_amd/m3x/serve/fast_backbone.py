@@ -305,6 +305,8 @@ class StaticBackbone:
             a.w_in0 = self.layers[0].input_layernorm.weight.data_ptr()
             a.sk_s, a.sk_h, a.sk_t = kc.stride(0), kc.stride(1), kc.stride(2)
             a.xchg, a.sync = self._run_xchg.data_ptr(), self._run_sync.data_ptr()
+            a.w_fin, a.y_out = self.norm.weight.data_ptr(), b.out.data_ptr()
+            a.lengths, a.real = self.lengths.data_ptr(), b.real.data_ptr()
         a.spin_limit = int(self.spin_limit)
         return a
 
@@ -324,10 +326,8 @@ class StaticBackbone:
         H, KV, D, eps = self.heads, self.kv_heads, self.head_dim, self.eps
         ops.positions(self.lengths, b.slots, b.offset, b.pos)
         if self._persistent_ok(b.rows) and not b.mixed:
-            # the 28 layers of the one-row step in one launch; the final norm and the lengths as the launch path
+            # the 28 layers of the one-row step, its final norm and its length update in one launch
             ops.backbone_run(self._run_args(b))
-            ops.add_rms(b.h, None, self.norm.weight, eps, y=b.out)
-            ops.lengths_add(self.lengths, b.slots, b.real)
             return b.out
         o3 = b.o.view(b.rows, H, D)
         fused = self.fused_norms
