@@ -58,16 +58,15 @@ def build_frame(torch, seats, lengths, seed_base=0, backbone=None, depth_model=N
     return fs, bb, dm
 
 
-def secondary(torch, bb, dm, steps):
+def secondary(torch, bb, dm, steps, only=None):
     """The other GPU configurations, timed through the reference surfaces on the frame's weights:
     C2 = FastDepth.__call__ over 16 seats (the 4-layer depth frame over codebooks 1..31, top-k 50, T 0.9, h N(0,1),
     cb0 uniform in [0, 2048)); C3 = StaticBackbone.step over 64 seats (lengths U[64, 2048]) + cb0; C4 =
     StaticBackbone.step_mixed with 216 decoding seats (lengths log-uniform in [128, 4096)) and 8 inline prefills of
     256 tokens (embedding rows of uniform ids from a [151936, 1024] N(0, 0.02) table, starting at length 0) = 2264
-    rows + cb0 over the 224 seats. Lengths are reset before every step, so each timed step does the same work."""
-    from m3x import roofline, synth
-    from m3x.cb0 import Cb0Sampler
-    from m3x.serve.fast_backbone import StaticBackbone
+    rows + cb0 over the 224 seats. Lengths are reset before every step, so each timed step does the same work.
+    only: "c2", "c3" or "c4" runs that line alone and returns."""
+    from m3x import roofline
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(300)
     out = {}
@@ -97,7 +96,19 @@ def secondary(torch, bb, dm, steps):
         log(f"{label}: {rows} rows, {ms:.3f} ms/step ({out[label]['hbm_fraction']:.1%} of the HBM and "
             f"{out[label]['mfma_fraction']:.1%} of the MFMA roofline)")
 
-    # C2: the depth frame alone at 16 seats
+    if only in (None, "c2"):
+        _c2(torch, dm, steps, g, dev, out, roofline)
+    if only in (None, "c3"):
+        _c3(torch, bb, g, dev, run)
+    if only in (None, "c4"):
+        _c4(torch, bb, g, dev, run)
+    if only is not None:
+        return out
+    return _rest(torch, bb, dev, g, out, steps)
+
+
+def _c2(torch, dm, steps, g, dev, out, roofline):
+    """C2: FastDepth.__call__ over 16 seats."""
     from m3x.serve.fast_depth import FastDepth
     B2 = 16
     fd = FastDepth(dm, B2, dtype=torch.bfloat16, temp=0.9, top_k=50, batch_buckets=(B2,), fused=True)
@@ -128,7 +139,12 @@ def secondary(torch, bb, dm, steps):
     del fd
     torch.cuda.empty_cache()
 
-    # C3
+
+def _c3(torch, bb, g, dev, run):
+    """C3: StaticBackbone.step over 64 seats + cb0."""
+    from m3x import synth
+    from m3x.cb0 import Cb0Sampler
+    from m3x.serve.fast_backbone import StaticBackbone
     B3 = 64
     sb = StaticBackbone(bb, B3, capacity=CAP, batch_buckets=(B3,), ctx_buckets=(CAP,), attention="triton",
                         fuse_rope=True)
@@ -145,7 +161,12 @@ def secondary(torch, bb, dm, steps):
     del sb, cb
     torch.cuda.empty_cache()
 
-    # C4
+
+def _c4(torch, bb, g, dev, run):
+    """C4: StaticBackbone.step_mixed over 216 decode rows and 8 inline prefills of 256 tokens + cb0."""
+    from m3x import synth
+    from m3x.cb0 import Cb0Sampler
+    from m3x.serve.fast_backbone import StaticBackbone
     nd, npf, T = 216, 8, 256
     sb = StaticBackbone(bb, nd + npf, capacity=CAP, batch_buckets=(nd + npf * T,), ctx_buckets=(CAP,),
                         attention="triton", fuse_rope=True)
@@ -171,6 +192,10 @@ def secondary(torch, bb, dm, steps):
     del sb, cb, pre
     torch.cuda.empty_cache()
 
+
+def _rest(torch, bb, dev, g, out, steps):
+    """The loop guard, the tick readout, time to first audio and the Mimi lines."""
+    from m3x.serve.fast_backbone import StaticBackbone
     # the engine's loop guard for 224 seats (maya3/guards.py:80-107): device history push + rule, graph-timed,
     # beside the same rule on the host over the same histories (the engine evaluates it on the host each tick)
     from types import SimpleNamespace
@@ -557,6 +582,7 @@ def main():
     ap.add_argument("--secondary-steps", type=int, default=5)
     ap.add_argument("--mimi-only", action="store_true", help="print only the Mimi decode line (for profiling)")
     ap.add_argument("--b1-only", action="store_true", help="print only the B=1 frame latency (for profiling)")
+    ap.add_argument("--only", choices=("c2", "c3", "c4"), help="print only that configuration's line (for profiling)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -578,6 +604,13 @@ def main():
     if args.b1_only:
         with torch.inference_mode():
             print(json.dumps({"b1_frame_us": round(b1_latency(torch, args.b1_replays), 1)}), flush=True)
+        return
+    if args.only:
+        with torch.inference_mode():
+            bb = synth.qwen3_backbone(layers=28, seed=0, device=dev, gen="cuda", affine=synth.AFFINE)
+            dm = synth.swiglu_depth(seed=1, device=dev, gen="cuda", affine=synth.AFFINE)
+            print(json.dumps({"backbone_configs": secondary(torch, bb, dm, args.secondary_steps, only=args.only)}),
+                  flush=True)
         return
     log(f"device {torch.cuda.get_device_name(0)}; building the B={B} frame (KV {B + 1} slots x {CAP})")
     lengths = synth.c5_lengths(B)

@@ -10,7 +10,7 @@ import numpy as np
 import torch
 
 from ._lib import check, lib
-from .ops import _p, _stream
+from .ops import _index, _need, _p, _stream
 
 
 def _codes_to_hits(codes):
@@ -21,6 +21,9 @@ def loop_guard(W, n, out, cfg, slots=None):
     """out[r] = 0 / -1 (stall) / p (period) for device history row W[slots[r]] with n[slots[r]] frames (W[r], n[r]
     without slots); W int32 [*, hist], n int64."""
     rows = n.numel() if slots is None else slots.numel()
+    _index(slots=slots)
+    _need(W, torch.int32, "W")
+    _need(n, torch.long, "n")
     check(lib().m3x_loop_guard(_p(W), W.stride(0), _p(slots), _p(n), _p(out), rows, W.shape[1], int(cfg.stall),
                                int(cfg.period_win), float(cfg.period_thr), int(cfg.pmin), int(cfg.pmax), _stream()),
           "loop_guard")
@@ -61,6 +64,8 @@ class LoopGuard:
     def push(self, slots, codes):
         """Append codes[b] (int64, any row stride) to slot slots[b]'s history and count the frame."""
         ld = codes.stride(0) if codes.dim() > 1 else 1
+        _index(slots=slots)
+        _need(codes, torch.long, "codes")
         check(lib().m3x_hist_push(_p(self.hist), self.hist.stride(0), _p(self.frames), _p(slots), _p(codes), ld,
                                   slots.numel(), self.hist_len, _stream()), "hist_push")
 

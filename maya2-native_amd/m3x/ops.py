@@ -60,6 +60,15 @@ def _need(t: torch.Tensor, dtype, name: str):
         raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
 
 
+def _index(slots=None, pos=None):
+    """The ABI's index types: slot tensors are int64, position tensors int32 (a wrong width would be read as
+    out-of-range indices on the device)."""
+    if slots is not None:
+        _need(slots, torch.long, "slots")
+    if pos is not None:
+        _need(pos, torch.int32, "pos")
+
+
 # ---------------------------------------------------------------- backbone step
 def positions(lengths, slots, offset, pos):
     _dev(lengths, slots, offset, pos)
@@ -73,6 +82,7 @@ def positions(lengths, slots, offset, pos):
 
 def lengths_add(lengths, slots, real):
     _dev(lengths, slots, real)
+    _index(slots=slots)
     check(lib().m3x_lengths_add(_p(lengths), _p(slots), _p(real), slots.numel(), _stream()), "lengths_add")
 
 
@@ -99,6 +109,7 @@ def add_rms(h, a, w, eps, h_out=None, y=None):
 
 def qk_norm_rope_cache(qkv, q_out, k_cache, v_cache, slots, pos, cos, sin, wq, wk, eps, heads, kv_heads):
     _dev(qkv, q_out, k_cache, v_cache, slots, pos, cos, sin, wq, wk)
+    _index(slots=slots, pos=pos)
     D = k_cache.shape[-1]
     rows = qkv.shape[0]
     if qkv.shape[1] != (heads + 2 * kv_heads) * D:
@@ -117,6 +128,7 @@ def linear_qk_rope(x, w, qkv, q_out, k_cache, v_cache, slots, pos, cos, sin, wq,
     qk_norm_rope_cache."""
     M, K, qkv = _lin_args(x, w, qkv, w.N)
     _dev(q_out, k_cache, v_cache, slots, pos, cos, sin, wq, wk, part)
+    _index(slots=slots, pos=pos)
     D = k_cache.shape[-1]
     if w.N != (heads + 2 * kv_heads) * D:
         raise ValueError(f"linear_qk_rope: weight rows {w.N} != (heads + 2*kv_heads)*head_dim")
@@ -142,6 +154,7 @@ def decode_attn(q, k_cache, v_cache, out, slots, pos, scale, max_ctx, chunk, wor
     items (int32, optional): the step's work items (attn_items with attn_item_bins bins); the rows of an inline
     prefill then share one pass over their slot's keys per 16 // (heads // kv_heads) rows."""
     _dev(q, k_cache, v_cache, out, slots, pos, workspace, items)
+    _index(slots=slots, pos=pos)
     rows = q.shape[0]
     if items is not None:
         bins = attn_item_bins(rows, kv_heads, max_ctx, chunk)
@@ -401,6 +414,7 @@ def cb0_sample(logits, aeos, slots, u, temp_t=None, temp=1.0, topk_t=None, top_k
                stop_out=None, topp_t=None, top_p=1.0):
     _dev(logits, slots, u, temp_t, topk_t, aeos_bias, rep_t, hist_t, frames_t, min_t, hazard_t, ctr_t, cb0_out,
          cb0_i32, stop_out, topp_t)
+    _index(slots=slots)
     if topp_t is not None and topp_t.dtype != torch.float32:
         raise ValueError("topp_t must be float32")
     _rows2d(logits, "logits")
@@ -417,6 +431,7 @@ def cb0_sample(logits, aeos, slots, u, temp_t=None, temp=1.0, topk_t=None, top_k
 def philox_uniforms(seeds, ctrs, slots, out, level0):
     """out [B, nlevels] (row stride free) = Philox uniforms for levels level0.. of each slot's stream."""
     _dev(seeds, ctrs, slots, out)
+    _index(slots=slots)
     _need(seeds, torch.int32, "seeds")
     _need(ctrs, torch.int32, "ctrs")
     _need(out, torch.float32, "out")
@@ -440,6 +455,7 @@ def philox_block(counter, key, out):
 
 def ctr_add(ctr, slots):
     _dev(ctr, slots)
+    _index(slots=slots)
     check(lib().m3x_ctr_add(_p(ctr), _p(slots), slots.numel(), _stream()), "ctr_add")
 
 
@@ -579,6 +595,7 @@ def rvq_decode(codes, tables, out):
 def dwconvt(x, w, tail, slots, out, k, s):
     """Depthwise transposed conv of one frame per seat with per-slot overlap tails; out [B * s, C]."""
     _dev(x, w, tail, slots, out)
+    _index(slots=slots)
     check(lib().m3x_dwconvt(_p(x), x.stride(0), _p(w), _p(tail), tail.stride(0), _p(slots), _p(out), x.shape[0],
                             x.shape[1], k, s, _dt3(x), _stream()), "dwconvt")
 
@@ -587,6 +604,7 @@ def conv_gather(x, state, slots, cols, B, T, C, k, dil, use_elu, chunk):
     """GEMM rows of a causal conv with per-slot input history (state [slots, pad * C] or None when pad = 0);
     cols None only advances the history."""
     _dev(x, state, slots, cols)
+    _index(slots=slots)
     check(lib().m3x_conv_gather(_p(x), x.stride(0), _p(state), 0 if state is None else state.stride(0), _p(slots),
                                 _p(cols), 0 if cols is None else cols.stride(0), B, T, C, k, dil, int(use_elu), chunk,
                                 _dt3(x), _stream()),
@@ -609,6 +627,7 @@ def conv_gemm(x, w, y, bias=None, res=None, use_elu=False, gather=None):
         raise TypeError("conv_gemm: the weight must be packed with ops.pack_weight")
     st, slots, T, C, dil, pre = gather if gather is not None else (None, None, 0, 0, 1, False)
     _dev(x, w.data, y, bias, res, st, slots)
+    _index(slots=slots)
     check(lib().m3x_conv_gemm(_p(x), x.stride(0), _p(w.data), _p(bias), _p(res), 0 if res is None else res.stride(0),
                               _p(y), y.stride(0), y.shape[0], w.N, w.K, int(use_elu), _p(st),
                               0 if st is None else st.stride(0), _p(slots), T, C, dil, int(pre), _dt3(x), _stream()),
@@ -626,6 +645,7 @@ def resid_ln(h, a, scale, w, b, eps, y):
 def convt_overlap(cols, tail, slots, bias, out, B, Tin, C, k, s, chunk):
     """Overlap-add of a transposed conv's GEMM columns with per-slot tails; out [B * Tin * s, C]."""
     _dev(cols, tail, slots, bias, out)
+    _index(slots=slots)
     check(lib().m3x_convt_overlap(_p(cols), cols.stride(0), _p(tail), tail.stride(0), _p(slots), _p(bias), _p(out),
                                   out.stride(0), B, Tin, C, k, s, chunk, _dt3(cols), _stream()), "convt_overlap")
 
@@ -633,6 +653,7 @@ def convt_overlap(cols, tail, slots, bias, out, B, Tin, C, k, s, chunk):
 def ring_attn(qkv, kring, vring, key_pos, tokens, slots, inv_freq, rope_scale, out, B, T, H, ring, window):
     """Sliding-window attention of T new tokens per seat over per-slot rings of post-RoPE keys."""
     _dev(qkv, kring, vring, key_pos, tokens, slots, inv_freq, out)
+    _index(slots=slots)
     check(lib().m3x_ring_attn(_p(qkv), qkv.stride(0), _p(kring), _p(vring), _p(key_pos), _p(tokens), _p(slots),
                               _p(inv_freq), float(rope_scale), _p(out), out.stride(0), B, T, H, 64, ring, window,
                               _dt3(qkv), _stream()), "ring_attn")
@@ -640,12 +661,14 @@ def ring_attn(qkv, kring, vring, key_pos, tokens, slots, inv_freq, rope_scale, o
 
 def advance_tokens(tokens, slots, B, T, dummy):
     _dev(tokens, slots)
+    _index(slots=slots)
     check(lib().m3x_advance_tokens(_p(tokens), _p(slots), B, T, dummy, _stream()), "advance_tokens")
 
 
 def final_conv(x, state, slots, w, bias, pcm, B, T, C, k, chunk):
     """fp32 PCM of the last causal conv (C -> 1 channel) with per-slot history; pcm [B, >= T] float32."""
     _dev(x, state, slots, w, pcm)
+    _index(slots=slots)
     check(lib().m3x_final_conv(_p(x), x.stride(0), _p(state), 0 if state is None else state.stride(0), _p(slots),
                                _p(w), float(bias), _p(pcm), pcm.stride(0), B, T, C, k, chunk, _dt3(x), _stream()),
           "final_conv")

@@ -630,6 +630,30 @@ def test_index_kernels(gpu):
     assert ctr.tolist() == [1, 1, 0, 0, 0, 2]
 
 
+def test_index_dtypes_rejected_before_launch(gpu):
+    """Slot tensors are int64 and position tensors int32 in the ABI: a tensor of the other width is refused on the
+    host (a kernel would read it as out-of-range indices)."""
+    from m3x import guards, ops
+    q = torch.zeros(2, 16, 128, dtype=torch.bfloat16, device=gpu)
+    kc = torch.zeros(3, 8, 64, 128, dtype=torch.bfloat16, device=gpu)
+    s64 = torch.tensor([0, 1], device=gpu)
+    p32 = torch.tensor([3, 5], dtype=torch.int32, device=gpu)
+    ws = torch.empty(16, device=gpu)
+    for slots, pos, what in ((s64.int(), p32, "slots"), (s64, p32.long(), "pos")):
+        with pytest.raises(ValueError, match=what):
+            ops.decode_attn(q, kc, kc, torch.empty_like(q), slots, pos, 0.1, 64, 128, ws, 16, 8)
+    with pytest.raises(ValueError, match="slots"):
+        ops.ctr_add(torch.zeros(4, dtype=torch.int32, device=gpu), s64.int())
+    with pytest.raises(ValueError, match="slots"):
+        ops.lengths_add(torch.zeros(4, dtype=torch.int64, device=gpu), s64.int(), s64)
+    lg = guards.LoopGuard(4, _guard_cfg(), device=gpu)
+    with pytest.raises(ValueError, match="slots"):
+        lg.push(s64.int(), s64)
+    with pytest.raises(ValueError, match="codes"):
+        lg.push(s64, s64.int())
+    torch.cuda.synchronize()
+
+
 # ---------------------------------------------------------------- loop guard (bit-exact vs the oracle)
 def _guard_cfg(**kw):
     from types import SimpleNamespace
