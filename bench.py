@@ -444,15 +444,24 @@ def _hf_eager_prefill_ms(torch, bb, x, steps):
     return sorted(ts)[len(ts) // 2] * 1e3
 
 
-def _cpu_frames(torch, O, bb, dm, seats, seconds, seed):
+def _cpu_frames(torch, O, bb, dm, seats, seconds, seed, tiled=False, min_frames=2):
     """Seconds per eager oracle frame (backbone + cb0 + depth + feedback) at `seats` seats of the C5 shapes, over
-    the frames that fit in `seconds` after one untimed frame (at least 2, at most 50)."""
+    the frames that fit in `seconds` after one untimed frame (at least min_frames, at most 50). tiled: every slot's K/V is
+    one random slot's, copied (drawing ~60 GB of normals for 224 seats would take minutes on one thread; the
+    arithmetic and the bytes streamed are the same)."""
     from m3x import synth
     lengths = synth.c5_lengths(seats, seed=seed)
     cap = int(lengths.max()) + 64
     g = torch.Generator().manual_seed(200 + seats)
-    kc = [torch.randn(seats + 1, 8, cap, 128, generator=g).to(torch.bfloat16) for _ in range(28)]
-    vc = [torch.randn(seats + 1, 8, cap, 128, generator=g).to(torch.bfloat16) for _ in range(28)]
+    if tiled:
+        def cache():
+            one = torch.randn(1, 8, cap, 128, generator=g).to(torch.bfloat16)
+            return one.expand(seats + 1, 8, cap, 128).contiguous()
+        kc = [cache() for _ in range(28)]
+        vc = [cache() for _ in range(28)]
+    else:
+        kc = [torch.randn(seats + 1, 8, cap, 128, generator=g).to(torch.bfloat16) for _ in range(28)]
+        vc = [torch.randn(seats + 1, 8, cap, 128, generator=g).to(torch.bfloat16) for _ in range(28)]
     L = torch.cat([lengths, torch.zeros(1, dtype=torch.long)])
     cos, sin = O.rope_tables(128, 1e6, cap, torch.bfloat16)
     x = torch.randn(seats, 1024, generator=g).to(torch.bfloat16)
@@ -470,17 +479,35 @@ def _cpu_frames(torch, O, bb, dm, seats, seconds, seed):
             continue
         el = time.perf_counter() - t0
         log(f"cpu baseline, {seats} seats, frame {frames}: {el:.1f}s")
-        if (el >= seconds and frames >= 2) or frames >= 50:
+        if (el >= seconds and frames >= min_frames) or frames >= 50:
             return el / frames, frames, lengths.tolist()
 
 
+def _host_ram_gib():
+    try:
+        return round(os.sysconf("SC_PAGE_SIZE") * os.sysconf("SC_PHYS_PAGES") / 2 ** 30, 1)
+    except (ValueError, OSError):
+        return None
+
+
+# host RAM that the full 224-seat CPU frame asks for: 2x its ~58 GB KV cache (its KV history is max length + 64
+# positions per slot, not the GPU cache's 4096)
+FULL_CPU_RAM_GIB = 120
+
+
 def cpu_baseline(torch, seconds, sizes=(2, 10)):
-    """The oracle's eager frame (backbone + cb0 + depth) on the host cores at the C5 shapes, timed at two seat
-    counts and fitted as t(B) = a + b B: the fixed part a (weights streamed and converted once per frame, whatever
-    the seats) and the per-seat part b (the seat's KV history, its rows through every projection, its sampling)
-    both measured, then the 224-seat frame time a + 224 b. A full 224-seat frame is not run: its 106 GB cache would
-    have to be drawn on the host first, and this line bounds the CPU work to about `seconds` so that the default
-    run ends in minutes."""
+    """The oracle's eager frame (backbone + cb0 + depth) on the host cores at the C5 shapes. With at least
+    FULL_CPU_RAM_GIB of host RAM the full 224-seat frame is timed (cpu_full_frame: one untimed frame, then one or
+    more timed frames filling about seconds / 2; ~40 s of wall time with the cache fill). Otherwise it is timed at
+    two seat counts and fitted as t(B) = a + b B: the fixed part a (weights streamed and converted once per frame,
+    whatever the seats) and the per-seat part b (the seat's KV history, its rows through every projection, its
+    sampling) both measured, then the 224-seat frame time a + 224 b, labelled extrapolated (the fit overstates the
+    per-seat cost: the full frame measured 12.5 s on 16 host threads where the fit gave ~23 s)."""
+    ram_gb = _host_ram_gib()
+    if ram_gb is not None and ram_gb >= FULL_CPU_RAM_GIB:
+        out = cpu_full_frame(torch, seconds / 2, min_frames=1)
+        out.update(host_ram_gib=ram_gb, host_cpus=os.cpu_count())
+        return out
     from m3x import synth
     from oracle import torch_oracle as O
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
@@ -492,10 +519,6 @@ def cpu_baseline(torch, seconds, sizes=(2, 10)):
     b = (t2 - t1) / (s2 - s1)
     a = t1 - b * s1
     t224 = a + 224 * b
-    try:
-        ram_gb = round(os.sysconf("SC_PAGE_SIZE") * os.sysconf("SC_PHYS_PAGES") / 2 ** 30, 1)
-    except (ValueError, OSError):
-        ram_gb = None
     return dict(value=round(224 / t224, 4), unit="frames/s", cores=threads, kind="port", extrapolated=True,
                 host_ram_gib=ram_gb, host_cpus=os.cpu_count(),
                 fit={"fixed_s_per_frame": round(a, 4), "s_per_seat_frame": round(b, 5),
@@ -504,8 +527,29 @@ def cpu_baseline(torch, seconds, sizes=(2, 10)):
                 sample=f"the PyTorch-eager oracle's frame (28 layers, cb0, depth over 31 codebooks) on {threads} host "
                        f"threads at {s1} seats (KV lengths {l1}: {t1:.2f} s per frame over {n1} frames) and {s2} "
                        f"seats ({t2:.2f} s over {n2} frames), fitted as {a:.3f} s + {b:.4f} s per seat: a 224-seat "
-                       f"frame takes {t224:.1f} s on this host (not run in full: its 106 GB cache would have to be drawn "
-                       f"on the host first, and this line is bounded to about {seconds:.0f} s of CPU work)")
+                       f"frame takes {t224:.1f} s on this host (not run in full: the host has {ram_gb} GiB of RAM, "
+                       f"under the {FULL_CPU_RAM_GIB} GiB the full frame's KV cache asks for)")
+
+
+def cpu_full_frame(torch, seconds, min_frames=2):
+    """The oracle's eager frame on the host cores at all 224 seats of the C5 shapes (the KV lengths of the GPU
+    frame, synth.c5_lengths(224)), timed in full rather than fitted from seat subsets: one untimed frame, then
+    timed frames until `seconds` have passed, at least min_frames (the KV cache alone is ~58 GB of host memory)."""
+    from m3x import synth
+    from oracle import torch_oracle as O
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    bb = synth.qwen3_backbone(layers=28, seed=0, device="cpu", affine=synth.AFFINE)
+    dm = synth.swiglu_depth(seed=1, device="cpu", affine=synth.AFFINE)
+    lengths = synth.c5_lengths(224)
+    t0 = time.perf_counter()
+    t, n, _ = _cpu_frames(torch, O, bb, dm, 224, seconds, 5, tiled=True, min_frames=min_frames)  # c5_lengths' seed
+    return dict(value=round(224 / t, 4), unit="frames/s", cores=threads, kind="port", extrapolated=False,
+                s_per_frame=round(t, 3), frames=n, wall_s=round(time.perf_counter() - t0, 1),
+                sample=f"the PyTorch-eager oracle's full frame (28 layers, cb0, depth over 31 codebooks) at 224 seats "
+                       f"(KV lengths synth.c5_lengths(224), mean {float(lengths.float().mean()):.0f}) on {threads} "
+                       f"host threads: {t:.2f} s per frame over {n} timed frames after one untimed; every slot's K/V "
+                       f"is one random slot's, copied")
 
 
 def c1_cpu(torch, reps=20):
@@ -583,6 +627,8 @@ def main():
     ap.add_argument("--mimi-only", action="store_true", help="print only the Mimi decode line (for profiling)")
     ap.add_argument("--b1-only", action="store_true", help="print only the B=1 frame latency (for profiling)")
     ap.add_argument("--only", choices=("c2", "c3", "c4"), help="print only that configuration's line (for profiling)")
+    ap.add_argument("--cpu-full", action="store_true",
+                    help="print only the oracle's full 224-seat frame on the host cores (minutes, ~60 GB of RAM)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -594,6 +640,10 @@ def main():
     from m3x import roofline, synth
     from m3x import ops
     torch.backends.cuda.matmul.allow_tf32 = False
+    if args.cpu_full:
+        log("the oracle's full 224-seat frame on the host cores")
+        print(json.dumps({"cpu_full_frame": cpu_full_frame(torch, args.cpu_seconds)}), flush=True)
+        return
     if args.mimi_only:
         print(json.dumps({"mimi_decode": mimi_decode(torch, torch.device("cuda:0"), max(args.secondary_steps, 20))}),
               flush=True)
