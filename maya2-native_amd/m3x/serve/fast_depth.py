@@ -311,9 +311,10 @@ class FastDepth:
         return b.codes, b.feedback
 
     # ---------------------------------------------------------------- persistent run
-    # The kernel takes up to 16 seats; past 8 its handovers (every residual workgroup reads the whole rows of each
-    # step's output) cost more than the launch path's kernels on MI355X, so larger batches take the launch path.
-    PERSISTENT_SEATS = 8
+    # The kernel takes up to 16 seats; past 4 its handovers (every residual workgroup reads the whole rows of each
+    # step's output) cost more than the launch path's kernels on MI355X (graph-timed 31-codebook frames: 2.70 vs
+    # 2.74 ms at 4 seats, 2.90 vs 2.87 at 5, 3.04 vs 2.78 at 8), so larger batches take the launch path.
+    PERSISTENT_SEATS = 4
     # a handover poll with more 16-byte chunks per thread than this first waits on one chunk per thread (0: every
     # poll does; measured best at 1-4 seats and within 1.5 % of the best at 8 and 16 on MI355X)
     POLL_PROBE = 0

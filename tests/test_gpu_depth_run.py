@@ -51,7 +51,7 @@ def test_swiglu_run_matches_oracle_and_launch_path(gpu, B):
     model_g = synth.swiglu_depth(seed=611, device=gpu, affine=synth.AFFINE)
     model_c = synth.swiglu_depth(seed=611, device="cpu", affine=synth.AFFINE)
     fd = FastDepth(model_g, 20, dtype=torch.bfloat16, temp=0.9, top_k=50, batch_buckets=(B,))
-    fd.PERSISTENT_SEATS = 16  # the kernel's own limit (serving switches to the launch path above 8 seats)
+    fd.PERSISTENT_SEATS = 16  # the kernel's own limit (serving switches to the launch path above 4 seats)
     fd.row_seed.copy_(torch.arange(21, dtype=torch.int32, device=gpu) * 7777 + 3)
     g = torch.Generator().manual_seed(612 + B)
     h = torch.randn(B, 1024, generator=g).to(torch.bfloat16)
@@ -82,6 +82,7 @@ def test_depthv2_runs_fp16_with_speaker(gpu):
     model_g, model_c = mk(gpu), mk("cpu")
     B = 6
     fd = FastDepth(model_g, 8, dtype=torch.float16, temp=0.7, top_k=64, batch_buckets=(B,))
+    fd.PERSISTENT_SEATS = 16  # the kernel's own limit: the run is tested past the seats serving gives it
     g = torch.Generator().manual_seed(622)
     mems = torch.randn(8, 1, 1, 1024, generator=g)
     for s in range(8):
