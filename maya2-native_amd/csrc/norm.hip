@@ -440,24 +440,27 @@ __global__ __launch_bounds__(256) void feedback_kernel(const Elt<DT>* __restrict
 #pragma unroll
   for (int e = 0; e < 8; ++e) v[e] = 0.f;
   float p = 0.f;
+  const V8<DT> wv = ldv<DT>(w + 8 * t);  // requested first: its latency overlaps the gathers
   if (active) {
-    // 32 codebooks at a time: their codes in one round trip, then their rows 16 at a time; the sum still runs
-    // over the codebooks in ascending order
+    // 32 codebooks at a time: their codes in one round trip, then their rows GB at a time, every load issued
+    // before the first add (codebooks past n_q re-read the last valid row and are not added: no load sits in a
+    // branch, which would make the compiler wait for it there); the sum runs over the codebooks in ascending order
+    constexpr int GB = sizeof(Elt<DT>) == 4 ? 16 : 32;
     for (int l0 = 0; l0 < n_q; l0 += 32) {
       int cd[32];
 #pragma unroll
       for (int i = 0; i < 32; ++i) {
-        const int c = l0 + i < n_q ? codes[(long)row * s_codes + l0 + i] : 0;
+        const int c = codes[(long)row * s_codes + min(l0 + i, n_q - 1)];
         cd[i] = c < 0 ? 0 : (c >= n_codes ? n_codes - 1 : c);
       }
 #pragma unroll
-      for (int h = 0; h < 32; h += 16) {
-        V8<DT> tv[16];
+      for (int h = 0; h < 32; h += GB) {
+        V8<DT> tv[GB];
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-          if (l0 + h + i < n_q) tv[i] = ldv<DT>(table + ((long)cd[h + i] + (long)n_codes * (l0 + h + i)) * N + 8 * t);
+        for (int i = 0; i < GB; ++i)
+          tv[i] = ldv<DT>(table + ((long)cd[h + i] + (long)n_codes * min(l0 + h + i, n_q - 1)) * N + 8 * t);
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
+        for (int i = 0; i < GB; ++i)
           if (l0 + h + i < n_q) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) v[e] = v[e] + E<DT>::to_f(tv[i].v[e]);
@@ -473,7 +476,7 @@ __global__ __launch_bounds__(256) void feedback_kernel(const Elt<DT>* __restrict
   const float ss = row_tree_sum<TPR>(p, red, bcast);
   if (!active) return;
   const float inv = 1.0f / sqrtf(ss / (float)N + eps);
-  V8<DT> wv = ldv<DT>(w + 8 * t), yv;
+  V8<DT> yv;
 #pragma unroll
   for (int e = 0; e < 8; ++e) yv.v[e] = E<DT>::from_f(v[e] * inv * E<DT>::to_f(wv.v[e]));
   stv<DT>(out + (long)row * s_out + 8 * t, yv);
