@@ -211,7 +211,8 @@ int m3x_topk_sample_embed(const void* logits, long ld_l, int V, const float* u, 
 /* cb0 controlled stop + sampling per seat (per-slot state indexed by slots[b]); any per-slot pointer may be NULL.
  * Replaces `Engine._cb0` (maya3/engine.py:652-694) with caller uniforms in place of `row_exponential`
  * (serve/fast_depth_kernels.py:82-98). topp_t[s] (or top_p when topp_t is NULL) below 1 applies the top-p cut
- * of :669-672 to the top-k set. */
+ * of :669-672 to the top-k set. hist_w (the repetition-penalty window, 12 frames by default in the engine) is at
+ * most 256 (M3X_EINVAL above). */
 int m3x_cb0_sample(const void* logits, long ld_l, int V, int aeos, const int64_t* slots, const float* u, long ld_u,
                    const float* temp_t, float temp, const int64_t* topk_t, int top_k, const float* topp_t,
                    float top_p, const float* aeos_bias,

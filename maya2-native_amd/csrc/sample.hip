@@ -51,12 +51,14 @@ __global__ __launch_bounds__(ST) void topk_sample_kernel(const Elt<DT>* __restri
   __shared__ SampleSmem sm;
   const int row = blockIdx.x;
   const float ur = greedy ? 0.f : u[(long)row * ld_u];  // loaded first: its latency overlaps the selection
+  // every element's load issued before the first is used (indices past V re-read element V - 1 and are masked
+  // after: a load under a condition would make the compiler wait for it there, one round trip per element)
+  Elt<DT> raw[NE];
+#pragma unroll
+  for (int e = 0; e < NE; ++e) raw[e] = logits[(long)row * ld_l + min((int)threadIdx.x + ST * e, V - 1)];
   float x[NE];
 #pragma unroll
-  for (int e = 0; e < NE; ++e) {
-    const int i = threadIdx.x + ST * e;
-    x[e] = i < V ? E<DT>::to_f(logits[(long)row * ld_l + i]) * inv_temp : -INFINITY;
-  }
+  for (int e = 0; e < NE; ++e) x[e] = (int)threadIdx.x + ST * e < V ? E<DT>::to_f(raw[e]) * inv_temp : -INFINITY;
   topk_select(x, V, top_k, sm);
   if (TPR == 0 && threadIdx.x >= 64) return;  // wave 0 draws
   if (threadIdx.x < 64) {
@@ -208,9 +210,16 @@ struct Cb0Args {
   int64_t* stop_out;   // [B] int64 or null
 };
 
+constexpr int CB0_HMAX = 256;  // the longest repetition-penalty history a row stages in LDS
 __global__ __launch_bounds__(ST) void cb0_sample_kernel(Cb0Args a) {
   __shared__ SampleSmem sm;
+  __shared__ int64_t hist[CB0_HMAX];
   const int row = blockIdx.x;
+  // the logits first, every element's load issued before any is used (indices past V re-read element V - 1 and are
+  // masked below: a load under a condition would make the compiler wait for it there, one round trip per element)
+  uint16_t raw[SMAXV / ST];
+#pragma unroll
+  for (int e = 0; e < SMAXV / ST; ++e) raw[e] = a.logits[(long)row * a.ld_l + min((int)threadIdx.x + ST * e, a.V - 1)];
   const long s = a.slots[row];
   const float temp = a.temp_t ? a.temp_t[s] : a.temp;
   int k = a.topk_t ? (int)a.topk_t[s] : a.top_k;
@@ -219,17 +228,22 @@ __global__ __launch_bounds__(ST) void cb0_sample_kernel(Cb0Args a) {
   const float rep = a.rep_t ? a.rep_t[s] : 0.f;
   const float top_p = a.topp_t ? a.topp_t[s] : a.top_p;
   const float uu = a.u[(long)row * a.ld_u];  // loaded first: its latency overlaps the selection
+  // the slot's recent codes for the repetition penalty, staged once in LDS (one load per entry, not per element)
+  const bool pen = a.hist_t && a.rep_t;
+  const int hw = pen ? a.hist_w : 0;  // <= CB0_HMAX (checked on the host)
+  for (int j = threadIdx.x; j < hw; j += ST) hist[j] = a.hist_t[s * a.hist_w + j];
+  __syncthreads();
   float x[SMAXV / ST];
 #pragma unroll
   for (int e = 0; e < SMAXV / ST; ++e) {
     const int i = threadIdx.x + ST * e;
     float v = -INFINITY;
     if (i < a.V) {
-      v = bf2f(a.logits[(long)row * a.ld_l + i]) / temp;
+      v = bf2f(raw[e]) / temp;
       if (i == a.aeos) v = v + bias;
-      if (a.hist_t && a.rep_t && i != a.aeos) {
+      if (pen && i != a.aeos) {
         bool seen = false;
-        for (int j = 0; j < a.hist_w; ++j) seen |= a.hist_t[s * a.hist_w + j] == (int64_t)i;
+        for (int j = 0; j < hw; ++j) seen |= hist[j] == (int64_t)i;
         if (seen) v = v - rep;
       }
     }
@@ -290,7 +304,7 @@ M3X_API int m3x_cb0_sample(const void* logits, long ld_l, int V, int aeos, const
                            const float* topp_t, float top_p, const float* aeos_bias, const float* rep_t, int64_t* hist_t, int hist_w, int64_t* frames_t,
                            const int64_t* min_t, float* hazard_t, int32_t* ctr_t, int64_t* cb0_out, int32_t* cb0_i32,
                            long ld_cb0_i32, int64_t* stop_out, int B, void* stream) {
-  if (B < 0 || V <= 0 || V > SMAXV || aeos >= V || hist_w < 0) return M3X_EINVAL;
+  if (B < 0 || V <= 0 || V > SMAXV || aeos >= V || hist_w < 0 || hist_w > CB0_HMAX) return M3X_EINVAL;
   if (B == 0) return M3X_OK;
   if (!logits || !slots || !u) return M3X_ENULL;
   if (!temp_t && !(temp > 0.f)) return M3X_EINVAL;
