@@ -97,15 +97,29 @@ M3X_API int m3x_copy_rows(const void* src, long ld_src, const void* src_idx, lon
 
 // Frame code ring: ring[(*head) % depth][b][0..nq) = codes[b][0..nq) for b < B, then *head += 1.
 // One workgroup, so the head update is ordered after every copy of this launch.
-__global__ __launch_bounds__(256) void code_ring_kernel(const int32_t* __restrict__ codes, long ld_codes,
-                                                        int32_t* __restrict__ ring, int32_t* head, int depth,
-                                                        int seats, int nq, int B) {
+__global__ __launch_bounds__(1024) void code_ring_kernel(const int32_t* __restrict__ codes, long ld_codes,
+                                                         int32_t* __restrict__ ring, int32_t* head, int depth,
+                                                         int seats, int nq, int B) {
+  // each thread's codes of a batch are all requested before the first store (clamped index, masked store), so a
+  // 224 x 32 frame is one round trip rather than one per element
+  constexpr int U = 8;
+  const int total = B * nq;
+  const int nt = blockDim.x;
   const int h = *head;
-  const int slotr = ((h % depth) + depth) % depth;
-  int32_t* dst = ring + (long)slotr * seats * nq;
-  for (int i = threadIdx.x; i < B * nq; i += blockDim.x) {
-    const int b = i / nq, j = i % nq;
-    dst[(long)b * nq + j] = codes[(long)b * ld_codes + j];
+  for (int base = 0; base < total; base += nt * U) {
+    int32_t v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = min(base + (int)threadIdx.x + nt * u, total - 1);
+      v[u] = codes[(long)(i / nq) * ld_codes + i % nq];
+    }
+    const int slotr = ((h % depth) + depth) % depth;
+    int32_t* dst = ring + (long)slotr * seats * nq;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = base + (int)threadIdx.x + nt * u;
+      if (i < total) dst[(long)(i / nq) * nq + i % nq] = v[u];
+    }
   }
   __syncthreads();
   if (threadIdx.x == 0) *head = h + 1;
@@ -116,7 +130,7 @@ M3X_API int m3x_code_ring_write(const int32_t* codes, long ld_codes, int32_t* ri
   if (B < 0 || depth <= 0 || nq <= 0 || B > seats || ld_codes < nq) return M3X_EINVAL;
   if (B == 0) return M3X_OK;
   if (!codes || !ring || !head) return M3X_ENULL;
-  hipLaunchKernelGGL(code_ring_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, codes, ld_codes, ring, head, depth,
+  hipLaunchKernelGGL(code_ring_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, codes, ld_codes, ring, head, depth,
                      seats, nq, B);
   M3X_CHECK_LAUNCH();
   return M3X_OK;

@@ -211,6 +211,14 @@ struct Cb0Args {
 };
 
 constexpr int CB0_HMAX = 256;  // the longest repetition-penalty history a row stages in LDS
+// A per-slot value, or dflt when the table is absent: the load is unconditional (an absent table reads `dummy`,
+// any valid 8-byte word), so it does not wait at a branch of its own.
+template <class T>
+__device__ __forceinline__ T slot_or(const T* p, long i, const void* dummy, T dflt) {
+  const T v = *reinterpret_cast<const T*>(p ? (const void*)(p + i) : dummy);
+  return p ? v : dflt;
+}
+
 __global__ __launch_bounds__(ST) void cb0_sample_kernel(Cb0Args a) {
   __shared__ SampleSmem sm;
   __shared__ int64_t hist[CB0_HMAX];
@@ -221,16 +229,23 @@ __global__ __launch_bounds__(ST) void cb0_sample_kernel(Cb0Args a) {
 #pragma unroll
   for (int e = 0; e < SMAXV / ST; ++e) raw[e] = a.logits[(long)row * a.ld_l + min((int)threadIdx.x + ST * e, a.V - 1)];
   const long s = a.slots[row];
-  const float temp = a.temp_t ? a.temp_t[s] : a.temp;
-  int k = a.topk_t ? (int)a.topk_t[s] : a.top_k;
+  // the slot's settings and state in one round trip
+  const void* dm = a.slots + row;
+  const float temp = slot_or(a.temp_t, s, dm, a.temp);
+  int k = (int)slot_or<int64_t>(a.topk_t, s, dm, a.top_k);
   k = k < 1 ? 1 : (k > a.V ? a.V : k);
-  const float bias = a.aeos_bias ? a.aeos_bias[s] : 0.f;
-  const float rep = a.rep_t ? a.rep_t[s] : 0.f;
-  const float top_p = a.topp_t ? a.topp_t[s] : a.top_p;
+  const float bias = slot_or(a.aeos_bias, s, dm, 0.f);
+  const float rep = slot_or(a.rep_t, s, dm, 0.f);
+  const float top_p = slot_or(a.topp_t, s, dm, a.top_p);
+  const bool stop_rule = a.frames_t && a.min_t && a.hazard_t;
+  const int64_t frames = slot_or<int64_t>(a.frames_t, s, dm, 0), min_frames = slot_or<int64_t>(a.min_t, s, dm, 0);
+  const float hz0 = slot_or(a.hazard_t, s, dm, 0.f);
+  const int32_t ctr = slot_or<int32_t>(a.ctr_t, s, dm, 0);
   const float uu = a.u[(long)row * a.ld_u];  // loaded first: its latency overlaps the selection
-  // the slot's recent codes for the repetition penalty, staged once in LDS (one load per entry, not per element)
-  const bool pen = a.hist_t && a.rep_t;
-  const int hw = pen ? a.hist_w : 0;  // <= CB0_HMAX (checked on the host)
+  // the slot's recent codes, staged once in LDS: the repetition penalty reads them, and wave 0 writes them back
+  // shifted by one with the drawn code last
+  const int hw = a.hist_t ? a.hist_w : 0;  // <= CB0_HMAX (checked on the host)
+  const bool pen = hw > 0 && a.rep_t;
   for (int j = threadIdx.x; j < hw; j += ST) hist[j] = a.hist_t[s * a.hist_w + j];
   __syncthreads();
   float x[SMAXV / ST];
@@ -250,11 +265,12 @@ __global__ __launch_bounds__(ST) void cb0_sample_kernel(Cb0Args a) {
     x[e] = v;
   }
   topk_select(x, a.V, k, sm);
-  if (threadIdx.x >= 64) return;  // wave 0 draws; lane 0 writes
+  if (threadIdx.x >= 64) return;  // wave 0 draws (every lane holds the code); lane 0 writes the rest
   int n = sm.nkeep;
   if (top_p < 1.0f) n = top_p_keep(sm, n, top_p);
   int cb0;
   int64_t stop = 0;
+  float hz = hz0;
   if (a.aeos >= 0) {
     float wa = 0.f;  // weight of the AEOS candidate (indices are distinct: at most one)
     for (int j0 = 0; j0 < n; j0 += 64) {
@@ -271,29 +287,26 @@ __global__ __launch_bounds__(ST) void cb0_sample_kernel(Cb0Args a) {
     }
     const float pa = wa / S;
     const int c = pick(sm, n, uu, a.aeos);
-    if (threadIdx.x != 0) return;
     const int arg = cand_index(sm.cand[0]);
-    if (a.frames_t && a.min_t && a.hazard_t) {
-      const bool can = a.frames_t[s] >= a.min_t[s];
-      const float hz0 = a.hazard_t[s];
-      const float hz = can ? 1.0f - (1.0f - hz0) * (1.0f - pa) : hz0;
+    if (stop_rule) {
+      const bool can = frames >= min_frames;
+      hz = can ? 1.0f - (1.0f - hz0) * (1.0f - pa) : hz0;
       if (can && arg == a.aeos) stop = 2;
       else if (can && pa >= 0.35f) stop = 3;
       else if (can && hz >= 0.6f) stop = 4;
-      a.hazard_t[s] = hz;
-      a.frames_t[s] = a.frames_t[s] + 1;
     }
     cb0 = c < 0 ? 0 : c;
   } else {
     const int c = pick(sm, n, uu, -1);
-    if (threadIdx.x != 0) return;
     cb0 = c < 0 ? cand_index(sm.cand[0]) : c;
   }
-  if (a.ctr_t) a.ctr_t[s] = a.ctr_t[s] + 1;
-  if (a.hist_t && a.hist_w > 0) {
-    for (int j = 0; j + 1 < a.hist_w; ++j) a.hist_t[s * a.hist_w + j] = a.hist_t[s * a.hist_w + j + 1];
-    a.hist_t[s * a.hist_w + a.hist_w - 1] = cb0;
+  for (int j = threadIdx.x; j < hw; j += 64) a.hist_t[s * a.hist_w + j] = j + 1 < hw ? hist[j + 1] : (int64_t)cb0;
+  if (threadIdx.x != 0) return;
+  if (a.aeos >= 0 && stop_rule) {
+    a.hazard_t[s] = hz;
+    a.frames_t[s] = frames + 1;
   }
+  if (a.ctr_t) a.ctr_t[s] = ctr + 1;
   if (a.cb0_out) a.cb0_out[row] = cb0;
   if (a.cb0_i32) a.cb0_i32[(long)row * a.ld_cb0_i32] = cb0;
   if (a.stop_out) a.stop_out[row] = stop;
