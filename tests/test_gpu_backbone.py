@@ -144,6 +144,69 @@ def test_graph_replay_equals_eager(gpu):
         assert torch.equal(a.k[i], b.k[i]) and torch.equal(a.v[i], b.v[i])
 
 
+def test_spread_decode_step_takes_item_launch(gpu):
+    """A decode step of 40 seats whose contexts are spread out (the longest above 1.5x the mean) runs its attention
+    as the item launch (splits dealt longest-first over one round of workgroups), its item list kept across steps
+    until a row crosses a split boundary. With the per-row launch's split size the outputs and caches equal that
+    launch's bit for bit, step after step (across a rebuild); with its own 1024-key splits the
+    outputs differ only by the split combine's rounding (the merge order of the fp32 partials). A step with
+    near-equal contexts, or of 16 rows, keeps the per-row launch."""
+    import m3x.serve.fast_backbone as fb
+    from m3x.serve.fast_backbone import StaticBackbone
+    bb = synth.qwen3_backbone(layers=2, seed=41, device=gpu, affine=synth.AFFINE)
+    B, cap = 40, 1024
+    lengths = torch.randint(8, 900, (B,), generator=torch.Generator().manual_seed(42))
+    lengths[0] = 950  # longest context: 950 + 1 keys against a mean near 450
+    lengths[1] = 510  # crosses a 512-key split boundary on the third step: the cached item list is rebuilt
+
+    def backbone(item_chunk=None):
+        saved = fb.item_chunk
+        if item_chunk is not None:
+            fb.item_chunk = item_chunk
+        try:
+            sb = StaticBackbone(bb, B, capacity=cap, batch_buckets=(48,), ctx_buckets=(cap,), attention="triton",
+                                fuse_rope=True)
+            sb.warmup()
+        finally:
+            fb.item_chunk = saved
+        g = torch.Generator(device=gpu).manual_seed(43)
+        with torch.inference_mode():  # the caches are inference tensors
+            for i in range(2):
+                sb.k[i].normal_(generator=g)
+                sb.v[i].normal_(generator=g)
+            sb.lengths[:B].copy_(lengths)
+        sb.lengths_cpu[:B] = lengths.tolist()
+        return sb
+
+    per_row_chunk = fb.attn_chunk(48, 8, cap)
+    same, own, ref = backbone(lambda rows: per_row_chunk), backbone(), backbone()
+    assert any(k[-1] == "items" for k in same.graphs)  # warmup captured both launches of the 48-row bucket
+    assert same._graph(48, cap, items=True).bufs.chunk == per_row_chunk and own._graph(48, cap, items=True).bufs.chunk == 1024
+    g = torch.Generator().manual_seed(44)
+    slots = list(range(B))
+    skew = fb.ITEM_SKEW
+    for t in range(3):
+        x = torch.randn(B, 1024, generator=g).to(torch.bfloat16).to(gpu)
+        runs = [(r, 1, same.lengths_cpu[s]) for r, s in enumerate(slots)]
+        assert same._spread(48, runs) and own._spread(48, runs)
+        y_same, y_own = same.step(slots, x), own.step(slots, x)
+        try:
+            fb.ITEM_SKEW = float("inf")  # the per-row launch for ref
+            assert not ref._spread(48, runs)
+            y_ref = ref.step(slots, x)
+        finally:
+            fb.ITEM_SKEW = skew
+        assert torch.equal(y_same, y_ref), t
+        # the list is rebuilt only when a row's split count changes (the 512-key lists at step 3)
+        assert same._graph(48, cap, items=True).items_key[1][1] == (same.lengths_cpu[1] - 1 + per_row_chunk) // per_row_chunk
+        ok, info = close(y_own, y_ref, atol=2e-2)
+        assert ok, (t, info)
+    for i in range(2):
+        assert torch.equal(same.k[i], ref.k[i]) and torch.equal(same.v[i], ref.v[i])
+    even = [(r, 1, 500 + r % 7) for r in range(B)]
+    assert not same._spread(48, even) and not same._spread(16, runs)
+
+
 def test_errors_match_reference_conventions(gpu):
     sb = _setup(gpu)[0]
     x = torch.zeros(2, 1024, dtype=torch.bfloat16, device=gpu)
