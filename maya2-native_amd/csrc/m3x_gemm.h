@@ -1022,6 +1022,224 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
   }
 }
 
+// Large-M projections in bf16, column strips (M > 512 rows; preferred over linear_tiled_kernel where an instance
+// exists). A workgroup of 4 waves owns BM = 16 RT activation rows x 4 strips of NG weight tiles: wave w's strip is
+// tiles (4 nb + w) NG .. + NG - 1 (16 NG columns; with SwiGLU NG gate tiles and the same NG up tiles). A wave loads
+// its strip's packed fragments from global memory straight into its registers (a fragment is one contiguous 1 KB
+// that no other wave of the workgroup reads), two K stages of 64 ahead in three register sets; only the activation
+// rows pass through LDS (double-buffered, 144-byte row stride), where all 4 waves read them. Against the 2-D tiles
+// of linear_tiled_kernel, where every wave reads both operands from LDS, this cuts the LDS traffic per product by
+// more than half (measured at 2264 rows: waves waiting on LDS issue 27 % -> 3 % of their cycles; q|k|v 34 -> 27.5
+// us, gate|up + SwiGLU 47 -> 40 us, down 38 -> 34 us). Products accumulate in the same K order with the same MFMA as
+// linear_tiled_kernel, so the two kernels give the same bits. Epilogues as linear_tiled_kernel's; EPI_QKR needs
+// BN = 64 NG to hold whole heads of 128 columns (2 per workgroup at NG = 4).
+template <int DT, int EPI, bool PRO, int RT, int NG>
+__global__ __launch_bounds__(256) void linear_strip_kernel(const uint16_t* __restrict__ X, long ldx,
+                                                          const uint16_t* __restrict__ Wp,
+                                                          const uint16_t* __restrict__ W2p, uint16_t* __restrict__ Y,
+                                                          long ldy, int M, int N, int K, int mblk, int nblk,
+                                                          NormIn ni, ResidOut ro, QkOut qk) {
+  constexpr bool DUAL = EPI == EPI_SWIGLU;
+  constexpr int NA = DUAL ? 2 : 1;           // weight operands (gate, up)
+  constexpr int BM = 16 * RT;                // activation rows per workgroup
+  constexpr int LDA = 72;                    // activation row stride in LDS, halfwords
+  constexpr int CPT = (BM * 8 + 255) / 256;  // 16-byte activation chunks per thread and stage
+  constexpr int BN = 64 * NG;                // columns per workgroup
+  constexpr int LDT = BN + 8;                // EPI_QKR's staged tile row stride, halfwords
+  constexpr int LDS_A = 2 * BM * LDA;
+  constexpr int LDS_T = EPI == EPI_QKR ? BM * LDT : 0;
+  __shared__ __align__(16) uint16_t smem[LDS_A > LDS_T ? LDS_A : LDS_T];
+  __shared__ float2 pst[PRO ? BM : 1];
+  uint16_t* const la0 = smem;
+  uint16_t* const la1 = smem + BM * LDA;
+
+  const int xcd = blockIdx.x & 7;
+  const int slot = blockIdx.x >> 3;
+  const int nb = (slot / mblk) * 8 + xcd;
+  const int mb = slot - (slot / mblk) * mblk;
+  if (nb >= nblk) return;  // padding block: the whole workgroup leaves before any barrier
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+  const int ksteps = K >> 5;
+  const int ntiles = (N + 15) >> 4;
+  const int m0 = mb * BM;
+  const int t0 = (nb * 4 + wave) * NG;  // the wave's first weight tile
+  NormStage<BM, 256, PRO_K / 128> ns;
+
+  // 32-bit element offsets (the host checks that both operands fit). Tiles past N and rows past M are read at a
+  // valid clamped place and never stored; activation chunks past the block repeat row BM - 1 (the same value to
+  // the same LDS place).
+  int wo[NG];
+#pragma unroll
+  for (int i = 0; i < NG; ++i) wo[i] = min(t0 + i, ntiles - 1) * ksteps * 512 + lane * 8;
+  int ga[CPT], lo[CPT];
+#pragma unroll
+  for (int q = 0; q < CPT; ++q) {
+    const int c = tid + 256 * q;
+    const int r = min(c >> 3, BM - 1);
+    ga[q] = min(m0 + r, M - 1) * (int)ldx + 8 * (c & 7);
+    lo[q] = r * LDA + 8 * (c & 7);
+  }
+
+  f32x4_t acc[NA][NG][RT];
+#pragma unroll
+  for (int a = 0; a < NA; ++a)
+#pragma unroll
+    for (int i = 0; i < NG; ++i)
+#pragma unroll
+      for (int j = 0; j < RT; ++j) acc[a][i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // stages past the end re-read the last stage (valid addresses, never used)
+  const int nst = K >> 6;
+  auto wload = [&](int stg, u16x8(&w)[NA][NG][2]) {
+    const int sc = min(stg, nst - 1);
+#pragma unroll
+    for (int a = 0; a < NA; ++a)
+#pragma unroll
+      for (int i = 0; i < NG; ++i)
+#pragma unroll
+        for (int s = 0; s < 2; ++s) w[a][i][s] = ld16((a ? W2p : Wp) + wo[i] + (2 * sc + s) * 512);
+  };
+  auto aload = [&](int stg, u16x8(&r)[CPT]) {
+    const int sc = min(stg, nst - 1);
+#pragma unroll
+    for (int q = 0; q < CPT; ++q) r[q] = ld16(X + ga[q] + sc * 64);
+  };
+  auto astore = [&](uint16_t* buf, const u16x8(&r)[CPT]) {
+#pragma unroll
+    for (int q = 0; q < CPT; ++q) st16(buf + lo[q], r[q]);
+  };
+  auto compute = [&](const uint16_t* buf, const u16x8(&w)[NA][NG][2]) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int j = 0; j < RT; ++j) {
+        const u16x8 b = *reinterpret_cast<const u16x8*>(buf + (16 * j + li) * LDA + 32 * s + 8 * lg);
+#pragma unroll
+        for (int a = 0; a < NA; ++a)
+#pragma unroll
+          for (int i = 0; i < NG; ++i) acc[a][i][j] = mfma16x16x32<DT>(w[a][i][s], b, acc[a][i][j]);
+      }
+  };
+  u16x8 W0[NA][NG][2], W1[NA][NG][2], W2[NA][NG][2];
+  u16x8 A0[CPT], A1[CPT];
+  wload(0, W0);
+  aload(0, A0);
+  wload(1, W1);
+  aload(1, A1);
+  astore(la0, A0);
+  __syncthreads();
+  // Stage s issues the weights (register set s + 2 mod 3) and activations (set s mod 2, stored to LDS during stage
+  // s - 1) of stage s + 2, multiplies stage s (weights from set s mod 3, activations from LDS buffer s mod 2),
+  // stores stage s + 1's activations to the other buffer, then meets the workgroup: unrolled by 6.
+#define M3X_STRIP_STAGE(S, WN, WC, AN, AS, BUF, OBUF) \
+  if (s0 + S < nst) {                                 \
+    wload(s0 + S + 2, WN);                            \
+    aload(s0 + S + 2, AN);                            \
+    compute(BUF, WC);                                 \
+    if (s0 + S + 1 < nst) astore(OBUF, AS);           \
+    __syncthreads();                                  \
+  }
+  for (int s0 = 0; s0 < nst; s0 += 6) {
+    M3X_STRIP_STAGE(0, W2, W0, A0, A1, la0, la1)
+    M3X_STRIP_STAGE(1, W0, W1, A1, A0, la1, la0)
+    M3X_STRIP_STAGE(2, W1, W2, A0, A1, la0, la1)
+    M3X_STRIP_STAGE(3, W2, W0, A1, A0, la1, la0)
+    M3X_STRIP_STAGE(4, W0, W1, A0, A1, la0, la1)
+    M3X_STRIP_STAGE(5, W1, W2, A1, A0, la1, la0)
+  }
+#undef M3X_STRIP_STAGE
+
+  // the epilogue's operands load after the products, as in linear_tiled_kernel
+  ResidPre pre[EPI == EPI_RESID ? NG : 1][RT];
+  if constexpr (EPI == EPI_RESID) {
+#pragma unroll
+    for (int i = 0; i < NG; ++i)
+#pragma unroll
+      for (int j = 0; j < RT; ++j) pre[i][j] = resid_prefetch(ro, m0 + 16 * j + li, (t0 + i) * 16 + 4 * lg, M, N);
+  }
+  if constexpr (PRO) {
+    ns.load(ni, m0, M, PRO_K);
+    ns.finish(ni, m0, M, PRO_K, pst);
+    __syncthreads();
+#pragma unroll
+    for (int a = 0; a < NA; ++a)
+#pragma unroll
+      for (int i = 0; i < NG; ++i)
+#pragma unroll
+        for (int j = 0; j < RT; ++j) norm_apply(acc[a][i][j], pst, 16 * j + li, ni, (t0 + i) * 16 + 4 * lg, N, a);
+  }
+  if constexpr (EPI == EPI_RESID) {
+#pragma unroll
+    for (int i = 0; i < NG; ++i)
+#pragma unroll
+      for (int j = 0; j < RT; ++j)
+        resid_quad<DT>(acc[0][i][j], pre[i][j], m0 + 16 * j + li, (t0 + i) * 16 + 4 * lg, t0 + i, M, N, lg, ro, Y,
+                       ldy);
+    return;
+  }
+  if constexpr (EPI == EPI_QKR) {
+    static_assert(DT == M3X_BF16 && BN % 128 == 0, "bf16, whole heads per workgroup");
+    // the workgroup's BN columns are BN / 128 heads: stage the tile in LDS (free after the loop's last barrier),
+    // then the per-head norm, RoPE and cache writes
+    uint16_t* tile = smem;
+#pragma unroll
+    for (int i = 0; i < NG; ++i)
+#pragma unroll
+      for (int j = 0; j < RT; ++j) qk_stage(tile, LDT, 16 * j + li, 16 * (wave * NG + i) + 4 * lg, acc[0][i][j]);
+    __syncthreads();
+    qk_items<BM, BN / 128, 256>(tile, LDT, nb, m0, M, qk);
+    return;
+  }
+  // lane (li, lg) of tile (i, j) holds columns 4 lg + r of weight tile t0 + i for activation row m0 + 16 j + li
+  const bool vec = (ldy & 3) == 0 && (((uintptr_t)Y) & 7) == 0;
+#pragma unroll
+  for (int i = 0; i < NG; ++i) {
+    const int n = (t0 + i) * 16 + 4 * lg;
+#pragma unroll
+    for (int j = 0; j < RT; ++j) {
+      const int m = m0 + 16 * j + li;
+      if (m >= M) continue;
+      uint16_t o[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float v = rnd<DT>(acc[0][i][j][r]);
+        if constexpr (DUAL) {
+          const float u = rnd<DT>(acc[1][i][j][r]);
+          v = rnd<DT>(silu16(v)) * u;
+        } else if constexpr (EPI == EPI_GELU) {
+          v = 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+        }
+        o[r] = E<DT>::from_f(v);
+      }
+      uint16_t* yp = Y + (long)m * ldy + n;
+      if (vec && n + 3 < N) {
+        uint2 pk;
+        pk.x = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
+        pk.y = (uint32_t)o[2] | ((uint32_t)o[3] << 16);
+        *reinterpret_cast<uint2*>(yp) = pk;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (n + r < N) yp[r] = o[r];
+      }
+    }
+  }
+}
+
+// The strip plan's geometry: 80-row blocks (RT = 5; measured best of 5, 8, 9 and 15 at 2264 and 4096 rows, with two
+// workgroups per CU), 4 weight tiles per wave (2 gate + 2 up pairs with SwiGLU, 2 for the residual projections,
+// whose N = 1024 otherwise leaves too few workgroups).
+constexpr int STRIP_RT = 5;
+template <int EPI>
+constexpr int strip_ng() {
+  return EPI == EPI_SWIGLU || EPI == EPI_RESID ? 2 : 4;
+}
+
 // Launch geometry: MT activation tiles of 16 rows per workgroup; NW weight tiles per workgroup; NWAVES waves
 // (NWAVES / NW K slices).
 struct LinearPlan {
@@ -1143,6 +1361,17 @@ static bool launch_linear(const LinearPlan& p, hipStream_t st, const uint16_t* X
                           const ResidOut& ro = ResidOut{}, const QkOut& qk = QkOut{}) {
   static_assert(!(PRO && EPI == EPI_RESID), "a residual projection takes its input as is");
   const dim3 grid(m3x_ceil_div(p.nblk, 8) * 8 * p.mblk);
+  if constexpr (DT == M3X_BF16) {
+    // the tiled plan's shapes in bf16 take the strip kernel (EPI_QKR: when its 256-column blocks hold whole heads)
+    constexpr int NG = strip_ng<EPI>();
+    if (p.tiled && (EPI != EPI_QKR || N % (64 * NG) == 0)) {
+      const int nblk = m3x_ceil_div(m3x_ceil_div(N, 16), 4 * NG);
+      const int mblk = m3x_ceil_div(M, 16 * STRIP_RT);
+      hipLaunchKernelGGL((linear_strip_kernel<DT, EPI, PRO, STRIP_RT, NG>), dim3(m3x_ceil_div(nblk, 8) * 8 * mblk),
+                         dim3(256), 0, st, X, ldx, W, W2, Y, ldy, M, N, K, mblk, nblk, ni, ro, qk);
+      return true;
+    }
+  }
   if constexpr (EPI == EPI_QKR) {
     // whole heads per workgroup: the tiled plan (128 columns) or the one-shot plan of 8 weight tiles in one K slice
     if (p.tiled) {
