@@ -480,6 +480,58 @@ __device__ __forceinline__ void qk_items(const uint16_t* tile, int LDT, int nb, 
   }
 }
 
+// qk_items for a kernel that staged each row's clamped position and slot in LDS at its start (sps, ssl). DPP row g
+// (of NT / 16) takes head g % HPW of rows g / HPW + (NT / 16 / HPW) k, and loads every cos/sin row of its items
+// before the first is used: one round trip for all of them rather than a dependent pos -> cos/sin pair per item.
+// Same arithmetic per item as qk_items.
+template <int ROWS, int HPW, int NT>
+__device__ __forceinline__ void qk_items_staged(const uint16_t* tile, int LDT, int nb, int m0, int M,
+                                                const QkOut& qk, const int* sps, const long* ssl) {
+  constexpr int HD = 128;
+  constexpr int G = NT / 16;
+  static_assert(G % HPW == 0 && (ROWS * HPW) % G == 0, "whole rows per DPP row");
+  constexpr int IPG = ROWS * HPW / G;  // items per DPP row
+  constexpr int RS = G / HPW;          // row stride between them
+  const int tid = threadIdx.x;
+  const int t = tid & 15;
+  const int g = tid >> 4;
+  const int hh = g % HPW;
+  const int r0 = g / HPW;
+  const int j = nb * HPW + hh;  // head of q|k|v (uniform in the DPP row)
+  if (j >= qk.H + qk.KV) {
+#pragma unroll
+    for (int k = 0; k < IPG; ++k) {
+      const int r = r0 + RS * k;
+      if (m0 + r < M)
+        st16(qk.vc + ssl[r] * qk.sk_s + (long)(j - qk.H - qk.KV) * qk.sk_h + (long)sps[r] * qk.sk_t + 8 * t,
+             *reinterpret_cast<const u16x8*>(&tile[r * LDT + HD * hh + 8 * t]));
+    }
+    return;
+  }
+  const u16x8 wv = ld16((j < qk.H ? qk.wq : qk.wk) + 8 * t);
+  u16x8 cv[IPG], sv[IPG];
+#pragma unroll
+  for (int k = 0; k < IPG; ++k) {
+    const long ps = sps[r0 + RS * k];
+    cv[k] = ld16(qk.cosb + ps * qk.s_cos + 8 * t);
+    sv[k] = ld16(qk.sinb + ps * qk.s_cos + 8 * t);
+  }
+#pragma unroll
+  for (int k = 0; k < IPG; ++k) {
+    const int r = r0 + RS * k;
+    const u16x8 xv = *reinterpret_cast<const u16x8*>(&tile[r * LDT + HD * hh + 8 * t]);
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = bf2f(xv.v[e]);
+    const u16x8 ov = qk_norm_rope8<HD>(x, wv, cv[k], sv[k], qk.eps, t);
+    if (m0 + r >= M) continue;
+    if (j < qk.H)
+      st16(qk.q + (long)(m0 + r) * qk.s_qb + (long)j * qk.s_qh + 8 * t, ov);
+    else
+      st16(qk.kc + ssl[r] * qk.sk_s + (long)(j - qk.H) * qk.sk_h + (long)sps[r] * qk.sk_t + 8 * t, ov);
+  }
+}
+
 // One lane's 4 outputs (columns c .. c + 3 of the workgroup, row r) rounded to bf16 into the staged tile.
 __device__ __forceinline__ void qk_stage(uint16_t* tile, int LDT, int r, int c, const f32x4_t& acc) {
   uint2 pk;
@@ -1050,6 +1102,8 @@ __global__ __launch_bounds__(256) void linear_strip_kernel(const uint16_t* __res
   constexpr int LDS_T = EPI == EPI_QKR ? BM * LDT : 0;
   __shared__ __align__(16) uint16_t smem[LDS_A > LDS_T ? LDS_A : LDS_T];
   __shared__ float2 pst[PRO ? BM : 1];
+  __shared__ int sps[EPI == EPI_QKR ? BM : 1];    // EPI_QKR: the rows' clamped positions
+  __shared__ long ssl[EPI == EPI_QKR ? BM : 1];   // and slots
   uint16_t* const la0 = smem;
   uint16_t* const la1 = smem + BM * LDA;
 
@@ -1114,23 +1168,69 @@ __global__ __launch_bounds__(256) void linear_strip_kernel(const uint16_t* __res
     for (int q = 0; q < CPT; ++q) st16(buf + lo[q], r[q]);
   };
   auto compute = [&](const uint16_t* buf, const u16x8(&w)[NA][NG][2]) {
+    if constexpr (NA * NG <= 2) {
+      // two products per activation fragment leave its LDS latency exposed: substep 0's fragments are read
+      // first, then substep 1's reads go out under substep 0's products (measured at 2264 rows: o 24.1 -> 21.8 us,
+      // down 31.8 -> 28.3 us; with 4 products per fragment the extra registers cost the second workgroup per CU)
+      u16x8 b0[RT], b1[RT];
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+      for (int j = 0; j < RT; ++j) b0[j] = *reinterpret_cast<const u16x8*>(buf + (16 * j + li) * LDA + 8 * lg);
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int j = 0; j < RT; ++j) {
-        const u16x8 b = *reinterpret_cast<const u16x8*>(buf + (16 * j + li) * LDA + 32 * s + 8 * lg);
+      for (int j = 0; j < RT; ++j) b1[j] = *reinterpret_cast<const u16x8*>(buf + (16 * j + li) * LDA + 32 + 8 * lg);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < RT; ++j)
 #pragma unroll
         for (int a = 0; a < NA; ++a)
 #pragma unroll
-          for (int i = 0; i < NG; ++i) acc[a][i][j] = mfma16x16x32<DT>(w[a][i][s], b, acc[a][i][j]);
-      }
+          for (int i = 0; i < NG; ++i) acc[a][i][j] = mfma16x16x32<DT>(w[a][i][0], b0[j], acc[a][i][j]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < RT; ++j)
+#pragma unroll
+        for (int a = 0; a < NA; ++a)
+#pragma unroll
+          for (int i = 0; i < NG; ++i) acc[a][i][j] = mfma16x16x32<DT>(w[a][i][1], b1[j], acc[a][i][j]);
+    } else {
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int j = 0; j < RT; ++j) {
+          const u16x8 b = *reinterpret_cast<const u16x8*>(buf + (16 * j + li) * LDA + 32 * s + 8 * lg);
+#pragma unroll
+          for (int a = 0; a < NA; ++a)
+#pragma unroll
+            for (int i = 0; i < NG; ++i) acc[a][i][j] = mfma16x16x32<DT>(w[a][i][s], b, acc[a][i][j]);
+        }
+    }
   };
+  // The epilogue's row operands are read here, with the first stages' loads, and kept in LDS, so that no global
+  // round trip is left after the products: EPI_QKR's positions and slots (loads clamped to valid rows, no branch
+  // around them) and PRO's row scale and shift (measured at 2264 rows in the C4 step: gate|up + SwiGLU + norm
+  // 45.9 -> us, q|k|v + norm + RoPE + cache 38.5 -> us).
+  int qps = 0;
+  long qsl = 0;
+  if constexpr (EPI == EPI_QKR) {
+    const int m = min(m0 + min(tid, BM - 1), M - 1);
+    qps = min(max(qk.pos[m], 0), qk.cap - 1);  // 0 <= pos < cap from the host; the clamp keeps writes in the slot
+    qsl = qk.slots[m];
+  }
+  if constexpr (PRO) ns.load(ni, m0, M, PRO_K);
   u16x8 W0[NA][NG][2], W1[NA][NG][2], W2[NA][NG][2];
   u16x8 A0[CPT], A1[CPT];
   wload(0, W0);
   aload(0, A0);
   wload(1, W1);
   aload(1, A1);
+  if constexpr (EPI == EPI_QKR) {
+    if (tid < BM) {
+      sps[tid] = qps;
+      ssl[tid] = qsl;
+    }
+  }
+  if constexpr (PRO) ns.finish(ni, m0, M, PRO_K, pst);
   astore(la0, A0);
   __syncthreads();
   // Stage s issues the weights (register set s + 2 mod 3) and activations (set s mod 2, stored to LDS during stage
@@ -1163,9 +1263,6 @@ __global__ __launch_bounds__(256) void linear_strip_kernel(const uint16_t* __res
       for (int j = 0; j < RT; ++j) pre[i][j] = resid_prefetch(ro, m0 + 16 * j + li, (t0 + i) * 16 + 4 * lg, M, N);
   }
   if constexpr (PRO) {
-    ns.load(ni, m0, M, PRO_K);
-    ns.finish(ni, m0, M, PRO_K, pst);
-    __syncthreads();
 #pragma unroll
     for (int a = 0; a < NA; ++a)
 #pragma unroll
@@ -1192,7 +1289,7 @@ __global__ __launch_bounds__(256) void linear_strip_kernel(const uint16_t* __res
 #pragma unroll
       for (int j = 0; j < RT; ++j) qk_stage(tile, LDT, 16 * j + li, 16 * (wave * NG + i) + 4 * lg, acc[0][i][j]);
     __syncthreads();
-    qk_items<BM, BN / 128, 256>(tile, LDT, nb, m0, M, qk);
+    qk_items_staged<BM, BN / 128, 256>(tile, LDT, nb, m0, M, qk, sps, ssl);
     return;
   }
   // lane (li, lg) of tile (i, j) holds columns 4 lg + r of weight tile t0 + i for activation row m0 + 16 j + li
