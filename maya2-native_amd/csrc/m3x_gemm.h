@@ -1082,7 +1082,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
 // rows pass through LDS (double-buffered, 144-byte row stride), where all 4 waves read them. Against the 2-D tiles
 // of linear_tiled_kernel, where every wave reads both operands from LDS, this cuts the LDS traffic per product by
 // more than half (measured at 2264 rows: waves waiting on LDS issue 27 % -> 3 % of their cycles; q|k|v 34 -> 27.5
-// us, gate|up + SwiGLU 47 -> 40 us, down 38 -> 34 us). Products accumulate in the same K order with the same MFMA as
+// us, gate|up + SwiGLU 47 -> 40 us, down 38 -> 28 us with its substep-pipelined reads). Products accumulate in the same K order with the same MFMA as
 // linear_tiled_kernel, so the two kernels give the same bits. Epilogues as linear_tiled_kernel's; EPI_QKR needs
 // BN = 64 NG to hold whole heads of 128 columns (2 per workgroup at NG = 4).
 template <int DT, int EPI, bool PRO, int RT, int NG>
@@ -1208,8 +1208,8 @@ __global__ __launch_bounds__(256) void linear_strip_kernel(const uint16_t* __res
   };
   // The epilogue's row operands are read here, with the first stages' loads, and kept in LDS, so that no global
   // round trip is left after the products: EPI_QKR's positions and slots (loads clamped to valid rows, no branch
-  // around them) and PRO's row scale and shift (measured at 2264 rows in the C4 step: gate|up + SwiGLU + norm
-  // 45.9 -> us, q|k|v + norm + RoPE + cache 38.5 -> us).
+  // around them) and PRO's row scale and shift (measured at 2264 rows inside the mixed step: gate|up + SwiGLU +
+  // norm 45.9 -> 43.0 us, q|k|v + norm + RoPE + cache 38.5 -> 33.0 us).
   int qps = 0;
   long qsl = 0;
   if constexpr (EPI == EPI_QKR) {
