@@ -475,6 +475,8 @@ M3X_API long m3x_decode_attn_items(const int32_t* runs, int nruns, int heads, in
   const int qb = std::max(1, 16 / (heads / kv_heads));
   std::vector<long> cost;
   std::vector<int32_t> code;
+  cost.reserve(nruns * 2);
+  code.reserve(nruns * 2);
   for (int i = 0; i < nruns; ++i) {
     const long r0 = runs[3 * i], n = runs[3 * i + 1], p0 = runs[3 * i + 2];
     if (r0 < 0 || n < 0 || p0 < 0 || r0 + n > (1L << 20)) return M3X_EINVAL;
@@ -494,30 +496,34 @@ M3X_API long m3x_decode_attn_items(const int32_t* runs, int nruns, int heads, in
   std::vector<long> order(nitems);
   for (long i = 0; i < nitems; ++i) order[i] = i;
   std::stable_sort(order.begin(), order.end(), [&](long a, long b) { return cost[a] > cost[b]; });
-  std::vector<std::vector<int32_t>> per(bins);
+  // the bin of the j-th item in dealing order, then the codes placed bin by bin in that order
+  std::vector<int> bin_of(nitems);
+  std::vector<long> count(bins, 0);
   using Load = std::pair<long, int>;
   std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
   const long k = std::min<long>(bins, nitems);
   for (long b = 0; b < k; ++b) {
-    per[b].push_back(code[order[b]]);
+    bin_of[b] = (int)b;
     heap.push(Load(cost[order[b]], (int)b));
   }
   for (long j = k; j < nitems; ++j) {
-    const long i = order[j];
     const Load top = heap.top();
     heap.pop();
-    per[top.second].push_back(code[i]);
-    heap.push(Load(top.first + cost[i], top.second));
+    bin_of[j] = top.second;
+    heap.push(Load(top.first + cost[order[j]], top.second));
   }
+  for (long j = 0; j < nitems; ++j) ++count[bin_of[j]];
   out[0] = bins;
   out[1] = 0;
-  long w = 2 + bins, acc = 0;
+  long acc = 0;
   for (int b = 0; b < bins; ++b) {
-    acc += (long)per[b].size();
+    const long c = count[b];
+    count[b] = 2 + bins + acc;  // the bin's next write position
+    acc += c;
     out[2 + b] = (int32_t)acc;
-    for (int32_t c : per[b]) out[w++] = c;
   }
-  return w;
+  for (long j = 0; j < nitems; ++j) out[count[bin_of[j]]++] = code[order[j]];
+  return 2 + bins + nitems;
 }
 
 template <int G>

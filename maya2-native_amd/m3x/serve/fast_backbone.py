@@ -32,6 +32,7 @@ from __future__ import annotations
 
 from types import SimpleNamespace
 
+import numpy as np
 import torch
 
 from .. import ops
@@ -419,22 +420,36 @@ class StaticBackbone:
         context more than ITEM_SKEW times the mean."""
         if rows < ITEM_MIN_ROWS or self._persistent_ok(rows):
             return False
-        ctxs = [p + 1 for _, _, p in runs]
-        return max(ctxs) > ITEM_SKEW * (sum(ctxs) / len(ctxs))
+        ctxs = np.asarray(runs, dtype=np.int64).reshape(-1, 3)[:, 2] + 1
+        return int(ctxs.max()) > ITEM_SKEW * (int(ctxs.sum()) / len(ctxs))
 
     def _rows_of(self, slots, prefills):
         """The step's rows: one per decoding seat, then T per prefill (same slot, offsets 0..T-1). Validates the
-        slots and the context; returns (row slots, row offsets, runs for the attention items, context needed)."""
+        slots and the context; returns (row slots, row offsets, runs for the attention items as int32 [runs, 3] of
+        (first row, rows, first position), context needed). Built as arrays: a step with inline prefills has
+        thousands of rows."""
         check_slots(list(slots) + [s for s, _ in prefills], self.max_slots)
-        row_slot, row_off = list(slots), [0] * len(slots)
-        runs = [(r, 1, self.lengths_cpu[s]) for r, s in enumerate(slots)]
-        need = max([self.lengths_cpu[s] + 1 for s in slots], default=0)
-        for s, t in prefills:
-            n = t.shape[0]
-            runs.append((len(row_slot), n, self.lengths_cpu[s]))
-            row_slot += [s] * n
-            row_off += range(n)
-            need = max(need, self.lengths_cpu[s] + n)
+        nd = len(slots)
+        dec = np.fromiter((self.lengths_cpu[s] for s in slots), dtype=np.int64, count=nd)
+        sizes = np.fromiter((t.shape[0] for _, t in prefills), dtype=np.int64, count=len(prefills))
+        pstart = np.fromiter((self.lengths_cpu[s] for s, _ in prefills), dtype=np.int64, count=len(prefills))
+        first = nd + np.concatenate(([0], np.cumsum(sizes)[:-1])) if len(prefills) else sizes
+        runs = np.empty((nd + len(prefills), 3), dtype=np.int32)
+        runs[:nd, 0] = np.arange(nd)
+        runs[:nd, 1] = 1
+        runs[:nd, 2] = dec
+        runs[nd:, 0] = first
+        runs[nd:, 1] = sizes
+        runs[nd:, 2] = pstart
+        total = nd + int(sizes.sum())
+        row_slot = np.empty(total, dtype=np.int64)
+        row_slot[:nd] = np.fromiter(slots, dtype=np.int64, count=nd)
+        row_off = np.zeros(total, dtype=np.int64)
+        if len(prefills):
+            pslots = np.fromiter((s for s, _ in prefills), dtype=np.int64, count=len(prefills))
+            row_slot[nd:] = np.repeat(pslots, sizes)
+            row_off[nd:] = np.arange(total - nd) - np.repeat(first - nd, sizes)
+        need = max(int(dec.max()) + 1 if nd else 0, int((pstart + sizes).max()) if len(prefills) else 0)
         if need > self.capacity:
             raise ValueError(f'context {need} exceeds capacity {self.capacity}')
         return row_slot, row_off, runs, need
@@ -451,15 +466,19 @@ class StaticBackbone:
         g = self._graph(rows, self._ctx.pick(need, 'context'), bool(prefills), spread)
         b = g.bufs
         # a decode step keyed by its seats restages nothing when they repeat
-        b.table.stage(dict(slot=row_slot, real=[1] * n, offset=row_off),
+        b.table.stage(dict(slot=row_slot, real=np.ones(n, dtype=np.int64), offset=row_off),
                       key=None if prefills else ('decode', tuple(slots)))
         if prefills or spread:
             # a decode step's list stays valid while every row keeps its number of splits (the kernels take each
             # split's keys and a row's split count from the positions at run time): it is rebuilt only when a row
             # crosses a split boundary or the seats change
-            key = None if prefills else (tuple(slots), tuple((p + b.chunk) // b.chunk for _, _, p in runs))
+            key = None if prefills else (tuple(slots), tuple(((runs[:, 2] + b.chunk) // b.chunk).tolist()))
             if key is None or key != g.items_key:
-                runs += [(r, 1, 0) for r in range(n, b.rows)]  # padding rows on the dummy slot
+                if b.rows > n:  # padding rows on the dummy slot
+                    pad = np.zeros((b.rows - n, 3), dtype=np.int32)
+                    pad[:, 0] = np.arange(n, b.rows)
+                    pad[:, 1] = 1
+                    runs = np.concatenate([runs, pad])
                 items = ops.attn_items(runs, self.heads, self.kv_heads, b.item_bins, b.chunk)
                 g.items.buffer()[:len(items)] = items
                 g.items.send(len(items))
