@@ -199,3 +199,42 @@ def test_row_table_staging_and_buckets():
     with pytest.raises(IndexError):
         check_slots([4], 4)
     check_slots([1, 1], 4, distinct=False)
+
+
+def test_mixed_step_rows_layout():
+    """The host side of StaticBackbone.step_mixed (serve/fast_backbone.py:326-359): the decoding seats' rows first,
+    then each prefill's T rows on its slot at offsets 0..T-1; one attention run per decode row (row, 1, its
+    position) and one per prefill (its first row, T, its first position); the context needed is the longest of
+    them, and a step past the capacity raises. Checked on random mixes against the rows spelled out one by one."""
+    import numpy as np
+    from types import SimpleNamespace
+    from m3x.serve.fast_backbone import StaticBackbone
+    rng = np.random.default_rng(17)
+    for _ in range(100):
+        S = 64
+        lengths = [int(v) for v in rng.integers(0, 900, S + 1)]
+        perm = [int(v) for v in rng.permutation(S)]
+        nd, npf = int(rng.integers(0, 12)), int(rng.integers(0, 4))
+        if nd + npf == 0:
+            continue
+        slots = perm[:nd]
+        prefills = [(s, torch.empty(int(rng.integers(1, 40)), 1)) for s in perm[nd:nd + npf]]
+        host = SimpleNamespace(lengths_cpu=lengths, max_slots=S, capacity=1000)
+        row_slot, row_off, runs, need = StaticBackbone._rows_of(host, slots, prefills)
+        want_slot, want_off, want_runs, want_need = [], [], [], 0
+        for s in slots:
+            want_runs.append([len(want_slot), 1, lengths[s]])
+            want_slot.append(s)
+            want_off.append(0)
+            want_need = max(want_need, lengths[s] + 1)
+        for s, t in prefills:
+            want_runs.append([len(want_slot), t.shape[0], lengths[s]])
+            for j in range(t.shape[0]):
+                want_slot.append(s)
+                want_off.append(j)
+            want_need = max(want_need, lengths[s] + t.shape[0])
+        assert row_slot.tolist() == want_slot and row_off.tolist() == want_off
+        assert runs.dtype == np.int32 and runs.tolist() == want_runs and need == want_need
+    host = SimpleNamespace(lengths_cpu=[995] + [0] * 8, max_slots=8, capacity=1000)
+    with pytest.raises(ValueError):
+        StaticBackbone._rows_of(host, [1], [(0, torch.empty(6, 1))])
