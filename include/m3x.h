@@ -359,13 +359,14 @@ int m3x_ring_attn(const void* qkv, long ld_qkv, void* kring, void* vring, int64_
                   const int64_t* slots, const float* inv_freq, float rope_scale, void* out, long ld_out, int B, int T,
                   int H, int head_dim, int ring, int window, int dtype, void* stream);
 
-/* tokens[slot] += T for each seat whose slot is not `dummy`, then tokens[dummy] = 0.
+/* tokens[slot] += T for each seat whose slot is not `dummy` (those slots distinct, one seat each), then
+ * tokens[dummy] = 0.
  * Replaces `self.tokens.index_copy_(0, slots, start + count); self.tokens[self.dummy].zero_()` (:183-184). */
 int m3x_advance_tokens(int64_t* tokens, const int64_t* slots, int B, int T, int dummy, void* stream);
 
 /* Last conv (C -> 1 channel, kernel k, causal; C % 8 == 0, k * C <= 4096) to fp32 PCM [B, T] with fp32 weights
- * w[j*C + c] and the slot's
- * k - 1 stored input frames. Replaces the final MimiConv1d of `_forward` (serve/fast_codec.py:189-191). */
+ * w[j*C + c] and the slot's k - 1 stored input frames; chunk (>= k - 1) is the samples per workgroup of the
+ * general path (C <= 64 and k <= 9 take a fixed 128). Replaces the final MimiConv1d of `_forward` (serve/fast_codec.py:189-191). */
 int m3x_final_conv(const void* x, long ld_x, void* state, long ld_state, const int64_t* slots, const float* w,
                    float bias, float* pcm, long ld_pcm, int B, int T, int C, int k, int chunk, int dtype,
                    void* stream);

@@ -565,12 +565,15 @@ __global__ __launch_bounds__(256) void ring_attn_kernel(const Elt<DT>* __restric
   }
 }
 
-// Seats' token counters advance by T after the transformer (:183-184); the dummy slot's counter returns to 0.
+// Seats' token counters advance by T after the transformer (:183-184); the dummy slot's counter returns to 0. One
+// thread per seat (the seats' slots other than the dummy are distinct, so no two threads touch one counter).
 __global__ void advance_tokens_kernel(int64_t* tokens, const int64_t* __restrict__ slots, int B, int T, int dummy) {
-  if (threadIdx.x) return;
-  for (int b = 0; b < B; ++b)
-    if (slots[b] != dummy) tokens[slots[b]] += T;
-  tokens[dummy] = 0;
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b < B) {
+    const int64_t s = slots[b];
+    if (s != dummy) tokens[s] += T;
+  }
+  if (b == 0) tokens[dummy] = 0;
 }
 
 // ---------------------------------------------------------------------------------------------------------
@@ -606,6 +609,75 @@ __global__ __launch_bounds__(CODEC_THREADS) void final_conv_kernel(const Elt<DT>
         const V8<DT> v = ldv<DT>(row + 8 * c8);
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc += wj[8 * c8 + e] * E<DT>::to_f(v.v[e]);
+      }
+    }
+    pcm[(long)b * ld_pcm + t] = acc + bias;
+  }
+  if (!pad || blockIdx.y) return;
+  V8<DT> keep[CODEC_KEEP / 8];
+  int n = 0;
+  for (int e = threadIdx.x; e < pad * cv; e += CODEC_THREADS)
+    keep[n++] = joined8<DT>(st, x, ld_x, row0, pad, T + e / cv, 8 * (e % cv), C, 0);
+  __syncthreads();
+  n = 0;
+  for (int e = threadIdx.x; e < pad * cv; e += CODEC_THREADS) stv<DT>(st + 8 * e, keep[n++]);
+}
+
+// final_conv_kernel for the codec's shape (C <= 64 channels, k <= 9 taps), FCS_CHUNK samples per workgroup: the
+// chunk's input rows and the k - 1 before it (the slot's stored frames for the first chunk) are staged in LDS as
+// fp32 with every 16-byte load issued before the first store (clamped indices, no branch around the loads); then
+// one thread per sample sums taps j and channels c in the same order as final_conv_kernel, so the two give the same
+// bits. One thread per sample reading its rows from memory made every load touch 64 cache lines (180 us for 224
+// seats of one frame).
+constexpr int FCS_CHUNK = 128, FCS_C = 64, FCS_K = 9, FCS_LD = FCS_C + 4;
+template <int DT>
+__global__ __launch_bounds__(CODEC_THREADS) void final_conv_staged_kernel(const Elt<DT>* __restrict__ x, long ld_x,
+                                                                          Elt<DT>* state, long ld_state,
+                                                                          const int64_t* __restrict__ slots,
+                                                                          const float* __restrict__ w, float bias,
+                                                                          float* __restrict__ pcm, long ld_pcm, int T,
+                                                                          int C, int k) {
+  __shared__ __align__(16) float ws[FCS_K * FCS_C];
+  __shared__ __align__(16) float xs[(FCS_CHUNK + FCS_K - 1) * FCS_LD];
+  const int b = blockIdx.x;
+  const int t0 = blockIdx.y * FCS_CHUNK, t1 = min(T, t0 + FCS_CHUNK);
+  const int pad = k - 1;
+  const long row0 = (long)b * T;
+  Elt<DT>* st = pad ? state + slots[b] * ld_state : nullptr;
+  for (int i = threadIdx.x; i < k * C; i += CODEC_THREADS) ws[i] = w[i];
+  const int cv = C / 8;
+  const int nvec = (t1 - t0 + pad) * cv;  // staged row r is the joined row t0 + r
+  constexpr int VPT = ((FCS_CHUNK + FCS_K - 1) * (FCS_C / 8) + CODEC_THREADS - 1) / CODEC_THREADS;
+  V8<DT> v[VPT];
+#pragma unroll
+  for (int p = 0; p < VPT; ++p) {
+    const int e = min((int)threadIdx.x + CODEC_THREADS * p, nvec - 1);
+    const int r = e / cv, q = e - (e / cv) * cv;
+    const int i = t0 + r;
+    v[p] = ldv<DT>(i < pad ? st + (long)i * C + 8 * q : x + (row0 + i - pad) * ld_x + 8 * q);
+  }
+#pragma unroll
+  for (int p = 0; p < VPT; ++p) {
+    const int e = min((int)threadIdx.x + CODEC_THREADS * p, nvec - 1);  // repeats store the same values
+    const int r = e / cv, q = e - (e / cv) * cv;
+    float* d = xs + r * FCS_LD + 8 * q;
+    *reinterpret_cast<float4*>(d) =
+        make_float4(E<DT>::to_f(v[p].v[0]), E<DT>::to_f(v[p].v[1]), E<DT>::to_f(v[p].v[2]), E<DT>::to_f(v[p].v[3]));
+    *reinterpret_cast<float4*>(d + 4) =
+        make_float4(E<DT>::to_f(v[p].v[4]), E<DT>::to_f(v[p].v[5]), E<DT>::to_f(v[p].v[6]), E<DT>::to_f(v[p].v[7]));
+  }
+  __syncthreads();
+  for (int t = t0 + threadIdx.x; t < t1; t += CODEC_THREADS) {
+    float acc = 0.f;
+    for (int j = 0; j < k; ++j) {
+      const float* row = xs + (t - t0 + j) * FCS_LD;
+      const float* wj = ws + j * C;
+      for (int c = 0; c < C; c += 4) {
+        const float4 xv = *reinterpret_cast<const float4*>(row + c);
+        acc += wj[c] * xv.x;
+        acc += wj[c + 1] * xv.y;
+        acc += wj[c + 2] * xv.z;
+        acc += wj[c + 3] * xv.w;
       }
     }
     pcm[(long)b * ld_pcm + t] = acc + bias;
@@ -736,7 +808,8 @@ M3X_API int m3x_ring_attn(const void* qkv, long ld_qkv, void* kring, void* vring
 M3X_API int m3x_advance_tokens(int64_t* tokens, const int64_t* slots, int B, int T, int dummy, void* stream) {
   if (B < 0 || T < 0 || dummy < 0) return M3X_EINVAL;
   if (!tokens || (B && !slots)) return M3X_ENULL;
-  hipLaunchKernelGGL(advance_tokens_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, tokens, slots, B, T, dummy);
+  hipLaunchKernelGGL(advance_tokens_kernel, dim3(m3x_ceil_div(std::max(B, 1), 256)), dim3(256), 0, (hipStream_t)stream,
+                     tokens, slots, B, T, dummy);
   M3X_CHECK_LAUNCH();
   return M3X_OK;
 }
@@ -752,6 +825,11 @@ M3X_API int m3x_final_conv(const void* x, long ld_x, void* state, long ld_state,
   if ((long)k * C > FC_W) return M3X_EINVAL;
   if (B == 0) return M3X_OK;
   if (!x || !slots || !w || !pcm || (k > 1 && !state)) return M3X_ENULL;
+  if (C <= FCS_C && k <= FCS_K) {  // the codec's shape: rows staged in LDS (chunk is the general path's)
+    CODEC_LAUNCH(final_conv_staged_kernel, dim3(B, m3x_ceil_div(T, FCS_CHUNK)), dim3(CODEC_THREADS), (const ET*)x,
+                 ld_x, (ET*)state, ld_state, slots, w, bias, pcm, ld_pcm, T, C, k);
+    return M3X_OK;
+  }
   CODEC_LAUNCH(final_conv_kernel, dim3(B, m3x_ceil_div(T, chunk)), dim3(CODEC_THREADS), (const ET*)x, ld_x,
                (ET*)state, ld_state, slots, w, bias, pcm, ld_pcm, T, C, k, chunk);
   return M3X_OK;
