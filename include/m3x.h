@@ -60,8 +60,9 @@ size_t m3x_decode_attn_workspace(int rows, int kv_heads, int max_ctx, int chunk)
  * · V[...]; heads/kv_heads in {1, 2}; head_dim 128; chunk = keys per split (multiple of 128); max_ctx >= pos+1
  * for every row; cap % 32 == 0.
  * items (nullable) lists the step's work for one launch of 2 workgroups per CU: an item is split s (keys
- * [s * chunk, (s + 1) * chunk)) of m rows of one slot (1 <= m <= 16 / G: a decode row, or up to 16 / G rows of an
- * inline prefill), code 2048 * first_row + 32 * s + m; every split of every row in exactly one item; rows < 2^20.
+ * [s * chunk, (s + 1) * chunk)) of m rows of one slot (1 <= m <= 16: a decode row, or up to 16 rows of an inline
+ * prefill, one or two blocks of 16 / G rows), code 2048 * first_row + 32 * s + m; every split of every row in exactly
+ * one item; rows < 2^20.
  * The items are dealt into bins = m3x_decode_attn_item_bins(...) bins, and items = [bins, start[0], ...,
  * start[bins], codes of bin 0, codes of bin 1, ...] (int32). An item's rows share one pass over the slot's keys,
  * each row causal up to its own pos; every row gets the same bits as without items. With items, out must be

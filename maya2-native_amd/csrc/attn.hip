@@ -233,40 +233,57 @@ __global__ __launch_bounds__(256, M3X_ATTN_MINB) void decode_attn_kernel(
   }
 }
 
-// One item of attn_block_kernel: rows row .. row + nb - 1, kv head kh, keys [kstart, kend) of split `split`.
-template <int G>
+// One item of attn_block_kernel: rows row .. row + nb - 1, kv head kh, keys [kstart, kend) of split `split`. The
+// rows are NB blocks of QB = 16 / G rows (NB = 2: a second block's 16 query vectors share every K/V tile the waves
+// load, so a prefill makes one pass over its keys per 2 QB rows); each query vector sees the same tiles on the same
+// wave and the same merge whatever NB, so its bits do not depend on the block it sits in.
+template <int G, int NB>
 __device__ __forceinline__ void attn_block_item(
     const uint16_t* __restrict__ q, long sq_b, long sq_h, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, long sk_s, long sk_h, long sk_t, uint16_t* __restrict__ out, long so_b,
     long so_h, const int64_t* __restrict__ slots, const int32_t* __restrict__ pos, float scale_log2, int chunk,
     float* __restrict__ part, int max_splits, int cap, int row, int nb, int kh, int KV, int split, int kstart,
     int kend, unsigned char* lds) {
+  constexpr int QB = 16 / G;
   constexpr int KT_LD = 136;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int li = lane & 15;  // query vector (column) of S^T: block row li / G, head li % G
   const int lg = lane >> 4;
   const int jq = li / G;
-  const bool qlive = jq < nb;
-  const int pq = qlive ? min(pos[row + jq], cap - 1) : -1;  // the vector's own position: it sees keys <= pq
+  bool qlive[NB];
+  int pq[NB];  // the vector's own position: it sees keys <= pq
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    qlive[b] = b * QB + jq < nb;
+    pq[b] = qlive[b] ? min(pos[row + b * QB + jq], cap - 1) : -1;
+  }
 
   const long slot = slots[row];
   const uint16_t* kbase = kc + slot * sk_s + (long)kh * sk_h;
   const uint16_t* vbase = vc + slot * sk_s + (long)kh * sk_h;
-  u16x8 qop[4];
+  u16x8 qop[NB][4];
 #pragma unroll
-  for (int kk = 0; kk < 4; ++kk) {
-    if (qlive) {
-      qop[kk] = ld16(q + (long)(row + jq) * sq_b + (long)(kh * G + li % G) * sq_h + 32 * kk + 8 * lg);
-    } else {
+  for (int b = 0; b < NB; ++b)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) qop[kk].v[e] = 0;
+    for (int kk = 0; kk < 4; ++kk) {
+      if (qlive[b]) {
+        qop[b][kk] =
+            ld16(q + (long)(row + b * QB + jq) * sq_b + (long)(kh * G + li % G) * sq_h + 32 * kk + 8 * lg);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qop[b][kk].v[e] = 0;
+      }
     }
-  }
-  float m_run = -INFINITY, l_run = 0.f;  // of vector li, equal across the 4 lanes of one li
-  f32x4_t acc[8];
+  float m_run[NB], l_run[NB];  // of vector li, equal across the 4 lanes of one li
+  f32x4_t acc[NB][8];
 #pragma unroll
-  for (int T = 0; T < 8; ++T) acc[T] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int b = 0; b < NB; ++b) {
+    m_run[b] = -INFINITY;
+    l_run[b] = 0.f;
+#pragma unroll
+    for (int T = 0; T < 8; ++T) acc[b][T] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
 
   uint16_t* kt = reinterpret_cast<uint16_t*>(lds) + wave * 32 * KT_LD;
   for (int k0 = kstart + 32 * wave; k0 < kend; k0 += 128) {
@@ -278,57 +295,77 @@ __device__ __forceinline__ void attn_block_item(
     for (int e = 0; e < 8; ++e) vld[e] = kv_load(vbase + (long)(k0 + 16 * (e >> 2) + 4 * lg + (e & 3)) * sk_t + 8 * li);
 #pragma unroll
     for (int e = 0; e < 8; ++e) st16(kt + (16 * (e >> 2) + 4 * lg + (e & 3)) * KT_LD + 8 * li, kld[e]);
-    u16x8 kop[2][4];
+    f32x4_t sb[NB][2];
+    if constexpr (NB == 1) {  // the whole tile's K operand read at once
+      u16x8 kop[2][4];
 #pragma unroll
-    for (int g2 = 0; g2 < 2; ++g2)
+      for (int g2 = 0; g2 < 2; ++g2)
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk)
-        kop[g2][kk] = *reinterpret_cast<const u16x8*>(kt + (16 * g2 + li) * KT_LD + 32 * kk + 8 * lg);
-    f32x4_t s[2];
+        for (int kk = 0; kk < 4; ++kk)
+          kop[g2][kk] = *reinterpret_cast<const u16x8*>(kt + (16 * g2 + li) * KT_LD + 32 * kk + 8 * lg);
 #pragma unroll
-    for (int g2 = 0; g2 < 2; ++g2) {
-      s[g2] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int g2 = 0; g2 < 2; ++g2) {
+        sb[0][g2] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) s[g2] = mfma16x16x32<M3X_BF16>(kop[g2][kk], qop[kk], s[g2]);
-    }
-    // mask: keys past the split or the block, and keys after the vector's own position (causal); dead vectors
-    // see nothing
-    const int klim = min(kend - 1, pq);
-    float sv[8];
-#pragma unroll
-    for (int g2 = 0; g2 < 2; ++g2)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = k0 + 16 * g2 + 4 * lg + r;
-        sv[4 * g2 + r] = (qlive && key <= klim) ? s[g2][r] * scale_log2 : -INFINITY;
+        for (int kk = 0; kk < 4; ++kk) sb[0][g2] = mfma16x16x32<M3X_BF16>(kop[g2][kk], qop[0][kk], sb[0][g2]);
       }
-    float tmax = sv[0];
+    } else {
 #pragma unroll
-    for (int e = 1; e < 8; ++e) tmax = fmaxf(tmax, sv[e]);
-    tmax = xor32_max(xor16_max(tmax));
-    const float m_new = fmaxf(m_run, tmax);
-    // a vector with no visible key yet keeps m = -inf: its weights are 0 and its rescale 1
-    const float alpha = m_new == -INFINITY ? 1.f : exp2f(m_run - m_new);
-    float p[8], psum = 0.f;
+      for (int g2 = 0; g2 < 2; ++g2) {  // one 16-key half of the tile at a time, shared by the blocks
+        u16x8 kop[4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      p[e] = sv[e] == -INFINITY ? 0.f : exp2f(sv[e] - m_new);
-      psum += p[e];
+        for (int kk = 0; kk < 4; ++kk)
+          kop[kk] = *reinterpret_cast<const u16x8*>(kt + (16 * g2 + li) * KT_LD + 32 * kk + 8 * lg);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          sb[b][g2] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk) sb[b][g2] = mfma16x16x32<M3X_BF16>(kop[kk], qop[b][kk], sb[b][g2]);
+        }
+      }
     }
-    psum = xor32_sum(xor16_sum(psum));
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-    // O rows are vectors 4 * lg + r: their rescale comes from lane 4 * lg + r
-    float al[4];
+    u16x8 pop[NB];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) al[r] = __shfl(alpha, 4 * lg + r, 64);
+    for (int b = 0; b < NB; ++b) {
+      const f32x4_t* s = sb[b];
+      // mask: keys past the split or the block, and keys after the vector's own position (causal); dead vectors
+      // see nothing
+      const int klim = min(kend - 1, pq[b]);
+      float sv[8];
 #pragma unroll
-    for (int T = 0; T < 8; ++T)
+      for (int g2 = 0; g2 < 2; ++g2)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[T][r] *= al[r];
-    u16x8 pop;
+        for (int r = 0; r < 4; ++r) {
+          const int key = k0 + 16 * g2 + 4 * lg + r;
+          sv[4 * g2 + r] = (qlive[b] && key <= klim) ? s[g2][r] * scale_log2 : -INFINITY;
+        }
+      float tmax = sv[0];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) pop.v[e] = f2bf(p[e]);
+      for (int e = 1; e < 8; ++e) tmax = fmaxf(tmax, sv[e]);
+      tmax = xor32_max(xor16_max(tmax));
+      const float m_new = fmaxf(m_run[b], tmax);
+      // a vector with no visible key yet keeps m = -inf: its weights are 0 and its rescale 1
+      const float alpha = m_new == -INFINITY ? 1.f : exp2f(m_run[b] - m_new);
+      float p[8], psum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        p[e] = sv[e] == -INFINITY ? 0.f : exp2f(sv[e] - m_new);
+        psum += p[e];
+      }
+      psum = xor32_sum(xor16_sum(psum));
+      l_run[b] = l_run[b] * alpha + psum;
+      m_run[b] = m_new;
+      // O rows are vectors 4 * lg + r: their rescale comes from lane 4 * lg + r
+      float al[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) al[r] = __shfl(alpha, 4 * lg + r, 64);
+#pragma unroll
+      for (int T = 0; T < 8; ++T)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[b][T][r] *= al[r];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pop[b].v[e] = f2bf(p[e]);
+    }
     if (k0 + 32 > kend) {  // zero V rows past the block's context in the tail tile
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -344,69 +381,77 @@ __device__ __forceinline__ void attn_block_item(
       u16x8 vop;
 #pragma unroll
       for (int e = 0; e < 8; ++e) vop.v[e] = vld[e].v[T];
-      acc[T] = mfma16x16x32<M3X_BF16>(pop, vop, acc[T]);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) acc[b][T] = mfma16x16x32<M3X_BF16>(pop[b], vop, acc[b][T]);
     }
   }
 
   // ---- merge the 4 waves (the K tiles are dead after the barrier)
   __syncthreads();
-  float* lo = reinterpret_cast<float*>(lds);  // [4][16][AD]
-  float* lm = lo + 4 * 16 * AD;               // [4][16]
-  float* ll = lm + 4 * 16;                    // [4][16]
+  float* lo = reinterpret_cast<float*>(lds);  // [4][16 NB][AD]
+  float* lm = lo + 4 * 16 * NB * AD;          // [4][16 NB]
+  float* ll = lm + 4 * 16 * NB;               // [4][16 NB]
 #pragma unroll
-  for (int T = 0; T < 8; ++T)
+  for (int b = 0; b < NB; ++b) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) lo[(wave * 16 + 4 * lg + r) * AD + 8 * li + T] = acc[T][r];
-  if (lg == 0) {
-    lm[wave * 16 + li] = m_run;
-    ll[wave * 16 + li] = l_run;
+    for (int T = 0; T < 8; ++T)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) lo[((wave * NB + b) * 16 + 4 * lg + r) * AD + 8 * li + T] = acc[b][T][r];
+    if (lg == 0) {
+      lm[(wave * NB + b) * 16 + li] = m_run[b];
+      ll[(wave * NB + b) * 16 + li] = l_run[b];
+    }
   }
   __syncthreads();
-  // thread t: vector t / 16, dims 8 * (t % 16) .. + 7
-  const int vq = threadIdx.x >> 4;
+  // thread t: vector t / 16 of each block, dims 8 * (t % 16) .. + 7
+  const int c = threadIdx.x >> 4;
   const int d0 = 8 * (threadIdx.x & 15);
-  const int j = vq / G, h = vq % G;
-  if (j >= nb) return;
-  const int pj = min(pos[row + j], cap - 1);
-  const int nsplit = min((pj + chunk) / chunk, max_splits);
-  if (split >= nsplit) return;  // this row has no keys in this split (the caller's barrier follows)
-  float M = lm[vq];
+  const int h = c % G;
 #pragma unroll
-  for (int w = 1; w < 4; ++w) M = fmaxf(M, lm[w * 16 + vq]);
-  float f[4], L = 0.f;
+  for (int b = 0; b < NB; ++b) {
+    const int j = b * QB + c / G;
+    if (j >= nb) continue;
+    const int pj = min(pos[row + j], cap - 1);
+    const int nsplit = min((pj + chunk) / chunk, max_splits);
+    if (split >= nsplit) continue;  // this row has no keys in this split (the caller's barrier follows)
+    float M = lm[b * 16 + c];
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    f[w] = exp2f(lm[w * 16 + vq] - M);  // 0 for a wave that saw no visible key (m = -inf)
-    L += ll[w * 16 + vq] * f[w];
-  }
-  float O[8];
+    for (int w = 1; w < 4; ++w) M = fmaxf(M, lm[(w * NB + b) * 16 + c]);
+    float f[4], L = 0.f;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    O[e] = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) O[e] += lo[(w * 16 + vq) * AD + d0 + e] * f[w];
-  }
-  if (nsplit == 1) {
-    u16x8 ov;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) ov.v[e] = f2bf(O[e] / L);
-    st16(out + (long)(row + j) * so_b + (long)(kh * G + h) * so_h + d0, ov);
-  } else {
-    float* pp = part + (((long)(row + j) * KV + kh) * max_splits + split) * PART_STRIDE;
-    if (d0 == 0) {
-      pp[h] = M;
-      pp[2 + h] = L;
+    for (int w = 0; w < 4; ++w) {
+      f[w] = exp2f(lm[(w * NB + b) * 16 + c] - M);  // 0 for a wave that saw no visible key (m = -inf)
+      L += ll[(w * NB + b) * 16 + c] * f[w];
     }
+    float O[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) pp[8 + h * AD + d0 + e] = O[e];
+    for (int e = 0; e < 8; ++e) {
+      O[e] = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) O[e] += lo[((w * NB + b) * 16 + c) * AD + d0 + e] * f[w];
+    }
+    if (nsplit == 1) {
+      u16x8 ov;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ov.v[e] = f2bf(O[e] / L);
+      st16(out + (long)(row + j) * so_b + (long)(kh * G + h) * so_h + d0, ov);
+    } else {
+      float* pp = part + (((long)(row + j) * KV + kh) * max_splits + split) * PART_STRIDE;
+      if (d0 == 0) {
+        pp[h] = M;
+        pp[2 + h] = L;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pp[8 + h * AD + d0 + e] = O[e];
+    }
   }
 }
 
 // Steps that hold inline prefill rows (serve/fast_backbone.py:326-359). The rows of one prefill are one slot at
-// consecutive positions, and the caller groups them into items of up to QB = 16 / G rows (a decode row is an item
-// of one row): items[0] = the item count n, items[1 + i] = 32 * (first row) + (rows of item i). One workgroup
-// takes an item: its 16 query vectors (row j, head h), column j * G + h, fill all 16 columns of the MFMA query
-// operand, so a prefill costs one pass over its slot's keys per QB rows instead of one per row. Same tile
+// consecutive positions, and the caller groups them into items of up to IB = min(16, 2 QB) rows, QB = 16 / G (a
+// decode row is an item of one row). One workgroup takes an item: each block of QB rows gives 16 query vectors
+// (row j, head h), column j * G + h, that fill all 16 columns of the MFMA query operand, and an item's one or two
+// blocks share each K/V tile, so a prefill costs one pass over its slot's keys per IB rows. Same tile
 // pipeline as decode_attn_kernel (K through the wave-private LDS tile, V in registers, S^T = K . Q^T,
 // O += P . V) and the same arithmetic per query vector, so every row gets the bits decode_attn_kernel would give
 // it; the differences are the causal mask (vector j sees keys <= pos[row + j]) and the per-vector rescale (O rows
@@ -425,6 +470,7 @@ __global__ __launch_bounds__(256, 2) void attn_block_kernel(
     long so_h, const int64_t* __restrict__ slots, const int32_t* __restrict__ pos, float scale_log2, int chunk,
     float* __restrict__ part, int max_splits, int cap, const int32_t* __restrict__ items, int rows) {
   constexpr int QB = 16 / G;
+  constexpr int NB = 2 * QB <= 16 ? 2 : 1;  // blocks per item
   const int kh = blockIdx.y;
   const int KV = gridDim.y;
   const int bins = items[0];
@@ -433,22 +479,27 @@ __global__ __launch_bounds__(256, 2) void attn_block_kernel(
   const int32_t* codes = items + 2 + bins;
   // LDS: the wave-private K tiles during the key loop, then the wave merge (after a barrier)
   constexpr int KTILE_BYTES = 4 * 32 * 136 * 2;
-  constexpr int MERGE_BYTES = (4 * 16 * AD + 2 * 4 * 16) * 4;
+  constexpr int MERGE_BYTES = (4 * 16 * NB * AD + 2 * 4 * 16 * NB) * 4;
   __shared__ __align__(16) unsigned char lds[KTILE_BYTES > MERGE_BYTES ? KTILE_BYTES : MERGE_BYTES];
   for (int it = i0; it < i1; ++it) {
     const int code = codes[it];
     const int row = code >> 11;
     const int split = (code >> 5) & 63;
     if (row < 0 || row >= rows || split >= max_splits) continue;
-    const int nb = min(min(code & 31, QB), rows - row);
+    const int nb = min(min(code & 31, NB * QB), rows - row);
     if (nb <= 0) continue;
     int plast = 0;
-    for (int j = 0; j < nb; ++j) plast = max(plast, min(pos[row + j], cap - 1));
+#pragma unroll
+    for (int j = 0; j < NB * QB; ++j) plast = max(plast, min(pos[row + min(j, nb - 1)], cap - 1));
     const int kstart = split * chunk;
     if (kstart > plast) continue;  // past the item's context (uniform per workgroup)
     const int kend = min(kstart + chunk, plast + 1);
-    attn_block_item<G>(q, sq_b, sq_h, kc, vc, sk_s, sk_h, sk_t, out, so_b, so_h, slots, pos, scale_log2, chunk, part,
-                       max_splits, cap, row, nb, kh, KV, split, kstart, kend, lds);
+    if (NB == 2 && nb > QB)
+      attn_block_item<G, NB>(q, sq_b, sq_h, kc, vc, sk_s, sk_h, sk_t, out, so_b, so_h, slots, pos, scale_log2, chunk,
+                             part, max_splits, cap, row, nb, kh, KV, split, kstart, kend, lds);
+    else
+      attn_block_item<G, 1>(q, sq_b, sq_h, kc, vc, sk_s, sk_h, sk_t, out, so_b, so_h, slots, pos, scale_log2, chunk,
+                            part, max_splits, cap, row, nb, kh, KV, split, kstart, kend, lds);
     __syncthreads();  // the next item's K tiles reuse the merge area
   }
 }
@@ -464,7 +515,8 @@ M3X_API int m3x_decode_attn_item_bins(int rows, int kv_heads, int max_ctx, int c
 }
 
 // Host side: the work items of an item launch for rows laid out as runs (first row, rows, first position): each run
-// cut into blocks of up to 16 / (heads / kv_heads) rows, each block's keys into splits of `chunk`; an item is one
+// cut into blocks of up to min(16, 2 * (16 / (heads / kv_heads))) rows (the rows one workgroup attends in one pass
+// over their keys), each block's keys into splits of `chunk`; an item is one
 // split of one block, cost = its keys + 64. Items are dealt into `bins` bins longest processing time first (stable
 // by item index on equal costs), each to the least loaded bin (the lowest index on equal loads). Writes
 // [bins, start[0..bins], codes bin by bin] with code = 2048 * first_row + 32 * split + rows and returns the count.
@@ -472,7 +524,7 @@ M3X_API long m3x_decode_attn_items(const int32_t* runs, int nruns, int heads, in
                                    int32_t* out, long out_cap) {
   if (!runs || !out) return M3X_ENULL;
   if (nruns < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads || bins <= 0 || chunk <= 0) return M3X_EINVAL;
-  const int qb = std::max(1, 16 / (heads / kv_heads));
+  const int qb = std::min(16, 2 * std::max(1, 16 / (heads / kv_heads)));
   std::vector<long> cost;
   std::vector<int32_t> code;
   cost.reserve(nruns * 2);

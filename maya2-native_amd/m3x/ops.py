@@ -152,7 +152,7 @@ def decode_attn(q, k_cache, v_cache, out, slots, pos, scale, max_ctx, chunk, wor
                 items=None):
     """q, out: [rows, heads, D] (any row/head strides, contiguous D); caches [slots, kv_heads, cap, D].
     items (int32, optional): the step's work items (attn_items with attn_item_bins bins); the rows of an inline
-    prefill then share one pass over their slot's keys per 16 // (heads // kv_heads) rows."""
+    prefill then share one pass over their slot's keys per min(16, 2 * (16 // (heads // kv_heads))) rows."""
     _dev(q, k_cache, v_cache, out, slots, pos, workspace, items)
     _index(slots=slots, pos=pos)
     rows = q.shape[0]
@@ -175,7 +175,7 @@ def attn_item_bins(rows, kv_heads, max_ctx, chunk) -> int:
 def attn_items(runs, heads, kv_heads, bins, chunk):
     """Work items of decode_attn for rows laid out as runs: (first row, rows, first position) per run, a decode
     row being a run of one row and an inline prefill of T tokens a run of T rows at consecutive positions of one
-    slot. Each run is cut into blocks of up to 16 // (heads // kv_heads) rows and each block's keys into splits of
+    slot. Each run is cut into blocks of up to min(16, 2 * (16 // (heads // kv_heads))) rows and each block's keys into splits of
     `chunk` keys; an item is one split of one block. The items are dealt into `bins` bins (attn_item_bins) longest
     processing time first: each goes to the least loaded bin, its cost its keys plus a fixed 64. Returns int32
     [bins, start[0..bins], codes bin by bin], code = 2048 * first_row + 32 * split + rows. Built on the host by the

@@ -242,7 +242,7 @@ def test_decode_attn(gpu, heads, kv, chunk, CAP):
 
 @pytest.mark.parametrize("heads,kv,chunk", [(16, 8, 2048), (16, 8, 128), (8, 8, 256), (16, 8, 1024)])
 def test_prefill_items_match_decode_rows(gpu, heads, kv, chunk):
-    """Inline prefill rows attended as items (16 query vectors per pass over their slot's keys, one persistent
+    """Inline prefill rows attended as items (up to 32 query vectors per pass over their slot's keys, one persistent
     grid walking the items) give exactly the bits of attending each row alone, and match the fp32 reference.
     Runs cover full items, a partial last item, an item of one row, lone rows and runs crossing split
     boundaries; the same rows as one-row items, and with the items listed in another order, give the same bits."""
@@ -262,7 +262,7 @@ def test_prefill_items_match_decode_rows(gpu, heads, kv, chunk):
         K[s, :, p0 + n:] = float("nan")  # past the run's last position nothing may leak
         V[s, :, p0 + n:] = float("nan")
     R = len(slots)
-    qb = 16 // (heads // kv)
+    qb = min(16, 2 * (16 // (heads // kv)))  # rows per item: two blocks of 16 query vectors where they fit 16 rows
     bins = ops.attn_item_bins(R, kv, CAP, chunk)
     items = ops.attn_items(spans, heads, kv, bins, chunk).tolist()
     blocks = [(r0 + s, min(qb, n - s), p0 + s + min(qb, n - s)) for r0, n, p0 in spans for s in range(0, n, qb)]

@@ -23,14 +23,14 @@ def test_attn_chunk_plan():
 
 def test_attn_items_cover_every_row_once():
     """The work list of a mixed step: every split of every row in exactly one item of one slot's run, items of at
-    most 16 / G rows that start at a run's start or a multiple of 16 / G into it and cover one chunk of the block's
+    most min(16, 2 (16 / G)) rows that start at a run's start or a multiple of that into it and cover one chunk of the block's
     keys, bins listed back to back, and the longest processing time deal (no bin exceeds the lightest by more than
     its largest item)."""
     from m3x import ops
     runs = [(0, 1, 3000), (1, 1, 10), (2, 20, 0), (22, 9, 700), (31, 1, 4000), (32, 256, 100)]
     rows = 288
     for heads, kv, bins, chunk in [(16, 8, 96, 4096), (8, 8, 7, 1024), (16, 8, 1, 512), (16, 8, 40, 128)]:
-        qb = 16 // (heads // kv)
+        qb = min(16, 2 * (16 // (heads // kv)))
         it = ops.attn_items(runs, heads, kv, bins, chunk).tolist()
         assert it[0] == bins and it[1] == 0
         start = it[1:2 + bins]
@@ -58,10 +58,10 @@ def test_attn_items_cover_every_row_once():
 
 
 def _items_restated(runs, heads, kv_heads, bins, chunk):
-    """The item list restated: blocks of 16 // G rows, splits of `chunk` keys, cost keys + 64, a stable longest-first
-    order and each item to the least loaded bin (lowest index on ties)."""
+    """The item list restated: blocks of min(16, 2 (16 // G)) rows, splits of `chunk` keys, cost keys + 64, a stable
+    longest-first order and each item to the least loaded bin (lowest index on ties)."""
     import heapq
-    qb = 16 // (heads // kv_heads)
+    qb = min(16, 2 * (16 // (heads // kv_heads)))
     costs, codes = [], []
     for r0, n, p0 in runs:
         for s in range(0, n, qb):
