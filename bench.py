@@ -632,8 +632,8 @@ def main():
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures one GPU: the frame step shards by seats with no collectives, and this build runs "
-              "on a single MI355X (run with --gpus 1).", file=sys.stderr)
+        print("bench.py measures one GPU: the frame step shards by seats with no collectives, and the benchmark "
+              "runs on a single MI355X (run with --gpus 1).", file=sys.stderr)
         sys.exit(2)
 
     import torch
