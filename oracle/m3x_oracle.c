@@ -1,7 +1,7 @@
 /* CPU oracle for the bit-exact parts of the m3x frame step.
  *
  * TEST INFRASTRUCTURE ONLY: tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg may load this as
- * the checker. The product path (maya2-native_amd/m3x) never links or calls it.
+ * the reference they compare with. The product path (maya2-native_amd/m3x) never links or calls it.
  *
  * Each function restates the reference's arithmetic with the rounding points and the summation order the HIP
  * kernels commit to, written the plain way (full sorts, sequential loops), so that agreement is a check of the

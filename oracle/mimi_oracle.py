@@ -1,5 +1,5 @@
 """fp32 CPU restatement of the one-frame streaming Mimi decode (test infrastructure only: tests/ and bench.py's CPU
-leg use it as the checker; the product package never imports it).
+leg use it as the reference they compare with; the product package never imports it).
 
 Follows serve/fast_codec.py StaticMimi._forward (:186-192) and the layers it walks:
   quantizer   sum of the semantic codebook row and of the 31 acoustic rows, each group through its 1x1 output
