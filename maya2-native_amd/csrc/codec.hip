@@ -683,13 +683,12 @@ __global__ __launch_bounds__(CODEC_THREADS) void final_conv_staged_kernel(const 
     pcm[(long)b * ld_pcm + t] = acc + bias;
   }
   if (!pad || blockIdx.y) return;
-  V8<DT> keep[CODEC_KEEP / 8];
-  int n = 0;
-  for (int e = threadIdx.x; e < pad * cv; e += CODEC_THREADS)
-    keep[n++] = joined8<DT>(st, x, ld_x, row0, pad, T + e / cv, 8 * (e % cv), C, 0);
+  // the new history: pad * C / 8 <= 64 vectors, at most one per thread (a register, not a private array)
+  const int e = threadIdx.x;
+  V8<DT> keep = zero_v8<DT>();
+  if (e < pad * cv) keep = joined8<DT>(st, x, ld_x, row0, pad, T + e / cv, 8 * (e % cv), C, 0);
   __syncthreads();
-  n = 0;
-  for (int e = threadIdx.x; e < pad * cv; e += CODEC_THREADS) stv<DT>(st + 8 * e, keep[n++]);
+  if (e < pad * cv) stv<DT>(st + 8 * e, keep);
 }
 
 // ---------------------------------------------------------------------------------------------------------
