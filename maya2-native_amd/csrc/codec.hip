@@ -96,13 +96,18 @@ __global__ __launch_bounds__(CODEC_THREADS) void conv_gather_kernel(const Elt<DT
     stv<DT>(cols + (row0 + t) * ld_cols + (long)j * C + c, joined8<DT>(st, x, ld_x, row0, pad, t + j * dil, c, C, use_elu));
   }
   if (!pad || blockIdx.y) return;
-  V8<DT> keep[CODEC_KEEP / 8];
-  int n = 0;
-  for (int e = threadIdx.x; e < pad * cv; e += CODEC_THREADS)
-    keep[n++] = joined8<DT>(st, x, ld_x, row0, pad, T + e / cv, 8 * (e % cv), C, use_elu);
+  V8<DT> keep[CODEC_KEEP / 8];  // constant indices: registers, not a private or LDS array
+#pragma unroll
+  for (int p = 0; p < CODEC_KEEP / 8; ++p) {
+    const int e = threadIdx.x + CODEC_THREADS * p;
+    if (e < pad * cv) keep[p] = joined8<DT>(st, x, ld_x, row0, pad, T + e / cv, 8 * (e % cv), C, use_elu);
+  }
   __syncthreads();
-  n = 0;
-  for (int e = threadIdx.x; e < pad * cv; e += CODEC_THREADS) stv<DT>(st + 8 * e, keep[n++]);
+#pragma unroll
+  for (int p = 0; p < CODEC_KEEP / 8; ++p) {
+    const int e = threadIdx.x + CODEC_THREADS * p;
+    if (e < pad * cv) stv<DT>(st + 8 * e, keep[p]);
+  }
 }
 
 // ---------------------------------------------------------------------------------------------------------
@@ -372,18 +377,23 @@ __global__ __launch_bounds__(CODEC_THREADS) void convt_overlap_kernel(const Elt<
     stv<DT>(out + ((long)b * nout + o) * ld_out + c, r);
   }
   if (blockIdx.y) return;
-  V8<DT> keep[CODEC_KEEP / 8];
-  int n = 0;
-  for (int e = threadIdx.x; e < ov * cv; e += CODEC_THREADS) {
-    float v[8];
-    convt_frame8<DT>(cols, ld_cols, row0, nout + e / cv, 8 * (e % cv), Tin, C, k, s, v);
+  V8<DT> keep[CODEC_KEEP / 8];  // constant indices: registers, not a private or LDS array
 #pragma unroll
-    for (int i = 0; i < 8; ++i) keep[n].v[i] = E<DT>::from_f(v[i]);
-    ++n;
+  for (int p = 0; p < CODEC_KEEP / 8; ++p) {
+    const int e = threadIdx.x + CODEC_THREADS * p;
+    if (e < ov * cv) {
+      float v[8];
+      convt_frame8<DT>(cols, ld_cols, row0, nout + e / cv, 8 * (e % cv), Tin, C, k, s, v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) keep[p].v[i] = E<DT>::from_f(v[i]);
+    }
   }
   __syncthreads();
-  n = 0;
-  for (int e = threadIdx.x; e < ov * cv; e += CODEC_THREADS) stv<DT>(tl + 8 * e, keep[n++]);
+#pragma unroll
+  for (int p = 0; p < CODEC_KEEP / 8; ++p) {
+    const int e = threadIdx.x + CODEC_THREADS * p;
+    if (e < ov * cv) stv<DT>(tl + 8 * e, keep[p]);
+  }
 }
 
 // ---------------------------------------------------------------------------------------------------------
@@ -614,13 +624,18 @@ __global__ __launch_bounds__(CODEC_THREADS) void final_conv_kernel(const Elt<DT>
     pcm[(long)b * ld_pcm + t] = acc + bias;
   }
   if (!pad || blockIdx.y) return;
-  V8<DT> keep[CODEC_KEEP / 8];
-  int n = 0;
-  for (int e = threadIdx.x; e < pad * cv; e += CODEC_THREADS)
-    keep[n++] = joined8<DT>(st, x, ld_x, row0, pad, T + e / cv, 8 * (e % cv), C, 0);
+  V8<DT> keep[CODEC_KEEP / 8];  // constant indices: registers, not a private or LDS array
+#pragma unroll
+  for (int p = 0; p < CODEC_KEEP / 8; ++p) {
+    const int e = threadIdx.x + CODEC_THREADS * p;
+    if (e < pad * cv) keep[p] = joined8<DT>(st, x, ld_x, row0, pad, T + e / cv, 8 * (e % cv), C, 0);
+  }
   __syncthreads();
-  n = 0;
-  for (int e = threadIdx.x; e < pad * cv; e += CODEC_THREADS) stv<DT>(st + 8 * e, keep[n++]);
+#pragma unroll
+  for (int p = 0; p < CODEC_KEEP / 8; ++p) {
+    const int e = threadIdx.x + CODEC_THREADS * p;
+    if (e < pad * cv) stv<DT>(st + 8 * e, keep[p]);
+  }
 }
 
 // final_conv_kernel for the codec's shape (C <= 64 channels, k <= 9 taps), FCS_CHUNK samples per workgroup: the
