@@ -33,7 +33,15 @@ __global__ __launch_bounds__(256) void rvq_decode_kernel(const int64_t* __restri
   for (int d = threadIdx.x; d < dim; d += blockDim.x) {
     out[(long)b * ld_out + d] = tables[code(0) * dim + d];
     float s = 0.f;
-    for (int q = 1; q < nq; ++q) s += E<DT>::to_f(tables[((long)q * n_codes + code(q)) * dim + d]);
+    int q = 1;
+    for (; q + 8 <= nq; q += 8) {  // eight rows' loads in flight, then added in codebook order
+      Elt<DT> v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = tables[((long)(q + u) * n_codes + code(q + u)) * dim + d];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) s += E<DT>::to_f(v[u]);
+    }
+    for (; q < nq; ++q) s += E<DT>::to_f(tables[((long)q * n_codes + code(q)) * dim + d]);
     out[(long)b * ld_out + dim + d] = E<DT>::from_f(s);
   }
 }
