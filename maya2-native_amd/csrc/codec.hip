@@ -195,8 +195,9 @@ __global__ __launch_bounds__(256) void resid_ln_kernel(Elt<DT>* h, long ld_h, co
 // Thin GEMM with the conv epilogue, for the SEANet convs with at most 128 output channels:
 // y[m, n] = act(res[m, n] + (dt(x[m, :] . w[n, :]) + bias[n])) (m3x_linear's product, then m3x_rows_op's
 // arithmetic), w packed by m3x_pack_weight, N = 16 NT, K % 32 == 0; bias and res optional, act = ELU when use_elu.
-// Each wave owns 16 MT rows and all N columns: the activation fragments are loaded straight into the MFMA's B
-// operand (each activation element is read once), the weight fragments (K * N * 2 bytes, cache resident) into A.
+// Each wave owns 16 MT rows and the 16 NT columns of its column group (blockIdx.y; one group unless the rows alone
+// make a small grid): the activation fragments are loaded straight into the MFMA's B operand (read once per column
+// group), the weight fragments (cache resident) into A. A column group does not change any output's K order.
 // Gathered form (G = 1): the conv's rows are read in place of a gathered copy. Row m = b * T + t, column
 // kk = j * C + c of the product is joined[t + j * dil][c] (m3x_conv_gather's rows: the slot's pad stored frames,
 // then x with ELU when pre_elu); the caller advances the history afterwards.
@@ -217,6 +218,13 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(const Elt<DT>* __restric
   const int l = threadIdx.x & 63, li = l & 15, lg = l >> 4;
   const long m0 = ((long)blockIdx.x * 4 + wave) * (16 * MT);
   if (m0 >= M) return;  // wave-uniform
+  {  // column group blockIdx.y: columns 16 NT y .. 16 NT (y + 1) - 1
+    const int n0 = 16 * NT * (int)blockIdx.y;
+    Wp += (long)n0 * K;  // NT tiles of K / 32 fragments of 512 elements
+    if (bias) bias += n0;
+    if (res) res += n0;
+    Y += n0;
+  }
   f32x4_t acc[NT][MT];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
@@ -891,11 +899,16 @@ M3X_API int m3x_conv_gemm(const void* x, long ldx, const void* w_packed, const v
       (bias && (((uintptr_t)bias) & 7)))
     return M3X_EINVAL;
   const int mt = M >= 64 * 1024 ? 2 : 1;  // two row tiles per wave once the grid fills the chip anyway
-  const dim3 grid(m3x_ceil_div(M, 4 * 16 * mt));
+  // few rows (one seat): the columns split into up to N / 16 groups until 128 workgroups run
+  const int gx = m3x_ceil_div(M, 4 * 16 * mt);
+  int ny = 1;
+  while (ny < N / 16 && (long)gx * ny < 128) ny *= 2;
+  const int nt = N / 16 / ny;
+  const dim3 grid(gx, ny);
   if (dtype == M3X_F32 && bias && !m3x_aligned16(bias)) return M3X_EINVAL;
   hipStream_t st = (hipStream_t)stream;
 #define CG_CASE(DTT, NTT, MTT)                                                                                   \
-  if (dtype == DTT && N == 16 * NTT && mt == MTT) {                                                              \
+  if (dtype == DTT && nt == NTT && mt == MTT) {                                                              \
     using ET = Elt<DTT>;                                                                                         \
     const ET *X = (const ET*)x, *W = (const ET*)w_packed, *Bi = (const ET*)bias, *R = (const ET*)res;                 \
     if (G)                                                                                                       \
