@@ -20,8 +20,8 @@ __global__ __launch_bounds__(256) void pack_weight_kernel(const Elt<DT>* __restr
 // fp32 projections (the fp32 compute paths: FastDepth and StaticMimi built with dtype=float32). The packed layout
 // is the 16-bit one with 4-byte elements (a fragment is 2 KB, lane l's 8 values at + 8 l), so one pack serves
 // both; each k step of 32 is eight v_mfma_f32_16x16x4_f32 (mfma16x16x32_f32). A workgroup of 4 waves = NW weight
-// tiles x KW = 4 / NW slices of K walks its slice in chunks of 32 U (U = 2 k steps; 4 for the tiles of one 16-row
-// block): the chunk's activation rows are staged in LDS (row stride 32 U + 4 floats), the next chunk's rows and
+// tiles x KW = 4 / NW slices of K walks its slice in chunks of 32 U (U = 4 k steps for 16- and 32-row tiles, 2 for
+// 64-row ones): the chunk's activation rows are staged in LDS (row stride 32 U + 4 floats), the next chunk's rows and
 // weight fragments load into registers while the
 // current one multiplies. The KW slice partials meet in LDS and are added in slice order (deterministic).
 // Epilogues in fp32: EPI_NONE y = acc; EPI_SWIGLU y = silu(g) * u; EPI_GELU y = gelu(acc) (erf form).
@@ -33,9 +33,10 @@ __global__ __launch_bounds__(256) void linear_f32_kernel(const float* __restrict
   constexpr int KW = 4 / NW;
   constexpr int ROWS = 16 * MT;
   static_assert(MT * KW <= 4, "activation chunks must fit the LDS budget");
-  // k steps (of 32) per chunk: 4 for the one-row-tile shapes (few rows, latency-bound: half the chunks, half the
-  // load round trips), 2 otherwise; each wave still adds its slice's steps in order, so U does not change the bits
-  constexpr int U = MT == 1 ? 4 : 2;
+  // k steps (of 32) per chunk: 4 for the tiles of one or two 16-row blocks (few rows, latency-bound: half the
+  // chunks, half the load round trips), 2 for the 64-row tiles; each wave still adds its slice's steps in order, so
+  // U does not change the bits
+  constexpr int U = MT <= 2 ? 4 : 2;
   constexpr int LDR = 32 * U + 4;   // LDS row stride in floats
   constexpr int GPR = 8 * U;        // 16-byte granules per row per chunk
   constexpr int NVEC = KW * ROWS * GPR;
